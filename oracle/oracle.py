@@ -1,0 +1,316 @@
+"""numpy front end of the CPU parity oracle (TEST INFRASTRUCTURE ONLY).
+
+Loads ``oracle/_build/librefcpu.so`` (built from ``refcpu.c`` and
+``refcpu_mt.c`` by ``oracle/Makefile``) and exposes its functions on numpy
+float32 arrays.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this module; the product path
+(``libcdml_hip.so`` and the host manager) never does.
+
+Each wrapper names the reference method it restates; the C source cites the
+exact reference lines.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "librefcpu.so")
+_lib = None
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_u8p = C.c_void_p
+
+
+class OracleError(ValueError):
+    """Raised where the reference throws ArgumentException and friends."""
+
+
+def build(force: bool = False) -> str:
+    """Compile the oracle library with make (CPU only, a few seconds)."""
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        build()
+        L = C.CDLL(_LIB_PATH)
+        i, f = C.c_int, C.c_float
+        sig = {
+            "ref_dot": (f, [_f32p, _f32p, i]),
+            "ref_project_qkv": (i, [_f32p] * 7 + [_f32p] * 3 + [i, i, i]),
+            "ref_project_output_batch": (i, [_f32p] * 4 + [i, i, i]),
+            "ref_batch_dot_add_bias": (i, [_f32p] * 4 + [i, i, i]),
+            "ref_activation_inplace": (None, [_f32p, C.c_long, i]),
+            "ref_rope_inplace": (i, [_f32p, i, i, i, f, i]),
+            "ref_rope_head_inplace": (i, [_f32p, i, i, i, i, f, i]),
+            "ref_sdpa": (i, [_f32p] * 4 + [i, i, i, i, _u8p, i]),
+            "ref_mha_forward": (i, [_f32p] * 4 + [i, i, i, i, f, _u8p]),
+            "ref_softmax": (i, [_f32p, _f32p, i, i, _u8p]),
+            "ref_residual_layernorm": (i, [_f32p] * 5 + [i, i, f]),
+            "ref_embed_tokens": (i, [_i32p, i, _f32p, i, i, _f32p]),
+            "ref_causal_mask": (None, [i, C.c_void_p]),
+            "ref_decode_attention": (i, [_f32p, _f32p, _f32p, i, i, i, f, _f32p]),
+            "ref_lm_forward": (i, [C.c_void_p, _i32p, i, _f32p]),
+            "ref_lm_generate_greedy": (i, [C.c_void_p, _i32p, i, i, _i32p, C.POINTER(i)]),
+            "mt_num_threads": (i, []),
+            "mt_set_threads": (None, [i]),
+            "mt_project_qkv": (i, [_f32p] * 10 + [i, i, i]),
+            "mt_project_output_batch": (i, [_f32p] * 4 + [i, i, i]),
+            "mt_batch_dot_add_bias": (i, [_f32p] * 4 + [i, i, i]),
+            "mt_rope_inplace": (i, [_f32p, i, i, i, f, i]),
+            "mt_sdpa": (i, [_f32p] * 4 + [i, i, i, i, _u8p, i]),
+            "mt_residual_layernorm": (i, [_f32p] * 5 + [i, i, f]),
+            "mt_decode_attention_batch": (i, [_f32p, _f32p, _f32p, _i32p, i, i, i, i, f, _f32p, i]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _mask_ptr(mask):
+    if mask is None:
+        return None, None
+    m = np.ascontiguousarray(mask, dtype=np.uint8)
+    return m, m.ctypes.data_as(C.c_void_p)
+
+
+def _check(rc: int, what: str):
+    if rc == -2:
+        raise OracleError(f"{what}: causal attention requires queryLen == keyLen")
+    if rc != 0:
+        raise OracleError(f"{what}: invalid argument (status {rc})")
+
+
+# ---- AccelerationCPU restatement -----------------------------------------
+
+def dot(a, b) -> float:
+    a, b = _f32(a), _f32(b)
+    return float(lib().ref_dot(a, b, a.size))
+
+
+def project_qkv(x, wq, bq, wk, bk, wv, bv, mt: bool = False):
+    """AccelerationCPU.ProjectQKV (mt: AccelerationMutliThreadCPU.ProjectQKV)."""
+    x = _f32(x)
+    rows, in_dim = x.shape
+    out_dim = wq.shape[0]
+    q = np.empty((rows, out_dim), np.float32)
+    k = np.empty_like(q)
+    v = np.empty_like(q)
+    fn = lib().mt_project_qkv if mt else lib().ref_project_qkv
+    _check(fn(x, _f32(wq), _f32(bq), _f32(wk), _f32(bk), _f32(wv), _f32(bv),
+              q, k, v, rows, in_dim, out_dim), "ProjectQKV")
+    return q, k, v
+
+
+def project_output_batch(h, w, b, mt: bool = False):
+    """AccelerationCPU.ProjectOutputBatch: y = b + h W^T."""
+    h = _f32(h)
+    rows, in_dim = h.shape
+    out_dim = w.shape[0]
+    y = np.empty((rows, out_dim), np.float32)
+    fn = lib().mt_project_output_batch if mt else lib().ref_project_output_batch
+    _check(fn(h, _f32(w), _f32(b), y, rows, in_dim, out_dim), "ProjectOutputBatch")
+    return y
+
+
+def batch_dot_add_bias(w, x, b, mt: bool = False):
+    """AccelerationCPU.BatchDotProductAddBias: y = x W^T + b."""
+    x = _f32(x)
+    rows, in_dim = x.shape
+    out_dim = w.shape[0]
+    y = np.empty((rows, out_dim), np.float32)
+    fn = lib().mt_batch_dot_add_bias if mt else lib().ref_batch_dot_add_bias
+    _check(fn(_f32(w), x, _f32(b), y, rows, in_dim, out_dim), "BatchDotProductAddBias")
+    return y
+
+
+def activation(x, act: int):
+    """NeuralNetwork.ApplyActivationInPlace on a copy."""
+    y = _f32(x).copy()
+    lib().ref_activation_inplace(y, y.size, act)
+    return y
+
+
+def rope(x, num_heads: int, base_theta: float = 10000.0, inverse: bool = False, mt: bool = False):
+    """AccelerationCPU.ApplyRotaryPositionEmbeddingInPlace on a copy."""
+    y = _f32(x).copy()
+    rows, dim = y.shape
+    fn = lib().mt_rope_inplace if mt else lib().ref_rope_inplace
+    _check(fn(y, rows, dim, num_heads, base_theta, int(inverse)), "ApplyRotaryPositionEmbeddingInPlace")
+    return y
+
+
+def rope_head(x, start_col: int, head_dim: int, base_theta: float = 10000.0, inverse: bool = False):
+    """AccelerationCPU.ApplyRotaryPositionEmbeddingHeadInPlace on a copy."""
+    y = _f32(x).copy()
+    rows, dim = y.shape
+    _check(lib().ref_rope_head_inplace(y, rows, dim, start_col, head_dim, base_theta, int(inverse)),
+           "ApplyRotaryPositionEmbeddingHeadInPlace")
+    return y
+
+
+def sdpa(q, k, v, num_heads: int, mask=None, causal: bool = False, mt: bool = False):
+    """AccelerationCPU.ScaledDotProductAttention."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    lq, dim = q.shape
+    lk = k.shape[0]
+    out = np.empty((lq, dim), np.float32)
+    _m, mp = _mask_ptr(mask)
+    fn = lib().mt_sdpa if mt else lib().ref_sdpa
+    _check(fn(q, k, v, out, lq, lk, dim, num_heads, mp, int(causal)), "ScaledDotProductAttention")
+    return out
+
+
+def mha_forward(q, k, v, num_heads: int, scale: float, mask=None):
+    """AccelerationCPU.MultiHeadAttentionForward."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    lq, dim = q.shape
+    lk = k.shape[0]
+    out = np.empty((lq, dim), np.float32)
+    _m, mp = _mask_ptr(mask)
+    _check(lib().ref_mha_forward(q, k, v, out, lq, lk, dim, num_heads, scale, mp),
+           "MultiHeadAttentionForward")
+    return out
+
+
+def softmax(x, mask=None):
+    """AccelerationCPU.Softmax."""
+    x = _f32(x)
+    out = np.empty_like(x)
+    _m, mp = _mask_ptr(mask)
+    rc = lib().ref_softmax(x, out, x.shape[0], x.shape[1], mp)
+    if rc == -3:
+        raise OracleError("Softmax input contains NaN")
+    return out
+
+
+def residual_layernorm(a, b, gamma, beta, eps: float = 1e-5, mt: bool = False):
+    """AccelerationCPU.ResidualLayerNorm."""
+    a = _f32(a)
+    rows, f = a.shape
+    out = np.empty_like(a)
+    fn = lib().mt_residual_layernorm if mt else lib().ref_residual_layernorm
+    _check(fn(a, _f32(b), _f32(gamma), _f32(beta), out, rows, f, eps), "ResidualLayerNorm")
+    return out
+
+
+def embed_tokens(ids, table):
+    """AccelerationCPU.EmbedTokenIds."""
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    table = _f32(table)
+    out = np.empty((ids.size, table.shape[1]), np.float32)
+    _check(lib().ref_embed_tokens(ids, ids.size, table, table.shape[0], table.shape[1], out),
+           "EmbedTokenIds")
+    return out
+
+
+def causal_mask(n: int):
+    """AccelerationCPU.CreateCausalMask."""
+    m = np.empty((n, n), np.uint8)
+    lib().ref_causal_mask(n, m.ctypes.data_as(C.c_void_p))
+    return m
+
+
+def decode_attention(q, kcache, vcache, key_len: int, num_heads: int, scale: float):
+    """LanguageModel.DecoderSelfAttentionStep attention core for one query row."""
+    q = _f32(q).reshape(-1)
+    dim = q.size
+    out = np.empty(dim, np.float32)
+    lib().ref_decode_attention(q, _f32(kcache), _f32(vcache), key_len, dim, num_heads, scale, out)
+    return out
+
+
+def decode_attention_batch(q, kcache, vcache, kv_len, num_heads: int, scale: float, parallel: bool):
+    """Decode attention for B sequences over a [B, Tmax, D] cache."""
+    q = _f32(q)
+    b, dim = q.shape
+    t_max = kcache.shape[1]
+    out = np.empty((b, dim), np.float32)
+    lib().mt_decode_attention_batch(q, _f32(kcache), _f32(vcache),
+                                    np.ascontiguousarray(kv_len, dtype=np.int32),
+                                    b, t_max, dim, num_heads, scale, out, int(parallel))
+    return out
+
+
+def num_threads() -> int:
+    return int(lib().mt_num_threads())
+
+
+def set_threads(n: int):
+    lib().mt_set_threads(int(n))
+
+
+# ---- LanguageModel restatement -------------------------------------------
+
+class _Layer(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in (
+        "wq", "wk", "wv", "wo", "bq", "bk", "bv", "bo",
+        "ln1_g", "ln1_b", "ln2_g", "ln2_b",
+        "ffn_w1", "ffn_b1", "ffn_w2", "ffn_b2")]
+
+
+class _LM(C.Structure):
+    _fields_ = [("vocab", C.c_int), ("dim", C.c_int), ("heads", C.c_int),
+                ("layers", C.c_int), ("ff", C.c_int), ("max_seq", C.c_int),
+                ("ffn_activation", C.c_int),
+                ("token_embedding", C.c_void_p), ("out_proj", C.c_void_p),
+                ("out_bias", C.c_void_p), ("layer", C.POINTER(_Layer))]
+
+
+class LanguageModel:
+    """Decoder-only LanguageModel over a dict of float32 weights.
+
+    ``weights`` keys: ``token_embedding`` [V, D], ``out_proj`` [V, D],
+    ``out_bias`` [V] and ``layers``: a list of dicts with the ``_Layer``
+    field names.  The arrays are kept alive by this object.
+    """
+
+    def __init__(self, cfg: dict, weights: dict):
+        self.cfg = dict(cfg)
+        self._keep = []
+
+        def p(a):
+            a = _f32(a)
+            self._keep.append(a)
+            return a.ctypes.data
+
+        nl = cfg["layers"]
+        self._layers = (_Layer * nl)()
+        for i, lw in enumerate(weights["layers"]):
+            for name, _ in _Layer._fields_:
+                setattr(self._layers[i], name, p(lw[name]))
+        self._lm = _LM(cfg["vocab"], cfg["dim"], cfg["heads"], nl, cfg["ff"],
+                       cfg["max_seq"], cfg.get("ffn_activation", 3),
+                       p(weights["token_embedding"]), p(weights["out_proj"]),
+                       p(weights["out_bias"]),
+                       C.cast(self._layers, C.POINTER(_Layer)))
+
+    def forward(self, ids):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        logits = np.empty((ids.size, self.cfg["vocab"]), np.float32)
+        _check(lib().ref_lm_forward(C.c_void_p(C.addressof(self._lm)), ids, ids.size, logits),
+               "LanguageModel.Forward")
+        return logits
+
+    def generate_greedy(self, prompt, max_new: int):
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.zeros(self.cfg["max_seq"] + max(0, max_new) + prompt.size, np.int32)
+        n = C.c_int(0)
+        _check(lib().ref_lm_generate_greedy(C.c_void_p(C.addressof(self._lm)), prompt, prompt.size,
+                                            max_new, out, C.byref(n)), "LanguageModel.Generate")
+        return out[: n.value].copy()

@@ -1,0 +1,245 @@
+"""Pins the CPU oracle (oracle/refcpu.c) before it is trusted as the checker.
+
+Three kinds of evidence, none of them a retyping of the oracle's loops:
+* the reference test suite's own known answers (RoPE cos/sin values,
+  MatrixMultiplyTranspose 17/23/67, masked-softmax sums, LayerNorm stats,
+  the all-masked-row and causal-cross-attention rules);
+* float64 textbook results on the reference tests' closed-form inputs
+  (tests/golden/ops.npz, lm_*.npz, written by tests/golden/gen_golden.py);
+* invariants the mathematics fixes (causal flag == explicit lower-triangular
+  mask, decode of the last position == last row of causal prefill, causal
+  invariance to future tokens, greedy decode with a KV cache == greedy with
+  full-prefix recompute).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from conftest import assert_parity, load_lm_golden
+from oracle import oracle as O
+from cdml import synth
+
+M, Vec = synth.matrix, synth.vector
+
+
+def close(a, e, atol=2e-6, rtol=1e-5, what=""):
+    assert_parity(a, e, atol=atol, rtol=rtol, what=what)
+
+
+# ----------------------------------------------------------- known answers
+def test_rope_known_values():
+    # RotaryPositionEmbeddingTests.cs:138-177
+    x = O.rope(np.array([[1, 2, 3, 4], [5, 6, 7, 8]], np.float32), 1)
+    assert np.allclose(x[0], [1, 2, 3, 4], atol=1e-5)
+    y = O.rope(np.array([[1, 0], [1, 0], [0, 1]], np.float32), 1)
+    assert np.allclose(y[0], [1, 0], atol=1e-5)
+    assert np.allclose(y[1], [math.cos(1), math.sin(1)], atol=1e-5)
+    assert np.allclose(y[2], [-math.sin(2), math.cos(2)], atol=1e-5)
+
+
+def test_rope_heads_independent_and_round_trip():
+    # RotaryPositionEmbeddingTests.cs:179-196, 223-266; parity tests :1107-1111
+    x = O.rope(np.array([[1, 2, 3, 4], [1, 0, 0, 1]], np.float32), 2)
+    assert np.allclose(x[1], [math.cos(1), math.sin(1), -math.sin(1), math.cos(1)], atol=1e-5)
+    m = M(4, 8, 97)
+    back = O.rope(O.rope(m, 2), 2, inverse=True)
+    assert np.allclose(back, m, atol=5e-4)
+
+
+def test_rope_rejects_odd_head_dim():
+    with pytest.raises(O.OracleError):
+        O.rope(np.zeros((2, 6), np.float32), 2)
+
+
+def test_matrix_multiply_transpose_known_values():
+    # MultiTypeTransformerTests.cs:664-674 via y = h W^T + 0
+    a = np.array([[1, 2], [3, 4]], np.float32)
+    b = np.array([[5, 6], [7, 8], [9, 10]], np.float32)
+    c = O.project_output_batch(a, b, np.zeros(3, np.float32))
+    assert c.shape == (2, 3)
+    assert c[0, 0] == 17 and c[0, 1] == 23 and c[1, 2] == 67
+
+
+def test_softmax_masked_rows():
+    # MultiTypeTransformerTests.cs:634-662
+    s = O.softmax(np.array([[1, 2, 3], [-1, 0, 1]], np.float32),
+                  np.array([[1, 0, 1], [0, 1, 1]], np.uint8))
+    assert abs(s[0, 1]) < 1e-7 and abs(s[1, 0]) < 1e-7
+    assert abs(s[0, 0] + s[0, 2] - 1) < 1e-6 and abs(s[1, 1] + s[1, 2] - 1) < 1e-6
+    z = O.softmax(np.array([[1, 2, 3]], np.float32), np.zeros((1, 3), np.uint8))
+    assert np.all(z == 0)
+
+
+def test_layernorm_row_stats():
+    # MultiTypeTransformerTests.cs:676-700
+    x = np.array([[1, 2, 3, 4], [-1, 0, 1, 2]], np.float32)
+    y = O.residual_layernorm(x, np.zeros_like(x), np.ones(4, np.float32), np.zeros(4, np.float32))
+    assert np.all(np.abs(y.mean(axis=1)) < 1e-5)
+    assert np.all(np.abs(y.var(axis=1) - 1) < 1e-3)
+
+
+def test_sdpa_rules():
+    # AccelerationManagerParityTests.cs:438-458
+    q, k, v = M(4, 8, 121), M(5, 8, 122), M(5, 8, 123)
+    with pytest.raises(O.OracleError):
+        O.sdpa(q, k, v, 2, causal=True)
+    m = np.ones((4, 5), np.uint8)
+    m[0] = 0
+    out = O.sdpa(q, k, v, 2, mask=m)
+    assert np.all(out[0] == 0)
+    # one key: softmax weight is exactly 1, so the output is V itself
+    one = O.sdpa(q[:1], k[:1], v[:1], 2)
+    assert np.array_equal(one, v[:1])
+
+
+# ------------------------------------------------------- float64 goldens
+def test_sdpa_golden(ops_golden):
+    g = ops_golden
+    qs, ks, vs = M(4, 8, 118), M(4, 8, 119), M(4, 8, 120)
+    qc, kc, vc = M(4, 8, 121), M(5, 8, 122), M(5, 8, 123)
+    close(O.sdpa(qs, ks, vs, 2), g["sdpa_self_nomask"], what="self/no mask")
+    close(O.sdpa(qs, ks, vs, 2, mask=g["self_mask"]), g["sdpa_self_mask"], what="self/mask")
+    close(O.sdpa(qs, ks, vs, 2, causal=True), g["sdpa_self_causal"], what="self/causal")
+    close(O.sdpa(qc, kc, vc, 2), g["sdpa_cross_nomask"], what="cross/no mask")
+    close(O.sdpa(qc, kc, vc, 2, mask=g["cross_mask"]), g["sdpa_cross_mask"], what="cross/mask")
+    close(O.sdpa(qc, kc, vc, 2, mask=g["all_masked_mask"]), g["sdpa_cross_allmasked"], what="all masked")
+
+
+def test_mha_golden(ops_golden):
+    g = ops_golden
+    q6, k6, v6 = M(4, 6, 31), M(4, 6, 32), M(4, 6, 33)
+    close(O.mha_forward(q6, k6, v6, 2, float(g["mha_causal_scale"]), mask=O.causal_mask(4)),
+          g["mha_causal"], what="mha causal d_h=3")
+    qg, kg, vg = M(128, 64, 110), M(128, 64, 111), M(128, 64, 112)
+    close(O.mha_forward(qg, kg, vg, 4, 0.25), g["mha128_nomask"], what="mha128")
+    close(O.sdpa(qg, kg, vg, 4, causal=True), g["mha128_causal"], what="sdpa128 causal")
+
+
+def test_causal_flag_equals_explicit_mask():
+    # AccelerationManagerParityTests.cs:410-421 (bit-identical in the reference CPU manager)
+    q, k, v = M(37, 16, 1), M(37, 16, 2), M(37, 16, 3)
+    a = O.sdpa(q, k, v, 2, causal=True)
+    b = O.sdpa(q, k, v, 2, mask=O.causal_mask(37))
+    assert np.array_equal(a, b)
+
+
+def test_projections_golden(ops_golden):
+    g = ops_golden
+    x = M(6, 5, 124)
+    q, k, v = O.project_qkv(x, M(8, 5, 125), Vec(8, 128), M(8, 5, 126), Vec(8, 129), M(8, 5, 127), Vec(8, 130))
+    close(q, g["qkv_small_q"], what="Q")
+    close(k, g["qkv_small_k"], what="K")
+    close(v, g["qkv_small_v"], what="V")
+    xg = M(192, 128, 142)
+    q, k, v = O.project_qkv(xg, M(128, 128, 143), Vec(128, 146), M(128, 128, 144), Vec(128, 147),
+                            M(128, 128, 145), Vec(128, 148))
+    close(q, g["qkv_big_q"], atol=1e-5, what="Q big")
+    close(k, g["qkv_big_k"], atol=1e-5, what="K big")
+    close(v, g["qkv_big_v"], atol=1e-5, what="V big")
+    close(O.project_output_batch(M(4, 6, 56), M(3, 6, 57), Vec(3, 58)), g["project_output"], what="POB")
+    assert np.array_equal(O.embed_tokens([0, 2, 4], M(6, 5, 64)), g["embed"])
+    with pytest.raises(O.OracleError):
+        O.embed_tokens([0, 6], M(6, 5, 64))
+
+
+def test_rope_golden(ops_golden):
+    g = ops_golden
+    close(O.rope(M(4, 8, 97), 2), g["rope_all"], what="rope all heads")
+    close(O.rope_head(M(4, 8, 97), 2, 4), g["rope_head"], what="rope one head")
+    close(O.rope(M(300, 32, 7), 4), g["rope_long"], atol=2e-5, what="rope 300 positions")
+
+
+def test_softmax_layernorm_golden(ops_golden):
+    g = ops_golden
+    close(O.softmax(M(4, 4, 26)), g["softmax_nomask"], what="softmax")
+    close(O.softmax(M(4, 4, 26), g["softmax_mask_in"]), g["softmax_mask"], what="softmax mask")
+    close(O.residual_layernorm(M(5, 6, 27), np.zeros((5, 6), np.float32), synth.positive_vector(6, 28),
+                               Vec(6, 29)), g["layernorm"], what="layernorm")
+
+
+# ---------------------------------------------------- language model flow
+def _oracle_lm(g):
+    return O.LanguageModel(g["cfg"], g["weights"])
+
+
+@pytest.mark.parametrize("name", ["lm_tiny", "lm_c1"])
+def test_lm_forward_golden(name):
+    g = load_lm_golden(name)
+    lm = _oracle_lm(g)
+    close(lm.forward(g["ids"]), g["logits"], atol=2e-5, rtol=1e-4, what=f"{name} logits")
+
+
+@pytest.mark.parametrize("name", ["lm_tiny", "lm_c1"])
+def test_lm_greedy_matches_full_recompute(name):
+    g = load_lm_golden(name)
+    assert np.all(g["greedy_margins"] > 1e-3), "fixture margins too small to pin argmax"
+    lm = _oracle_lm(g)
+    out = lm.generate_greedy(g["ids"][: int(g["prompt_len"])], int(g["n_new"]))
+    assert np.array_equal(out, g["greedy"])
+
+
+def test_lm_causal_invariance():
+    # MultiTypeTransformerTests.cs:135-166: a future token never changes earlier logits
+    g = load_lm_golden("lm_tiny")
+    lm = _oracle_lm(g)
+    ids = g["ids"].copy()
+    a = lm.forward(ids)
+    ids[-1] = (ids[-1] + 1) % g["cfg"]["vocab"]
+    b = lm.forward(ids)
+    assert np.max(np.abs(a[:-1] - b[:-1])) < 1e-5
+    assert np.max(np.abs(a[-1] - b[-1])) > 0
+
+
+def test_lm_generate_bounds():
+    # LanguageModel.cs:487-496
+    g = load_lm_golden("lm_tiny")
+    lm = _oracle_lm(g)
+    full = np.zeros(g["cfg"]["max_seq"], np.int32)
+    assert np.array_equal(lm.generate_greedy(full, 5), full)
+    assert np.array_equal(lm.generate_greedy(g["ids"][:3], 0), g["ids"][:3])
+    with pytest.raises(O.OracleError):
+        lm.generate_greedy(np.array([g["cfg"]["vocab"]], np.int32), 2)
+
+
+def test_decode_equals_last_prefill_row():
+    D, H, T = 64, 4, 77
+    q, k, v = synth.normal(11, (T, D)), synth.normal(12, (T, D)), synth.normal(13, (T, D))
+    pre = O.sdpa(q, k, v, H, causal=True)
+    for t in (1, 2, 40, T):
+        dec = O.decode_attention(q[t - 1], k, v, t, H, 1.0 / math.sqrt(D // H))
+        close(dec, pre[t - 1], atol=1e-5, what=f"decode t={t}")
+
+
+def test_mt_restatement_matches_single_thread():
+    x = synth.normal(1, (33, 48))
+    w = [synth.xavier_uniform(2 + i, 48, 48) for i in range(3)]
+    b = [synth.normal(9 + i, (48,)) for i in range(3)]
+    st = O.project_qkv(x, w[0], b[0], w[1], b[1], w[2], b[2])
+    mt = O.project_qkv(x, w[0], b[0], w[1], b[1], w[2], b[2], mt=True)
+    for a, e in zip(mt, st):
+        close(a, e, atol=1e-5)
+    close(O.project_output_batch(x, w[0], b[0], mt=True), O.project_output_batch(x, w[0], b[0]), atol=1e-5)
+    close(O.batch_dot_add_bias(w[0], x, b[0], mt=True), O.batch_dot_add_bias(w[0], x, b[0]), atol=1e-5)
+    assert np.array_equal(O.rope(x, 4, mt=True), O.rope(x, 4))
+    close(O.sdpa(x, x, x, 4, causal=True, mt=True), O.sdpa(x, x, x, 4, causal=True), atol=1e-5)
+    close(O.residual_layernorm(x, x, b[0], b[1], mt=True), O.residual_layernorm(x, x, b[0], b[1]))
+    kc = synth.normal(5, (3, 20, 48))
+    vc = synth.normal(6, (3, 20, 48))
+    qd = synth.normal(7, (3, 48))
+    lens = np.array([20, 7, 1], np.int32)
+    seq = O.decode_attention_batch(qd, kc, vc, lens, 4, 0.25, parallel=False)
+    par = O.decode_attention_batch(qd, kc, vc, lens, 4, 0.25, parallel=True)
+    assert np.array_equal(seq, par)
+    for i in range(3):
+        assert np.array_equal(seq[i], O.decode_attention(qd[i], kc[i], vc[i], int(lens[i]), 4, 0.25))
+
+
+def test_oracle_detects_planted_mistake(ops_golden):
+    """A plausible slip (keys and values swapped) must fail the golden check."""
+    qs, ks, vs = M(4, 8, 118), M(4, 8, 119), M(4, 8, 120)
+    wrong = O.sdpa(qs, vs, ks, 2)
+    with pytest.raises(AssertionError):
+        close(wrong, ops_golden["sdpa_self_nomask"])
