@@ -1,0 +1,288 @@
+// Single-query decode attention over a cached K/V (the device form of the
+// inline loop in LanguageModel.DecoderSelfAttentionStep, LanguageModel.cs:365-427).
+//
+// HBM-bound: every cached K and V element is read exactly once.  The cache
+// of each (sequence, head) is split into chunks of 256 keys; one 256-thread
+// workgroup owns a chunk.  Inside a wave, each group of 8 lanes owns one key
+// per step (8 keys per wave-step), each lane covering head_dim/8 contiguous
+// floats of that key's row, so every load instruction reads whole 128-byte
+// lines.  Pass 1 computes the chunk's scores (dot products reduced across the
+// 8-lane group), pass 2 reads V and accumulates exp2(score - chunk max) * v.
+// A combine kernel merges the chunks with the usual (max, sum) rescaling.
+#include "common.h"
+
+namespace cdml {
+namespace {
+
+constexpr int DC_THREADS = 256;
+constexpr int DC_CHUNK = 256;               // keys per workgroup
+constexpr int DC_KITER = DC_CHUNK / 4 / 8;  // steps of 8 keys per wave
+
+struct DecodeArgs {
+  const float *q, *kc, *vc;
+  const int *kv_len;
+  float *o;
+  float *part;  // [batch*heads][nsplit][hd + 2]: o[hd], max, sum
+  int t_max, dim, heads, hd, nsplit;
+  float scale_log2;
+};
+
+typedef float vf4 __attribute__((ext_vector_type(4)));
+typedef float vf2 __attribute__((ext_vector_type(2)));
+
+// Streams one lane's slice of a cached row (read once: non-temporal).
+template <int EPL>
+__device__ __forceinline__ void load_row(const float *__restrict__ p, float (&r)[EPL]) {
+  if constexpr (EPL % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < EPL / 4; ++i) {
+      vf4 t = __builtin_nontemporal_load(reinterpret_cast<const vf4 *>(p) + i);
+      r[4 * i] = t.x;
+      r[4 * i + 1] = t.y;
+      r[4 * i + 2] = t.z;
+      r[4 * i + 3] = t.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < EPL / 2; ++i) {
+      vf2 t = __builtin_nontemporal_load(reinterpret_cast<const vf2 *>(p) + i);
+      r[2 * i] = t.x;
+      r[2 * i + 1] = t.y;
+    }
+  }
+}
+
+template <int HD>
+__global__ void __launch_bounds__(DC_THREADS) decode_split_kernel(const DecodeArgs a) {
+  constexpr int EPL = HD / 8;
+  __shared__ float red_m[4], red_l[4];
+  __shared__ float red_o[4][HD];
+
+  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 3, e = lane & 7;
+  const int len = min(max(a.kv_len[b], 0), a.t_max);
+  const int chunk0 = split * DC_CHUNK;
+  float *part = a.part + ((size_t)(b * a.heads + h) * a.nsplit + split) * (HD + 2);
+
+  if (chunk0 >= len) {
+    for (int d = threadIdx.x; d < HD + 2; d += DC_THREADS)
+      part[d] = d == HD ? -INFINITY : 0.f;
+    return;
+  }
+
+  const size_t col = (size_t)h * HD + e * EPL;
+  float q[EPL];
+  load_row<EPL>(a.q + (size_t)b * a.dim + col, q);
+
+  const float *kb = a.kc + (size_t)b * a.t_max * a.dim + col;
+  const float *vb = a.vc + (size_t)b * a.t_max * a.dim + col;
+  const int key0 = chunk0 + wave * (DC_KITER * 8) + g;
+
+  float sc[DC_KITER];
+#pragma unroll
+  for (int it = 0; it < DC_KITER; ++it) {
+    const int key = key0 + it * 8;
+    float kr[EPL];
+    if (key < len) {
+      load_row<EPL>(kb + (size_t)key * a.dim, kr);
+    } else {
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) kr[i] = 0.f;
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) s += q[i] * kr[i];
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    sc[it] = key < len ? s * a.scale_log2 : -INFINITY;
+  }
+
+  float mx = sc[0];
+#pragma unroll
+  for (int it = 1; it < DC_KITER; ++it) mx = fmaxf(mx, sc[it]);
+  mx = fmaxf(mx, __shfl_xor(mx, 8));
+  mx = fmaxf(mx, __shfl_xor(mx, 16));
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  if (lane == 0) red_m[wave] = mx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+  const float m_use = M == -INFINITY ? 0.f : M;
+
+  float o[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) o[i] = 0.f;
+  float lsum = 0.f;
+#pragma unroll
+  for (int it = 0; it < DC_KITER; ++it) {
+    const int key = key0 + it * 8;
+    if (key < len) {
+      float vr[EPL];
+      load_row<EPL>(vb + (size_t)key * a.dim, vr);
+      const float p = fast_exp2(sc[it] - m_use);
+      lsum += p;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) o[i] += p * vr[i];
+    }
+  }
+  // Sum over the 8 key groups of the wave (lanes with equal e).
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    o[i] += __shfl_xor(o[i], 8);
+    o[i] += __shfl_xor(o[i], 16);
+    o[i] += __shfl_xor(o[i], 32);
+  }
+  lsum += __shfl_xor(lsum, 8);
+  lsum += __shfl_xor(lsum, 16);
+  lsum += __shfl_xor(lsum, 32);
+  if (g == 0) {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) red_o[wave][e * EPL + i] = o[i];
+  }
+  if (lane == 0) red_l[wave] = lsum;
+  __syncthreads();
+  for (int d = threadIdx.x; d < HD; d += DC_THREADS)
+    part[d] = red_o[0][d] + red_o[1][d] + red_o[2][d] + red_o[3][d];
+  if (threadIdx.x == 0) {
+    part[HD] = M;
+    part[HD + 1] = red_l[0] + red_l[1] + red_l[2] + red_l[3];
+  }
+}
+
+__global__ void __launch_bounds__(256) decode_combine_kernel(const DecodeArgs a) {
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int hd = a.hd;
+  const float *part = a.part + (size_t)(b * a.heads + h) * a.nsplit * (hd + 2);
+  float M = -INFINITY;
+  for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, part[s * (hd + 2) + hd]);
+  const float m_use = M == -INFINITY ? 0.f : M;
+  float l = 0.f;
+  for (int s = 0; s < a.nsplit; ++s)
+    l += part[s * (hd + 2) + hd + 1] * fast_exp2(part[s * (hd + 2) + hd] - m_use);
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+    float acc = 0.f;
+    for (int s = 0; s < a.nsplit; ++s)
+      acc += part[s * (hd + 2) + d] * fast_exp2(part[s * (hd + 2) + hd] - m_use);
+    a.o[(size_t)b * a.dim + (size_t)h * hd + d] = acc * inv;
+  }
+}
+
+// Any head dim: one workgroup per (sequence, head, chunk), one thread per key.
+__global__ void __launch_bounds__(256) decode_split_generic_kernel(const DecodeArgs a) {
+  extern __shared__ float sm[];  // p[256] | red[8]
+  float *pv = sm;
+  float *red = sm + 256;
+  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int t = threadIdx.x, hd = a.hd;
+  const int len = min(max(a.kv_len[b], 0), a.t_max);
+  const int chunk0 = split * DC_CHUNK;
+  float *part = a.part + ((size_t)(b * a.heads + h) * a.nsplit + split) * (hd + 2);
+  if (chunk0 >= len) {
+    for (int d = t; d < hd + 2; d += 256) part[d] = d == hd ? -INFINITY : 0.f;
+    return;
+  }
+  const float *qrow = a.q + (size_t)b * a.dim + (size_t)h * hd;
+  const size_t cache = (size_t)b * a.t_max * a.dim + (size_t)h * hd;
+  const int key = chunk0 + t;
+  float s = -INFINITY;
+  if (key < len) {
+    float acc = 0.f;
+    const float *kr = a.kc + cache + (size_t)key * a.dim;
+    for (int d = 0; d < hd; ++d) acc += qrow[d] * kr[d];
+    s = acc * a.scale_log2;
+  }
+  float mx = s;
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  if ((t & 63) == 0) red[t >> 6] = mx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float m_use = M == -INFINITY ? 0.f : M;
+  const float p = fast_exp2(s - m_use);
+  pv[t] = p;
+  float ps = p;
+  for (int off = 32; off > 0; off >>= 1) ps += __shfl_xor(ps, off);
+  if ((t & 63) == 0) red[4 + (t >> 6)] = ps;
+  __syncthreads();
+  const int n = min(DC_CHUNK, len - chunk0);
+  for (int d = t; d < hd; d += 256) {
+    float acc = 0.f;
+    for (int j = 0; j < n; ++j) acc += pv[j] * a.vc[cache + (size_t)(chunk0 + j) * a.dim + d];
+    part[d] = acc;
+  }
+  if (t == 0) {
+    part[hd] = M;
+    part[hd + 1] = red[4] + red[5] + red[6] + red[7];
+  }
+}
+
+bool fast_hd(int hd) { return hd == 16 || hd == 32 || hd == 64 || hd == 128 || hd == 256; }
+
+}  // namespace
+}  // namespace cdml
+
+using namespace cdml;
+
+extern "C" int cdml_decode_attn_workspace_size(int batch, int t_max, int dim, int num_heads,
+                                               size_t *bytes) {
+  if (!bytes) return fail(CDML_E_INVALID, "cdml_decode_attn_workspace_size: bytes is NULL");
+  if (batch < 0 || t_max < 0 || dim <= 0 || num_heads <= 0 || dim % num_heads)
+    return fail(CDML_E_INVALID, "cdml_decode_attn_workspace_size: bad size");
+  const int hd = dim / num_heads;
+  const int nsplit = (t_max + DC_CHUNK - 1) / DC_CHUNK;
+  *bytes = sizeof(float) * (size_t)batch * num_heads * (size_t)nsplit * (hd + 2);
+  return CDML_OK;
+}
+
+extern "C" int cdml_decode_attn(const float *q, const float *kcache, const float *vcache,
+                                const int *kv_len, float *o, int batch, int t_max, int dim,
+                                int num_heads, float scale, void *workspace,
+                                size_t workspace_bytes, cdml_stream stream) {
+  size_t need = 0;
+  int rc = cdml_decode_attn_workspace_size(batch, t_max, dim, num_heads, &need);
+  if (rc) return rc;
+  if (batch == 0) return CDML_OK;
+  if (t_max == 0) return cdml_zero_f32_async(o, (size_t)batch * dim, stream);
+  if (!q || !kcache || !vcache || !kv_len || !o)
+    return fail(CDML_E_INVALID, "cdml_decode_attn: NULL pointer");
+  if (!workspace || workspace_bytes < need)
+    return fail(CDML_E_INVALID, "cdml_decode_attn: workspace of %zu bytes needed, %zu given", need,
+                workspace_bytes);
+  if (batch > 65535 || num_heads > 65535)
+    return fail(CDML_E_INVALID, "cdml_decode_attn: batch and heads must be <= 65535");
+  rc = ensure_device();
+  if (rc) return rc;
+  DecodeArgs a{};
+  a.q = q;
+  a.kc = kcache;
+  a.vc = vcache;
+  a.kv_len = kv_len;
+  a.o = o;
+  a.part = static_cast<float *>(workspace);
+  a.t_max = t_max;
+  a.dim = dim;
+  a.heads = num_heads;
+  a.hd = dim / num_heads;
+  a.nsplit = (t_max + DC_CHUNK - 1) / DC_CHUNK;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  hipStream_t st = as_hip(stream);
+  dim3 grid(a.nsplit, num_heads, batch);
+  const bool vec = fast_hd(a.hd) && dim % 4 == 0 && aligned16(q) && aligned16(kcache) &&
+                   aligned16(vcache);
+  if (vec) {
+    switch (a.hd) {
+      case 16: decode_split_kernel<16><<<grid, DC_THREADS, 0, st>>>(a); break;
+      case 32: decode_split_kernel<32><<<grid, DC_THREADS, 0, st>>>(a); break;
+      case 64: decode_split_kernel<64><<<grid, DC_THREADS, 0, st>>>(a); break;
+      case 128: decode_split_kernel<128><<<grid, DC_THREADS, 0, st>>>(a); break;
+      default: decode_split_kernel<256><<<grid, DC_THREADS, 0, st>>>(a); break;
+    }
+  } else {
+    decode_split_generic_kernel<<<grid, 256, sizeof(float) * (256 + 8), st>>>(a);
+  }
+  rc = check_launch("decode_split_kernel");
+  if (rc) return rc;
+  decode_combine_kernel<<<dim3(num_heads, batch), dim3(a.hd < 256 ? 128 : 256), 0, st>>>(a);
+  return check_launch("decode_combine_kernel");
+}

@@ -1,0 +1,418 @@
+// Fused flash-style fp32 attention forward for gfx950 (ScaledDotProductAttention
+// and MultiHeadAttentionForward of the reference, AccelerationCPU.cs:1647-1956).
+//
+// One 256-thread workgroup owns 128 queries of one (sequence, head); each of
+// its four waves owns 32 queries for the whole key loop.  Per key tile of BN
+// keys (K and V staged through double-buffered LDS, next tile prefetched into
+// registers while the current one is consumed):
+//
+//   S^T = K Q^T     v_mfma_f32_32x32x2_f32, A = K rows from LDS (16-byte
+//                   reads), B = the wave's Q held in registers for the whole
+//                   loop.  Computing S transposed puts one query per lane
+//                   (lane % 32) and 16 keys per lane in the accumulator, so the
+//                   softmax row reductions are in-lane plus one swap between
+//                   the two half-waves.
+//   online softmax  running max / sum per query in the exp2 domain
+//                   (scale * log2 e folded into one FMA), masked keys -inf.
+//   O^T += V^T P^T  the probabilities stay in the S accumulator registers:
+//                   accumulator r of a lane holds key 8*(r/4) + 4*h + r%4,
+//                   exactly the key the B operand of MFMA step r needs, so
+//                   P is consumed in place; V^T comes from LDS (b32 reads).
+//
+// Causal: tiles entirely above the diagonal are never loaded; a wave skips
+// MFMA work for its 32-key sub-blocks that lie wholly in its future; heavy
+// query tiles are dispatched first.  A row whose keys are all masked ends
+// with sum 0 and is written as 0 (AccelerationCPU.cs:1908-1911).
+#include <cfloat>
+
+#include "common.h"
+
+namespace cdml {
+namespace {
+
+constexpr int FA_THREADS = 256;
+constexpr int FA_BM = 128;  // queries per workgroup (32 per wave)
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct FlashArgs {
+  const float *q, *k, *v;
+  float *o;
+  const uint8_t *mask;
+  int ldq, ldk, ldv, ldo;
+  int lq, lk, heads, hd;
+  float scale_log2;
+  int n_qt, total, padded;
+};
+
+// Stages one BN x HD tile of K or V (rows [k0, k0+BN) of head column block
+// `col0`) from global memory into registers and then into LDS.
+template <int HD, int BN, bool VEC>
+struct KvStage {
+  static constexpr int F4_ROW = HD / 4;
+  static constexpr int ROWS_PER_PASS = FA_THREADS / F4_ROW;
+  static constexpr int NV = BN / ROWS_PER_PASS;
+  static constexpr int NS = BN * HD / FA_THREADS;
+  float4 r[VEC ? NV : 1];
+  float s[VEC ? 1 : NS];
+
+  __device__ __forceinline__ void load(const float *__restrict__ base, int ld, int k0, int lk,
+                                       int hd) {
+    const int t = threadIdx.x;
+    if constexpr (VEC) {
+      const int c = (t % F4_ROW) * 4;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int row = t / F4_ROW + ROWS_PER_PASS * i;
+        const int key = k0 + row;
+        r[i] = key < lk ? *reinterpret_cast<const float4 *>(base + (size_t)key * ld + c)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        const int e = t + FA_THREADS * i;
+        const int row = e / HD, c = e % HD;
+        const int key = k0 + row;
+        s[i] = (key < lk && c < hd) ? base[(size_t)key * ld + c] : 0.f;
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(float (*lds)[HD + 4]) {
+    const int t = threadIdx.x;
+    if constexpr (VEC) {
+      const int c = (t % F4_ROW) * 4;
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        *reinterpret_cast<float4 *>(&lds[t / F4_ROW + ROWS_PER_PASS * i][c]) = r[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        const int e = t + FA_THREADS * i;
+        lds[e / HD][e % HD] = s[i];
+      }
+    }
+  }
+};
+
+template <int HD, int BN, bool CAUSAL, bool HAS_MASK, bool VEC>
+__global__ void __launch_bounds__(FA_THREADS) flash_fwd_kernel(const FlashArgs a) {
+  constexpr int NKB = BN / 32;  // 32-key sub-blocks per tile
+  constexpr int NDB = HD / 32;  // 32-wide head-dim blocks of O^T
+  constexpr int NQ = HD / 2;    // MFMA k-steps of Q.K
+  __shared__ __attribute__((aligned(16))) float Ks[2][BN][HD + 4];
+  __shared__ __attribute__((aligned(16))) float Vs[2][BN][HD + 4];
+
+  const int lid = xcd_remap(blockIdx.x, a.padded);
+  if (lid >= a.total) return;
+  const int bh = lid / a.n_qt;
+  int qt = lid % a.n_qt;
+  if (CAUSAL) qt = a.n_qt - 1 - qt;  // longest rows first
+  const int b = bh / a.heads, h = bh % a.heads;
+  const int q0 = qt * FA_BM;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = lane & 31, hf = lane >> 5;
+  const int qw0 = q0 + wave * 32;   // first query of this wave
+  const int qi = qw0 + li;          // this lane's query
+  const int col0 = h * a.hd;
+
+  const float *__restrict__ kbase = a.k + (size_t)b * a.lk * a.ldk + col0;
+  const float *__restrict__ vbase = a.v + (size_t)b * a.lk * a.ldv + col0;
+
+  // Q^T operand: register 4u + r holds q[qi][8u + 4*hf + r].
+  float qreg[NQ];
+  {
+    const float *qrow = a.q + ((size_t)b * a.lq + qi) * a.ldq + col0;
+    const bool qok = qi < a.lq;
+#pragma unroll
+    for (int u = 0; u < HD / 8; ++u) {
+      const int d = 8 * u + 4 * hf;
+      if constexpr (VEC) {
+        float4 t4 = qok ? *reinterpret_cast<const float4 *>(qrow + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+        qreg[4 * u + 0] = t4.x;
+        qreg[4 * u + 1] = t4.y;
+        qreg[4 * u + 2] = t4.z;
+        qreg[4 * u + 3] = t4.w;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) qreg[4 * u + r] = (qok && d + r < a.hd) ? qrow[d + r] : 0.f;
+      }
+    }
+  }
+
+  const int kend = CAUSAL ? min(q0 + FA_BM, a.lk) : a.lk;
+  const int n_kt = (kend + BN - 1) / BN;
+
+  KvStage<HD, BN, VEC> sk, sv;
+  sk.load(kbase, a.ldk, 0, a.lk, a.hd);
+  sv.load(vbase, a.ldv, 0, a.lk, a.hd);
+  sk.store(Ks[0]);
+  sv.store(Vs[0]);
+  __syncthreads();
+
+  floatx16 oacc[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
+  float m_i = -INFINITY;  // running max (exp2 domain) for query qi
+  float l_i = 0.f;        // running sum over this half-wave's keys
+
+  const uint8_t *mrow = HAS_MASK ? a.mask + (size_t)min(qi, a.lq - 1) * a.lk : nullptr;
+
+  for (int kt = 0; kt < n_kt; ++kt) {
+    const int cur = kt & 1;
+    const int k0 = kt * BN;
+    const bool more = kt + 1 < n_kt;
+    if (more) {
+      sk.load(kbase, a.ldk, k0 + BN, a.lk, a.hd);
+      sv.load(vbase, a.ldv, k0 + BN, a.lk, a.hd);
+    }
+
+    floatx16 sacc[NKB];
+    bool active[NKB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const int kb0 = k0 + kb * 32;
+      active[kb] = kb0 < a.lk && (!CAUSAL || kb0 <= qw0 + 31);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+      if (active[kb]) {
+#pragma unroll
+        for (int u = 0; u < HD / 8; ++u) {
+          const float4 k4 = *reinterpret_cast<const float4 *>(&Ks[cur][kb * 32 + li][8 * u + 4 * hf]);
+          sacc[kb] = mfma32x32x2(k4.x, qreg[4 * u + 0], sacc[kb]);
+          sacc[kb] = mfma32x32x2(k4.y, qreg[4 * u + 1], sacc[kb]);
+          sacc[kb] = mfma32x32x2(k4.z, qreg[4 * u + 2], sacc[kb]);
+          sacc[kb] = mfma32x32x2(k4.w, qreg[4 * u + 3], sacc[kb]);
+        }
+      }
+    }
+
+    // Scale into the exp2 domain and mask.
+    const bool edge = HAS_MASK || (k0 + BN > a.lk) || (CAUSAL && k0 + BN - 1 > qw0);
+    float rmax = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float t = sacc[kb][r] * a.scale_log2;
+        if (edge) {
+          const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
+          bool ok = active[kb] && key < a.lk;
+          if (CAUSAL) ok = ok && key <= qi;
+          if (HAS_MASK) ok = ok && qi < a.lq && mrow[key] != 0;
+          t = ok ? t : -INFINITY;
+        }
+        sacc[kb][r] = t;
+        rmax = fmaxf(rmax, t);
+      }
+    }
+    rmax = fmaxf(rmax, __shfl_xor(rmax, 32));
+    const float m_new = fmaxf(m_i, rmax);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = fast_exp2(m_i - m_use);
+    float rsum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(sacc[kb][r] - m_use);
+        sacc[kb][r] = p;
+        rsum += p;
+      }
+    l_i = l_i * alpha + rsum;
+    m_i = m_new;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      if (!active[kb]) continue;
+#pragma unroll
+      for (int s = 0; s < 16; ++s) {
+        const int krow = kb * 32 + 8 * (s >> 2) + 4 * hf + (s & 3);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+          oacc[db] = mfma32x32x2(Vs[cur][krow][db * 32 + li], sacc[kb][s], oacc[db]);
+      }
+    }
+
+    if (more) {
+      sk.store(Ks[cur ^ 1]);
+      sv.store(Vs[cur ^ 1]);
+    }
+    __syncthreads();
+  }
+
+  // Normalise and store: lane holds query qi, dims db*32 + 8*(r/4) + 4*hf + r%4.
+  const float l_tot = l_i + __shfl_xor(l_i, 32);
+  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  if (qi < a.lq) {
+    float *orow = a.o + ((size_t)b * a.lq + qi) * a.ldo + col0;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = db * 32 + 8 * g + 4 * hf;
+        if constexpr (VEC) {
+          *reinterpret_cast<float4 *>(orow + d) =
+              make_float4(oacc[db][4 * g] * inv, oacc[db][4 * g + 1] * inv,
+                          oacc[db][4 * g + 2] * inv, oacc[db][4 * g + 3] * inv);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (d + r < a.hd) orow[d + r] = oacc[db][4 * g + r] * inv;
+        }
+      }
+    }
+  }
+}
+
+// Head dims above 128: one workgroup per (sequence, head, query), keys in
+// chunks of 256 with an online softmax; correctness path only.
+__global__ void __launch_bounds__(256) flash_generic_kernel(const FlashArgs a, int causal) {
+  extern __shared__ float sm[];  // q[hd] | o[hd] | p[256] | red[8]
+  float *qv = sm;
+  float *ov = sm + a.hd;
+  float *pv = ov + a.hd;
+  float *red = pv + 256;
+  const int row = blockIdx.x;  // b * lq + i
+  const int b = row / a.lq, i = row % a.lq;
+  const int h = blockIdx.y;
+  const int col0 = h * a.hd;
+  const int t = threadIdx.x;
+  const float *qrow = a.q + ((size_t)b * a.lq + i) * a.ldq + col0;
+  for (int d = t; d < a.hd; d += 256) {
+    qv[d] = qrow[d];
+    ov[d] = 0.f;
+  }
+  __syncthreads();
+  const int usable = causal ? min(i + 1, a.lk) : a.lk;
+  float m_run = -INFINITY, l_run = 0.f;
+  for (int c0 = 0; c0 < usable; c0 += 256) {
+    const int j = c0 + t;
+    float s = -INFINITY;
+    if (j < usable && (!a.mask || a.mask[(size_t)i * a.lk + j])) {
+      const float *krow = a.k + ((size_t)b * a.lk + j) * a.ldk + col0;
+      float acc = 0.f;
+      for (int d = 0; d < a.hd; ++d) acc += qv[d] * krow[d];
+      s = acc * a.scale_log2;
+    }
+    float mx = s;
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if ((t & 63) == 0) red[t >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = fast_exp2(m_run - m_use);
+    const float p = fast_exp2(s - m_use);
+    pv[t] = p;
+    float ps = p;
+    for (int off = 32; off > 0; off >>= 1) ps += __shfl_xor(ps, off);
+    if ((t & 63) == 0) red[4 + (t >> 6)] = ps;
+    __syncthreads();
+    l_run = l_run * alpha + (red[4] + red[5] + red[6] + red[7]);
+    m_run = m_new;
+    const int n = min(256, usable - c0);
+    for (int d = t; d < a.hd; d += 256) {
+      float acc = ov[d] * alpha;
+      for (int jj = 0; jj < n; ++jj)
+        acc += pv[jj] * a.v[((size_t)b * a.lk + c0 + jj) * a.ldv + col0 + d];
+      ov[d] = acc;
+    }
+    __syncthreads();
+  }
+  const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
+  float *orow = a.o + ((size_t)b * a.lq + i) * a.ldo + col0;
+  for (int d = t; d < a.hd; d += 256) orow[d] = ov[d] * inv;
+}
+
+template <int HD, int BN, bool CAUSAL, bool HAS_MASK>
+void launch_tpl(const FlashArgs &a, bool vec, hipStream_t st) {
+  if (vec)
+    flash_fwd_kernel<HD, BN, CAUSAL, HAS_MASK, true><<<dim3(a.padded), dim3(FA_THREADS), 0, st>>>(a);
+  else
+    flash_fwd_kernel<HD, BN, CAUSAL, HAS_MASK, false><<<dim3(a.padded), dim3(FA_THREADS), 0, st>>>(a);
+}
+
+template <int HD, int BN>
+void launch_hd(const FlashArgs &a, bool causal, bool vec, hipStream_t st) {
+  const bool m = a.mask != nullptr;
+  if (causal) {
+    if (m) launch_tpl<HD, BN, true, true>(a, vec, st);
+    else launch_tpl<HD, BN, true, false>(a, vec, st);
+  } else {
+    if (m) launch_tpl<HD, BN, false, true>(a, vec, st);
+    else launch_tpl<HD, BN, false, false>(a, vec, st);
+  }
+}
+
+}  // namespace
+}  // namespace cdml
+
+using namespace cdml;
+
+extern "C" int cdml_sdpa_fwd(const float *q, int ldq, const float *k, int ldk, const float *v,
+                             int ldv, float *o, int ldo, int batch, int lq, int lk, int dim,
+                             int num_heads, float scale, int causal, const uint8_t *mask,
+                             cdml_stream stream) {
+  if (batch < 0 || lq < 0 || lk < 0 || dim <= 0 || num_heads <= 0)
+    return fail(CDML_E_INVALID, "cdml_sdpa_fwd: bad size (batch %d, lq %d, lk %d, dim %d, heads %d)",
+                batch, lq, lk, dim, num_heads);
+  if (dim % num_heads != 0)
+    return fail(CDML_E_INVALID, "cdml_sdpa_fwd: dim %d not divisible by num_heads %d", dim, num_heads);
+  if (causal && lq != lk)
+    return fail(CDML_E_CAUSAL, "cdml_sdpa_fwd: causal attention requires lq == lk (got %d, %d)", lq, lk);
+  if (ldq < dim || ldk < dim || ldv < dim || ldo < dim)
+    return fail(CDML_E_INVALID, "cdml_sdpa_fwd: row stride smaller than dim");
+  if (batch == 0 || lq == 0) return CDML_OK;
+  if (lk == 0) return fail(CDML_E_INVALID, "cdml_sdpa_fwd: lk must be >= 1");
+  if (!q || !k || !v || !o) return fail(CDML_E_INVALID, "cdml_sdpa_fwd: NULL pointer");
+  int rc = ensure_device();
+  if (rc) return rc;
+
+  FlashArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.mask = mask;
+  a.ldq = ldq;
+  a.ldk = ldk;
+  a.ldv = ldv;
+  a.ldo = ldo;
+  a.lq = lq;
+  a.lk = lk;
+  a.heads = num_heads;
+  a.hd = dim / num_heads;
+  a.scale_log2 = scale * kLog2e;
+  hipStream_t st = as_hip(stream);
+
+  const int hd = a.hd;
+  if (hd > 128) {
+    a.n_qt = lq;
+    size_t smem = sizeof(float) * (2 * (size_t)hd + 256 + 8);
+    if (smem > 160 * 1024) return fail(CDML_E_INVALID, "cdml_sdpa_fwd: head dim %d too large", hd);
+    flash_generic_kernel<<<dim3(batch * lq, num_heads), dim3(256), smem, st>>>(a, causal);
+    return check_launch("flash_generic_kernel");
+  }
+  const int hd_pad = hd <= 32 ? 32 : (hd <= 64 ? 64 : 128);
+  const bool vec = hd == hd_pad && ldq % 4 == 0 && ldk % 4 == 0 && ldv % 4 == 0 && ldo % 4 == 0 &&
+                   aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
+  a.n_qt = (lq + FA_BM - 1) / FA_BM;
+  long long total = (long long)batch * num_heads * a.n_qt;
+  if (total > (1LL << 30)) return fail(CDML_E_INVALID, "cdml_sdpa_fwd: problem too large");
+  a.total = (int)total;
+  a.padded = pad_to_xcd(a.total);
+  if (hd_pad == 32) launch_hd<32, 64>(a, causal, vec, st);
+  else if (hd_pad == 64) launch_hd<64, 64>(a, causal, vec, st);
+  else launch_hd<128, 32>(a, causal, vec, st);
+  return check_launch("flash_fwd_kernel");
+}

@@ -1,0 +1,274 @@
+// fp32 MFMA GEMM for the projections of the attention path:
+//   C[m, n] = act(sum_k A[m, k] * W[n, k] + bias[n])
+// A is the activation [M, K] (row stride lda), W the weight [N, K] ([out, in],
+// the reference's layout), C the output [M, N] (row stride ldc).  Up to three
+// problems that share A (the fused Q/K/V projection) run in one launch.
+//
+// Tiling for gfx950: a 256-thread workgroup computes a 128x128 tile of C; each
+// of its four waves owns a 64x64 quadrant as 2x2 blocks of
+// v_mfma_f32_32x32x2_f32.  K advances in steps of 32 through double-buffered
+// LDS tiles (row stride 36 floats); every lane fetches its A and B operands as
+// 16-byte LDS reads that feed four MFMAs each.  The reduction index k is
+// visited in the permuted order kappa(s, h) = 8*(s/4) + 4*h + s%4 on both
+// operands, which leaves the sum unchanged.
+#include "common.h"
+
+namespace cdml {
+namespace {
+
+constexpr int BM = 128, BN = 128, BK = 32, LDSK = BK + 4;
+constexpr int NTHREADS = 256;
+constexpr int GROUP_M = 8;
+
+struct GemmProblem {
+  const float *w;
+  const float *bias;
+  float *c;
+};
+
+struct GemmArgs {
+  const float *a;
+  GemmProblem p[3];
+  int lda, ldc;
+  int M, N, K;
+  int nprob;
+  int tiles_m, tiles_n;  // tiles_n counts the tiles of one problem
+  int total, padded;
+  int act;
+};
+
+__device__ __forceinline__ float activate(float x, int act) {
+  switch (act) {
+    case CDML_ACT_SIGMOID:
+      return x >= 0.f ? 1.f / (1.f + expf(-x)) : expf(x) / (1.f + expf(x));
+    case CDML_ACT_TANH:
+      return tanhf(x);
+    case CDML_ACT_RELU:
+      return x > 0.f ? x : 0.f;
+    case CDML_ACT_LEAKYRELU:
+      return x > 0.f ? x : 0.01f * x;
+    case CDML_ACT_SWISH: {
+      float s = x >= 0.f ? 1.f / (1.f + expf(-x)) : expf(x) / (1.f + expf(x));
+      return x * s;
+    }
+    default:
+      return x;
+  }
+}
+
+// Global -> register staging of one 128x32 tile of a row-major [rows, K]
+// matrix.  VEC: K % 4 == 0 and 16-byte aligned rows, four float4 per thread;
+// otherwise sixteen guarded scalars per thread.
+template <bool VEC>
+struct TileStage {
+  float4 r[4];
+  float s[16];
+
+  __device__ __forceinline__ void load(const float *__restrict__ src, int ld, int row0, int rows,
+                                       int k0, int K) {
+    const int t = threadIdx.x;
+    if constexpr (VEC) {
+      const int c = (t & 7) * 4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = row0 + (t >> 3) + 32 * i;
+        if (row < rows && k0 + c < K)
+          r[i] = *reinterpret_cast<const float4 *>(src + (size_t)row * ld + k0 + c);
+        else
+          r[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    } else {
+      const int c = t & 31;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = row0 + (t >> 5) + 8 * i;
+        s[i] = (row < rows && k0 + c < K) ? src[(size_t)row * ld + k0 + c] : 0.f;
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(float (*lds)[LDSK]) {
+    const int t = threadIdx.x;
+    if constexpr (VEC) {
+      const int c = (t & 7) * 4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<float4 *>(&lds[(t >> 3) + 32 * i][c]) = r[i];
+    } else {
+      const int c = t & 31;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) lds[(t >> 5) + 8 * i][c] = s[i];
+    }
+  }
+};
+
+template <bool VEC>
+__global__ void __launch_bounds__(NTHREADS) gemm_nt_kernel(const GemmArgs args) {
+  __shared__ __attribute__((aligned(16))) float As[2][BM][LDSK];
+  __shared__ __attribute__((aligned(16))) float Bs[2][BN][LDSK];
+
+  const int lid = xcd_remap(blockIdx.x, args.padded);
+  if (lid >= args.total) return;
+
+  // Grouped ordering over (tiles_m, nprob * tiles_n): GROUP_M tile-rows share
+  // each weight panel while it is hot in L2.
+  const int tiles_n_all = args.tiles_n * args.nprob;
+  const int in_group = GROUP_M * tiles_n_all;
+  const int group = lid / in_group;
+  const int first_m = group * GROUP_M;
+  const int gsize = min(args.tiles_m - first_m, GROUP_M);
+  const int tm = first_m + (lid % in_group) % gsize;
+  const int tn_all = (lid % in_group) / gsize;
+  const int prob = tn_all / args.tiles_n;
+  const int tn = tn_all % args.tiles_n;
+
+  const GemmProblem P = args.p[prob];
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int M = args.M, N = args.N, K = args.K;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int li = lane & 31, hf = lane >> 5;
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  TileStage<VEC> sa, sb;
+  const int nk = (K + BK - 1) / BK;
+  sa.load(args.a, args.lda, m0, M, 0, K);
+  sb.load(P.w, K, n0, N, 0, K);
+  sa.store(As[0]);
+  sb.store(Bs[0]);
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < nk;
+    if (more) {
+      sa.load(args.a, args.lda, m0, M, (kt + 1) * BK, K);
+      sb.load(P.w, K, n0, N, (kt + 1) * BK, K);
+    }
+#pragma unroll
+    for (int u = 0; u < BK / 8; ++u) {
+      float4 a4[2], b4[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        a4[i] = *reinterpret_cast<const float4 *>(&As[cur][wm * 64 + i * 32 + li][u * 8 + hf * 4]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        b4[j] = *reinterpret_cast<const float4 *>(&Bs[cur][wn * 64 + j * 32 + li][u * 8 + hf * 4]);
+      const float av[2][4] = {{a4[0].x, a4[0].y, a4[0].z, a4[0].w},
+                              {a4[1].x, a4[1].y, a4[1].z, a4[1].w}};
+      const float bv[2][4] = {{b4[0].x, b4[0].y, b4[0].z, b4[0].w},
+                              {b4[1].x, b4[1].y, b4[1].z, b4[1].w}};
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x2(av[i][r], bv[j][r], acc[i][j]);
+    }
+    if (more) {
+      sa.store(As[cur ^ 1]);
+      sb.store(Bs[cur ^ 1]);
+    }
+    __syncthreads();
+  }
+
+  // Epilogue: D[i][j] of block (bi, bj) sits at row 8*(r/4) + 4*hf + r%4,
+  // column li; 32 lanes store 32 consecutive columns of one row.
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = n0 + wn * 64 + j * 32 + li;
+    if (n >= N) continue;
+    const float bias = P.bias ? P.bias[n] : 0.f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
+        if (m < M) P.c[(size_t)m * args.ldc + n] = activate(acc[i][j][r] + bias, args.act);
+      }
+    }
+  }
+}
+
+int launch_gemm(GemmArgs &g, hipStream_t stream, const char *what) {
+  if (g.M == 0 || g.N == 0) return CDML_OK;
+  g.tiles_m = (g.M + BM - 1) / BM;
+  g.tiles_n = (g.N + BN - 1) / BN;
+  g.total = g.tiles_m * g.tiles_n * g.nprob;
+  g.padded = pad_to_xcd(g.total);
+  bool vec = (g.K % 4 == 0) && (g.lda % 4 == 0) && aligned16(g.a);
+  for (int i = 0; i < g.nprob; ++i) vec = vec && aligned16(g.p[i].w);
+  if (vec)
+    gemm_nt_kernel<true><<<dim3(g.padded), dim3(NTHREADS), 0, stream>>>(g);
+  else
+    gemm_nt_kernel<false><<<dim3(g.padded), dim3(NTHREADS), 0, stream>>>(g);
+  return check_launch(what);
+}
+
+}  // namespace
+}  // namespace cdml
+
+using namespace cdml;
+
+extern "C" int cdml_project_qkv(const float *x, const float *wq, const float *bq, const float *wk,
+                                const float *bk, const float *wv, const float *bv, float *q,
+                                float *k, float *v, int rows, int in_dim, int out_dim,
+                                cdml_stream stream) {
+  if (rows < 0 || in_dim < 0 || out_dim < 0)
+    return fail(CDML_E_INVALID, "cdml_project_qkv: negative size");
+  if (rows == 0 || out_dim == 0) return CDML_OK;
+  if (!x || !wq || !wk || !wv || !q || !k || !v)
+    return fail(CDML_E_INVALID, "cdml_project_qkv: NULL pointer");
+  int rc = ensure_device();
+  if (rc) return rc;
+  if (in_dim == 0) {
+    // y = bias only; a K of zero leaves the accumulators at 0.
+  }
+  GemmArgs g{};
+  g.a = x;
+  g.lda = in_dim;
+  g.ldc = out_dim;
+  g.M = rows;
+  g.N = out_dim;
+  g.K = in_dim;
+  g.nprob = 3;
+  g.p[0] = {wq, bq, q};
+  g.p[1] = {wk, bk, k};
+  g.p[2] = {wv, bv, v};
+  g.act = CDML_ACT_NONE;
+  return launch_gemm(g, as_hip(stream), "cdml_project_qkv");
+}
+
+extern "C" int cdml_linear(const float *x, int ldx, const float *w, const float *b, float *y,
+                           int ldy, int rows, int in_dim, int out_dim, int activation,
+                           cdml_stream stream) {
+  if (rows < 0 || in_dim < 0 || out_dim < 0)
+    return fail(CDML_E_INVALID, "cdml_linear: negative size");
+  if (activation < CDML_ACT_NONE || activation > CDML_ACT_SWISH)
+    return fail(CDML_E_INVALID, "cdml_linear: unknown activation %d", activation);
+  if (rows == 0 || out_dim == 0) return CDML_OK;
+  if (!x || !w || !y) return fail(CDML_E_INVALID, "cdml_linear: NULL pointer");
+  if (ldx < in_dim || ldy < out_dim)
+    return fail(CDML_E_INVALID, "cdml_linear: row stride smaller than the row");
+  int rc = ensure_device();
+  if (rc) return rc;
+  GemmArgs g{};
+  g.a = x;
+  g.lda = ldx;
+  g.ldc = ldy;
+  g.M = rows;
+  g.N = out_dim;
+  g.K = in_dim;
+  g.nprob = 1;
+  g.p[0] = {w, b, y};
+  g.act = activation;
+  return launch_gemm(g, as_hip(stream), "cdml_linear");
+}

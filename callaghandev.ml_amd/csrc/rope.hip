@@ -1,0 +1,88 @@
+// Interleaved-pair rotary position embedding, in place
+// (AccelerationCPU.cs:4929-4980, LanguageModel.cs:432-480,
+// TransformerTrainer.cs:811-848).
+//
+// The per-pair denominators powf(base, 2p / head_dim) are computed on the host
+// with the same float expression as the reference and passed by value, so
+// every device thread forms theta = pos / denom[p] from bit-identical
+// operands (the rotation angle reaches thousands of radians at long
+// positions, where a one-ulp difference in denom would show in sin/cos).
+#include <cmath>
+
+#include "common.h"
+
+namespace cdml {
+namespace {
+
+constexpr int kMaxPairs = 256;
+
+struct RopeArgs {
+  float *x;
+  const int *positions;
+  int rows, ld, start_col, head_dim, num_heads, pairs;
+  int inverse, pos_offset, seg_len;
+  float denom[kMaxPairs];
+};
+
+__global__ void __launch_bounds__(256) rope_kernel(const RopeArgs a) {
+  const long long total = (long long)a.rows * a.num_heads * a.pairs;
+  for (long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (long long)gridDim.x * blockDim.x) {
+    const int p = (int)(idx % a.pairs);
+    const long long rh = idx / a.pairs;
+    const int head = (int)(rh % a.num_heads);
+    const int row = (int)(rh / a.num_heads);
+    int pos;
+    if (a.positions) pos = a.positions[row];
+    else pos = a.pos_offset + (a.seg_len > 0 ? row % a.seg_len : row);
+    const float theta = (float)pos / a.denom[p];
+    float s, c;
+    sincosf(theta, &s, &c);
+    if (a.inverse) s = -s;
+    float *px = a.x + (size_t)row * a.ld + a.start_col + head * a.head_dim + 2 * p;
+    const float x0 = px[0], x1 = px[1];
+    px[0] = x0 * c - x1 * s;
+    px[1] = x0 * s + x1 * c;
+  }
+}
+
+}  // namespace
+}  // namespace cdml
+
+using namespace cdml;
+
+extern "C" int cdml_rope(float *x, int rows, int ld, int start_col, int head_dim, int num_heads,
+                         float base_theta, int inverse, int pos_offset, int seg_len,
+                         const int *positions, cdml_stream stream) {
+  if (rows < 0 || start_col < 0 || head_dim < 0 || num_heads <= 0 || seg_len < 0)
+    return fail(CDML_E_INVALID, "cdml_rope: bad size");
+  if (head_dim & 1) return fail(CDML_E_INVALID, "cdml_rope: RoPE requires an even head dimension");
+  if (!(base_theta > 0.f) || std::isinf(base_theta))
+    return fail(CDML_E_INVALID, "cdml_rope: base_theta must be positive and finite");
+  if (head_dim / 2 > kMaxPairs) return fail(CDML_E_INVALID, "cdml_rope: head_dim above %d", 2 * kMaxPairs);
+  if ((long long)start_col + (long long)head_dim * num_heads > ld)
+    return fail(CDML_E_INVALID, "cdml_rope: heads exceed the row");
+  if (rows == 0 || head_dim == 0) return CDML_OK;
+  if (!x) return fail(CDML_E_INVALID, "cdml_rope: x is NULL");
+  int rc = ensure_device();
+  if (rc) return rc;
+  RopeArgs a{};
+  a.x = x;
+  a.positions = positions;
+  a.rows = rows;
+  a.ld = ld;
+  a.start_col = start_col;
+  a.head_dim = head_dim;
+  a.num_heads = num_heads;
+  a.pairs = head_dim / 2;
+  a.inverse = inverse ? 1 : 0;
+  a.pos_offset = pos_offset;
+  a.seg_len = seg_len;
+  for (int p = 0; p < a.pairs; ++p)
+    a.denom[p] = powf(base_theta, (2.0f * (float)p) / (float)head_dim);
+  long long total = (long long)rows * num_heads * a.pairs;
+  long long blocks = (total + 255) / 256;
+  if (blocks > 16384) blocks = 16384;
+  rope_kernel<<<dim3((unsigned)blocks), dim3(256), 0, as_hip(stream)>>>(a);
+  return check_launch("rope_kernel");
+}

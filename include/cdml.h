@@ -1,0 +1,195 @@
+/*
+ * cdml.h -- C ABI of libcdml_hip.so, the MI355X (gfx950) implementation of
+ * CallaghanDev.ML's causal multi-head attention forward path.
+ *
+ * The library is the native half of a HIP-backed IAccelerationManager: the
+ * host side (a C# manager via P/Invoke, or the C++ HipAccelerationManager in
+ * callaghandev.ml_amd/host/) owns every device buffer, stream and pinned
+ * staging buffer and passes plain pointers and sizes here.  The library
+ * never frees a caller buffer and never allocates device memory inside a
+ * kernel entry point.
+ *
+ * Conventions
+ *   - Matrices are row-major float32 (C# float[,] layout).  A matrix
+ *     argument is (pointer, rows, cols, ld) with ld >= cols the row stride
+ *     in elements.  Weights are [out, in]; y = x W^T + b.
+ *   - Head h of a [rows, D] activation owns columns [h*d_h, (h+1)*d_h).
+ *   - Masks are uint8 [Lq, Lk], 1 = attend (bool[,] true = attend).
+ *   - Kernel entry points only enqueue work on `stream` (NULL = the null
+ *     stream) and return; only *_synchronize and cdml_event_elapsed_ms block.
+ *   - Every function returns a status; CDML_OK is 0.  On failure
+ *     cdml_last_error() returns a message for the calling thread.
+ *   - Calls on distinct streams from distinct threads are safe.  One stream
+ *     is not re-entrant.
+ *
+ * Reference paths below are relative to CallaghanDev.ML/ in the reference
+ * repository.
+ */
+#ifndef CDML_H
+#define CDML_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CDML_OK 0
+#define CDML_E_INVALID (-1)  /* bad shape, null pointer, bad option         */
+#define CDML_E_NODEVICE (-2) /* no usable HIP device                        */
+#define CDML_E_HIP (-3)      /* a HIP runtime call failed (text in message) */
+#define CDML_E_CAUSAL (-4)   /* causal attention with Lq != Lk              */
+
+/* FFN activations, numbered as Enums/ActivationType.cs:7-15. */
+#define CDML_ACT_NONE 0
+#define CDML_ACT_SIGMOID 1
+#define CDML_ACT_TANH 2
+#define CDML_ACT_RELU 3
+#define CDML_ACT_LEAKYRELU 4
+#define CDML_ACT_SWISH 5
+
+typedef struct cdml_stream_opaque *cdml_stream; /* a hipStream_t */
+typedef struct cdml_event_opaque *cdml_event;   /* a hipEvent_t  */
+
+typedef struct cdml_device_info {
+  char name[128];
+  char arch[64];         /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+  int compute_units;
+  int max_clock_mhz;     /* shader clock used for the fp32 MFMA roofline */
+  int memory_clock_mhz;
+  int memory_bus_bits;
+  size_t total_memory;
+  size_t lds_per_workgroup;
+} cdml_device_info;
+
+/* ---- device, errors ----------------------------------------------------
+ * Replaces the device set-up of AccelerationManagers/GPU/AccelerationGPU.cs:85-147
+ * (ILGPU Context/Accelerator creation).  The device is process-wide; a
+ * manager instance only owns streams and buffers. */
+int cdml_device_count(int *count);
+int cdml_init(int device);
+int cdml_device_info_get(int device, cdml_device_info *info);
+const char *cdml_last_error(void);
+const char *cdml_version(void);
+
+/* ---- streams and events (owned by the caller) ------------------------- */
+int cdml_stream_create(cdml_stream *stream);
+int cdml_stream_destroy(cdml_stream stream);
+int cdml_stream_synchronize(cdml_stream stream);
+int cdml_event_create(cdml_event *event);
+int cdml_event_destroy(cdml_event event);
+int cdml_event_record(cdml_event event, cdml_stream stream);
+/* Waits for `stop`, then returns the time between the two events. */
+int cdml_event_elapsed_ms(cdml_event start, cdml_event stop, float *ms);
+
+/* ---- memory (owned by the caller) --------------------------------------
+ * Replace the per-call Allocate1D/CopyFromCPU/CopyToCPU/Dispose pattern of
+ * AccelerationManagers/GPU/TransformerCore.cs:1300-1348. */
+int cdml_malloc(void **ptr, size_t bytes);
+int cdml_free(void *ptr);
+int cdml_host_alloc_pinned(void **ptr, size_t bytes);
+int cdml_host_free_pinned(void *ptr);
+int cdml_memcpy_h2d_async(void *dst, const void *src, size_t bytes, cdml_stream stream);
+int cdml_memcpy_d2h_async(void *dst, const void *src, size_t bytes, cdml_stream stream);
+int cdml_memcpy_d2d_async(void *dst, const void *src, size_t bytes, cdml_stream stream);
+/* Zero `count` floats with a fill kernel (safe under stream capture). */
+int cdml_zero_f32_async(float *dst, size_t count, cdml_stream stream);
+
+/* ---- hot-path kernels (device pointers) -------------------------------- */
+
+/* IAccelerationManager.ProjectQKV (IAccelerationManager.cs:169), replacing
+ * AccelerationCPU.cs:2005-2069 / AccelerationMutliThreadCPU.cs:798-831 /
+ * GPU/TransformerCore.cs:1386-1464,1629-1665:
+ *   q = x wq^T + bq,  k = x wk^T + bk,  v = x wv^T + bv
+ * x [rows, in_dim]; w* [out_dim, in_dim]; b* [out_dim] (NULL = zero bias);
+ * q, k, v [rows, out_dim], contiguous.  One launch, fp32 MFMA. */
+int cdml_project_qkv(const float *x, const float *wq, const float *bq,
+                     const float *wk, const float *bk, const float *wv,
+                     const float *bv, float *q, float *k, float *v, int rows,
+                     int in_dim, int out_dim, cdml_stream stream);
+
+/* IAccelerationManager.ProjectOutputBatch (IAccelerationManager.cs:259) and
+ * BatchDotProductAddBias (:45-50) followed by ApplyActivationInPlace
+ * (Neural Network/NeuralNetwork.cs:670-702), replacing
+ * AccelerationCPU.cs:2694-2715 and :342-404:
+ *   y = act(x w^T + b)
+ * x [rows, in_dim] with row stride ldx; w [out_dim, in_dim]; b [out_dim] or
+ * NULL; y [rows, out_dim] with row stride ldy; activation CDML_ACT_*. */
+int cdml_linear(const float *x, int ldx, const float *w, const float *b,
+                float *y, int ldy, int rows, int in_dim, int out_dim,
+                int activation, cdml_stream stream);
+
+/* IAccelerationManager.ApplyRotaryPositionEmbeddingInPlace (:320) and
+ * ApplyRotaryPositionEmbeddingHeadInPlace (:319), replacing
+ * AccelerationCPU.cs:4855-4980 and GPU/RotaryPositionEmbeddings.cs:58-156.
+ * In place on x [rows, ld]: heads h = 0..num_heads-1 of width head_dim start
+ * at column start_col + h*head_dim; pairs (2p, 2p+1) rotate by
+ * theta = pos / powf(base_theta, 2p / head_dim) (sin negated when inverse).
+ * Position of row r: positions[r] when `positions` (device int32[rows]) is
+ * non-NULL, else pos_offset + (seg_len > 0 ? r % seg_len : r); seg_len is the
+ * segmented trainer's per-sequence length (TransformerTrainer.cs:811-848),
+ * positions the decode step's absolute position (LanguageModel.cs:432-480).
+ * head_dim must be even and <= 512. */
+int cdml_rope(float *x, int rows, int ld, int start_col, int head_dim,
+              int num_heads, float base_theta, int inverse, int pos_offset,
+              int seg_len, const int *positions, cdml_stream stream);
+
+/* IAccelerationManager.ScaledDotProductAttention (:167) and
+ * MultiHeadAttentionForward (:155), replacing AccelerationCPU.cs:1797-1956
+ * and :1647-1792 and GPU/TransformerCore.cs:659-834,1142-1349.
+ * Fused flash-style forward over `batch` independent sequences:
+ *   q [batch, lq, ldq], k [batch, lk, ldk], v [batch, lk, ldv],
+ *   o [batch, lq, ldo]; dim = num_heads * head_dim columns are used.
+ * For each sequence, head and query i: keys j < (causal ? i+1 : lk) with
+ * mask[i*lk + j] != 0 (mask NULL = all) get weight softmax(q.k * scale);
+ * a row with no such key is written as 0.  ScaledDotProductAttention passes
+ * scale = 1/sqrtf(head_dim) (AccelerationCPU.cs:1865).  causal requires
+ * lq == lk (CDML_E_CAUSAL otherwise, AccelerationCPU.cs:1859-1862). */
+int cdml_sdpa_fwd(const float *q, int ldq, const float *k, int ldk,
+                  const float *v, int ldv, float *o, int ldo, int batch,
+                  int lq, int lk, int dim, int num_heads, float scale,
+                  int causal, const uint8_t *mask, cdml_stream stream);
+
+/* Single-query decode attention over a cached K/V, the device form of the
+ * inline loop in LanguageModel.DecoderSelfAttentionStep
+ * (Transformers/MultiTypeTransformer/LanguageModel.cs:365-427), which has no
+ * IAccelerationManager slot in the reference.
+ *   q [batch, dim]; kcache, vcache [batch, t_max, dim]; kv_len device
+ *   int32[batch] (keys [0, kv_len[b]) are attended, 0 <= kv_len <= t_max);
+ *   o [batch, dim].
+ * Split-K over the cache with a combine pass; `workspace` is caller-owned
+ * device memory of at least cdml_decode_attn_workspace_size() bytes. */
+int cdml_decode_attn_workspace_size(int batch, int t_max, int dim,
+                                    int num_heads, size_t *bytes);
+int cdml_decode_attn(const float *q, const float *kcache, const float *vcache,
+                     const int *kv_len, float *o, int batch, int t_max,
+                     int dim, int num_heads, float scale, void *workspace,
+                     size_t workspace_bytes, cdml_stream stream);
+
+/* Appends one K row and one V row per sequence to the decode cache, as
+ * LanguageModel.cs:356-363 does: kcache[b, positions[b], :] = k_new[b, :]
+ * (same for V).  positions is device int32[batch], each in [0, t_max). */
+int cdml_kv_cache_append(const float *k_new, const float *v_new,
+                         float *kcache, float *vcache, const int *positions,
+                         int batch, int t_max, int dim, cdml_stream stream);
+
+/* IAccelerationManager.ResidualLayerNorm (:132), replacing
+ * AccelerationCPU.cs:1376-1438: y = gamma * (s - mean) / sqrt(var + eps) + beta
+ * with s = a + b per row, biased variance.  a, b, y [rows, features]. */
+int cdml_residual_layernorm(const float *a, const float *b, const float *gamma,
+                            const float *beta, float *y, int rows,
+                            int features, float eps, cdml_stream stream);
+
+/* IAccelerationManager.EmbedTokenIds (:275-277), replacing
+ * AccelerationCPU.cs:3473-3515: out[i, :] = table[ids[i], :].  ids is device
+ * int32[count]; an id outside [0, vocab) writes a zero row and, when
+ * bad_count (device int32) is non-NULL, increments it. */
+int cdml_embed_tokens(const int *ids, int count, const float *table, int vocab,
+                      int dim, float *out, int *bad_count, cdml_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CDML_H */

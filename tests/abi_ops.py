@@ -1,0 +1,123 @@
+"""numpy-in, numpy-out calls of the C-ABI kernels (test helper).
+
+Each call uploads its operands into caller-owned device buffers, enqueues one
+C-ABI entry point on a stream, and downloads the result, which is what a
+P/Invoke manager does per IAccelerationManager call.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import numpy as np
+
+from cdml import native as N
+
+_stream = None
+
+
+def stream() -> N.Stream:
+    global _stream
+    if _stream is None:
+        N.init(0)
+        _stream = N.Stream()
+    return _stream
+
+
+def up(a, dtype=np.float32) -> N.DeviceBuffer:
+    return N.DeviceBuffer.from_array(np.ascontiguousarray(a, dtype=dtype), stream())
+
+
+def down(buf, shape, dtype=np.float32):
+    return buf.download(shape, dtype, stream())
+
+
+def project_qkv(x, wq, bq, wk, bk, wv, bv):
+    rows, ind = x.shape
+    out = wq.shape[0]
+    bufs = [up(a) for a in (x, wq, bq, wk, bk, wv, bv)]
+    q, k, v = (N.DeviceBuffer(max(4, rows * out * 4)) for _ in range(3))
+    N.check(N.lib().cdml_project_qkv(*(b.ptr for b in bufs), q.ptr, k.ptr, v.ptr, rows, ind, out,
+                                     stream().handle))
+    return tuple(down(t, (rows, out)) for t in (q, k, v))
+
+
+def linear(x, w, b, act=0):
+    rows, ind = x.shape
+    out = w.shape[0]
+    bx, bw = up(x), up(w)
+    bb = up(b) if b is not None else None
+    y = N.DeviceBuffer(max(4, rows * out * 4))
+    N.check(N.lib().cdml_linear(bx.ptr, ind, bw.ptr, bb.ptr if bb else None, y.ptr, out, rows, ind,
+                                out, act, stream().handle))
+    return down(y, (rows, out))
+
+
+def rope(x, num_heads=None, start_col=0, head_dim=None, base=10000.0, inverse=False,
+         pos_offset=0, seg_len=0, positions=None):
+    rows, dim = x.shape
+    if head_dim is None:
+        head_dim = dim // num_heads
+    if num_heads is None:
+        num_heads = 1
+    bx = up(x)
+    bp = up(positions, np.int32) if positions is not None else None
+    N.check(N.lib().cdml_rope(bx.ptr, rows, dim, start_col, head_dim, num_heads, base, int(inverse),
+                              pos_offset, seg_len, bp.ptr if bp else None, stream().handle))
+    return down(bx, (rows, dim))
+
+
+def sdpa(q, k, v, num_heads, mask=None, causal=False, scale=None, batch=1):
+    """q [batch*lq, D], k/v [batch*lk, D]."""
+    rows_q, dim = q.shape
+    lq, lk = rows_q // batch, k.shape[0] // batch
+    if scale is None:  # ScaledDotProductAttention: 1f / MathF.Sqrt(headDim)
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(dim // num_heads)))
+    bq, bk, bv = up(q), up(k), up(v)
+    bo = N.DeviceBuffer(max(4, rows_q * dim * 4))
+    bm = up(mask, np.uint8) if mask is not None else None
+    N.check(N.lib().cdml_sdpa_fwd(bq.ptr, dim, bk.ptr, dim, bv.ptr, dim, bo.ptr, dim, batch, lq, lk, dim,
+                                  num_heads, scale, int(causal), bm.ptr if bm else None,
+                                  stream().handle))
+    return down(bo, (rows_q, dim))
+
+
+def decode(q, kcache, vcache, kv_len, num_heads, scale):
+    b, dim = q.shape
+    t_max = kcache.shape[1]
+    ws = C.c_size_t(0)
+    N.check(N.lib().cdml_decode_attn_workspace_size(b, t_max, dim, num_heads, C.byref(ws)))
+    bq, bk, bv = up(q), up(kcache), up(vcache)
+    bl = up(kv_len, np.int32)
+    bo = N.DeviceBuffer(b * dim * 4)
+    bw = N.DeviceBuffer(max(4, ws.value))
+    N.check(N.lib().cdml_decode_attn(bq.ptr, bk.ptr, bv.ptr, bl.ptr, bo.ptr, b, t_max, dim, num_heads,
+                                     scale, bw.ptr, ws.value, stream().handle))
+    return down(bo, (b, dim))
+
+
+def residual_layernorm(a, b, gamma, beta, eps=1e-5):
+    rows, f = a.shape
+    ba, bb, bg, bt = up(a), up(b), up(gamma), up(beta)
+    y = N.DeviceBuffer(max(4, rows * f * 4))
+    N.check(N.lib().cdml_residual_layernorm(ba.ptr, bb.ptr, bg.ptr, bt.ptr, y.ptr, rows, f, eps,
+                                            stream().handle))
+    return down(y, (rows, f))
+
+
+def embed(ids, table):
+    ids = np.ascontiguousarray(ids, np.int32)
+    vocab, dim = table.shape
+    bi, bt = up(ids, np.int32), up(table)
+    bad = up(np.zeros(1, np.int32), np.int32)
+    out = N.DeviceBuffer(max(4, ids.size * dim * 4))
+    N.check(N.lib().cdml_embed_tokens(bi.ptr, ids.size, bt.ptr, vocab, dim, out.ptr, bad.ptr,
+                                      stream().handle))
+    return down(out, (ids.size, dim)), int(down(bad, (1,), np.int32)[0])
+
+
+def kv_append(k_new, v_new, kcache, vcache, positions):
+    b, t_max, dim = kcache.shape
+    bk, bv, bkc, bvc = up(k_new), up(v_new), up(kcache), up(vcache)
+    bp = up(positions, np.int32)
+    N.check(N.lib().cdml_kv_cache_append(bk.ptr, bv.ptr, bkc.ptr, bvc.ptr, bp.ptr, b, t_max, dim,
+                                         stream().handle))
+    return down(bkc, kcache.shape), down(bvc, vcache.shape)

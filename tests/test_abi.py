@@ -1,0 +1,64 @@
+"""CPU-side checks of the C ABI: the library loads, exports exactly what
+include/cdml.h declares, and rejects bad arguments before touching a device
+(the reference's argument checks, e.g. AccelerationCPU.cs:1859-1862)."""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+
+import pytest
+
+from cdml import native as N
+
+
+def test_library_exports_every_header_function():
+    names = N.header_functions()
+    assert len(names) >= 25
+    lib = N.lib()
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"not exported: {missing}"
+    assert set(names) == set(N.SIGNATURES), "ctypes signatures out of sync with cdml.h"
+    out = subprocess.run(["nm", "-D", "--defined-only", N.LIB_PATH], capture_output=True, text=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if " T cdml_" in l}
+    assert exported == set(names)
+
+
+def test_version_and_error_text():
+    assert b"gfx950" in N.lib().cdml_version()
+    rc = N.lib().cdml_sdpa_fwd(None, 8, None, 8, None, 8, None, 8, 1, 4, 5, 8, 2, 0.5, 1, None, None)
+    assert rc == N.E_CAUSAL
+    assert b"causal" in N.lib().cdml_last_error()
+
+
+@pytest.mark.parametrize("args,code", [
+    ((None, 8, None, 8, None, 8, None, 8, 1, 4, 4, 8, 3, 0.5, 0, None, None), N.E_INVALID),  # 8 % 3
+    ((None, 4, None, 8, None, 8, None, 8, 1, 4, 4, 8, 2, 0.5, 0, None, None), N.E_INVALID),  # ldq < dim
+    ((None, 8, None, 8, None, 8, None, 8, 1, 4, 4, 8, 2, 0.5, 0, None, None), N.E_INVALID),  # NULL q
+])
+def test_sdpa_argument_checks(args, code):
+    assert N.lib().cdml_sdpa_fwd(*args) == code
+
+
+def test_other_argument_checks():
+    L = N.lib()
+    assert L.cdml_rope(None, 4, 6, 0, 3, 2, 10000.0, 0, 0, 0, None, None) == N.E_INVALID  # odd head dim
+    assert L.cdml_rope(None, 4, 8, 0, 4, 2, -1.0, 0, 0, 0, None, None) == N.E_INVALID   # bad base
+    assert L.cdml_rope(None, 4, 8, 2, 4, 2, 10000.0, 0, 0, 0, None, None) == N.E_INVALID  # heads past row
+    assert L.cdml_linear(None, 4, None, None, None, 4, 2, 4, 4, 9, None) == N.E_INVALID   # activation
+    assert L.cdml_linear(None, 2, None, None, None, 4, 2, 4, 4, 0, None) == N.E_INVALID   # ldx < in
+    assert L.cdml_project_qkv(*([None] * 10), -1, 4, 4, None) == N.E_INVALID
+    sz = C.c_size_t(0)
+    assert L.cdml_decode_attn_workspace_size(64, 8192, 2048, 16, C.byref(sz)) == N.OK
+    assert sz.value == 4 * 64 * 16 * 32 * 130
+    assert L.cdml_decode_attn_workspace_size(1, 1, 10, 3, C.byref(sz)) == N.E_INVALID
+    # empty work is a no-op even without a device
+    assert L.cdml_project_qkv(*([None] * 10), 0, 4, 4, None) == N.OK
+    assert L.cdml_residual_layernorm(None, None, None, None, None, 0, 8, 1e-5, None) == N.OK
+
+
+def test_no_device_is_reported_not_faked():
+    if N.device_count() > 0:
+        pytest.skip("a device is visible")
+    assert N.lib().cdml_init(0) == N.E_NODEVICE
+    with pytest.raises(N.CdmlError):
+        N.DeviceBuffer(1024)

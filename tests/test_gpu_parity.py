@@ -1,0 +1,260 @@
+"""GPU parity of every C-ABI kernel against the CPU oracle (run on the MI355X).
+
+Bar: per element |gpu - oracle| <= 1e-4 + 1e-3 |oracle| (the north-star
+tolerance, fp32), and bit-exact for the gather / copy kernels.  Cases mirror
+the reference's own parity suite (AccelerationManagerParityTests.cs) plus the
+BASELINE shapes, ragged lengths and the edge rules (all-masked rows, causal
+with Lq != Lk, head dims 3 .. 160).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import abi_ops as G
+from conftest import assert_parity
+from oracle import oracle as O
+from cdml import native as N
+from cdml import synth
+
+pytestmark = pytest.mark.gpu
+
+M, Vec = synth.matrix, synth.vector
+ATOL, RTOL = 1e-4, 1e-3
+
+
+def parity(a, e, what=""):
+    assert_parity(a, e, atol=ATOL, rtol=RTOL, what=what)
+
+
+def setup_module(module):
+    N.init(0)
+    info = N.device_info(0)
+    print(f"\n[device] {info['name']} {info['arch']} CUs={info['compute_units']} "
+          f"sclk={info['max_clock_mhz']}MHz", flush=True)
+
+
+# ------------------------------------------------------------- projections
+def test_project_qkv_reference_cases():
+    x = M(6, 5, 124)
+    args = (M(8, 5, 125), Vec(8, 128), M(8, 5, 126), Vec(8, 129), M(8, 5, 127), Vec(8, 130))
+    for got, want, n in zip(G.project_qkv(x, *args), O.project_qkv(x, *args), "QKV"):
+        parity(got, want, f"ProjectQKV 6x5->8 {n}")
+    xg = M(192, 128, 142)
+    args = (M(128, 128, 143), Vec(128, 146), M(128, 128, 144), Vec(128, 147), M(128, 128, 145), Vec(128, 148))
+    for got, want, n in zip(G.project_qkv(xg, *args), O.project_qkv(xg, *args), "QKV"):
+        parity(got, want, f"ProjectQKV 192x128->128 {n}")
+
+
+@pytest.mark.parametrize("rows,ind,out", [(1, 64, 64), (33, 96, 200), (130, 257, 129), (1024, 512, 512),
+                                          (300, 1024, 1024)])
+def test_project_qkv_shapes(rows, ind, out):
+    x = synth.normal(rows * 7 + ind, (rows, ind))
+    w = [synth.xavier_uniform(i + out, out, ind) for i in range(3)]
+    b = [synth.normal(9 + i, (out,)) * np.float32(0.1) for i in range(3)]
+    args = (w[0], b[0], w[1], b[1], w[2], b[2])
+    for got, want, n in zip(G.project_qkv(x, *args), O.project_qkv(x, *args, mt=True), "QKV"):
+        parity(got, want, f"ProjectQKV {rows}x{ind}->{out} {n}")
+
+
+@pytest.mark.parametrize("act", [0, 1, 2, 3, 4, 5])
+def test_linear_with_activation(act):
+    x = synth.normal(3, (77, 64))
+    w = synth.xavier_uniform(4, 130, 64)
+    b = synth.normal(5, (130,))
+    want = O.activation(O.batch_dot_add_bias(w, x, b), act)
+    parity(G.linear(x, w, b, act), want, f"linear act={act}")
+
+
+def test_project_output_batch_reference_case():
+    parity(G.linear(M(4, 6, 56), M(3, 6, 57), Vec(3, 58)),
+           O.project_output_batch(M(4, 6, 56), M(3, 6, 57), Vec(3, 58)), "ProjectOutputBatch")
+    # MatrixMultiplyTranspose known answers 17 / 23 / 67 (MultiTypeTransformerTests.cs:664-674)
+    c = G.linear(np.array([[1, 2], [3, 4]], np.float32), np.array([[5, 6], [7, 8], [9, 10]], np.float32), None)
+    assert c[0, 0] == 17 and c[0, 1] == 23 and c[1, 2] == 67
+
+
+# -------------------------------------------------------------------- RoPE
+def test_rope_reference_cases():
+    m = M(4, 8, 97)
+    parity(G.rope(m, 2), O.rope(m, 2), "RoPE all heads")
+    parity(G.rope(m, start_col=2, head_dim=4, num_heads=1), O.rope_head(m, 2, 4), "RoPE one head")
+    back = G.rope(G.rope(m, 2), 2, inverse=True)
+    assert np.allclose(back, m, atol=5e-4)
+    y = G.rope(np.array([[1, 0], [1, 0], [0, 1]], np.float32), 1)
+    assert np.allclose(y[1], [math.cos(1), math.sin(1)], atol=1e-5)
+    assert np.allclose(y[2], [-math.sin(2), math.cos(2)], atol=1e-5)
+
+
+@pytest.mark.parametrize("rows,dim,heads", [(4096, 1024, 16), (512, 256, 8), (64, 64, 4), (100, 2048, 16)])
+def test_rope_long_positions(rows, dim, heads):
+    x = synth.normal(rows + dim, (rows, dim))
+    parity(G.rope(x, heads), O.rope(x, heads, mt=True), f"RoPE {rows}x{dim}/{heads}")
+
+
+def test_rope_segmented_and_absolute_positions():
+    x = synth.normal(1, (3 * 50, 64))
+    want = np.concatenate([O.rope(x[i * 50:(i + 1) * 50], 4) for i in range(3)])
+    parity(G.rope(x, 4, seg_len=50), want, "RoPE segmented")
+    pos = np.array([0, 7, 4095, 123], np.int32)
+    xr = synth.normal(2, (4, 64))
+    want = np.stack([O.rope(np.vstack([np.zeros((p, 64), np.float32), xr[i:i + 1]]), 4)[-1]
+                     for i, p in enumerate(pos)])
+    parity(G.rope(xr, 4, positions=pos), want, "RoPE absolute positions")
+
+
+# ------------------------------------------------------------------- SDPA
+def test_sdpa_reference_cases(ops_golden):
+    g = ops_golden
+    qs, ks, vs = M(4, 8, 118), M(4, 8, 119), M(4, 8, 120)
+    qc, kc, vc = M(4, 8, 121), M(5, 8, 122), M(5, 8, 123)
+    parity(G.sdpa(qs, ks, vs, 2), O.sdpa(qs, ks, vs, 2), "self/no mask")
+    parity(G.sdpa(qs, ks, vs, 2, mask=g["self_mask"]), O.sdpa(qs, ks, vs, 2, mask=g["self_mask"]), "self/mask")
+    flag = G.sdpa(qs, ks, vs, 2, causal=True)
+    parity(flag, O.sdpa(qs, ks, vs, 2, causal=True), "self/causal")
+    parity(G.sdpa(qs, ks, vs, 2, mask=O.causal_mask(4)), flag, "causal flag == explicit mask")
+    parity(G.sdpa(qc, kc, vc, 2), O.sdpa(qc, kc, vc, 2), "cross/no mask")
+    parity(G.sdpa(qc, kc, vc, 2, mask=g["cross_mask"]), O.sdpa(qc, kc, vc, 2, mask=g["cross_mask"]), "cross/mask")
+    am = G.sdpa(qc, kc, vc, 2, mask=g["all_masked_mask"])
+    assert np.all(am[0] == 0), "all-masked row must be exactly 0"
+    parity(am, O.sdpa(qc, kc, vc, 2, mask=g["all_masked_mask"]), "all-masked row")
+    with pytest.raises(N.CdmlError) as ei:
+        G.sdpa(qc, kc, vc, 2, causal=True)
+    assert ei.value.code == N.E_CAUSAL
+
+
+def test_mha_forward_reference_cases(ops_golden):
+    q6, k6, v6 = M(4, 6, 31), M(4, 6, 32), M(4, 6, 33)  # d_h = 3
+    sc = float(ops_golden["mha_causal_scale"])
+    parity(G.sdpa(q6, k6, v6, 2, mask=O.causal_mask(4), scale=sc),
+           O.mha_forward(q6, k6, v6, 2, sc, mask=O.causal_mask(4)), "MHA causal d_h=3")
+    qg, kg, vg = M(128, 64, 110), M(128, 64, 111), M(128, 64, 112)
+    parity(G.sdpa(qg, kg, vg, 4, scale=0.25), O.mha_forward(qg, kg, vg, 4, 0.25), "MHA 128 no mask")
+    pm = synth.periodic_mask(128, 128)
+    parity(G.sdpa(qg, kg, vg, 4, scale=0.25, mask=pm), O.mha_forward(qg, kg, vg, 4, 0.25, mask=pm),
+           "MHA 128 periodic mask")
+    parity(G.sdpa(qg, kg, vg, 4, causal=True), O.sdpa(qg, kg, vg, 4, causal=True), "SDPA 128 causal")
+
+
+@pytest.mark.parametrize("L,D,H", [(64, 64, 4), (1, 64, 4), (33, 96, 3), (130, 512, 8), (257, 256, 8),
+                                   (300, 128, 1), (200, 160, 1), (77, 80, 5), (96, 1024, 64)])
+def test_sdpa_causal_shapes(L, D, H):
+    q, k, v = (synth.normal(L * 3 + D + i, (L, D)) for i in range(3))
+    parity(G.sdpa(q, k, v, H, causal=True), O.sdpa(q, k, v, H, causal=True, mt=True), f"causal L={L} D={D} H={H}")
+
+
+@pytest.mark.parametrize("lq,lk", [(5, 300), (129, 64), (64, 1)])
+def test_sdpa_cross_lengths(lq, lk):
+    D, H = 128, 2
+    q = synth.normal(1, (lq, D))
+    k, v = synth.normal(2, (lk, D)), synth.normal(3, (lk, D))
+    parity(G.sdpa(q, k, v, H), O.sdpa(q, k, v, H), f"cross {lq}x{lk}")
+    mask = synth.periodic_mask(lq, lk)
+    parity(G.sdpa(q, k, v, H, mask=mask), O.sdpa(q, k, v, H, mask=mask), f"cross mask {lq}x{lk}")
+
+
+def test_sdpa_batched_equals_per_sequence():
+    B, L, D, H = 3, 200, 128, 4
+    q, k, v = (synth.normal(40 + i, (B * L, D)) for i in range(3))
+    got = G.sdpa(q, k, v, H, causal=True, batch=B)
+    for b in range(B):
+        s = slice(b * L, (b + 1) * L)
+        parity(got[s], O.sdpa(q[s], k[s], v[s], H, causal=True), f"batch {b}")
+
+
+@pytest.mark.parametrize("name,B,L,D,H", [("c2", 16, 1024, 512, 8), ("c5", 256, 512, 256, 8)])
+def test_sdpa_baseline_configs_sampled(name, B, L, D, H):
+    """Whole-batch launch at the BASELINE shape; three sequences checked."""
+    q, k, v = (synth.normal(100 + i, (B * L, D)) for i in range(3))
+    got = G.sdpa(q, k, v, H, causal=True, batch=B)
+    for b in (0, B // 2, B - 1):
+        s = slice(b * L, (b + 1) * L)
+        parity(got[s], O.sdpa(q[s], k[s], v[s], H, causal=True, mt=True), f"{name} seq {b}")
+
+
+def test_sdpa_c3_long_context_sampled():
+    """c3 shape (B 4, L 4096, D 1024, H 16): one full sequence's sampled heads vs the
+    oracle, plus the causal-prefix property on the whole batch."""
+    B, L, D, H = 4, 4096, 1024, 16
+    q, k, v = (synth.normal(200 + i, (B * L, D)) for i in range(3))
+    got = G.sdpa(q, k, v, H, causal=True, batch=B)
+    assert np.all(np.isfinite(got))
+    b = 1
+    s = slice(b * L, (b + 1) * L)
+    for h in (0, 9):
+        cols = slice(h * 64, (h + 1) * 64)
+        want = O.sdpa(q[s, cols], k[s, cols], v[s, cols], 1, causal=True)
+        parity(got[s, cols], want, f"c3 seq {b} head {h}")
+    # causal prefix: attention of the first 1000 positions alone equals the prefix rows
+    pre = G.sdpa(q[:1000], k[:1000], v[:1000], H, causal=True)
+    parity(pre, got[:1000], "causal prefix property")
+
+
+# ----------------------------------------------------------------- decode
+@pytest.mark.parametrize("B,T,D,H", [(2, 1000, 2048, 16), (3, 300, 64, 4), (2, 513, 96, 3), (1, 1, 256, 2)])
+def test_decode_vs_oracle(B, T, D, H):
+    q = synth.normal(1, (B, D))
+    kc, vc = synth.normal(2, (B, T, D)), synth.normal(3, (B, T, D))
+    lens = np.array([T, max(1, T // 3)] + [1] * (B - 2), np.int32)[:B]
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D // H)))
+    got = G.decode(q, kc, vc, lens, H, scale)
+    want = O.decode_attention_batch(q, kc, vc, lens, H, scale, parallel=True)
+    parity(got, want, f"decode B={B} T={T} D={D} H={H}")
+
+
+def test_decode_equals_last_prefill_row():
+    T, D, H = 700, 512, 4
+    q, k, v = (synth.normal(50 + i, (T, D)) for i in range(3))
+    pre = G.sdpa(q, k, v, H, causal=True)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D // H)))
+    dec = G.decode(q[-1:], k[None], v[None], np.array([T], np.int32), H, scale)
+    parity(dec[0], pre[-1], "decode == last prefill row")
+
+
+def test_decode_c4_shape_sampled():
+    """c4 shape (B 64, T 8192, H 16, d_h 128), full kernel launch; 4 sequences checked."""
+    B, T, D, H = 64, 8192, 2048, 16
+    rng = np.random.default_rng(4)  # 2 x 4 GiB of N(0,1): numpy's generator for speed
+    q = rng.standard_normal((B, D), dtype=np.float32)
+    kc = rng.standard_normal((B, T, D), dtype=np.float32)
+    vc = rng.standard_normal((B, T, D), dtype=np.float32)
+    lens = np.full(B, T, np.int32)
+    lens[5] = 4097
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(128)))
+    got = G.decode(q, kc, vc, lens, H, scale)
+    assert np.all(np.isfinite(got))
+    idx = [0, 5, 31, 63]
+    want = O.decode_attention_batch(q[idx], kc[idx], vc[idx], lens[idx], H, scale, parallel=True)
+    parity(got[idx], want, "c4 sampled")
+
+
+def test_kv_cache_append():
+    kc, vc = np.zeros((3, 5, 8), np.float32), np.zeros((3, 5, 8), np.float32)
+    kn, vn = synth.normal(1, (3, 8)), synth.normal(2, (3, 8))
+    pos = np.array([0, 4, 2], np.int32)
+    k2, v2 = G.kv_append(kn, vn, kc, vc, pos)
+    for b, p in enumerate(pos):
+        assert np.array_equal(k2[b, p], kn[b]) and np.array_equal(v2[b, p], vn[b])
+        assert np.count_nonzero(k2[b]) == np.count_nonzero(kn[b])
+
+
+# ------------------------------------------------------ layernorm, embed
+@pytest.mark.parametrize("rows,f", [(5, 6), (64, 64), (100, 1024), (7, 2500)])
+def test_residual_layernorm(rows, f):
+    a, b = synth.normal(rows, (rows, f)), synth.normal(f, (rows, f))
+    g, be = synth.positive_vector(f, 28), synth.vector(f, 29)
+    parity(G.residual_layernorm(a, b, g, be), O.residual_layernorm(a, b, g, be), f"LN {rows}x{f}")
+
+
+def test_embed_tokens_exact():
+    table = M(6, 5, 64)
+    out, bad = G.embed([0, 2, 4], table)
+    assert bad == 0 and np.array_equal(out, O.embed_tokens([0, 2, 4], table))
+    t2 = synth.normal(3, (200, 64))
+    ids = synth.token_ids(4, 64, 200)
+    out, bad = G.embed(ids, t2)
+    assert bad == 0 and np.array_equal(out, O.embed_tokens(ids, t2))
+    out, bad = G.embed([1, 200, -1], t2)
+    assert bad == 2 and np.all(out[1:] == 0) and np.array_equal(out[0], t2[1])
