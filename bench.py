@@ -1,0 +1,299 @@
+"""Benchmark of the causal multi-head attention forward path on one MI355X.
+
+Headline (``value``): full causal MHA forward at BASELINE config c3
+(batch 4, seq 4096, d_model 1024, 16 heads x 64), one "step" being one pass
+of the hot path over the whole batch, every kernel through the C ABI:
+
+    cdml_project_qkv   (fused Q/K/V fp32-MFMA GEMM, bias epilogue)
+    cdml_rope x2       (interleaved RoPE on Q and K, per-sequence positions)
+    cdml_sdpa_fwd      (flash-style fp32-MFMA causal attention)
+    cdml_linear        (output projection, bias epilogue)
+
+``value`` = algorithmic matmul FLOPs of that step (274.91 GFLOP) / step time,
+in TFLOP/s.  Beside it the line carries the flash kernel alone (``roofline``,
+bound "mfma", timed with HIP events on the library stream around every
+launch in the timed region), the c4 decode step (B 64 queries against a
+K/V cache of 8192 x 2048, ``decode``, bound "hbm") and the multi-threaded
+CPU restatement of the reference's AccelerationMutliThreadCPU timed on this
+host (``cpu_baseline``).
+
+Inputs are resident in HBM before the timed region starts.  The process never
+imports torch: torch ships its own HIP runtime, and the C ABI is driven
+through ctypes exactly as a P/Invoke host would.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "callaghandev.ml_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+
+METRIC = "attn fwd TFLOP/s (% fp32 MFMA peak) @seq4096; decode HBM GB/s @KV8192"
+FP32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense fp32 matrix, AMD published
+HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, AMD published
+
+# c3: one MHA layer of the long-context stack
+C3 = dict(batch=4, seq=4096, dim=1024, heads=16)
+# c4: decode step
+C4 = dict(batch=64, t=8192, dim=2048, heads=16)
+
+
+def mha_flops(batch, seq, dim, heads):
+    hd = dim // heads
+    pairs = seq * (seq + 1) // 2
+    core = 4 * batch * heads * hd * pairs          # Q.K^T and P.V over causal pairs
+    qkv = 6 * batch * seq * dim * dim
+    out = 2 * batch * seq * dim * dim
+    return core, qkv, out
+
+
+def decode_bytes(batch, t, dim):
+    return 2 * batch * t * dim * 4 + 2 * batch * dim * 4   # K, V read once; q read, o written
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Timer:
+    """Pairs of HIP events on the library stream around each launch of one kernel."""
+
+    def __init__(self, N, n):
+        self.N = N
+        self.pairs = [(N.Event(), N.Event()) for _ in range(n)]
+        self.i = 0
+
+    def start(self, st):
+        self.pairs[self.i][0].record(st)
+
+    def stop(self, st):
+        self.pairs[self.i][1].record(st)
+        self.i += 1
+
+    def ms(self):
+        return [a.elapsed_ms(b) for a, b in self.pairs[: self.i]]
+
+
+def bench_mha(N, st, steps, warmup):
+    lib = N.lib()
+    B, L, D, H = C3["batch"], C3["seq"], C3["dim"], C3["heads"]
+    hd = D // H
+    rows = B * L
+    from cdml import synth
+
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((rows, D), dtype=np.float32)          # N(0,1) embeddings
+    ws = [synth.xavier_uniform(30 + i, D, D) for i in range(4)]   # Wq Wk Wv Wo, Xavier-uniform
+    bz = np.zeros(D, np.float32)                                   # biases 0 (reference init)
+    dx = N.DeviceBuffer.from_array(x, st)
+    dw = [N.DeviceBuffer.from_array(w, st) for w in ws]
+    db = N.DeviceBuffer.from_array(bz, st)
+    dq, dk, dv, da, dy = (N.DeviceBuffer(rows * D * 4) for _ in range(5))
+    s = st.handle
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+
+    def step(t_flash=None, t_qkv=None, t_out=None):
+        if t_qkv:
+            t_qkv.start(st)
+        N.check(lib.cdml_project_qkv(dx.ptr, dw[0].ptr, db.ptr, dw[1].ptr, db.ptr, dw[2].ptr, db.ptr,
+                                     dq.ptr, dk.ptr, dv.ptr, rows, D, D, s))
+        if t_qkv:
+            t_qkv.stop(st)
+        for t in (dq, dk):
+            N.check(lib.cdml_rope(t.ptr, rows, D, 0, hd, H, 10000.0, 0, 0, L, None, s))
+        if t_flash:
+            t_flash.start(st)
+        N.check(lib.cdml_sdpa_fwd(dq.ptr, D, dk.ptr, D, dv.ptr, D, da.ptr, D, B, L, L, D, H, scale, 1,
+                                  None, s))
+        if t_flash:
+            t_flash.stop(st)
+        if t_out:
+            t_out.start(st)
+        N.check(lib.cdml_linear(da.ptr, D, dw[3].ptr, db.ptr, dy.ptr, D, rows, D, D, 0, s))
+        if t_out:
+            t_out.stop(st)
+
+    log(f"[bench] c3 MHA warmup {warmup}")
+    for _ in range(warmup):
+        step()
+    st.synchronize()
+    # Timed region 1: whole steps, host clock (the step time) ...
+    log(f"[bench] c3 MHA timed {steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    st.synchronize()
+    wall = time.perf_counter() - t0
+    # ... timed region 2: the same steps with HIP events around each kernel.
+    tf, tq, to = Timer(N, steps), Timer(N, steps), Timer(N, steps)
+    e0, e1 = N.Event(), N.Event()
+    e0.record(st)
+    for _ in range(steps):
+        step(tf, tq, to)
+    e1.record(st)
+    st.synchronize()
+    dev_ms = e0.elapsed_ms(e1) / steps
+    flash_ms, qkv_ms, out_ms = (float(np.mean(t.ms())) for t in (tf, tq, to))
+    y = dy.download((rows, D), stream=st)
+    assert np.all(np.isfinite(y)), "non-finite MHA output"
+    return dict(wall_s=wall, dev_ms=dev_ms, flash_ms=flash_ms, qkv_ms=qkv_ms, out_ms=out_ms)
+
+
+def bench_decode(N, st, steps, warmup):
+    lib = N.lib()
+    B, T, D, H = C4["batch"], C4["t"], C4["dim"], C4["heads"]
+    rng = np.random.default_rng(4)
+    per_seq = T * D * 4
+    dk, dv = N.DeviceBuffer(B * per_seq), N.DeviceBuffer(B * per_seq)
+    # N(0,1) cache rows: 16 distinct [T, D] blocks per tensor, tiled over the batch.
+    blocks = 16
+    for buf in (dk, dv):
+        for j in range(blocks):
+            blk = rng.standard_normal((T, D), dtype=np.float32)
+            hb = N.DeviceBuffer.from_array(blk, st)
+            for b in range(j, B, blocks):
+                N.check(lib.cdml_memcpy_d2d_async(buf.ptr + b * per_seq, hb.ptr, per_seq, st.handle))
+            st.synchronize()
+            hb.free()
+    dq = N.DeviceBuffer.from_array(rng.standard_normal((B, D), dtype=np.float32), st)
+    dl = N.DeviceBuffer.from_array(np.full(B, T, np.int32), st)
+    do = N.DeviceBuffer(B * D * 4)
+    wsz = C.c_size_t(0)
+    N.check(lib.cdml_decode_attn_workspace_size(B, T, D, H, C.byref(wsz)))
+    dws = N.DeviceBuffer(max(4, wsz.value))
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D // H)))
+
+    def step():
+        N.check(lib.cdml_decode_attn(dq.ptr, dk.ptr, dv.ptr, dl.ptr, do.ptr, B, T, D, H, scale, dws.ptr,
+                                     wsz.value, st.handle))
+
+    for _ in range(warmup):
+        step()
+    st.synchronize()
+    tm = Timer(N, steps)
+    for _ in range(steps):
+        tm.start(st)
+        step()
+        tm.stop(st)
+    st.synchronize()
+    ms = tm.ms()
+    o = do.download((B, D), stream=st)
+    assert np.all(np.isfinite(o)), "non-finite decode output"
+    return dict(ms=float(np.mean(ms)), ms_min=float(np.min(ms)))
+
+
+def cpu_baseline(sample_seqs=3):
+    """The multi-threaded CPU restatement of AccelerationMutliThreadCPU's
+    ProjectQKV / RoPE / ScaledDotProductAttention / ProjectOutputBatch
+    (oracle/refcpu_mt.c) on `sample_seqs` of the c3 batch's sequences, one
+    LanguageModel.Forward-style call per sequence.  Timed, not checked."""
+    from oracle import oracle as O
+    from cdml import synth
+
+    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16") or 16))
+    O.set_threads(threads)
+    L, D, H = C3["seq"], C3["dim"], C3["heads"]
+    rng = np.random.default_rng(5)
+    ws = [synth.xavier_uniform(30 + i, D, D) for i in range(4)]
+    bz = np.zeros(D, np.float32)
+    xs = [rng.standard_normal((L, D), dtype=np.float32) for _ in range(sample_seqs)]
+    O.project_qkv(xs[0][:64], ws[0], bz, ws[1], bz, ws[2], bz, mt=True)  # load + warm the library
+    t0 = time.perf_counter()
+    for x in xs:
+        q, k, v = O.project_qkv(x, ws[0], bz, ws[1], bz, ws[2], bz, mt=True)
+        q, k = O.rope(q, H, mt=True), O.rope(k, H, mt=True)
+        a = O.sdpa(q, k, v, H, causal=True, mt=True)
+        O.project_output_batch(a, ws[3], bz, mt=True)
+    dt = time.perf_counter() - t0
+    core, qkv, out = mha_flops(sample_seqs, L, D, H)
+    return dict(value=(core + qkv + out) / dt / 1e12, unit="TFLOP/s", cores=threads, kind="port",
+                seconds=dt,
+                sample=f"{sample_seqs} of the 4 c3 sequences (L 4096, D 1024, H 16), full MHA forward "
+                       f"through the C restatement of AccelerationMutliThreadCPU (-O2, no fast-math), "
+                       f"{threads} threads, {dt:.1f} s")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the attention path is single-device by design "
+              "(batch x head shards need no exchange); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    from cdml import native as N
+
+    N.init(0)
+    info = N.device_info(0)
+    log(f"[bench] device {info['name']} {info['arch']} CUs {info['compute_units']} "
+        f"sclk {info['max_clock_mhz']} MHz")
+    st = N.Stream()
+
+    mha = bench_mha(N, st, args.steps, args.warmup)
+    core, qkv, out = mha_flops(**C3)
+    total = core + qkv + out
+    ms_per_step = mha["wall_s"] / args.steps * 1e3
+    value = total / (ms_per_step * 1e-3) / 1e12
+    flash_tflops = core / (mha["flash_ms"] * 1e-3) / 1e12
+    res = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: x ~ N(0,1), Wq/Wk/Wv/Wo Xavier-uniform, zero biases, causal",
+        "config": {"workload": "c3 causal MHA layer forward (QKV proj + RoPE + flash SDPA + out proj)",
+                   "batch": C3["batch"], "seq_len": C3["seq"], "d_model": C3["dim"],
+                   "heads": C3["heads"], "head_dim": C3["dim"] // C3["heads"], "parallelism": "none"},
+        "frac_of_fp32_mfma_peak": round(value / FP32_MFMA_PEAK_TFLOPS, 4),
+        "tokens_per_s": round(C3["batch"] * C3["seq"] / (ms_per_step * 1e-3), 1),
+        "kernels_ms": {"project_qkv": round(mha["qkv_ms"], 4), "flash_sdpa": round(mha["flash_ms"], 4),
+                       "out_proj": round(mha["out_ms"], 4), "step_events": round(mha["dev_ms"], 4)},
+        "roofline": {"kernel": "flash_fwd_kernel (cdml_sdpa_fwd, c3)", "bound": "mfma",
+                     "achieved": round(flash_tflops, 3), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(flash_tflops / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                     "algorithmic_per_launch": core},
+        "device": {k: info[k] for k in ("name", "arch", "compute_units", "max_clock_mhz")},
+    }
+    if not args.no_decode:
+        log("[bench] c4 decode")
+        dec = bench_decode(N, st, max(args.steps, 10), args.warmup)
+        nbytes = decode_bytes(C4["batch"], C4["t"], C4["dim"])
+        gbs = nbytes / (dec["ms"] * 1e-3) / 1e9
+        res["decode"] = {"workload": "c4 decode step (B 64, KV 8192, 16 heads x 128)",
+                         "ms": round(dec["ms"], 4), "tokens_per_s": round(C4["batch"] / (dec["ms"] * 1e-3), 1),
+                         "roofline": {"kernel": "decode_split_kernel + decode_combine_kernel", "bound": "hbm",
+                                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                                      "algorithmic_per_launch": nbytes}}
+    if not args.no_cpu_baseline:
+        log("[bench] CPU baseline (multi-threaded restatement)")
+        cb = cpu_baseline()
+        res["cpu_baseline"] = {k: (round(v, 6) if isinstance(v, float) else v) for k, v in cb.items()}
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()
