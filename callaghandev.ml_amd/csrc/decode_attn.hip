@@ -2,21 +2,26 @@
 // inline loop in LanguageModel.DecoderSelfAttentionStep, LanguageModel.cs:365-427).
 //
 // HBM-bound: every cached K and V element is read exactly once.  The cache
-// of each (sequence, head) is split into chunks of 256 keys; one 256-thread
-// workgroup owns a chunk.  Inside a wave, each group of 8 lanes owns one key
-// per step (8 keys per wave-step), each lane covering head_dim/8 contiguous
-// floats of that key's row, so every load instruction reads whole 128-byte
-// lines.  Pass 1 computes the chunk's scores (dot products reduced across the
-// 8-lane group), pass 2 reads V and accumulates exp2(score - chunk max) * v.
-// A combine kernel merges the chunks with the usual (max, sum) rescaling.
+// of each (sequence, head) is split into chunks of DC_CHUNK keys; one
+// 256-thread workgroup owns a chunk and each of its four waves a quarter of
+// it.  Inside a wave, each group of 8 lanes owns one key per step (8 keys per
+// wave-step).  Lane e of a group holds the head dims
+// {VW*e + 8*VW*i + c : i < NV, c < VW}, so one vector load instruction of the
+// group covers 8*VW contiguous floats (a whole 128-byte line for VW = 4).
+// K and V rows of a step are loaded together and the next step's rows are in
+// flight while the current one is consumed: the scores are reduced across the
+// 8 lanes of a group and folded into a per-group online softmax (running max,
+// running sum, running output), so no workgroup barrier separates the K and V
+// streams.  The eight groups of a wave and then the four waves are merged with
+// the (max, sum) rescaling; a combine kernel merges the chunks.
 #include "common.h"
 
 namespace cdml {
 namespace {
 
 constexpr int DC_THREADS = 256;
-constexpr int DC_CHUNK = 256;               // keys per workgroup
-constexpr int DC_KITER = DC_CHUNK / 4 / 8;  // steps of 8 keys per wave
+constexpr int DC_CHUNK = 256;                // keys per workgroup
+constexpr int DC_KITER = DC_CHUNK / 4 / 8;   // steps of 8 keys per wave
 
 struct DecodeArgs {
   const float *q, *kc, *vc;
@@ -27,34 +32,47 @@ struct DecodeArgs {
   float scale_log2;
 };
 
-typedef float vf4 __attribute__((ext_vector_type(4)));
-typedef float vf2 __attribute__((ext_vector_type(2)));
+template <int VW>
+struct VecT;
+template <>
+struct VecT<4> {
+  typedef float type __attribute__((ext_vector_type(4)));
+};
+template <>
+struct VecT<2> {
+  typedef float type __attribute__((ext_vector_type(2)));
+};
 
-// Streams one lane's slice of a cached row (read once: non-temporal).
-template <int EPL>
-__device__ __forceinline__ void load_row(const float *__restrict__ p, float (&r)[EPL]) {
-  if constexpr (EPL % 4 == 0) {
+// One lane's NV vectors of a cached row (streamed once: non-temporal).
+template <int VW, int NV>
+__device__ __forceinline__ void load_slice(const float *__restrict__ p, float (&r)[VW * NV]) {
+  typedef typename VecT<VW>::type V;
 #pragma unroll
-    for (int i = 0; i < EPL / 4; ++i) {
-      vf4 t = __builtin_nontemporal_load(reinterpret_cast<const vf4 *>(p) + i);
-      r[4 * i] = t.x;
-      r[4 * i + 1] = t.y;
-      r[4 * i + 2] = t.z;
-      r[4 * i + 3] = t.w;
-    }
-  } else {
+  for (int i = 0; i < NV; ++i) {
+    V t = __builtin_nontemporal_load(reinterpret_cast<const V *>(p + 8 * VW * i));
 #pragma unroll
-    for (int i = 0; i < EPL / 2; ++i) {
-      vf2 t = __builtin_nontemporal_load(reinterpret_cast<const vf2 *>(p) + i);
-      r[2 * i] = t.x;
-      r[2 * i + 1] = t.y;
-    }
+    for (int c = 0; c < VW; ++c) r[VW * i + c] = t[c];
   }
+}
+
+// Merges online-softmax state (m, l, o) with a partner's (exp2 domain).
+template <int EPL>
+__device__ __forceinline__ void merge_state(float &m, float &l, float (&o)[EPL], float m2, float l2,
+                                            const float (&o2)[EPL]) {
+  const float mn = fmaxf(m, m2);
+  const float mu = mn == -INFINITY ? 0.f : mn;
+  const float a1 = fast_exp2(m - mu), a2 = fast_exp2(m2 - mu);
+  l = l * a1 + l2 * a2;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) o[i] = o[i] * a1 + o2[i] * a2;
+  m = mn;
 }
 
 template <int HD>
 __global__ void __launch_bounds__(DC_THREADS) decode_split_kernel(const DecodeArgs a) {
-  constexpr int EPL = HD / 8;
+  constexpr int VW = HD >= 32 ? 4 : 2;  // floats per vector load
+  constexpr int NV = HD / (8 * VW);     // vector loads per lane per row
+  constexpr int EPL = VW * NV;          // head dims per lane (= HD / 8)
   __shared__ float red_m[4], red_l[4];
   __shared__ float red_o[4][HD];
 
@@ -66,87 +84,90 @@ __global__ void __launch_bounds__(DC_THREADS) decode_split_kernel(const DecodeAr
   float *part = a.part + ((size_t)(b * a.heads + h) * a.nsplit + split) * (HD + 2);
 
   if (chunk0 >= len) {
-    for (int d = threadIdx.x; d < HD + 2; d += DC_THREADS)
-      part[d] = d == HD ? -INFINITY : 0.f;
+    for (int d = threadIdx.x; d < HD + 2; d += DC_THREADS) part[d] = d == HD ? -INFINITY : 0.f;
     return;
   }
 
-  const size_t col = (size_t)h * HD + e * EPL;
+  const size_t col = (size_t)h * HD + VW * e;
   float q[EPL];
-  load_row<EPL>(a.q + (size_t)b * a.dim + col, q);
+  load_slice<VW, NV>(a.q + (size_t)b * a.dim + col, q);
 
   const float *kb = a.kc + (size_t)b * a.t_max * a.dim + col;
   const float *vb = a.vc + (size_t)b * a.t_max * a.dim + col;
   const int key0 = chunk0 + wave * (DC_KITER * 8) + g;
 
-  float sc[DC_KITER];
-#pragma unroll
-  for (int it = 0; it < DC_KITER; ++it) {
-    const int key = key0 + it * 8;
-    float kr[EPL];
-    if (key < len) {
-      load_row<EPL>(kb + (size_t)key * a.dim, kr);
-    } else {
-#pragma unroll
-      for (int i = 0; i < EPL; ++i) kr[i] = 0.f;
-    }
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) s += q[i] * kr[i];
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    s += __shfl_xor(s, 4);
-    sc[it] = key < len ? s * a.scale_log2 : -INFINITY;
-  }
-
-  float mx = sc[0];
-#pragma unroll
-  for (int it = 1; it < DC_KITER; ++it) mx = fmaxf(mx, sc[it]);
-  mx = fmaxf(mx, __shfl_xor(mx, 8));
-  mx = fmaxf(mx, __shfl_xor(mx, 16));
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
-  if (lane == 0) red_m[wave] = mx;
-  __syncthreads();
-  const float M = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
-  const float m_use = M == -INFINITY ? 0.f : M;
-
+  float m = -INFINITY, l = 0.f;
   float o[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) o[i] = 0.f;
-  float lsum = 0.f;
-#pragma unroll
-  for (int it = 0; it < DC_KITER; ++it) {
+
+  float kr[2][EPL], vr[2][EPL];
+  auto fetch = [&](int it, int buf) {
     const int key = key0 + it * 8;
     if (key < len) {
-      float vr[EPL];
-      load_row<EPL>(vb + (size_t)key * a.dim, vr);
-      const float p = fast_exp2(sc[it] - m_use);
-      lsum += p;
+      load_slice<VW, NV>(kb + (size_t)key * a.dim, kr[buf]);
+      load_slice<VW, NV>(vb + (size_t)key * a.dim, vr[buf]);
+    } else {
 #pragma unroll
-      for (int i = 0; i < EPL; ++i) o[i] += p * vr[i];
+      for (int i = 0; i < EPL; ++i) kr[buf][i] = vr[buf][i] = 0.f;
+    }
+  };
+  fetch(0, 0);
+#pragma unroll
+  for (int it = 0; it < DC_KITER; ++it) {
+    const int cur = it & 1;
+    if (it + 1 < DC_KITER) fetch(it + 1, cur ^ 1);
+    const int key = key0 + it * 8;
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) s += q[i] * kr[cur][i];
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    if (key < len) {
+      s *= a.scale_log2;
+      const float mn = fmaxf(m, s);
+      const float alpha = fast_exp2(m - mn);  // m = -inf on the first key: 0
+      const float p = fast_exp2(s - mn);
+      l = l * alpha + p;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) o[i] = o[i] * alpha + p * vr[cur][i];
+      m = mn;
     }
   }
-  // Sum over the 8 key groups of the wave (lanes with equal e).
+
+  // Merge the 8 key groups of the wave (lanes with equal e).
 #pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    o[i] += __shfl_xor(o[i], 8);
-    o[i] += __shfl_xor(o[i], 16);
-    o[i] += __shfl_xor(o[i], 32);
+  for (int off = 8; off < 64; off <<= 1) {
+    float o2[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) o2[i] = __shfl_xor(o[i], off);
+    merge_state<EPL>(m, l, o, __shfl_xor(m, off), __shfl_xor(l, off), o2);
   }
-  lsum += __shfl_xor(lsum, 8);
-  lsum += __shfl_xor(lsum, 16);
-  lsum += __shfl_xor(lsum, 32);
+  if (lane == 0) {
+    red_m[wave] = m;
+    red_l[wave] = l;
+  }
+  __syncthreads();
+  // Rescale each wave's output to the workgroup max before the LDS sum.
+  const float M = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+  const float mu = M == -INFINITY ? 0.f : M;
+  const float aw = fast_exp2(m - mu);
   if (g == 0) {
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) red_o[wave][e * EPL + i] = o[i];
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int c = 0; c < VW; ++c) red_o[wave][VW * e + 8 * VW * i + c] = o[VW * i + c] * aw;
   }
-  if (lane == 0) red_l[wave] = lsum;
   __syncthreads();
   for (int d = threadIdx.x; d < HD; d += DC_THREADS)
     part[d] = red_o[0][d] + red_o[1][d] + red_o[2][d] + red_o[3][d];
   if (threadIdx.x == 0) {
+    float L = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) L += red_l[w] * fast_exp2(red_m[w] - mu);
     part[HD] = M;
-    part[HD + 1] = red_l[0] + red_l[1] + red_l[2] + red_l[3];
+    part[HD + 1] = L;
   }
 }
 
