@@ -43,6 +43,11 @@ METRIC = "attn fwd TFLOP/s (% fp32 MFMA peak) @seq4096; decode HBM GB/s @KV8192"
 FP32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense fp32 matrix, AMD published
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, AMD published
 
+# HBM bytes per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded in
+# profiles/mha_c3_decode_c4_hbm_traffic.md (FETCH_SIZE scaled by 1.99915, the factor a
+# 64 MiB device copy reads on that counter; WRITE_SIZE by 1.0).
+TRAFFIC_BYTES = {"flash_c3": 273834340, "decode_c4": 8644067896}
+
 # c3: one MHA layer of the long-context stack
 C3 = dict(batch=4, seq=4096, dim=1024, heads=16)
 # c4: decode step
@@ -273,7 +278,8 @@ def main():
                        "out_proj": round(mha["out_ms"], 4), "step_events": round(mha["dev_ms"], 4)},
         "roofline": {"kernel": "flash_fwd_kernel (cdml_sdpa_fwd, c3)", "bound": "mfma",
                      "achieved": round(flash_tflops, 3), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(flash_tflops / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                     "frac": round(flash_tflops / FP32_MFMA_PEAK_TFLOPS, 4),
+                     "traffic": TRAFFIC_BYTES["flash_c3"],
                      "algorithmic_per_launch": core},
         "device": {k: info[k] for k in ("name", "arch", "compute_units", "max_clock_mhz")},
     }
@@ -286,7 +292,8 @@ def main():
                          "ms": round(dec["ms"], 4), "tokens_per_s": round(C4["batch"] / (dec["ms"] * 1e-3), 1),
                          "roofline": {"kernel": "decode_split_kernel + decode_combine_kernel", "bound": "hbm",
                                       "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                                      "frac": round(gbs / HBM_PEAK_GBS, 4),
+                                      "traffic": TRAFFIC_BYTES["decode_c4"],
                                       "algorithmic_per_launch": nbytes}}
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (multi-threaded restatement)")
