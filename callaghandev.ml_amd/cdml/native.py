@@ -58,6 +58,9 @@ SIGNATURES = {
     "cdml_memcpy_d2h_async": [_vp, _vp, _sz, _vp],
     "cdml_memcpy_d2d_async": [_vp, _vp, _sz, _vp],
     "cdml_zero_f32_async": [_vp, _sz, _vp],
+    "cdml_fill_i32_async": [_vp, _sz, _i, _vp],
+    "cdml_memcpy2d_d2d_async": [_vp, _sz, _vp, _sz, _sz, _sz, _vp],
+    "cdml_argmax_rows": [_vp, _i, _i, _i, _vp, _i, _vp],
     "cdml_project_qkv": [_vp] * 10 + [_i, _i, _i, _vp],
     "cdml_linear": [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
     "cdml_rope": [_vp, _i, _i, _i, _i, _i, _f, _i, _i, _i, _vp, _vp],

@@ -127,3 +127,15 @@ def lm_weights(cfg: dict, seed: int, biased: bool = False) -> dict:
             "ffn_w2": xavier_uniform(nxt(), D, FF), "ffn_b2": bias(D),
         })
     return w
+
+
+def random_walk_windows(seed: int, batch: int, length: int, features: int, step: float = 0.02) -> np.ndarray:
+    """float32 [batch, length, features] time-series windows: x_0 ~ U[0, 1],
+    x_t = x_{t-1} + N(0, step^2) per feature, then min-max rescaled to [0, 1]
+    per window and feature (the BASELINE config-5 inputs)."""
+    x0 = uniform(seed, batch * features).reshape(batch, 1, features)
+    steps = normal(seed + 1, (batch, length - 1, features)).astype(np.float64) * step
+    x = np.concatenate([x0, x0 + np.cumsum(steps, axis=1)], axis=1)
+    lo = x.min(axis=1, keepdims=True)
+    hi = x.max(axis=1, keepdims=True)
+    return ((x - lo) / np.where(hi > lo, hi - lo, 1.0)).astype(np.float32)

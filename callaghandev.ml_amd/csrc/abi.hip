@@ -81,6 +81,43 @@ __global__ void embed_kernel(const int *__restrict__ ids, int count,
   }
 }
 
+__global__ void fill_i32_kernel(int *__restrict__ p, size_t n, int value) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) p[i] = value;
+}
+
+// One wave per row: lane-strided scan keeping (max, lowest index), then a
+// butterfly reduction that prefers the larger value and, on ties, the lower
+// index.  NaN never compares greater, so it never wins.
+__global__ void __launch_bounds__(256) argmax_rows_kernel(const float *__restrict__ x, int rows,
+                                                          int cols, int ld, int *__restrict__ out,
+                                                          int out_stride) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float *xr = x + (size_t)row * ld;
+  float best = -INFINITY;
+  int idx = cols;  // sentinel: no finite candidate seen yet
+  for (int c = lane; c < cols; c += 64) {
+    const float v = xr[c];
+    if (v > best || (v == best && c < idx)) {
+      best = v;
+      idx = c;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(best, off);
+    const int oi = __shfl_xor(idx, off);
+    if (ov > best || (ov == best && oi < idx)) {
+      best = ov;
+      idx = oi;
+    }
+  }
+  if (lane == 0) out[(size_t)row * out_stride] = idx < cols ? idx : 0;
+}
+
 __global__ void kv_append_kernel(const float *__restrict__ k_new, const float *__restrict__ v_new,
                                  float *__restrict__ kc, float *__restrict__ vc,
                                  const int *__restrict__ pos, int t_max, int dim) {
@@ -285,6 +322,45 @@ int cdml_zero_f32_async(float *dst, size_t count, cdml_stream stream) {
   if (blocks > 65536) blocks = 65536;
   fill_zero_kernel<<<dim3((unsigned)blocks), dim3(256), 0, as_hip(stream)>>>(dst, count);
   return check_launch("fill_zero_kernel");
+}
+
+int cdml_fill_i32_async(int *dst, size_t count, int value, cdml_stream stream) {
+  if (count == 0) return CDML_OK;
+  if (!dst) return fail(CDML_E_INVALID, "cdml_fill_i32_async: dst is NULL");
+  int rc = ensure_device();
+  if (rc) return rc;
+  size_t blocks = (count + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  fill_i32_kernel<<<dim3((unsigned)blocks), dim3(256), 0, as_hip(stream)>>>(dst, count, value);
+  return check_launch("fill_i32_kernel");
+}
+
+int cdml_memcpy2d_d2d_async(void *dst, size_t dpitch, const void *src, size_t spitch,
+                            size_t width_bytes, size_t height, cdml_stream stream) {
+  if (width_bytes == 0 || height == 0) return CDML_OK;
+  if (!dst || !src) return fail(CDML_E_INVALID, "cdml_memcpy2d_d2d_async: NULL pointer");
+  if (dpitch < width_bytes || spitch < width_bytes)
+    return fail(CDML_E_INVALID, "cdml_memcpy2d_d2d_async: pitch smaller than the row");
+  int rc = ensure_device();
+  if (rc) return rc;
+  hipError_t e = hipMemcpy2DAsync(dst, dpitch, src, spitch, width_bytes, height,
+                                  hipMemcpyDeviceToDevice, as_hip(stream));
+  if (e != hipSuccess) return hip_fail(e, "cdml_memcpy2d_d2d_async");
+  return CDML_OK;
+}
+
+int cdml_argmax_rows(const float *x, int rows, int cols, int ld, int *out, int out_stride,
+                     cdml_stream stream) {
+  if (rows < 0 || cols <= 0 || ld < cols || out_stride < 1)
+    return fail(CDML_E_INVALID, "cdml_argmax_rows: bad size (rows %d, cols %d, ld %d, stride %d)",
+                rows, cols, ld, out_stride);
+  if (rows == 0) return CDML_OK;
+  if (!x || !out) return fail(CDML_E_INVALID, "cdml_argmax_rows: NULL pointer");
+  int rc = ensure_device();
+  if (rc) return rc;
+  argmax_rows_kernel<<<dim3((rows + 3) / 4), dim3(256), 0, as_hip(stream)>>>(x, rows, cols, ld, out,
+                                                                            out_stride);
+  return check_launch("argmax_rows_kernel");
 }
 
 int cdml_embed_tokens(const int *ids, int count, const float *table, int vocab, int dim,

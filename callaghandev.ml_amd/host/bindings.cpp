@@ -1,0 +1,383 @@
+// Python module _cdml_host: the C++ host side (HipAccelerationManager and the
+// MultiTypeTransformer classes) on numpy arrays, for the parity tests, the
+// smoke check and the benchmark.  float32 arrays are passed by pointer; the
+// manager's resident cache keys weights by those pointers exactly as the C#
+// manager keys them by array identity.
+#include <pybind11/numpy.h>
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+
+#include <cstring>
+
+#include "cdml_host.h"
+
+namespace py = pybind11;
+using namespace cdml_host;
+
+namespace {
+
+using F32 = py::array_t<float, py::array::c_style | py::array::forcecast>;
+using I32 = py::array_t<int, py::array::c_style | py::array::forcecast>;
+using U8 = py::array_t<uint8_t, py::array::c_style | py::array::forcecast>;
+
+// Arrays handed to the C++ side stay alive for the duration of the call
+// through these holders.
+struct MatArg {
+  F32 arr;
+  MatView view;
+};
+
+MatArg mat(const py::object &o) {
+  MatArg a;
+  if (o.is_none()) return a;
+  a.arr = F32::ensure(o);
+  if (!a.arr) throw ArgumentException("expected a float32 matrix");
+  if (a.arr.ndim() != 2) throw ArgumentException("expected a 2-D array");
+  a.view = MatView(a.arr.data(), (int)a.arr.shape(0), (int)a.arr.shape(1));
+  return a;
+}
+
+struct VecArg {
+  F32 arr;
+  VecView view;
+};
+
+VecArg vec(const py::object &o) {
+  VecArg a;
+  if (o.is_none()) return a;
+  a.arr = F32::ensure(o);
+  if (!a.arr) throw ArgumentException("expected a float32 vector");
+  if (a.arr.ndim() != 1) throw ArgumentException("expected a 1-D array");
+  a.view = VecView(a.arr.data(), (int)a.arr.shape(0));
+  return a;
+}
+
+struct MaskArg {
+  U8 arr;
+  MaskView view;
+};
+
+MaskArg mask(const py::object &o) {
+  MaskArg a;
+  if (o.is_none()) return a;
+  a.arr = U8::ensure(o);
+  if (!a.arr || a.arr.ndim() != 2) throw ArgumentException("expected a 2-D bool mask", "mask");
+  a.view.data = a.arr.data();
+  a.view.rows = (int)a.arr.shape(0);
+  a.view.cols = (int)a.arr.shape(1);
+  return a;
+}
+
+// In-place arguments must be writable float32 C-contiguous arrays (no copy).
+MatRef mat_inplace(py::array &a) {
+  if (!(a.flags() & py::array::c_style) || !a.dtype().is(py::dtype::of<float>()) || a.ndim() != 2 ||
+      !a.writeable())
+    throw ArgumentException("in-place argument must be a writable float32 C-contiguous matrix");
+  return MatRef(static_cast<float *>(a.mutable_data()), (int)a.shape(0), (int)a.shape(1));
+}
+
+py::array_t<float> to_numpy(Matrix &&m) {
+  auto *v = new std::vector<float>(std::move(m.data));
+  py::capsule owner(v, [](void *p) { delete static_cast<std::vector<float> *>(p); });
+  return py::array_t<float>({(py::ssize_t)m.rows, (py::ssize_t)m.cols},
+                            {(py::ssize_t)(m.cols * sizeof(float)), (py::ssize_t)sizeof(float)}, v->data(),
+                            owner);
+}
+
+Matrix from_numpy(const py::object &o) {
+  MatArg a = mat(o);
+  if (a.view.null()) throw ArgumentNullException("matrix");
+  Matrix m(a.view.rows, a.view.cols);
+  std::memcpy(m.ptr(), a.view.data, m.data.size() * sizeof(float));
+  return m;
+}
+
+std::vector<float> vec_from_numpy(const py::object &o) {
+  VecArg a = vec(o);
+  if (a.view.null()) throw ArgumentNullException("vector");
+  return std::vector<float>(a.view.data, a.view.data + a.view.length);
+}
+
+// Weights in the layout of cdml.synth.lm_weights.
+void load_weights(LanguageModel &lm, const py::dict &w) {
+  auto get = [&](const py::dict &d, const char *k) -> py::object {
+    if (!d.contains(k)) throw ArgumentException(std::string("missing weight '") + k + "'");
+    return d[k];
+  };
+  auto assign_mat = [](Matrix &dst, const py::object &o, const char *name) {
+    Matrix m = from_numpy(o);
+    if (m.rows != dst.rows || m.cols != dst.cols)
+      throw ArgumentException(std::string("shape mismatch for ") + name);
+    dst = std::move(m);
+  };
+  auto assign_vec = [](std::vector<float> &dst, const py::object &o, const char *name) {
+    std::vector<float> v = vec_from_numpy(o);
+    if (v.size() != dst.size()) throw ArgumentException(std::string("length mismatch for ") + name);
+    dst = std::move(v);
+  };
+  const TransformerConfig &c = lm.config();
+  if (c.UsesDiscreteTokens) {
+    assign_mat(lm.TokenEmbedding, get(w, "token_embedding"), "token_embedding");
+  } else {
+    assign_mat(lm.InputProjection, get(w, "input_proj"), "input_proj");
+    assign_vec(lm.InputProjectionBias, get(w, "input_bias"), "input_bias");
+  }
+  assign_mat(lm.OutputProjection, get(w, "out_proj"), "out_proj");
+  assign_vec(lm.OutputBias, get(w, "out_bias"), "out_bias");
+  py::list layers = get(w, "layers");
+  if ((int)py::len(layers) != c.NumLayers) throw ArgumentException("layer count mismatch");
+  for (int i = 0; i < c.NumLayers; ++i) {
+    py::dict L = layers[i];
+    TransformerBlock &b = lm.Blocks[i];
+    assign_mat(b.Attention.WQ, get(L, "wq"), "wq");
+    assign_mat(b.Attention.WK, get(L, "wk"), "wk");
+    assign_mat(b.Attention.WV, get(L, "wv"), "wv");
+    assign_mat(b.Attention.WO, get(L, "wo"), "wo");
+    assign_vec(b.Attention.BiasQ, get(L, "bq"), "bq");
+    assign_vec(b.Attention.BiasK, get(L, "bk"), "bk");
+    assign_vec(b.Attention.BiasV, get(L, "bv"), "bv");
+    assign_vec(b.Attention.BiasO, get(L, "bo"), "bo");
+    assign_vec(b.LN1Gamma, get(L, "ln1_g"), "ln1_g");
+    assign_vec(b.LN1Beta, get(L, "ln1_b"), "ln1_b");
+    assign_vec(b.LN2Gamma, get(L, "ln2_g"), "ln2_g");
+    assign_vec(b.LN2Beta, get(L, "ln2_b"), "ln2_b");
+    assign_mat(b.FeedForward.weights[0], get(L, "ffn_w1"), "ffn_w1");
+    assign_vec(b.FeedForward.biases[0], get(L, "ffn_b1"), "ffn_b1");
+    assign_mat(b.FeedForward.weights[1], get(L, "ffn_w2"), "ffn_w2");
+    assign_vec(b.FeedForward.biases[1], get(L, "ffn_b2"), "ffn_b2");
+  }
+}
+
+std::vector<int> ids_from(const py::object &o) {
+  I32 a = I32::ensure(o);
+  if (!a) throw ArgumentNullException("tokenIds");
+  return std::vector<int>(a.data(), a.data() + a.size());
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_cdml_host, m) {
+  m.doc() = "C++ host side of the gfx950 attention path (HipAccelerationManager and models)";
+
+  auto arg_exc = py::register_exception<ArgumentException>(m, "ArgumentException", PyExc_ValueError);
+  py::register_exception<ArgumentNullException>(m, "ArgumentNullException", arg_exc.ptr());
+  py::register_exception<ArgumentOutOfRangeException>(m, "ArgumentOutOfRangeException", arg_exc.ptr());
+  py::register_exception<InvalidOperationException>(m, "InvalidOperationException", PyExc_RuntimeError);
+
+  py::class_<HipAccelerationManager>(m, "HipAccelerationManager")
+      .def(py::init<int>(), py::arg("device") = 0)
+      .def("ProjectQKV",
+           [](HipAccelerationManager &a, py::object x, py::object wq, py::object bq, py::object wk,
+              py::object bk, py::object wv, py::object bv) {
+             auto X = mat(x), WQ = mat(wq), WK = mat(wk), WV = mat(wv);
+             auto BQ = vec(bq), BK = vec(bk), BV = vec(bv);
+             auto r = a.ProjectQKV(X.view, WQ.view, BQ.view, WK.view, BK.view, WV.view, BV.view);
+             return py::make_tuple(to_numpy(std::move(std::get<0>(r))), to_numpy(std::move(std::get<1>(r))),
+                                   to_numpy(std::move(std::get<2>(r))));
+           })
+      .def("ScaledDotProductAttention",
+           [](HipAccelerationManager &a, py::object q, py::object k, py::object v, int numHeads,
+              py::object msk, bool causal) {
+             auto Q = mat(q), K = mat(k), V = mat(v);
+             auto M = mask(msk);
+             return to_numpy(a.ScaledDotProductAttention(Q.view, K.view, V.view, numHeads, M.view, causal));
+           },
+           py::arg("q"), py::arg("k"), py::arg("v"), py::arg("numHeads"), py::arg("mask") = py::none(),
+           py::arg("causal") = false)
+      .def("MultiHeadAttentionForward",
+           [](HipAccelerationManager &a, py::object q, py::object k, py::object v, int numHeads,
+              float scale, py::object msk) {
+             auto Q = mat(q), K = mat(k), V = mat(v);
+             auto M = mask(msk);
+             return to_numpy(a.MultiHeadAttentionForward(Q.view, K.view, V.view, numHeads, scale, M.view));
+           },
+           py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("numHeads"), py::arg("scale"),
+           py::arg("mask") = py::none())
+      .def("ProjectOutputBatch",
+           [](HipAccelerationManager &a, py::object h, py::object w, py::object b, int seqLen, int outputDim) {
+             auto Hh = mat(h), W = mat(w);
+             auto B = vec(b);
+             return to_numpy(a.ProjectOutputBatch(Hh.view, W.view, B.view, seqLen, outputDim));
+           })
+      .def("BatchDotProductAddBias",
+           [](HipAccelerationManager &a, py::object w, py::object x, py::object b) {
+             auto W = mat(w), X = mat(x);
+             auto B = vec(b);
+             return to_numpy(a.BatchDotProductAddBias(W.view, X.view, B.view));
+           })
+      .def("BatchDotProductAddBias",
+           [](HipAccelerationManager &a, py::object w, py::object x, int rowStart, int rowCount, py::object b) {
+             auto W = mat(w), X = mat(x);
+             auto B = vec(b);
+             return to_numpy(a.BatchDotProductAddBias(W.view, X.view, rowStart, rowCount, B.view));
+           })
+      .def("ApplyRotaryPositionEmbeddingInPlace",
+           [](HipAccelerationManager &a, py::object mtx, int numHeads, float baseTheta, bool inverse) {
+             if (mtx.is_none()) throw ArgumentNullException("matrix");
+             py::array arr = mtx;
+             a.ApplyRotaryPositionEmbeddingInPlace(mat_inplace(arr), numHeads, baseTheta, inverse);
+           })
+      .def("ApplyRotaryPositionEmbeddingHeadInPlace",
+           [](HipAccelerationManager &a, py::object mtx, int startCol, int headDim, float baseTheta,
+              bool inverse) {
+             if (mtx.is_none()) throw ArgumentNullException("matrix");
+             py::array arr = mtx;
+             a.ApplyRotaryPositionEmbeddingHeadInPlace(mat_inplace(arr), startCol, headDim, baseTheta, inverse);
+           })
+      .def("ResidualLayerNorm",
+           [](HipAccelerationManager &a, py::object x, py::object s, py::object g, py::object b, float eps) {
+             auto X = mat(x), S = mat(s);
+             auto G = vec(g), B = vec(b);
+             return to_numpy(a.ResidualLayerNorm(X.view, S.view, G.view, B.view, eps));
+           },
+           py::arg("input"), py::arg("subLayer"), py::arg("gamma"), py::arg("beta"), py::arg("epsilon") = 1e-5f)
+      .def("EmbedTokenIds",
+           [](HipAccelerationManager &a, py::object ids, py::object emb, int dim) {
+             if (ids.is_none()) throw ArgumentNullException("tokenIds");
+             auto E = mat(emb);
+             return to_numpy(a.EmbedTokenIds(ids_from(ids), E.view, dim));
+           })
+      .def("EmbedTokenIds",
+           [](HipAccelerationManager &a, py::object ids, int start, int count, py::object emb, int dim) {
+             if (ids.is_none()) throw ArgumentNullException("tokenIds");
+             auto E = mat(emb);
+             return to_numpy(a.EmbedTokenIds(ids_from(ids), start, count, E.view, dim));
+           })
+      .def("CreateCausalMask",
+           [](HipAccelerationManager &a, int n) {
+             BoolMatrix b = a.CreateCausalMask(n);
+             py::array_t<bool> out({(py::ssize_t)b.rows, (py::ssize_t)b.cols});
+             std::memcpy(out.mutable_data(), b.data.data(), b.data.size());
+             return out;
+           })
+      .def("FFNForwardBatch",
+           [](HipAccelerationManager &a, py::object x, int seqLen, int outputDim, py::list ws, py::list bs,
+              std::vector<int> acts) {
+             auto X = mat(x);
+             FeedForwardNetwork ffn;
+             for (auto w : ws) ffn.weights.push_back(from_numpy(py::reinterpret_borrow<py::object>(w)));
+             for (auto b : bs) ffn.biases.push_back(vec_from_numpy(py::reinterpret_borrow<py::object>(b)));
+             ffn.activations = acts;
+             if (ffn.biases.size() != ffn.weights.size() || ffn.activations.size() != ffn.weights.size())
+               throw ArgumentException("FFN weights, biases and activations must have equal counts");
+             return to_numpy(a.FFNForwardBatch(X.view, seqLen, outputDim, ffn));
+           })
+      .def("DecodeSelfAttention",
+           [](HipAccelerationManager &a, py::array q, py::array k, py::object v, py::array keys,
+              py::array values, int pos, int numHeads) {
+             auto V = mat(v);
+             return to_numpy(a.DecodeSelfAttention(mat_inplace(q), mat_inplace(k), V.view, mat_inplace(keys),
+                                                   mat_inplace(values), pos, numHeads));
+           })
+      .def("Dispose", &HipAccelerationManager::Dispose);
+
+  py::class_<TransformerConfig>(m, "TransformerConfig")
+      .def(py::init<>())
+      .def_readwrite("VocabSize", &TransformerConfig::VocabSize)
+      .def_readwrite("MaxSequenceLength", &TransformerConfig::MaxSequenceLength)
+      .def_readwrite("EmbeddingDim", &TransformerConfig::EmbeddingDim)
+      .def_readwrite("NumHeads", &TransformerConfig::NumHeads)
+      .def_readwrite("NumLayers", &TransformerConfig::NumLayers)
+      .def_readwrite("FeedForwardDim", &TransformerConfig::FeedForwardDim)
+      .def_readwrite("UseDecoderOnly", &TransformerConfig::UseDecoderOnly)
+      .def_readwrite("UsesDiscreteTokens", &TransformerConfig::UsesDiscreteTokens)
+      .def_readwrite("InputFeatureDim", &TransformerConfig::InputFeatureDim)
+      .def_readwrite("OutputDim", &TransformerConfig::OutputDim)
+      .def_readwrite("FFNActivationType", &TransformerConfig::FFNActivationType)
+      .def("Validate", &TransformerConfig::Validate);
+
+  py::class_<LanguageModel>(m, "LanguageModel")
+      .def(py::init<const TransformerConfig &, HipAccelerationManager *>(), py::keep_alive<1, 3>())
+      .def("load_weights", &load_weights)
+      .def("Forward", [](LanguageModel &lm, py::object ids) { return to_numpy(lm.Forward(ids_from(ids))); })
+      .def("ForwardContinuous",
+           [](LanguageModel &lm, py::object x) {
+             auto X = mat(x);
+             return to_numpy(lm.Forward(X.view));
+           })
+      .def("PredictNext",
+           [](LanguageModel &lm, py::object x) {
+             auto X = mat(x);
+             return lm.PredictNext(X.view);
+           })
+      .def("Generate",
+           [](LanguageModel &lm, py::object prompt, int maxNew, float temperature, bool greedy, uint64_t seed) {
+             return lm.Generate(ids_from(prompt), maxNew, temperature, greedy, seed);
+           },
+           py::arg("prompt"), py::arg("maxNewTokens"), py::arg("temperature") = 1.0f,
+           py::arg("greedy") = true, py::arg("seed") = 0);
+
+  py::class_<DeviceLanguageModel>(m, "DeviceLanguageModel")
+      .def(py::init<const LanguageModel &, int, int>(), py::arg("model"), py::arg("batch_capacity"),
+           py::arg("device") = 0)
+      .def("Forward",
+           [](DeviceLanguageModel &d, py::object ids) {
+             I32 a = I32::ensure(ids);
+             if (!a || a.ndim() != 2) throw ArgumentException("ids must be [batch, seqLen]", "ids");
+             std::vector<int> v(a.data(), a.data() + a.size());
+             return to_numpy(d.Forward(v, (int)a.shape(0), (int)a.shape(1)));
+           })
+      .def("ForwardContinuous",
+           [](DeviceLanguageModel &d, py::object x, int batch, int seqLen) {
+             auto X = mat(x);
+             return to_numpy(d.ForwardContinuous(X.view, batch, seqLen));
+           })
+      .def("GenerateGreedy",
+           [](DeviceLanguageModel &d, py::object prompts, int maxNew) {
+             I32 a = I32::ensure(prompts);
+             if (!a || a.ndim() != 2) throw ArgumentException("prompts must be [batch, promptLen]", "prompts");
+             std::vector<int> v(a.data(), a.data() + a.size());
+             int total = 0;
+             std::vector<int> out = d.GenerateGreedy(v, (int)a.shape(0), (int)a.shape(1), maxNew, &total);
+             py::array_t<int> r({(py::ssize_t)a.shape(0), (py::ssize_t)total});
+             std::memcpy(r.mutable_data(), out.data(), out.size() * sizeof(int));
+             return r;
+           })
+      .def("time_forward",
+           // Device-resident forward of `batch` sequences of `seqLen` inputs
+           // that are already in HBM: returns the mean ms of `steps` launches
+           // (HIP events on the model's stream) after `warmup` untimed ones.
+           [](DeviceLanguageModel &d, py::object inputs, int batch, int seqLen, int steps, int warmup,
+              bool continuous) {
+             void *din = nullptr, *dout = nullptr;
+             auto chk = [](int rc) {
+               if (rc != CDML_OK) throw InvalidOperationException(cdml_last_error());
+             };
+             if (batch <= 0 || batch > d.batch_capacity()) throw ArgumentOutOfRangeException("batch");
+             py::array arr = inputs;
+             const size_t need = (size_t)batch * seqLen * (continuous ? sizeof(float) : sizeof(int));
+             if (!(arr.flags() & py::array::c_style) || (size_t)arr.nbytes() < need ||
+                 arr.itemsize() != 4)
+               throw ArgumentException("inputs must be a C-contiguous 4-byte array of batch * seqLen rows",
+                                       "inputs");
+             chk(cdml_malloc(&din, arr.nbytes()));
+             chk(cdml_memcpy_h2d_async(din, arr.data(), arr.nbytes(), d.stream()));
+             chk(cdml_malloc(&dout, (size_t)batch * seqLen * d.output_dim() * sizeof(float)));
+             cdml_event e0, e1;
+             chk(cdml_event_create(&e0));
+             chk(cdml_event_create(&e1));
+             float ms = 0.f;
+             {
+               py::gil_scoped_release nogil;
+               for (int i = 0; i < warmup; ++i)
+                 d.forward_device(continuous ? nullptr : static_cast<int *>(din),
+                                  continuous ? static_cast<float *>(din) : nullptr, batch, seqLen,
+                                  static_cast<float *>(dout));
+               d.synchronize();
+               chk(cdml_event_record(e0, d.stream()));
+               for (int i = 0; i < steps; ++i)
+                 d.forward_device(continuous ? nullptr : static_cast<int *>(din),
+                                  continuous ? static_cast<float *>(din) : nullptr, batch, seqLen,
+                                  static_cast<float *>(dout));
+               chk(cdml_event_record(e1, d.stream()));
+               chk(cdml_event_elapsed_ms(e0, e1, &ms));
+             }
+             cdml_event_destroy(e0);
+             cdml_event_destroy(e1);
+             cdml_free(din);
+             cdml_free(dout);
+             return ms / std::max(steps, 1);
+           },
+           py::arg("inputs"), py::arg("batch"), py::arg("seqLen"), py::arg("steps") = 10,
+           py::arg("warmup") = 2, py::arg("continuous") = false);
+}

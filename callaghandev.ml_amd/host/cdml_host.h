@@ -1,0 +1,356 @@
+// Host side of the MI355X attention path, above the C ABI of include/cdml.h.
+//
+// HipAccelerationManager mirrors the hot-path methods of the reference's
+// IAccelerationManager (CallaghanDev.ML/AccelerationManagers/
+// IAccelerationManager.cs): same method names, same argument meaning, same
+// validation order and the same exception kinds (ArgumentNullException,
+// ArgumentOutOfRangeException, ArgumentException, InvalidOperationException),
+// host arrays in and host arrays out.  It is what a C# HipAccelerationManager
+// does through P/Invoke: the manager owns its stream, device buffers and a
+// resident copy of every weight array it has seen (identity-keyed, with a
+// shadow compare, as AccelerationManagers/GPU/DeviceResidentCache.cs:44-120).
+//
+// MultiHeadAttention, TransformerBlock and LanguageModel restate the
+// reference's Transformers/MultiTypeTransformer classes on top of the manager,
+// so the reference's call sequence (ProjectQKV -> RoPE -> ScaledDotProduct-
+// Attention -> ProjectOutputBatch -> ResidualLayerNorm -> FFN -> ...) runs
+// unchanged against the HIP kernels.
+//
+// DeviceLanguageModel is the device-resident engine for the same model: all
+// weights and activations stay in HBM, a whole batch of sequences runs per
+// launch, prompts are prefilled in one pass, and greedy generation keeps its
+// KV cache and its chosen tokens on the device.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <tuple>
+#include <unordered_map>
+#include <vector>
+
+#include "cdml.h"
+
+namespace cdml_host {
+
+// ---- exceptions named after the .NET ones the reference throws -----------
+struct ArgumentException : std::invalid_argument {
+  std::string param;
+  explicit ArgumentException(const std::string &msg, const std::string &p = "")
+      : std::invalid_argument(p.empty() ? msg : msg + " (Parameter '" + p + "')"), param(p) {}
+};
+struct ArgumentNullException : ArgumentException {
+  explicit ArgumentNullException(const std::string &p)
+      : ArgumentException("Value cannot be null.", p) {}
+};
+struct ArgumentOutOfRangeException : ArgumentException {
+  explicit ArgumentOutOfRangeException(const std::string &p, const std::string &msg = "")
+      : ArgumentException(msg.empty() ? "Specified argument was out of the range of valid values."
+                                      : msg,
+                          p) {}
+};
+struct InvalidOperationException : std::logic_error {
+  explicit InvalidOperationException(const std::string &msg) : std::logic_error(msg) {}
+};
+
+// ---- host arrays (row-major, the float[,] layout) ------------------------
+struct Matrix {
+  int rows = 0, cols = 0;
+  std::vector<float> data;
+  Matrix() = default;
+  Matrix(int r, int c) : rows(r), cols(c), data((size_t)r * c, 0.f) {}
+  float *ptr() { return data.data(); }
+  const float *ptr() const { return data.data(); }
+  float &at(int r, int c) { return data[(size_t)r * cols + c]; }
+  float at(int r, int c) const { return data[(size_t)r * cols + c]; }
+};
+
+// Non-owning views; `data == nullptr` plays the role of a null reference.
+struct MatView {
+  const float *data = nullptr;
+  int rows = 0, cols = 0;
+  MatView() = default;
+  MatView(const float *d, int r, int c) : data(d), rows(r), cols(c) {}
+  MatView(const Matrix &m) : data(m.ptr()), rows(m.rows), cols(m.cols) {}  // NOLINT
+  bool null() const { return data == nullptr; }
+};
+struct MatRef {
+  float *data = nullptr;
+  int rows = 0, cols = 0;
+  MatRef() = default;
+  MatRef(float *d, int r, int c) : data(d), rows(r), cols(c) {}
+  MatRef(Matrix &m) : data(m.ptr()), rows(m.rows), cols(m.cols) {}  // NOLINT
+};
+struct VecView {
+  const float *data = nullptr;
+  int length = 0;
+  VecView() = default;
+  VecView(const float *d, int n) : data(d), length(n) {}
+  VecView(const std::vector<float> &v) : data(v.data()), length((int)v.size()) {}  // NOLINT
+  bool null() const { return data == nullptr; }
+};
+struct MaskView {  // bool[Lq, Lk], nonzero = attend
+  const uint8_t *data = nullptr;
+  int rows = 0, cols = 0;
+  bool null() const { return data == nullptr; }
+};
+struct BoolMatrix {
+  int rows = 0, cols = 0;
+  std::vector<uint8_t> data;
+};
+
+// FFN activations, numbered as the reference's Enums/ActivationType.cs:7-15.
+enum ActivationType { None = 0, Sigmoid = 1, Tanh = 2, Relu = 3, Leakyrelu = 4, Swish = 5 };
+
+// The transformer FFN: a NeuralNetwork with layer widths [D, FF, D] and
+// activations [None, act, None] (TransformerBlock.cs:101-123).  Layer i
+// (i >= 1) maps with weights[i-1] [width_i, width_{i-1}] and biases[i-1],
+// then applies activations[i-1] (NeuralNetwork.cs:629-668).
+struct FeedForwardNetwork {
+  std::vector<Matrix> weights;
+  std::vector<std::vector<float>> biases;
+  std::vector<int> activations;
+  int input_size() const { return weights.empty() ? 0 : weights.front().cols; }
+  int output_size() const { return weights.empty() ? 0 : weights.back().rows; }
+};
+
+// ---- the manager -----------------------------------------------------------
+class HipAccelerationManager {
+ public:
+  explicit HipAccelerationManager(int device = 0);
+  ~HipAccelerationManager();
+  HipAccelerationManager(const HipAccelerationManager &) = delete;
+  HipAccelerationManager &operator=(const HipAccelerationManager &) = delete;
+
+  // IAccelerationManager.ProjectQKV (IAccelerationManager.cs:169)
+  std::tuple<Matrix, Matrix, Matrix> ProjectQKV(MatView input, MatView WQ, VecView biasQ,
+                                                MatView WK, VecView biasK, MatView WV,
+                                                VecView biasV);
+  // IAccelerationManager.ScaledDotProductAttention (:167)
+  Matrix ScaledDotProductAttention(MatView q, MatView k, MatView v, int numHeads,
+                                   MaskView mask = {}, bool causal = false);
+  // IAccelerationManager.MultiHeadAttentionForward (:155)
+  Matrix MultiHeadAttentionForward(MatView Q, MatView K, MatView V, int numHeads, float scale,
+                                   MaskView mask = {});
+  // IAccelerationManager.ProjectOutputBatch (:259)
+  Matrix ProjectOutputBatch(MatView hidden, MatView outputProjection, VecView outputBias,
+                            int seqLen, int outputDim);
+  // IAccelerationManager.BatchDotProductAddBias (:45-50), both overloads
+  Matrix BatchDotProductAddBias(MatView weights, MatView inputMatrix, VecView bias);
+  Matrix BatchDotProductAddBias(MatView weights, MatView inputMatrix, int rowStart, int rowCount,
+                                VecView bias);
+  // IAccelerationManager.ApplyRotaryPositionEmbeddingInPlace / HeadInPlace (:319-320)
+  void ApplyRotaryPositionEmbeddingInPlace(MatRef matrix, int numHeads, float baseTheta,
+                                           bool inverse);
+  void ApplyRotaryPositionEmbeddingHeadInPlace(MatRef matrix, int startCol, int headDim,
+                                               float baseTheta, bool inverse);
+  // IAccelerationManager.ResidualLayerNorm (:132)
+  Matrix ResidualLayerNorm(MatView input, MatView subLayer, VecView gamma, VecView beta,
+                           float epsilon = 1e-5f);
+  // IAccelerationManager.EmbedTokenIds (:275-277), both overloads
+  Matrix EmbedTokenIds(const std::vector<int> &tokenIds, MatView embedding, int embeddingDim);
+  Matrix EmbedTokenIds(const std::vector<int> &tokenIds, int tokenStart, int tokenCount,
+                       MatView embedding, int embeddingDim);
+  // IAccelerationManager.CreateCausalMask (:149)
+  BoolMatrix CreateCausalMask(int seqLen);
+  // IAccelerationManager.FFNForwardBatch (:165) with the network the reference
+  // passes as a delegate target (AccelerationCPU.cs:1957-2002 takes the
+  // NeuralNetwork.ForwardPassOnlyBatch route for it).
+  Matrix FFNForwardBatch(MatView input, int seqLen, int outputDim, const FeedForwardNetwork &ffn);
+
+  // Optional decode capability (no IAccelerationManager counterpart: the
+  // reference runs this inline in LanguageModel.DecoderSelfAttentionStep,
+  // LanguageModel.cs:353-427).  q, k, v [1, D] are the step's projections
+  // before RoPE.  On the device: RoPE of q and k at absolutePosition (the
+  // single-row form of LanguageModel.cs:432-480, base 10000), append of k and
+  // v as row absolutePosition of the layer's cache, attention of q over the
+  // absolutePosition + 1 cached keys with scale 1/sqrt(d_h).  q and k are
+  // rotated in place and the host caches keys/values [maxSeq, D] receive the
+  // appended rows, as the reference's cache does.  The device mirror of a
+  // cache is keyed by its keys array; when it does not hold exactly the rows
+  // below absolutePosition it is refreshed from the host arrays.
+  Matrix DecodeSelfAttention(MatRef q, MatRef k, MatView v, MatRef keys, MatRef values,
+                             int absolutePosition, int numHeads);
+
+  void Dispose();
+  bool disposed() const { return disposed_; }
+  cdml_stream stream();  // the manager's own stream (created on first use)
+
+ private:
+  struct Resident {
+    int rows = 0, cols = 0;
+    void *dev = nullptr;
+    std::vector<float> shadow;
+  };
+  struct DeviceBuf {
+    void *p = nullptr;
+    size_t bytes = 0;
+  };
+  struct DecodeMirror {
+    void *k = nullptr, *v = nullptr;
+    int rows = 0, cols = 0, uploaded = 0;
+  };
+
+  void ensure_ready();
+  void *scratch(int slot, size_t bytes);
+  const float *resident(const float *host, int rows, int cols);
+  void upload(void *dev, const void *host, size_t bytes);
+  void download(void *host, const void *dev, size_t bytes);
+  void sync();
+  Matrix attention(MatView q, MatView k, MatView v, int numHeads, float scale, MaskView mask,
+                   bool causal);
+  Matrix linear(MatView x, int rowStart, int rowCount, MatView w, VecView b, int act);
+
+  int device_;
+  bool ready_ = false, disposed_ = false;
+  cdml_stream stream_ = nullptr;
+  std::mutex mu_;
+  std::unordered_map<const float *, Resident> resident_;
+  std::vector<DeviceBuf> scratch_;
+  std::unordered_map<const float *, DecodeMirror> decode_;
+};
+
+// ---- the MultiTypeTransformer classes on the manager ----------------------
+struct TransformerConfig {
+  int VocabSize = 50000;
+  int MaxSequenceLength = 512;
+  int EmbeddingDim = 512;
+  int NumHeads = 8;
+  int NumLayers = 6;
+  int FeedForwardDim = 2048;
+  bool UseDecoderOnly = true;
+  bool UsesDiscreteTokens = true;
+  int InputFeatureDim = 1;
+  int OutputDim = 1;
+  int FFNActivationType = Relu;
+  int EffectiveOutputDim() const { return UsesDiscreteTokens ? VocabSize : OutputDim; }
+  void Validate() const;  // TransformerConfig.cs:62-102
+};
+
+class MultiHeadAttention {  // MultiHeadAttention.cs:6-159
+ public:
+  MultiHeadAttention(int embeddingDim, int numHeads, HipAccelerationManager *accel);
+  Matrix Forward(MatView input, MaskView mask = {}, bool causal = false);
+  Matrix WQ, WK, WV, WO;
+  std::vector<float> BiasQ, BiasK, BiasV, BiasO;
+  int embedding_dim() const { return dim_; }
+  int num_heads() const { return heads_; }
+
+ private:
+  int dim_, heads_, head_dim_;
+  HipAccelerationManager *accel_;
+};
+
+class TransformerBlock {  // TransformerBlock.cs:35-136
+ public:
+  TransformerBlock(int embeddingDim, int numHeads, int feedForwardDim, int ffnActivation,
+                   HipAccelerationManager *accel);
+  Matrix Forward(MatView x, MaskView selfMask = {}, bool causal = false);
+  MultiHeadAttention Attention;
+  FeedForwardNetwork FeedForward;
+  std::vector<float> LN1Gamma, LN1Beta, LN2Gamma, LN2Beta;
+
+ private:
+  HipAccelerationManager *accel_;
+};
+
+// LanguageModel.cs restated: Forward (:112-233) and Generate (:482-537), the
+// latter feeding the prompt token by token through per-layer host KV caches
+// (:270-480) with the attention itself on the manager's decode capability.
+class LanguageModel {
+ public:
+  LanguageModel(const TransformerConfig &cfg, HipAccelerationManager *accel);
+  Matrix Forward(const std::vector<int> &tokenIds);
+  Matrix Forward(MatView inputSequence);  // continuous inputs (InputProjection)
+  // Greedy: argmax with the lowest index on ties.  Otherwise logits / T are
+  // sampled with the SplitMix64 stream seeded by `seed` (the reference uses
+  // System.Random, which this does not reproduce).
+  std::vector<int> Generate(const std::vector<int> &prompt, int maxNewTokens,
+                            float temperature = 1.0f, bool greedy = true, uint64_t seed = 0);
+  std::vector<float> PredictNext(MatView inputSequence);
+  const TransformerConfig &config() const { return cfg_; }
+
+  Matrix TokenEmbedding, InputProjection, OutputProjection;
+  std::vector<float> InputProjectionBias, OutputBias;
+  std::vector<TransformerBlock> Blocks;
+
+ private:
+  struct LayerCache {
+    Matrix Keys, Values;
+    int Length = 0;
+  };
+  Matrix ForwardHidden(Matrix x);
+  Matrix ProjectToOutput(const Matrix &hidden);
+  std::vector<float> ProjectLastTokenOnly(const Matrix &hidden);
+  Matrix DecoderTokenStep(int tokenId, int absolutePosition, std::vector<LayerCache> &caches);
+  Matrix DecoderSelfAttentionStep(MultiHeadAttention &attn, const Matrix &input,
+                                  int absolutePosition, LayerCache &cache);
+  int NextToken(const std::vector<float> &logits, float temperature, bool greedy,
+                uint64_t &rng_state) const;
+  void ValidateTokenSequence(const std::vector<int> &ids) const;
+
+  TransformerConfig cfg_;
+  HipAccelerationManager *accel_;
+};
+
+// ---- device-resident engine ----------------------------------------------
+class DeviceLanguageModel {
+ public:
+  // Uploads every weight of `model` once; the model's arrays are not read
+  // again.  batch_capacity / the config's MaxSequenceLength size the HBM
+  // activations and the KV caches.
+  DeviceLanguageModel(const LanguageModel &model, int batch_capacity, int device = 0);
+  ~DeviceLanguageModel();
+  DeviceLanguageModel(const DeviceLanguageModel &) = delete;
+  DeviceLanguageModel &operator=(const DeviceLanguageModel &) = delete;
+
+  // Discrete tokens: ids [batch, seqLen] -> logits [batch * seqLen, outputDim].
+  Matrix Forward(const std::vector<int> &ids, int batch, int seqLen);
+  // Continuous inputs: x [batch * seqLen, InputFeatureDim] -> [batch * seqLen, outputDim].
+  Matrix ForwardContinuous(MatView x, int batch, int seqLen);
+  // Greedy generation for `batch` prompts of equal length promptLen (ids
+  // [batch, promptLen]); returns [batch, promptLen + n] with n =
+  // min(maxNewTokens, MaxSequenceLength - promptLen) (0 when promptLen >=
+  // MaxSequenceLength), the count the reference's Generate produces.
+  std::vector<int> GenerateGreedy(const std::vector<int> &prompts, int batch, int promptLen,
+                                  int maxNewTokens, int *outLen);
+  // Enqueue-only forms over device pointers for benchmarking.
+  void forward_device(const int *dev_ids, const float *dev_x, int batch, int seqLen,
+                      float *dev_out);
+  cdml_stream stream() const { return stream_; }
+  int output_dim() const { return cfg_.EffectiveOutputDim(); }
+  int batch_capacity() const { return cap_; }
+  void synchronize();
+
+ private:
+  struct Layer {
+    float *wq, *wk, *wv, *wo, *bq, *bk, *bv, *bo;
+    float *ln1g, *ln1b, *ln2g, *ln2b;
+    std::vector<float *> ffw, ffb;
+    std::vector<int> ffrows, ffcols, ffact;
+    float *kcache, *vcache;  // [batch_capacity, maxSeq, D]
+  };
+  float *alloc(size_t floats);
+  float *upload(const float *host, size_t floats);
+  void hidden_pass(float *x, int batch, int seqLen, bool fill_cache);
+  void decode_step(const int *dev_tok, int batch, int pos, float *x);
+
+  TransformerConfig cfg_;
+  int cap_, device_;
+  cdml_stream stream_ = nullptr;
+  std::vector<void *> allocs_;
+  std::vector<Layer> layers_;
+  float *emb_ = nullptr, *inproj_ = nullptr, *inbias_ = nullptr, *outproj_ = nullptr,
+        *outbias_ = nullptr;
+  // activations [cap * maxSeq, width]
+  float *x_, *q_, *k_, *v_, *att_, *proj_, *h_, *ff_, *ff2_, *logits_;
+  int *ids_, *pos_, *kvlen_, *gen_;
+  void *ws_ = nullptr;
+  size_t ws_bytes_ = 0;
+  int ff_max_ = 0;
+};
+
+}  // namespace cdml_host

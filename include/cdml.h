@@ -95,6 +95,14 @@ int cdml_memcpy_d2h_async(void *dst, const void *src, size_t bytes, cdml_stream 
 int cdml_memcpy_d2d_async(void *dst, const void *src, size_t bytes, cdml_stream stream);
 /* Zero `count` floats with a fill kernel (safe under stream capture). */
 int cdml_zero_f32_async(float *dst, size_t count, cdml_stream stream);
+/* dst[i] = value for i < count, a fill kernel (safe under stream capture). */
+int cdml_fill_i32_async(int *dst, size_t count, int value, cdml_stream stream);
+/* Strided device copy: `height` rows of `width_bytes` bytes, row pitches in
+ * bytes (used to place a [batch, len, dim] block into a [batch, t_max, dim]
+ * decode cache). */
+int cdml_memcpy2d_d2d_async(void *dst, size_t dpitch, const void *src,
+                            size_t spitch, size_t width_bytes, size_t height,
+                            cdml_stream stream);
 
 /* ---- hot-path kernels (device pointers) -------------------------------- */
 
@@ -187,6 +195,15 @@ int cdml_residual_layernorm(const float *a, const float *b, const float *gamma,
  * bad_count (device int32) is non-NULL, increments it. */
 int cdml_embed_tokens(const int *ids, int count, const float *table, int vocab,
                       int dim, float *out, int *bad_count, cdml_stream stream);
+
+/* Greedy next-token choice over logits x [rows, cols] (row stride ld):
+ * out[i * out_stride] = the lowest column index holding the row maximum
+ * (NaN entries never win).  The reference always samples
+ * (LanguageModel.SampleFromLogits, LanguageModel.cs:551-584); this is the
+ * deterministic argmax the greedy-generation parity checks use, kept on the
+ * device so a generation loop needs no host round trip per token. */
+int cdml_argmax_rows(const float *x, int rows, int cols, int ld, int *out,
+                     int out_stride, cdml_stream stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,132 @@
+"""CPU-side checks of the C++ host layer: the module loads, and every
+argument rule the reference enforces raises the reference's exception kind
+before any device work (AccelerationCPU.cs validation blocks,
+AccelerationManagerParityTests.cs:454-458, TransformerConfig.cs:62-102,
+LanguageModel.cs:482-600).  Without a device a compute call must fail loudly
+with InvalidOperationException, never fall back to the CPU."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from cdml import host, native as N, synth
+
+H = host.module()
+M, Vec = synth.matrix, synth.vector
+
+
+@pytest.fixture(scope="module")
+def mgr():
+    return H.HipAccelerationManager(0)
+
+
+def test_exception_hierarchy_mirrors_dotnet():
+    assert issubclass(H.ArgumentNullException, H.ArgumentException)
+    assert issubclass(H.ArgumentOutOfRangeException, H.ArgumentException)
+    assert issubclass(H.ArgumentException, ValueError)
+    assert issubclass(H.InvalidOperationException, RuntimeError)
+
+
+def test_sdpa_argument_rules(mgr):
+    q, k, v = M(4, 8, 121), M(5, 8, 122), M(5, 8, 123)
+    with pytest.raises(H.ArgumentException, match="causal"):
+        mgr.ScaledDotProductAttention(q, k, v, 2, None, True)  # :454-458
+    with pytest.raises(H.ArgumentNullException):
+        mgr.ScaledDotProductAttention(None, k, v, 2)
+    with pytest.raises(H.ArgumentOutOfRangeException):
+        mgr.ScaledDotProductAttention(q, k, v, 0)
+    with pytest.raises(H.ArgumentException, match="divisible"):
+        mgr.ScaledDotProductAttention(q, k, v, 3)
+    with pytest.raises(H.ArgumentException, match="Mask shape"):
+        mgr.ScaledDotProductAttention(q, k, v, 2, np.ones((4, 4), bool))
+    with pytest.raises(H.ArgumentException, match="V row count"):
+        mgr.ScaledDotProductAttention(q, k, v[:4], 2)
+    with pytest.raises(H.ArgumentException, match="at least one row"):
+        mgr.ScaledDotProductAttention(q[:0], k, v, 2)
+
+
+def test_mha_forward_argument_rules(mgr):
+    q, k, v = M(4, 6, 31), M(4, 6, 32), M(4, 6, 33)
+    with pytest.raises(H.ArgumentException, match="same sequence length"):
+        mgr.MultiHeadAttentionForward(q, k, v[:3], 2, 0.5)
+    with pytest.raises(H.ArgumentException, match="Mask shape"):
+        mgr.MultiHeadAttentionForward(q, k, v, 2, 0.5, np.ones((3, 4), bool))
+    out = mgr.MultiHeadAttentionForward(q[:0], k, v, 2, 0.5)  # empty query: zeros, no device work
+    assert out.shape == (0, 6)
+
+
+def test_project_qkv_argument_rules(mgr):
+    x = M(6, 5, 124)
+    w, b = M(8, 5, 125), Vec(8, 128)
+    with pytest.raises(H.ArgumentNullException):
+        mgr.ProjectQKV(x, w, None, w, b, w, b)
+    with pytest.raises(H.ArgumentException, match="WK input dimension"):
+        mgr.ProjectQKV(x, w, b, M(8, 4, 1), b, w, b)
+    with pytest.raises(H.ArgumentException, match="biasV length"):
+        mgr.ProjectQKV(x, w, b, w, b, w, Vec(7, 1))
+    with pytest.raises(H.ArgumentException, match="output dimensions must match"):
+        mgr.ProjectQKV(x, w, b, M(7, 5, 1), Vec(7, 1), w, b)
+
+
+def test_other_argument_rules(mgr):
+    x = M(4, 8, 1)
+    with pytest.raises(H.ArgumentOutOfRangeException):
+        mgr.BatchDotProductAddBias(M(3, 8, 2), x, 2, 3, Vec(3, 1))
+    with pytest.raises(H.ArgumentException, match="Bias length"):
+        mgr.BatchDotProductAddBias(M(3, 8, 2), x, Vec(4, 1))
+    with pytest.raises(H.ArgumentException, match="even per-head"):
+        mgr.ApplyRotaryPositionEmbeddingInPlace(np.zeros((2, 6), np.float32), 2, 10000.0, False)
+    with pytest.raises(H.ArgumentOutOfRangeException):
+        mgr.ApplyRotaryPositionEmbeddingInPlace(np.zeros((2, 8), np.float32), 2, -1.0, False)
+    with pytest.raises(H.ArgumentException, match="Head range"):
+        mgr.ApplyRotaryPositionEmbeddingHeadInPlace(np.zeros((2, 8), np.float32), 6, 4, 10000.0, False)
+    with pytest.raises(H.ArgumentOutOfRangeException):
+        mgr.EmbedTokenIds(np.array([0, 6], np.int32), M(6, 5, 64), 5)
+    with pytest.raises(H.ArgumentException, match="Embedding dimension mismatch"):
+        mgr.EmbedTokenIds(np.array([0], np.int32), M(6, 5, 64), 4)
+    assert mgr.EmbedTokenIds(np.zeros(0, np.int32), M(6, 5, 64), 5).shape == (0, 5)
+    with pytest.raises(H.ArgumentException, match="Residual input dimensions"):
+        mgr.ResidualLayerNorm(x, M(4, 7, 1), Vec(8, 1), Vec(8, 2))
+    with pytest.raises(H.ArgumentOutOfRangeException):
+        mgr.CreateCausalMask(-1)
+
+
+def test_create_causal_mask_is_lower_triangular(mgr):
+    # AccelerationCPU.cs:1566-1586 / parity test :410-421
+    m = mgr.CreateCausalMask(5)
+    assert m.dtype == bool and np.array_equal(m, np.tril(np.ones((5, 5), bool)))
+
+
+def test_config_and_model_rules():
+    with pytest.raises(H.ArgumentException, match="divisible"):
+        host.config({"vocab": 12, "dim": 8, "heads": 3, "layers": 1, "ff": 16, "max_seq": 8})
+    with pytest.raises(H.ArgumentException, match="even per-head"):
+        host.config({"vocab": 12, "dim": 6, "heads": 2, "layers": 1, "ff": 16, "max_seq": 8})
+    with pytest.raises(H.ArgumentOutOfRangeException):
+        host.config({"vocab": 12, "dim": 8, "heads": 2, "layers": 0, "ff": 16, "max_seq": 8})
+    cfg = {"vocab": 12, "dim": 8, "heads": 2, "layers": 1, "ff": 16, "max_seq": 8}
+    lm, _ = host.language_model(cfg, synth.lm_weights(cfg, 1))
+    with pytest.raises(H.ArgumentOutOfRangeException):
+        lm.Generate(np.array([1, 2], np.int32), 3, temperature=0.0)
+    with pytest.raises(H.ArgumentOutOfRangeException):
+        lm.Generate(np.array([1, 2], np.int32), -1)
+    with pytest.raises(H.ArgumentOutOfRangeException):
+        lm.Forward(np.array([1, 12], np.int32))
+    with pytest.raises(H.ArgumentException, match="exceeds MaxSequenceLength"):
+        lm.Forward(np.zeros(9, np.int32))
+    with pytest.raises(H.ArgumentException, match="at least one token"):
+        lm.Forward(np.zeros(0, np.int32))
+    with pytest.raises(H.InvalidOperationException):
+        lm.ForwardContinuous(np.zeros((2, 1), np.float32))
+    full = np.zeros(8, np.int32)  # a full prompt comes back unchanged (LanguageModel.cs:495-496)
+    assert np.array_equal(lm.Generate(full, 5), full)
+    assert np.array_equal(lm.Generate(np.array([3, 4], np.int32), 0), [3, 4])
+    with pytest.raises(H.ArgumentException, match="shape mismatch"):
+        lm.load_weights(synth.lm_weights(dict(cfg, vocab=13), 1))
+
+
+def test_no_device_means_loud_failure(mgr):
+    if N.device_count() > 0:
+        pytest.skip("a device is visible")
+    with pytest.raises(H.InvalidOperationException, match="no HIP device"):
+        mgr.ScaledDotProductAttention(M(4, 8, 1), M(4, 8, 2), M(4, 8, 3), 2)

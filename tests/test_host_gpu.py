@@ -1,0 +1,238 @@
+"""GPU parity of the C++ host layer (run on the MI355X).
+
+* HipAccelerationManager: every hot-path IAccelerationManager method against
+  the CPU oracle on the reference parity suite's closed-form inputs
+  (AccelerationManagerParityTests.cs:313-500, 755-768, 1087-1218), plus the
+  resident-weight shadow compare and the decode capability.
+* LanguageModel (the reference's call sequence on the manager) and
+  DeviceLanguageModel (device-resident engine): logits against the float64
+  golden fixtures and the oracle, and greedy token ids identical to the
+  oracle's, for the tiny test model and the config-1 text model.
+* The config-5 time-series regression transformer (continuous inputs) against
+  a composition of oracle functions.
+
+Bar: |got - want| <= 1e-4 + 1e-3 |want| per element; token ids exact.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import assert_parity, load_lm_golden
+from oracle import oracle as O
+from cdml import host, synth
+
+pytestmark = pytest.mark.gpu
+
+M, Vec = synth.matrix, synth.vector
+
+
+def parity(a, e, what="", atol=1e-4, rtol=1e-3):
+    assert_parity(a, e, atol=atol, rtol=rtol, what=what)
+
+
+@pytest.fixture(scope="module")
+def H():
+    return host.module()
+
+
+@pytest.fixture(scope="module")
+def mgr(H):
+    m = H.HipAccelerationManager(0)
+    yield m
+    m.Dispose()
+
+
+# ------------------------------------------------------------ the manager
+def test_manager_project_qkv(mgr):
+    x = M(6, 5, 124)
+    args = (M(8, 5, 125), Vec(8, 128), M(8, 5, 126), Vec(8, 129), M(8, 5, 127), Vec(8, 130))
+    for got, want, n in zip(mgr.ProjectQKV(x, *args), O.project_qkv(x, *args), "QKV"):
+        parity(got, want, f"ProjectQKV {n}")
+    xg = M(192, 128, 142)
+    args = (M(128, 128, 143), Vec(128, 146), M(128, 128, 144), Vec(128, 147), M(128, 128, 145), Vec(128, 148))
+    for got, want, n in zip(mgr.ProjectQKV(xg, *args), O.project_qkv(xg, *args), "QKV"):
+        parity(got, want, f"ProjectQKV 192x128 {n}")
+
+
+def test_manager_attention(mgr, ops_golden):
+    g = ops_golden
+    qs, ks, vs = M(4, 8, 118), M(4, 8, 119), M(4, 8, 120)
+    qc, kc, vc = M(4, 8, 121), M(5, 8, 122), M(5, 8, 123)
+    parity(mgr.ScaledDotProductAttention(qs, ks, vs, 2), O.sdpa(qs, ks, vs, 2), "SDPA self")
+    parity(mgr.ScaledDotProductAttention(qs, ks, vs, 2, g["self_mask"].astype(bool)),
+           O.sdpa(qs, ks, vs, 2, mask=g["self_mask"]), "SDPA self mask")
+    causal = mgr.ScaledDotProductAttention(qs, ks, vs, 2, None, True)
+    parity(causal, O.sdpa(qs, ks, vs, 2, causal=True), "SDPA causal")
+    parity(mgr.ScaledDotProductAttention(qs, ks, vs, 2, mgr.CreateCausalMask(4)), causal, "flag == mask")
+    parity(mgr.ScaledDotProductAttention(qc, kc, vc, 2, g["cross_mask"].astype(bool)),
+           O.sdpa(qc, kc, vc, 2, mask=g["cross_mask"]), "SDPA cross mask")
+    am = mgr.ScaledDotProductAttention(qc, kc, vc, 2, g["all_masked_mask"].astype(bool))
+    assert np.all(am[0] == 0)
+    q6, k6, v6 = M(4, 6, 31), M(4, 6, 32), M(4, 6, 33)
+    sc = float(g["mha_causal_scale"])
+    parity(mgr.MultiHeadAttentionForward(q6, k6, v6, 2, sc, O.causal_mask(4).astype(bool)),
+           O.mha_forward(q6, k6, v6, 2, sc, mask=O.causal_mask(4)), "MHA d_h=3")
+    qg, kg, vg = M(128, 64, 110), M(128, 64, 111), M(128, 64, 112)
+    parity(mgr.MultiHeadAttentionForward(qg, kg, vg, 4, 0.25), O.mha_forward(qg, kg, vg, 4, 0.25), "MHA 128")
+    parity(mgr.ScaledDotProductAttention(qg, kg, vg, 4, None, True), O.sdpa(qg, kg, vg, 4, causal=True),
+           "SDPA 128 causal")
+
+
+def test_manager_projection_rope_layernorm_embed(mgr):
+    parity(mgr.ProjectOutputBatch(M(4, 6, 56), M(3, 6, 57), Vec(3, 58), 4, 3),
+           O.project_output_batch(M(4, 6, 56), M(3, 6, 57), Vec(3, 58)), "ProjectOutputBatch")
+    x = M(10, 8, 3)
+    parity(mgr.BatchDotProductAddBias(M(5, 8, 4), x, 2, 6, Vec(5, 5)),
+           O.batch_dot_add_bias(M(5, 8, 4), x[2:8], Vec(5, 5)), "BatchDotProductAddBias slice")
+    m = M(4, 8, 97)
+    got = m.copy()
+    mgr.ApplyRotaryPositionEmbeddingInPlace(got, 2, 10000.0, False)
+    parity(got, O.rope(m, 2), "RoPE in place")
+    mgr.ApplyRotaryPositionEmbeddingInPlace(got, 2, 10000.0, True)
+    assert np.allclose(got, m, atol=5e-4)  # AccelerationManagerParityTests.cs:1107-1111
+    h = m.copy()
+    mgr.ApplyRotaryPositionEmbeddingHeadInPlace(h, 2, 4, 10000.0, False)
+    parity(h, O.rope_head(m, 2, 4), "RoPE one head")
+    a, b = M(5, 6, 27), M(5, 6, 28)
+    g, be = synth.positive_vector(6, 28), Vec(6, 29)
+    parity(mgr.ResidualLayerNorm(a, b, g, be), O.residual_layernorm(a, b, g, be), "ResidualLayerNorm")
+    table = M(6, 5, 64)
+    assert np.array_equal(mgr.EmbedTokenIds(np.array([0, 2, 4], np.int32), table, 5),
+                          O.embed_tokens([0, 2, 4], table))
+    assert np.array_equal(mgr.EmbedTokenIds(np.array([9, 1, 3, 9], np.int32), 1, 2, table, 5),
+                          O.embed_tokens([1, 3], table))
+
+
+def test_manager_ffn(mgr):
+    x = synth.normal(1, (40, 32))
+    w1, b1 = synth.xavier_uniform(2, 64, 32), synth.normal(3, (64,)) * np.float32(0.1)
+    w2, b2 = synth.xavier_uniform(4, 32, 64), synth.normal(5, (32,)) * np.float32(0.1)
+    want = O.batch_dot_add_bias(w2, O.activation(O.batch_dot_add_bias(w1, x, b1), 3), b2)
+    parity(mgr.FFNForwardBatch(x, 40, 32, [w1, w2], [b1, b2], [3, 0]), want, "FFNForwardBatch")
+
+
+def test_manager_resident_weights_follow_host_changes(mgr):
+    """A weight array changed in place after its first upload must be seen
+    (the shadow compare of DeviceResidentCache.cs:65-69)."""
+    x, w, b = M(7, 16, 1), M(9, 16, 2), Vec(9, 3)
+    first = mgr.ProjectOutputBatch(x, w, b, 7, 9)
+    parity(first, O.project_output_batch(x, w, b), "first")
+    w[3, 5] += np.float32(1.0)
+    b[0] -= np.float32(0.5)
+    parity(mgr.ProjectOutputBatch(x, w, b, 7, 9), O.project_output_batch(x, w, b), "after in-place change")
+
+
+def test_manager_decode_step_matches_prefill(mgr):
+    """The decode capability over T steps reproduces causal prefill row by row
+    (RoPE at the absolute position, append, attend)."""
+    T, D, Hh = 40, 64, 4
+    q, k, v = (synth.normal(60 + i, (T, D)) for i in range(3))
+    qr, kr = O.rope(q, Hh), O.rope(k, Hh)
+    pre = O.sdpa(qr, kr, v, Hh, causal=True)
+    keys = np.zeros((T, D), np.float32)
+    vals = np.zeros((T, D), np.float32)
+    for t in range(T):
+        qt, kt = q[t:t + 1].copy(), k[t:t + 1].copy()
+        out = mgr.DecodeSelfAttention(qt, kt, v[t:t + 1], keys, vals, t, Hh)
+        parity(out[0], pre[t], f"decode step {t}")
+        parity(qt[0], qr[t], f"rotated q {t}")
+    parity(keys, kr, "host key cache")
+    assert np.array_equal(vals, v)
+
+
+# ------------------------------------------------------ language models
+@pytest.mark.parametrize("name", ["lm_tiny", "lm_c1"])
+def test_language_model_forward_and_generate(mgr, name):
+    g = load_lm_golden(name)
+    lm, _ = host.language_model(g["cfg"], g["weights"], mgr)
+    logits = lm.Forward(g["ids"])
+    parity(logits, g["logits"], f"{name} LanguageModel.Forward vs float64 golden")
+    parity(logits, O.LanguageModel(g["cfg"], g["weights"]).forward(g["ids"]), f"{name} vs oracle")
+    out = lm.Generate(g["ids"][: int(g["prompt_len"])], int(g["n_new"]))
+    assert np.array_equal(out, g["greedy"]), f"{name}: greedy tokens differ"
+
+
+@pytest.mark.parametrize("name", ["lm_tiny", "lm_c1"])
+def test_device_language_model(H, mgr, name):
+    g = load_lm_golden(name)
+    lm, _ = host.language_model(g["cfg"], g["weights"], mgr)
+    dev = H.DeviceLanguageModel(lm, 4)
+    ids = g["ids"]
+    got = dev.Forward(ids[None, :])
+    parity(got, g["logits"], f"{name} device forward vs golden")
+    P = int(g["prompt_len"])
+    out = dev.GenerateGreedy(ids[None, :P], int(g["n_new"]))
+    assert np.array_equal(out[0], g["greedy"]), f"{name}: device greedy tokens differ"
+
+
+def test_device_language_model_c1_batch():
+    """Config 1: batch 4 of 64 uniform token ids, full forward, then greedy
+    generation of 20 tokens from 32-token prompts, per sequence against the
+    oracle's LanguageModel (which feeds the prompt token by token)."""
+    Hm = host.module()
+    cfg = {"vocab": 200, "dim": 64, "heads": 4, "layers": 2, "ff": 128, "max_seq": 64}
+    w = synth.lm_weights(cfg, 7)
+    lm, _ = host.language_model(cfg, w)
+    dev = Hm.DeviceLanguageModel(lm, 4)
+    ids = synth.token_ids(11, 4 * 64, 200).reshape(4, 64)
+    logits = dev.Forward(ids)
+    ref = O.LanguageModel(cfg, w)
+    for b in range(4):
+        parity(logits[b * 64:(b + 1) * 64], ref.forward(ids[b]), f"c1 seq {b}")
+    gen = dev.GenerateGreedy(ids[:, :32], 20)
+    assert gen.shape == (4, 52)
+    for b in range(4):
+        assert np.array_equal(gen[b], ref.generate_greedy(ids[b, :32], 20)), f"c1 seq {b} tokens"
+    # the length cap: a 60-token prompt yields only 4 new tokens (MaxSequenceLength 64)
+    cap = dev.GenerateGreedy(ids[:, :60], 20)
+    assert cap.shape == (4, 64)
+    for b in range(2):
+        assert np.array_equal(cap[b], ref.generate_greedy(ids[b, :60], 20))
+    full = dev.GenerateGreedy(ids, 5)
+    assert np.array_equal(full, ids)
+
+
+def _oracle_continuous(cfg, w, x):
+    """LanguageModel.Forward(float[,]) from oracle functions: input projection,
+    post-LN blocks, output projection."""
+    H = cfg["heads"]
+    h = O.batch_dot_add_bias(w["input_proj"], x, w["input_bias"])
+    for L in w["layers"]:
+        q, k, v = O.project_qkv(h, L["wq"], L["bq"], L["wk"], L["bk"], L["wv"], L["bv"])
+        a = O.sdpa(O.rope(q, H), O.rope(k, H), v, H, causal=True)
+        n1 = O.residual_layernorm(h, O.project_output_batch(a, L["wo"], L["bo"]), L["ln1_g"], L["ln1_b"])
+        f = O.batch_dot_add_bias(L["ffn_w2"], O.activation(O.batch_dot_add_bias(L["ffn_w1"], n1, L["ffn_b1"]), 3),
+                                 L["ffn_b2"])
+        h = O.residual_layernorm(n1, f, L["ln2_g"], L["ln2_b"])
+    return O.project_output_batch(h, w["out_proj"], w["out_bias"])
+
+
+def c5_weights(cfg, seed):
+    w = synth.lm_weights(dict(cfg, vocab=2), seed, biased=True)
+    D, F = cfg["dim"], cfg["input_dim"]
+    w["input_proj"] = synth.xavier_uniform(seed + 900, D, F)
+    w["input_bias"] = np.float32(0.1) * synth.normal(seed + 901, (D,))
+    w["out_proj"] = synth.xavier_uniform(seed + 902, cfg["output_dim"], D)
+    w["out_bias"] = np.float32(0.1) * synth.normal(seed + 903, (cfg["output_dim"],))
+    return w
+
+
+def test_time_series_transformer_c5_sampled():
+    """Config 5 (F 5 -> D 256, 8 x 32, 6 layers, FF 1024, out 1; B 256 x 512,
+    random-walk features): the whole batch on the device engine, three windows
+    against the oracle composition, and the drop-in LanguageModel on one."""
+    Hm = host.module()
+    cfg = {"dim": 256, "heads": 8, "layers": 6, "ff": 1024, "max_seq": 512, "discrete": False,
+           "input_dim": 5, "output_dim": 1}
+    w = c5_weights(cfg, 21)
+    lm, _ = host.language_model(cfg, w)
+    B, L = 256, 512
+    x = synth.random_walk_windows(31, B, L, 5)
+    dev = Hm.DeviceLanguageModel(lm, B)
+    out = dev.ForwardContinuous(x.reshape(B * L, 5), B, L)
+    assert out.shape == (B * L, 1) and np.all(np.isfinite(out))
+    for b in (0, 100, 255):
+        want = _oracle_continuous(cfg, w, x[b])
+        parity(out[b * L:(b + 1) * L], want, f"c5 window {b}")
+    parity(lm.ForwardContinuous(x[100]), _oracle_continuous(cfg, w, x[100]), "c5 drop-in LanguageModel")
