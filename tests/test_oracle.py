@@ -243,3 +243,18 @@ def test_oracle_detects_planted_mistake(ops_golden):
     wrong = O.sdpa(qs, vs, ks, 2)
     with pytest.raises(AssertionError):
         close(wrong, ops_golden["sdpa_self_nomask"])
+
+
+def test_activation_library_values():
+    """The FFN activations (NeuralNetwork.cs:670-716) against library routines:
+    scipy's logistic function, numpy's tanh, and the piecewise-linear forms."""
+    from scipy.special import expit
+
+    x = np.concatenate([np.linspace(-30, 30, 601), [0.0, -0.0, 1e-8, -1e-8]]).astype(np.float32)
+    x64 = x.astype(np.float64)
+    close(O.activation(x, 0), x, atol=0, rtol=0, what="none")
+    close(O.activation(x, 1), expit(x64), atol=1e-7, rtol=1e-6, what="sigmoid")
+    close(O.activation(x, 2), np.tanh(x64), atol=1e-7, rtol=1e-6, what="tanh")
+    close(O.activation(x, 3), np.maximum(x64, 0), atol=0, rtol=0, what="relu")
+    close(O.activation(x, 4), np.where(x64 > 0, x64, 0.01 * x64), atol=1e-9, rtol=1e-6, what="leakyrelu")
+    close(O.activation(x, 5), x64 * expit(x64), atol=1e-6, rtol=1e-6, what="swish")
