@@ -45,7 +45,11 @@ struct FlashArgs {
 };
 
 // Stages one BN x HD tile of K or V (rows [k0, k0+BN) of head column block
-// `col0`) from global memory into registers and then into LDS.
+// `col0`) from global memory into registers and then into LDS.  Each
+// thread's element offsets inside a tile are fixed (set once); a tile load
+// adds them to the wave-uniform tile base.  Rows past lk (the sequence end)
+// are clamped to row lk - 1: their scores are masked to -inf and their
+// probabilities are exactly 0.
 template <int HD, int BN, bool VEC>
 struct KvStage {
   static constexpr int F4_ROW = HD / 4;
@@ -54,20 +58,27 @@ struct KvStage {
   static constexpr int NS = BN * HD / FA_THREADS;
   float4 r[VEC ? NV : 1];
   float s[VEC ? 1 : NS];
+  uint32_t off[VEC ? NV : 1];  // element offsets of this thread's rows in a tile
+  int col;
+
+  __device__ __forceinline__ void init(int ld) {
+    if constexpr (VEC) {
+      const int t = threadIdx.x;
+      col = (t % F4_ROW) * 4;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) off[i] = (uint32_t)((t / F4_ROW + ROWS_PER_PASS * i) * ld + col);
+    }
+  }
 
   __device__ __forceinline__ void load(const float *__restrict__ base, int ld, int k0, int lk,
                                        int hd) {
-    const int t = threadIdx.x;
     if constexpr (VEC) {
-      const int c = (t % F4_ROW) * 4;
+      const float *tile = base + (size_t)k0 * ld;  // wave-uniform
+      const uint32_t lim = (uint32_t)(min(lk - 1 - k0, BN - 1) * ld) + col;
 #pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int row = t / F4_ROW + ROWS_PER_PASS * i;
-        const int key = k0 + row;
-        r[i] = key < lk ? *reinterpret_cast<const float4 *>(base + (size_t)key * ld + c)
-                        : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+      for (int i = 0; i < NV; ++i) r[i] = *reinterpret_cast<const float4 *>(tile + min(off[i], lim));
     } else {
+      const int t = threadIdx.x;
 #pragma unroll
       for (int i = 0; i < NS; ++i) {
         const int e = t + FA_THREADS * i;
@@ -81,10 +92,9 @@ struct KvStage {
   __device__ __forceinline__ void store(float (*lds)[HD + 4]) {
     const int t = threadIdx.x;
     if constexpr (VEC) {
-      const int c = (t % F4_ROW) * 4;
 #pragma unroll
       for (int i = 0; i < NV; ++i)
-        *reinterpret_cast<float4 *>(&lds[t / F4_ROW + ROWS_PER_PASS * i][c]) = r[i];
+        *reinterpret_cast<float4 *>(&lds[t / F4_ROW + ROWS_PER_PASS * i][col]) = r[i];
     } else {
 #pragma unroll
       for (int i = 0; i < NS; ++i) {
@@ -95,11 +105,41 @@ struct KvStage {
   }
 };
 
+// max / sum of a value over the two half-waves (lanes l and l ^ 32) with
+// v_permlane32_swap: both results hold the value of lane l % 32 and of lane
+// l % 32 + 32.
+__device__ __forceinline__ float halves_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// max of three scores.  The scores come from MFMA accumulators and are
+// never signalling NaNs, so the IEEE quieting that fmaxf otherwise adds to
+// each operand is dropped (one v_max3_f32 instead of five instructions).
+__device__ __forceinline__ float max3_scores(float a, float b, float c) {
+#pragma float_control(precise, off)
+  return __builtin_fmaxf(__builtin_fmaxf(a, b), c);
+}
+
+// Growth of the running max (log2 units) tolerated before the output is
+// rescaled: probabilities stay <= 2^8, far from fp32 overflow.
+constexpr float kRescaleThreshold = 8.0f;
+
+// Offset of accumulator register r's key inside its 32-key sub-block for a
+// lane of half-wave h: 8 * (r / 4) + 4 * h + r % 4 (the 32x32 MFMA D layout).
+__device__ __forceinline__ constexpr int acc_key(int r) { return 8 * (r >> 2) + (r & 3); }
+
 template <int HD, int BN, bool CAUSAL, bool HAS_MASK, bool VEC>
-__global__ void __launch_bounds__(FA_THREADS) flash_fwd_kernel(const FlashArgs a) {
-  constexpr int NKB = BN / 32;  // 32-key sub-blocks per tile
-  constexpr int NDB = HD / 32;  // 32-wide head-dim blocks of O^T
-  constexpr int NQ = HD / 2;    // MFMA k-steps of Q.K
+__global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArgs a) {
+  constexpr int NKB = BN / 32;   // 32-key sub-blocks per tile
+  constexpr int NDB = HD / 32;   // 32-wide head-dim blocks of O^T
+  constexpr int NQ = HD / 2;     // MFMA k-steps of Q.K
+  constexpr int NKG = HD / 8;    // float4 groups of a K row slice
+  constexpr int VCH = HD <= 64 ? 16 : 8;  // P.V steps whose V operands are read at once
   __shared__ __attribute__((aligned(16))) float Ks[2][BN][HD + 4];
   __shared__ __attribute__((aligned(16))) float Vs[2][BN][HD + 4];
 
@@ -112,9 +152,9 @@ __global__ void __launch_bounds__(FA_THREADS) flash_fwd_kernel(const FlashArgs a
   const int q0 = qt * FA_BM;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = lane & 31, hf = lane >> 5;
-  const int qw0 = q0 + wave * 32;   // first query of this wave
+  const int qw0 = q0 + wave * 32;   // first query of this wave (wave-uniform)
   const int qi = qw0 + li;          // this lane's query
   const int col0 = h * a.hd;
 
@@ -124,17 +164,17 @@ __global__ void __launch_bounds__(FA_THREADS) flash_fwd_kernel(const FlashArgs a
   // Q^T operand: register 4u + r holds q[qi][8u + 4*hf + r].
   float qreg[NQ];
   {
-    const float *qrow = a.q + ((size_t)b * a.lq + qi) * a.ldq + col0;
+    const float *qrow = a.q + ((size_t)b * a.lq + min(qi, a.lq - 1)) * a.ldq + col0;
     const bool qok = qi < a.lq;
 #pragma unroll
     for (int u = 0; u < HD / 8; ++u) {
       const int d = 8 * u + 4 * hf;
       if constexpr (VEC) {
-        float4 t4 = qok ? *reinterpret_cast<const float4 *>(qrow + d) : make_float4(0.f, 0.f, 0.f, 0.f);
-        qreg[4 * u + 0] = t4.x;
-        qreg[4 * u + 1] = t4.y;
-        qreg[4 * u + 2] = t4.z;
-        qreg[4 * u + 3] = t4.w;
+        float4 t4 = *reinterpret_cast<const float4 *>(qrow + d);
+        qreg[4 * u + 0] = qok ? t4.x : 0.f;
+        qreg[4 * u + 1] = qok ? t4.y : 0.f;
+        qreg[4 * u + 2] = qok ? t4.z : 0.f;
+        qreg[4 * u + 3] = qok ? t4.w : 0.f;
       } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r) qreg[4 * u + r] = (qok && d + r < a.hd) ? qrow[d + r] : 0.f;
@@ -146,6 +186,8 @@ __global__ void __launch_bounds__(FA_THREADS) flash_fwd_kernel(const FlashArgs a
   const int n_kt = (kend + BN - 1) / BN;
 
   KvStage<HD, BN, VEC> sk, sv;
+  sk.init(a.ldk);
+  sv.init(a.ldv);
   sk.load(kbase, a.ldk, 0, a.lk, a.hd);
   sv.load(vbase, a.ldv, 0, a.lk, a.hd);
   sk.store(Ks[0]);
@@ -157,8 +199,16 @@ __global__ void __launch_bounds__(FA_THREADS) flash_fwd_kernel(const FlashArgs a
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
-  float m_i = -INFINITY;  // running max (exp2 domain) for query qi
-  float l_i = 0.f;        // running sum over this half-wave's keys
+  // Scores enter the exp2 domain as s * c.  For c > 0 the tile max is taken
+  // on the raw scores and p = exp2(fma(s, c, -m)); otherwise the scores are
+  // scaled first and c becomes 1.
+  const bool pos_scale = a.scale_log2 > 0.f;
+  const float c = pos_scale ? a.scale_log2 : 1.0f;
+  float m_run = -INFINITY;   // reference max of this lane's query (exp2 domain)
+  float l_a = 0.f, l_b = 0.f;  // running sums over this half-wave's keys
+  const floatx16 zero = {};
+  // Last key this lane may attend (the causal diagonal and the sequence end).
+  const int key_last = CAUSAL ? min(qi, a.lk - 1) : a.lk - 1;
 
   const uint8_t *mrow = HAS_MASK ? a.mask + (size_t)min(qi, a.lq - 1) * a.lk : nullptr;
 
@@ -166,91 +216,112 @@ __global__ void __launch_bounds__(FA_THREADS) flash_fwd_kernel(const FlashArgs a
     const int cur = kt & 1;
     const int k0 = kt * BN;
     const bool more = kt + 1 < n_kt;
-    if (more) {
-      sk.load(kbase, a.ldk, k0 + BN, a.lk, a.hd);
-      sv.load(vbase, a.ldv, k0 + BN, a.lk, a.hd);
-    }
+    // Next tile into registers.  The last iteration re-stages its own tile
+    // into the idle buffer (nobody reads it again): an unconditional stage
+    // keeps the staging registers out of scratch memory.
+    sk.load(kbase, a.ldk, more ? k0 + BN : k0, a.lk, a.hd);
+    sv.load(vbase, a.ldv, more ? k0 + BN : k0, a.lk, a.hd);
 
-    floatx16 sacc[NKB];
-    bool active[NKB];
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
       const int kb0 = k0 + kb * 32;
-      active[kb] = kb0 < a.lk && (!CAUSAL || kb0 <= qw0 + 31);
+      // A sub-block wholly past the sequence end or in this wave's future
+      // contributes nothing (every probability would be 0): skip it.
+      if (kb0 >= a.lk || (CAUSAL && kb0 > qw0 + 31)) continue;
+      const float(*krow)[HD + 4] = &Ks[cur][kb * 32];
+      const float(*vrow)[HD + 4] = &Vs[cur][kb * 32];
+
+      // S^T = K Q^T; the K operand group u + 1 is read while group u multiplies.
+      floatx16 sacc;
+      float4 kcur = *reinterpret_cast<const float4 *>(&krow[li][4 * hf]);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
-      if (active[kb]) {
+      for (int u = 0; u < NKG; ++u) {
+        float4 knext;
+        if (u + 1 < NKG) knext = *reinterpret_cast<const float4 *>(&krow[li][8 * (u + 1) + 4 * hf]);
+        sacc = mfma32x32x2(kcur.x, qreg[4 * u + 0], u == 0 ? zero : sacc);
+        sacc = mfma32x32x2(kcur.y, qreg[4 * u + 1], sacc);
+        sacc = mfma32x32x2(kcur.z, qreg[4 * u + 2], sacc);
+        sacc = mfma32x32x2(kcur.w, qreg[4 * u + 3], sacc);
+        if (u + 1 < NKG) kcur = knext;
+      }
+      // V^T operands of the first P.V chunk, in flight during the softmax.
+      float vr[VCH][NDB];
 #pragma unroll
-        for (int u = 0; u < HD / 8; ++u) {
-          const float4 k4 = *reinterpret_cast<const float4 *>(&Ks[cur][kb * 32 + li][8 * u + 4 * hf]);
-          sacc[kb] = mfma32x32x2(k4.x, qreg[4 * u + 0], sacc[kb]);
-          sacc[kb] = mfma32x32x2(k4.y, qreg[4 * u + 1], sacc[kb]);
-          sacc[kb] = mfma32x32x2(k4.z, qreg[4 * u + 2], sacc[kb]);
-          sacc[kb] = mfma32x32x2(k4.w, qreg[4 * u + 3], sacc[kb]);
+      for (int st = 0; st < VCH; ++st)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) vr[st][db] = vrow[acc_key(st) + 4 * hf][db * 32 + li];
+
+      if (!pos_scale) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[r] *= a.scale_log2;
+      }
+      // Masking (wave-uniform decision): the diagonal, the sequence end, a mask.
+      if (HAS_MASK || kb0 + 31 > (CAUSAL ? qw0 : a.lk - 1)) {
+        const int thr = key_last - kb0 - 4 * hf;  // last visible offset for this lane
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          bool ok = acc_key(r) <= thr;
+          if (HAS_MASK) {
+            const int key = min(kb0 + acc_key(r) + 4 * hf, a.lk - 1);
+            ok = ok && qi < a.lq && mrow[key] != 0;
+          }
+          sacc[r] = ok ? sacc[r] : -INFINITY;
         }
       }
-    }
+      float smax = max3_scores(sacc[0], sacc[1], sacc[2]);
+#pragma unroll
+      for (int r = 3; r < 15; r += 2) smax = max3_scores(smax, sacc[r], sacc[r + 1]);
+      smax = max3_scores(smax, sacc[15], -INFINITY);
+      smax = halves_max(smax);
+      const float m_tile = smax * c;  // exact max of fl(s * c) for c > 0
 
-    // Scale into the exp2 domain and mask.
-    const bool edge = HAS_MASK || (k0 + BN > a.lk) || (CAUSAL && k0 + BN - 1 > qw0);
-    float rmax = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float t = sacc[kb][r] * a.scale_log2;
-        if (edge) {
-          const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
-          bool ok = active[kb] && key < a.lk;
-          if (CAUSAL) ok = ok && key <= qi;
-          if (HAS_MASK) ok = ok && qi < a.lq && mrow[key] != 0;
-          t = ok ? t : -INFINITY;
-        }
-        sacc[kb][r] = t;
-        rmax = fmaxf(rmax, t);
-      }
-    }
-    rmax = fmaxf(rmax, __shfl_xor(rmax, 32));
-    const float m_new = fmaxf(m_i, rmax);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = fast_exp2(m_i - m_use);
-    float rsum = 0.f;
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(sacc[kb][r] - m_use);
-        sacc[kb][r] = p;
-        rsum += p;
-      }
-    l_i = l_i * alpha + rsum;
-    m_i = m_new;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
-
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-      if (!active[kb]) continue;
-#pragma unroll
-      for (int s = 0; s < 16; ++s) {
-        const int krow = kb * 32 + 8 * (s >> 2) + 4 * hf + (s & 3);
+      // Lazy rescale: only when this lane's max grew by more than the threshold.
+      const float m_new = fmaxf(m_run, m_tile);
+      const bool need = m_new > m_run + kRescaleThreshold;
+      if (__builtin_amdgcn_ballot_w64(need)) {
+        const float alpha = need ? fast_exp2(m_run - m_new) : 1.0f;
+        m_run = need ? m_new : m_run;
+        l_a *= alpha;
+        l_b *= alpha;
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
-          oacc[db] = mfma32x32x2(Vs[cur][krow][db * 32 + li], sacc[kb][s], oacc[db]);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+      }
+      const float nm = m_run == -INFINITY ? 0.f : -m_run;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(fmaf(sacc[r], c, nm));
+        sacc[r] = p;
+        if (r & 1) l_b += p;
+        else l_a += p;
+      }
+
+      // O^T += V^T P^T: accumulator r of the lane holds the probability of
+      // key acc_key(r) + 4*hf, the key B-operand slot of MFMA step r needs.
+#pragma unroll
+      for (int ch = 0; ch < 16 / VCH; ++ch) {
+        if (ch > 0) {
+#pragma unroll
+          for (int st = 0; st < VCH; ++st)
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+              vr[st][db] = vrow[acc_key(ch * VCH + st) + 4 * hf][db * 32 + li];
+        }
+#pragma unroll
+        for (int st = 0; st < VCH; ++st)
+#pragma unroll
+          for (int db = 0; db < NDB; ++db) oacc[db] = mfma32x32x2(vr[st][db], sacc[ch * VCH + st], oacc[db]);
       }
     }
 
-    if (more) {
-      sk.store(Ks[cur ^ 1]);
-      sv.store(Vs[cur ^ 1]);
-    }
+    sk.store(Ks[cur ^ 1]);
+    sv.store(Vs[cur ^ 1]);
     __syncthreads();
   }
 
   // Normalise and store: lane holds query qi, dims db*32 + 8*(r/4) + 4*hf + r%4.
-  const float l_tot = l_i + __shfl_xor(l_i, 32);
+  const float l_tot = halves_sum(l_a + l_b);
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
   if (qi < a.lq) {
     float *orow = a.o + ((size_t)b * a.lq + qi) * a.ldo + col0;
@@ -372,6 +443,8 @@ extern "C" int cdml_sdpa_fwd(const float *q, int ldq, const float *k, int ldk, c
     return fail(CDML_E_CAUSAL, "cdml_sdpa_fwd: causal attention requires lq == lk (got %d, %d)", lq, lk);
   if (ldq < dim || ldk < dim || ldv < dim || ldo < dim)
     return fail(CDML_E_INVALID, "cdml_sdpa_fwd: row stride smaller than dim");
+  if ((long long)ldk * 128 > INT32_MAX || (long long)ldv * 128 > INT32_MAX)
+    return fail(CDML_E_INVALID, "cdml_sdpa_fwd: row stride above %d elements", INT32_MAX / 128);
   if (batch == 0 || lq == 0) return CDML_OK;
   if (lk == 0) return fail(CDML_E_INVALID, "cdml_sdpa_fwd: lk must be >= 1");
   if (!q || !k || !v || !o) return fail(CDML_E_INVALID, "cdml_sdpa_fwd: NULL pointer");
