@@ -44,6 +44,9 @@ inline int pad_to_xcd(int n) { return (n + kNumXcd - 1) / kNumXcd * kNumXcd; }
 //   A[i][k]: i = l % 32, k = h      B[k][j]: j = l % 32, k = h
 //   D[i][j]: j = l % 32, i = 8*(r/4) + 4*h + (r%4) for accumulator r = 0..15
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+// Native 4-float vector for register staging: unlike HIP's float4 struct it
+// is always kept in registers (no private-memory copies of staging arrays).
+typedef float vf4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ floatx16 mfma32x32x2(float a, float b, floatx16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);

@@ -198,6 +198,175 @@ __global__ void __launch_bounds__(NTHREADS) gemm_nt_kernel(const GemmArgs args) 
   }
 }
 
+// Tiled fast path (K % BKK == 0, 16-byte aligned rows, element offsets
+// below 2^32).  A workgroup of WM x WN waves computes a TM x TN tile of C,
+// each wave a (TM/WM) x (TN/WN) block of 32x32 MFMA tiles.  K advances by BKK
+// through double-buffered LDS (row pitch BKK + 4 floats).  Every thread's
+// staging rows are fixed for the whole K loop (rows past M or N are clamped
+// to the last row: they feed only accumulators that are never stored), so a
+// k-tile load is the wave-uniform base plus precomputed 32-bit offsets, with
+// no predication.  The LDS operands of group u + 1 are read while the MFMAs of
+// group u run, and the k-tile after next is fetched while the current one is
+// consumed.  Measured on MI355X, high occupancy (four waves per SIMD with two
+// 512-thread workgroups per CU) hides latency better than deeper register
+// blocking.
+template <int TM, int TN, int BKK, int WM, int WN, int MINB, int ACT>
+__global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const GemmArgs args) {
+  constexpr int NT = 64 * WM * WN;
+  constexpr int LD = BKK + 4;
+  constexpr int F4R = BKK / 4;   // float4 per row of a k-tile
+  constexpr int RPP = NT / F4R;  // rows per staging pass
+  constexpr int NA = TM / RPP, NB = TN / RPP;
+  constexpr int BI = TM / WM / 32, BJ = TN / WN / 32;
+  static_assert(NA >= 1 && NB >= 1 && BI >= 1 && BJ >= 1, "tile shape");
+  __shared__ __attribute__((aligned(16))) float As[2][TM][LD];
+  __shared__ __attribute__((aligned(16))) float Bs[2][TN][LD];
+
+  const int lid = xcd_remap(blockIdx.x, args.padded);
+  if (lid >= args.total) return;
+  // Grouped ordering over (tiles_m, nprob * tiles_n): GROUP_M tile-rows share
+  // each weight panel while it is hot in L2.
+  const int tiles_n_all = args.tiles_n * args.nprob;
+  const int in_group = GROUP_M * tiles_n_all;
+  const int group = lid / in_group;
+  const int first_m = group * GROUP_M;
+  const int gsize = min(args.tiles_m - first_m, GROUP_M);
+  const int tm = first_m + (lid % in_group) % gsize;
+  const int tn_all = (lid % in_group) / gsize;
+  const int prob = tn_all / args.tiles_n;
+  const int tn = tn_all % args.tiles_n;
+
+  const GemmProblem P = args.p[prob];
+  const int m0 = tm * TM, n0 = tn * TN;
+  const int M = args.M, N = args.N, K = args.K;
+
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int li = lane & 31, hf = lane >> 5;
+
+  const int srow = t / F4R, scol = (t % F4R) * 4;
+  uint32_t aoff[NA], boff[NB];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) aoff[i] = (uint32_t)min(m0 + srow + RPP * i, M - 1) * (uint32_t)args.lda + scol;
+#pragma unroll
+  for (int i = 0; i < NB; ++i) boff[i] = (uint32_t)min(n0 + srow + RPP * i, N - 1) * (uint32_t)K + scol;
+  vf4 ra[NA], rb[NB];
+  floatx16 acc[BI][BJ];
+#pragma unroll
+  for (int i = 0; i < BI; ++i)
+#pragma unroll
+    for (int j = 0; j < BJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  const int nk = K / BKK;
+  const float *__restrict__ A = args.a;
+  const float *__restrict__ W = P.w;
+
+  // k-tile 0 -> LDS, k-tile 1 -> registers
+#pragma unroll
+  for (int i = 0; i < NA; ++i) ra[i] = *reinterpret_cast<const vf4 *>(A + aoff[i]);
+#pragma unroll
+  for (int i = 0; i < NB; ++i) rb[i] = *reinterpret_cast<const vf4 *>(W + boff[i]);
+#pragma unroll
+  for (int i = 0; i < NA; ++i) *reinterpret_cast<vf4 *>(&As[0][srow + RPP * i][scol]) = ra[i];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) *reinterpret_cast<vf4 *>(&Bs[0][srow + RPP * i][scol]) = rb[i];
+  {
+    const int k1 = min(BKK, (nk - 1) * BKK);
+#pragma unroll
+    for (int i = 0; i < NA; ++i) ra[i] = *reinterpret_cast<const vf4 *>(A + k1 + aoff[i]);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) rb[i] = *reinterpret_cast<const vf4 *>(W + k1 + boff[i]);
+  }
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    const float(*as)[LD] = &As[cur][wm * (TM / WM) + li];
+    const float(*bs)[LD] = &Bs[cur][wn * (TN / WN) + li];
+    vf4 a4[BI], b4[BJ];
+#pragma unroll
+    for (int i = 0; i < BI; ++i) a4[i] = *reinterpret_cast<const vf4 *>(&as[i * 32][hf * 4]);
+#pragma unroll
+    for (int j = 0; j < BJ; ++j) b4[j] = *reinterpret_cast<const vf4 *>(&bs[j * 32][hf * 4]);
+#pragma unroll
+    for (int u = 0; u < BKK / 8; ++u) {
+      vf4 an[BI], bn[BJ];
+      if (u + 1 < BKK / 8) {
+#pragma unroll
+        for (int i = 0; i < BI; ++i) an[i] = *reinterpret_cast<const vf4 *>(&as[i * 32][(u + 1) * 8 + hf * 4]);
+#pragma unroll
+        for (int j = 0; j < BJ; ++j) bn[j] = *reinterpret_cast<const vf4 *>(&bs[j * 32][(u + 1) * 8 + hf * 4]);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int i = 0; i < BI; ++i)
+#pragma unroll
+          for (int j = 0; j < BJ; ++j) acc[i][j] = mfma32x32x2(a4[i][r], b4[j][r], acc[i][j]);
+      if (u + 1 < BKK / 8) {
+#pragma unroll
+        for (int i = 0; i < BI; ++i) a4[i] = an[i];
+#pragma unroll
+        for (int j = 0; j < BJ; ++j) b4[j] = bn[j];
+      }
+    }
+    // Stage k-tile kt + 1 (already in registers) and fetch k-tile kt + 2.
+    // Past the end both are unconditional re-stages of the last tile into
+    // the idle buffer, which nothing reads again: keeping them unconditional
+    // keeps the staging registers out of scratch memory.
+#pragma unroll
+    for (int i = 0; i < NA; ++i) *reinterpret_cast<vf4 *>(&As[cur ^ 1][srow + RPP * i][scol]) = ra[i];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) *reinterpret_cast<vf4 *>(&Bs[cur ^ 1][srow + RPP * i][scol]) = rb[i];
+    const int k2 = min((kt + 2) * BKK, (nk - 1) * BKK);
+#pragma unroll
+    for (int i = 0; i < NA; ++i) ra[i] = *reinterpret_cast<const vf4 *>(A + k2 + aoff[i]);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) rb[i] = *reinterpret_cast<const vf4 *>(W + k2 + boff[i]);
+    __syncthreads();
+  }
+
+  // Epilogue: D[i][j] of block (bi, bj) sits at row 8*(r/4) + 4*hf + r%4,
+  // column li; 32 lanes store 32 consecutive columns of one row.
+#pragma unroll
+  for (int j = 0; j < BJ; ++j) {
+    const int n = n0 + wn * (TN / WN) + j * 32 + li;
+    if (n >= N) continue;
+    const float bias = P.bias ? P.bias[n] : 0.f;
+#pragma unroll
+    for (int i = 0; i < BI; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * (TM / WM) + i * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
+        if (m < M) P.c[(size_t)m * args.ldc + n] = activate(acc[i][j][r] + bias, ACT);
+      }
+    }
+  }
+}
+
+// Two tile configurations: 256 x 128 with eight waves for M >= 1024, and
+// 128 x 128 with four waves for smaller M (decode rows, short sequences).
+template <int TM, int TN, int BKK, int WM, int WN, int MINB>
+int launch_tile(GemmArgs g, hipStream_t stream) {
+  g.tiles_m = (g.M + TM - 1) / TM;
+  g.tiles_n = (g.N + TN - 1) / TN;
+  g.total = g.tiles_m * g.tiles_n * g.nprob;
+  g.padded = pad_to_xcd(g.total);
+  const dim3 grid(g.padded), block(64 * WM * WN);
+  switch (g.act) {
+    case CDML_ACT_NONE: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_NONE><<<grid, block, 0, stream>>>(g); break;
+    case CDML_ACT_SIGMOID: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_SIGMOID><<<grid, block, 0, stream>>>(g); break;
+    case CDML_ACT_TANH: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_TANH><<<grid, block, 0, stream>>>(g); break;
+    case CDML_ACT_RELU: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_RELU><<<grid, block, 0, stream>>>(g); break;
+    case CDML_ACT_LEAKYRELU: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_LEAKYRELU><<<grid, block, 0, stream>>>(g); break;
+    default: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_SWISH><<<grid, block, 0, stream>>>(g); break;
+  }
+  return CDML_OK;
+}
+
 int launch_gemm(GemmArgs &g, hipStream_t stream, const char *what) {
   if (g.M == 0 || g.N == 0) return CDML_OK;
   g.tiles_m = (g.M + BM - 1) / BM;
@@ -206,7 +375,16 @@ int launch_gemm(GemmArgs &g, hipStream_t stream, const char *what) {
   g.padded = pad_to_xcd(g.total);
   bool vec = (g.K % 4 == 0) && (g.lda % 4 == 0) && aligned16(g.a);
   for (int i = 0; i < g.nprob; ++i) vec = vec && aligned16(g.p[i].w);
-  if (vec)
+  const bool fast = vec && g.K % 16 == 0 && g.K > 0 &&
+                    (unsigned long long)g.M * g.lda < (1ull << 32) &&
+                    (unsigned long long)g.N * g.K < (1ull << 32);
+  if (fast && g.M >= 1024) {
+    int rc = launch_tile<256, 128, 16, 4, 2, 2>(g, stream);
+    if (rc) return rc;
+  } else if (fast) {
+    int rc = launch_tile<128, 128, 16, 2, 2, 2>(g, stream);
+    if (rc) return rc;
+  } else if (vec)
     gemm_nt_kernel<true><<<dim3(g.padded), dim3(NTHREADS), 0, stream>>>(g);
   else
     gemm_nt_kernel<false><<<dim3(g.padded), dim3(NTHREADS), 0, stream>>>(g);
