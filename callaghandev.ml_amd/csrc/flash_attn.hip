@@ -143,11 +143,17 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArg
   __shared__ __attribute__((aligned(16))) float Ks[2][BN][HD + 4];
   __shared__ __attribute__((aligned(16))) float Vs[2][BN][HD + 4];
 
-  const int lid = xcd_remap(blockIdx.x, a.padded);
-  if (lid >= a.total) return;
-  const int bh = lid / a.n_qt;
-  int qt = lid % a.n_qt;
-  if (CAUSAL) qt = a.n_qt - 1 - qt;  // longest rows first
+  // Query-tile-major order: workgroup i takes (sequence, head) i % n_bh and
+  // query tile i / n_bh, counted from the last (longest under causal
+  // masking) tile down.  Every XCD therefore receives the heaviest tiles
+  // first and the lightest last (a near-optimal greedy schedule), and since
+  // workgroup i runs on XCD i % 8, all tiles of one (sequence, head) share an
+  // XCD and its L2 whenever n_bh is a multiple of 8.
+  const int lid = blockIdx.x;
+  const int n_bh = a.total / a.n_qt;
+  const int bh = lid % n_bh;
+  int qt = lid / n_bh;
+  if (CAUSAL) qt = a.n_qt - 1 - qt;
   const int b = bh / a.heads, h = bh % a.heads;
   const int q0 = qt * FA_BM;
 
@@ -408,9 +414,9 @@ __global__ void __launch_bounds__(256) flash_generic_kernel(const FlashArgs a, i
 template <int HD, int BN, bool CAUSAL, bool HAS_MASK>
 void launch_tpl(const FlashArgs &a, bool vec, hipStream_t st) {
   if (vec)
-    flash_fwd_kernel<HD, BN, CAUSAL, HAS_MASK, true><<<dim3(a.padded), dim3(FA_THREADS), 0, st>>>(a);
+    flash_fwd_kernel<HD, BN, CAUSAL, HAS_MASK, true><<<dim3(a.total), dim3(FA_THREADS), 0, st>>>(a);
   else
-    flash_fwd_kernel<HD, BN, CAUSAL, HAS_MASK, false><<<dim3(a.padded), dim3(FA_THREADS), 0, st>>>(a);
+    flash_fwd_kernel<HD, BN, CAUSAL, HAS_MASK, false><<<dim3(a.total), dim3(FA_THREADS), 0, st>>>(a);
 }
 
 template <int HD, int BN>
