@@ -139,7 +139,7 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArg
   constexpr int NDB = HD / 32;   // 32-wide head-dim blocks of O^T
   constexpr int NQ = HD / 2;     // MFMA k-steps of Q.K
   constexpr int NKG = HD / 8;    // float4 groups of a K row slice
-  constexpr int VCH = HD <= 64 ? 16 : 8;  // P.V steps whose V operands are read at once
+  constexpr int VCH = HD <= 32 ? 16 : 8;  // P.V steps whose V operands are read at once
   __shared__ __attribute__((aligned(16))) float Ks[2][BN][HD + 4];
   __shared__ __attribute__((aligned(16))) float Vs[2][BN][HD + 4];
 
@@ -491,7 +491,7 @@ extern "C" int cdml_sdpa_fwd(const float *q, int ldq, const float *k, int ldk, c
   a.total = (int)total;
   a.padded = pad_to_xcd(a.total);
   if (hd_pad == 32) launch_hd<32, 64>(a, causal, vec, st);
-  else if (hd_pad == 64) launch_hd<64, 64>(a, causal, vec, st);
+  else if (hd_pad == 64) launch_hd<64, 32>(a, causal, vec, st);
   else launch_hd<128, 32>(a, causal, vec, st);
   return check_launch("flash_fwd_kernel");
 }
