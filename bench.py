@@ -21,7 +21,12 @@ Inputs are resident in HBM before the timed region starts.  The process never
 imports torch: torch ships its own HIP runtime, and the C ABI is driven
 through ctypes exactly as a P/Invoke host would.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+``other_configs`` adds end-to-end figures for the other BASELINE configs: a
+c2 MHA layer, the c3 12-layer decoder stack (MHA + FFN + LayerNorms), the c5
+time-series model, the c1 text model's forward and greedy generation, and one
+c3 sequence through the drop-in manager with host arrays (PCIe included).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-extras]
 """
 from __future__ import annotations
 
@@ -90,9 +95,10 @@ class Timer:
         return [a.elapsed_ms(b) for a, b in self.pairs[: self.i]]
 
 
-def bench_mha(N, st, steps, warmup):
+def bench_mha(N, st, steps, warmup, cfg=None):
     lib = N.lib()
-    B, L, D, H = C3["batch"], C3["seq"], C3["dim"], C3["heads"]
+    cfg = cfg or C3
+    B, L, D, H = cfg["batch"], cfg["seq"], cfg["dim"], cfg["heads"]
     hd = D // H
     rows = B * L
     from cdml import synth
@@ -198,6 +204,91 @@ def bench_decode(N, st, steps, warmup):
     return dict(ms=float(np.mean(ms)), ms_min=float(np.min(ms)))
 
 
+def extras(N, st):
+    """End-to-end figures for the other BASELINE configs (device-resident,
+    events on the engine's stream) and the PCIe-inclusive drop-in path."""
+    from cdml import host, synth
+
+    H = host.module()
+    out = {}
+    # c2: one causal MHA layer, B 16 x L 1024, D 512, 8 heads
+    c2 = dict(batch=16, seq=1024, dim=512, heads=8)
+    r = bench_mha(N, st, 10, 5, c2)
+    core, qkv, o = mha_flops(**c2)
+    out["c2_mha_layer"] = {"ms": round(r["wall_s"] / 10 * 1e3, 4),
+                           "tflops": round((core + qkv + o) / (r["wall_s"] / 10) / 1e12, 2),
+                           "flash_ms": round(r["flash_ms"], 4)}
+    log("[bench] extras: c3 12-layer decoder stack")
+    # c3: 12 post-LN decoder layers (MHA + FFN 4096 + 2 LayerNorms) on N(0,1) embeddings
+    cfg3 = {"dim": 1024, "heads": 16, "layers": 12, "ff": 4096, "max_seq": 4096, "discrete": False,
+            "input_dim": 1024, "output_dim": 1}
+    lm3, mgr = host.language_model(cfg3, synth.continuous_lm_weights(cfg3, 41, biased=False))
+    dev3 = H.DeviceLanguageModel(lm3, 4)
+    x3 = np.random.default_rng(6).standard_normal((4 * 4096, 1024), dtype=np.float32)
+    ms3 = dev3.time_layers(x3, 4, 4096, steps=3, warmup=1)
+    core, qkv, o = mha_flops(**C3)
+    ffn = 4 * 4 * 4096 * 1024 * 4096
+    fl3 = 12 * (core + qkv + o + ffn)
+    out["c3_decoder_stack_12_layers"] = {"ms": round(ms3, 3), "tflops": round(fl3 / (ms3 * 1e-3) / 1e12, 2),
+                                         "frac_of_fp32_mfma_peak": round(fl3 / (ms3 * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
+                                         "tokens_per_s": round(4 * 4096 / (ms3 * 1e-3), 1),
+                                         "gflop": round(fl3 / 1e9, 1)}
+    del dev3, lm3
+    # drop-in manager path on one c3 sequence: host arrays in and out (PCIe inclusive)
+    log("[bench] extras: drop-in manager (host arrays)")
+    D, Hh, L = 1024, 16, 4096
+    xs = np.random.default_rng(7).standard_normal((L, D), dtype=np.float32)
+    wq, wk, wv, wo = (synth.xavier_uniform(60 + i, D, D) for i in range(4))
+    bz = np.zeros(D, np.float32)
+
+    def mha_host():
+        q, k, v = mgr.ProjectQKV(xs, wq, bz, wk, bz, wv, bz)
+        mgr.ApplyRotaryPositionEmbeddingInPlace(q, Hh, 10000.0, False)
+        mgr.ApplyRotaryPositionEmbeddingInPlace(k, Hh, 10000.0, False)
+        a = mgr.ScaledDotProductAttention(q, k, v, Hh, None, True)
+        return mgr.ProjectOutputBatch(a, wo, bz, L, D)
+
+    mha_host()
+    t0 = time.perf_counter()
+    for _ in range(3):
+        mha_host()
+    dt = (time.perf_counter() - t0) / 3
+    core, qkv, o = mha_flops(1, L, D, Hh)
+    out["c3_mha_one_sequence_dropin_host_arrays"] = {
+        "ms": round(dt * 1e3, 3), "tflops": round((core + qkv + o) / dt / 1e12, 3),
+        "note": "HipAccelerationManager with float[,]-style host arrays: every call uploads its "
+                "activations and downloads its result (PCIe included); weights stay resident"}
+    # c5: time-series regression transformer, full forward, B 256 x L 512
+    log("[bench] extras: c5 time-series model")
+    cfg5 = {"dim": 256, "heads": 8, "layers": 6, "ff": 1024, "max_seq": 512, "discrete": False,
+            "input_dim": 5, "output_dim": 1}
+    lm5, _ = host.language_model(cfg5, synth.continuous_lm_weights(cfg5, 21), mgr)
+    dev5 = H.DeviceLanguageModel(lm5, 256)
+    x5 = synth.random_walk_windows(31, 256, 512, 5).reshape(256 * 512, 5)
+    ms5 = dev5.time_forward(x5, 256, 512, steps=5, warmup=2, continuous=True)
+    core, qkv, o = mha_flops(256, 512, 256, 8)
+    fl5 = 6 * (core + qkv + o + 4 * 256 * 512 * 256 * 1024) + 2 * 256 * 512 * 256 * (5 + 1)
+    out["c5_time_series_model"] = {"ms": round(ms5, 3), "tflops": round(fl5 / (ms5 * 1e-3) / 1e12, 2),
+                                   "windows_per_s": round(256 / (ms5 * 1e-3), 1)}
+    del dev5, lm5
+    # c1: README text model, forward of 4 x 64 tokens and greedy generation of 20 tokens
+    log("[bench] extras: c1 text model")
+    cfg1 = {"vocab": 200, "dim": 64, "heads": 4, "layers": 2, "ff": 128, "max_seq": 64}
+    lm1, _ = host.language_model(cfg1, synth.lm_weights(cfg1, 7), mgr)
+    dev1 = H.DeviceLanguageModel(lm1, 4)
+    ids = synth.token_ids(11, 4 * 64, 200).reshape(4, 64)
+    ms1 = dev1.time_forward(ids, 4, 64, steps=50, warmup=5)
+    dev1.GenerateGreedy(ids[:, :32], 20)
+    t0 = time.perf_counter()
+    for _ in range(5):
+        dev1.GenerateGreedy(ids[:, :32], 20)
+    gen_ms = (time.perf_counter() - t0) / 5 * 1e3
+    out["c1_text_model"] = {"forward_ms": round(ms1, 4), "forward_tokens_per_s": round(256 / (ms1 * 1e-3), 1),
+                            "generate_20_tokens_batch4_ms": round(gen_ms, 3),
+                            "generated_tokens_per_s": round(80 / (gen_ms * 1e-3), 1)}
+    return out
+
+
 def cpu_baseline(sample_seqs=3):
     """The multi-threaded CPU restatement of AccelerationMutliThreadCPU's
     ProjectQKV / RoPE / ScaledDotProductAttention / ProjectOutputBatch
@@ -236,6 +327,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-extras", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the attention path is single-device by design "
@@ -295,6 +387,9 @@ def main():
                                       "frac": round(gbs / HBM_PEAK_GBS, 4),
                                       "traffic": TRAFFIC_BYTES["decode_c4"],
                                       "algorithmic_per_launch": nbytes}}
+    if not args.no_extras:
+        log("[bench] extras")
+        res["other_configs"] = extras(N, st)
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (multi-threaded restatement)")
         cb = cpu_baseline()

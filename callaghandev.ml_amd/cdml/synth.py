@@ -139,3 +139,20 @@ def random_walk_windows(seed: int, batch: int, length: int, features: int, step:
     lo = x.min(axis=1, keepdims=True)
     hi = x.max(axis=1, keepdims=True)
     return ((x - lo) / np.where(hi > lo, hi - lo, 1.0)).astype(np.float32)
+
+
+def continuous_lm_weights(cfg: dict, seed: int, biased: bool = True) -> dict:
+    """Weights of a continuous-input model (LanguageModel.Forward(float[,])):
+    the lm_weights blocks plus InputProjection [D, F] with bias [D] and the
+    output head [OutputDim, D] with bias, Xavier-uniform."""
+    w = lm_weights(dict(cfg, vocab=2), seed, biased=biased)
+    D, F, O = cfg["dim"], cfg["input_dim"], cfg["output_dim"]
+    w["input_proj"] = xavier_uniform(seed + 900, D, F)
+    w["out_proj"] = xavier_uniform(seed + 902, O, D)
+    if biased:
+        w["input_bias"] = np.float32(0.1) * normal(seed + 901, (D,))
+        w["out_bias"] = np.float32(0.1) * normal(seed + 903, (O,))
+    else:
+        w["input_bias"] = np.zeros(D, np.float32)
+        w["out_bias"] = np.zeros(O, np.float32)
+    return w

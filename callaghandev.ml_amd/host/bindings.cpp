@@ -379,5 +379,39 @@ PYBIND11_MODULE(_cdml_host, m) {
              return ms / std::max(steps, 1);
            },
            py::arg("inputs"), py::arg("batch"), py::arg("seqLen"), py::arg("steps") = 10,
-           py::arg("warmup") = 2, py::arg("continuous") = false);
+           py::arg("warmup") = 2, py::arg("continuous") = false)
+      .def("time_layers",
+           // The decoder blocks alone on embeddings x [batch * seqLen, D]
+           // resident in HBM: mean ms of `steps` passes after `warmup`.
+           [](DeviceLanguageModel &d, py::object x, int batch, int seqLen, int steps, int warmup) {
+             auto X = mat(x);
+             if (X.view.null() || X.view.rows != batch * seqLen)
+               throw ArgumentException("x must be [batch * seqLen, D]", "x");
+             if (batch <= 0 || batch > d.batch_capacity()) throw ArgumentOutOfRangeException("batch");
+             auto chk = [](int rc) {
+               if (rc != CDML_OK) throw InvalidOperationException(cdml_last_error());
+             };
+             void *dx = nullptr;
+             const size_t bytes = (size_t)X.view.rows * X.view.cols * sizeof(float);
+             chk(cdml_malloc(&dx, bytes));
+             chk(cdml_memcpy_h2d_async(dx, X.view.data, bytes, d.stream()));
+             cdml_event e0, e1;
+             chk(cdml_event_create(&e0));
+             chk(cdml_event_create(&e1));
+             float ms = 0.f;
+             {
+               py::gil_scoped_release nogil;
+               for (int i = 0; i < warmup; ++i) d.layers_device(static_cast<float *>(dx), batch, seqLen);
+               d.synchronize();
+               chk(cdml_event_record(e0, d.stream()));
+               for (int i = 0; i < steps; ++i) d.layers_device(static_cast<float *>(dx), batch, seqLen);
+               chk(cdml_event_record(e1, d.stream()));
+               chk(cdml_event_elapsed_ms(e0, e1, &ms));
+             }
+             cdml_event_destroy(e0);
+             cdml_event_destroy(e1);
+             cdml_free(dx);
+             return ms / std::max(steps, 1);
+           },
+           py::arg("x"), py::arg("batch"), py::arg("seqLen"), py::arg("steps") = 3, py::arg("warmup") = 1);
 }

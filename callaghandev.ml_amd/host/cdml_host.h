@@ -320,6 +320,8 @@ class DeviceLanguageModel {
   // Enqueue-only forms over device pointers for benchmarking.
   void forward_device(const int *dev_ids, const float *dev_x, int batch, int seqLen,
                       float *dev_out);
+  // The decoder blocks alone, in place on device rows x [batch * seqLen, D].
+  void layers_device(float *dev_x, int batch, int seqLen);
   cdml_stream stream() const { return stream_; }
   int output_dim() const { return cfg_.EffectiveOutputDim(); }
   int batch_capacity() const { return cap_; }

@@ -429,6 +429,12 @@ void DeviceLanguageModel::hidden_pass(float *x, int batch, int seqLen, bool fill
   }
 }
 
+void DeviceLanguageModel::layers_device(float *dev_x, int batch, int seqLen) {
+  if (batch <= 0 || batch > cap_) throw ArgumentOutOfRangeException("batch");
+  if (seqLen <= 0 || seqLen > cfg_.MaxSequenceLength) throw ArgumentOutOfRangeException("seqLen");
+  hidden_pass(dev_x, batch, seqLen, false);
+}
+
 void DeviceLanguageModel::forward_device(const int *dev_ids, const float *dev_x, int batch,
                                          int seqLen, float *dev_out) {
   const int D = cfg_.EmbeddingDim, O = cfg_.EffectiveOutputDim();

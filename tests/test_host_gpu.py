@@ -208,16 +208,6 @@ def _oracle_continuous(cfg, w, x):
     return O.project_output_batch(h, w["out_proj"], w["out_bias"])
 
 
-def c5_weights(cfg, seed):
-    w = synth.lm_weights(dict(cfg, vocab=2), seed, biased=True)
-    D, F = cfg["dim"], cfg["input_dim"]
-    w["input_proj"] = synth.xavier_uniform(seed + 900, D, F)
-    w["input_bias"] = np.float32(0.1) * synth.normal(seed + 901, (D,))
-    w["out_proj"] = synth.xavier_uniform(seed + 902, cfg["output_dim"], D)
-    w["out_bias"] = np.float32(0.1) * synth.normal(seed + 903, (cfg["output_dim"],))
-    return w
-
-
 def test_time_series_transformer_c5_sampled():
     """Config 5 (F 5 -> D 256, 8 x 32, 6 layers, FF 1024, out 1; B 256 x 512,
     random-walk features): the whole batch on the device engine, three windows
@@ -225,7 +215,7 @@ def test_time_series_transformer_c5_sampled():
     Hm = host.module()
     cfg = {"dim": 256, "heads": 8, "layers": 6, "ff": 1024, "max_seq": 512, "discrete": False,
            "input_dim": 5, "output_dim": 1}
-    w = c5_weights(cfg, 21)
+    w = synth.continuous_lm_weights(cfg, 21)
     lm, _ = host.language_model(cfg, w)
     B, L = 256, 512
     x = synth.random_walk_windows(31, B, L, 5)
