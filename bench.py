@@ -382,7 +382,7 @@ def main():
         gbs = nbytes / (dec["ms"] * 1e-3) / 1e9
         res["decode"] = {"workload": "c4 decode step (B 64, KV 8192, 16 heads x 128)",
                          "ms": round(dec["ms"], 4), "tokens_per_s": round(C4["batch"] / (dec["ms"] * 1e-3), 1),
-                         "roofline": {"kernel": "decode_split_kernel + decode_combine_kernel", "bound": "hbm",
+                         "roofline": {"kernel": "decode_split_kernel + decode_combine_vec_kernel", "bound": "hbm",
                                       "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                       "frac": round(gbs / HBM_PEAK_GBS, 4),
                                       "traffic": TRAFFIC_BYTES["decode_c4"],

@@ -22,6 +22,7 @@ namespace {
 constexpr int DC_THREADS = 256;
 constexpr int DC_CHUNK = 256;                // keys per workgroup
 constexpr int DC_KITER = DC_CHUNK / 4 / 8;   // steps of 8 keys per wave
+static_assert(DC_KITER % 2 == 0, "the key loop alternates two register sets");
 
 struct DecodeArgs {
   const float *q, *kc, *vc;
@@ -101,26 +102,17 @@ __global__ void __launch_bounds__(DC_THREADS) decode_split_kernel(const DecodeAr
 #pragma unroll
   for (int i = 0; i < EPL; ++i) o[i] = 0.f;
 
-  float kr[2][EPL], vr[2][EPL];
-  auto fetch = [&](int it, int buf) {
-    const int key = key0 + it * 8;
-    if (key < len) {
-      load_slice<VW, NV>(kb + (size_t)key * a.dim, kr[buf]);
-      load_slice<VW, NV>(vb + (size_t)key * a.dim, vr[buf]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < EPL; ++i) kr[buf][i] = vr[buf][i] = 0.f;
-    }
-  };
-  fetch(0, 0);
-#pragma unroll
-  for (int it = 0; it < DC_KITER; ++it) {
-    const int cur = it & 1;
-    if (it + 1 < DC_KITER) fetch(it + 1, cur ^ 1);
+  // Rows past the cache length are clamped to its last row (the chunk holds
+  // at least one valid key) and left out of the softmax below, so the loads
+  // need no branch.  Two register sets alternate: the next step's K and V
+  // rows are in flight while the current ones are consumed.
+  const int last = len - 1;
+  float k0r[EPL], v0r[EPL], k1r[EPL], v1r[EPL];
+  auto step = [&](int it, const float(&kr)[EPL], const float(&vr)[EPL]) {
     const int key = key0 + it * 8;
     float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) s += q[i] * kr[cur][i];
+    for (int i = 0; i < EPL; ++i) s += q[i] * kr[i];
     s += __shfl_xor(s, 1);
     s += __shfl_xor(s, 2);
     s += __shfl_xor(s, 4);
@@ -131,9 +123,24 @@ __global__ void __launch_bounds__(DC_THREADS) decode_split_kernel(const DecodeAr
       const float p = fast_exp2(s - mn);
       l = l * alpha + p;
 #pragma unroll
-      for (int i = 0; i < EPL; ++i) o[i] = o[i] * alpha + p * vr[cur][i];
+      for (int i = 0; i < EPL; ++i) o[i] = o[i] * alpha + p * vr[i];
       m = mn;
     }
+  };
+  load_slice<VW, NV>(kb + (size_t)min(key0, last) * a.dim, k0r);
+  load_slice<VW, NV>(vb + (size_t)min(key0, last) * a.dim, v0r);
+#pragma unroll
+  for (int it = 0; it < DC_KITER; it += 2) {
+    const int k1 = min(key0 + (it + 1) * 8, last);
+    load_slice<VW, NV>(kb + (size_t)k1 * a.dim, k1r);
+    load_slice<VW, NV>(vb + (size_t)k1 * a.dim, v1r);
+    step(it, k0r, v0r);
+    if (it + 2 < DC_KITER) {
+      const int k2 = min(key0 + (it + 2) * 8, last);
+      load_slice<VW, NV>(kb + (size_t)k2 * a.dim, k0r);
+      load_slice<VW, NV>(vb + (size_t)k2 * a.dim, v0r);
+    }
+    step(it + 1, k1r, v1r);
   }
 
   // Merge the 8 key groups of the wave (lanes with equal e).
@@ -168,6 +175,53 @@ __global__ void __launch_bounds__(DC_THREADS) decode_split_kernel(const DecodeAr
     for (int w = 0; w < 4; ++w) L += red_l[w] * fast_exp2(red_m[w] - mu);
     part[HD] = M;
     part[HD + 1] = L;
+  }
+}
+
+// Merges the chunks of one (sequence, head) for the head dims of
+// decode_split_kernel: with M the max over the chunk maxima and
+// w_s = 2^(m_s - M), o = sum_s w_s o_s / sum_s w_s l_s.  Thread t sums dim
+// t % HD over every G-th chunk from t / HD, so all G*HD threads have loads in
+// flight; the G partial sums meet in LDS.
+template <int HD>
+__global__ void __launch_bounds__(DC_THREADS) decode_combine_vec_kernel(const DecodeArgs a) {
+  constexpr int G = DC_THREADS / HD;
+  __shared__ float red_m[4], red_l[4];
+  __shared__ float acc_s[G][HD];
+  const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int n = a.nsplit;
+  const float *part = a.part + (size_t)(b * a.heads + h) * n * (HD + 2);
+
+  float M = -INFINITY;
+  for (int s = t; s < n; s += DC_THREADS) M = fmaxf(M, part[s * (HD + 2) + HD]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+  if (lane == 0) red_m[wave] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+  const float mu = M == -INFINITY ? 0.f : M;
+
+  float l = 0.f;
+  for (int s = t; s < n; s += DC_THREADS)
+    l += part[s * (HD + 2) + HD + 1] * fast_exp2(part[s * (HD + 2) + HD] - mu);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
+  if (lane == 0) red_l[wave] = l;
+
+  const int d = t % HD, sg = t / HD;
+  float acc = 0.f;
+#pragma unroll 4
+  for (int s = sg; s < n; s += G)
+    acc += part[s * (HD + 2) + d] * fast_exp2(part[s * (HD + 2) + HD] - mu);
+  acc_s[sg][d] = acc;
+  __syncthreads();
+  if (t < HD) {
+    float sum = 0.f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) sum += acc_s[g][t];
+    const float L = red_l[0] + red_l[1] + red_l[2] + red_l[3];
+    a.o[(size_t)b * a.dim + (size_t)h * HD + t] = L > 0.f ? sum / L : 0.f;
   }
 }
 
@@ -292,17 +346,33 @@ extern "C" int cdml_decode_attn(const float *q, const float *kcache, const float
   const bool vec = fast_hd(a.hd) && dim % 4 == 0 && aligned16(q) && aligned16(kcache) &&
                    aligned16(vcache);
   if (vec) {
+    const dim3 cgrid(num_heads, batch);
     switch (a.hd) {
-      case 16: decode_split_kernel<16><<<grid, DC_THREADS, 0, st>>>(a); break;
-      case 32: decode_split_kernel<32><<<grid, DC_THREADS, 0, st>>>(a); break;
-      case 64: decode_split_kernel<64><<<grid, DC_THREADS, 0, st>>>(a); break;
-      case 128: decode_split_kernel<128><<<grid, DC_THREADS, 0, st>>>(a); break;
-      default: decode_split_kernel<256><<<grid, DC_THREADS, 0, st>>>(a); break;
+      case 16:
+        decode_split_kernel<16><<<grid, DC_THREADS, 0, st>>>(a);
+        decode_combine_vec_kernel<16><<<cgrid, DC_THREADS, 0, st>>>(a);
+        break;
+      case 32:
+        decode_split_kernel<32><<<grid, DC_THREADS, 0, st>>>(a);
+        decode_combine_vec_kernel<32><<<cgrid, DC_THREADS, 0, st>>>(a);
+        break;
+      case 64:
+        decode_split_kernel<64><<<grid, DC_THREADS, 0, st>>>(a);
+        decode_combine_vec_kernel<64><<<cgrid, DC_THREADS, 0, st>>>(a);
+        break;
+      case 128:
+        decode_split_kernel<128><<<grid, DC_THREADS, 0, st>>>(a);
+        decode_combine_vec_kernel<128><<<cgrid, DC_THREADS, 0, st>>>(a);
+        break;
+      default:
+        decode_split_kernel<256><<<grid, DC_THREADS, 0, st>>>(a);
+        decode_combine_vec_kernel<256><<<cgrid, DC_THREADS, 0, st>>>(a);
+        break;
     }
-  } else {
-    decode_split_generic_kernel<<<grid, 256, sizeof(float) * (256 + 8), st>>>(a);
+    return check_launch("decode_split_kernel/decode_combine_vec_kernel");
   }
-  rc = check_launch("decode_split_kernel");
+  decode_split_generic_kernel<<<grid, 256, sizeof(float) * (256 + 8), st>>>(a);
+  rc = check_launch("decode_split_generic_kernel");
   if (rc) return rc;
   decode_combine_kernel<<<dim3(num_heads, batch), dim3(a.hd < 256 ? 128 : 256), 0, st>>>(a);
   return check_launch("decode_combine_kernel");
