@@ -11,6 +11,8 @@
 // 16-byte LDS reads that feed four MFMAs each.  The reduction index k is
 // visited in the permuted order kappa(s, h) = 8*(s/4) + 4*h + s%4 on both
 // operands, which leaves the sum unchanged.
+#include <algorithm>
+
 #include "common.h"
 
 namespace cdml {
@@ -19,6 +21,9 @@ namespace {
 constexpr int BM = 128, BN = 128, BK = 32, LDSK = BK + 4;
 constexpr int NTHREADS = 256;
 constexpr int GROUP_M = 8;
+// Epilogue selector of the tiled kernel beyond the activations: no
+// activation, rotary embedding on problems 0 and 1.
+constexpr int kActRope = 100;
 
 struct GemmProblem {
   const float *w;
@@ -35,7 +40,55 @@ struct GemmArgs {
   int tiles_m, tiles_n;  // tiles_n counts the tiles of one problem
   int total, padded;
   int act;
+  // Rotary position embedding applied to problems 0 and 1 (Q and K) in the
+  // epilogue when rope_cs is set: rope_cs[pos * rope_hd / 2 + p] holds
+  // (cos, sin) of position pos for pair p; row m has position
+  // rope_pos0 + (rope_seg > 0 ? m % rope_seg : m), below rope_npos.
+  const float2 *rope_cs;
+  int rope_hd, rope_npos, rope_pos0, rope_seg;
 };
+
+// Epilogue of both GEMM kernels with the rotary embedding of
+// AccelerationCPU.cs:4947-4975 folded in.  A lane holds column n of rows
+// mrow0 + 32 i + 8 (r / 4) + 4 hf + r % 4, so the pair partner of column n
+// (n ^ 1; head dims are even) sits in lane li ^ 1 of the same register: one
+// lane swap gives each lane both halves of its pair.  The swap runs in every
+// lane; only the store is predicated.
+template <int BI, int BJ>
+__device__ __forceinline__ void store_rope(const GemmArgs &args, const GemmProblem &P,
+                                           const floatx16 (&acc)[BI][BJ], int mrow0, int ncol0,
+                                           int li, int hf) {
+  const int pairs = args.rope_hd >> 1;
+  int n[BJ], pidx[BJ];
+  bool odd[BJ];
+  float bias[BJ];
+#pragma unroll
+  for (int j = 0; j < BJ; ++j) {
+    n[j] = ncol0 + j * 32 + li;
+    const int c = n[j] % args.rope_hd;
+    pidx[j] = c >> 1;
+    odd[j] = c & 1;
+    bias[j] = (P.bias && n[j] < args.N) ? P.bias[n[j]] : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < BI; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = mrow0 + i * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
+      int pos = args.rope_pos0 + (args.rope_seg > 0 ? m % args.rope_seg : m);
+      pos = min(pos, args.rope_npos - 1);  // rows past M are never stored
+      const float2 *cs = args.rope_cs + (size_t)pos * pairs;
+#pragma unroll
+      for (int j = 0; j < BJ; ++j) {
+        const float y = acc[i][j][r] + bias[j];
+        const float yp = __shfl_xor(y, 1);
+        const float2 t = cs[pidx[j]];
+        const float out = odd[j] ? yp * t.y + y * t.x : y * t.x - yp * t.y;
+        if (m < args.M && n[j] < args.N) P.c[(size_t)m * args.ldc + n[j]] = out;
+      }
+    }
+  }
+}
 
 __device__ __forceinline__ float activate(float x, int act) {
   switch (act) {
@@ -180,6 +233,10 @@ __global__ void __launch_bounds__(NTHREADS) gemm_nt_kernel(const GemmArgs args) 
     __syncthreads();
   }
 
+  if (args.rope_cs && prob < 2) {
+    store_rope<2, 2>(args, P, acc, m0 + wm * 64, n0 + wn * 64, li, hf);
+    return;
+  }
   // Epilogue: D[i][j] of block (bi, bj) sits at row 8*(r/4) + 4*hf + r%4,
   // column li; 32 lanes store 32 consecutive columns of one row.
 #pragma unroll
@@ -329,6 +386,12 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const Gem
     __syncthreads();
   }
 
+  if constexpr (ACT == kActRope) {
+    if (prob < 2) {
+      store_rope<BI, BJ>(args, P, acc, m0 + wm * (TM / WM), n0 + wn * (TN / WN), li, hf);
+      return;
+    }
+  }
   // Epilogue: D[i][j] of block (bi, bj) sits at row 8*(r/4) + 4*hf + r%4,
   // column li; 32 lanes store 32 consecutive columns of one row.
 #pragma unroll
@@ -356,6 +419,10 @@ int launch_tile(GemmArgs g, hipStream_t stream) {
   g.total = g.tiles_m * g.tiles_n * g.nprob;
   g.padded = pad_to_xcd(g.total);
   const dim3 grid(g.padded), block(64 * WM * WN);
+  if (g.rope_cs) {
+    gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, kActRope><<<grid, block, 0, stream>>>(g);
+    return CDML_OK;
+  }
   switch (g.act) {
     case CDML_ACT_NONE: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_NONE><<<grid, block, 0, stream>>>(g); break;
     case CDML_ACT_SIGMOID: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_SIGMOID><<<grid, block, 0, stream>>>(g); break;
@@ -423,6 +490,47 @@ extern "C" int cdml_project_qkv(const float *x, const float *wq, const float *bq
   g.p[2] = {wv, bv, v};
   g.act = CDML_ACT_NONE;
   return launch_gemm(g, as_hip(stream), "cdml_project_qkv");
+}
+
+extern "C" int cdml_project_qkv_rope(const float *x, const float *wq, const float *bq,
+                                     const float *wk, const float *bk, const float *wv,
+                                     const float *bv, float *q, float *k, float *v, int rows,
+                                     int in_dim, int out_dim, int head_dim, const float *rope_cs,
+                                     int n_pos, int pos_offset, int seg_len, cdml_stream stream) {
+  if (rows < 0 || in_dim < 0 || out_dim < 0 || n_pos < 0 || pos_offset < 0 || seg_len < 0)
+    return fail(CDML_E_INVALID, "cdml_project_qkv_rope: negative size");
+  if (head_dim <= 0 || (head_dim & 1) || out_dim % head_dim)
+    return fail(CDML_E_INVALID,
+                "cdml_project_qkv_rope: head_dim must be even, positive and divide out_dim");
+  if (rows == 0 || out_dim == 0) return CDML_OK;
+  if (!x || !wq || !wk || !wv || !q || !k || !v || !rope_cs)
+    return fail(CDML_E_INVALID, "cdml_project_qkv_rope: NULL pointer");
+  if (reinterpret_cast<uintptr_t>(rope_cs) % 8)
+    return fail(CDML_E_INVALID, "cdml_project_qkv_rope: rope_cs must be 8-byte aligned");
+  const long long last_pos = (long long)pos_offset + (seg_len > 0 ? std::min(rows, seg_len) : rows) - 1;
+  if (last_pos >= n_pos)
+    return fail(CDML_E_INVALID, "cdml_project_qkv_rope: position %lld outside the %d-row table",
+                last_pos, n_pos);
+  int rc = ensure_device();
+  if (rc) return rc;
+  GemmArgs g{};
+  g.a = x;
+  g.lda = in_dim;
+  g.ldc = out_dim;
+  g.M = rows;
+  g.N = out_dim;
+  g.K = in_dim;
+  g.nprob = 3;
+  g.p[0] = {wq, bq, q};
+  g.p[1] = {wk, bk, k};
+  g.p[2] = {wv, bv, v};
+  g.act = CDML_ACT_NONE;
+  g.rope_cs = reinterpret_cast<const float2 *>(rope_cs);
+  g.rope_hd = head_dim;
+  g.rope_npos = n_pos;
+  g.rope_pos0 = pos_offset;
+  g.rope_seg = seg_len;
+  return launch_gemm(g, as_hip(stream), "cdml_project_qkv_rope");
 }
 
 extern "C" int cdml_linear(const float *x, int ldx, const float *w, const float *b, float *y,

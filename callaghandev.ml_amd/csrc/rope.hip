@@ -46,6 +46,22 @@ __global__ void __launch_bounds__(256) rope_kernel(const RopeArgs a) {
   }
 }
 
+// (cos, sin) of every (position, pair) with the arithmetic of rope_kernel,
+// so a projection epilogue that reads the table rotates exactly as the
+// in-place kernel does.
+__global__ void __launch_bounds__(256) rope_table_kernel(const RopeArgs a, float2 *cs) {
+  const long long total = (long long)a.rows * a.pairs;
+  for (long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (long long)gridDim.x * blockDim.x) {
+    const int p = (int)(idx % a.pairs);
+    const int pos = (int)(idx / a.pairs);
+    const float theta = (float)pos / a.denom[p];
+    float s, c;
+    sincosf(theta, &s, &c);
+    cs[idx] = make_float2(c, s);
+  }
+}
+
 }  // namespace
 }  // namespace cdml
 
@@ -85,4 +101,31 @@ extern "C" int cdml_rope(float *x, int rows, int ld, int start_col, int head_dim
   if (blocks > 16384) blocks = 16384;
   rope_kernel<<<dim3((unsigned)blocks), dim3(256), 0, as_hip(stream)>>>(a);
   return check_launch("rope_kernel");
+}
+
+extern "C" int cdml_rope_table(float *cs, int n_pos, int head_dim, float base_theta,
+                               cdml_stream stream) {
+  if (n_pos < 0 || head_dim <= 0 || (head_dim & 1))
+    return fail(CDML_E_INVALID, "cdml_rope_table: n_pos >= 0 and an even head_dim > 0 required");
+  if (!(base_theta > 0.f) || std::isinf(base_theta))
+    return fail(CDML_E_INVALID, "cdml_rope_table: base_theta must be positive and finite");
+  if (head_dim / 2 > kMaxPairs)
+    return fail(CDML_E_INVALID, "cdml_rope_table: head_dim above %d", 2 * kMaxPairs);
+  if (n_pos == 0) return CDML_OK;
+  if (!cs) return fail(CDML_E_INVALID, "cdml_rope_table: cs is NULL");
+  if (reinterpret_cast<uintptr_t>(cs) % 8)
+    return fail(CDML_E_INVALID, "cdml_rope_table: cs must be 8-byte aligned");
+  int rc = ensure_device();
+  if (rc) return rc;
+  RopeArgs a{};
+  a.rows = n_pos;
+  a.pairs = head_dim / 2;
+  for (int p = 0; p < a.pairs; ++p)
+    a.denom[p] = powf(base_theta, (2.0f * (float)p) / (float)head_dim);
+  const long long total = (long long)n_pos * a.pairs;
+  long long blocks = (total + 255) / 256;
+  if (blocks > 16384) blocks = 16384;
+  rope_table_kernel<<<dim3((unsigned)blocks), dim3(256), 0, as_hip(stream)>>>(
+      a, reinterpret_cast<float2 *>(cs));
+  return check_launch("rope_table_kernel");
 }

@@ -350,6 +350,7 @@ class DeviceLanguageModel {
   // activations [cap * maxSeq, width]
   float *x_, *q_, *k_, *v_, *att_, *proj_, *h_, *ff_, *ff2_, *logits_;
   int *ids_, *pos_, *kvlen_, *gen_;
+  float *rope_cs_;  // cdml_rope_table of MaxSequenceLength positions
   void *ws_ = nullptr;
   size_t ws_bytes_ = 0;
   int ff_max_ = 0;

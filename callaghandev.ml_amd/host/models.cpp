@@ -375,6 +375,9 @@ DeviceLanguageModel::DeviceLanguageModel(const LanguageModel &model, int batch_c
     gen_ = reinterpret_cast<int *>(alloc(rows));
     check(cdml_decode_attn_workspace_size(cap_, S, D, cfg_.NumHeads, &ws_bytes_), "workspace size");
     ws_ = alloc(ws_bytes_ / sizeof(float) + 1);
+    // (cos, sin) of every position the model can see, shared by all layers
+    rope_cs_ = alloc((size_t)S * (D / cfg_.NumHeads));
+    check(cdml_rope_table(rope_cs_, S, D / cfg_.NumHeads, 10000.0f, stream_), "cdml_rope_table");
     synchronize();
   } catch (...) {
     for (void *p : allocs_) cdml_free(p);
@@ -400,10 +403,10 @@ void DeviceLanguageModel::hidden_pass(float *x, int batch, int seqLen, bool fill
   const int rows = batch * seqLen;
   const float scale = 1.0f / std::sqrt((float)hd);
   for (auto &L : layers_) {
-    check(cdml_project_qkv(x, L.wq, L.bq, L.wk, L.bk, L.wv, L.bv, q_, k_, v_, rows, D, D, stream_),
-          "cdml_project_qkv");
-    check(cdml_rope(q_, rows, D, 0, hd, H, 10000.0f, 0, 0, seqLen, nullptr, stream_), "cdml_rope");
-    check(cdml_rope(k_, rows, D, 0, hd, H, 10000.0f, 0, 0, seqLen, nullptr, stream_), "cdml_rope");
+    // ProjectQKV + RoPE on Q and K (MultiHeadAttention.cs:108-110) in one launch
+    check(cdml_project_qkv_rope(x, L.wq, L.bq, L.wk, L.bk, L.wv, L.bv, q_, k_, v_, rows, D, D, hd,
+                                rope_cs_, S, 0, seqLen, stream_),
+          "cdml_project_qkv_rope");
     if (fill_cache) {
       const size_t rowb = (size_t)seqLen * D * sizeof(float), pitch = (size_t)S * D * sizeof(float);
       check(cdml_memcpy2d_d2d_async(L.kcache, pitch, k_, rowb, rowb, batch, stream_), "cache fill");
@@ -494,10 +497,10 @@ void DeviceLanguageModel::decode_step(const int *dev_tok, int batch, int pos, fl
   check(cdml_fill_i32_async(pos_, batch, pos, stream_), "positions");
   check(cdml_fill_i32_async(kvlen_, batch, pos + 1, stream_), "kv lengths");
   for (auto &L : layers_) {
-    check(cdml_project_qkv(x, L.wq, L.bq, L.wk, L.bk, L.wv, L.bv, q_, k_, v_, batch, D, D, stream_),
-          "cdml_project_qkv");
-    check(cdml_rope(q_, batch, D, 0, hd, H, 10000.0f, 0, pos, 1, nullptr, stream_), "cdml_rope");
-    check(cdml_rope(k_, batch, D, 0, hd, H, 10000.0f, 0, pos, 1, nullptr, stream_), "cdml_rope");
+    // every row at position pos (seg_len 1)
+    check(cdml_project_qkv_rope(x, L.wq, L.bq, L.wk, L.bk, L.wv, L.bv, q_, k_, v_, batch, D, D, hd,
+                                rope_cs_, S, pos, 1, stream_),
+          "cdml_project_qkv_rope");
     check(cdml_kv_cache_append(k_, v_, L.kcache, L.vcache, pos_, batch, S, D, stream_), "kv append");
     check(cdml_decode_attn(q_, L.kcache, L.vcache, kvlen_, att_, batch, S, D, H, scale, ws_, ws_bytes_,
                            stream_),

@@ -143,6 +143,30 @@ int cdml_rope(float *x, int rows, int ld, int start_col, int head_dim,
               int num_heads, float base_theta, int inverse, int pos_offset,
               int seg_len, const int *positions, cdml_stream stream);
 
+/* The rotation table of cdml_rope for positions 0..n_pos-1: cs (device,
+ * 8-byte aligned, n_pos * head_dim floats) receives (cos theta, sin theta) of
+ * pair p at position pos in cs[2 * (pos * head_dim/2 + p) + {0, 1}], computed
+ * with cdml_rope's arithmetic.  No counterpart of its own in the reference:
+ * it serves cdml_project_qkv_rope, the fusion of the ProjectQKV and
+ * ApplyRotaryPositionEmbeddingInPlace calls of MultiHeadAttention.Forward
+ * (MultiHeadAttention.cs:96-111). */
+int cdml_rope_table(float *cs, int n_pos, int head_dim, float base_theta,
+                    cdml_stream stream);
+
+/* cdml_project_qkv followed by the forward rotary embedding of Q and K, as
+ * MultiHeadAttention.Forward calls ProjectQKV and then
+ * applies the rotary embedding to Q and K (MultiHeadAttention.cs:108-110,
+ * RotaryPositionEmbedding.cs:20-73), in one launch: the rotation is applied in the projection's
+ * epilogue from a cdml_rope_table of n_pos positions.  Row r has position
+ * pos_offset + (seg_len > 0 ? r % seg_len : r), which must be below n_pos.
+ * head_dim must be even and divide out_dim; V is not rotated. */
+int cdml_project_qkv_rope(const float *x, const float *wq, const float *bq,
+                          const float *wk, const float *bk, const float *wv,
+                          const float *bv, float *q, float *k, float *v,
+                          int rows, int in_dim, int out_dim, int head_dim,
+                          const float *rope_cs, int n_pos, int pos_offset,
+                          int seg_len, cdml_stream stream);
+
 /* IAccelerationManager.ScaledDotProductAttention (:167) and
  * MultiHeadAttentionForward (:155), replacing AccelerationCPU.cs:1797-1956
  * and :1647-1792 and GPU/TransformerCore.cs:659-834,1142-1349.

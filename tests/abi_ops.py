@@ -40,6 +40,28 @@ def project_qkv(x, wq, bq, wk, bk, wv, bv):
     return tuple(down(t, (rows, out)) for t in (q, k, v))
 
 
+def rope_table(n_pos, head_dim, base=10000.0):
+    cs = N.DeviceBuffer(max(8, n_pos * head_dim * 4))
+    N.check(N.lib().cdml_rope_table(cs.ptr, n_pos, head_dim, base, stream().handle))
+    return down(cs, (n_pos, head_dim // 2, 2))
+
+
+def project_qkv_rope(x, wq, bq, wk, bk, wv, bv, head_dim, n_pos=None, pos_offset=0, seg_len=0,
+                     base=10000.0):
+    rows, ind = x.shape
+    out = wq.shape[0]
+    if n_pos is None:
+        n_pos = pos_offset + (min(rows, seg_len) if seg_len else rows)
+    cs = N.DeviceBuffer(max(8, n_pos * head_dim * 4))
+    N.check(N.lib().cdml_rope_table(cs.ptr, n_pos, head_dim, base, stream().handle))
+    bufs = [up(a) for a in (x, wq, bq, wk, bk, wv, bv)]
+    q, k, v = (N.DeviceBuffer(max(4, rows * out * 4)) for _ in range(3))
+    N.check(N.lib().cdml_project_qkv_rope(*(b.ptr for b in bufs), q.ptr, k.ptr, v.ptr, rows, ind, out,
+                                          head_dim, cs.ptr, n_pos, pos_offset, seg_len,
+                                          stream().handle))
+    return tuple(down(t, (rows, out)) for t in (q, k, v))
+
+
 def linear(x, w, b, act=0):
     rows, ind = x.shape
     out = w.shape[0]

@@ -47,6 +47,16 @@ def test_other_argument_checks():
     assert L.cdml_linear(None, 4, None, None, None, 4, 2, 4, 4, 9, None) == N.E_INVALID   # activation
     assert L.cdml_linear(None, 2, None, None, None, 4, 2, 4, 4, 0, None) == N.E_INVALID   # ldx < in
     assert L.cdml_project_qkv(*([None] * 10), -1, 4, 4, None) == N.E_INVALID
+    qkv = [C.c_void_p(16)] * 10  # never dereferenced: every case fails before a launch
+    assert L.cdml_project_qkv_rope(*qkv, 8, 4, 8, 3, qkv[0], 8, 0, 0, None) == N.E_INVALID  # odd head_dim
+    assert L.cdml_project_qkv_rope(*qkv, 8, 4, 8, 6, qkv[0], 8, 0, 0, None) == N.E_INVALID  # 6 !| 8
+    assert L.cdml_project_qkv_rope(*qkv, 8, 4, 8, 4, qkv[0], 7, 0, 0, None) == N.E_INVALID  # row 7 > table
+    assert L.cdml_project_qkv_rope(*qkv, 8, 4, 8, 4, qkv[0], 8, 1, 0, None) == N.E_INVALID  # offset past
+    assert L.cdml_project_qkv_rope(*qkv, 8, 4, 8, 4, None, 8, 0, 0, None) == N.E_INVALID    # no table
+    assert L.cdml_project_qkv_rope(*qkv, 0, 4, 8, 4, None, 0, 0, 0, None) == N.OK           # empty
+    assert L.cdml_rope_table(None, 4, 5, 10000.0, None) == N.E_INVALID                     # odd head_dim
+    assert L.cdml_rope_table(None, 4, 4, 0.0, None) == N.E_INVALID                         # bad base
+    assert L.cdml_rope_table(None, 0, 4, 10000.0, None) == N.OK                            # empty
     sz = C.c_size_t(0)
     assert L.cdml_decode_attn_workspace_size(64, 8192, 2048, 16, C.byref(sz)) == N.OK
     assert sz.value == 4 * 64 * 16 * 32 * 130

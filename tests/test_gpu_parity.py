@@ -105,6 +105,47 @@ def test_rope_segmented_and_absolute_positions():
     parity(G.rope(xr, 4, positions=pos), want, "RoPE absolute positions")
 
 
+def test_rope_table_values():
+    cs = G.rope_table(4096, 64)
+    # position 1, pair 0: theta = 1 (the known answer of the reference's RoPE tests)
+    assert np.allclose(cs[1, 0], [math.cos(1), math.sin(1)], atol=1e-6)
+    assert np.array_equal(cs[0], np.tile([1.0, 0.0], (32, 1)).astype(np.float32))
+    # every entry against float64 cos/sin of the float32 angle pos / powf(base, 2p/d)
+    denom = np.array([np.float32(10000.0) ** (np.float32(2 * p) / np.float32(64)) for p in range(32)],
+                     np.float32)
+    theta = (np.arange(4096, dtype=np.float32)[:, None] / denom[None, :]).astype(np.float64)
+    assert np.abs(cs[..., 0] - np.cos(theta)).max() < 2e-6
+    assert np.abs(cs[..., 1] - np.sin(theta)).max() < 2e-6
+
+
+@pytest.mark.parametrize("rows,ind,out,hd,seg,off", [
+    (1024, 512, 512, 64, 0, 0),    # 256x128 tiles
+    (300, 1024, 1024, 64, 0, 0),   # 128x128 tiles, ragged rows
+    (150, 64, 64, 16, 50, 0),      # segmented positions (row % 50)
+    (40, 96, 192, 32, 0, 17),      # position offset
+    (33, 130, 36, 12, 0, 0),       # generic kernel (K not a multiple of 4)
+])
+def test_project_qkv_rope(rows, ind, out, hd, seg, off):
+    x = synth.normal(rows + ind, (rows, ind))
+    w = [synth.xavier_uniform(i + out, out, ind) for i in range(3)]
+    b = [synth.normal(19 + i, (out,)) * np.float32(0.1) for i in range(3)]
+    args = (w[0], b[0], w[1], b[1], w[2], b[2])
+    q, k, v = G.project_qkv_rope(x, *args, head_dim=hd, pos_offset=off, seg_len=seg)
+    wq, wk, wv = O.project_qkv(x, *args, mt=True)
+    heads = out // hd
+
+    def rotated(t):
+        if seg:
+            return np.concatenate([O.rope(t[i:i + seg], heads) for i in range(0, rows, seg)])
+        if off:
+            return O.rope(np.vstack([np.zeros((off, out), np.float32), t]), heads)[off:]
+        return O.rope(t, heads)
+
+    parity(q, rotated(wq), f"QKV+RoPE {rows}x{ind}->{out} Q")
+    parity(k, rotated(wk), f"QKV+RoPE {rows}x{ind}->{out} K")
+    parity(v, wv, f"QKV+RoPE {rows}x{ind}->{out} V")
+
+
 # ------------------------------------------------------------------- SDPA
 def test_sdpa_reference_cases(ops_golden):
     g = ops_golden
