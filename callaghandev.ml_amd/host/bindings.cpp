@@ -84,6 +84,14 @@ py::array_t<float> to_numpy(Matrix &&m) {
                             owner);
 }
 
+py::array_t<float> to_numpy(const Matrix &m) { return to_numpy(Matrix(m)); }
+
+py::array_t<float> vec_to_numpy(const std::vector<float> &v) {
+  py::array_t<float> a((py::ssize_t)v.size());
+  if (!v.empty()) std::memcpy(a.mutable_data(), v.data(), v.size() * sizeof(float));
+  return a;
+}
+
 Matrix from_numpy(const py::object &o) {
   MatArg a = mat(o);
   if (a.view.null()) throw ArgumentNullException("matrix");
@@ -163,6 +171,7 @@ PYBIND11_MODULE(_cdml_host, m) {
   py::register_exception<ArgumentNullException>(m, "ArgumentNullException", arg_exc.ptr());
   py::register_exception<ArgumentOutOfRangeException>(m, "ArgumentOutOfRangeException", arg_exc.ptr());
   py::register_exception<InvalidOperationException>(m, "InvalidOperationException", PyExc_RuntimeError);
+  py::register_exception<FileNotFoundException>(m, "FileNotFoundException", PyExc_FileNotFoundError);
 
   py::class_<HipAccelerationManager>(m, "HipAccelerationManager")
       .def(py::init<int>(), py::arg("device") = 0)
@@ -284,11 +293,69 @@ PYBIND11_MODULE(_cdml_host, m) {
       .def_readwrite("InputFeatureDim", &TransformerConfig::InputFeatureDim)
       .def_readwrite("OutputDim", &TransformerConfig::OutputDim)
       .def_readwrite("FFNActivationType", &TransformerConfig::FFNActivationType)
+      .def_readwrite("DataType", &TransformerConfig::DataType)
+      .def_readwrite("AccelerationType", &TransformerConfig::AccelerationType)
+      .def_readwrite("AccelerationDeviceId", &TransformerConfig::AccelerationDeviceId)
+      .def_readwrite("L2RegulationLamda", &TransformerConfig::L2RegulationLamda)
+      .def_readwrite("GradientClippingThreshold", &TransformerConfig::GradientClippingThreshold)
+      .def_readwrite("CostFunction", &TransformerConfig::CostFunction)
+      .def_readwrite("ActivationDistribution", &TransformerConfig::ActivationDistribution)
       .def("Validate", &TransformerConfig::Validate);
 
   py::class_<LanguageModel>(m, "LanguageModel")
       .def(py::init<const TransformerConfig &, HipAccelerationManager *>(), py::keep_alive<1, 3>())
       .def("load_weights", &load_weights)
+      .def("Save", &LanguageModel::Save, py::arg("directory"))
+      .def_static("Load", &LanguageModel::Load, py::arg("directory"), py::arg("accel"), py::keep_alive<0, 2>())
+      .def_property_readonly("config", &LanguageModel::config)
+      .def("weights",
+           [](const LanguageModel &lm) {
+             // the cdml.synth.lm_weights layout (arrays copied out)
+             py::dict w;
+             const TransformerConfig &c = lm.config();
+             if (c.UsesDiscreteTokens) {
+               w["token_embedding"] = to_numpy(lm.TokenEmbedding);
+             } else {
+               w["input_proj"] = to_numpy(lm.InputProjection);
+               w["input_bias"] = vec_to_numpy(lm.InputProjectionBias);
+             }
+             w["out_proj"] = to_numpy(lm.OutputProjection);
+             w["out_bias"] = vec_to_numpy(lm.OutputBias);
+             py::list layers;
+             for (const TransformerBlock &b : lm.Blocks) {
+               py::dict L;
+               L["wq"] = to_numpy(b.Attention.WQ);
+               L["wk"] = to_numpy(b.Attention.WK);
+               L["wv"] = to_numpy(b.Attention.WV);
+               L["wo"] = to_numpy(b.Attention.WO);
+               L["bq"] = vec_to_numpy(b.Attention.BiasQ);
+               L["bk"] = vec_to_numpy(b.Attention.BiasK);
+               L["bv"] = vec_to_numpy(b.Attention.BiasV);
+               L["bo"] = vec_to_numpy(b.Attention.BiasO);
+               L["ln1_g"] = vec_to_numpy(b.LN1Gamma);
+               L["ln1_b"] = vec_to_numpy(b.LN1Beta);
+               L["ln2_g"] = vec_to_numpy(b.LN2Gamma);
+               L["ln2_b"] = vec_to_numpy(b.LN2Beta);
+               py::list fw, fb, fa;
+               for (size_t i = 0; i < b.FeedForward.weights.size(); ++i) {
+                 fw.append(to_numpy(b.FeedForward.weights[i]));
+                 fb.append(vec_to_numpy(b.FeedForward.biases[i]));
+                 fa.append(b.FeedForward.activations[i]);
+               }
+               if (b.FeedForward.weights.size() == 2) {
+                 L["ffn_w1"] = fw[0];
+                 L["ffn_b1"] = fb[0];
+                 L["ffn_w2"] = fw[1];
+                 L["ffn_b2"] = fb[1];
+               }
+               L["ffn_weights"] = fw;
+               L["ffn_biases"] = fb;
+               L["ffn_activations"] = fa;
+               layers.append(L);
+             }
+             w["layers"] = layers;
+             return w;
+           })
       .def("Forward", [](LanguageModel &lm, py::object ids) { return to_numpy(lm.Forward(ids_from(ids))); })
       .def("ForwardContinuous",
            [](LanguageModel &lm, py::object x) {

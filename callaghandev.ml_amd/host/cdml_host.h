@@ -55,6 +55,9 @@ struct ArgumentOutOfRangeException : ArgumentException {
 struct InvalidOperationException : std::logic_error {
   explicit InvalidOperationException(const std::string &msg) : std::logic_error(msg) {}
 };
+struct FileNotFoundException : std::runtime_error {  // System.IO.FileNotFoundException
+  explicit FileNotFoundException(const std::string &msg) : std::runtime_error(msg) {}
+};
 
 // ---- host arrays (row-major, the float[,] layout) ------------------------
 struct Matrix {
@@ -226,6 +229,18 @@ struct TransformerConfig {
   int InputFeatureDim = 1;
   int OutputDim = 1;
   int FFNActivationType = Relu;
+  // Carried through config.json (LanguageModel.cs:710-728) and the FFN files;
+  // no effect on the forward pass.  DataType is TransformerDataType
+  // (Text 0, TimeSeriesRegression 1, TimeSeriesClassification 2,
+  // SymbolicSequence 3; discrete tokens for 0 and 3).  AccelerationType 4 is
+  // the HIP manager appended to the reference's enum.
+  int DataType = 0;
+  int AccelerationType = 4;
+  int AccelerationDeviceId = 0;
+  float L2RegulationLamda = 0.01f;
+  float GradientClippingThreshold = 1.0f;
+  int CostFunction = 0;
+  int ActivationDistribution = 0;
   int EffectiveOutputDim() const { return UsesDiscreteTokens ? VocabSize : OutputDim; }
   void Validate() const;  // TransformerConfig.cs:62-102
 };
@@ -272,6 +287,10 @@ class LanguageModel {
                             float temperature = 1.0f, bool greedy = true, uint64_t seed = 0);
   std::vector<float> PredictNext(MatView inputSequence);
   const TransformerConfig &config() const { return cfg_; }
+  // LanguageModel.Save / Load (LanguageModel.cs:706-839): config.json,
+  // weights.bin and ffn/ffn_layer_<i>.json in the reference's formats.
+  void Save(const std::string &directory) const;
+  static LanguageModel Load(const std::string &directory, HipAccelerationManager *accel);
 
   Matrix TokenEmbedding, InputProjection, OutputProjection;
   std::vector<float> InputProjectionBias, OutputBias;

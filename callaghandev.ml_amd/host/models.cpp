@@ -4,6 +4,7 @@
 // same weights.
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 
 #include "cdml_host.h"
@@ -28,28 +29,58 @@ uint64_t splitmix64(uint64_t &s) {
 }  // namespace
 
 // ---- TransformerConfig.Validate: TransformerConfig.cs:62-102 ---------------
+// TransformerConfig.Validate (TransformerConfig.cs:61-101) in the reference's
+// order: the module base (SharedConfigs.cs:150-157), the sizes, then
+// DataConfig / RuntimeConfig / RegularizationConfig (DataConfig.cs:30-40,
+// SharedConfigs.cs:239-254,266-270), then the attention rules.  Positive-size
+// and enum checks throw ArgumentException, as ConfigBase.RequirePositive does
+// (ConfigBase.cs:16-54).
 void TransformerConfig::Validate() const {
   auto positive = [](int v, const char *n) {
-    if (v <= 0) throw ArgumentOutOfRangeException(n, std::string(n) + " must be positive.");
+    if (v <= 0) throw ArgumentException(std::string(n) + " must be positive, got " + std::to_string(v) + ".");
+  };
+  auto fmt = [](float v) {
+    char b[32];
+    std::snprintf(b, sizeof b, "%g", (double)v);
+    return std::string(b);
   };
   positive(EmbeddingDim, "EmbeddingDim");
+  positive(NumHeads, "NumHeads");
   positive(NumLayers, "NumLayers");
   positive(FeedForwardDim, "FeedForwardDim");
-  positive(VocabSize, "VocabSize");
-  positive(MaxSequenceLength, "MaxSequenceLength");
-  positive(InputFeatureDim, "InputFeatureDim");
-  positive(OutputDim, "OutputDim");
-  if (NumHeads <= 0) throw ArgumentOutOfRangeException("NumHeads", "NumHeads must be positive.");
   if (EmbeddingDim % NumHeads != 0)
     throw ArgumentException("EmbeddingDim (" + std::to_string(EmbeddingDim) +
                                 ") must be divisible by NumHeads (" + std::to_string(NumHeads) + ").",
                             "EmbeddingDim");
-  if ((EmbeddingDim / NumHeads) & 1)
-    throw ArgumentException("RoPE requires an even per-head dimension.", "EmbeddingDim");
-  if (UsesDiscreteTokens && VocabSize < 2)
-    throw ArgumentException("Discrete token models require VocabSize >= 2.", "VocabSize");
+  positive(VocabSize, "VocabSize");
+  positive(MaxSequenceLength, "MaxSequenceLength");
+  positive(InputFeatureDim, "InputFeatureDim");
+  positive(OutputDim, "OutputDim");
+  if (DataType < 0 || DataType > 3) throw ArgumentException("Invalid DataType: " + std::to_string(DataType) + ".");
+  if (CostFunction < 0 || CostFunction > 5)
+    throw ArgumentException("Invalid CostFunction: " + std::to_string(CostFunction) + ".");
+  if (ActivationDistribution < 0 || ActivationDistribution > 1)
+    throw ArgumentException("Invalid ActivationDistribution: " + std::to_string(ActivationDistribution) + ".");
   if (FFNActivationType < None || FFNActivationType > Swish)
-    throw ArgumentOutOfRangeException("FFNActivationType");
+    throw ArgumentException("Invalid FFNActivationType value: " + std::to_string(FFNActivationType) + ".");
+  if (AccelerationType < 0 || AccelerationType > 4)
+    throw ArgumentException("Invalid AccelerationType value: " + std::to_string(AccelerationType) + ".");
+  if (AccelerationDeviceId < 0)
+    throw ArgumentException("AccelerationDeviceId must be non-negative, got " +
+                            std::to_string(AccelerationDeviceId) + ".");
+  if (!(L2RegulationLamda >= 0.f))
+    throw ArgumentException("L2RegulationLamda must be non-negative, got " + fmt(L2RegulationLamda) + ".");
+  if (!(GradientClippingThreshold > 0.f))
+    throw ArgumentException("GradientClippingThreshold must be positive, got " + fmt(GradientClippingThreshold) + ".");
+  if ((EmbeddingDim / NumHeads) & 1)
+    throw ArgumentException("RoPE requires an even per-head dimension. EmbeddingDim / NumHeads = " +
+                                std::to_string(EmbeddingDim / NumHeads) + ".",
+                            "EmbeddingDim");
+  if (UsesDiscreteTokens) {
+    if (VocabSize < 2) throw ArgumentException("Discrete token models require VocabSize >= 2.", "VocabSize");
+  } else if (DataType == 2 && OutputDim < 2) {
+    throw ArgumentException("TimeSeriesClassification requires OutputDim >= 2 classes.", "OutputDim");
+  }
 }
 
 // ---- MultiHeadAttention: MultiHeadAttention.cs:23-159 ------------------------

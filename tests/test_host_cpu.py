@@ -102,8 +102,22 @@ def test_config_and_model_rules():
         host.config({"vocab": 12, "dim": 8, "heads": 3, "layers": 1, "ff": 16, "max_seq": 8})
     with pytest.raises(H.ArgumentException, match="even per-head"):
         host.config({"vocab": 12, "dim": 6, "heads": 2, "layers": 1, "ff": 16, "max_seq": 8})
-    with pytest.raises(H.ArgumentOutOfRangeException):
+    # ConfigBase.RequirePositive throws ArgumentException itself (ConfigBase.cs:16-22)
+    with pytest.raises(H.ArgumentException, match="NumLayers must be positive, got 0") as e:
         host.config({"vocab": 12, "dim": 8, "heads": 2, "layers": 0, "ff": 16, "max_seq": 8})
+    assert type(e.value) is H.ArgumentException
+    base = {"vocab": 12, "dim": 8, "heads": 2, "layers": 1, "ff": 16, "max_seq": 8}
+    for field, value, text in [("DataType", 4, "Invalid DataType: 4"),
+                               ("CostFunction", 6, "Invalid CostFunction: 6"),
+                               ("ActivationDistribution", 2, "Invalid ActivationDistribution: 2"),
+                               ("AccelerationType", 5, "Invalid AccelerationType value: 5"),
+                               ("AccelerationDeviceId", -1, "AccelerationDeviceId must be non-negative"),
+                               ("L2RegulationLamda", -0.5, "L2RegulationLamda must be non-negative"),
+                               ("GradientClippingThreshold", 0.0, "GradientClippingThreshold must be positive")]:
+        with pytest.raises(H.ArgumentException, match=text):
+            host.config(base, **{field: value})
+    with pytest.raises(H.ArgumentException, match="TimeSeriesClassification requires OutputDim >= 2"):
+        host.config(dict(base, discrete=False), DataType=2)
     cfg = {"vocab": 12, "dim": 8, "heads": 2, "layers": 1, "ff": 16, "max_seq": 8}
     lm, _ = host.language_model(cfg, synth.lm_weights(cfg, 1))
     with pytest.raises(H.ArgumentOutOfRangeException):

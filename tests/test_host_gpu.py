@@ -166,6 +166,30 @@ def test_device_language_model(H, mgr, name):
     assert np.array_equal(out[0], g["greedy"]), f"{name}: device greedy tokens differ"
 
 
+def test_checkpoint_load_then_forward(H, mgr, tmp_path):
+    """LanguageModel.Load of the golden checkpoint directory (written by
+    tests/golden/make_checkpoint_fixture.py in the reference's format), then
+    Forward against the oracle on the stored arrays; Save -> Load keeps Forward
+    within the reference's own 1e-5 (MultiTypeTransformerTests.cs:858-874), here
+    exactly, and the device engine built from the loaded model agrees."""
+    import os
+    gold = os.path.join(os.path.dirname(__file__), "golden")
+    e = np.load(os.path.join(gold, "checkpoint_tiny_expected.npz"))
+    cfg = {"vocab": 5, "dim": 4, "heads": 2, "layers": 2, "ff": 6, "max_seq": 8, "activation": 3}
+    w = {"token_embedding": e["token_embedding"], "out_proj": e["out_proj"], "out_bias": e["out_bias"],
+         "layers": [{k[3:]: e[k] for k in e.files if k.startswith(f"l{i}_")} for i in range(2)]}
+    lm = H.LanguageModel.Load(os.path.join(gold, "checkpoint_tiny"), mgr)
+    ids = np.array([1, 4, 0, 3, 2, 2, 1], np.int32)
+    got = lm.Forward(ids)
+    parity(got, O.LanguageModel(cfg, w).forward(ids), "loaded checkpoint Forward vs oracle")
+    lm.Save(str(tmp_path))
+    again = H.LanguageModel.Load(str(tmp_path), mgr).Forward(ids)
+    assert np.array_equal(got, again), "Save -> Load changed Forward"
+    dev = H.DeviceLanguageModel(lm, 2)
+    parity(dev.Forward(np.stack([ids, ids[::-1].copy()])),
+           np.vstack([got, lm.Forward(ids[::-1].copy())]), "device engine from the loaded model")
+
+
 def test_device_language_model_c1_batch():
     """Config 1: batch 4 of 64 uniform token ids, full forward, then greedy
     generation of 20 tokens from 32-token prompts, per sequence against the
