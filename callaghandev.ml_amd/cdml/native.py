@@ -64,6 +64,8 @@ SIGNATURES = {
     "cdml_project_qkv": [_vp] * 10 + [_i, _i, _i, _vp],
     "cdml_linear": [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
     "cdml_rope": [_vp, _i, _i, _i, _i, _i, _f, _i, _i, _i, _vp, _vp],
+    "cdml_linear_backward": [_vp, _i, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _vp],
+    "cdml_backprop_qkv": [_vp] * 14 + [_i, _i, _i, _vp],
     "cdml_rope_table": [_vp, _i, _i, _f, _vp],
     "cdml_project_qkv_rope": [_vp] * 10 + [_i, _i, _i, _i, _vp, _i, _i, _i, _vp],
     "cdml_sdpa_fwd": [_vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, _vp],

@@ -1,16 +1,23 @@
-// fp32 MFMA GEMM for the projections of the attention path:
-//   C[m, n] = act(sum_k A[m, k] * W[n, k] + bias[n])
-// A is the activation [M, K] (row stride lda), W the weight [N, K] ([out, in],
-// the reference's layout), C the output [M, N] (row stride ldc).  Up to three
-// problems that share A (the fused Q/K/V projection) run in one launch.
+// fp32 MFMA GEMM for the projections of the attention path and their
+// gradients:
+//   C[m, n] = act(sum_k opA[m, k] * opB[k, n] + bias[n])  (+ C[m, n] when beta)
+// opA is A [M, K] (row stride lda) or, transposed, A stored [K, M]; opB is the
+// weight W [N, K] ([out, in], the reference's layout: y = x W^T) or, for
+// gradients, B stored [K, N].  Up to three problems with the same shape run in
+// one launch (the fused Q/K/V projection and its weight gradients).
 //
-// Tiling for gfx950: a 256-thread workgroup computes a 128x128 tile of C; each
-// of its four waves owns a 64x64 quadrant as 2x2 blocks of
-// v_mfma_f32_32x32x2_f32.  K advances in steps of 32 through double-buffered
-// LDS tiles (row stride 36 floats); every lane fetches its A and B operands as
-// 16-byte LDS reads that feed four MFMAs each.  The reduction index k is
-// visited in the permuted order kappa(s, h) = 8*(s/4) + 4*h + s%4 on both
-// operands, which leaves the sum unchanged.
+// Forward (A [M, K], W [N, K]):                  y = x W^T    ProjectQKV, linear
+// Input gradient (A = dY [M, K], B = W [K, N]):  dX = dY W    BackpropQKV, ...
+// Weight gradient (A = dY stored [K, M], B = X [K, N]): dW += dY^T X, with the
+//   bias gradient (row sums of opA = column sums of dY) folded into the
+//   staging of opA.
+//
+// The MFMA inner loop is the same for every layout: both operand tiles sit in
+// LDS as [rows][k] with row pitch BK + 4 floats, and every lane reads its A
+// and B operands as 16-byte LDS reads that feed four v_mfma_f32_32x32x2_f32
+// each.  The reduction index k is visited in the permuted order
+// kappa(s, h) = 8*(s/4) + 4*h + s%4 on both operands, which leaves the sum
+// unchanged.  A transposed operand is transposed on its way into LDS.
 #include <algorithm>
 
 #include "common.h"
@@ -26,20 +33,22 @@ constexpr int GROUP_M = 8;
 constexpr int kActRope = 100;
 
 struct GemmProblem {
-  const float *w;
-  const float *bias;
+  const float *a;     // opA source
+  const float *w;     // opB source
+  const float *bias;  // [N] or NULL
   float *c;
+  float *bgrad;       // [M] += row sums of opA (transposed-A launches only), or NULL
 };
 
 struct GemmArgs {
-  const float *a;
   GemmProblem p[3];
-  int lda, ldc;
+  int lda, ldb, ldc;
   int M, N, K;
   int nprob;
   int tiles_m, tiles_n;  // tiles_n counts the tiles of one problem
   int total, padded;
   int act;
+  int beta;  // 1: add the result to C
   // Rotary position embedding applied to problems 0 and 1 (Q and K) in the
   // epilogue when rope_cs is set: rope_cs[pos * rope_hd / 2 + p] holds
   // (cos, sin) of position pos for pair p; row m has position
@@ -48,7 +57,7 @@ struct GemmArgs {
   int rope_hd, rope_npos, rope_pos0, rope_seg;
 };
 
-// Epilogue of both GEMM kernels with the rotary embedding of
+// Epilogue of both forward GEMM kernels with the rotary embedding of
 // AccelerationCPU.cs:4947-4975 folded in.  A lane holds column n of rows
 // mrow0 + 32 i + 8 (r / 4) + 4 hf + r % 4, so the pair partner of column n
 // (n ^ 1; head dims are even) sits in lane li ^ 1 of the same register: one
@@ -154,6 +163,7 @@ struct TileStage {
   }
 };
 
+// Guarded fallback of the forward layout (any K, any alignment).
 template <bool VEC>
 __global__ void __launch_bounds__(NTHREADS) gemm_nt_kernel(const GemmArgs args) {
   __shared__ __attribute__((aligned(16))) float As[2][BM][LDSK];
@@ -193,8 +203,8 @@ __global__ void __launch_bounds__(NTHREADS) gemm_nt_kernel(const GemmArgs args) 
 
   TileStage<VEC> sa, sb;
   const int nk = (K + BK - 1) / BK;
-  sa.load(args.a, args.lda, m0, M, 0, K);
-  sb.load(P.w, K, n0, N, 0, K);
+  sa.load(P.a, args.lda, m0, M, 0, K);
+  sb.load(P.w, args.ldb, n0, N, 0, K);
   sa.store(As[0]);
   sb.store(Bs[0]);
   __syncthreads();
@@ -203,8 +213,8 @@ __global__ void __launch_bounds__(NTHREADS) gemm_nt_kernel(const GemmArgs args) 
     const int cur = kt & 1;
     const bool more = kt + 1 < nk;
     if (more) {
-      sa.load(args.a, args.lda, m0, M, (kt + 1) * BK, K);
-      sb.load(P.w, K, n0, N, (kt + 1) * BK, K);
+      sa.load(P.a, args.lda, m0, M, (kt + 1) * BK, K);
+      sb.load(P.w, args.ldb, n0, N, (kt + 1) * BK, K);
     }
 #pragma unroll
     for (int u = 0; u < BK / 8; ++u) {
@@ -249,33 +259,99 @@ __global__ void __launch_bounds__(NTHREADS) gemm_nt_kernel(const GemmArgs args) 
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
-        if (m < M) P.c[(size_t)m * args.ldc + n] = activate(acc[i][j][r] + bias, args.act);
+        if (m < M) {
+          float *pc = P.c + (size_t)m * args.ldc + n;
+          const float v = activate(acc[i][j][r] + bias, args.act);
+          *pc = args.beta ? *pc + v : v;
+        }
       }
     }
   }
 }
 
+// Global -> LDS staging of one ROWS x BKK operand tile of the tiled kernel;
+// the tile lands in LDS as [rows][k] (pitch BKK + 4) for either source layout.
+//   T = false: the source is [rows][K] (k contiguous, row stride ld): each
+//     thread moves 16-byte row pieces straight into LDS.
+//   T = true:  the source is [K][rows] (rows contiguous, k-row stride ld):
+//     each thread loads four consecutive rows of one k and stores them as four
+//     LDS words.  Consecutive lanes take consecutive k, so the four stores of
+//     a wave fall in distinct banks.
+// Each thread's offsets are fixed for the whole K loop; rows past the end are
+// clamped to the last row (T: the last four rows; rows % 4 == 0), so loads
+// need no predication and clamped rows only feed results that are never
+// stored.
+template <int ROWS, int BKK, int NT, bool T>
+struct OpStage {
+  static constexpr int LD = BKK + 4;
+  static constexpr int F4R = BKK / 4;   // T = false: vectors per row
+  static constexpr int RPP = NT / F4R;  // T = false: rows per pass
+  static constexpr int G = NT / BKK;    // T = true: four-row groups per pass
+  static constexpr int NP = T ? ROWS / (4 * G) : ROWS / RPP;
+  static_assert(NP >= 1 && (T ? ROWS % (4 * G) == 0 : ROWS % RPP == 0), "staging shape");
+  uint32_t off[NP];
+  vf4 v[NP];
+  int sa, sb;  // T = false: (row, column); T = true: (k, row group)
+
+  __device__ __forceinline__ void init(int row0, int rows, int ld) {
+    const int t = threadIdx.x;
+    if constexpr (T) {
+      sa = t % BKK;
+      sb = t / BKK;
+#pragma unroll
+      for (int i = 0; i < NP; ++i)
+        off[i] = (uint32_t)sa * (uint32_t)ld + (uint32_t)min(row0 + 4 * (sb + G * i), rows - 4);
+    } else {
+      sa = t / F4R;
+      sb = (t % F4R) * 4;
+#pragma unroll
+      for (int i = 0; i < NP; ++i) off[i] = (uint32_t)min(row0 + sa + RPP * i, rows - 1) * (uint32_t)ld + sb;
+    }
+  }
+  // First element of k-tile kt.
+  static __device__ __forceinline__ const float *tile(const float *x, int kt, int ld) {
+    return T ? x + (size_t)kt * BKK * ld : x + (size_t)kt * BKK;
+  }
+  __device__ __forceinline__ void load(const float *__restrict__ base) {
+#pragma unroll
+    for (int i = 0; i < NP; ++i) v[i] = *reinterpret_cast<const vf4 *>(base + off[i]);
+  }
+  __device__ __forceinline__ void store(float (*lds)[LD]) const {
+    if constexpr (T) {
+#pragma unroll
+      for (int i = 0; i < NP; ++i)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) lds[4 * (sb + G * i) + c][sa] = v[i][c];
+    } else {
+#pragma unroll
+      for (int i = 0; i < NP; ++i) *reinterpret_cast<vf4 *>(&lds[sa + RPP * i][sb]) = v[i];
+    }
+  }
+};
+
 // Tiled fast path (K % BKK == 0, 16-byte aligned rows, element offsets
-// below 2^32).  A workgroup of WM x WN waves computes a TM x TN tile of C,
-// each wave a (TM/WM) x (TN/WN) block of 32x32 MFMA tiles.  K advances by BKK
-// through double-buffered LDS (row pitch BKK + 4 floats).  Every thread's
-// staging rows are fixed for the whole K loop (rows past M or N are clamped
-// to the last row: they feed only accumulators that are never stored), so a
-// k-tile load is the wave-uniform base plus precomputed 32-bit offsets, with
-// no predication.  The LDS operands of group u + 1 are read while the MFMAs of
-// group u run, and the k-tile after next is fetched while the current one is
-// consumed.  Measured on MI355X, high occupancy (four waves per SIMD with two
-// 512-thread workgroups per CU) hides latency better than deeper register
-// blocking.
-template <int TM, int TN, int BKK, int WM, int WN, int MINB, int ACT>
+// below 2^32; a transposed operand also needs rows % 4 == 0).  A workgroup of
+// WM x WN waves computes a TM x TN tile of C, each wave a (TM/WM) x (TN/WN)
+// block of 32x32 MFMA tiles.  K advances by BKK through double-buffered LDS.
+// The LDS operands of group u + 1 are read while the MFMAs of group u run, and
+// the k-tile after next is fetched while the current one is consumed.
+// Measured on MI355X, high occupancy (four waves per SIMD with two 512-thread
+// workgroups per CU) hides latency better than deeper register blocking.
+//
+// With TA and a bias-gradient pointer, the workgroups of the first column
+// tile also sum each opA tile in LDS while it is current (every valid k-tile
+// exactly once) and add the row sums to bgrad: the bias gradient of a
+// weight-gradient GEMM costs no extra pass over dY.  Each thread keeps one
+// partial sum (row t % TM, a 1/(NT/TM) slice of the k-tile); the slices meet
+// in LDS at the end.
+template <int TM, int TN, int BKK, int WM, int WN, int MINB, int ACT, bool TA, bool TB>
 __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const GemmArgs args) {
   constexpr int NT = 64 * WM * WN;
   constexpr int LD = BKK + 4;
-  constexpr int F4R = BKK / 4;   // float4 per row of a k-tile
-  constexpr int RPP = NT / F4R;  // rows per staging pass
-  constexpr int NA = TM / RPP, NB = TN / RPP;
   constexpr int BI = TM / WM / 32, BJ = TN / WN / 32;
-  static_assert(NA >= 1 && NB >= 1 && BI >= 1 && BJ >= 1, "tile shape");
+  static_assert(BI >= 1 && BJ >= 1, "tile shape");
+  typedef OpStage<TM, BKK, NT, TA> StageA;
+  typedef OpStage<TN, BKK, NT, TB> StageB;
   __shared__ __attribute__((aligned(16))) float As[2][TM][LD];
   __shared__ __attribute__((aligned(16))) float Bs[2][TN][LD];
 
@@ -303,13 +379,10 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const Gem
   const int wm = wave / WN, wn = wave % WN;
   const int li = lane & 31, hf = lane >> 5;
 
-  const int srow = t / F4R, scol = (t % F4R) * 4;
-  uint32_t aoff[NA], boff[NB];
-#pragma unroll
-  for (int i = 0; i < NA; ++i) aoff[i] = (uint32_t)min(m0 + srow + RPP * i, M - 1) * (uint32_t)args.lda + scol;
-#pragma unroll
-  for (int i = 0; i < NB; ++i) boff[i] = (uint32_t)min(n0 + srow + RPP * i, N - 1) * (uint32_t)K + scol;
-  vf4 ra[NA], rb[NB];
+  StageA sa;
+  StageB sb;
+  sa.init(m0, M, args.lda);
+  sb.init(n0, N, args.ldb);
   floatx16 acc[BI][BJ];
 #pragma unroll
   for (int i = 0; i < BI; ++i)
@@ -318,36 +391,34 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const Gem
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
   const int nk = K / BKK;
-  const float *__restrict__ A = args.a;
+  const float *__restrict__ A = P.a;
   const float *__restrict__ W = P.w;
+  const bool bsum = TA && P.bgrad && tn == 0;
+  constexpr int KCH = NT / TM;  // k slices per row for the bias-gradient sums
+  static_assert(NT % TM == 0 && BKK % (4 * KCH) == 0, "bias-gradient slices");
+  float bpart = 0.f;
 
   // k-tile 0 -> LDS, k-tile 1 -> registers
-#pragma unroll
-  for (int i = 0; i < NA; ++i) ra[i] = *reinterpret_cast<const vf4 *>(A + aoff[i]);
-#pragma unroll
-  for (int i = 0; i < NB; ++i) rb[i] = *reinterpret_cast<const vf4 *>(W + boff[i]);
-#pragma unroll
-  for (int i = 0; i < NA; ++i) *reinterpret_cast<vf4 *>(&As[0][srow + RPP * i][scol]) = ra[i];
-#pragma unroll
-  for (int i = 0; i < NB; ++i) *reinterpret_cast<vf4 *>(&Bs[0][srow + RPP * i][scol]) = rb[i];
+  sa.load(StageA::tile(A, 0, args.lda));
+  sb.load(StageB::tile(W, 0, args.ldb));
+  sa.store(As[0]);
+  sb.store(Bs[0]);
   {
-    const int k1 = min(BKK, (nk - 1) * BKK);
-#pragma unroll
-    for (int i = 0; i < NA; ++i) ra[i] = *reinterpret_cast<const vf4 *>(A + k1 + aoff[i]);
-#pragma unroll
-    for (int i = 0; i < NB; ++i) rb[i] = *reinterpret_cast<const vf4 *>(W + k1 + boff[i]);
+    const int k1 = min(1, nk - 1);
+    sa.load(StageA::tile(A, k1, args.lda));
+    sb.load(StageB::tile(W, k1, args.ldb));
   }
   __syncthreads();
 
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
     const float(*as)[LD] = &As[cur][wm * (TM / WM) + li];
-    const float(*bs)[LD] = &Bs[cur][wn * (TN / WN) + li];
+    const float(*bsh)[LD] = &Bs[cur][wn * (TN / WN) + li];
     vf4 a4[BI], b4[BJ];
 #pragma unroll
     for (int i = 0; i < BI; ++i) a4[i] = *reinterpret_cast<const vf4 *>(&as[i * 32][hf * 4]);
 #pragma unroll
-    for (int j = 0; j < BJ; ++j) b4[j] = *reinterpret_cast<const vf4 *>(&bs[j * 32][hf * 4]);
+    for (int j = 0; j < BJ; ++j) b4[j] = *reinterpret_cast<const vf4 *>(&bsh[j * 32][hf * 4]);
 #pragma unroll
     for (int u = 0; u < BKK / 8; ++u) {
       vf4 an[BI], bn[BJ];
@@ -355,7 +426,7 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const Gem
 #pragma unroll
         for (int i = 0; i < BI; ++i) an[i] = *reinterpret_cast<const vf4 *>(&as[i * 32][(u + 1) * 8 + hf * 4]);
 #pragma unroll
-        for (int j = 0; j < BJ; ++j) bn[j] = *reinterpret_cast<const vf4 *>(&bs[j * 32][(u + 1) * 8 + hf * 4]);
+        for (int j = 0; j < BJ; ++j) bn[j] = *reinterpret_cast<const vf4 *>(&bsh[j * 32][(u + 1) * 8 + hf * 4]);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r)
@@ -374,16 +445,36 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const Gem
     // Past the end both are unconditional re-stages of the last tile into
     // the idle buffer, which nothing reads again: keeping them unconditional
     // keeps the staging registers out of scratch memory.
+    sa.store(As[cur ^ 1]);
+    sb.store(Bs[cur ^ 1]);
+    if constexpr (TA) {
+      if (bsum) {  // k-tile kt, stable in As[cur] until the barrier below
+        const float *row = &As[cur][t % TM][(t / TM) * (BKK / KCH)];
 #pragma unroll
-    for (int i = 0; i < NA; ++i) *reinterpret_cast<vf4 *>(&As[cur ^ 1][srow + RPP * i][scol]) = ra[i];
-#pragma unroll
-    for (int i = 0; i < NB; ++i) *reinterpret_cast<vf4 *>(&Bs[cur ^ 1][srow + RPP * i][scol]) = rb[i];
-    const int k2 = min((kt + 2) * BKK, (nk - 1) * BKK);
-#pragma unroll
-    for (int i = 0; i < NA; ++i) ra[i] = *reinterpret_cast<const vf4 *>(A + k2 + aoff[i]);
-#pragma unroll
-    for (int i = 0; i < NB; ++i) rb[i] = *reinterpret_cast<const vf4 *>(W + k2 + boff[i]);
+        for (int e = 0; e < BKK / KCH; e += 4) {
+          const vf4 x = *reinterpret_cast<const vf4 *>(row + e);
+          bpart += (x[0] + x[1]) + (x[2] + x[3]);
+        }
+      }
+    }
+    const int k2 = min(kt + 2, nk - 1);
+    sa.load(StageA::tile(A, k2, args.lda));
+    sb.load(StageB::tile(W, k2, args.ldb));
     __syncthreads();
+  }
+
+  if constexpr (TA) {
+    if (bsum) {  // uniform over the workgroup; the loop ended on a barrier
+      float *red = &As[0][0][0];
+      red[t] = bpart;
+      __syncthreads();
+      if (t < TM && m0 + t < M) {
+        float s = 0.f;
+#pragma unroll
+        for (int c = 0; c < KCH; ++c) s += red[t + c * TM];
+        P.bgrad[m0 + t] += s;
+      }
+    }
   }
 
   if constexpr (ACT == kActRope) {
@@ -404,52 +495,153 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const Gem
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + wm * (TM / WM) + i * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
-        if (m < M) P.c[(size_t)m * args.ldc + n] = activate(acc[i][j][r] + bias, ACT);
+        if (m < M) {
+          float *pc = P.c + (size_t)m * args.ldc + n;
+          const float v = activate(acc[i][j][r] + bias, ACT == kActRope ? CDML_ACT_NONE : ACT);
+          *pc = args.beta ? *pc + v : v;
+        }
       }
     }
   }
 }
 
+// Any layout, any shape (the gradient GEMMs whose sizes miss the tiled
+// kernel's conditions): a 64 x 64 tile of C per 256-thread workgroup, 4 x 4
+// outputs per thread, K in steps of 16 through LDS with guarded loads that
+// walk each source along its contiguous dimension.
+template <bool TA, bool TB>
+__global__ void __launch_bounds__(256) gemm_any_kernel(const GemmArgs args) {
+  __shared__ float As[16][65], Bs[16][65];  // [k][m], [k][n]
+  const GemmProblem P = args.p[blockIdx.z];
+  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  const int M = args.M, N = args.N, K = args.K;
+  const int t = threadIdx.x, tx = t & 15, ty = t >> 4;
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    for (int e = t; e < 1024; e += 256) {
+      const int kk = TA ? e / 64 : e % 16, mm = TA ? e % 64 : e / 16;
+      const int m = m0 + mm, k = k0 + kk;
+      As[kk][mm] = (m < M && k < K) ? (TA ? P.a[(size_t)k * args.lda + m] : P.a[(size_t)m * args.lda + k]) : 0.f;
+      const int kb = TB ? e / 64 : e % 16, nn = TB ? e % 64 : e / 16;
+      const int n = n0 + nn, kq = k0 + kb;
+      Bs[kb][nn] = (n < N && kq < K) ? (TB ? P.w[(size_t)kq * args.ldb + n] : P.w[(size_t)n * args.ldb + kq]) : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = As[kk][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * b[j];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + ty * 4 + i;
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + tx * 4 + j;
+      if (n >= N) continue;
+      float *pc = P.c + (size_t)m * args.ldc + n;
+      const float v = activate(acc[i][j] + (P.bias ? P.bias[n] : 0.f), args.act);
+      *pc = args.beta ? *pc + v : v;
+    }
+  }
+}
+
+// bgrad[m] += sum_k opA[m, k] for the problems of a gemm_any_kernel launch.
+template <bool TA>
+__global__ void __launch_bounds__(256) op_rowsum_kernel(const GemmArgs args) {
+  const GemmProblem P = args.p[blockIdx.y];
+  const int m = blockIdx.x * 256 + threadIdx.x;
+  if (!P.bgrad || m >= args.M) return;
+  float s = 0.f;
+  for (int k = 0; k < args.K; ++k) s += TA ? P.a[(size_t)k * args.lda + m] : P.a[(size_t)m * args.lda + k];
+  P.bgrad[m] += s;
+}
+
 // Two tile configurations: 256 x 128 with eight waves for M >= 1024, and
 // 128 x 128 with four waves for smaller M (decode rows, short sequences).
-template <int TM, int TN, int BKK, int WM, int WN, int MINB>
+template <int TM, int TN, int BKK, int WM, int WN, int MINB, bool TA, bool TB>
 int launch_tile(GemmArgs g, hipStream_t stream) {
   g.tiles_m = (g.M + TM - 1) / TM;
   g.tiles_n = (g.N + TN - 1) / TN;
   g.total = g.tiles_m * g.tiles_n * g.nprob;
   g.padded = pad_to_xcd(g.total);
   const dim3 grid(g.padded), block(64 * WM * WN);
-  if (g.rope_cs) {
-    gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, kActRope><<<grid, block, 0, stream>>>(g);
-    return CDML_OK;
-  }
-  switch (g.act) {
-    case CDML_ACT_NONE: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_NONE><<<grid, block, 0, stream>>>(g); break;
-    case CDML_ACT_SIGMOID: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_SIGMOID><<<grid, block, 0, stream>>>(g); break;
-    case CDML_ACT_TANH: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_TANH><<<grid, block, 0, stream>>>(g); break;
-    case CDML_ACT_RELU: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_RELU><<<grid, block, 0, stream>>>(g); break;
-    case CDML_ACT_LEAKYRELU: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_LEAKYRELU><<<grid, block, 0, stream>>>(g); break;
-    default: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_SWISH><<<grid, block, 0, stream>>>(g); break;
+  if constexpr (TA || TB) {
+    gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_NONE, TA, TB><<<grid, block, 0, stream>>>(g);
+  } else {
+    if (g.rope_cs) {
+      gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, kActRope, false, false><<<grid, block, 0, stream>>>(g);
+      return CDML_OK;
+    }
+    switch (g.act) {
+      case CDML_ACT_NONE: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_NONE, false, false><<<grid, block, 0, stream>>>(g); break;
+      case CDML_ACT_SIGMOID: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_SIGMOID, false, false><<<grid, block, 0, stream>>>(g); break;
+      case CDML_ACT_TANH: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_TANH, false, false><<<grid, block, 0, stream>>>(g); break;
+      case CDML_ACT_RELU: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_RELU, false, false><<<grid, block, 0, stream>>>(g); break;
+      case CDML_ACT_LEAKYRELU: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_LEAKYRELU, false, false><<<grid, block, 0, stream>>>(g); break;
+      default: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_SWISH, false, false><<<grid, block, 0, stream>>>(g); break;
+    }
   }
   return CDML_OK;
 }
 
-int launch_gemm(GemmArgs &g, hipStream_t stream, const char *what) {
+// Whether a [rows, K] (T = false) or [K, rows] (T = true) operand with row
+// stride ld and base p suits the tiled kernel's staging.
+bool stage_ok(const float *p, int rows, int ld, bool T, int bkk) {
+  if (!aligned16(p) || ld % 4) return false;
+  if (T) return rows % 4 == 0 && (unsigned long long)bkk * ld + rows < (1ull << 32);
+  return (unsigned long long)rows * ld < (1ull << 32);
+}
+
+template <bool TA, bool TB>
+int launch_layout(GemmArgs &g, bool fast, hipStream_t stream) {
+  if (fast) return g.M >= 1024 ? launch_tile<256, 128, 16, 4, 2, 2, TA, TB>(g, stream)
+                               : launch_tile<128, 128, 16, 2, 2, 2, TA, TB>(g, stream);
+  const dim3 grid((g.N + 63) / 64, (g.M + 63) / 64, g.nprob);
+  gemm_any_kernel<TA, TB><<<grid, dim3(256), 0, stream>>>(g);
+  bool bgrad = false;
+  for (int i = 0; i < g.nprob; ++i) bgrad = bgrad || g.p[i].bgrad;
+  if (bgrad && g.K > 0) op_rowsum_kernel<TA><<<dim3((g.M + 255) / 256, g.nprob), dim3(256), 0, stream>>>(g);
+  return CDML_OK;
+}
+
+// ta / tb: opA / opB stored transposed ([K, M] / [K, N]).
+int launch_gemm(GemmArgs &g, bool ta, bool tb, hipStream_t stream, const char *what) {
   if (g.M == 0 || g.N == 0) return CDML_OK;
+  if ((ta || tb) && (g.M > 65535 * 64 || g.N > 65535 * 64))
+    return fail(CDML_E_INVALID, "%s: matrix too large", what);
+  bool fast = g.K % 16 == 0 && g.K > 0;
+  for (int i = 0; i < g.nprob; ++i)
+    fast = fast && stage_ok(g.p[i].a, g.M, g.lda, ta, 16) && stage_ok(g.p[i].w, g.N, g.ldb, tb, 16);
+  if (ta || tb) {
+    int rc;
+    if (ta && tb) rc = launch_layout<true, true>(g, fast, stream);
+    else if (tb) rc = launch_layout<false, true>(g, fast, stream);
+    else rc = launch_layout<true, false>(g, false, stream);
+    if (rc) return rc;
+    return check_launch(what);
+  }
   g.tiles_m = (g.M + BM - 1) / BM;
   g.tiles_n = (g.N + BN - 1) / BN;
   g.total = g.tiles_m * g.tiles_n * g.nprob;
   g.padded = pad_to_xcd(g.total);
-  bool vec = (g.K % 4 == 0) && (g.lda % 4 == 0) && aligned16(g.a);
-  for (int i = 0; i < g.nprob; ++i) vec = vec && aligned16(g.p[i].w);
-  const bool fast = vec && g.K % 16 == 0 && g.K > 0 &&
-                    (unsigned long long)g.M * g.lda < (1ull << 32) &&
-                    (unsigned long long)g.N * g.K < (1ull << 32);
+  bool vec = (g.K % 4 == 0) && (g.lda % 4 == 0) && (g.ldb % 4 == 0);
+  for (int i = 0; i < g.nprob; ++i) vec = vec && aligned16(g.p[i].a) && aligned16(g.p[i].w);
   if (fast && g.M >= 1024) {
-    int rc = launch_tile<256, 128, 16, 4, 2, 2>(g, stream);
+    int rc = launch_tile<256, 128, 16, 4, 2, 2, false, false>(g, stream);
     if (rc) return rc;
   } else if (fast) {
-    int rc = launch_tile<128, 128, 16, 2, 2, 2>(g, stream);
+    int rc = launch_tile<128, 128, 16, 2, 2, 2, false, false>(g, stream);
     if (rc) return rc;
   } else if (vec)
     gemm_nt_kernel<true><<<dim3(g.padded), dim3(NTHREADS), 0, stream>>>(g);
@@ -474,22 +666,20 @@ extern "C" int cdml_project_qkv(const float *x, const float *wq, const float *bq
     return fail(CDML_E_INVALID, "cdml_project_qkv: NULL pointer");
   int rc = ensure_device();
   if (rc) return rc;
-  if (in_dim == 0) {
-    // y = bias only; a K of zero leaves the accumulators at 0.
-  }
+  // in_dim == 0: a K of zero leaves the accumulators at 0 and y = bias.
   GemmArgs g{};
-  g.a = x;
   g.lda = in_dim;
+  g.ldb = in_dim;
   g.ldc = out_dim;
   g.M = rows;
   g.N = out_dim;
   g.K = in_dim;
   g.nprob = 3;
-  g.p[0] = {wq, bq, q};
-  g.p[1] = {wk, bk, k};
-  g.p[2] = {wv, bv, v};
+  g.p[0] = {x, wq, bq, q, nullptr};
+  g.p[1] = {x, wk, bk, k, nullptr};
+  g.p[2] = {x, wv, bv, v, nullptr};
   g.act = CDML_ACT_NONE;
-  return launch_gemm(g, as_hip(stream), "cdml_project_qkv");
+  return launch_gemm(g, false, false, as_hip(stream), "cdml_project_qkv");
 }
 
 extern "C" int cdml_project_qkv_rope(const float *x, const float *wq, const float *bq,
@@ -514,23 +704,23 @@ extern "C" int cdml_project_qkv_rope(const float *x, const float *wq, const floa
   int rc = ensure_device();
   if (rc) return rc;
   GemmArgs g{};
-  g.a = x;
   g.lda = in_dim;
+  g.ldb = in_dim;
   g.ldc = out_dim;
   g.M = rows;
   g.N = out_dim;
   g.K = in_dim;
   g.nprob = 3;
-  g.p[0] = {wq, bq, q};
-  g.p[1] = {wk, bk, k};
-  g.p[2] = {wv, bv, v};
+  g.p[0] = {x, wq, bq, q, nullptr};
+  g.p[1] = {x, wk, bk, k, nullptr};
+  g.p[2] = {x, wv, bv, v, nullptr};
   g.act = CDML_ACT_NONE;
   g.rope_cs = reinterpret_cast<const float2 *>(rope_cs);
   g.rope_hd = head_dim;
   g.rope_npos = n_pos;
   g.rope_pos0 = pos_offset;
   g.rope_seg = seg_len;
-  return launch_gemm(g, as_hip(stream), "cdml_project_qkv_rope");
+  return launch_gemm(g, false, false, as_hip(stream), "cdml_project_qkv_rope");
 }
 
 extern "C" int cdml_linear(const float *x, int ldx, const float *w, const float *b, float *y,
@@ -547,14 +737,127 @@ extern "C" int cdml_linear(const float *x, int ldx, const float *w, const float 
   int rc = ensure_device();
   if (rc) return rc;
   GemmArgs g{};
-  g.a = x;
   g.lda = ldx;
+  g.ldb = in_dim;
   g.ldc = ldy;
   g.M = rows;
   g.N = out_dim;
   g.K = in_dim;
   g.nprob = 1;
-  g.p[0] = {w, b, y};
+  g.p[0] = {x, w, b, y, nullptr};
   g.act = activation;
-  return launch_gemm(g, as_hip(stream), "cdml_linear");
+  return launch_gemm(g, false, false, as_hip(stream), "cdml_linear");
+}
+
+extern "C" int cdml_linear_backward(const float *x, int ldx, const float *dy, int lddy,
+                                    const float *w, float *dx, int lddx, float *wgrad,
+                                    float *bgrad, int rows, int in_dim, int out_dim,
+                                    int accumulate_dx, cdml_stream stream) {
+  if (rows < 0 || in_dim < 0 || out_dim < 0)
+    return fail(CDML_E_INVALID, "cdml_linear_backward: negative size");
+  if (lddy < out_dim || (dx && lddx < in_dim) || (wgrad && ldx < in_dim))
+    return fail(CDML_E_INVALID, "cdml_linear_backward: row stride smaller than the row");
+  if (rows == 0) return CDML_OK;
+  if (!dy || (dx && !w) || (wgrad && !x))
+    return fail(CDML_E_INVALID, "cdml_linear_backward: NULL pointer");
+  int rc = ensure_device();
+  if (rc) return rc;
+  hipStream_t st = as_hip(stream);
+  if (dx && in_dim > 0) {
+    // dX (+)= dY W: opA = dY [rows, out], opB = W read as [out, in]
+    GemmArgs g{};
+    g.lda = lddy;
+    g.ldb = in_dim;
+    g.ldc = lddx;
+    g.M = rows;
+    g.N = in_dim;
+    g.K = out_dim;
+    g.nprob = 1;
+    g.p[0] = {dy, w, nullptr, dx, nullptr};
+    g.beta = accumulate_dx ? 1 : 0;
+    rc = launch_gemm(g, false, true, st, "cdml_linear_backward (input gradient)");
+    if (rc) return rc;
+  }
+  if ((wgrad || bgrad) && out_dim > 0) {
+    // W_grad += dY^T X: opA = dY read as [out, rows], opB = X read as
+    // [rows, in]; the bias gradient rides on the staging of opA.
+    GemmArgs g{};
+    g.lda = lddy;
+    g.ldb = ldx;
+    g.ldc = in_dim;
+    g.M = out_dim;
+    g.N = in_dim;
+    g.K = rows;
+    g.nprob = 1;
+    g.p[0] = {dy, x, nullptr, wgrad, bgrad};
+    g.beta = 1;
+    if (wgrad && in_dim > 0) {
+      rc = launch_gemm(g, true, true, st, "cdml_linear_backward (weight gradient)");
+    } else if (bgrad) {
+      op_rowsum_kernel<true><<<dim3((out_dim + 255) / 256, 1), dim3(256), 0, st>>>(g);
+      rc = check_launch("cdml_linear_backward (bias gradient)");
+    }
+    if (rc) return rc;
+  }
+  return CDML_OK;
+}
+
+extern "C" int cdml_backprop_qkv(const float *x, const float *dq, const float *dk, const float *dv,
+                                 const float *wq, const float *wk, const float *wv, float *wq_grad,
+                                 float *bq_grad, float *wk_grad, float *bk_grad, float *wv_grad,
+                                 float *bv_grad, float *dx, int rows, int in_dim, int out_dim,
+                                 cdml_stream stream) {
+  if (rows < 0 || in_dim < 0 || out_dim < 0)
+    return fail(CDML_E_INVALID, "cdml_backprop_qkv: negative size");
+  if (rows == 0) return CDML_OK;
+  if (!x || !dq || !dk || !dv || !wq || !wk || !wv || !wq_grad || !bq_grad || !wk_grad ||
+      !bk_grad || !wv_grad || !bv_grad || !dx)
+    return fail(CDML_E_INVALID, "cdml_backprop_qkv: NULL pointer");
+  int rc = ensure_device();
+  if (rc) return rc;
+  hipStream_t st = as_hip(stream);
+  if (out_dim > 0) {
+    // W*_grad += d*^T X and b*_grad += column sums of d*, three problems in
+    // one launch
+    GemmArgs g{};
+    g.lda = out_dim;
+    g.ldb = in_dim;
+    g.ldc = in_dim;
+    g.M = out_dim;
+    g.N = in_dim;
+    g.K = rows;
+    g.nprob = 3;
+    g.p[0] = {dq, x, nullptr, wq_grad, bq_grad};
+    g.p[1] = {dk, x, nullptr, wk_grad, bk_grad};
+    g.p[2] = {dv, x, nullptr, wv_grad, bv_grad};
+    g.beta = 1;
+    if (in_dim > 0) {
+      rc = launch_gemm(g, true, true, st, "cdml_backprop_qkv (weight gradients)");
+    } else {
+      op_rowsum_kernel<true><<<dim3((out_dim + 255) / 256, 3), dim3(256), 0, st>>>(g);
+      rc = check_launch("cdml_backprop_qkv (bias gradients)");
+    }
+    if (rc) return rc;
+  }
+  if (in_dim > 0) {
+    // dX = dQ WQ + dK WK + dV WV, the three products accumulated in turn
+    // (out_dim == 0: dX = 0)
+    const float *d[3] = {dq, dk, dv};
+    const float *w[3] = {wq, wk, wv};
+    for (int s = 0; s < 3; ++s) {
+      GemmArgs g{};
+      g.lda = out_dim;
+      g.ldb = in_dim;
+      g.ldc = in_dim;
+      g.M = rows;
+      g.N = in_dim;
+      g.K = out_dim;
+      g.nprob = 1;
+      g.p[0] = {d[s], w[s], nullptr, dx, nullptr};
+      g.beta = s > 0;
+      rc = launch_gemm(g, false, true, st, "cdml_backprop_qkv (input gradient)");
+      if (rc) return rc;
+    }
+  }
+  return CDML_OK;
 }

@@ -128,6 +128,34 @@ int cdml_linear(const float *x, int ldx, const float *w, const float *b,
                 float *y, int ldy, int rows, int in_dim, int out_dim,
                 int activation, cdml_stream stream);
 
+/* IAccelerationManager.BackpropLinearProjection (:182) and
+ * BackpropOutputProjection (:184), replacing AccelerationCPU.cs:2188-2270:
+ *   wgrad += dy^T x,  bgrad += column sums of dy,  dx (+)= dy w
+ * x [rows, in_dim] (row stride ldx); dy [rows, out_dim] (row stride lddy);
+ * w [out_dim, in_dim]; wgrad [out_dim, in_dim] and bgrad [out_dim]
+ * accumulate; dx [rows, in_dim] (row stride lddx) is overwritten
+ * (accumulate_dx = 0, BackpropOutputProjection) or added to (1,
+ * BackpropLinearProjection).  dx = NULL skips the input gradient; wgrad and
+ * bgrad may be NULL to skip theirs.  fp32 MFMA; the bias gradient is summed
+ * inside the weight-gradient GEMM. */
+int cdml_linear_backward(const float *x, int ldx, const float *dy, int lddy,
+                         const float *w, float *dx, int lddx, float *wgrad,
+                         float *bgrad, int rows, int in_dim, int out_dim,
+                         int accumulate_dx, cdml_stream stream);
+
+/* IAccelerationManager.BackpropQKV (:171), replacing AccelerationCPU.cs:
+ * 2071-2186:
+ *   dx = dq wq + dk wk + dv wv   (overwritten)
+ *   w*_grad += d*^T x,  b*_grad += column sums of d*   (accumulated)
+ * x [rows, in_dim]; dq, dk, dv [rows, out_dim]; w* and w*_grad
+ * [out_dim, in_dim]; b*_grad [out_dim]; dx [rows, in_dim]; all contiguous. */
+int cdml_backprop_qkv(const float *x, const float *dq, const float *dk,
+                      const float *dv, const float *wq, const float *wk,
+                      const float *wv, float *wq_grad, float *bq_grad,
+                      float *wk_grad, float *bk_grad, float *wv_grad,
+                      float *bv_grad, float *dx, int rows, int in_dim,
+                      int out_dim, cdml_stream stream);
+
 /* IAccelerationManager.ApplyRotaryPositionEmbeddingInPlace (:320) and
  * ApplyRotaryPositionEmbeddingHeadInPlace (:319), replacing
  * AccelerationCPU.cs:4855-4980 and GPU/RotaryPositionEmbeddings.cs:58-156.

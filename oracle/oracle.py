@@ -60,6 +60,10 @@ def lib():
             "ref_decode_attention": (i, [_f32p, _f32p, _f32p, i, i, i, f, _f32p]),
             "ref_lm_forward": (i, [C.c_void_p, _i32p, i, _f32p]),
             "ref_lm_generate_greedy": (i, [C.c_void_p, _i32p, i, i, _i32p, C.POINTER(i)]),
+            "ref_mha_backward": (i, [_f32p] * 7 + [i, i, i, i, f, _u8p, i]),
+            "ref_backprop_qkv": (i, [_f32p] * 14 + [i, i, i]),
+            "ref_backprop_linear_projection": (i, [_f32p] * 6 + [i, i, i]),
+            "ref_backprop_output_projection": (i, [_f32p] * 6 + [i, i, i]),
             "mt_num_threads": (i, []),
             "mt_set_threads": (None, [i]),
             "mt_project_qkv": (i, [_f32p] * 10 + [i, i, i]),
@@ -245,6 +249,58 @@ def decode_attention_batch(q, kcache, vcache, kv_len, num_heads: int, scale: flo
                                     np.ascontiguousarray(kv_len, dtype=np.int32),
                                     b, t_max, dim, num_heads, scale, out, int(parallel))
     return out
+
+
+# ---- backward path (refcpu_bwd.c) ----------------------------------------
+
+def mha_backward(q, k, v, dout, num_heads: int, scale: float, mask=None, use_decoder_mask: bool = False):
+    """AccelerationCPU.MultiHeadAttentionBackward (bool and mask overloads) -> (dQ, dK, dV)."""
+    q, k, v, dout = _f32(q), _f32(k), _f32(v), _f32(dout)
+    lq, dim = q.shape
+    lk = k.shape[0]
+    dq = np.empty((lq, dim), np.float32)
+    dk = np.empty((lk, dim), np.float32)
+    dv = np.empty((lk, dim), np.float32)
+    m, mp = _mask_ptr(mask)
+    _check(lib().ref_mha_backward(q, k, v, dout, dq, dk, dv, lq, lk, dim, num_heads, scale, mp,
+                                  int(use_decoder_mask)), "MultiHeadAttentionBackward")
+    return dq, dk, dv
+
+
+def backprop_qkv(x, dq, dk, dv, wq, wk, wv, wq_grad, bq_grad, wk_grad, bk_grad, wv_grad, bv_grad):
+    """AccelerationCPU.BackpropQKV on copies of the gradient accumulators ->
+    (dInput, WQGrad, biasQGrad, WKGrad, biasKGrad, WVGrad, biasVGrad)."""
+    x = _f32(x)
+    rows, in_dim = x.shape
+    out_dim = wq.shape[0]
+    g = [_f32(a).copy() for a in (wq_grad, bq_grad, wk_grad, bk_grad, wv_grad, bv_grad)]
+    dx = np.empty((rows, in_dim), np.float32)
+    _check(lib().ref_backprop_qkv(x, _f32(dq), _f32(dk), _f32(dv), _f32(wq), _f32(wk), _f32(wv), *g, dx,
+                                  rows, in_dim, out_dim), "BackpropQKV")
+    return (dx, *g)
+
+
+def backprop_linear_projection(x, dy, w, w_grad, b_grad, dx):
+    """AccelerationCPU.BackpropLinearProjection on copies -> (weightGrad, biasGrad, dInput)."""
+    x, dy = _f32(x), _f32(dy)
+    rows, in_dim = x.shape
+    out_dim = dy.shape[1]
+    wg, bg, dxo = _f32(w_grad).copy(), _f32(b_grad).copy(), _f32(dx).copy()
+    _check(lib().ref_backprop_linear_projection(x, dy, _f32(w), wg, bg, dxo, rows, in_dim, out_dim),
+           "BackpropLinearProjection")
+    return wg, bg, dxo
+
+
+def backprop_output_projection(dl, x, w, w_grad, b_grad):
+    """AccelerationCPU.BackpropOutputProjection on copies -> (dX, weightGrad, biasGrad)."""
+    dl, x = _f32(dl), _f32(x)
+    rows, out_dim = dl.shape
+    emb = x.shape[1]
+    wg, bg = _f32(w_grad).copy(), _f32(b_grad).copy()
+    dx = np.empty((rows, emb), np.float32)
+    _check(lib().ref_backprop_output_projection(dl, x, _f32(w), wg, bg, dx, rows, out_dim, emb),
+           "BackpropOutputProjection")
+    return dx, wg, bg
 
 
 def num_threads() -> int:

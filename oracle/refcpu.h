@@ -100,6 +100,26 @@ int ref_decode_attention(const float *q, const float *kcache,
                          const float *vcache, int key_len, int dim,
                          int num_heads, float scale, float *out);
 
+/* ---- backward path (refcpu_bwd.c) -------------------------------------- */
+
+int ref_mha_backward(const float *q, const float *k, const float *v,
+                     const float *dout, float *dq, float *dk, float *dv, int lq,
+                     int lk, int dim, int num_heads, float scale,
+                     const uint8_t *mask, int use_decoder_mask);
+int ref_backprop_qkv(const float *x, const float *dq, const float *dk,
+                     const float *dv, const float *wq, const float *wk,
+                     const float *wv, float *wqg, float *bqg, float *wkg,
+                     float *bkg, float *wvg, float *bvg, float *dx, int rows,
+                     int in_dim, int out_dim);
+int ref_backprop_linear_projection(const float *x, const float *dy,
+                                   const float *w, float *wg, float *bg,
+                                   float *dx, int rows, int in_dim,
+                                   int out_dim);
+int ref_backprop_output_projection(const float *dl, const float *x,
+                                   const float *w, float *wg, float *bg,
+                                   float *dx, int rows, int out_dim,
+                                   int emb_dim);
+
 /* ---- multi-threaded restatement of AccelerationMutliThreadCPU ---------- */
 
 int mt_num_threads(void);

@@ -73,6 +73,30 @@ def linear(x, w, b, act=0):
     return down(y, (rows, out))
 
 
+def linear_backward(x, dy, w, wgrad, bgrad, dx=None, accumulate=False, want_dx=True):
+    """cdml_linear_backward -> (wgrad, bgrad, dx) after the call (dx None when skipped)."""
+    rows, ind = x.shape
+    out = dy.shape[1]
+    bx, bdy, bw, bwg, bbg = up(x), up(dy), up(w), up(wgrad), up(bgrad)
+    bdx = up(dx) if dx is not None else N.DeviceBuffer(max(4, rows * ind * 4))
+    N.check(N.lib().cdml_linear_backward(bx.ptr, ind, bdy.ptr, out, bw.ptr, bdx.ptr if want_dx else None, ind,
+                                         bwg.ptr, bbg.ptr, rows, ind, out, int(accumulate), stream().handle))
+    return down(bwg, (out, ind)), down(bbg, (out,)), down(bdx, (rows, ind)) if want_dx else None
+
+
+def backprop_qkv(x, dq, dk, dv, wq, wk, wv, wq_grad, bq_grad, wk_grad, bk_grad, wv_grad, bv_grad):
+    """cdml_backprop_qkv -> (dx, wq_grad, bq_grad, wk_grad, bk_grad, wv_grad, bv_grad)."""
+    rows, ind = x.shape
+    out = wq.shape[0]
+    ins = [up(a) for a in (x, dq, dk, dv, wq, wk, wv)]
+    grads = [up(a) for a in (wq_grad, bq_grad, wk_grad, bk_grad, wv_grad, bv_grad)]
+    bdx = N.DeviceBuffer(max(4, rows * ind * 4))
+    N.check(N.lib().cdml_backprop_qkv(*(b.ptr for b in ins), *(g.ptr for g in grads), bdx.ptr, rows, ind, out,
+                                      stream().handle))
+    shapes = [(out, ind), (out,)] * 3
+    return (down(bdx, (rows, ind)), *(down(g, sh) for g, sh in zip(grads, shapes)))
+
+
 def rope(x, num_heads=None, start_col=0, head_dim=None, base=10000.0, inverse=False,
          pos_offset=0, seg_len=0, positions=None):
     rows, dim = x.shape

@@ -146,6 +146,76 @@ def test_project_qkv_rope(rows, ind, out, hd, seg, off):
     parity(v, wv, f"QKV+RoPE {rows}x{ind}->{out} V")
 
 
+# ------------------------------------------------------- projection gradients
+def test_backprop_qkv_reference_case():
+    """BackpropQKV on the closed-form inputs of AccelerationManagerParityTests.cs:462-537."""
+    x = M(6, 5, 124)
+    w = (M(8, 5, 125), M(8, 5, 126), M(8, 5, 127))
+    d = (M(6, 8, 131), M(6, 8, 132), M(6, 8, 133))
+    g0 = (M(8, 5, 134), Vec(8, 137), M(8, 5, 135), Vec(8, 138), M(8, 5, 136), Vec(8, 139))
+    got = G.backprop_qkv(x, *d, *w, *g0)
+    want = O.backprop_qkv(x, *d, *w, *g0)
+    for a, e, n in zip(got, want, ["dInput", "WQGrad", "biasQGrad", "WKGrad", "biasKGrad", "WVGrad", "biasVGrad"]):
+        parity(a, e, f"BackpropQKV {n}")
+
+
+@pytest.mark.parametrize("rows,ind,out", [(1024, 512, 512),   # tiled kernels (128-row tiles)
+                                          (2048, 256, 1024),  # 256-row tiles for W_grad
+                                          (300, 1024, 96),    # K = 300 rows: generic W_grad kernel
+                                          (130, 257, 129),    # ragged everywhere
+                                          (1, 64, 64)])
+def test_backprop_qkv_shapes(rows, ind, out):
+    x = synth.normal(rows + ind, (rows, ind))
+    w = [synth.xavier_uniform(i + out, out, ind) for i in range(3)]
+    d = [synth.normal(50 + i, (rows, out)) for i in range(3)]
+    g0 = [synth.normal(60, (out, ind)), synth.normal(61, (out,)), synth.normal(62, (out, ind)),
+          synth.normal(63, (out,)), synth.normal(64, (out, ind)), synth.normal(65, (out,))]
+    got = G.backprop_qkv(x, *d, *w, *g0)
+    want = O.backprop_qkv(x, *d, *w, *g0)
+    for a, e, n in zip(got, want, ["dInput", "WQGrad", "biasQGrad", "WKGrad", "biasKGrad", "WVGrad", "biasVGrad"]):
+        parity(a, e, f"BackpropQKV {rows}x{ind}->{out} {n}")
+
+
+def test_backprop_qkv_c3_shape_float64():
+    """One c3 sequence (4096 rows, 1024 -> 1024) against float64 matrix
+    algebra: the identities dInput = sum dX W, W_grad += dX^T x and
+    b_grad += column sums that the oracle's loops were pinned on."""
+    rows, ind, out = 4096, 1024, 1024
+    x = synth.normal(1, (rows, ind))
+    w = [synth.xavier_uniform(2 + i, out, ind) for i in range(3)]
+    d = [synth.normal(5 + i, (rows, out)) * np.float32(0.05) for i in range(3)]
+    g0 = [np.zeros((out, ind), np.float32), np.zeros(out, np.float32)] * 3
+    dx, wqg, bqg, wkg, bkg, wvg, bvg = G.backprop_qkv(x, *d, *w, *g0)
+    X = x.astype(np.float64)
+    D = [a.astype(np.float64) for a in d]
+    parity(dx, sum(Di @ Wi.astype(np.float64) for Di, Wi in zip(D, w)), "c3 dInput")
+    for got_w, got_b, Di, n in [(wqg, bqg, D[0], "Q"), (wkg, bkg, D[1], "K"), (wvg, bvg, D[2], "V")]:
+        parity(got_w, Di.T @ X, f"c3 W{n}Grad")
+        parity(got_b, Di.sum(0), f"c3 bias{n}Grad")
+
+
+@pytest.mark.parametrize("rows,ind,out", [(4, 8, 8), (16, 16, 32), (512, 256, 256), (77, 64, 130)])
+def test_linear_backward(rows, ind, out):
+    """BackpropLinearProjection (dInput accumulates) and BackpropOutputProjection
+    (dX overwritten) on the shapes of AccelerationConsistencyTests.cs:633-700,
+    1108-1125 and larger tiled ones."""
+    x, dy, w = synth.normal(1, (rows, ind)), synth.normal(2, (rows, out)), synth.normal(3, (out, ind))
+    wg0, bg0, dx0 = synth.normal(4, (out, ind)), synth.normal(5, (out,)), synth.normal(6, (rows, ind))
+    wg, bg, dx = G.linear_backward(x, dy, w, wg0, bg0, dx=dx0, accumulate=True)
+    ewg, ebg, edx = O.backprop_linear_projection(x, dy, w, wg0, bg0, dx0)
+    parity(wg, ewg, "linear weightGrad")
+    parity(bg, ebg, "linear biasGrad")
+    parity(dx, edx, "linear dInput")
+    wg, bg, dx = G.linear_backward(x, dy, w, wg0, bg0)
+    edx, ewg, ebg = O.backprop_output_projection(dy, x, w, wg0, bg0)
+    parity(dx, edx, "output dX")
+    parity(wg, ewg, "output weightGrad")
+    parity(bg, ebg, "output biasGrad")
+    wg, bg, none = G.linear_backward(x, dy, w, wg0, bg0, want_dx=False)
+    assert none is None
+    parity(wg, ewg, "weightGrad without dX")
+
+
 # ------------------------------------------------------------------- SDPA
 def test_sdpa_reference_cases(ops_golden):
     g = ops_golden

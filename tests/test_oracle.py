@@ -258,3 +258,123 @@ def test_activation_library_values():
     close(O.activation(x, 3), np.maximum(x64, 0), atol=0, rtol=0, what="relu")
     close(O.activation(x, 4), np.where(x64 > 0, x64, 0.01 * x64), atol=1e-9, rtol=1e-6, what="leakyrelu")
     close(O.activation(x, 5), x64 * expit(x64), atol=1e-6, rtol=1e-6, what="swish")
+
+
+# ------------------------------------------------------------ backward path
+def _attention64(q, k, v, heads, scale, visible):
+    """float64 attention forward: per head softmax(q k^T * scale) v over the
+    visible keys (bool [lq, lk]); a row with no visible key gives zeros."""
+    lq, dim = q.shape
+    hd = dim // heads
+    out = np.zeros((lq, dim))
+    for h in range(heads):
+        sl = slice(h * hd, (h + 1) * hd)
+        s = (q[:, sl] @ k[:, sl].T) * scale
+        s = np.where(visible, s, -np.inf)
+        for i in range(lq):
+            if not visible[i].any():
+                continue
+            e = np.exp(s[i] - s[i].max())
+            out[i, sl] = (e / e.sum()) @ v[:, sl]
+    return out
+
+
+def _fd_grads(q, k, v, dout, heads, scale, visible, eps=1e-6):
+    """Central differences of L = sum(dout * attention(q, k, v)) in float64:
+    the gradients by brute force, with no derivation of the backward."""
+    args = [np.array(a, np.float64) for a in (q, k, v)]
+    g = [np.zeros_like(a) for a in args]
+    for t in range(3):
+        for idx in np.ndindex(args[t].shape):
+            keep = args[t][idx]
+            args[t][idx] = keep + eps
+            up = np.sum(dout * _attention64(*args, heads, scale, visible))
+            args[t][idx] = keep - eps
+            dn = np.sum(dout * _attention64(*args, heads, scale, visible))
+            args[t][idx] = keep
+            g[t][idx] = (up - dn) / (2 * eps)
+    return g
+
+
+@pytest.mark.parametrize("case", ["parity_decoder", "parity_mask", "nomask_6x8", "decoder_6x8", "cross_5x8",
+                                  "decoder_lq_gt_lk", "sparse_mask"])
+def test_mha_backward_against_finite_differences(case):
+    """MultiHeadAttentionBackward (AccelerationCPU.cs:1011-1280) on the shapes
+    of AccelerationManagerParityTests.cs:354-383 (closed-form inputs, 4 x 6,
+    2 heads, scale 1/sqrt(3)) and AccelerationConsistencyTests.cs:964-1022
+    (6 x 8 and cross 5 x 8, 2 heads)."""
+    if case.startswith("parity"):
+        q, k, v, dout = M(4, 6, 31), M(4, 6, 32), M(4, 6, 33), M(4, 6, 34)
+        heads, scale = 2, float(np.float32(1.0) / np.sqrt(np.float32(3.0)))
+    else:
+        lq, lk = {"cross_5x8": (5, 8), "decoder_lq_gt_lk": (7, 4)}.get(case, (6, 6))
+        q, k, v = synth.normal(1, (lq, 8)), synth.normal(2, (lk, 8)), synth.normal(3, (lk, 8))
+        dout = synth.normal(4, (lq, 8))
+        heads, scale = 2, 0.5
+    lq, lk = q.shape[0], k.shape[0]
+    tril = np.tril(np.ones((lq, lk), bool))  # key j visible to query i iff j <= i
+    mask = None
+    if case == "parity_mask":
+        mask = O.causal_mask(4).astype(bool)
+        got = O.mha_backward(q, k, v, dout, heads, scale, mask=mask)
+        visible = mask
+    elif case == "sparse_mask":
+        mask = synth.normal(9, (lq, lk)) > 0.3
+        mask[2] = False  # a row with no visible key contributes nothing
+        got = O.mha_backward(q, k, v, dout, heads, scale, mask=mask)
+        visible = mask
+    elif case in ("parity_decoder", "decoder_6x8", "decoder_lq_gt_lk"):
+        got = O.mha_backward(q, k, v, dout, heads, scale, use_decoder_mask=True)
+        visible = tril
+    else:
+        got = O.mha_backward(q, k, v, dout, heads, scale)
+        visible = np.ones((lq, lk), bool)
+    want = _fd_grads(q, k, v, np.asarray(dout, np.float64), heads, scale, visible)
+    for g, w, n in zip(got, want, "QKV"):
+        close(g, w, atol=2e-5, rtol=1e-4, what=f"{case} d{n}")
+    if case == "sparse_mask":
+        assert np.all(got[0][2] == 0)
+    # a planted sign error in the oracle's softmax-gradient term must fail the check
+    dq_bad = got[0] + 0.01 * np.sign(want[0] + 1e-9)
+    with pytest.raises(AssertionError):
+        close(dq_bad, want[0], atol=2e-5, rtol=1e-4)
+
+
+def test_backprop_qkv_closed_form():
+    """BackpropQKV (AccelerationCPU.cs:2071-2186) on the closed-form inputs of
+    AccelerationManagerParityTests.cs:462-537 (6 rows, 5 -> 8, accumulators
+    starting from nonzero values): dInput = dQ WQ + dK WK + dV WV,
+    W*Grad += d*^T x, bias*Grad += column sums of d*, in float64."""
+    x = M(6, 5, 124)
+    wq, wk, wv = M(8, 5, 125), M(8, 5, 126), M(8, 5, 127)
+    dq, dk, dv = M(6, 8, 131), M(6, 8, 132), M(6, 8, 133)
+    g0 = [M(8, 5, 134), Vec(8, 137), M(8, 5, 135), Vec(8, 138), M(8, 5, 136), Vec(8, 139)]
+    dx, wqg, bqg, wkg, bkg, wvg, bvg = O.backprop_qkv(x, dq, dk, dv, wq, wk, wv, *g0)
+    X, D = x.astype(np.float64), [a.astype(np.float64) for a in (dq, dk, dv)]
+    W = [a.astype(np.float64) for a in (wq, wk, wv)]
+    close(dx, D[0] @ W[0] + D[1] @ W[1] + D[2] @ W[2], what="dInput")
+    for got, g_init, d, n in [(wqg, g0[0], D[0], "WQ"), (wkg, g0[2], D[1], "WK"), (wvg, g0[4], D[2], "WV")]:
+        close(got, g_init + d.T @ X, what=f"{n}Grad")
+    for got, b_init, d, n in [(bqg, g0[1], D[0], "bQ"), (bkg, g0[3], D[1], "bK"), (bvg, g0[5], D[2], "bV")]:
+        close(got, b_init + d.sum(0), what=f"{n}Grad")
+
+
+def test_backprop_linear_and_output_projection():
+    """BackpropLinearProjection (AccelerationCPU.cs:2188-2229: dInput
+    accumulates) and BackpropOutputProjection (:2231-2270: dX overwritten) on
+    the shapes of AccelerationConsistencyTests.cs:633-700,1108-1125."""
+    x, dy, w = synth.normal(1, (4, 8)), synth.normal(2, (4, 8)), synth.normal(3, (8, 8))
+    wg0, bg0, dx0 = synth.normal(4, (8, 8)), synth.normal(5, (8,)), synth.normal(6, (4, 8))
+    wg, bg, dx = O.backprop_linear_projection(x, dy, w, wg0, bg0, dx0)
+    X, DY, W = (a.astype(np.float64) for a in (x, dy, w))
+    close(wg, wg0 + DY.T @ X, what="linear weightGrad")
+    close(bg, bg0 + DY.sum(0), what="linear biasGrad")
+    close(dx, dx0 + DY @ W, what="linear dInput (accumulated)")
+    for seq, out, emb in [(4, 8, 6), (16, 32, 16)]:
+        dl, xin, wo = synth.normal(7, (seq, out)), synth.normal(8, (seq, emb)), synth.normal(9, (out, emb))
+        wg0, bg0 = synth.normal(10, (out, emb)), synth.normal(11, (out,))
+        dxo, wgo, bgo = O.backprop_output_projection(dl, xin, wo, wg0, bg0)
+        DL, XI, WO = (a.astype(np.float64) for a in (dl, xin, wo))
+        close(dxo, DL @ WO, what="output dX")
+        close(wgo, wg0 + DL.T @ XI, what="output weightGrad")
+        close(bgo, bg0 + DL.sum(0), what="output biasGrad")
