@@ -66,6 +66,9 @@ SIGNATURES = {
     "cdml_rope": [_vp, _i, _i, _i, _i, _i, _f, _i, _i, _i, _vp, _vp],
     "cdml_linear_backward": [_vp, _i, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _vp],
     "cdml_backprop_qkv": [_vp] * 14 + [_i, _i, _i, _vp],
+    "cdml_sdpa_bwd_workspace_size": [_i, _i, _i, _i, _i, C.POINTER(_sz)],
+    "cdml_sdpa_bwd": [_vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i,
+                      _i, _i, _i, _i, _i, _f, _i, _vp, _vp, _sz, _vp],
     "cdml_rope_table": [_vp, _i, _i, _f, _vp],
     "cdml_project_qkv_rope": [_vp] * 10 + [_i, _i, _i, _i, _vp, _i, _i, _i, _vp],
     "cdml_sdpa_fwd": [_vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, _vp],

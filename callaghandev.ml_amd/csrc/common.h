@@ -54,4 +54,12 @@ __device__ __forceinline__ floatx16 mfma32x32x2(float a, float b, floatx16 c) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// The forward attention launcher (flash_attn.hip) for callers that have
+// validated their arguments.  With lse non-NULL it also writes each row's
+// log2 softmax normaliser ([batch * heads][lq]; head dims up to 128).
+// causal: key j is visible to query i iff j <= i (lq may differ from lk).
+int flash_forward(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv,
+                  float *o, int ldo, float *lse, int batch, int lq, int lk, int dim, int num_heads,
+                  float scale, bool causal, const uint8_t *mask, hipStream_t st);
+
 }  // namespace cdml

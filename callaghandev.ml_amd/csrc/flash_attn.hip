@@ -37,6 +37,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 struct FlashArgs {
   const float *q, *k, *v;
   float *o;
+  float *lse;  // optional [batch * heads][lq]: log2 of each row's softmax normaliser
   const uint8_t *mask;
   int ldq, ldk, ldv, ldo;
   int lq, lk, heads, hd;
@@ -262,7 +263,7 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArg
         for (int r = 0; r < 16; ++r) sacc[r] *= a.scale_log2;
       }
       // Masking (wave-uniform decision): the diagonal, the sequence end, a mask.
-      if (HAS_MASK || kb0 + 31 > (CAUSAL ? qw0 : a.lk - 1)) {
+      if (HAS_MASK || kb0 + 31 > (CAUSAL ? min(qw0, a.lk - 1) : a.lk - 1)) {
         const int thr = key_last - kb0 - 4 * hf;  // last visible offset for this lane
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -329,6 +330,10 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArg
   // Normalise and store: lane holds query qi, dims db*32 + 8*(r/4) + 4*hf + r%4.
   const float l_tot = halves_sum(l_a + l_b);
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  // For the backward pass: p = exp2(s * scale * log2(e) - lse) recovers every
+  // probability (+inf for a row with no visible key, whose p are all 0).
+  if (a.lse && hf == 0 && qi < a.lq)
+    a.lse[(size_t)bh * a.lq + qi] = l_tot > 0.f ? m_run + __log2f(l_tot) : INFINITY;
   if (qi < a.lq) {
     float *orow = a.o + ((size_t)b * a.lq + qi) * a.ldo + col0;
 #pragma unroll
@@ -436,6 +441,55 @@ void launch_hd(const FlashArgs &a, bool causal, bool vec, hipStream_t st) {
 
 using namespace cdml;
 
+namespace cdml {
+
+// Launches the forward kernels; the arguments are validated by the caller.
+// causal here admits lq != lk (key j visible to query i iff j <= i).
+int flash_forward(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv,
+                  float *o, int ldo, float *lse, int batch, int lq, int lk, int dim, int num_heads,
+                  float scale, bool causal, const uint8_t *mask, hipStream_t st) {
+  FlashArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.lse = lse;
+  a.mask = mask;
+  a.ldq = ldq;
+  a.ldk = ldk;
+  a.ldv = ldv;
+  a.ldo = ldo;
+  a.lq = lq;
+  a.lk = lk;
+  a.heads = num_heads;
+  a.hd = dim / num_heads;
+  a.scale_log2 = scale * kLog2e;
+
+  const int hd = a.hd;
+  if (hd > 128) {
+    if (lse) return fail(CDML_E_INVALID, "flash_forward: no row statistics above head dim 128");
+    a.n_qt = lq;
+    size_t smem = sizeof(float) * (2 * (size_t)hd + 256 + 8);
+    if (smem > 160 * 1024) return fail(CDML_E_INVALID, "cdml_sdpa_fwd: head dim %d too large", hd);
+    flash_generic_kernel<<<dim3(batch * lq, num_heads), dim3(256), smem, st>>>(a, causal);
+    return check_launch("flash_generic_kernel");
+  }
+  const int hd_pad = hd <= 32 ? 32 : (hd <= 64 ? 64 : 128);
+  const bool vec = hd == hd_pad && ldq % 4 == 0 && ldk % 4 == 0 && ldv % 4 == 0 && ldo % 4 == 0 &&
+                   aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
+  a.n_qt = (lq + FA_BM - 1) / FA_BM;
+  long long total = (long long)batch * num_heads * a.n_qt;
+  if (total > (1LL << 30)) return fail(CDML_E_INVALID, "cdml_sdpa_fwd: problem too large");
+  a.total = (int)total;
+  a.padded = pad_to_xcd(a.total);
+  if (hd_pad == 32) launch_hd<32, 64>(a, causal, vec, st);
+  else if (hd_pad == 64) launch_hd<64, 32>(a, causal, vec, st);
+  else launch_hd<128, 32>(a, causal, vec, st);
+  return check_launch("flash_fwd_kernel");
+}
+
+}  // namespace cdml
+
 extern "C" int cdml_sdpa_fwd(const float *q, int ldq, const float *k, int ldk, const float *v,
                              int ldv, float *o, int ldo, int batch, int lq, int lk, int dim,
                              int num_heads, float scale, int causal, const uint8_t *mask,
@@ -456,42 +510,6 @@ extern "C" int cdml_sdpa_fwd(const float *q, int ldq, const float *k, int ldk, c
   if (!q || !k || !v || !o) return fail(CDML_E_INVALID, "cdml_sdpa_fwd: NULL pointer");
   int rc = ensure_device();
   if (rc) return rc;
-
-  FlashArgs a{};
-  a.q = q;
-  a.k = k;
-  a.v = v;
-  a.o = o;
-  a.mask = mask;
-  a.ldq = ldq;
-  a.ldk = ldk;
-  a.ldv = ldv;
-  a.ldo = ldo;
-  a.lq = lq;
-  a.lk = lk;
-  a.heads = num_heads;
-  a.hd = dim / num_heads;
-  a.scale_log2 = scale * kLog2e;
-  hipStream_t st = as_hip(stream);
-
-  const int hd = a.hd;
-  if (hd > 128) {
-    a.n_qt = lq;
-    size_t smem = sizeof(float) * (2 * (size_t)hd + 256 + 8);
-    if (smem > 160 * 1024) return fail(CDML_E_INVALID, "cdml_sdpa_fwd: head dim %d too large", hd);
-    flash_generic_kernel<<<dim3(batch * lq, num_heads), dim3(256), smem, st>>>(a, causal);
-    return check_launch("flash_generic_kernel");
-  }
-  const int hd_pad = hd <= 32 ? 32 : (hd <= 64 ? 64 : 128);
-  const bool vec = hd == hd_pad && ldq % 4 == 0 && ldk % 4 == 0 && ldv % 4 == 0 && ldo % 4 == 0 &&
-                   aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
-  a.n_qt = (lq + FA_BM - 1) / FA_BM;
-  long long total = (long long)batch * num_heads * a.n_qt;
-  if (total > (1LL << 30)) return fail(CDML_E_INVALID, "cdml_sdpa_fwd: problem too large");
-  a.total = (int)total;
-  a.padded = pad_to_xcd(a.total);
-  if (hd_pad == 32) launch_hd<32, 64>(a, causal, vec, st);
-  else if (hd_pad == 64) launch_hd<64, 32>(a, causal, vec, st);
-  else launch_hd<128, 32>(a, causal, vec, st);
-  return check_launch("flash_fwd_kernel");
+  return flash_forward(q, ldq, k, ldk, v, ldv, o, ldo, nullptr, batch, lq, lk, dim, num_heads, scale,
+                       causal != 0, mask, as_hip(stream));
 }

@@ -1,0 +1,690 @@
+// Attention backward for gfx950: MultiHeadAttentionBackward of the reference
+// (AccelerationCPU.cs:1011-1280) on fp32 MFMA.
+//
+// With P = softmax(S), S = scale * Q K^T per (sequence, head) under the
+// causal rule (key j visible to query i iff j <= i) and/or a mask:
+//   dV = P^T dO,  dP = dO V^T,  dS = P (dP - D) with D_i = sum_j P_ij dP_ij,
+//   dQ = scale dS K,  dK = scale dS^T Q.
+// D_i equals dO_i . O_i, so the pass runs in four launches:
+//   1. the forward kernel with row statistics: O and lse_i (log2 of the
+//      softmax normaliser), so that P_ij = exp2(s_ij * scale * log2 e - lse_i);
+//   2. bwd_delta_kernel: D = rowsum(dO * O) per head;
+//   3. flash_bwd_dkdv_kernel, key-block major: a workgroup owns 128 keys of
+//      one (sequence, head), each wave 32 keys whose K and V rows stay in
+//      registers; Q, dO, lse and D tiles stream through double-buffered LDS.
+//      Per 32-query sub-block: S = Q K^T and dP = dO V^T land with one key
+//      per lane and 16 queries per lane in registers, exactly the B operand
+//      layout that dV^T += dO^T P and dK^T += Q^T dS need, so P and dS are
+//      consumed in place;
+//   4. flash_bwd_dq_kernel, query-block major like the forward: S^T = K Q^T
+//      and dP^T = V dO^T put one query per lane, dS^T is consumed in place by
+//      dQ^T += K^T dS^T.
+// Every output element is written by one lane of one workgroup: no atomics,
+// and the result is the same on every run.  Head dims other than 32, 64 and
+// 128 (or unaligned strides) take flash_bwd_generic_kernel, which follows the
+// reference's per-row loops.
+#include "common.h"
+
+namespace cdml {
+namespace {
+
+constexpr int BW_THREADS = 256;
+constexpr int BW_TILE = 128;  // keys (dK/dV) or queries (dQ) per workgroup
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct BwdArgs {
+  const float *q, *k, *v, *dout;
+  float *dq, *dk, *dv;
+  const float *o;      // forward output [batch * lq][dim] (row stride dim)
+  const float *lse;    // [batch * heads][lq]
+  float *delta;        // [batch * heads][lq]
+  const uint8_t *mask; // [lq][lk] or NULL
+  int ldq, ldk, ldv, lddo, lddq, lddk, lddv;
+  int batch, lq, lk, dim, heads, hd;
+  float scale, scale_log2;
+  int n_tiles, total;
+};
+
+// Offset of accumulator register r's row inside its 32-row block for a lane of
+// half-wave h: 8 * (r / 4) + 4 * h + r % 4 (the 32x32 MFMA D layout).
+__device__ __forceinline__ constexpr int acc_row(int r) { return 8 * (r >> 2) + (r & 3); }
+
+// One ROWS x HD tile of a row-major matrix (rows [row0, row0 + ROWS) of the
+// head's column block), global -> registers -> LDS.  Each thread's offsets
+// inside a tile are fixed; rows past `nrows` are clamped to the last row
+// (their contributions are masked or never stored).
+template <int HD, int ROWS>
+struct RowStage {
+  static constexpr int F4 = HD / 4;
+  static constexpr int RPP = BW_THREADS / F4;
+  static constexpr int NV = ROWS / RPP;
+  static_assert(NV >= 1 && ROWS % RPP == 0, "tile shape");
+  vf4 r[NV];
+  uint32_t off[NV];
+  int col;
+
+  __device__ __forceinline__ void init(int ld) {
+    const int t = threadIdx.x;
+    col = (t % F4) * 4;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) off[i] = (uint32_t)((t / F4 + RPP * i) * ld + col);
+  }
+  __device__ __forceinline__ void load(const float *__restrict__ base, int ld, int row0, int nrows) {
+    const float *tile = base + (size_t)row0 * ld;
+    const uint32_t lim = (uint32_t)(min(nrows - 1 - row0, ROWS - 1) * ld) + col;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) r[i] = *reinterpret_cast<const vf4 *>(tile + min(off[i], lim));
+  }
+  __device__ __forceinline__ void store(float (*lds)[HD + 4]) const {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) *reinterpret_cast<vf4 *>(&lds[t / F4 + RPP * i][col]) = r[i];
+  }
+};
+
+// D[b, h, i] = dO_i . O_i over head h's columns; one thread per (row, head).
+__global__ void __launch_bounds__(256) bwd_delta_kernel(const BwdArgs a, bool vec) {
+  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (long long)a.batch * a.lq * a.heads) return;
+  const int h = (int)(idx % a.heads);
+  const long long row = idx / a.heads;  // b * lq + i
+  const float *g = a.dout + row * a.lddo + (size_t)h * a.hd;
+  const float *o = a.o + row * a.dim + (size_t)h * a.hd;
+  float s = 0.f;
+  if (vec) {
+    for (int d = 0; d < a.hd; d += 4) {
+      const vf4 x = *reinterpret_cast<const vf4 *>(g + d), y = *reinterpret_cast<const vf4 *>(o + d);
+      s += x[0] * y[0] + x[1] * y[1] + x[2] * y[2] + x[3] * y[3];
+    }
+  } else {
+    for (int d = 0; d < a.hd; ++d) s += g[d] * o[d];
+  }
+  const int b = (int)(row / a.lq), i = (int)(row % a.lq);
+  a.delta[((size_t)b * a.heads + h) * a.lq + i] = s;
+}
+
+// dK and dV.  Workgroup i takes (sequence, head) i % n_bh and key tile
+// i / n_bh: under the causal rule the first key tiles are seen by the most
+// queries, so the heaviest tiles go out first on every XCD.
+template <int HD, int BQ, bool CAUSAL, bool HAS_MASK>
+__global__ void __launch_bounds__(BW_THREADS, HD <= 64 ? 2 : 1) flash_bwd_dkdv_kernel(const BwdArgs a) {
+  constexpr int NQB = BQ / 32;  // 32-query sub-blocks per tile
+  constexpr int NDB = HD / 32;  // 32-wide head-dim blocks of dK^T / dV^T
+  constexpr int NKG = HD / 8;   // 8-dim groups of the Q.K and dO.V products
+  __shared__ __attribute__((aligned(16))) float Qs[2][BQ][HD + 4];
+  __shared__ __attribute__((aligned(16))) float Gs[2][BQ][HD + 4];  // dO
+  __shared__ __attribute__((aligned(16))) float Ls[2][BQ];          // lse
+  __shared__ __attribute__((aligned(16))) float Ds[2][BQ];          // D
+
+  const int n_bh = a.batch * a.heads;
+  const int bh = blockIdx.x % n_bh, kt = blockIdx.x / n_bh;
+  const int b = bh / a.heads, h = bh % a.heads;
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int li = lane & 31, hf = lane >> 5;
+  const int k0 = kt * BW_TILE;
+  const int kw0 = k0 + wave * 32;  // first key of this wave
+  const int key = kw0 + li;        // this lane's key
+  const int col0 = h * HD;
+
+  // B operands of S = Q K^T and dP = dO V^T: register 4u + r holds
+  // K[key][8u + 4*hf + r] (and likewise V), fixed for the whole loop.
+  float kreg[HD / 2], vreg[HD / 2];
+  {
+    const int kr = min(key, a.lk - 1);
+    const float *krow = a.k + ((size_t)b * a.lk + kr) * a.ldk + col0;
+    const float *vrow = a.v + ((size_t)b * a.lk + kr) * a.ldv + col0;
+#pragma unroll
+    for (int u = 0; u < NKG; ++u) {
+      const vf4 x = *reinterpret_cast<const vf4 *>(krow + 8 * u + 4 * hf);
+      const vf4 y = *reinterpret_cast<const vf4 *>(vrow + 8 * u + 4 * hf);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        kreg[4 * u + r] = x[r];
+        vreg[4 * u + r] = y[r];
+      }
+    }
+  }
+
+  const int q_begin = CAUSAL ? k0 : 0;  // queries before k0 see none of these keys
+  const int n_it = q_begin < a.lq ? (a.lq - q_begin + BQ - 1) / BQ : 0;
+  const float *__restrict__ qbase = a.q + (size_t)b * a.lq * a.ldq + col0;
+  const float *__restrict__ gbase = a.dout + (size_t)b * a.lq * a.lddo + col0;
+  const float *__restrict__ lse = a.lse + (size_t)bh * a.lq;
+  const float *__restrict__ dlt = a.delta + (size_t)bh * a.lq;
+
+  floatx16 dk[NDB], dv[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dk[db][r] = dv[db][r] = 0.f;
+  const floatx16 zero = {};
+
+  RowStage<HD, BQ> sq, sg;
+  sq.init(a.ldq);
+  sg.init(a.lddo);
+  float lreg = 0.f, dreg = 0.f;
+  if (n_it > 0) {
+    sq.load(qbase, a.ldq, q_begin, a.lq);
+    sg.load(gbase, a.lddo, q_begin, a.lq);
+    if (t < BQ) {
+      const int qq = min(q_begin + t, a.lq - 1);
+      lreg = lse[qq];
+      dreg = dlt[qq];
+    }
+    sq.store(Qs[0]);
+    sg.store(Gs[0]);
+    if (t < BQ) {
+      Ls[0][t] = lreg;
+      Ds[0][t] = dreg;
+    }
+  }
+  __syncthreads();
+
+  for (int it = 0; it < n_it; ++it) {
+    const int cur = it & 1;
+    const int qt0 = q_begin + it * BQ;
+    // Next tile into registers; the last iteration re-stages its own tile
+    // into the idle buffer (an unconditional stage keeps the registers out
+    // of scratch memory).
+    const int nxt = it + 1 < n_it ? qt0 + BQ : qt0;
+    sq.load(qbase, a.ldq, nxt, a.lq);
+    sg.load(gbase, a.lddo, nxt, a.lq);
+    if (t < BQ) {
+      const int qq = min(nxt + t, a.lq - 1);
+      lreg = lse[qq];
+      dreg = dlt[qq];
+    }
+
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+      const int qb0 = qt0 + qb * 32;
+      // Sub-blocks past the sequence end or wholly before this wave's keys
+      // contribute nothing.
+      if (qb0 >= a.lq || (CAUSAL && qb0 + 31 < kw0)) continue;
+      const float(*qrow)[HD + 4] = &Qs[cur][qb * 32];
+      const float(*grow)[HD + 4] = &Gs[cur][qb * 32];
+
+      // S = Q K^T and dP = dO V^T (two independent MFMA chains).
+      floatx16 s, dp;
+      vf4 qa = *reinterpret_cast<const vf4 *>(&qrow[li][4 * hf]);
+      vf4 ga = *reinterpret_cast<const vf4 *>(&grow[li][4 * hf]);
+#pragma unroll
+      for (int u = 0; u < NKG; ++u) {
+        vf4 qn, gn;
+        if (u + 1 < NKG) {
+          qn = *reinterpret_cast<const vf4 *>(&qrow[li][8 * (u + 1) + 4 * hf]);
+          gn = *reinterpret_cast<const vf4 *>(&grow[li][8 * (u + 1) + 4 * hf]);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          s = mfma32x32x2(qa[r], kreg[4 * u + r], (u == 0 && r == 0) ? zero : s);
+          dp = mfma32x32x2(ga[r], vreg[4 * u + r], (u == 0 && r == 0) ? zero : dp);
+        }
+        if (u + 1 < NKG) {
+          qa = qn;
+          ga = gn;
+        }
+      }
+
+      // P = exp2(S * scale * log2 e - lse) and dS = P (dP - D), per query row
+      // 8g + 4*hf + c of the sub-block (registers 4g + c).
+      const bool need = HAS_MASK || (CAUSAL && qb0 < kw0 + 31) || qb0 + 31 >= a.lq;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const vf4 l4 = *reinterpret_cast<const vf4 *>(&Ls[cur][qb * 32 + 8 * g + 4 * hf]);
+        const vf4 d4 = *reinterpret_cast<const vf4 *>(&Ds[cur][qb * 32 + 8 * g + 4 * hf]);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int r = 4 * g + c;
+          float p = fast_exp2(fmaf(s[r], a.scale_log2, -l4[c]));
+          if (need) {
+            const int qq = qb0 + 8 * g + 4 * hf + c;
+            bool ok = qq < a.lq;
+            if (CAUSAL) ok = ok && key <= qq;
+            if (HAS_MASK) ok = ok && key < a.lk && a.mask[(size_t)min(qq, a.lq - 1) * a.lk + min(key, a.lk - 1)];
+            p = ok ? p : 0.f;
+          }
+          s[r] = p;
+          dp[r] = p * (dp[r] - d4[c]);
+        }
+      }
+
+      // dV^T += dO^T P and dK^T += Q^T dS: MFMA step st pairs query rows
+      // acc_row(st) (half 0) and acc_row(st) + 4 (half 1), the rows held by
+      // register st of P and dS.
+#pragma unroll
+      for (int st = 0; st < 16; ++st) {
+        const int qr = acc_row(st) + 4 * hf;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          dv[db] = mfma32x32x2(grow[qr][db * 32 + li], s[st], dv[db]);
+          dk[db] = mfma32x32x2(qrow[qr][db * 32 + li], dp[st], dk[db]);
+        }
+      }
+    }
+
+    sq.store(Qs[cur ^ 1]);
+    sg.store(Gs[cur ^ 1]);
+    if (t < BQ) {
+      Ls[cur ^ 1][t] = lreg;
+      Ds[cur ^ 1][t] = dreg;
+    }
+    __syncthreads();
+  }
+
+  // Lane li holds key `key`: register 4g + c of block db is dimension
+  // db*32 + 8g + 4*hf + c.
+  if (key < a.lk) {
+    float *dkrow = a.dk + ((size_t)b * a.lk + key) * a.lddk + col0;
+    float *dvrow = a.dv + ((size_t)b * a.lk + key) * a.lddv + col0;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = db * 32 + 8 * g + 4 * hf;
+        vf4 x, y;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          x[c] = dk[db][4 * g + c] * a.scale;
+          y[c] = dv[db][4 * g + c];
+        }
+        *reinterpret_cast<vf4 *>(dkrow + d) = x;
+        *reinterpret_cast<vf4 *>(dvrow + d) = y;
+      }
+    }
+  }
+}
+
+// dQ.  Query-tile major with the heaviest causal tiles first, as the forward.
+template <int HD, int BN, bool CAUSAL, bool HAS_MASK>
+__global__ void __launch_bounds__(BW_THREADS, 2) flash_bwd_dq_kernel(const BwdArgs a) {
+  constexpr int NKB = BN / 32;
+  constexpr int NDB = HD / 32;
+  constexpr int NKG = HD / 8;
+  __shared__ __attribute__((aligned(16))) float Ks[2][BN][HD + 4];
+  __shared__ __attribute__((aligned(16))) float Vs[2][BN][HD + 4];
+
+  const int n_bh = a.batch * a.heads;
+  const int bh = blockIdx.x % n_bh;
+  int qt = blockIdx.x / n_bh;
+  if (CAUSAL) qt = a.n_tiles - 1 - qt;
+  const int b = bh / a.heads, h = bh % a.heads;
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int li = lane & 31, hf = lane >> 5;
+  const int q0 = qt * BW_TILE;
+  const int qw0 = q0 + wave * 32;
+  const int qi = qw0 + li;
+  const int qc = min(qi, a.lq - 1);
+  const int col0 = h * HD;
+
+  // B operands of S^T = K Q^T and dP^T = V dO^T: register 4u + r holds
+  // Q[qi][8u + 4*hf + r] (and likewise dO).
+  float qreg[HD / 2], greg[HD / 2];
+  {
+    const float *qrow = a.q + ((size_t)b * a.lq + qc) * a.ldq + col0;
+    const float *grow = a.dout + ((size_t)b * a.lq + qc) * a.lddo + col0;
+#pragma unroll
+    for (int u = 0; u < NKG; ++u) {
+      const vf4 x = *reinterpret_cast<const vf4 *>(qrow + 8 * u + 4 * hf);
+      const vf4 y = *reinterpret_cast<const vf4 *>(grow + 8 * u + 4 * hf);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        qreg[4 * u + r] = x[r];
+        greg[4 * u + r] = y[r];
+      }
+    }
+  }
+  const float lse_q = a.lse[(size_t)bh * a.lq + qc];
+  const float d_q = a.delta[(size_t)bh * a.lq + qc];
+  const int key_last = CAUSAL ? min(qi, a.lk - 1) : a.lk - 1;
+  const uint8_t *mrow = HAS_MASK ? a.mask + (size_t)qc * a.lk : nullptr;
+
+  const int kend = CAUSAL ? min(q0 + BW_TILE, a.lk) : a.lk;
+  const int n_kt = (kend + BN - 1) / BN;
+  const float *__restrict__ kbase = a.k + (size_t)b * a.lk * a.ldk + col0;
+  const float *__restrict__ vbase = a.v + (size_t)b * a.lk * a.ldv + col0;
+
+  floatx16 dq[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[db][r] = 0.f;
+  const floatx16 zero = {};
+
+  RowStage<HD, BN> sk, sv;
+  sk.init(a.ldk);
+  sv.init(a.ldv);
+  sk.load(kbase, a.ldk, 0, a.lk);
+  sv.load(vbase, a.ldv, 0, a.lk);
+  sk.store(Ks[0]);
+  sv.store(Vs[0]);
+  __syncthreads();
+
+  for (int kt = 0; kt < n_kt; ++kt) {
+    const int cur = kt & 1;
+    const int k0 = kt * BN;
+    const int nxt = kt + 1 < n_kt ? k0 + BN : k0;
+    sk.load(kbase, a.ldk, nxt, a.lk);
+    sv.load(vbase, a.ldv, nxt, a.lk);
+
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const int kb0 = k0 + kb * 32;
+      if (kb0 >= a.lk || (CAUSAL && kb0 > qw0 + 31)) continue;
+      const float(*krow)[HD + 4] = &Ks[cur][kb * 32];
+      const float(*vrow)[HD + 4] = &Vs[cur][kb * 32];
+
+      // S^T = K Q^T and dP^T = V dO^T
+      floatx16 s, dp;
+      vf4 ka = *reinterpret_cast<const vf4 *>(&krow[li][4 * hf]);
+      vf4 va = *reinterpret_cast<const vf4 *>(&vrow[li][4 * hf]);
+#pragma unroll
+      for (int u = 0; u < NKG; ++u) {
+        vf4 kn, vn;
+        if (u + 1 < NKG) {
+          kn = *reinterpret_cast<const vf4 *>(&krow[li][8 * (u + 1) + 4 * hf]);
+          vn = *reinterpret_cast<const vf4 *>(&vrow[li][8 * (u + 1) + 4 * hf]);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          s = mfma32x32x2(ka[r], qreg[4 * u + r], (u == 0 && r == 0) ? zero : s);
+          dp = mfma32x32x2(va[r], greg[4 * u + r], (u == 0 && r == 0) ? zero : dp);
+        }
+        if (u + 1 < NKG) {
+          ka = kn;
+          va = vn;
+        }
+      }
+
+      // dS^T = P^T (dP^T - D); register r holds key kb0 + acc_row(r) + 4*hf.
+      const bool need = HAS_MASK || kb0 + 31 > (CAUSAL ? min(qw0, a.lk - 1) : a.lk - 1);
+      const int thr = key_last - kb0 - 4 * hf;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float p = fast_exp2(fmaf(s[r], a.scale_log2, -lse_q));
+        if (need) {
+          bool ok = acc_row(r) <= thr;
+          if (HAS_MASK) ok = ok && mrow[min(kb0 + acc_row(r) + 4 * hf, a.lk - 1)] != 0;
+          p = ok ? p : 0.f;
+        }
+        dp[r] = p * (dp[r] - d_q);
+      }
+
+      // dQ^T += K^T dS^T
+#pragma unroll
+      for (int st = 0; st < 16; ++st) {
+        const int kr = acc_row(st) + 4 * hf;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) dq[db] = mfma32x32x2(krow[kr][db * 32 + li], dp[st], dq[db]);
+      }
+    }
+
+    sk.store(Ks[cur ^ 1]);
+    sv.store(Vs[cur ^ 1]);
+    __syncthreads();
+  }
+
+  if (qi < a.lq) {
+    float *dqrow = a.dq + ((size_t)b * a.lq + qi) * a.lddq + col0;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        vf4 x;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) x[c] = dq[db][4 * g + c] * a.scale;
+        *reinterpret_cast<vf4 *>(dqrow + db * 32 + 8 * g + 4 * hf) = x;
+      }
+    }
+  }
+}
+
+// Any head dim, any strides: one workgroup per (sequence, head) walks the
+// queries in order, as AccelerationCPU.cs:1092-1268 does per head, with the
+// keys spread over the threads.  scratch holds two floats per key.
+__global__ void __launch_bounds__(256) flash_bwd_generic_kernel(const BwdArgs a, float *scratch,
+                                                                 int causal) {
+  extern __shared__ float sm[];  // q_i[hd] | dout_i[hd] | red[8]
+  float *qv = sm, *gv = sm + a.hd, *red = sm + 2 * a.hd;
+  const int bh = blockIdx.x;
+  const int b = bh / a.heads, h = bh % a.heads;
+  const int t = threadIdx.x, hd = a.hd, col0 = h * hd;
+  float *w = scratch + (size_t)bh * 2 * a.lk;
+  float *da = w + a.lk;
+  const float *K = a.k + (size_t)b * a.lk * a.ldk + col0;
+  const float *V = a.v + (size_t)b * a.lk * a.ldv + col0;
+  float *dK = a.dk + (size_t)b * a.lk * a.lddk + col0;
+  float *dV = a.dv + (size_t)b * a.lk * a.lddv + col0;
+  for (int j = t; j < a.lk; j += 256)
+    for (int d = 0; d < hd; ++d) dK[(size_t)j * a.lddk + d] = dV[(size_t)j * a.lddv + d] = 0.f;
+
+  auto block_max = [&](float x) {
+    for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
+    __syncthreads();
+    if ((t & 63) == 0) red[t >> 6] = x;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  };
+  auto block_sum = [&](float x) {
+    for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
+    __syncthreads();
+    if ((t & 63) == 0) red[t >> 6] = x;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+  };
+
+  for (int i = 0; i < a.lq; ++i) {
+    const float *qrow = a.q + ((size_t)b * a.lq + i) * a.ldq + col0;
+    const float *grow = a.dout + ((size_t)b * a.lq + i) * a.lddo + col0;
+    float *dqrow = a.dq + ((size_t)b * a.lq + i) * a.lddq + col0;
+    __syncthreads();
+    for (int d = t; d < hd; d += 256) {
+      qv[d] = qrow[d];
+      gv[d] = grow[d];
+    }
+    __syncthreads();
+    const int visible = causal ? min(i + 1, a.lk) : a.lk;
+    float mx = -INFINITY;
+    for (int j = t; j < visible; j += 256) {
+      float s = -INFINITY;
+      if (!a.mask || a.mask[(size_t)i * a.lk + j]) {
+        float acc = 0.f;
+        for (int d = 0; d < hd; ++d) acc += qv[d] * K[(size_t)j * a.ldk + d];
+        s = acc * a.scale;
+      }
+      w[j] = s;
+      mx = fmaxf(mx, s);
+    }
+    mx = block_max(mx);
+    float sum = 0.f;
+    if (mx != -INFINITY) {
+      for (int j = t; j < visible; j += 256) {
+        const float e = w[j] == -INFINITY ? 0.f : expf(w[j] - mx);
+        w[j] = e;
+        sum += e;
+      }
+    }
+    sum = block_sum(sum);
+    if (!(mx != -INFINITY && sum > 0.f)) {  // the row contributes nothing
+      for (int d = t; d < hd; d += 256) dqrow[d] = 0.f;
+      continue;
+    }
+    const float inv = 1.0f / sum;
+    float rd = 0.f;
+    for (int j = t; j < visible; j += 256) {
+      const float wj = w[j] * inv;
+      float g = 0.f;
+      for (int d = 0; d < hd; ++d) g += gv[d] * V[(size_t)j * a.ldv + d];
+      w[j] = wj;
+      da[j] = g;
+      rd += wj * g;
+    }
+    rd = block_sum(rd);
+    for (int j = t; j < visible; j += 256) {
+      const float wj = w[j];
+      const float dd = wj * (da[j] - rd) * a.scale;
+      for (int d = 0; d < hd; ++d) {
+        dV[(size_t)j * a.lddv + d] += wj * gv[d];
+        if (dd != 0.f) dK[(size_t)j * a.lddk + d] += dd * qv[d];
+      }
+      da[j] = dd;
+    }
+    __syncthreads();
+    for (int d = t; d < hd; d += 256) {
+      float acc = 0.f;
+      for (int j = 0; j < visible; ++j) acc += da[j] * K[(size_t)j * a.ldk + d];
+      dqrow[d] = acc;
+    }
+  }
+}
+
+// rows x cols block (row stride ld) set to zero.
+__global__ void __launch_bounds__(256) zero_rows_kernel(float *p, long long rows, int cols, int ld) {
+  const long long n = rows * cols;
+  for (long long e = (long long)blockIdx.x * 256 + threadIdx.x; e < n; e += (long long)gridDim.x * 256)
+    p[(e / cols) * ld + e % cols] = 0.f;
+}
+
+int zero_rows(float *p, long long rows, int cols, int ld, hipStream_t st) {
+  if (rows <= 0 || cols <= 0) return CDML_OK;
+  const long long n = rows * cols;
+  zero_rows_kernel<<<dim3((unsigned)std::min<long long>((n + 255) / 256, 16384)), dim3(256), 0, st>>>(
+      p, rows, cols, ld);
+  return check_launch("zero_rows_kernel");
+}
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+template <int HD, int BQ, int BN, bool CAUSAL, bool HAS_MASK>
+void launch_bwd(BwdArgs &a, hipStream_t st) {
+  const int n_bh = a.batch * a.heads;
+  const int kt = (a.lk + BW_TILE - 1) / BW_TILE;
+  flash_bwd_dkdv_kernel<HD, BQ, CAUSAL, HAS_MASK><<<dim3(n_bh * kt), dim3(BW_THREADS), 0, st>>>(a);
+  a.n_tiles = (a.lq + BW_TILE - 1) / BW_TILE;
+  flash_bwd_dq_kernel<HD, BN, CAUSAL, HAS_MASK><<<dim3(n_bh * a.n_tiles), dim3(BW_THREADS), 0, st>>>(a);
+}
+
+template <int HD, int BQ, int BN>
+void launch_bwd_hd(BwdArgs &a, bool causal, hipStream_t st) {
+  if (causal) {
+    if (a.mask) launch_bwd<HD, BQ, BN, true, true>(a, st);
+    else launch_bwd<HD, BQ, BN, true, false>(a, st);
+  } else {
+    if (a.mask) launch_bwd<HD, BQ, BN, false, true>(a, st);
+    else launch_bwd<HD, BQ, BN, false, false>(a, st);
+  }
+}
+
+}  // namespace
+}  // namespace cdml
+
+using namespace cdml;
+
+extern "C" int cdml_sdpa_bwd_workspace_size(int batch, int lq, int lk, int dim, int num_heads,
+                                            size_t *bytes) {
+  if (!bytes) return fail(CDML_E_INVALID, "cdml_sdpa_bwd_workspace_size: bytes is NULL");
+  if (batch < 0 || lq < 0 || lk < 0 || dim <= 0 || num_heads <= 0 || dim % num_heads)
+    return fail(CDML_E_INVALID, "cdml_sdpa_bwd_workspace_size: bad size");
+  const size_t f = sizeof(float), bh = (size_t)batch * num_heads;
+  // O | lse | D | two floats per key for the generic kernel
+  *bytes = align256(f * (size_t)batch * lq * dim) + 2 * align256(f * bh * lq) + align256(f * 2 * bh * lk);
+  return CDML_OK;
+}
+
+extern "C" int cdml_sdpa_bwd(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv,
+                             const float *dout, int lddo, float *dq, int lddq, float *dk, int lddk,
+                             float *dv, int lddv, int batch, int lq, int lk, int dim, int num_heads,
+                             float scale, int causal, const uint8_t *mask, void *workspace,
+                             size_t workspace_bytes, cdml_stream stream) {
+  size_t need = 0;
+  int rc = cdml_sdpa_bwd_workspace_size(batch, lq, lk, dim, num_heads, &need);
+  if (rc) return rc;
+  if (ldq < dim || ldk < dim || ldv < dim || lddo < dim || lddq < dim || lddk < dim || lddv < dim)
+    return fail(CDML_E_INVALID, "cdml_sdpa_bwd: row stride smaller than dim");
+  if ((long long)ldq * 128 > INT32_MAX || (long long)ldk * 128 > INT32_MAX ||
+      (long long)ldv * 128 > INT32_MAX || (long long)lddo * 128 > INT32_MAX)
+    return fail(CDML_E_INVALID, "cdml_sdpa_bwd: row stride above %d elements", INT32_MAX / 128);
+  if (batch == 0 || (lq == 0 && lk == 0)) return CDML_OK;
+  if ((lq && (!dq || !q || !dout)) || (lk && (!dk || !dv || !k || !v)))
+    return fail(CDML_E_INVALID, "cdml_sdpa_bwd: NULL pointer");
+  rc = ensure_device();
+  if (rc) return rc;
+  hipStream_t st = as_hip(stream);
+  if (lq == 0 || lk == 0) {  // nothing attends: every gradient is 0
+    rc = zero_rows(dq, (long long)batch * lq, dim, lddq, st);
+    if (!rc) rc = zero_rows(dk, (long long)batch * lk, dim, lddk, st);
+    if (!rc) rc = zero_rows(dv, (long long)batch * lk, dim, lddv, st);
+    return rc;
+  }
+  if (!workspace || workspace_bytes < need)
+    return fail(CDML_E_INVALID, "cdml_sdpa_bwd: workspace of %zu bytes needed, %zu given", need,
+                workspace_bytes);
+  if ((long long)batch * num_heads * ((std::max(lq, lk) + BW_TILE - 1) / BW_TILE) > (1LL << 30))
+    return fail(CDML_E_INVALID, "cdml_sdpa_bwd: problem too large");
+
+  BwdArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.dout = dout;
+  a.dq = dq;
+  a.dk = dk;
+  a.dv = dv;
+  a.mask = mask;
+  a.ldq = ldq;
+  a.ldk = ldk;
+  a.ldv = ldv;
+  a.lddo = lddo;
+  a.lddq = lddq;
+  a.lddk = lddk;
+  a.lddv = lddv;
+  a.batch = batch;
+  a.lq = lq;
+  a.lk = lk;
+  a.dim = dim;
+  a.heads = num_heads;
+  a.hd = dim / num_heads;
+  a.scale = scale;
+  a.scale_log2 = scale * kLog2e;
+  char *ws = static_cast<char *>(workspace);
+  const size_t f = sizeof(float), bh = (size_t)batch * num_heads;
+  float *o = reinterpret_cast<float *>(ws);
+  float *lse = reinterpret_cast<float *>(ws + align256(f * (size_t)batch * lq * dim));
+  float *delta = reinterpret_cast<float *>(reinterpret_cast<char *>(lse) + align256(f * bh * lq));
+  float *scratch = reinterpret_cast<float *>(reinterpret_cast<char *>(delta) + align256(f * bh * lq));
+  a.o = o;
+  a.lse = lse;
+  a.delta = delta;
+
+  const int hd = a.hd;
+  const bool fast = (hd == 32 || hd == 64 || hd == 128) && ldq % 4 == 0 && ldk % 4 == 0 &&
+                    ldv % 4 == 0 && lddo % 4 == 0 && lddq % 4 == 0 && lddk % 4 == 0 &&
+                    lddv % 4 == 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
+                    aligned16(dout) && aligned16(dq) && aligned16(dk) && aligned16(dv);
+  if (!fast) {
+    const size_t smem = f * (2 * (size_t)hd + 8);
+    if (smem > 64 * 1024) return fail(CDML_E_INVALID, "cdml_sdpa_bwd: head dim %d too large", hd);
+    flash_bwd_generic_kernel<<<dim3((unsigned)bh), dim3(256), smem, st>>>(a, scratch, causal ? 1 : 0);
+    return check_launch("flash_bwd_generic_kernel");
+  }
+  // 1. O and the row statistics
+  rc = flash_forward(q, ldq, k, ldk, v, ldv, o, dim, lse, batch, lq, lk, dim, num_heads, scale,
+                     causal != 0, mask, st);
+  if (rc) return rc;
+  // 2. D = rowsum(dO * O)
+  {
+    const long long n = (long long)batch * lq * num_heads;
+    bwd_delta_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a, true);
+    rc = check_launch("bwd_delta_kernel");
+    if (rc) return rc;
+  }
+  // 3. dK, dV and 4. dQ
+  if (hd == 32) launch_bwd_hd<32, 64, 64>(a, causal != 0, st);
+  else if (hd == 64) launch_bwd_hd<64, 64, 32>(a, causal != 0, st);
+  else launch_bwd_hd<128, 32, 32>(a, causal != 0, st);
+  return check_launch("flash_bwd_dkdv_kernel / flash_bwd_dq_kernel");
+}

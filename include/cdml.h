@@ -211,6 +211,29 @@ int cdml_sdpa_fwd(const float *q, int ldq, const float *k, int ldk,
                   int lq, int lk, int dim, int num_heads, float scale,
                   int causal, const uint8_t *mask, cdml_stream stream);
 
+/* IAccelerationManager.MultiHeadAttentionBackward, both overloads (:161,
+ * :163), replacing AccelerationCPU.cs:1011-1280.  For `batch` independent
+ * sequences (the segmented trainer's SegmentedMultiHeadAttentionBackward,
+ * TransformerTrainer.cs:989-1060, is batch = segment count):
+ *   q, dout [batch, lq, ld*]; k, v [batch, lk, ld*]; dq [batch, lq, lddq];
+ *   dk, dv [batch, lk, ld*]; all three gradients are overwritten.
+ * Visible keys of query i: j <= i when causal (the useDecoderMask overload;
+ * lq may differ from lk), and mask[i*lk + j] != 0 when mask is non-NULL
+ * (the bool[,] overload).  scale is used as passed (the attention scores are
+ * q.k * scale).  A query with no visible key contributes nothing.
+ * `workspace`: device memory of cdml_sdpa_bwd_workspace_size() bytes.  Head
+ * dims 32, 64 and 128 with 16-byte aligned rows run on fp32 MFMA (a forward
+ * pass with row statistics, then dK/dV and dQ kernels, no atomics); other
+ * shapes run a per-row kernel. */
+int cdml_sdpa_bwd_workspace_size(int batch, int lq, int lk, int dim,
+                                 int num_heads, size_t *bytes);
+int cdml_sdpa_bwd(const float *q, int ldq, const float *k, int ldk,
+                  const float *v, int ldv, const float *dout, int lddo,
+                  float *dq, int lddq, float *dk, int lddk, float *dv,
+                  int lddv, int batch, int lq, int lk, int dim, int num_heads,
+                  float scale, int causal, const uint8_t *mask,
+                  void *workspace, size_t workspace_bytes, cdml_stream stream);
+
 /* Single-query decode attention over a cached K/V, the device form of the
  * inline loop in LanguageModel.DecoderSelfAttentionStep
  * (Transformers/MultiTypeTransformer/LanguageModel.cs:365-427), which has no

@@ -73,6 +73,23 @@ def linear(x, w, b, act=0):
     return down(y, (rows, out))
 
 
+def sdpa_bwd(q, k, v, dout, num_heads, scale, causal=False, mask=None, batch=1):
+    """cdml_sdpa_bwd on q/dout [batch*lq, D], k/v [batch*lk, D] -> (dq, dk, dv)."""
+    rows_q, dim = q.shape
+    rows_k = k.shape[0]
+    lq, lk = rows_q // batch, rows_k // batch
+    bq, bk, bv, bg = up(q), up(k), up(v), up(dout)
+    dq, dk, dv = (N.DeviceBuffer(max(4, n * dim * 4)) for n in (rows_q, rows_k, rows_k))
+    bm = up(mask, np.uint8) if mask is not None else None
+    ws = C.c_size_t(0)
+    N.check(N.lib().cdml_sdpa_bwd_workspace_size(batch, lq, lk, dim, num_heads, C.byref(ws)))
+    bws = N.DeviceBuffer(max(256, ws.value))
+    N.check(N.lib().cdml_sdpa_bwd(bq.ptr, dim, bk.ptr, dim, bv.ptr, dim, bg.ptr, dim, dq.ptr, dim, dk.ptr, dim,
+                                  dv.ptr, dim, batch, lq, lk, dim, num_heads, scale, int(causal),
+                                  bm.ptr if bm else None, bws.ptr, ws.value, stream().handle))
+    return down(dq, (rows_q, dim)), down(dk, (rows_k, dim)), down(dv, (rows_k, dim))
+
+
 def linear_backward(x, dy, w, wgrad, bgrad, dx=None, accumulate=False, want_dx=True):
     """cdml_linear_backward -> (wgrad, bgrad, dx) after the call (dx None when skipped)."""
     rows, ind = x.shape

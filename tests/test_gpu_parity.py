@@ -216,6 +216,91 @@ def test_linear_backward(rows, ind, out):
     parity(wg, ewg, "weightGrad without dX")
 
 
+# ------------------------------------------------------- attention backward
+@pytest.mark.parametrize("case", ["parity_decoder", "parity_mask", "nomask_6x8", "decoder_6x8", "cross_5x8"])
+def test_sdpa_bwd_reference_cases(case):
+    """MultiHeadAttentionBackward on the cases of AccelerationManagerParityTests.cs:354-383
+    (closed-form 4 x 6, 2 heads, scale 1/sqrt(3), decoder mask and explicit causal mask)
+    and AccelerationConsistencyTests.cs:964-1022 (6 x 8 and cross 5 x 8, 2 heads)."""
+    if case.startswith("parity"):
+        q, k, v, g = M(4, 6, 31), M(4, 6, 32), M(4, 6, 33), M(4, 6, 34)
+        heads, scale = 2, float(np.float32(1.0) / np.sqrt(np.float32(3.0)))
+    else:
+        lq, lk = (5, 8) if case == "cross_5x8" else (6, 6)
+        q, k, v = synth.normal(1, (lq, 8)), synth.normal(2, (lk, 8)), synth.normal(3, (lk, 8))
+        g = synth.normal(4, (lq, 8))
+        heads, scale = 2, 0.5
+    if case == "parity_mask":
+        mask = O.causal_mask(4)
+        got, want = G.sdpa_bwd(q, k, v, g, heads, scale, mask=mask), O.mha_backward(q, k, v, g, heads, scale, mask=mask)
+    else:
+        causal = "decoder" in case
+        got = G.sdpa_bwd(q, k, v, g, heads, scale, causal=causal)
+        want = O.mha_backward(q, k, v, g, heads, scale, use_decoder_mask=causal)
+    for a, e, n in zip(got, want, "QKV"):
+        parity(a, e, f"{case} d{n}")
+
+
+@pytest.mark.parametrize("b,lq,lk,dim,heads,causal,masked", [
+    (1, 256, 256, 128, 2, True, False),    # head dim 64, causal
+    (1, 1000, 1000, 128, 2, True, False),  # ragged causal
+    (2, 300, 700, 64, 2, False, False),    # head dim 32, cross attention, two sequences
+    (1, 200, 100, 64, 1, True, False),     # decoder mask with lq > lk
+    (1, 100, 200, 64, 1, True, False),     # decoder mask with lq < lk
+    (1, 257, 257, 128, 2, False, True),    # explicit mask
+    (1, 200, 200, 128, 2, True, True),     # mask and decoder rule together
+    (1, 300, 300, 256, 2, True, False),    # head dim 128
+    (3, 64, 64, 64, 4, True, False),       # segments (head dim 16: per-row kernel)
+    (1, 130, 130, 96, 2, True, False),     # head dim 48: per-row kernel
+])
+def test_sdpa_bwd_shapes(b, lq, lk, dim, heads, causal, masked):
+    hd = dim // heads
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    q, g = synth.normal(lq + dim, (b * lq, dim)), synth.normal(7, (b * lq, dim))
+    k, v = synth.normal(lk + 3, (b * lk, dim)), synth.normal(lk + 5, (b * lk, dim))
+    mask = (synth.normal(11, (lq, lk)) > -0.5).astype(np.uint8) if masked else None
+    if masked:
+        mask[lq // 3] = 0  # a row that sees no key
+    got = G.sdpa_bwd(q, k, v, g, heads, scale, causal=causal, mask=mask, batch=b)
+    # The reference's overloads take the decoder rule or a mask; the ABI
+    # composes them, which the oracle sees as the mask of both.
+    omask = mask * np.tril(np.ones((lq, lk), np.uint8)) if (masked and causal) else mask
+    for s in range(b):
+        qs, gs = slice(s * lq, (s + 1) * lq), slice(s * lk, (s + 1) * lk)
+        want = O.mha_backward(q[qs], k[gs], v[gs], g[qs], heads, scale, mask=omask,
+                              use_decoder_mask=causal and not masked)
+        for a, e, n in zip((got[0][qs], got[1][gs], got[2][gs]), want, "QKV"):
+            parity(a, e, f"seq {s} d{n} ({lq}x{lk}, hd {hd}, causal {causal}, mask {masked})")
+
+
+def _attention_bwd64(q, k, v, g, scale):
+    """float64 causal attention backward of one head by matrix algebra
+    (the identities pinned on the oracle by finite differences)."""
+    n = q.shape[0]
+    s = (q @ k.T) * scale
+    s[np.triu_indices(n, 1)] = -np.inf
+    p = np.exp(s - s.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    dp = g @ v.T
+    ds = p * (dp - (p * dp).sum(1, keepdims=True))
+    return (ds @ k) * scale, (ds.T @ q) * scale, p.T @ g
+
+
+def test_sdpa_bwd_c3_shape_sampled_heads():
+    """The c3 shape (4 x 4096, 16 heads of 64, causal) on the GPU; two
+    (sequence, head) pairs checked against float64."""
+    B, L, D, H = 4, 4096, 1024, 16
+    hd = D // H
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    q, k, v, g = (synth.normal(20 + i, (B * L, D)) for i in range(4))
+    dq, dk, dv = G.sdpa_bwd(q, k, v, g, H, scale, causal=True, batch=B)
+    for b, h in [(0, 0), (3, 13)]:
+        rows, cols = slice(b * L, (b + 1) * L), slice(h * hd, (h + 1) * hd)
+        want = _attention_bwd64(*(t[rows, cols].astype(np.float64) for t in (q, k, v, g)), scale)
+        for a, e, n in zip((dq, dk, dv), want, "QKV"):
+            parity(a[rows, cols], e, f"c3 (b {b}, h {h}) d{n}")
+
+
 # ------------------------------------------------------------------- SDPA
 def test_sdpa_reference_cases(ops_golden):
     g = ops_golden
