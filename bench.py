@@ -208,6 +208,76 @@ def bench_decode(N, st, steps, warmup):
     return dict(ms=float(np.mean(ms)), ms_min=float(np.min(ms)))
 
 
+def bench_mha_backward(N, st, steps, warmup, cfg=None):
+    """The c3 MHA layer backward as TransformerTrainer.BackpropAttention runs it
+    (TransformerTrainer.cs:933-987): BackpropLinearProjection of the output
+    projection, MultiHeadAttentionBackward with the decoder mask, the inverse
+    RoPE of dQ and dK, BackpropQKV.  Events around the attention-core kernels
+    (cdml_sdpa_bwd) and around the whole chain."""
+    lib = N.lib()
+    cfg = cfg or C3
+    B, L, D, H = cfg["batch"], cfg["seq"], cfg["dim"], cfg["heads"]
+    hd = D // H
+    rows = B * L
+    from cdml import synth
+
+    rng = np.random.default_rng(8)
+    bufs = {n: N.DeviceBuffer.from_array(rng.standard_normal((rows, D), dtype=np.float32), st)
+            for n in ("x", "q", "k", "v", "att", "dy")}
+    dw = [N.DeviceBuffer.from_array(synth.xavier_uniform(50 + i, D, D), st) for i in range(4)]
+    gw = [N.DeviceBuffer.from_array(np.zeros((D, D), np.float32), st) for _ in range(4)]
+    gb = [N.DeviceBuffer.from_array(np.zeros(D, np.float32), st) for _ in range(4)]
+    dcat, dq, dk, dv, dxin = (N.DeviceBuffer(rows * D * 4) for _ in range(5))
+    wsz, wsl, wsq = C.c_size_t(0), C.c_size_t(0), C.c_size_t(0)
+    N.check(lib.cdml_sdpa_bwd_workspace_size(B, L, L, D, H, C.byref(wsz)))
+    N.check(lib.cdml_linear_backward_workspace_size(rows, D, D, C.byref(wsl)))
+    N.check(lib.cdml_backprop_qkv_workspace_size(rows, D, D, C.byref(wsq)))
+    dws = N.DeviceBuffer(max(16, wsz.value))
+    dwsg = N.DeviceBuffer(max(16, wsl.value, wsq.value))
+    s = st.handle
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    b = bufs
+
+    def step(t_core=None):
+        N.check(lib.cdml_linear_backward(b["att"].ptr, D, b["dy"].ptr, D, dw[3].ptr, dcat.ptr, D, gw[3].ptr,
+                                         gb[3].ptr, rows, D, D, 0, dwsg.ptr, wsl.value, s))
+        if t_core:
+            t_core.start(st)
+        N.check(lib.cdml_sdpa_bwd(b["q"].ptr, D, b["k"].ptr, D, b["v"].ptr, D, dcat.ptr, D, dq.ptr, D,
+                                  dk.ptr, D, dv.ptr, D, B, L, L, D, H, scale, 1, None, dws.ptr, wsz.value, s))
+        if t_core:
+            t_core.stop(st)
+        for t in (dq, dk):
+            N.check(lib.cdml_rope(t.ptr, rows, D, 0, hd, H, 10000.0, 1, 0, L, None, s))
+        N.check(lib.cdml_backprop_qkv(b["x"].ptr, dq.ptr, dk.ptr, dv.ptr, dw[0].ptr, dw[1].ptr, dw[2].ptr,
+                                      gw[0].ptr, gb[0].ptr, gw[1].ptr, gb[1].ptr, gw[2].ptr, gb[2].ptr,
+                                      dxin.ptr, rows, D, D, dwsg.ptr, wsq.value, s))
+
+    for _ in range(warmup):
+        step()
+    st.synchronize()
+    tc = Timer(N, steps)
+    e0, e1 = N.Event(), N.Event()
+    e0.record(st)
+    for _ in range(steps):
+        step(tc)
+    e1.record(st)
+    st.synchronize()
+    g = dxin.download((rows, D), stream=st)
+    assert np.all(np.isfinite(g)), "non-finite MHA backward output"
+    core_ms = float(np.mean(tc.ms()))
+    step_ms = e0.elapsed_ms(e1) / steps
+    pairs = L * (L + 1) // 2
+    core_fl = 8 * B * H * hd * pairs          # dV = P^T dO, dP = dO V^T, dQ = dS K, dK = dS^T Q
+    proj_fl = 16 * rows * D * D               # out-proj dX + dW, and Q/K/V dX + dW
+    return {"ms": round(step_ms, 4), "tflops": round((core_fl + proj_fl) / (step_ms * 1e-3) / 1e12, 2),
+            "attention_core_ms": round(core_ms, 4),
+            "attention_core_tflops": round(core_fl / (core_ms * 1e-3) / 1e12, 2),
+            "attention_core_frac_of_fp32_mfma_peak": round(core_fl / (core_ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
+            "flop_count": "matmul FLOPs of the gradients only: 8 x head_dim per causal (query, key) pair "
+                          "for the core (no recompute counted), 4 x rows x D^2 per projection"}
+
+
 def extras(N, st):
     """End-to-end figures for the other BASELINE configs (device-resident,
     events on the engine's stream) and the PCIe-inclusive drop-in path."""
@@ -222,6 +292,8 @@ def extras(N, st):
     out["c2_mha_layer"] = {"ms": round(r["wall_s"] / 10 * 1e3, 4),
                            "tflops": round((core + qkv + o) / (r["wall_s"] / 10) / 1e12, 2),
                            "flash_ms": round(r["flash_ms"], 4)}
+    log("[bench] extras: c3 MHA layer backward")
+    out["c3_mha_layer_backward"] = bench_mha_backward(N, st, 5, 3)
     log("[bench] extras: c3 12-layer decoder stack")
     # c3: 12 post-LN decoder layers (MHA + FFN 4096 + 2 LayerNorms) on N(0,1) embeddings
     cfg3 = {"dim": 1024, "heads": 16, "layers": 12, "ff": 4096, "max_seq": 4096, "discrete": False,

@@ -64,8 +64,10 @@ SIGNATURES = {
     "cdml_project_qkv": [_vp] * 10 + [_i, _i, _i, _vp],
     "cdml_linear": [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
     "cdml_rope": [_vp, _i, _i, _i, _i, _i, _f, _i, _i, _i, _vp, _vp],
-    "cdml_linear_backward": [_vp, _i, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _vp],
-    "cdml_backprop_qkv": [_vp] * 14 + [_i, _i, _i, _vp],
+    "cdml_linear_backward_workspace_size": [_i, _i, _i, C.POINTER(_sz)],
+    "cdml_linear_backward": [_vp, _i, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp],
+    "cdml_backprop_qkv_workspace_size": [_i, _i, _i, C.POINTER(_sz)],
+    "cdml_backprop_qkv": [_vp] * 14 + [_i, _i, _i, _vp, _sz, _vp],
     "cdml_sdpa_bwd_workspace_size": [_i, _i, _i, _i, _i, C.POINTER(_sz)],
     "cdml_sdpa_bwd": [_vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i,
                       _i, _i, _i, _i, _i, _f, _i, _vp, _vp, _sz, _vp],

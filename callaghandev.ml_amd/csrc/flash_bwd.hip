@@ -83,24 +83,29 @@ struct RowStage {
 };
 
 // D[b, h, i] = dO_i . O_i over head h's columns; one thread per (row, head).
-__global__ void __launch_bounds__(256) bwd_delta_kernel(const BwdArgs a, bool vec) {
-  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (long long)a.batch * a.lq * a.heads) return;
-  const int h = (int)(idx % a.heads);
-  const long long row = idx / a.heads;  // b * lq + i
-  const float *g = a.dout + row * a.lddo + (size_t)h * a.hd;
-  const float *o = a.o + row * a.dim + (size_t)h * a.hd;
-  float s = 0.f;
-  if (vec) {
-    for (int d = 0; d < a.hd; d += 4) {
-      const vf4 x = *reinterpret_cast<const vf4 *>(g + d), y = *reinterpret_cast<const vf4 *>(o + d);
-      s += x[0] * y[0] + x[1] * y[1] + x[2] * y[2] + x[3] * y[3];
-    }
-  } else {
-    for (int d = 0; d < a.hd; ++d) s += g[d] * o[d];
+// D[b, h, i] = dO[b, i, head h] . O[b, i, head h].  Thread e owns float4 e of
+// the flat [batch * lq, dim / 4] view, so a wave reads whole rows (coalesced);
+// the HD / 4 consecutive lanes of one head sum their partials with xor
+// shuffles (HD / 4 divides 64, so a head never straddles two waves).
+template <int HD>
+__global__ void __launch_bounds__(256) bwd_delta_kernel(const BwdArgs a) {
+  constexpr int G = HD / 4;
+  const int d4 = a.dim >> 2;
+  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+  const long long n = (long long)a.batch * a.lq * d4;
+  const long long ec = e < n ? e : n - 1;  // every lane joins the shuffles
+  const long long row = ec / d4;
+  const int c4 = (int)(ec % d4);
+  const vf4 x = *reinterpret_cast<const vf4 *>(a.dout + row * a.lddo + 4 * c4);
+  const vf4 y = *reinterpret_cast<const vf4 *>(a.o + row * a.dim + 4 * c4);
+  float s = (x[0] * y[0] + x[1] * y[1]) + (x[2] * y[2] + x[3] * y[3]);
+#pragma unroll
+  for (int off = G / 2; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+  if (e < n && c4 % G == 0) {
+    const int h = c4 / G;
+    const int b = (int)(row / a.lq), i = (int)(row % a.lq);
+    a.delta[((size_t)b * a.heads + h) * a.lq + i] = s;
   }
-  const int b = (int)(row / a.lq), i = (int)(row % a.lq);
-  a.delta[((size_t)b * a.heads + h) * a.lq + i] = s;
 }
 
 // dK and dV.  Workgroup i takes (sequence, head) i % n_bh and key tile
@@ -677,8 +682,11 @@ extern "C" int cdml_sdpa_bwd(const float *q, int ldq, const float *k, int ldk, c
   if (rc) return rc;
   // 2. D = rowsum(dO * O)
   {
-    const long long n = (long long)batch * lq * num_heads;
-    bwd_delta_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a, true);
+    const long long n = (long long)batch * lq * (dim / 4);
+    const dim3 grid((unsigned)((n + 255) / 256));
+    if (hd == 32) bwd_delta_kernel<32><<<grid, dim3(256), 0, st>>>(a);
+    else if (hd == 64) bwd_delta_kernel<64><<<grid, dim3(256), 0, st>>>(a);
+    else bwd_delta_kernel<128><<<grid, dim3(256), 0, st>>>(a);
     rc = check_launch("bwd_delta_kernel");
     if (rc) return rc;
   }

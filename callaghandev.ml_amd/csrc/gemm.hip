@@ -55,6 +55,14 @@ struct GemmArgs {
   // rope_pos0 + (rope_seg > 0 ? m % rope_seg : m), below rope_npos.
   const float2 *rope_cs;
   int rope_hd, rope_npos, rope_pos0, rope_seg;
+  // Split-K of the weight-gradient GEMMs (transposed-A launches): ksplit
+  // chunks of kchunk k-tiles each; chunk c of problem p writes its partial
+  // C to ws + (c * nprob + p) * M * N ([M][N], row stride N) and its partial
+  // bias-gradient row sums to wsb + (c * nprob + p) * M; splitk_reduce_kernel
+  // adds the chunks, in chunk order, to C and bgrad.  tiles counts the
+  // output tiles of all problems (total = tiles * ksplit).
+  int ksplit, kchunk, tiles;
+  float *ws, *wsb;
 };
 
 // Epilogue of both forward GEMM kernels with the rotary embedding of
@@ -355,8 +363,15 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const Gem
   __shared__ __attribute__((aligned(16))) float As[2][TM][LD];
   __shared__ __attribute__((aligned(16))) float Bs[2][TN][LD];
 
-  const int lid = xcd_remap(blockIdx.x, args.padded);
+  int lid = xcd_remap(blockIdx.x, args.padded);
   if (lid >= args.total) return;
+  // Split-K: chunk-major, so the workgroups of one chunk (which share its
+  // k-range of both operands) sit together on an XCD.
+  int chunk = 0;
+  if (args.ksplit > 1) {
+    chunk = lid / args.tiles;
+    lid -= chunk * args.tiles;
+  }
   // Grouped ordering over (tiles_m, nprob * tiles_n): GROUP_M tile-rows share
   // each weight panel while it is hot in L2.
   const int tiles_n_all = args.tiles_n * args.nprob;
@@ -390,9 +405,10 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const Gem
     for (int j = 0; j < BJ; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-  const int nk = K / BKK;
-  const float *__restrict__ A = P.a;
-  const float *__restrict__ W = P.w;
+  const int kt0 = chunk * args.kchunk;
+  const int nk = args.ksplit > 1 ? min(args.kchunk, K / BKK - kt0) : K / BKK;
+  const float *__restrict__ A = StageA::tile(P.a, kt0, args.lda);
+  const float *__restrict__ W = StageB::tile(P.w, kt0, args.ldb);
   const bool bsum = TA && P.bgrad && tn == 0;
   constexpr int KCH = NT / TM;  // k slices per row for the bias-gradient sums
   static_assert(NT % TM == 0 && BKK % (4 * KCH) == 0, "bias-gradient slices");
@@ -472,8 +488,27 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const Gem
         float s = 0.f;
 #pragma unroll
         for (int c = 0; c < KCH; ++c) s += red[t + c * TM];
-        P.bgrad[m0 + t] += s;
+        if (args.ksplit > 1)
+          args.wsb[((size_t)chunk * args.nprob + prob) * M + m0 + t] = s;
+        else
+          P.bgrad[m0 + t] += s;
       }
+    }
+    if (args.ksplit > 1) {  // the partial product of this chunk, reduced later
+      float *out = args.ws + ((size_t)chunk * args.nprob + prob) * (size_t)M * N;
+#pragma unroll
+      for (int j = 0; j < BJ; ++j) {
+        const int n = n0 + wn * (TN / WN) + j * 32 + li;
+        if (n >= N) continue;
+#pragma unroll
+        for (int i = 0; i < BI; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int m = m0 + wm * (TM / WM) + i * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
+            if (m < M) out[(size_t)m * N + n] = acc[i][j][r];
+          }
+      }
+      return;
     }
   }
 
@@ -567,17 +602,84 @@ __global__ void __launch_bounds__(256) op_rowsum_kernel(const GemmArgs args) {
   P.bgrad[m] += s;
 }
 
+// Sum of the split-K partials in chunk order: C (+)= sum_c ws[c], bgrad +=
+// sum_c wsb[c].  N % 4 == 0 (the tiled path's transposed staging of opB needs
+// it), so each thread owns four consecutive columns.
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs args) {
+  const int prob = blockIdx.y;
+  const GemmProblem P = args.p[prob];
+  const int M = args.M, N = args.N, n4 = N >> 2;
+  const size_t plane = (size_t)args.nprob * M * N;
+  const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (e < (size_t)M * n4) {
+    const int m = (int)(e / n4), n = (int)(e % n4) * 4;
+    const float *src = args.ws + (size_t)prob * M * N + (size_t)m * N + n;
+    vf4 s = *reinterpret_cast<const vf4 *>(src);
+    for (int c = 1; c < args.ksplit; ++c) {
+      const vf4 x = *reinterpret_cast<const vf4 *>(src + c * plane);
+      s[0] += x[0];
+      s[1] += x[1];
+      s[2] += x[2];
+      s[3] += x[3];
+    }
+    float *dst = P.c + (size_t)m * args.ldc + n;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dst[q] = args.beta ? dst[q] + s[q] : s[q];
+  }
+  if (P.bgrad && e < (size_t)M) {
+    float s = 0.f;
+    for (int c = 0; c < args.ksplit; ++c) s += args.wsb[((size_t)c * args.nprob + prob) * M + e];
+    P.bgrad[e] += s;
+  }
+}
+
+// Split-K plan of a weight-gradient GEMM (M = out, N = in, K = rows): enough
+// chunks to give every CU two resident workgroups when the output alone has
+// too few tiles, at least eight k-tiles (128 rows) per chunk.
+struct SplitPlan {
+  int ksplit = 1, kchunk = 0;
+  size_t bytes = 0;  // workspace: ksplit * nprob * (M * N + M) floats
+};
+
+SplitPlan splitk_plan(int M, int N, int K, int nprob) {
+  SplitPlan sp;
+  const int nk = K / 16;
+  sp.kchunk = nk;
+  if (M <= 0 || N <= 0 || K % 16 || N % 4) return sp;
+  const bool big = M >= 1024;
+  const int TM = big ? 256 : 128, TN = 128;
+  const int tiles = ((M + TM - 1) / TM) * ((N + TN - 1) / TN) * nprob;
+  const int slots = big ? 512 : 1024;
+  const int s = std::min(slots / tiles, nk / 8);
+  if (s <= 1) return sp;
+  sp.kchunk = (nk + s - 1) / s;
+  sp.ksplit = (nk + sp.kchunk - 1) / sp.kchunk;
+  if (sp.ksplit <= 1) {
+    sp = SplitPlan{};
+    sp.kchunk = nk;
+    return sp;
+  }
+  sp.bytes = (size_t)sp.ksplit * nprob * ((size_t)M * N + M) * sizeof(float);
+  return sp;
+}
+
 // Two tile configurations: 256 x 128 with eight waves for M >= 1024, and
 // 128 x 128 with four waves for smaller M (decode rows, short sequences).
 template <int TM, int TN, int BKK, int WM, int WN, int MINB, bool TA, bool TB>
 int launch_tile(GemmArgs g, hipStream_t stream) {
   g.tiles_m = (g.M + TM - 1) / TM;
   g.tiles_n = (g.N + TN - 1) / TN;
-  g.total = g.tiles_m * g.tiles_n * g.nprob;
+  g.tiles = g.tiles_m * g.tiles_n * g.nprob;
+  if (g.ksplit < 1) g.ksplit = 1;
+  g.total = g.tiles * g.ksplit;
   g.padded = pad_to_xcd(g.total);
   const dim3 grid(g.padded), block(64 * WM * WN);
   if constexpr (TA || TB) {
     gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_NONE, TA, TB><<<grid, block, 0, stream>>>(g);
+    if (g.ksplit > 1) {
+      const size_t n = std::max((size_t)g.M * (g.N / 4), (size_t)g.M);
+      splitk_reduce_kernel<<<dim3((unsigned)((n + 255) / 256), g.nprob), dim3(256), 0, stream>>>(g);
+    }
   } else {
     if (g.rope_cs) {
       gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, kActRope, false, false><<<grid, block, 0, stream>>>(g);
@@ -650,10 +752,43 @@ int launch_gemm(GemmArgs &g, bool ta, bool tb, hipStream_t stream, const char *w
   return check_launch(what);
 }
 
+// Attaches the split-K workspace of a weight-gradient launch (M = out, N =
+// in, K = rows) to g; fails when the caller's workspace is smaller than
+// splitk_plan asks for.
+int attach_split(GemmArgs &g, void *workspace, size_t workspace_bytes, const char *what) {
+  const SplitPlan sp = splitk_plan(g.M, g.N, g.K, g.nprob);
+  if (sp.ksplit <= 1) return CDML_OK;
+  if (!workspace || workspace_bytes < sp.bytes)
+    return fail(CDML_E_INVALID, "%s: workspace of %zu bytes needed, %zu given", what, sp.bytes,
+                workspace ? workspace_bytes : (size_t)0);
+  if (!aligned16(workspace)) return fail(CDML_E_INVALID, "%s: workspace must be 16-byte aligned", what);
+  g.ksplit = sp.ksplit;
+  g.kchunk = sp.kchunk;
+  g.ws = static_cast<float *>(workspace);
+  g.wsb = g.ws + (size_t)sp.ksplit * g.nprob * g.M * g.N;
+  return CDML_OK;
+}
+
 }  // namespace
 }  // namespace cdml
 
 using namespace cdml;
+
+extern "C" int cdml_linear_backward_workspace_size(int rows, int in_dim, int out_dim, size_t *bytes) {
+  if (!bytes) return fail(CDML_E_INVALID, "cdml_linear_backward_workspace_size: NULL pointer");
+  if (rows < 0 || in_dim < 0 || out_dim < 0)
+    return fail(CDML_E_INVALID, "cdml_linear_backward_workspace_size: negative size");
+  *bytes = splitk_plan(out_dim, in_dim, rows, 1).bytes;
+  return CDML_OK;
+}
+
+extern "C" int cdml_backprop_qkv_workspace_size(int rows, int in_dim, int out_dim, size_t *bytes) {
+  if (!bytes) return fail(CDML_E_INVALID, "cdml_backprop_qkv_workspace_size: NULL pointer");
+  if (rows < 0 || in_dim < 0 || out_dim < 0)
+    return fail(CDML_E_INVALID, "cdml_backprop_qkv_workspace_size: negative size");
+  *bytes = splitk_plan(out_dim, in_dim, rows, 3).bytes;
+  return CDML_OK;
+}
 
 extern "C" int cdml_project_qkv(const float *x, const float *wq, const float *bq, const float *wk,
                                 const float *bk, const float *wv, const float *bv, float *q,
@@ -752,7 +887,8 @@ extern "C" int cdml_linear(const float *x, int ldx, const float *w, const float 
 extern "C" int cdml_linear_backward(const float *x, int ldx, const float *dy, int lddy,
                                     const float *w, float *dx, int lddx, float *wgrad,
                                     float *bgrad, int rows, int in_dim, int out_dim,
-                                    int accumulate_dx, cdml_stream stream) {
+                                    int accumulate_dx, void *workspace, size_t workspace_bytes,
+                                    cdml_stream stream) {
   if (rows < 0 || in_dim < 0 || out_dim < 0)
     return fail(CDML_E_INVALID, "cdml_linear_backward: negative size");
   if (lddy < out_dim || (dx && lddx < in_dim) || (wgrad && ldx < in_dim))
@@ -792,6 +928,8 @@ extern "C" int cdml_linear_backward(const float *x, int ldx, const float *dy, in
     g.p[0] = {dy, x, nullptr, wgrad, bgrad};
     g.beta = 1;
     if (wgrad && in_dim > 0) {
+      rc = attach_split(g, workspace, workspace_bytes, "cdml_linear_backward");
+      if (rc) return rc;
       rc = launch_gemm(g, true, true, st, "cdml_linear_backward (weight gradient)");
     } else if (bgrad) {
       op_rowsum_kernel<true><<<dim3((out_dim + 255) / 256, 1), dim3(256), 0, st>>>(g);
@@ -806,7 +944,7 @@ extern "C" int cdml_backprop_qkv(const float *x, const float *dq, const float *d
                                  const float *wq, const float *wk, const float *wv, float *wq_grad,
                                  float *bq_grad, float *wk_grad, float *bk_grad, float *wv_grad,
                                  float *bv_grad, float *dx, int rows, int in_dim, int out_dim,
-                                 cdml_stream stream) {
+                                 void *workspace, size_t workspace_bytes, cdml_stream stream) {
   if (rows < 0 || in_dim < 0 || out_dim < 0)
     return fail(CDML_E_INVALID, "cdml_backprop_qkv: negative size");
   if (rows == 0) return CDML_OK;
@@ -832,6 +970,8 @@ extern "C" int cdml_backprop_qkv(const float *x, const float *dq, const float *d
     g.p[2] = {dv, x, nullptr, wv_grad, bv_grad};
     g.beta = 1;
     if (in_dim > 0) {
+      rc = attach_split(g, workspace, workspace_bytes, "cdml_backprop_qkv");
+      if (rc) return rc;
       rc = launch_gemm(g, true, true, st, "cdml_backprop_qkv (weight gradients)");
     } else {
       op_rowsum_kernel<true><<<dim3((out_dim + 255) / 256, 3), dim3(256), 0, st>>>(g);

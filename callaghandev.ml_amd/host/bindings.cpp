@@ -76,6 +76,22 @@ MatRef mat_inplace(py::array &a) {
   return MatRef(static_cast<float *>(a.mutable_data()), (int)a.shape(0), (int)a.shape(1));
 }
 
+// Gradient accumulators: writable float32 C-contiguous arrays, None = null.
+MatRef mat_inout(const py::object &o) {
+  if (o.is_none()) return MatRef();
+  py::array a = o;
+  return mat_inplace(a);
+}
+
+VecRef vec_inout(const py::object &o) {
+  if (o.is_none()) return VecRef();
+  py::array a = o;
+  if (!(a.flags() & py::array::c_style) || !a.dtype().is(py::dtype::of<float>()) || a.ndim() != 1 ||
+      !a.writeable())
+    throw ArgumentException("in-place argument must be a writable float32 C-contiguous vector");
+  return VecRef(static_cast<float *>(a.mutable_data()), (int)a.shape(0));
+}
+
 py::array_t<float> to_numpy(Matrix &&m) {
   auto *v = new std::vector<float>(std::move(m.data));
   py::capsule owner(v, [](void *p) { delete static_cast<std::vector<float> *>(p); });
@@ -277,6 +293,46 @@ PYBIND11_MODULE(_cdml_host, m) {
              auto V = mat(v);
              return to_numpy(a.DecodeSelfAttention(mat_inplace(q), mat_inplace(k), V.view, mat_inplace(keys),
                                                    mat_inplace(values), pos, numHeads));
+           })
+      .def("MultiHeadAttentionBackward",
+           [](HipAccelerationManager &a, py::object q, py::object k, py::object v, py::object dout,
+              int numHeads, float scale, py::object maskOrDecoder) {
+             auto Q = mat(q), K = mat(k), V = mat(v), D = mat(dout);
+             std::tuple<Matrix, Matrix, Matrix> r;
+             if (py::isinstance<py::bool_>(maskOrDecoder))  // the useDecoderMask overload
+               r = a.MultiHeadAttentionBackward(Q.view, K.view, V.view, D.view, numHeads, scale,
+                                                maskOrDecoder.cast<bool>());
+             else {
+               auto M = mask(maskOrDecoder);
+               r = a.MultiHeadAttentionBackward(Q.view, K.view, V.view, D.view, numHeads, scale, M.view);
+             }
+             return py::make_tuple(to_numpy(std::move(std::get<0>(r))), to_numpy(std::move(std::get<1>(r))),
+                                   to_numpy(std::move(std::get<2>(r))));
+           },
+           py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("dConcatenated"), py::arg("numHeads"),
+           py::arg("scale"), py::arg("mask") = false)
+      .def("BackpropQKV",
+           [](HipAccelerationManager &a, py::object x, py::object dq, py::object dk, py::object dv,
+              py::object wq, py::object wk, py::object wv, py::object wqg, py::object bqg, py::object wkg,
+              py::object bkg, py::object wvg, py::object bvg) {
+             auto X = mat(x), DQ = mat(dq), DK = mat(dk), DV = mat(dv), WQ = mat(wq), WK = mat(wk),
+                  WV = mat(wv);
+             return to_numpy(a.BackpropQKV(X.view, DQ.view, DK.view, DV.view, WQ.view, WK.view, WV.view,
+                                           mat_inout(wqg), vec_inout(bqg), mat_inout(wkg), vec_inout(bkg),
+                                           mat_inout(wvg), vec_inout(bvg)));
+           })
+      .def("BackpropLinearProjection",
+           [](HipAccelerationManager &a, py::object x, py::object dy, py::object w, py::object wg,
+              py::object bg, py::object dx) {
+             auto X = mat(x), DY = mat(dy), W = mat(w);
+             a.BackpropLinearProjection(X.view, DY.view, W.view, mat_inout(wg), vec_inout(bg), mat_inout(dx));
+           })
+      .def("BackpropOutputProjection",
+           [](HipAccelerationManager &a, py::object dl, py::object x, py::object w, py::object wg,
+              py::object bg, int seqLen, int outputDim, int embeddingDim) {
+             auto DL = mat(dl), X = mat(x), W = mat(w);
+             return to_numpy(a.BackpropOutputProjection(DL.view, X.view, W.view, mat_inout(wg), vec_inout(bg),
+                                                        seqLen, outputDim, embeddingDim));
            })
       .def("Dispose", &HipAccelerationManager::Dispose);
 

@@ -95,6 +95,14 @@ struct VecView {
   VecView(const std::vector<float> &v) : data(v.data()), length((int)v.size()) {}  // NOLINT
   bool null() const { return data == nullptr; }
 };
+struct VecRef {  // a writable float[] (gradient accumulators)
+  float *data = nullptr;
+  int length = 0;
+  VecRef() = default;
+  VecRef(float *d, int n) : data(d), length(n) {}
+  VecRef(std::vector<float> &v) : data(v.data()), length((int)v.size()) {}  // NOLINT
+  bool null() const { return data == nullptr; }
+};
 struct MaskView {  // bool[Lq, Lk], nonzero = attend
   const uint8_t *data = nullptr;
   int rows = 0, cols = 0;
@@ -164,6 +172,34 @@ class HipAccelerationManager {
   // NeuralNetwork.ForwardPassOnlyBatch route for it).
   Matrix FFNForwardBatch(MatView input, int seqLen, int outputDim, const FeedForwardNetwork &ffn);
 
+  // ---- attention backward (the training path of TransformerTrainer) -------
+  // IAccelerationManager.MultiHeadAttentionBackward (:161, :163): gradients
+  // of the attention core with respect to post-RoPE Q, K and V.  The first
+  // overload is causal when useDecoderMask (keys j <= i), the second takes an
+  // explicit bool[seqLenQ, seqLenK] mask (null = all keys).
+  std::tuple<Matrix, Matrix, Matrix> MultiHeadAttentionBackward(MatView Q, MatView K, MatView V,
+                                                                MatView dConcatenated,
+                                                                int numHeads, float scale,
+                                                                bool useDecoderMask = false);
+  std::tuple<Matrix, Matrix, Matrix> MultiHeadAttentionBackward(MatView Q, MatView K, MatView V,
+                                                                MatView dConcatenated,
+                                                                int numHeads, float scale,
+                                                                MaskView mask);
+  // IAccelerationManager.BackpropQKV (:171): returns dInput; the weight and
+  // bias gradients accumulate into the caller's arrays.
+  Matrix BackpropQKV(MatView input, MatView dQ, MatView dK, MatView dV, MatView WQ, MatView WK,
+                     MatView WV, MatRef WQGrad, VecRef biasQGrad, MatRef WKGrad, VecRef biasKGrad,
+                     MatRef WVGrad, VecRef biasVGrad);
+  // IAccelerationManager.BackpropLinearProjection (:182): weightGrad, biasGrad
+  // and dInput all accumulate.
+  void BackpropLinearProjection(MatView input, MatView dOutput, MatView weights, MatRef weightGrad,
+                                VecRef biasGrad, MatRef dInput);
+  // IAccelerationManager.BackpropOutputProjection (:184): returns dX
+  // [seqLen, embeddingDim]; weightGrad and biasGrad accumulate.
+  Matrix BackpropOutputProjection(MatView dLogits, MatView input, MatView weights,
+                                  MatRef weightGrad, VecRef biasGrad, int seqLen, int outputDim,
+                                  int embeddingDim);
+
   // Optional decode capability (no IAccelerationManager counterpart: the
   // reference runs this inline in LanguageModel.DecoderSelfAttentionStep,
   // LanguageModel.cs:353-427).  q, k, v [1, D] are the step's projections
@@ -206,6 +242,11 @@ class HipAccelerationManager {
   Matrix attention(MatView q, MatView k, MatView v, int numHeads, float scale, MaskView mask,
                    bool causal);
   Matrix linear(MatView x, int rowStart, int rowCount, MatView w, VecView b, int act);
+  std::tuple<Matrix, Matrix, Matrix> attention_backward(MatView Q, MatView K, MatView V,
+                                                        MatView dO, int numHeads, float scale,
+                                                        MaskView mask, bool causal);
+  void linear_backward(MatView x, MatView dy, int rows, MatView w, MatRef wgrad, VecRef bgrad,
+                       float *dx_host, bool accumulate_dx);
 
   int device_;
   bool ready_ = false, disposed_ = false;

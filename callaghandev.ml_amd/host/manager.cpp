@@ -20,7 +20,10 @@ void check(int rc, const char *what) {
 }
 
 // Scratch slots of the manager's device buffer pool.
-enum Slot { S_X = 0, S_Q, S_K, S_V, S_O, S_MASK, S_IDS, S_KVLEN, S_WS, S_BIAS, S_COUNT };
+enum Slot {
+  S_X = 0, S_Q, S_K, S_V, S_O, S_MASK, S_IDS, S_KVLEN, S_WS, S_BIAS,
+  S_DQ, S_DK, S_DV, S_GW0, S_GW1, S_GW2, S_GB0, S_GB1, S_GB2, S_COUNT
+};
 
 }  // namespace
 
@@ -474,6 +477,252 @@ Matrix HipAccelerationManager::FFNForwardBatch(MatView input, int seqLen, int ou
   download(out.ptr(), a, (size_t)seqLen * width * sizeof(float));
   sync();
   return out;
+}
+
+// ---- MultiHeadAttentionBackward: AccelerationCPU.cs:1011-1280 ----------------
+std::tuple<Matrix, Matrix, Matrix> HipAccelerationManager::MultiHeadAttentionBackward(
+    MatView Q, MatView K, MatView V, MatView dConcatenated, int numHeads, float scale,
+    bool useDecoderMask) {
+  return attention_backward(Q, K, V, dConcatenated, numHeads, scale, MaskView{}, useDecoderMask);
+}
+
+std::tuple<Matrix, Matrix, Matrix> HipAccelerationManager::MultiHeadAttentionBackward(
+    MatView Q, MatView K, MatView V, MatView dConcatenated, int numHeads, float scale,
+    MaskView mask) {
+  return attention_backward(Q, K, V, dConcatenated, numHeads, scale, mask, false);
+}
+
+// MultiHeadAttentionBackwardCore's checks (AccelerationCPU.cs:1037-1063) in
+// order, then cdml_sdpa_bwd on the manager's stream.
+std::tuple<Matrix, Matrix, Matrix> HipAccelerationManager::attention_backward(
+    MatView Q, MatView K, MatView V, MatView dO, int numHeads, float scale, MaskView mask,
+    bool causal) {
+  if (Q.null()) throw ArgumentNullException("Q");
+  if (K.null()) throw ArgumentNullException("K");
+  if (V.null()) throw ArgumentNullException("V");
+  if (dO.null()) throw ArgumentNullException("dConcatenated");
+  if (numHeads <= 0) throw ArgumentOutOfRangeException("numHeads");
+  const int lq = Q.rows, lk = K.rows, dim = Q.cols;
+  if (K.cols != dim || V.cols != dim)
+    throw ArgumentException("Q, K and V must have the same embedding dimension.");
+  if (V.rows != lk) throw ArgumentException("K and V must have the same sequence length.");
+  if (dO.rows != lq || dO.cols != dim)
+    throw ArgumentException("dConcatenated shape must match Q shape.", "dConcatenated");
+  if (dim % numHeads != 0)
+    throw ArgumentException("Embedding dim must be divisible by numHeads.", "numHeads");
+  if (!mask.null() && (mask.rows != lq || mask.cols != lk))
+    throw ArgumentException("Mask shape must be [" + std::to_string(lq) + "," + std::to_string(lk) +
+                                "], got [" + std::to_string(mask.rows) + "," +
+                                std::to_string(mask.cols) + "].",
+                            "mask");
+  Matrix dQ(lq, dim), dK(lk, dim), dV(lk, dim);
+  if (lq == 0 || lk == 0 || dim == 0) return {std::move(dQ), std::move(dK), std::move(dV)};
+  std::lock_guard<std::mutex> lock(mu_);
+  ensure_ready();
+  const size_t qb = (size_t)lq * dim * sizeof(float), kb = (size_t)lk * dim * sizeof(float);
+  float *dq_in = static_cast<float *>(scratch(S_Q, qb));
+  float *dk_in = static_cast<float *>(scratch(S_K, kb));
+  float *dv_in = static_cast<float *>(scratch(S_V, kb));
+  float *ddo = static_cast<float *>(scratch(S_O, qb));
+  float *gq = static_cast<float *>(scratch(S_DQ, qb));
+  float *gk = static_cast<float *>(scratch(S_DK, kb));
+  float *gv = static_cast<float *>(scratch(S_DV, kb));
+  size_t ws = 0;
+  check(cdml_sdpa_bwd_workspace_size(1, lq, lk, dim, numHeads, &ws), "cdml_sdpa_bwd_workspace_size");
+  void *dws = scratch(S_WS, ws);
+  upload(dq_in, Q.data, qb);
+  upload(dk_in, K.data, kb);
+  upload(dv_in, V.data, kb);
+  upload(ddo, dO.data, qb);
+  const uint8_t *dm = nullptr;
+  if (!mask.null()) {
+    void *m = scratch(S_MASK, (size_t)lq * lk);
+    upload(m, mask.data, (size_t)lq * lk);
+    dm = static_cast<const uint8_t *>(m);
+  }
+  check(cdml_sdpa_bwd(dq_in, dim, dk_in, dim, dv_in, dim, ddo, dim, gq, dim, gk, dim, gv, dim, 1,
+                      lq, lk, dim, numHeads, scale, causal ? 1 : 0, dm, dws, ws, stream_),
+        "cdml_sdpa_bwd");
+  download(dQ.ptr(), gq, qb);
+  download(dK.ptr(), gk, kb);
+  download(dV.ptr(), gv, kb);
+  sync();
+  return {std::move(dQ), std::move(dK), std::move(dV)};
+}
+
+// ---- BackpropQKV: AccelerationCPU.cs:2071-2186 ------------------------------
+Matrix HipAccelerationManager::BackpropQKV(MatView input, MatView dQ, MatView dK, MatView dV,
+                                           MatView WQ, MatView WK, MatView WV, MatRef WQGrad,
+                                           VecRef biasQGrad, MatRef WKGrad, VecRef biasKGrad,
+                                           MatRef WVGrad, VecRef biasVGrad) {
+  if (input.null()) throw ArgumentNullException("input");
+  if (dQ.null()) throw ArgumentNullException("dQ");
+  if (dK.null()) throw ArgumentNullException("dK");
+  if (dV.null()) throw ArgumentNullException("dV");
+  if (WQ.null()) throw ArgumentNullException("WQ");
+  if (WK.null()) throw ArgumentNullException("WK");
+  if (WV.null()) throw ArgumentNullException("WV");
+  if (!WQGrad.data) throw ArgumentNullException("WQGrad");
+  if (!WKGrad.data) throw ArgumentNullException("WKGrad");
+  if (!WVGrad.data) throw ArgumentNullException("WVGrad");
+  if (biasQGrad.null()) throw ArgumentNullException("biasQGrad");
+  if (biasKGrad.null()) throw ArgumentNullException("biasKGrad");
+  if (biasVGrad.null()) throw ArgumentNullException("biasVGrad");
+  const int rows = input.rows, inputDim = input.cols;
+  const int outputDim = WQ.rows;
+  if (WK.rows != outputDim || WV.rows != outputDim)
+    throw ArgumentException("Q, K and V dimensions must match.");
+  if (WQ.cols != inputDim || WK.cols != inputDim || WV.cols != inputDim)
+    throw ArgumentException("Q/K/V weight input dimensions must match input width.");
+  if (dQ.rows != rows || dK.rows != rows || dV.rows != rows)
+    throw ArgumentException("dQ, dK and dV row counts must match input row count.");
+  if (dQ.cols != outputDim || dK.cols != outputDim || dV.cols != outputDim)
+    throw ArgumentException("dQ, dK and dV widths must match Q/K/V output dimension.");
+  if (WQGrad.rows != outputDim || WQGrad.cols != inputDim)
+    throw ArgumentException("WQGrad shape mismatch.", "WQGrad");
+  if (WKGrad.rows != outputDim || WKGrad.cols != inputDim)
+    throw ArgumentException("WKGrad shape mismatch.", "WKGrad");
+  if (WVGrad.rows != outputDim || WVGrad.cols != inputDim)
+    throw ArgumentException("WVGrad shape mismatch.", "WVGrad");
+  if (biasQGrad.length != outputDim || biasKGrad.length != outputDim || biasVGrad.length != outputDim)
+    throw ArgumentException("Q/K/V bias gradient lengths must match output dimension.");
+  Matrix dInput(rows, inputDim);
+  if (rows == 0 || inputDim == 0 || outputDim == 0) return dInput;
+  std::lock_guard<std::mutex> lock(mu_);
+  ensure_ready();
+  const size_t xb = (size_t)rows * inputDim * sizeof(float);
+  const size_t db = (size_t)rows * outputDim * sizeof(float);
+  const size_t wb = (size_t)outputDim * inputDim * sizeof(float), bb = (size_t)outputDim * sizeof(float);
+  const float *wq = resident(WQ.data, outputDim, inputDim), *wk = resident(WK.data, outputDim, inputDim),
+              *wv = resident(WV.data, outputDim, inputDim);
+  float *dx_in = static_cast<float *>(scratch(S_X, xb));
+  float *ddq = static_cast<float *>(scratch(S_DQ, db));
+  float *ddk = static_cast<float *>(scratch(S_DK, db));
+  float *ddv = static_cast<float *>(scratch(S_DV, db));
+  float *ddx = static_cast<float *>(scratch(S_O, xb));
+  float *gw[3] = {static_cast<float *>(scratch(S_GW0, wb)), static_cast<float *>(scratch(S_GW1, wb)),
+                  static_cast<float *>(scratch(S_GW2, wb))};
+  float *gb[3] = {static_cast<float *>(scratch(S_GB0, bb)), static_cast<float *>(scratch(S_GB1, bb)),
+                  static_cast<float *>(scratch(S_GB2, bb))};
+  MatRef hw[3] = {WQGrad, WKGrad, WVGrad};
+  VecRef hb[3] = {biasQGrad, biasKGrad, biasVGrad};
+  upload(dx_in, input.data, xb);
+  upload(ddq, dQ.data, db);
+  upload(ddk, dK.data, db);
+  upload(ddv, dV.data, db);
+  for (int i = 0; i < 3; ++i) {
+    upload(gw[i], hw[i].data, wb);
+    upload(gb[i], hb[i].data, bb);
+  }
+  size_t ws = 0;
+  check(cdml_backprop_qkv_workspace_size(rows, inputDim, outputDim, &ws),
+        "cdml_backprop_qkv_workspace_size");
+  void *dws = ws ? scratch(S_WS, ws) : nullptr;
+  check(cdml_backprop_qkv(dx_in, ddq, ddk, ddv, wq, wk, wv, gw[0], gb[0], gw[1], gb[1], gw[2], gb[2],
+                          ddx, rows, inputDim, outputDim, dws, ws, stream_),
+        "cdml_backprop_qkv");
+  download(dInput.ptr(), ddx, xb);
+  for (int i = 0; i < 3; ++i) {
+    download(hw[i].data, gw[i], wb);
+    download(hb[i].data, gb[i], bb);
+  }
+  sync();
+  return dInput;
+}
+
+// Shared body of BackpropLinearProjection / BackpropOutputProjection
+// (AccelerationCPU.cs:2188-2270): wgrad += dy^T x, bgrad += column sums of
+// dy, dx (+)= dy w, over `rows` rows of x and dy.
+void HipAccelerationManager::linear_backward(MatView x, MatView dy, int rows, MatView w,
+                                             MatRef wgrad, VecRef bgrad, float *dx_host,
+                                             bool accumulate_dx) {
+  const int in = w.cols, out = w.rows;
+  if (rows == 0 || in == 0) return;
+  std::lock_guard<std::mutex> lock(mu_);
+  ensure_ready();
+  const size_t xb = (size_t)rows * in * sizeof(float), yb = (size_t)rows * out * sizeof(float);
+  const size_t wb = (size_t)out * in * sizeof(float), bb = (size_t)out * sizeof(float);
+  const float *dw = resident(w.data, out, in);
+  float *dxin = static_cast<float *>(scratch(S_X, xb));
+  float *ddy = static_cast<float *>(scratch(S_Q, yb > 0 ? yb : 4));
+  float *ddx = static_cast<float *>(scratch(S_O, xb));
+  float *gw = static_cast<float *>(scratch(S_GW0, wb > 0 ? wb : 4));
+  float *gb = static_cast<float *>(scratch(S_GB0, bb > 0 ? bb : 4));
+  upload(dxin, x.data, xb);
+  if (out > 0) {
+    upload(ddy, dy.data, yb);
+    upload(gw, wgrad.data, wb);
+    upload(gb, bgrad.data, bb);
+  }
+  if (accumulate_dx) upload(ddx, dx_host, xb);
+  if (out > 0) {
+    size_t ws = 0;
+    check(cdml_linear_backward_workspace_size(rows, in, out, &ws),
+          "cdml_linear_backward_workspace_size");
+    void *dws = ws ? scratch(S_WS, ws) : nullptr;
+    check(cdml_linear_backward(dxin, in, ddy, out, dw, ddx, in, gw, gb, rows, in, out,
+                               accumulate_dx ? 1 : 0, dws, ws, stream_),
+          "cdml_linear_backward");
+  } else if (!accumulate_dx) {
+    check(cdml_zero_f32_async(ddx, (size_t)rows * in, stream_), "cdml_zero_f32_async");
+  }
+  download(dx_host, ddx, xb);
+  if (out > 0) {
+    download(wgrad.data, gw, wb);
+    download(bgrad.data, gb, bb);
+  }
+  sync();
+}
+
+// ---- BackpropLinearProjection: AccelerationCPU.cs:2188-2227 -----------------
+// The reference indexes the arrays without checks (a mismatch surfaces as an
+// IndexOutOfRangeException mid-update); here every shape is checked before
+// any device work, with ArgumentException.
+void HipAccelerationManager::BackpropLinearProjection(MatView input, MatView dOutput,
+                                                      MatView weights, MatRef weightGrad,
+                                                      VecRef biasGrad, MatRef dInput) {
+  if (input.null()) throw ArgumentNullException("input");
+  if (dOutput.null()) throw ArgumentNullException("dOutput");
+  if (weights.null()) throw ArgumentNullException("weights");
+  if (!weightGrad.data) throw ArgumentNullException("weightGrad");
+  if (biasGrad.null()) throw ArgumentNullException("biasGrad");
+  if (!dInput.data) throw ArgumentNullException("dInput");
+  const int rows = input.rows, in = input.cols, out = dOutput.cols;
+  if (dOutput.rows != rows) throw ArgumentException("dOutput rows must match input rows.", "dOutput");
+  if (weights.rows != out || weights.cols != in)
+    throw ArgumentException("weights must be [outDim, inDim].", "weights");
+  if (weightGrad.rows != out || weightGrad.cols != in)
+    throw ArgumentException("weightGrad must be [outDim, inDim].", "weightGrad");
+  if (biasGrad.length != out) throw ArgumentException("biasGrad length must match outDim.", "biasGrad");
+  if (dInput.rows != rows || dInput.cols != in)
+    throw ArgumentException("dInput must be [seqLen, inDim].", "dInput");
+  linear_backward(input, dOutput, rows, weights, weightGrad, biasGrad, dInput.data, true);
+}
+
+// ---- BackpropOutputProjection: AccelerationCPU.cs:2229-2270 ------------------
+Matrix HipAccelerationManager::BackpropOutputProjection(MatView dLogits, MatView input,
+                                                        MatView weights, MatRef weightGrad,
+                                                        VecRef biasGrad, int seqLen, int outputDim,
+                                                        int embeddingDim) {
+  if (dLogits.null()) throw ArgumentNullException("dLogits");
+  if (input.null()) throw ArgumentNullException("input");
+  if (weights.null()) throw ArgumentNullException("weights");
+  if (!weightGrad.data) throw ArgumentNullException("weightGrad");
+  if (biasGrad.null()) throw ArgumentNullException("biasGrad");
+  if (seqLen < 0 || seqLen > dLogits.rows || seqLen > input.rows)
+    throw ArgumentException("seqLen exceeds the dLogits or input rows.", "seqLen");
+  if (outputDim < 0 || dLogits.cols != outputDim)
+    throw ArgumentException("dLogits width must equal outputDim.", "outputDim");
+  if (embeddingDim < 0 || input.cols != embeddingDim)
+    throw ArgumentException("input width must equal embeddingDim.", "embeddingDim");
+  if (weights.rows != outputDim || weights.cols != embeddingDim)
+    throw ArgumentException("weights must be [outputDim, embeddingDim].", "weights");
+  if (weightGrad.rows != outputDim || weightGrad.cols != embeddingDim)
+    throw ArgumentException("weightGrad must be [outputDim, embeddingDim].", "weightGrad");
+  if (biasGrad.length != outputDim) throw ArgumentException("biasGrad length must match outputDim.", "biasGrad");
+  Matrix dX(seqLen, embeddingDim);
+  linear_backward(input, dLogits, seqLen, weights, weightGrad, biasGrad, dX.ptr(), false);
+  return dX;
 }
 
 // ---- decode capability ------------------------------------------------------

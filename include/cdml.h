@@ -137,24 +137,37 @@ int cdml_linear(const float *x, int ldx, const float *w, const float *b,
  * (accumulate_dx = 0, BackpropOutputProjection) or added to (1,
  * BackpropLinearProjection).  dx = NULL skips the input gradient; wgrad and
  * bgrad may be NULL to skip theirs.  fp32 MFMA; the bias gradient is summed
- * inside the weight-gradient GEMM. */
+ * inside the weight-gradient GEMM.  When the weight gradient has too few
+ * output tiles to fill the device (rows >> in_dim * out_dim / 2^15), its
+ * reduction over rows is split into chunks whose partial sums go to
+ * `workspace` and are added in a fixed order (deterministic, no atomics):
+ * `workspace` is 16-byte aligned device memory of at least
+ * cdml_linear_backward_workspace_size() bytes (NULL when that is 0). */
+int cdml_linear_backward_workspace_size(int rows, int in_dim, int out_dim,
+                                        size_t *bytes);
 int cdml_linear_backward(const float *x, int ldx, const float *dy, int lddy,
                          const float *w, float *dx, int lddx, float *wgrad,
                          float *bgrad, int rows, int in_dim, int out_dim,
-                         int accumulate_dx, cdml_stream stream);
+                         int accumulate_dx, void *workspace,
+                         size_t workspace_bytes, cdml_stream stream);
 
 /* IAccelerationManager.BackpropQKV (:171), replacing AccelerationCPU.cs:
  * 2071-2186:
  *   dx = dq wq + dk wk + dv wv   (overwritten)
  *   w*_grad += d*^T x,  b*_grad += column sums of d*   (accumulated)
  * x [rows, in_dim]; dq, dk, dv [rows, out_dim]; w* and w*_grad
- * [out_dim, in_dim]; b*_grad [out_dim]; dx [rows, in_dim]; all contiguous. */
+ * [out_dim, in_dim]; b*_grad [out_dim]; dx [rows, in_dim]; all contiguous.
+ * `workspace`: split-K partials of the three weight gradients, as for
+ * cdml_linear_backward, of cdml_backprop_qkv_workspace_size() bytes. */
+int cdml_backprop_qkv_workspace_size(int rows, int in_dim, int out_dim,
+                                     size_t *bytes);
 int cdml_backprop_qkv(const float *x, const float *dq, const float *dk,
                       const float *dv, const float *wq, const float *wk,
                       const float *wv, float *wq_grad, float *bq_grad,
                       float *wk_grad, float *bk_grad, float *wv_grad,
                       float *bv_grad, float *dx, int rows, int in_dim,
-                      int out_dim, cdml_stream stream);
+                      int out_dim, void *workspace, size_t workspace_bytes,
+                      cdml_stream stream);
 
 /* IAccelerationManager.ApplyRotaryPositionEmbeddingInPlace (:320) and
  * ApplyRotaryPositionEmbeddingHeadInPlace (:319), replacing

@@ -96,8 +96,12 @@ def linear_backward(x, dy, w, wgrad, bgrad, dx=None, accumulate=False, want_dx=T
     out = dy.shape[1]
     bx, bdy, bw, bwg, bbg = up(x), up(dy), up(w), up(wgrad), up(bgrad)
     bdx = up(dx) if dx is not None else N.DeviceBuffer(max(4, rows * ind * 4))
+    ws = C.c_size_t(0)
+    N.check(N.lib().cdml_linear_backward_workspace_size(rows, ind, out, C.byref(ws)))
+    bws = N.DeviceBuffer(max(16, ws.value))
     N.check(N.lib().cdml_linear_backward(bx.ptr, ind, bdy.ptr, out, bw.ptr, bdx.ptr if want_dx else None, ind,
-                                         bwg.ptr, bbg.ptr, rows, ind, out, int(accumulate), stream().handle))
+                                         bwg.ptr, bbg.ptr, rows, ind, out, int(accumulate), bws.ptr, ws.value,
+                                         stream().handle))
     return down(bwg, (out, ind)), down(bbg, (out,)), down(bdx, (rows, ind)) if want_dx else None
 
 
@@ -108,8 +112,11 @@ def backprop_qkv(x, dq, dk, dv, wq, wk, wv, wq_grad, bq_grad, wk_grad, bk_grad, 
     ins = [up(a) for a in (x, dq, dk, dv, wq, wk, wv)]
     grads = [up(a) for a in (wq_grad, bq_grad, wk_grad, bk_grad, wv_grad, bv_grad)]
     bdx = N.DeviceBuffer(max(4, rows * ind * 4))
+    ws = C.c_size_t(0)
+    N.check(N.lib().cdml_backprop_qkv_workspace_size(rows, ind, out, C.byref(ws)))
+    bws = N.DeviceBuffer(max(16, ws.value))
     N.check(N.lib().cdml_backprop_qkv(*(b.ptr for b in ins), *(g.ptr for g in grads), bdx.ptr, rows, ind, out,
-                                      stream().handle))
+                                      bws.ptr, ws.value, stream().handle))
     shapes = [(out, ind), (out,)] * 3
     return (down(bdx, (rows, ind)), *(down(g, sh) for g, sh in zip(grads, shapes)))
 

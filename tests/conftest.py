@@ -51,3 +51,18 @@ def assert_parity(actual, expected, atol=1e-4, rtol=1e-3, what=""):
             f"{what}: {int(bad.sum())} of {e.size} elements out of tolerance "
             f"(atol {atol}, rtol {rtol}); worst at {i}: got {a[i]}, want {e[i]}; "
             f"max abs err {err.max():.3e}")
+
+
+def assert_parity_with_exact(actual, oracle, exact, atol=1e-4, rtol=1e-3, what=""):
+    """Parity for long fp32 reductions (weight gradients summed over thousands
+    of rows).  The oracle sums in the reference's sequential fp32 order, and on
+    elements that cancel to near zero its own rounding can exceed the bar: a
+    2048-row gradient sum of O(1) products drifts by up to 3e-4 from exact
+    arithmetic.  So the result must meet the bar against the float64 value
+    everywhere, and against the oracle wherever the oracle itself meets the
+    bar against the float64 value."""
+    e64 = np.asarray(exact, np.float64)
+    o = np.asarray(oracle, np.float64)
+    assert_parity(actual, e64, atol, rtol, what + " (vs float64)")
+    ok = np.abs(o - e64) <= atol + rtol * np.abs(e64)
+    assert_parity(np.asarray(actual)[ok], o[ok], atol, rtol, what + " (vs oracle)")

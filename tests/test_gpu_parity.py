@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 import abi_ops as G
-from conftest import assert_parity
+from conftest import assert_parity, assert_parity_with_exact
 from oracle import oracle as O
 from cdml import native as N
 from cdml import synth
@@ -161,6 +161,7 @@ def test_backprop_qkv_reference_case():
 
 @pytest.mark.parametrize("rows,ind,out", [(1024, 512, 512),   # tiled kernels (128-row tiles)
                                           (2048, 256, 1024),  # 256-row tiles for W_grad
+                                          (656, 256, 256),    # split K with a short last chunk
                                           (300, 1024, 96),    # K = 300 rows: generic W_grad kernel
                                           (130, 257, 129),    # ragged everywhere
                                           (1, 64, 64)])
@@ -172,8 +173,13 @@ def test_backprop_qkv_shapes(rows, ind, out):
           synth.normal(63, (out,)), synth.normal(64, (out, ind)), synth.normal(65, (out,))]
     got = G.backprop_qkv(x, *d, *w, *g0)
     want = O.backprop_qkv(x, *d, *w, *g0)
-    for a, e, n in zip(got, want, ["dInput", "WQGrad", "biasQGrad", "WKGrad", "biasKGrad", "WVGrad", "biasVGrad"]):
-        parity(a, e, f"BackpropQKV {rows}x{ind}->{out} {n}")
+    X, Dd = x.astype(np.float64), [a.astype(np.float64) for a in d]
+    exact = [sum(Di @ Wi.astype(np.float64) for Di, Wi in zip(Dd, w))]
+    for i in range(3):
+        exact += [g0[2 * i] + Dd[i].T @ X, g0[2 * i + 1] + Dd[i].sum(0)]
+    for a, e, e64, n in zip(got, want, exact, ["dInput", "WQGrad", "biasQGrad", "WKGrad", "biasKGrad", "WVGrad",
+                                               "biasVGrad"]):
+        assert_parity_with_exact(a, e, e64, what=f"BackpropQKV {rows}x{ind}->{out} {n}")
 
 
 def test_backprop_qkv_c3_shape_float64():
@@ -194,26 +200,55 @@ def test_backprop_qkv_c3_shape_float64():
         parity(got_b, Di.sum(0), f"c3 bias{n}Grad")
 
 
-@pytest.mark.parametrize("rows,ind,out", [(4, 8, 8), (16, 16, 32), (512, 256, 256), (77, 64, 130)])
+@pytest.mark.parametrize("rows,ind,out", [(4, 8, 8), (16, 16, 32), (512, 256, 256), (77, 64, 130),
+                                          (4112, 128, 1024)])  # split K, 257 k-tiles
 def test_linear_backward(rows, ind, out):
     """BackpropLinearProjection (dInput accumulates) and BackpropOutputProjection
     (dX overwritten) on the shapes of AccelerationConsistencyTests.cs:633-700,
     1108-1125 and larger tiled ones."""
     x, dy, w = synth.normal(1, (rows, ind)), synth.normal(2, (rows, out)), synth.normal(3, (out, ind))
     wg0, bg0, dx0 = synth.normal(4, (out, ind)), synth.normal(5, (out,)), synth.normal(6, (rows, ind))
+    X, DY, W = x.astype(np.float64), dy.astype(np.float64), w.astype(np.float64)
+    xwg, xbg, xdx = wg0 + DY.T @ X, bg0 + DY.sum(0), DY @ W
     wg, bg, dx = G.linear_backward(x, dy, w, wg0, bg0, dx=dx0, accumulate=True)
     ewg, ebg, edx = O.backprop_linear_projection(x, dy, w, wg0, bg0, dx0)
-    parity(wg, ewg, "linear weightGrad")
-    parity(bg, ebg, "linear biasGrad")
-    parity(dx, edx, "linear dInput")
+    assert_parity_with_exact(wg, ewg, xwg, what="linear weightGrad")
+    assert_parity_with_exact(bg, ebg, xbg, what="linear biasGrad")
+    assert_parity_with_exact(dx, edx, dx0 + xdx, what="linear dInput")
     wg, bg, dx = G.linear_backward(x, dy, w, wg0, bg0)
     edx, ewg, ebg = O.backprop_output_projection(dy, x, w, wg0, bg0)
-    parity(dx, edx, "output dX")
-    parity(wg, ewg, "output weightGrad")
-    parity(bg, ebg, "output biasGrad")
+    assert_parity_with_exact(dx, edx, xdx, what="output dX")
+    assert_parity_with_exact(wg, ewg, xwg, what="output weightGrad")
+    assert_parity_with_exact(bg, ebg, xbg, what="output biasGrad")
     wg, bg, none = G.linear_backward(x, dy, w, wg0, bg0, want_dx=False)
     assert none is None
-    parity(wg, ewg, "weightGrad without dX")
+    assert_parity_with_exact(wg, ewg, xwg, what="weightGrad without dX")
+
+
+def test_weight_gradient_workspace_contract():
+    """The split weight-gradient GEMM asks for a workspace and refuses a
+    smaller one with CDML_E_INVALID before launching anything; two calls with
+    the same inputs give bit-identical gradients (fixed reduction order)."""
+    import ctypes as C
+    from cdml import native as N
+    rows, ind, out = 8192, 256, 256
+    need = C.c_size_t(0)
+    N.check(N.lib().cdml_linear_backward_workspace_size(rows, ind, out, C.byref(need)))
+    assert need.value > 0
+    x, dy = synth.normal(7, (rows, ind)), synth.normal(8, (rows, out))
+    w = synth.normal(9, (out, ind))
+    bx, bdy, bw = (N.DeviceBuffer.from_array(a) for a in (x, dy, w))
+    bwg, bbg = N.DeviceBuffer.from_array(np.zeros((out, ind), np.float32)), N.DeviceBuffer.from_array(np.zeros(out, np.float32))
+    small = N.DeviceBuffer(need.value // 2)
+    rc = N.lib().cdml_linear_backward(bx.ptr, ind, bdy.ptr, out, bw.ptr, None, ind, bwg.ptr, bbg.ptr, rows, ind,
+                                      out, 0, small.ptr, need.value // 2, None)
+    assert rc == -1 and b"workspace" in N.lib().cdml_last_error()
+    g1 = G.linear_backward(x, dy, w, np.zeros((out, ind), np.float32), np.zeros(out, np.float32), want_dx=False)
+    g2 = G.linear_backward(x, dy, w, np.zeros((out, ind), np.float32), np.zeros(out, np.float32), want_dx=False)
+    assert np.array_equal(g1[0], g2[0]) and np.array_equal(g1[1], g2[1])
+    X, DY = x.astype(np.float64), dy.astype(np.float64)
+    parity(g1[0], DY.T @ X, "split weightGrad vs float64")
+    parity(g1[1], DY.sum(0), "split biasGrad vs float64")
 
 
 # ------------------------------------------------------- attention backward

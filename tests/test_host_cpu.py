@@ -139,6 +139,52 @@ def test_config_and_model_rules():
         lm.load_weights(synth.lm_weights(dict(cfg, vocab=13), 1))
 
 
+def test_backward_argument_rules(mgr):
+    """MultiHeadAttentionBackwardCore (AccelerationCPU.cs:1037-1063) and
+    BackpropQKV (:2071-2133) checks, in the reference's order."""
+    q, k, v = M(4, 8, 41), M(5, 8, 42), M(5, 8, 43)
+    d = M(4, 8, 44)
+    with pytest.raises(H.ArgumentNullException, match="dConcatenated"):
+        mgr.MultiHeadAttentionBackward(q, k, v, None, 2, 0.5)
+    with pytest.raises(H.ArgumentOutOfRangeException, match="numHeads"):
+        mgr.MultiHeadAttentionBackward(q, k, v, d, 0, 0.5)
+    with pytest.raises(H.ArgumentException, match="same embedding dimension"):
+        mgr.MultiHeadAttentionBackward(q, k[:, :6], v, d, 2, 0.5)
+    with pytest.raises(H.ArgumentException, match="same sequence length"):
+        mgr.MultiHeadAttentionBackward(q, k, v[:4], d, 2, 0.5)
+    with pytest.raises(H.ArgumentException, match="dConcatenated shape"):
+        mgr.MultiHeadAttentionBackward(q, k, v, d[:3], 2, 0.5)
+    with pytest.raises(H.ArgumentException, match="divisible"):
+        mgr.MultiHeadAttentionBackward(q, k, v, d, 3, 0.5)
+    with pytest.raises(H.ArgumentException, match="Mask shape"):
+        mgr.MultiHeadAttentionBackward(q, k, v, d, 2, 0.5, np.ones((4, 4), bool))
+    z = np.zeros
+    x, dq = M(3, 6, 45), M(3, 4, 46)
+    w = M(4, 6, 47)
+    g = lambda: (z((4, 6), np.float32), z(4, np.float32), z((4, 6), np.float32), z(4, np.float32),
+                 z((4, 6), np.float32), z(4, np.float32))
+    with pytest.raises(H.ArgumentNullException, match="WKGrad"):
+        gg = list(g()); gg[2] = None
+        mgr.BackpropQKV(x, dq, dq, dq, w, w, w, *gg)
+    with pytest.raises(H.ArgumentException, match="dimensions must match"):
+        mgr.BackpropQKV(x, dq, dq, dq, w, w[:3], w, *g())
+    with pytest.raises(H.ArgumentException, match="row counts"):
+        mgr.BackpropQKV(x, dq, dq[:2], dq, w, w, w, *g())
+    with pytest.raises(H.ArgumentException, match="WVGrad shape"):
+        gg = list(g()); gg[4] = z((4, 5), np.float32)
+        mgr.BackpropQKV(x, dq, dq, dq, w, w, w, *gg)
+    with pytest.raises(H.ArgumentException, match="bias gradient lengths"):
+        gg = list(g()); gg[1] = z(3, np.float32)
+        mgr.BackpropQKV(x, dq, dq, dq, w, w, w, *gg)
+    with pytest.raises(H.ArgumentException, match="dInput"):
+        mgr.BackpropLinearProjection(x, dq, w, z((4, 6), np.float32), z(4, np.float32), z((2, 6), np.float32))
+    with pytest.raises(H.ArgumentException, match="outputDim"):
+        mgr.BackpropOutputProjection(dq, x, w, z((4, 6), np.float32), z(4, np.float32), 3, 5, 6)
+    # empty inputs need no device: zero-row gradients come back
+    r = mgr.MultiHeadAttentionBackward(q[:0], k, v, d[:0], 2, 0.5, True)
+    assert [a.shape for a in r] == [(0, 8), (5, 8), (5, 8)] and not any(a.any() for a in r)
+
+
 def test_no_device_means_loud_failure(mgr):
     if N.device_count() > 0:
         pytest.skip("a device is visible")

@@ -123,6 +123,74 @@ def test_manager_resident_weights_follow_host_changes(mgr):
     parity(mgr.ProjectOutputBatch(x, w, b, 7, 9), O.project_output_batch(x, w, b), "after in-place change")
 
 
+def test_manager_attention_backward(mgr):
+    """MultiHeadAttentionBackward, both overloads, on the parity suite's
+    closed-form case (AccelerationManagerParityTests.cs:355-382: 4x6, 2 heads,
+    scale 1/sqrt 3, decoder flag and explicit causal mask), the consistency
+    suite's 6x8 no-mask / decoder and 5x8 cross cases
+    (AccelerationConsistencyTests.cs:962-1020), and a 300x128 causal case on
+    the MFMA kernels (head dim 64)."""
+    q, k, v, d = M(4, 6, 31), M(4, 6, 32), M(4, 6, 33), M(4, 6, 34)
+    scale = float(np.float32(1) / np.sqrt(np.float32(3)))
+    causal = np.tril(np.ones((4, 4), bool))
+    want = O.mha_backward(q, k, v, d, 2, scale, use_decoder_mask=True)
+    for got, w, n in zip(mgr.MultiHeadAttentionBackward(q, k, v, d, 2, scale, True), want, ("dQ", "dK", "dV")):
+        parity(got, w, f"MHA backward (bool) {n}")
+    for got, w, n in zip(mgr.MultiHeadAttentionBackward(q, k, v, d, 2, scale, causal), want, ("dQ", "dK", "dV")):
+        parity(got, w, f"MHA backward (mask) {n}")
+    for lq, lk, dec in ((6, 6, False), (6, 6, True), (5, 8, False)):
+        q, k, v, d = M(lq, 8, 51), M(lk, 8, 52), M(lk, 8, 53), M(lq, 8, 54)
+        s = float(np.float32(1) / np.sqrt(np.float32(4)))
+        want = O.mha_backward(q, k, v, d, 2, s, use_decoder_mask=dec)
+        for got, w, n in zip(mgr.MultiHeadAttentionBackward(q, k, v, d, 2, s, dec), want, ("dQ", "dK", "dV")):
+            parity(got, w, f"MHA backward {lq}x{lk} decoder={dec} {n}")
+    L, D, Hh = 300, 128, 2
+    q, k, v, d = (synth.normal(60 + i, (L, D)) for i in range(4))
+    s = 0.125
+    want = O.mha_backward(q, k, v, d, Hh, s, use_decoder_mask=True)
+    for got, w, n in zip(mgr.MultiHeadAttentionBackward(q, k, v, d, Hh, s, True), want, ("dQ", "dK", "dV")):
+        parity(got, w, f"MHA backward 300x128 causal {n}")
+
+
+def test_manager_projection_backward(mgr):
+    """BackpropQKV, BackpropLinearProjection and BackpropOutputProjection with
+    nonzero gradient accumulators on entry (they must accumulate), on the
+    consistency suite's shapes (AccelerationConsistencyTests.cs:633-700) and a
+    projection-sized case."""
+    for rows, ind, out in ((4, 8, 8), (300, 256, 256)):
+        x, dq, dk, dv = M(rows, ind, 71), M(rows, out, 72), M(rows, out, 73), M(rows, out, 74)
+        w = [M(out, ind, 75 + i) for i in range(3)]
+        g0 = [M(out, ind, 80), Vec(out, 81), M(out, ind, 82), Vec(out, 83), M(out, ind, 84), Vec(out, 85)]
+        want = O.backprop_qkv(x, dq, dk, dv, *w, *g0)
+        g = [a.copy() for a in g0]
+        dx = mgr.BackpropQKV(x, dq, dk, dv, *w, *g)
+        for got, e, n in zip((dx, *g), want, ("dInput", "WQGrad", "biasQGrad", "WKGrad", "biasKGrad",
+                                               "WVGrad", "biasVGrad")):
+            parity(got, e, f"BackpropQKV {rows}x{ind} {n}")
+        wg0, bg0, dx0 = M(out, ind, 90), Vec(out, 91), M(rows, ind, 92)
+        want = O.backprop_linear_projection(x, dq, w[0], wg0, bg0, dx0)
+        wg, bg, dxi = wg0.copy(), bg0.copy(), dx0.copy()
+        mgr.BackpropLinearProjection(x, dq, w[0], wg, bg, dxi)
+        for got, e, n in zip((wg, bg, dxi), want, ("weightGrad", "biasGrad", "dInput")):
+            parity(got, e, f"BackpropLinearProjection {rows}x{ind} {n}")
+    seq, outd, emb = 4, 8, 6
+    dl, x, w = M(seq, outd, 93), M(seq, emb, 94), M(outd, emb, 95)
+    wg0, bg0 = M(outd, emb, 96), Vec(outd, 97)
+    want = O.backprop_output_projection(dl, x, w, wg0, bg0)
+    wg, bg = wg0.copy(), bg0.copy()
+    dX = mgr.BackpropOutputProjection(dl, x, w, wg, bg, seq, outd, emb)
+    for got, e, n in zip((dX, wg, bg), want, ("dX", "weightGrad", "biasGrad")):
+        parity(got, e, f"BackpropOutputProjection {n}")
+    # the LM-head shape of config 1: vocab 200, D 64, 64 rows
+    dl, x, w = synth.normal(98, (64, 200)), synth.normal(99, (64, 64)), M(200, 64, 100)
+    wg0, bg0 = np.zeros((200, 64), np.float32), np.zeros(200, np.float32)
+    want = O.backprop_output_projection(dl, x, w, wg0, bg0)
+    wg, bg = wg0.copy(), bg0.copy()
+    dX = mgr.BackpropOutputProjection(dl, x, w, wg, bg, 64, 200, 64)
+    for got, e, n in zip((dX, wg, bg), want, ("dX", "weightGrad", "biasGrad")):
+        parity(got, e, f"BackpropOutputProjection LM head {n}")
+
+
 def test_manager_decode_step_matches_prefill(mgr):
     """The decode capability over T steps reproduces causal prefill row by row
     (RoPE at the absolute position, append, attend)."""
