@@ -64,6 +64,15 @@ def lib():
             "ref_backprop_qkv": (i, [_f32p] * 14 + [i, i, i]),
             "ref_backprop_linear_projection": (i, [_f32p] * 6 + [i, i, i]),
             "ref_backprop_output_projection": (i, [_f32p] * 6 + [i, i, i]),
+            "ref_residual_layernorm_forward": (i, [_f32p] * 9 + [i, i, f]),
+            "ref_layernorm_backward": (i, [_f32p] * 9 + [i, i, f]),
+            "ref_cross_entropy": (i, [_f32p, i, i, _i32p, i, i, i, C.POINTER(f), _f32p]),
+            "ref_ffn_input_gradient": (i, [_f32p, _f32p, i, i, _i32p, C.c_void_p, C.c_void_p, _i32p,
+                                           C.c_void_p, C.c_void_p, _f32p]),
+            "ref_accumulate_token_embedding_grad": (i, [_f32p, _f32p, _i32p, i, i, i]),
+            "ref_squared_norm": (f, [_f32p, C.c_long]),
+            "ref_scale_inplace": (None, [_f32p, C.c_long, f]),
+            "ref_sgd_update": (None, [_f32p, _f32p, C.c_long, f]),
             "mt_num_threads": (i, []),
             "mt_set_threads": (None, [i]),
             "mt_project_qkv": (i, [_f32p] * 10 + [i, i, i]),
@@ -301,6 +310,229 @@ def backprop_output_projection(dl, x, w, w_grad, b_grad):
     _check(lib().ref_backprop_output_projection(dl, x, _f32(w), wg, bg, dx, rows, out_dim, emb),
            "BackpropOutputProjection")
     return dx, wg, bg
+
+
+# ---- training step (refcpu_train.c) ---------------------------------------
+
+def residual_layernorm_forward(a, b, gamma, beta, eps: float = 1e-5):
+    """AccelerationCPU.ResidualLayerNormForward -> (out, means, variances, normalized, residual)."""
+    a, b = _f32(a), _f32(b)
+    rows, f = a.shape
+    out, norm, res = (np.empty((rows, f), np.float32) for _ in range(3))
+    mean, var = np.empty(rows, np.float32), np.empty(rows, np.float32)
+    _check(lib().ref_residual_layernorm_forward(a, b, _f32(gamma), _f32(beta), out, mean, var, norm, res,
+                                                rows, f, eps), "ResidualLayerNormForward")
+    return out, mean, var, norm, res
+
+
+def layernorm_backward(dout, normalized, gamma, inp, mean, var, eps: float = 1e-5):
+    """AccelerationCPU.LayerNormBackward -> (dInput, dGamma, dBeta)."""
+    dout = _f32(dout)
+    rows, f = dout.shape
+    dx = np.empty((rows, f), np.float32)
+    dg, db = np.empty(f, np.float32), np.empty(f, np.float32)
+    _check(lib().ref_layernorm_backward(dout, _f32(normalized), _f32(gamma), _f32(inp), _f32(mean), _f32(var),
+                                        dx, dg, db, rows, f, eps), "LayerNormBackward")
+    return dx, dg, db
+
+
+def cross_entropy(logits, targets, effective_len: int, target_start: int = 0):
+    """AccelerationCPU.CrossEntropyLossAndGradient -> (loss, dLogits)."""
+    logits = _f32(logits)
+    t = np.ascontiguousarray(targets, dtype=np.int32)
+    rows, v = logits.shape
+    dl = np.empty((rows, v), np.float32)
+    loss = C.c_float(0)
+    _check(lib().ref_cross_entropy(logits, rows, v, t, t.size, target_start, effective_len, C.byref(loss), dl),
+           "CrossEntropyLossAndGradient")
+    return float(np.float32(loss.value)), dl
+
+
+def ffn_input_gradient(inp, dout, weights, biases, acts, wgrads=None, bgrads=None):
+    """NeuralNetwork.ComputeInputGradientBatch: returns dInput; wgrads / bgrads
+    (lists of float32 arrays, one per weight layer) accumulate in place."""
+    inp, dout = _f32(inp), _f32(dout)
+    rows = inp.shape[0]
+    n = len(weights)
+    ws = [_f32(w) for w in weights]
+    bs = [_f32(b) for b in biases]
+    widths = np.array([ws[0].shape[1]] + [w.shape[0] for w in ws], np.int32)
+    a = np.array(acts, np.int32)
+    P = C.c_void_p * n
+    wp, bp = P(*[w.ctypes.data for w in ws]), P(*[b.ctypes.data for b in bs])
+    if wgrads is not None:
+        for g in list(wgrads) + list(bgrads):
+            assert g.dtype == np.float32 and g.flags.c_contiguous
+        wgp, bgp = P(*[g.ctypes.data for g in wgrads]), P(*[g.ctypes.data for g in bgrads])
+    else:
+        wgp = bgp = None
+    dx = np.empty((rows, widths[0]), np.float32)
+    _check(lib().ref_ffn_input_gradient(inp, dout, rows, n, widths, wp, bp, a, wgp, bgp, dx),
+           "ComputeInputGradientBatch")
+    return dx
+
+
+def accumulate_token_embedding_grad(eg, dx, ids):
+    """AccelerationCPU.AccumulateTokenEmbeddingGrad on a copy of eg."""
+    eg = _f32(eg).copy()
+    dx = _f32(dx)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    _check(lib().ref_accumulate_token_embedding_grad(eg, dx, ids, ids.size, eg.shape[1], eg.shape[0]),
+           "AccumulateTokenEmbeddingGrad")
+    return eg
+
+
+def squared_norm(x) -> float:
+    x = _f32(x)
+    return float(np.float32(lib().ref_squared_norm(x, x.size)))
+
+
+def scale_inplace(x, scale: float):
+    assert x.dtype == np.float32 and x.flags.c_contiguous
+    lib().ref_scale_inplace(x, x.size, scale)
+
+
+def sgd_update(w, g, lr: float):
+    assert w.dtype == np.float32 and w.flags.c_contiguous
+    lib().ref_sgd_update(w, _f32(g), w.size, lr)
+
+
+# Parameter order of the trainer's ZeroAllGradients / ComputeGradientNorm /
+# ScaleGradients / UpdateParameters walks (TransformerTrainer.cs:1269-1400).
+_ATTN = ("wq", "wk", "wv", "wo")
+_ATTN_B = ("bq", "bk", "bv", "bo")
+
+
+def train_step(cfg: dict, weights: dict, seqs, lr: float, clip: float = 1.0, use_clipping: bool = True):
+    """TransformerTrainer.TrainBatchDiscrete (TransformerTrainer.cs:217-327) for
+    one bucket of equal-length token sequences [B, S + 1]: forward with cache
+    (:540-622, segmented attention :723-848 when B > 1), cross-entropy over
+    the B * S next-token targets (:660-674), dLogits scaled by B, backward
+    (:874-987, 989-1060), gradients scaled by 1/B, global-norm clipping and
+    the SGD update (:1269-1384).  ``weights`` (the lm_weights layout) is not
+    modified.  Returns (loss, grads, new_weights); grads are the gradients the
+    update applied (after the 1/B and clipping scales), keyed like weights,
+    plus ``norm`` (the pre-clipping global norm)."""
+    seqs = np.ascontiguousarray(seqs, dtype=np.int32)
+    B, S = seqs.shape[0], seqs.shape[1] - 1
+    D, H, nl = cfg["dim"], cfg["heads"], cfg["layers"]
+    hd = D // H
+    act = cfg.get("ffn_activation", 3)
+    ids, targets = seqs[:, :S].reshape(-1), seqs[:, 1:].reshape(-1)
+    rows = B * S
+    w = weights
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+
+    def seg_rope(m, inverse=False):
+        out = m.copy()
+        for b in range(B):
+            out[b * S:(b + 1) * S] = rope(m[b * S:(b + 1) * S], H, inverse=inverse)
+        return out
+
+    # forward with cache
+    x = embed_tokens(ids, w["token_embedding"])
+    cache = []
+    for L in w["layers"]:
+        c = {"input": x}
+        q, k, v = project_qkv(x, L["wq"], L["bq"], L["wk"], L["bk"], L["wv"], L["bv"])
+        q, k = seg_rope(q), seg_rope(k)
+        att = np.vstack([sdpa(q[b * S:(b + 1) * S], k[b * S:(b + 1) * S], v[b * S:(b + 1) * S], H, causal=True)
+                         for b in range(B)])
+        c.update(q=q, k=k, v=v, att=att)
+        ao = project_output_batch(att, L["wo"], L["bo"])
+        n1, c["m1"], c["v1"], c["n1"], c["r1"] = residual_layernorm_forward(x, ao, L["ln1_g"], L["ln1_b"])
+        c["normed1"] = n1
+        h = batch_dot_add_bias(L["ffn_w1"], n1, L["ffn_b1"])
+        h = activation(h, act)
+        ff = batch_dot_add_bias(L["ffn_w2"], h, L["ffn_b2"])
+        x, c["m2"], c["v2"], c["n2"], c["r2"] = residual_layernorm_forward(n1, ff, L["ln2_g"], L["ln2_b"])
+        cache.append(c)
+    logits = project_output_batch(x, w["out_proj"], w["out_bias"])
+    loss, dl = cross_entropy(logits, targets, rows)
+    if B > 1:
+        scale_inplace(dl, float(B))
+
+    z = lambda a: np.zeros_like(_f32(a))
+    g = {"token_embedding": z(w["token_embedding"]), "out_proj": z(w["out_proj"]), "out_bias": z(w["out_bias"]),
+         "layers": [{k: z(v) for k, v in L.items()} for L in w["layers"]]}
+    dx, g["out_proj"], g["out_bias"] = backprop_output_projection(dl, x, w["out_proj"], g["out_proj"],
+                                                                  g["out_bias"])
+    for li in reversed(range(nl)):
+        L, c, G = w["layers"][li], cache[li], g["layers"][li]
+        dr2, dg2, db2 = layernorm_backward(dx, c["n2"], L["ln2_g"], c["r2"], c["m2"], c["v2"])
+        G["ln2_g"] += dg2
+        G["ln2_b"] += db2
+        wg, bg = [G["ffn_w1"], G["ffn_w2"]], [G["ffn_b1"], G["ffn_b2"]]
+        dn1 = ffn_input_gradient(c["normed1"], dr2, [L["ffn_w1"], L["ffn_w2"]], [L["ffn_b1"], L["ffn_b2"]],
+                                 [act, 0], wg, bg)
+        dn1 += dr2
+        dr1, dg1, db1 = layernorm_backward(dn1, c["n1"], L["ln1_g"], c["r1"], c["m1"], c["v1"])
+        G["ln1_g"] += dg1
+        G["ln1_b"] += db1
+        G["wo"], G["bo"], dcat = backprop_linear_projection(c["att"], dr1, L["wo"], G["wo"], G["bo"],
+                                                            np.zeros((rows, D), np.float32))
+        parts = [mha_backward(c["q"][b * S:(b + 1) * S], c["k"][b * S:(b + 1) * S], c["v"][b * S:(b + 1) * S],
+                              dcat[b * S:(b + 1) * S], H, scale, use_decoder_mask=True) for b in range(B)]
+        dq, dk, dv = (np.vstack([p[i] for p in parts]) for i in range(3))
+        dq, dk = seg_rope(dq, inverse=True), seg_rope(dk, inverse=True)
+        dxa, G["wq"], G["bq"], G["wk"], G["bk"], G["wv"], G["bv"] = backprop_qkv(
+            c["input"], dq, dk, dv, L["wq"], L["wk"], L["wv"], G["wq"], G["bq"], G["wk"], G["bk"], G["wv"], G["bv"])
+        dx = dxa + dr1
+    g["token_embedding"] = accumulate_token_embedding_grad(g["token_embedding"], dx, ids)
+
+    def walk(d):  # every gradient / parameter array once
+        yield d["token_embedding"]
+        yield d["out_proj"]
+        yield d["out_bias"]
+        for L in d["layers"]:
+            for k in _ATTN + _ATTN_B:
+                yield L[k]
+        for L in d["layers"]:
+            yield L["ln1_g"]
+            yield L["ln1_b"]
+        for L in d["layers"]:
+            yield L["ln2_g"]
+            yield L["ln2_b"]
+        for L in d["layers"]:
+            for k in ("ffn_w1", "ffn_w2", "ffn_b1", "ffn_b2"):
+                yield L[k]
+
+    inv = float(np.float32(1.0) / np.float32(B))
+    for a in walk(g):
+        scale_inplace(a, inv)
+    # ComputeGradientNorm (TransformerTrainer.cs:1319-1352): the embedding
+    # gradient over its touched rows in first-use order
+    # (SparseRowGradientTracker.SquaredNorm), then the terms in the trainer's
+    # grouping
+    f32, sn = np.float32, lambda a: np.float32(squared_norm(a))
+    _, first = np.unique(ids, return_index=True)
+    touched = ids[np.sort(first)]
+    total = sn(g["token_embedding"][touched])
+    total = f32(total + sn(g["out_proj"]))
+    total = f32(total + sn(g["out_bias"]))
+    for G in g["layers"]:
+        total = f32(total + f32(f32(f32(sn(G["wq"]) + sn(G["wk"])) + sn(G["wv"])) + sn(G["wo"])))
+        total = f32(total + f32(f32(f32(sn(G["bq"]) + sn(G["bk"])) + sn(G["bv"])) + sn(G["bo"])))
+    for key in ("ln1", "ln2"):
+        for G in g["layers"]:
+            total = f32(total + f32(sn(G[key + "_g"]) + sn(G[key + "_b"])))
+    for G in g["layers"]:
+        for k in ("ffn_w1", "ffn_w2", "ffn_b1", "ffn_b2"):
+            total = f32(total + sn(G[k]))
+    norm = float(np.sqrt(f32(total), dtype=np.float32))
+    g["norm"] = norm
+    neww = {"token_embedding": _f32(w["token_embedding"]).copy(), "out_proj": _f32(w["out_proj"]).copy(),
+            "out_bias": _f32(w["out_bias"]).copy(), "layers": [{k: _f32(v).copy() for k, v in L.items()}
+                                                              for L in w["layers"]]}
+    if not np.isfinite(norm):
+        return loss, g, neww
+    if use_clipping and norm > clip:
+        s = float(np.float32(clip) / np.float32(norm))
+        for a in walk(g):
+            scale_inplace(a, s)
+    for a, p in zip(walk(g), walk(neww)):
+        sgd_update(p, a, lr)
+    return loss, g, neww
 
 
 def num_threads() -> int:

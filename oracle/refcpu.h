@@ -120,6 +120,29 @@ int ref_backprop_output_projection(const float *dl, const float *x,
                                    float *dx, int rows, int out_dim,
                                    int emb_dim);
 
+/* ---- training step (refcpu_train.c) ----------------------------------- */
+
+int ref_residual_layernorm_forward(const float *a, const float *b, const float *gamma,
+                                   const float *beta, float *out, float *means, float *vars,
+                                   float *normalized, float *residual, int rows, int features,
+                                   float eps);
+int ref_layernorm_backward(const float *dout, const float *normalized, const float *gamma,
+                           const float *input, const float *mean, const float *var,
+                           float *dinput, float *dgamma, float *dbeta, int rows, int features,
+                           float eps);
+int ref_cross_entropy(const float *logits, int rows, int out_dim, const int *targets,
+                      int n_targets, int target_start, int effective_len, float *loss,
+                      float *dlogits);
+int ref_ffn_input_gradient(const float *input, const float *dout, int rows, int n_layers,
+                           const int *widths, const float *const *w, const float *const *b,
+                           const int *act, float *const *wgrad, float *const *bgrad,
+                           float *dinput);
+int ref_accumulate_token_embedding_grad(float *eg, const float *dx, const int *ids, int n, int dim,
+                                        int vocab);
+float ref_squared_norm(const float *x, long n);
+void ref_scale_inplace(float *x, long n, float scale);
+void ref_sgd_update(float *w, const float *g, long n, float lr);
+
 /* ---- multi-threaded restatement of AccelerationMutliThreadCPU ---------- */
 
 int mt_num_threads(void);
