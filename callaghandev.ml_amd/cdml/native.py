@@ -79,7 +79,25 @@ SIGNATURES = {
     "cdml_kv_cache_append": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp],
     "cdml_residual_layernorm": [_vp, _vp, _vp, _vp, _vp, _i, _i, _f, _vp],
     "cdml_embed_tokens": [_vp, _i, _vp, _i, _i, _vp, _vp, _vp],
+    "cdml_linear_preact": [_vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
+    "cdml_linear_backward_act": [_vp, _i, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _i, _i,
+                                 _vp, _sz, _vp],
+    "cdml_residual_layernorm_fwd": [_vp] * 9 + [_i, _i, _f, _vp],
+    "cdml_layernorm_backward_workspace_size": [_i, _i, C.POINTER(_sz)],
+    "cdml_layernorm_backward": [_vp] * 10 + [_i, _i, _f, _i, _vp, _sz, _vp],
+    "cdml_cross_entropy_workspace_size": [_i, C.POINTER(_sz)],
+    "cdml_cross_entropy": [_vp, _i, _vp, _i, _i, _i, _f, _f, _vp, _vp, _i, _vp, _sz, _vp],
+    "cdml_embedding_grad": [_vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _i, _vp],
+    "cdml_grad_norm_workspace_size": [_i, C.POINTER(_sz)],
+    "cdml_grad_norm": [_vp, _i, _f, _i, _f, _vp, _vp, _sz, _vp],
+    "cdml_sgd_update": [_vp, _i, _f, _f, _vp, _i, _vp],
 }
+
+
+class Param(C.Structure):
+    """cdml_param: one parameter tensor of cdml_grad_norm / cdml_sgd_update."""
+    _fields_ = [("weight", C.c_void_p), ("grad", C.c_void_p), ("count", C.c_longlong),
+                ("group", C.c_int), ("reserved", C.c_int)]
 
 _lib = None
 

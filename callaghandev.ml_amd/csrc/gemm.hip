@@ -63,6 +63,14 @@ struct GemmArgs {
   // output tiles of all problems (total = tiles * ksplit).
   int ksplit, kchunk, tiles;
   float *ws, *wsb;
+  // Single-problem epilogue options (store_elem): pre receives the
+  // pre-activation acc + bias (forward layers whose backward needs it); dz
+  // multiplies the result by act'(dz) with act = dact (the hidden deltas of
+  // NeuralNetwork.ComputeInputGradientBatch); add is added last (a residual
+  // gradient, MatrixAddInPlace).
+  float *pre;
+  const float *dz, *add;
+  int ldpre, lddz, ldadd, dact;
 };
 
 // Epilogue of both forward GEMM kernels with the rotary embedding of
@@ -107,23 +115,66 @@ __device__ __forceinline__ void store_rope(const GemmArgs &args, const GemmProbl
   }
 }
 
+__device__ __forceinline__ float stable_sigmoid(float x) {
+  if (x >= 0.f) return 1.f / (1.f + expf(-x));
+  const float z = expf(x);
+  return z / (1.f + z);
+}
+
+// Activation derivative at the pre-activation z, as FillActivationAndDerivative
+// (Neural Network/NeuralNetwork.cs:885-944) defines it, including its ReLU
+// derivative of 1 at z = 0 and leaky-ReLU slope 0.1 for z <= 0.
+__device__ __forceinline__ float act_deriv(float z, int act) {
+  switch (act) {
+    case CDML_ACT_SIGMOID: {
+      const float s = stable_sigmoid(z);
+      return s * (1.f - s);
+    }
+    case CDML_ACT_TANH: {
+      const float t = tanhf(z);
+      return 1.f - t * t;
+    }
+    case CDML_ACT_RELU:
+      return z >= 0.f ? 1.f : 0.f;
+    case CDML_ACT_LEAKYRELU:
+      return z <= 0.f ? 0.1f : 1.f;
+    case CDML_ACT_SWISH: {
+      const float s = stable_sigmoid(z);
+      return s + z * s * (1.f - s);
+    }
+    default:
+      return 1.f;
+  }
+}
+
 __device__ __forceinline__ float activate(float x, int act) {
   switch (act) {
     case CDML_ACT_SIGMOID:
-      return x >= 0.f ? 1.f / (1.f + expf(-x)) : expf(x) / (1.f + expf(x));
+      return stable_sigmoid(x);
     case CDML_ACT_TANH:
       return tanhf(x);
     case CDML_ACT_RELU:
       return x > 0.f ? x : 0.f;
     case CDML_ACT_LEAKYRELU:
       return x > 0.f ? x : 0.01f * x;
-    case CDML_ACT_SWISH: {
-      float s = x >= 0.f ? 1.f / (1.f + expf(-x)) : expf(x) / (1.f + expf(x));
-      return x * s;
-    }
+    case CDML_ACT_SWISH:
+      return x * stable_sigmoid(x);
     default:
       return x;
   }
+}
+
+// Stores output (m, n) of problem P from z = acc + bias: pre <- z,
+// v = act(z), v *= act'(dz) and v += add when those options are set, then
+// C = v (or C + v with beta).
+__device__ __forceinline__ void store_elem(const GemmArgs &args, const GemmProblem &P, int m, int n,
+                                           float z, int act) {
+  if (args.pre) args.pre[(size_t)m * args.ldpre + n] = z;
+  float v = activate(z, act);
+  if (args.dz) v *= act_deriv(args.dz[(size_t)m * args.lddz + n], args.dact);
+  if (args.add) v += args.add[(size_t)m * args.ldadd + n];
+  float *pc = P.c + (size_t)m * args.ldc + n;
+  *pc = args.beta ? *pc + v : v;
 }
 
 // Global -> register staging of one 128x32 tile of a row-major [rows, K]
@@ -267,11 +318,7 @@ __global__ void __launch_bounds__(NTHREADS) gemm_nt_kernel(const GemmArgs args) 
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
-        if (m < M) {
-          float *pc = P.c + (size_t)m * args.ldc + n;
-          const float v = activate(acc[i][j][r] + bias, args.act);
-          *pc = args.beta ? *pc + v : v;
-        }
+        if (m < M) store_elem(args, P, m, n, acc[i][j][r] + bias, args.act);
       }
     }
   }
@@ -530,11 +577,7 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const Gem
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + wm * (TM / WM) + i * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
-        if (m < M) {
-          float *pc = P.c + (size_t)m * args.ldc + n;
-          const float v = activate(acc[i][j][r] + bias, ACT == kActRope ? CDML_ACT_NONE : ACT);
-          *pc = args.beta ? *pc + v : v;
-        }
+        if (m < M) store_elem(args, P, m, n, acc[i][j][r] + bias, ACT == kActRope ? CDML_ACT_NONE : ACT);
       }
     }
   }
@@ -584,9 +627,7 @@ __global__ void __launch_bounds__(256) gemm_any_kernel(const GemmArgs args) {
     for (int j = 0; j < 4; ++j) {
       const int n = n0 + tx * 4 + j;
       if (n >= N) continue;
-      float *pc = P.c + (size_t)m * args.ldc + n;
-      const float v = activate(acc[i][j] + (P.bias ? P.bias[n] : 0.f), args.act);
-      *pc = args.beta ? *pc + v : v;
+      store_elem(args, P, m, n, acc[i][j] + (P.bias ? P.bias[n] : 0.f), args.act);
     }
   }
 }
@@ -884,18 +925,21 @@ extern "C" int cdml_linear(const float *x, int ldx, const float *w, const float 
   return launch_gemm(g, false, false, as_hip(stream), "cdml_linear");
 }
 
-extern "C" int cdml_linear_backward(const float *x, int ldx, const float *dy, int lddy,
-                                    const float *w, float *dx, int lddx, float *wgrad,
-                                    float *bgrad, int rows, int in_dim, int out_dim,
-                                    int accumulate_dx, void *workspace, size_t workspace_bytes,
-                                    cdml_stream stream) {
-  if (rows < 0 || in_dim < 0 || out_dim < 0)
-    return fail(CDML_E_INVALID, "cdml_linear_backward: negative size");
+namespace {
+
+// cdml_linear_backward with the epilogue options of the input gradient:
+// dx = (dY W) * act'(dz) + add (dz / add NULL: not applied; both use row
+// stride lddx), or dx += dY W with accumulate_dx.
+int linear_backward_impl(const float *x, int ldx, const float *dy, int lddy, const float *w,
+                         const float *dz, int dact, const float *add, float *dx, int lddx,
+                         float *wgrad, float *bgrad, int rows, int in_dim, int out_dim,
+                         int accumulate_dx, void *workspace, size_t workspace_bytes,
+                         cdml_stream stream, const char *what) {
+  if (rows < 0 || in_dim < 0 || out_dim < 0) return fail(CDML_E_INVALID, "%s: negative size", what);
   if (lddy < out_dim || (dx && lddx < in_dim) || (wgrad && ldx < in_dim))
-    return fail(CDML_E_INVALID, "cdml_linear_backward: row stride smaller than the row");
+    return fail(CDML_E_INVALID, "%s: row stride smaller than the row", what);
   if (rows == 0) return CDML_OK;
-  if (!dy || (dx && !w) || (wgrad && !x))
-    return fail(CDML_E_INVALID, "cdml_linear_backward: NULL pointer");
+  if (!dy || (dx && !w) || (wgrad && !x)) return fail(CDML_E_INVALID, "%s: NULL pointer", what);
   int rc = ensure_device();
   if (rc) return rc;
   hipStream_t st = as_hip(stream);
@@ -911,7 +955,12 @@ extern "C" int cdml_linear_backward(const float *x, int ldx, const float *dy, in
     g.nprob = 1;
     g.p[0] = {dy, w, nullptr, dx, nullptr};
     g.beta = accumulate_dx ? 1 : 0;
-    rc = launch_gemm(g, false, true, st, "cdml_linear_backward (input gradient)");
+    g.dz = dz;
+    g.lddz = lddx;
+    g.dact = dact;
+    g.add = add;
+    g.ldadd = lddx;
+    rc = launch_gemm(g, false, true, st, what);
     if (rc) return rc;
   }
   if ((wgrad || bgrad) && out_dim > 0) {
@@ -928,16 +977,69 @@ extern "C" int cdml_linear_backward(const float *x, int ldx, const float *dy, in
     g.p[0] = {dy, x, nullptr, wgrad, bgrad};
     g.beta = 1;
     if (wgrad && in_dim > 0) {
-      rc = attach_split(g, workspace, workspace_bytes, "cdml_linear_backward");
+      rc = attach_split(g, workspace, workspace_bytes, what);
       if (rc) return rc;
-      rc = launch_gemm(g, true, true, st, "cdml_linear_backward (weight gradient)");
+      rc = launch_gemm(g, true, true, st, what);
     } else if (bgrad) {
       op_rowsum_kernel<true><<<dim3((out_dim + 255) / 256, 1), dim3(256), 0, st>>>(g);
-      rc = check_launch("cdml_linear_backward (bias gradient)");
+      rc = check_launch(what);
     }
     if (rc) return rc;
   }
   return CDML_OK;
+}
+
+}  // namespace
+
+extern "C" int cdml_linear_backward(const float *x, int ldx, const float *dy, int lddy,
+                                    const float *w, float *dx, int lddx, float *wgrad,
+                                    float *bgrad, int rows, int in_dim, int out_dim,
+                                    int accumulate_dx, void *workspace, size_t workspace_bytes,
+                                    cdml_stream stream) {
+  return linear_backward_impl(x, ldx, dy, lddy, w, nullptr, CDML_ACT_NONE, nullptr, dx, lddx, wgrad,
+                              bgrad, rows, in_dim, out_dim, accumulate_dx, workspace, workspace_bytes,
+                              stream, "cdml_linear_backward");
+}
+
+extern "C" int cdml_linear_backward_act(const float *x, int ldx, const float *dy, int lddy,
+                                        const float *w, const float *dz, int activation,
+                                        const float *add, float *dx, int lddx, float *wgrad,
+                                        float *bgrad, int rows, int in_dim, int out_dim,
+                                        void *workspace, size_t workspace_bytes,
+                                        cdml_stream stream) {
+  if (activation < CDML_ACT_NONE || activation > CDML_ACT_SWISH)
+    return fail(CDML_E_INVALID, "cdml_linear_backward_act: unknown activation %d", activation);
+  return linear_backward_impl(x, ldx, dy, lddy, w, dz, activation, add, dx, lddx, wgrad, bgrad,
+                              rows, in_dim, out_dim, 0, workspace, workspace_bytes, stream,
+                              "cdml_linear_backward_act");
+}
+
+extern "C" int cdml_linear_preact(const float *x, int ldx, const float *w, const float *b, float *z,
+                                  float *y, int ldy, int rows, int in_dim, int out_dim,
+                                  int activation, cdml_stream stream) {
+  if (rows < 0 || in_dim < 0 || out_dim < 0)
+    return fail(CDML_E_INVALID, "cdml_linear_preact: negative size");
+  if (activation < CDML_ACT_NONE || activation > CDML_ACT_SWISH)
+    return fail(CDML_E_INVALID, "cdml_linear_preact: unknown activation %d", activation);
+  if (rows == 0 || out_dim == 0) return CDML_OK;
+  if (!x || !w || !y || !z) return fail(CDML_E_INVALID, "cdml_linear_preact: NULL pointer");
+  if (ldx < in_dim || ldy < out_dim)
+    return fail(CDML_E_INVALID, "cdml_linear_preact: row stride smaller than the row");
+  int rc = ensure_device();
+  if (rc) return rc;
+  GemmArgs g{};
+  g.lda = ldx;
+  g.ldb = in_dim;
+  g.ldc = ldy;
+  g.M = rows;
+  g.N = out_dim;
+  g.K = in_dim;
+  g.nprob = 1;
+  g.p[0] = {x, w, b, y, nullptr};
+  g.act = activation;
+  g.pre = z;
+  g.ldpre = ldy;
+  return launch_gemm(g, false, false, as_hip(stream), "cdml_linear_preact");
 }
 
 extern "C" int cdml_backprop_qkv(const float *x, const float *dq, const float *dk, const float *dv,

@@ -1,0 +1,540 @@
+// Training-step kernels of the decoder LM (TransformerTrainer.TrainBatchDiscrete,
+// Transformers/MultiTypeTransformer/TransformerTrainer.cs:217-327): the
+// LayerNorm forward with its cache and its backward, the cross-entropy loss
+// and gradient, the token-embedding gradient, and the global-norm clipping
+// and SGD update over every parameter.  All reductions run in a fixed order
+// (no atomics), so a step gives the same bits on every run.
+#include <cmath>
+
+#include "common.h"
+
+namespace cdml {
+namespace {
+
+constexpr int kRowCache = 32;  // features kept in registers per lane (64 * 32 = 2048)
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+
+// ResidualLayerNormForward (AccelerationCPU.cs:1440-1514) for one row per
+// wave: residual = a + b, mean, biased variance (two passes), out = gamma *
+// (residual - mean) * invStd + beta; mean / var / residual / normalized are
+// written when non-NULL.
+__global__ void __launch_bounds__(256) ln_forward_kernel(const float *__restrict__ a,
+                                                         const float *__restrict__ b,
+                                                         const float *__restrict__ gamma,
+                                                         const float *__restrict__ beta,
+                                                         float *__restrict__ out,
+                                                         float *__restrict__ mean_out,
+                                                         float *__restrict__ var_out,
+                                                         float *__restrict__ res_out,
+                                                         float *__restrict__ norm_out, int rows,
+                                                         int f, float eps) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const size_t base = (size_t)row * f;
+  float cache[kRowCache];
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < kRowCache; ++i) {
+    const int j = lane + 64 * i;
+    cache[i] = j < f ? a[base + j] + b[base + j] : 0.f;
+    sum += cache[i];
+  }
+  const float mean = wave_sum(sum) / (float)f;
+  float var = 0.f;
+#pragma unroll
+  for (int i = 0; i < kRowCache; ++i) {
+    const int j = lane + 64 * i;
+    const float d = cache[i] - mean;
+    var += j < f ? d * d : 0.f;
+  }
+  var = wave_sum(var) / (float)f;
+  const float inv_std = 1.0f / sqrtf(var + eps);
+#pragma unroll
+  for (int i = 0; i < kRowCache; ++i) {
+    const int j = lane + 64 * i;
+    if (j < f) {
+      const float n = (cache[i] - mean) * inv_std;
+      out[base + j] = gamma[j] * n + beta[j];
+      if (res_out) res_out[base + j] = cache[i];
+      if (norm_out) norm_out[base + j] = n;
+    }
+  }
+  if (lane == 0) {
+    if (mean_out) mean_out[row] = mean;
+    if (var_out) var_out[row] = var;
+  }
+}
+
+// LayerNormBackward (AccelerationCPU.cs:1516-1564), dX part: one row per
+// wave.  g = dout (+ dout2: the two gradients of a residual branch, summed
+// first as MatrixAddInPlace does); normalized is recomputed from the
+// residual input when not given.  Each workgroup owns kLnRowsPerBlock rows
+// and writes its partial column sums of g * normalized and g to the
+// workspace for ln_param_grad_kernel.
+constexpr int kLnRowsPerBlock = 64;
+
+__global__ void __launch_bounds__(256) ln_backward_kernel(
+    const float *__restrict__ dout, const float *__restrict__ dout2,
+    const float *__restrict__ normalized, const float *__restrict__ gamma,
+    const float *__restrict__ x, const float *__restrict__ mean, const float *__restrict__ var,
+    float *__restrict__ dx, float *__restrict__ part_g, float *__restrict__ part_b, int rows,
+    int f, float eps) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row0 = blockIdx.x * kLnRowsPerBlock;
+  float pg[kRowCache], pb[kRowCache];
+#pragma unroll
+  for (int i = 0; i < kRowCache; ++i) pg[i] = pb[i] = 0.f;
+  for (int rr = wave; rr < kLnRowsPerBlock; rr += 4) {
+    const int row = row0 + rr;
+    if (row >= rows) break;
+    const size_t base = (size_t)row * f;
+    const float inv_std = 1.0f / sqrtf(var[row] + eps);
+    const float inv_std3 = inv_std * inv_std * inv_std;
+    const float m = mean[row];
+    float gv[kRowCache], xm[kRowCache];
+    float dvar = 0.f, dmean = 0.f;
+#pragma unroll
+    for (int i = 0; i < kRowCache; ++i) {
+      const int j = lane + 64 * i;
+      gv[i] = 0.f;
+      xm[i] = 0.f;
+      if (j < f) {
+        float g = dout[base + j];
+        if (dout2) g += dout2[base + j];
+        const float xmj = x[base + j] - m;
+        const float n = normalized ? normalized[base + j] : xmj * inv_std;
+        pg[i] += g * n;
+        pb[i] += g;
+        const float dnorm = g * gamma[j];
+        dvar += dnorm * xmj * (-0.5f) * inv_std3;
+        dmean += dnorm * (-inv_std);
+        gv[i] = g;
+        xm[i] = xmj;
+      }
+    }
+    dvar = wave_sum(dvar);
+    dmean = wave_sum(dmean);
+    const float inv_n = 1.0f / (float)f;
+    const float dvar_scale = dvar * 2.0f * inv_n;
+    const float dmean_scale = dmean * inv_n;
+#pragma unroll
+    for (int i = 0; i < kRowCache; ++i) {
+      const int j = lane + 64 * i;
+      if (j < f) dx[base + j] = (gv[i] * gamma[j]) * inv_std + dvar_scale * xm[i] + dmean_scale;
+    }
+  }
+  // the four waves' column partials meet in LDS, in wave order
+  __shared__ float red[4][64];
+#pragma unroll
+  for (int i = 0; i < kRowCache; ++i) {
+    if (64 * i >= f) break;  // uniform
+    red[wave][lane] = pg[i];
+    __syncthreads();
+    const int j = lane + 64 * i;
+    if (wave == 0 && j < f)
+      part_g[(size_t)blockIdx.x * f + j] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+    __syncthreads();
+    red[wave][lane] = pb[i];
+    __syncthreads();
+    if (wave == 0 && j < f)
+      part_b[(size_t)blockIdx.x * f + j] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+    __syncthreads();
+  }
+}
+
+// dGamma / dBeta: the row-block partials summed in block order; written, or
+// added to the caller's accumulators (the trainer's VectorAccumulate).
+__global__ void __launch_bounds__(256) ln_param_grad_kernel(const float *__restrict__ part_g,
+                                                            const float *__restrict__ part_b,
+                                                            float *__restrict__ dgamma,
+                                                            float *__restrict__ dbeta, int nblk,
+                                                            int f, int accumulate) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= f) return;
+  float sg = 0.f, sb = 0.f;
+  for (int k = 0; k < nblk; ++k) {
+    sg += part_g[(size_t)k * f + j];
+    sb += part_b[(size_t)k * f + j];
+  }
+  if (dgamma) dgamma[j] = accumulate ? dgamma[j] + sg : sg;
+  if (dbeta) dbeta[j] = accumulate ? dbeta[j] + sb : sb;
+}
+
+// CrossEntropyLossAndGradient (AccelerationCPU.cs:2377-2440): one workgroup per
+// row.  Rows below effective_len: p = exp(l - max) / sum, loss term
+// -log(p[target] + 1e-10), gradient (p / effective_len, minus 1 / effective_len
+// at the target) times grad_scale; rows at or past effective_len get a zero
+// gradient.  grad_scale is the trainer's ScaleMatrixLocal of a bucket
+// (TransformerTrainer.cs:291-294), 1 otherwise.
+__global__ void __launch_bounds__(256) ce_row_kernel(const float *__restrict__ logits, int ldl,
+                                                     const int *__restrict__ targets, int rows,
+                                                     int v, int effective_len, float grad_scale,
+                                                     float *__restrict__ dl, int lddl,
+                                                     float *__restrict__ row_loss) {
+  const int row = blockIdx.x;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const float *l = logits + (size_t)row * ldl;
+  float *g = dl + (size_t)row * lddl;
+  if (row >= effective_len) {
+    for (int j = t; j < v; j += 256) g[j] = 0.f;
+    return;
+  }
+  __shared__ float red[4];
+  float mx = -INFINITY;
+  for (int j = t; j < v; j += 256) mx = fmaxf(mx, l[j]);
+  mx = wave_max(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float sum = 0.f;
+  for (int j = t; j < v; j += 256) {
+    const float e = expf(l[j] - mx);
+    g[j] = e;
+    sum += e;
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) red[wave] = sum;
+  __syncthreads();
+  sum = ((red[0] + red[1]) + red[2]) + red[3];
+  const float inv_sum = 1.0f / sum;
+  const float inv_len = 1.0f / (float)effective_len;
+  const int target = targets[row];
+  if (t == 0 && (target < 0 || target >= v)) row_loss[row] = NAN;  // surfaces as a non-finite loss
+  for (int j = t; j < v; j += 256) {
+    float gr = (g[j] * inv_sum) * inv_len;
+    if (j == target) {
+      row_loss[row] = -logf((g[j] * inv_sum) + 1e-10f);
+      gr -= inv_len;
+    }
+    g[j] = gr * grad_scale;
+  }
+}
+
+// loss = sum of the row terms (fixed order) / effective_len, times loss_scale.
+__global__ void __launch_bounds__(256) ce_loss_kernel(const float *__restrict__ row_loss, int n,
+                                                      float loss_scale, float *__restrict__ loss) {
+  __shared__ float red[256];
+  float s = 0.f;
+  for (int i = threadIdx.x; i < n; i += 256) s += row_loss[i];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *loss = (red[0] / (float)n) * loss_scale;
+}
+
+// AccumulateTokenEmbeddingGrad (AccelerationCPU.cs:2339-2370) as a gather: group
+// k adds rows order[start[k] .. start[k+1]) of dx (+ dx2) to row token[k] of
+// the gradient, one column per thread, rows in increasing order (the
+// reference's order), so repeated tokens need no atomics.
+__global__ void __launch_bounds__(256) embed_grad_kernel(float *__restrict__ eg,
+                                                         const float *__restrict__ dx,
+                                                         const float *__restrict__ dx2, int ldx,
+                                                         const int *__restrict__ order,
+                                                         const int *__restrict__ start,
+                                                         const int *__restrict__ token, int dim) {
+  const int k = blockIdx.x;
+  const int j = blockIdx.y * 256 + threadIdx.x;
+  if (j >= dim) return;
+  float *dst = eg + (size_t)token[k] * dim + j;
+  float v = *dst;
+  for (int r = start[k]; r < start[k + 1]; ++r) {
+    const size_t o = (size_t)order[r] * ldx + j;
+    v += dx2 ? dx[o] + dx2[o] : dx[o];
+  }
+  *dst = v;
+}
+
+constexpr int kNormBlocks = 512;
+
+// Squared norm of every parameter's gradient after `prescale` (the trainer's
+// ScaleGradients by 1 / validCount, TransformerTrainer.cs:313): each block
+// walks every tensor with a stride of kNormBlocks float4s and writes one
+// partial per tensor.
+__global__ void __launch_bounds__(256) sumsq_kernel(const cdml_param *__restrict__ params,
+                                                    int count, float prescale,
+                                                    float *__restrict__ partial) {
+  __shared__ float red[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int t = 0; t < count; ++t) {
+    const float *g = params[t].grad;
+    const long long n = params[t].count;
+    float s = 0.f;
+    if ((reinterpret_cast<uintptr_t>(g) & 15) == 0) {
+      const long long n4 = n >> 2;
+      for (long long e = (long long)blockIdx.x * 256 + threadIdx.x; e < n4; e += (long long)kNormBlocks * 256) {
+        const vf4 x = reinterpret_cast<const vf4 *>(g)[e];
+        const float a0 = x[0] * prescale, a1 = x[1] * prescale, a2 = x[2] * prescale, a3 = x[3] * prescale;
+        s += ((a0 * a0 + a1 * a1) + a2 * a2) + a3 * a3;
+      }
+      for (long long e = (n4 << 2) + (long long)blockIdx.x * 256 + threadIdx.x; e < n;
+           e += (long long)kNormBlocks * 256) {
+        const float a = g[e] * prescale;
+        s += a * a;
+      }
+    } else {
+      for (long long e = (long long)blockIdx.x * 256 + threadIdx.x; e < n; e += (long long)kNormBlocks * 256) {
+        const float a = g[e] * prescale;
+        s += a * a;
+      }
+    }
+    s = wave_sum(s);
+    if (lane == 0) red[wave] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) partial[(size_t)t * kNormBlocks + blockIdx.x] = ((red[0] + red[1]) + red[2]) + red[3];
+    __syncthreads();
+  }
+}
+
+// ComputeGradientNorm + ClipGradients (TransformerTrainer.cs:1306-1352): the
+// per-tensor sums in block order, tensors with equal consecutive group ids
+// summed first (the trainer adds WQ + WK + WV + WO before adding them to the
+// total), norm = sqrt(total).  result[0] = norm, result[1] = the clipping
+// factor (threshold / norm when clipping and norm > threshold, else 1),
+// result[2] = 1 when the norm is finite (the update runs), else 0.
+__global__ void __launch_bounds__(64) norm_finalize_kernel(const cdml_param *__restrict__ params,
+                                                           int count,
+                                                           const float *__restrict__ partial,
+                                                           int use_clipping, float threshold,
+                                                           float *__restrict__ result) {
+  __shared__ float tensor_sum[64];
+  float total = 0.f, group_sum = 0.f;
+  int group = 0;
+  for (int t0 = 0; t0 < count; t0 += 64) {
+    const int t = t0 + threadIdx.x;
+    if (t < count) {
+      float s = 0.f;
+      for (int b = 0; b < kNormBlocks; ++b) s += partial[(size_t)t * kNormBlocks + b];
+      tensor_sum[threadIdx.x] = s;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int i = 0; i < 64 && t0 + i < count; ++i) {
+        const int g = params[t0 + i].group;
+        if (t0 + i == 0) {
+          group = g;
+          group_sum = tensor_sum[i];
+        } else if (g == group) {
+          group_sum += tensor_sum[i];
+        } else {
+          total += group_sum;
+          group = g;
+          group_sum = tensor_sum[i];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    if (count > 0) total += group_sum;
+    const float norm = sqrtf(total);
+    const bool finite = isfinite(norm);
+    result[0] = norm;
+    result[1] = (use_clipping && finite && norm > threshold) ? threshold / norm : 1.f;
+    result[2] = finite ? 1.f : 0.f;
+  }
+}
+
+// UpdateParameters (TransformerTrainer.cs:1269-1305, MatrixUpdate
+// AccelerationCPU.cs:2548-2597): g' = (g * prescale) * clip (the in-place
+// ScaleGradients calls, the second only when clipping applied), w -= lr * g'.
+// With a non-finite norm nothing is updated (TransformerTrainer.cs:316-320).
+// zero_grads: the gradients are cleared for the next step (ZeroAllGradients);
+// otherwise g' is written back, as the reference's in-place scaling leaves it.
+__global__ void __launch_bounds__(256) sgd_kernel(const cdml_param *__restrict__ params, int count,
+                                                  float lr, float prescale,
+                                                  const float *__restrict__ result, int zero_grads) {
+#pragma clang fp contract(off)
+  const bool run = result[2] != 0.f;
+  const float clip = result[1];
+  const bool clipped = clip != 1.f;
+  const long long stride = (long long)gridDim.x * 256;
+  for (int t = 0; t < count; ++t) {
+    float *w = params[t].weight, *g = params[t].grad;
+    const long long n = params[t].count;
+    for (long long e = (long long)blockIdx.x * 256 + threadIdx.x; e < n; e += stride) {
+      float gs = g[e] * prescale;
+      if (clipped) gs = gs * clip;
+      if (run) w[e] -= lr * gs;  // multiply and subtract rounded separately, as MatrixUpdate
+      g[e] = zero_grads ? 0.f : gs;
+    }
+  }
+}
+
+}  // namespace
+}  // namespace cdml
+
+using namespace cdml;
+
+extern "C" int cdml_residual_layernorm_fwd(const float *a, const float *b, const float *gamma,
+                                           const float *beta, float *out, float *mean,
+                                           float *variance, float *residual, float *normalized,
+                                           int rows, int features, float eps,
+                                           cdml_stream stream) {
+  if (rows < 0 || features < 0)
+    return fail(CDML_E_INVALID, "cdml_residual_layernorm_fwd: negative size");
+  if (rows == 0 || features == 0) return CDML_OK;
+  if (!a || !b || !gamma || !beta || !out)
+    return fail(CDML_E_INVALID, "cdml_residual_layernorm_fwd: NULL pointer");
+  if (features > 64 * kRowCache)
+    return fail(CDML_E_INVALID, "cdml_residual_layernorm_fwd: more than %d features", 64 * kRowCache);
+  int rc = ensure_device();
+  if (rc) return rc;
+  ln_forward_kernel<<<dim3((rows + 3) / 4), dim3(256), 0, as_hip(stream)>>>(
+      a, b, gamma, beta, out, mean, variance, residual, normalized, rows, features, eps);
+  return check_launch("ln_forward_kernel");
+}
+
+extern "C" int cdml_layernorm_backward_workspace_size(int rows, int features, size_t *bytes) {
+  if (!bytes || rows < 0 || features < 0)
+    return fail(CDML_E_INVALID, "cdml_layernorm_backward_workspace_size: bad argument");
+  const size_t nblk = ((size_t)rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock;
+  *bytes = 2 * nblk * (size_t)features * sizeof(float);
+  return CDML_OK;
+}
+
+extern "C" int cdml_layernorm_backward(const float *dout, const float *dout2,
+                                       const float *normalized, const float *gamma,
+                                       const float *input, const float *mean,
+                                       const float *variance, float *dinput, float *dgamma,
+                                       float *dbeta, int rows, int features, float eps,
+                                       int accumulate, void *workspace, size_t workspace_bytes,
+                                       cdml_stream stream) {
+  if (rows < 0 || features < 0)
+    return fail(CDML_E_INVALID, "cdml_layernorm_backward: negative size");
+  if (features == 0) return CDML_OK;
+  if (features > 64 * kRowCache)
+    return fail(CDML_E_INVALID, "cdml_layernorm_backward: more than %d features", 64 * kRowCache);
+  if (!dout || !gamma || !input || !mean || !variance || !dinput)
+    return fail(CDML_E_INVALID, "cdml_layernorm_backward: NULL pointer");
+  size_t need = 0;
+  cdml_layernorm_backward_workspace_size(rows, features, &need);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(CDML_E_INVALID, "cdml_layernorm_backward: workspace of %zu bytes needed, %zu given", need,
+                workspace_bytes);
+  int rc = ensure_device();
+  if (rc) return rc;
+  hipStream_t st = as_hip(stream);
+  const int nblk = (rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock;
+  float *pg = static_cast<float *>(workspace), *pb = pg + (size_t)nblk * features;
+  if (rows > 0) {
+    ln_backward_kernel<<<dim3(nblk), dim3(256), 0, st>>>(dout, dout2, normalized, gamma, input, mean,
+                                                         variance, dinput, pg, pb, rows, features, eps);
+    rc = check_launch("ln_backward_kernel");
+    if (rc) return rc;
+  }
+  if (dgamma || dbeta) {
+    ln_param_grad_kernel<<<dim3((features + 255) / 256), dim3(256), 0, st>>>(pg, pb, dgamma, dbeta, nblk,
+                                                                             features, accumulate);
+    rc = check_launch("ln_param_grad_kernel");
+  }
+  return rc;
+}
+
+extern "C" int cdml_cross_entropy_workspace_size(int rows, size_t *bytes) {
+  if (!bytes || rows < 0) return fail(CDML_E_INVALID, "cdml_cross_entropy_workspace_size: bad argument");
+  *bytes = (size_t)(rows > 0 ? rows : 1) * sizeof(float);
+  return CDML_OK;
+}
+
+extern "C" int cdml_cross_entropy(const float *logits, int ldl, const int *targets, int rows,
+                                  int out_dim, int effective_len, float grad_scale,
+                                  float loss_scale, float *loss, float *dlogits, int lddl,
+                                  void *workspace, size_t workspace_bytes, cdml_stream stream) {
+  if (rows < 0 || out_dim <= 0 || effective_len < 0 || effective_len > rows)
+    return fail(CDML_E_INVALID, "cdml_cross_entropy: bad size");
+  if (ldl < out_dim || lddl < out_dim)
+    return fail(CDML_E_INVALID, "cdml_cross_entropy: row stride smaller than the row");
+  if (!logits || !dlogits || !loss || (effective_len > 0 && !targets))
+    return fail(CDML_E_INVALID, "cdml_cross_entropy: NULL pointer");
+  if (!workspace || workspace_bytes < (size_t)(rows > 0 ? rows : 1) * sizeof(float))
+    return fail(CDML_E_INVALID, "cdml_cross_entropy: workspace too small");
+  int rc = ensure_device();
+  if (rc) return rc;
+  hipStream_t st = as_hip(stream);
+  float *row_loss = static_cast<float *>(workspace);
+  if (rows > 0) {
+    ce_row_kernel<<<dim3(rows), dim3(256), 0, st>>>(logits, ldl, targets, rows, out_dim, effective_len,
+                                                    grad_scale, dlogits, lddl, row_loss);
+    rc = check_launch("ce_row_kernel");
+    if (rc) return rc;
+  }
+  if (effective_len == 0) return cdml_zero_f32_async(loss, 1, stream);
+  ce_loss_kernel<<<dim3(1), dim3(256), 0, st>>>(row_loss, effective_len, loss_scale, loss);
+  return check_launch("ce_loss_kernel");
+}
+
+extern "C" int cdml_embedding_grad(float *grad, const float *dx, const float *dx2, int ldx,
+                                   const int *order, const int *group_start,
+                                   const int *group_token, int n_groups, int dim,
+                                   cdml_stream stream) {
+  if (n_groups < 0 || dim < 0 || ldx < dim) return fail(CDML_E_INVALID, "cdml_embedding_grad: bad size");
+  if (n_groups == 0 || dim == 0) return CDML_OK;
+  if (!grad || !dx || !order || !group_start || !group_token)
+    return fail(CDML_E_INVALID, "cdml_embedding_grad: NULL pointer");
+  int rc = ensure_device();
+  if (rc) return rc;
+  embed_grad_kernel<<<dim3(n_groups, (dim + 255) / 256), dim3(256), 0, as_hip(stream)>>>(
+      grad, dx, dx2, ldx, order, group_start, group_token, dim);
+  return check_launch("embed_grad_kernel");
+}
+
+extern "C" int cdml_grad_norm_workspace_size(int count, size_t *bytes) {
+  if (!bytes || count < 0) return fail(CDML_E_INVALID, "cdml_grad_norm_workspace_size: bad argument");
+  *bytes = (size_t)(count > 0 ? count : 1) * kNormBlocks * sizeof(float);
+  return CDML_OK;
+}
+
+extern "C" int cdml_grad_norm(const cdml_param *params, int count, float prescale,
+                              int use_clipping, float threshold, float *result, void *workspace,
+                              size_t workspace_bytes, cdml_stream stream) {
+  if (count < 0) return fail(CDML_E_INVALID, "cdml_grad_norm: negative count");
+  if (!params || !result) return fail(CDML_E_INVALID, "cdml_grad_norm: NULL pointer");
+  if (use_clipping && !(threshold > 0.f && std::isfinite(threshold)))
+    return fail(CDML_E_INVALID, "cdml_grad_norm: clip threshold must be finite and positive");
+  size_t need = 0;
+  cdml_grad_norm_workspace_size(count, &need);
+  if (!workspace || workspace_bytes < need)
+    return fail(CDML_E_INVALID, "cdml_grad_norm: workspace of %zu bytes needed, %zu given", need,
+                workspace_bytes);
+  int rc = ensure_device();
+  if (rc) return rc;
+  hipStream_t st = as_hip(stream);
+  float *partial = static_cast<float *>(workspace);
+  if (count > 0) {
+    sumsq_kernel<<<dim3(kNormBlocks), dim3(256), 0, st>>>(params, count, prescale, partial);
+    rc = check_launch("sumsq_kernel");
+    if (rc) return rc;
+  }
+  norm_finalize_kernel<<<dim3(1), dim3(64), 0, st>>>(params, count, partial, use_clipping, threshold,
+                                                     result);
+  return check_launch("norm_finalize_kernel");
+}
+
+extern "C" int cdml_sgd_update(const cdml_param *params, int count, float learning_rate,
+                               float prescale, const float *result, int zero_grads,
+                               cdml_stream stream) {
+  if (count < 0) return fail(CDML_E_INVALID, "cdml_sgd_update: negative count");
+  if (count == 0) return CDML_OK;
+  if (!params || !result) return fail(CDML_E_INVALID, "cdml_sgd_update: NULL pointer");
+  int rc = ensure_device();
+  if (rc) return rc;
+  sgd_kernel<<<dim3(2048), dim3(256), 0, as_hip(stream)>>>(params, count, learning_rate, prescale, result,
+                                                            zero_grads);
+  return check_launch("sgd_kernel");
+}

@@ -7,6 +7,7 @@
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
 
+#include <chrono>
 #include <cstring>
 
 #include "cdml_host.h"
@@ -429,6 +430,76 @@ PYBIND11_MODULE(_cdml_host, m) {
            },
            py::arg("prompt"), py::arg("maxNewTokens"), py::arg("temperature") = 1.0f,
            py::arg("greedy") = true, py::arg("seed") = 0);
+
+  py::class_<TrainingConfig>(m, "TrainingConfig")
+      .def(py::init<>())
+      .def_readwrite("LearningRate", &TrainingConfig::LearningRate)
+      .def_readwrite("BatchSize", &TrainingConfig::BatchSize)
+      .def_readwrite("Epochs", &TrainingConfig::Epochs)
+      .def_readwrite("UseGradientClipping", &TrainingConfig::UseGradientClipping)
+      .def_readwrite("GradientClipThreshold", &TrainingConfig::GradientClipThreshold)
+      .def_readwrite("UseLearningRateDecay", &TrainingConfig::UseLearningRateDecay)
+      .def_readwrite("LearningRateDecay", &TrainingConfig::LearningRateDecay)
+      .def_readwrite("Verbose", &TrainingConfig::Verbose);
+
+  auto seqs_from = [](const py::object &o) {
+    std::vector<std::vector<int>> out;
+    for (py::handle h : o) {
+      I32 a = I32::ensure(py::reinterpret_borrow<py::object>(h));
+      if (!a || a.ndim() != 1) throw ArgumentException("each sequence must be a 1-D int array", "batch");
+      out.emplace_back(a.data(), a.data() + a.size());
+    }
+    return out;
+  };
+  auto flat_dict = [](DeviceTrainer &t, const std::vector<float> &flat) {
+    py::dict d;
+    for (size_t i = 0; i < t.names().size(); ++i) {
+      const auto &o = t.offsets()[i];
+      py::array_t<float> a((py::ssize_t)o.second);
+      std::memcpy(a.mutable_data(), flat.data() + o.first, o.second * sizeof(float));
+      d[py::str(t.names()[i])] = a;
+    }
+    return d;
+  };
+  py::class_<DeviceTrainer>(m, "DeviceTrainer")
+      .def(py::init<const LanguageModel &, const TrainingConfig &, int, int, int>(), py::arg("model"),
+           py::arg("config"), py::arg("batch_capacity"), py::arg("seq_capacity"), py::arg("device") = 0)
+      .def("TrainBatch",
+           [seqs_from](DeviceTrainer &t, py::object batch, float lr) {
+             auto b = seqs_from(batch);
+             py::gil_scoped_release nogil;
+             return t.TrainBatch(b, lr);
+           },
+           py::arg("batch"), py::arg("learningRate"))
+      .def("Train",
+           [seqs_from](DeviceTrainer &t, py::object seqs, uint64_t seed) {
+             auto b = seqs_from(seqs);
+             py::gil_scoped_release nogil;
+             return t.Train(b, seed);
+           },
+           py::arg("sequences"), py::arg("seed") = 0)
+      .def("CopyWeightsTo", &DeviceTrainer::CopyWeightsTo, py::arg("model"))
+      .def("weights", [flat_dict](DeviceTrainer &t) { return flat_dict(t, t.weights_flat()); })
+      .def("gradients", [flat_dict](DeviceTrainer &t) { return flat_dict(t, t.gradients_flat()); })
+      .def_property_readonly("last_norm", &DeviceTrainer::last_norm)
+      .def("time_step",
+           // Whole training steps on one fixed bucket (tokens [batch, seqLen + 1])
+           // resident in HBM: mean ms of `steps` steps after `warmup`, host clock
+           // with the stream synchronised on both sides.
+           [](DeviceTrainer &t, py::object tokens, float lr, int steps, int warmup) {
+             I32 a = I32::ensure(tokens);
+             if (!a || a.ndim() != 2) throw ArgumentException("tokens must be [batch, seqLen + 1]", "tokens");
+             py::gil_scoped_release nogil;
+             t.load_batch(a.data(), (int)a.shape(0), (int)a.shape(1));
+             for (int i = 0; i < warmup; ++i) t.step_loaded(lr);
+             t.synchronize();
+             const auto t0 = std::chrono::steady_clock::now();
+             for (int i = 0; i < steps; ++i) t.step_loaded(lr);
+             t.synchronize();
+             const auto t1 = std::chrono::steady_clock::now();
+             return std::chrono::duration<double, std::milli>(t1 - t0).count() / std::max(steps, 1);
+           },
+           py::arg("tokens"), py::arg("learningRate"), py::arg("steps") = 5, py::arg("warmup") = 2);
 
   py::class_<DeviceLanguageModel>(m, "DeviceLanguageModel")
       .def(py::init<const LanguageModel &, int, int>(), py::arg("model"), py::arg("batch_capacity"),

@@ -416,4 +416,101 @@ class DeviceLanguageModel {
   int ff_max_ = 0;
 };
 
+// ---- device-resident training --------------------------------------------
+// TrainingConfig (Transformers/Configuration/SharedConfigs.cs:24-60), the
+// fields the discrete-token trainer reads.
+struct TrainingConfig {
+  float LearningRate = 0.0001f;
+  int BatchSize = 32;
+  int Epochs = 10;
+  bool UseGradientClipping = true;
+  float GradientClipThreshold = 1.0f;
+  bool UseLearningRateDecay = false;
+  float LearningRateDecay = 0.95f;
+  bool Verbose = false;
+};
+
+// TransformerTrainer for decoder-only token models on the device
+// (Transformers/MultiTypeTransformer/TransformerTrainer.cs).  Every weight and
+// gradient of the model lives in HBM in two contiguous buffers; a batch step
+// (TrainBatchDiscrete, :217-327) runs the forward pass with its cache, the
+// cross-entropy gradient, the backward pass through every block, the
+// token-embedding gradient, the global-norm clipping and the SGD update
+// without leaving the device (one loss read-back per length bucket).
+class DeviceTrainer {
+ public:
+  // batch_capacity x seq_capacity input tokens (seq_capacity <=
+  // MaxSequenceLength) size the activation cache of one bucket.
+  DeviceTrainer(const LanguageModel &model, const TrainingConfig &config, int batch_capacity,
+                int seq_capacity, int device = 0);
+  ~DeviceTrainer();
+  DeviceTrainer(const DeviceTrainer &) = delete;
+  DeviceTrainer &operator=(const DeviceTrainer &) = delete;
+
+  // TrainBatchDiscrete: sequences shorter than 2 tokens or with ids outside
+  // the vocabulary are skipped, the rest bucketed by length; returns the
+  // average loss (0 when nothing was valid).
+  float TrainBatch(const std::vector<std::vector<int>> &batch, float learningRate);
+  // Train (:43-128): epochs over shuffled batches (SplitMix64 seeded by
+  // `seed`; the reference's System.Random is not reproduced) with the
+  // configured learning-rate decay; returns the last epoch's average loss.
+  float Train(const std::vector<std::vector<int>> &sequences, uint64_t seed = 0);
+  // Writes the device weights into the model's host arrays.
+  void CopyWeightsTo(LanguageModel &model);
+  // Current weights / the last step's gradients (after its 1/validCount and
+  // clipping scales), flattened in the device layout; `offsets()` gives each
+  // tensor's (offset, count) in the order of `names()`.
+  std::vector<float> weights_flat();
+  std::vector<float> gradients_flat();
+  const std::vector<std::string> &names() const { return names_; }
+  const std::vector<std::pair<size_t, size_t>> &offsets() const { return offs_; }
+  float last_norm() const { return last_norm_; }
+  cdml_stream stream() const { return stream_; }
+  // The benchmark's form of a step: load_batch uploads one bucket of `batch`
+  // sequences of seqLenPlus1 tokens; step_loaded enqueues a whole step on it
+  // (zero, forward, loss, backward, norm, update) with no read-back.
+  void load_batch(const int *host_tokens, int batch, int seqLenPlus1);
+  void step_loaded(float learningRate);
+  void synchronize();
+
+ private:
+  struct Layer {
+    float *wq, *wk, *wv, *wo, *bq, *bk, *bv, *bo, *ln1g, *ln1b, *ln2g, *ln2b;
+    float *gwq, *gwk, *gwv, *gwo, *gbq, *gbk, *gbv, *gbo, *gln1g, *gln1b, *gln2g, *gln2b;
+    std::vector<float *> ffw, ffb, gffw, gffb;
+    std::vector<int> ffrows, ffcols, ffact;
+    // forward cache of the current bucket
+    float *x, *q, *k, *v, *att, *r1, *n1, *m1, *v1, *r2, *m2, *v2;
+    std::vector<float *> z, h;  // pre-activation / activation of each FFN hidden layer
+  };
+  float *alloc(size_t floats);
+  void zero_grads();
+  void bucket_forward(int batch, int seqLen, float grad_scale, float *loss_dev);
+  void bucket_backward(int batch, int seqLen);
+  void upload_bucket(const std::vector<const std::vector<int> *> &seqs, int seqLen);
+  void update(int validCount, float learningRate);
+
+  TransformerConfig cfg_;
+  TrainingConfig tc_;
+  int cap_b_, cap_s_, device_;
+  cdml_stream stream_ = nullptr;
+  std::vector<void *> allocs_;
+  float *params_ = nullptr, *grads_ = nullptr;
+  size_t nparams_ = 0;
+  std::vector<std::string> names_;
+  std::vector<std::pair<size_t, size_t>> offs_;
+  void *param_table_ = nullptr;
+  int param_count_ = 0;
+  float *emb_, *outproj_, *outbias_, *gemb_, *goutproj_, *goutbias_;
+  std::vector<Layer> layers_;
+  float *xfinal_, *logits_, *dx_, *dxa_, *dr1_, *dr2_, *dn1_, *dcat_, *dq_, *dk_, *dv_, *tmp_;
+  std::vector<float *> dh_;  // FFN hidden gradients
+  float *rope_cs_, *result_, *losses_;
+  int *ids_, *targets_, *order_, *gstart_, *gtoken_;
+  int ngroups_ = 0, loaded_b_ = 0, loaded_s_ = 0;
+  void *ws_ = nullptr;
+  size_t ws_bytes_ = 0;
+  float last_norm_ = 0.f;
+};
+
 }  // namespace cdml_host

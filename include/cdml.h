@@ -247,6 +247,127 @@ int cdml_sdpa_bwd(const float *q, int ldq, const float *k, int ldk,
                   float scale, int causal, const uint8_t *mask,
                   void *workspace, size_t workspace_bytes, cdml_stream stream);
 
+/* ---- training step (TransformerTrainer.TrainBatchDiscrete,
+ * Transformers/MultiTypeTransformer/TransformerTrainer.cs:217-327) -------- */
+
+/* IAccelerationManager.FFNForwardBatch's layer with its cache, the forward
+ * pass that NeuralNetwork.ComputeInputGradientBatch recomputes
+ * (Neural Network/NeuralNetwork.cs:824-839): z = x w^T + b and y = act(z),
+ * both [rows, out_dim] with row stride ldy. */
+int cdml_linear_preact(const float *x, int ldx, const float *w, const float *b,
+                       float *z, float *y, int ldy, int rows, int in_dim,
+                       int out_dim, int activation, cdml_stream stream);
+
+/* One layer of NeuralNetwork.ComputeInputGradientBatch (NeuralNetwork.cs:
+ * 841-881) on fp32 MFMA, with cdml_linear_backward's gradients:
+ *   wgrad += dy^T x,  bgrad += column sums of dy,
+ *   dx = (dy w) * act'(dz) + add
+ * dz (the layer below's pre-activation, for its hidden deltas) and add (a
+ * residual gradient, MatrixAddInPlace) may be NULL; both have row stride
+ * lddx.  act' follows FillActivationAndDerivative (NeuralNetwork.cs:885-944).
+ * workspace as cdml_linear_backward. */
+int cdml_linear_backward_act(const float *x, int ldx, const float *dy,
+                             int lddy, const float *w, const float *dz,
+                             int activation, const float *add, float *dx,
+                             int lddx, float *wgrad, float *bgrad, int rows,
+                             int in_dim, int out_dim, void *workspace,
+                             size_t workspace_bytes, cdml_stream stream);
+
+/* IAccelerationManager.ResidualLayerNormForward (:140), replacing
+ * AccelerationCPU.cs:1440-1514: out = gamma * normalized + beta with
+ * residual = a + b, per-row mean and biased variance, normalized =
+ * (residual - mean) / sqrt(variance + eps).  mean / variance [rows],
+ * residual / normalized [rows, features] are written when non-NULL.
+ * features <= 2048. */
+int cdml_residual_layernorm_fwd(const float *a, const float *b,
+                                const float *gamma, const float *beta,
+                                float *out, float *mean, float *variance,
+                                float *residual, float *normalized, int rows,
+                                int features, float eps, cdml_stream stream);
+
+/* IAccelerationManager.LayerNormBackward (:143), replacing AccelerationCPU.cs:
+ * 1516-1564.  The upstream gradient is dout + dout2 (dout2 NULL: dout alone;
+ * the two gradients of a residual branch).  normalized may be NULL: it is
+ * then recomputed from input (the residual), mean and variance with the
+ * forward's arithmetic.  dinput [rows, features] is written; dgamma / dbeta
+ * [features] are written, or added to (accumulate = 1, the trainer's
+ * VectorAccumulate), or skipped when NULL.  Column sums run in a fixed
+ * order through `workspace` (cdml_layernorm_backward_workspace_size bytes).
+ * features <= 2048. */
+int cdml_layernorm_backward_workspace_size(int rows, int features,
+                                           size_t *bytes);
+int cdml_layernorm_backward(const float *dout, const float *dout2,
+                            const float *normalized, const float *gamma,
+                            const float *input, const float *mean,
+                            const float *variance, float *dinput,
+                            float *dgamma, float *dbeta, int rows,
+                            int features, float eps, int accumulate,
+                            void *workspace, size_t workspace_bytes,
+                            cdml_stream stream);
+
+/* IAccelerationManager.CrossEntropyLossAndGradient (:207-209), replacing
+ * AccelerationCPU.cs:2377-2440: for rows i < effective_len with target
+ * targets[i] (device int32, in [0, out_dim)): p = softmax(logits[i]),
+ * dlogits[i] = (p - onehot) / effective_len * grad_scale; rows past
+ * effective_len get 0.  *loss (device float) = mean over those rows of
+ * -log(p[target] + 1e-10), times loss_scale.  grad_scale is the trainer's
+ * per-bucket ScaleMatrixLocal (TransformerTrainer.cs:291-294).  A target
+ * outside [0, out_dim) makes the loss NaN.  workspace:
+ * cdml_cross_entropy_workspace_size bytes. */
+int cdml_cross_entropy_workspace_size(int rows, size_t *bytes);
+int cdml_cross_entropy(const float *logits, int ldl, const int *targets,
+                       int rows, int out_dim, int effective_len,
+                       float grad_scale, float loss_scale, float *loss,
+                       float *dlogits, int lddl, void *workspace,
+                       size_t workspace_bytes, cdml_stream stream);
+
+/* IAccelerationManager.AccumulateTokenEmbeddingGrad (:203-205), replacing
+ * AccelerationCPU.cs:2339-2370, as a gather over groups of rows that share a
+ * token: for group k, rows order[group_start[k] .. group_start[k+1]) of
+ * dx (+ dx2, both row stride ldx) are added in that order to row
+ * group_token[k] of grad [vocab, dim].  With rows listed in increasing
+ * order this is the reference's summation order, and no two groups share a
+ * token, so no atomics are needed.  All index arrays are device int32. */
+int cdml_embedding_grad(float *grad, const float *dx, const float *dx2,
+                        int ldx, const int *order, const int *group_start,
+                        const int *group_token, int n_groups, int dim,
+                        cdml_stream stream);
+
+/* One parameter tensor of the update: weight and grad are device arrays of
+ * `count` floats.  Consecutive entries with equal `group` are summed
+ * together before being added to the global squared norm (the trainer adds
+ * WQ + WK + WV + WO as one term). */
+typedef struct cdml_param {
+  float *weight;
+  float *grad;
+  long long count;
+  int group;
+  int reserved;
+} cdml_param;
+
+/* ScaleGradients + ComputeGradientNorm + ClipGradients
+ * (TransformerTrainer.cs:1306-1384, MatrixSquaredNorm AccelerationCPU.cs:
+ * 2493-2512): params is a device array of `count` entries.  Norm of the
+ * gradients scaled by `prescale` (1 / validCount); result (device float[3])
+ * receives the norm, the clipping factor (threshold / norm when use_clipping
+ * and norm > threshold, else 1) and 1 if the norm is finite, else 0.
+ * workspace: cdml_grad_norm_workspace_size bytes. */
+int cdml_grad_norm_workspace_size(int count, size_t *bytes);
+int cdml_grad_norm(const cdml_param *params, int count, float prescale,
+                   int use_clipping, float threshold, float *result,
+                   void *workspace, size_t workspace_bytes,
+                   cdml_stream stream);
+
+/* UpdateParameters (TransformerTrainer.cs:1269-1305; MatrixUpdate /
+ * VectorUpdate AccelerationCPU.cs:2548-2597): with g' = (g * prescale) *
+ * clip factor (result[1] from cdml_grad_norm), w -= learning_rate * g' when
+ * result[2] is nonzero.  zero_grads = 1 clears the gradients for the next
+ * step (ZeroAllGradients); 0 leaves g' in them, as the reference's in-place
+ * scaling does. */
+int cdml_sgd_update(const cdml_param *params, int count, float learning_rate,
+                    float prescale, const float *result, int zero_grads,
+                    cdml_stream stream);
+
 /* Single-query decode attention over a cached K/V, the device form of the
  * inline loop in LanguageModel.DecoderSelfAttentionStep
  * (Transformers/MultiTypeTransformer/LanguageModel.cs:365-427), which has no

@@ -404,15 +404,15 @@ _ATTN_B = ("bq", "bk", "bv", "bo")
 
 
 def train_step(cfg: dict, weights: dict, seqs, lr: float, clip: float = 1.0, use_clipping: bool = True):
-    """TransformerTrainer.TrainBatchDiscrete (TransformerTrainer.cs:217-327) for
-    one bucket of equal-length token sequences [B, S + 1]: forward with cache
-    (:540-622, segmented attention :723-848 when B > 1), cross-entropy over
-    the B * S next-token targets (:660-674), dLogits scaled by B, backward
-    (:874-987, 989-1060), gradients scaled by 1/B, global-norm clipping and
-    the SGD update (:1269-1384).  ``weights`` (the lm_weights layout) is not
-    modified.  Returns (loss, grads, new_weights); grads are the gradients the
-    update applied (after the 1/B and clipping scales), keyed like weights,
-    plus ``norm`` (the pre-clipping global norm)."""
+    """TransformerTrainer.TrainBatchDiscrete for one bucket of equal-length
+    token sequences [B, S + 1]; see train_batch."""
+    return train_batch(cfg, weights, list(np.ascontiguousarray(seqs, dtype=np.int32)), lr, clip, use_clipping)
+
+
+def _bucket_forward_backward(cfg, w, g, seqs):
+    """Forward with cache, loss and backward of one bucket [B, S + 1]
+    (TransformerTrainer.cs:255-300); gradients accumulate into g.  Returns
+    the bucket's loss, or None when it is not finite (no backward)."""
     seqs = np.ascontiguousarray(seqs, dtype=np.int32)
     B, S = seqs.shape[0], seqs.shape[1] - 1
     D, H, nl = cfg["dim"], cfg["heads"], cfg["layers"]
@@ -420,7 +420,6 @@ def train_step(cfg: dict, weights: dict, seqs, lr: float, clip: float = 1.0, use
     act = cfg.get("ffn_activation", 3)
     ids, targets = seqs[:, :S].reshape(-1), seqs[:, 1:].reshape(-1)
     rows = B * S
-    w = weights
     scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
 
     def seg_rope(m, inverse=False):
@@ -449,12 +448,11 @@ def train_step(cfg: dict, weights: dict, seqs, lr: float, clip: float = 1.0, use
         cache.append(c)
     logits = project_output_batch(x, w["out_proj"], w["out_bias"])
     loss, dl = cross_entropy(logits, targets, rows)
+    if not (np.isfinite(loss) and np.all(np.isfinite(dl))):
+        return None
     if B > 1:
         scale_inplace(dl, float(B))
 
-    z = lambda a: np.zeros_like(_f32(a))
-    g = {"token_embedding": z(w["token_embedding"]), "out_proj": z(w["out_proj"]), "out_bias": z(w["out_bias"]),
-         "layers": [{k: z(v) for k, v in L.items()} for L in w["layers"]]}
     dx, g["out_proj"], g["out_bias"] = backprop_output_projection(dl, x, w["out_proj"], g["out_proj"],
                                                                   g["out_bias"])
     for li in reversed(range(nl)):
@@ -479,6 +477,51 @@ def train_step(cfg: dict, weights: dict, seqs, lr: float, clip: float = 1.0, use
             c["input"], dq, dk, dv, L["wq"], L["wk"], L["wv"], G["wq"], G["bq"], G["wk"], G["bk"], G["wv"], G["bv"])
         dx = dxa + dr1
     g["token_embedding"] = accumulate_token_embedding_grad(g["token_embedding"], dx, ids)
+    g.setdefault("_ids", []).append(ids)
+    return loss
+
+
+def train_batch(cfg: dict, weights: dict, batch, lr: float, clip: float = 1.0, use_clipping: bool = True):
+    """TransformerTrainer.TrainBatchDiscrete (TransformerTrainer.cs:217-327):
+    sequences shorter than 2 tokens or with ids outside the vocabulary are
+    skipped, the rest are bucketed by length in order of first appearance;
+    per bucket a forward pass with cache (:540-622, segmented attention
+    :723-848), cross-entropy over the next-token targets (:660-674) with
+    dLogits scaled by the bucket size when it holds several sequences, and
+    the backward pass (:874-987, 989-1060) accumulate the gradients; then the
+    1/validCount scale, the global norm, clipping and the SGD update
+    (:311-327, :1269-1384).  ``weights`` (the lm_weights layout) is not
+    modified.  Returns (loss, grads, new_weights); grads are the gradients
+    the update applied, keyed like weights, plus ``norm`` (the pre-clipping
+    global norm, None when nothing was valid)."""
+    w = weights
+    nl = cfg["layers"]
+    z = lambda a: np.zeros_like(_f32(a))
+    g = {"token_embedding": z(w["token_embedding"]), "out_proj": z(w["out_proj"]), "out_bias": z(w["out_bias"]),
+         "layers": [{k: z(v) for k, v in L.items()} for L in w["layers"]]}
+    buckets = {}
+    for seq in batch:
+        seq = np.asarray(seq, np.int32)
+        if seq.size < 2 or seq.min() < 0 or seq.max() >= cfg["vocab"]:
+            continue
+        buckets.setdefault(seq.size - 1, []).append(seq)
+    total_loss = np.float32(0)
+    valid = 0
+    for _, members in buckets.items():
+        loss = _bucket_forward_backward(cfg, w, g, np.stack(members))
+        if loss is None:
+            continue
+        n = len(members)
+        total_loss = np.float32(total_loss + (np.float32(loss) * np.float32(n) if n > 1 else np.float32(loss)))
+        valid += n
+    neww = {"token_embedding": _f32(w["token_embedding"]).copy(), "out_proj": _f32(w["out_proj"]).copy(),
+            "out_bias": _f32(w["out_bias"]).copy(), "layers": [{k: _f32(v).copy() for k, v in L.items()}
+                                                              for L in w["layers"]]}
+    ids = np.concatenate(g.pop("_ids")) if "_ids" in g else np.zeros(0, np.int32)
+    if valid == 0:
+        g["norm"] = None
+        return 0.0, g, neww
+    loss = float(np.float32(total_loss / np.float32(valid)))
 
     def walk(d):  # every gradient / parameter array once
         yield d["token_embedding"]
@@ -497,7 +540,7 @@ def train_step(cfg: dict, weights: dict, seqs, lr: float, clip: float = 1.0, use
             for k in ("ffn_w1", "ffn_w2", "ffn_b1", "ffn_b2"):
                 yield L[k]
 
-    inv = float(np.float32(1.0) / np.float32(B))
+    inv = float(np.float32(1.0) / np.float32(valid))
     for a in walk(g):
         scale_inplace(a, inv)
     # ComputeGradientNorm (TransformerTrainer.cs:1319-1352): the embedding
@@ -521,9 +564,6 @@ def train_step(cfg: dict, weights: dict, seqs, lr: float, clip: float = 1.0, use
             total = f32(total + sn(G[k]))
     norm = float(np.sqrt(f32(total), dtype=np.float32))
     g["norm"] = norm
-    neww = {"token_embedding": _f32(w["token_embedding"]).copy(), "out_proj": _f32(w["out_proj"]).copy(),
-            "out_bias": _f32(w["out_bias"]).copy(), "layers": [{k: _f32(v).copy() for k, v in L.items()}
-                                                              for L in w["layers"]]}
     if not np.isfinite(norm):
         return loss, g, neww
     if use_clipping and norm > clip:

@@ -191,3 +191,114 @@ def kv_append(k_new, v_new, kcache, vcache, positions):
     N.check(N.lib().cdml_kv_cache_append(bk.ptr, bv.ptr, bkc.ptr, bvc.ptr, bp.ptr, b, t_max, dim,
                                          stream().handle))
     return down(bkc, kcache.shape), down(bvc, vcache.shape)
+
+
+# ---- training step ----------------------------------------------------------
+
+def _ws(fn, *args):
+    n = C.c_size_t(0)
+    N.check(getattr(N.lib(), fn)(*args, C.byref(n)))
+    return N.DeviceBuffer(max(16, n.value)), n.value
+
+
+def linear_preact(x, w, b, act):
+    rows, ind = x.shape
+    out = w.shape[0]
+    bx, bw, bb = up(x), up(w), up(b)
+    z, y = N.DeviceBuffer(max(4, rows * out * 4)), N.DeviceBuffer(max(4, rows * out * 4))
+    N.check(N.lib().cdml_linear_preact(bx.ptr, ind, bw.ptr, bb.ptr, z.ptr, y.ptr, out, rows, ind, out, act,
+                                       stream().handle))
+    return down(z, (rows, out)), down(y, (rows, out))
+
+
+def linear_backward_act(x, dy, w, wgrad, bgrad, dz=None, act=0, add=None):
+    """cdml_linear_backward_act -> (dx, wgrad, bgrad)."""
+    rows, ind = x.shape
+    out = dy.shape[1]
+    bx, bdy, bw, bwg, bbg = up(x), up(dy), up(w), up(wgrad), up(bgrad)
+    bdz = up(dz) if dz is not None else None
+    badd = up(add) if add is not None else None
+    bdx = N.DeviceBuffer(max(4, rows * ind * 4))
+    ws, nws = _ws("cdml_linear_backward_workspace_size", rows, ind, out)
+    N.check(N.lib().cdml_linear_backward_act(bx.ptr, ind, bdy.ptr, out, bw.ptr, bdz.ptr if bdz else None, act,
+                                             badd.ptr if badd else None, bdx.ptr, ind, bwg.ptr, bbg.ptr, rows,
+                                             ind, out, ws.ptr, nws, stream().handle))
+    return down(bdx, (rows, ind)), down(bwg, (out, ind)), down(bbg, (out,))
+
+
+def residual_layernorm_fwd(a, b, gamma, beta, eps=1e-5):
+    """-> (out, mean, var, normalized, residual) like oracle.residual_layernorm_forward."""
+    rows, f = a.shape
+    ba, bb, bg, bbe = up(a), up(b), up(gamma), up(beta)
+    out, res, nrm = (N.DeviceBuffer(max(4, rows * f * 4)) for _ in range(3))
+    mean, var = N.DeviceBuffer(max(4, rows * 4)), N.DeviceBuffer(max(4, rows * 4))
+    N.check(N.lib().cdml_residual_layernorm_fwd(ba.ptr, bb.ptr, bg.ptr, bbe.ptr, out.ptr, mean.ptr, var.ptr,
+                                                res.ptr, nrm.ptr, rows, f, eps, stream().handle))
+    return (down(out, (rows, f)), down(mean, (rows,)), down(var, (rows,)), down(nrm, (rows, f)),
+            down(res, (rows, f)))
+
+
+def layernorm_backward(dout, normalized, gamma, inp, mean, var, dout2=None, dgamma0=None, dbeta0=None,
+                       eps=1e-5):
+    """-> (dinput, dgamma, dbeta); with dgamma0 / dbeta0 the gradients accumulate onto them."""
+    rows, f = dout.shape
+    acc = dgamma0 is not None
+    bd, bg, bx, bm, bv = up(dout), up(gamma), up(inp), up(mean), up(var)
+    bn = up(normalized) if normalized is not None else None
+    bd2 = up(dout2) if dout2 is not None else None
+    bdg = up(dgamma0) if acc else N.DeviceBuffer(max(4, f * 4))
+    bdb = up(dbeta0) if acc else N.DeviceBuffer(max(4, f * 4))
+    bdx = N.DeviceBuffer(max(4, rows * f * 4))
+    ws, nws = _ws("cdml_layernorm_backward_workspace_size", rows, f)
+    N.check(N.lib().cdml_layernorm_backward(bd.ptr, bd2.ptr if bd2 else None, bn.ptr if bn else None, bg.ptr,
+                                            bx.ptr, bm.ptr, bv.ptr, bdx.ptr, bdg.ptr, bdb.ptr, rows, f, eps,
+                                            int(acc), ws.ptr, nws, stream().handle))
+    return down(bdx, (rows, f)), down(bdg, (f,)), down(bdb, (f,))
+
+
+def cross_entropy(logits, targets, effective_len, grad_scale=1.0, loss_scale=1.0):
+    rows, v = logits.shape
+    bl, bt = up(logits), up(np.asarray(targets, np.int32), np.int32)
+    bd, bloss = N.DeviceBuffer(max(4, rows * v * 4)), N.DeviceBuffer(4)
+    ws, nws = _ws("cdml_cross_entropy_workspace_size", rows)
+    N.check(N.lib().cdml_cross_entropy(bl.ptr, v, bt.ptr, rows, v, effective_len, grad_scale, loss_scale,
+                                       bloss.ptr, bd.ptr, v, ws.ptr, nws, stream().handle))
+    return float(down(bloss, (1,))[0]), down(bd, (rows, v))
+
+
+def embedding_groups(ids):
+    """Rows grouped by token, each group in increasing row order: (order, start, token)."""
+    ids = np.asarray(ids, np.int64)
+    order = np.argsort(ids, kind="stable").astype(np.int32)
+    tok, start = np.unique(ids[order], return_index=True)
+    return order, np.append(start, len(ids)).astype(np.int32), tok.astype(np.int32)
+
+
+def embedding_grad(eg, dx, ids, dx2=None):
+    rows, dim = dx.shape
+    order, start, tok = embedding_groups(ids)
+    beg, bdx = up(eg), up(dx)
+    bdx2 = up(dx2) if dx2 is not None else None
+    bo, bs, btk = (up(a, np.int32) for a in (order, start, tok))
+    N.check(N.lib().cdml_embedding_grad(beg.ptr, bdx.ptr, bdx2.ptr if bdx2 else None, dim, bo.ptr, bs.ptr,
+                                        btk.ptr, len(tok), dim, stream().handle))
+    return down(beg, eg.shape)
+
+
+def norm_and_update(weights, grads, groups, lr, prescale, use_clipping, threshold, zero_grads=False):
+    """cdml_grad_norm then cdml_sgd_update -> (norm, clip, finite, new weights, grads after)."""
+    bw = [up(w) for w in weights]
+    bg = [up(g) for g in grads]
+    params = (N.Param * len(weights))(*[N.Param(w.ptr, g.ptr, int(a.size), int(gr), 0)
+                                        for w, g, a, gr in zip(bw, bg, weights, groups)])
+    bp = N.DeviceBuffer(C.sizeof(params))
+    N.check(N.lib().cdml_memcpy_h2d_async(bp.ptr, C.addressof(params), C.sizeof(params), stream().handle))
+    res = N.DeviceBuffer(16)
+    ws, nws = _ws("cdml_grad_norm_workspace_size", len(weights))
+    N.check(N.lib().cdml_grad_norm(bp.ptr, len(weights), prescale, int(use_clipping), threshold, res.ptr, ws.ptr,
+                                   nws, stream().handle))
+    N.check(N.lib().cdml_sgd_update(bp.ptr, len(weights), lr, prescale, res.ptr, int(zero_grads),
+                                    stream().handle))
+    r = down(res, (3,))
+    return (float(r[0]), float(r[1]), float(r[2]), [down(b, w.shape) for b, w in zip(bw, weights)],
+            [down(b, g.shape) for b, g in zip(bg, grads)])

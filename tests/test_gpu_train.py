@@ -1,0 +1,264 @@
+"""GPU parity of the training-step kernels against the CPU oracle
+(oracle/refcpu_train.c), through the C ABI.
+
+Bar: |got - want| <= 1e-4 + 1e-3 |want| per element (gradients summed over
+many rows also against float64, see conftest.assert_parity_with_exact);
+the SGD update is bit-exact given the same gradient.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import abi_ops as G
+from cdml import synth
+from conftest import assert_parity, assert_parity_with_exact
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+F64 = np.float64
+
+
+def parity(a, e, what=""):
+    assert_parity(a, e, 1e-4, 1e-3, what)
+
+
+@pytest.mark.parametrize("rows,ind,out,act", [(64, 64, 128, 3), (300, 256, 1024, 3), (77, 130, 33, 1),
+                                              (1024, 512, 2048, 5), (40, 32, 64, 2)])
+def test_linear_preact(rows, ind, out, act):
+    """The FFN hidden layer with its cache: z = x W^T + b, y = act(z)."""
+    x, w, b = synth.normal(1, (rows, ind)), synth.xavier_uniform(2, out, ind), synth.normal(3, (out,))
+    z, y = G.linear_preact(x, w, b, act)
+    zw = O.batch_dot_add_bias(w, x, b)
+    parity(z, zw, "pre-activation")
+    parity(y, O.activation(zw, act), "activation")
+    assert np.array_equal(y, O.activation(z, act)) if act == 3 else True  # ReLU of the stored z, exactly
+
+
+@pytest.mark.parametrize("rows,ind,out,act", [(64, 64, 128, 3), (600, 256, 512, 3), (77, 130, 33, 1),
+                                              (2048, 128, 512, 5), (40, 32, 64, 4)])
+def test_ffn_backward_layers(rows, ind, out, act):
+    """NeuralNetwork.ComputeInputGradientBatch of a [ind, out, ind] FFN as two
+    cdml_linear_backward_act calls (hidden deltas through act'(z), the input
+    gradient plus a residual gradient), against the oracle's FFN backward
+    followed by MatrixAddInPlace."""
+    x = synth.normal(4, (rows, ind))
+    w1, b1 = synth.xavier_uniform(5, out, ind), synth.normal(6, (out,)) * np.float32(0.1)
+    w2, b2 = synth.xavier_uniform(7, ind, out), synth.normal(8, (ind,)) * np.float32(0.1)
+    dout, resid = synth.normal(9, (rows, ind)), synth.normal(10, (rows, ind))
+    wg = [synth.normal(11, (out, ind)), synth.normal(12, (ind, out))]
+    bg = [synth.normal(13, (out,)), synth.normal(14, (ind,))]
+    wg_o, bg_o = [a.copy() for a in wg], [a.copy() for a in bg]
+    want = O.ffn_input_gradient(x, dout, [w1, w2], [b1, b2], [act, 0], wg_o, bg_o) + resid
+    z, h = G.linear_preact(x, w1, b1, act)
+    dh, gw2, gb2 = G.linear_backward_act(h, dout, w2, wg[1], bg[1], dz=z, act=act)
+    dx, gw1, gb1 = G.linear_backward_act(x, dh, w1, wg[0], bg[0], add=resid)
+    # float64 of the same chain for the long reductions
+    X, D = x.astype(F64), dout.astype(F64)
+    Z = X @ w1.T.astype(F64) + b1
+    deriv = {3: (Z >= 0).astype(F64), 1: (lambda s: s * (1 - s))(1 / (1 + np.exp(-Z))),
+             5: (lambda s: s + Z * s * (1 - s))(1 / (1 + np.exp(-Z))), 4: np.where(Z <= 0, 0.1, 1.0)}[act]
+    Hh = {3: np.maximum(Z, 0), 1: 1 / (1 + np.exp(-Z)), 5: Z / (1 + np.exp(-Z)), 4: np.where(Z > 0, Z, 0.01 * Z)}[act]
+    DH = (D @ w2.astype(F64)) * deriv
+    assert_parity_with_exact(gw2, wg_o[1], wg[1] + D.T @ Hh, what="W2 grad")
+    assert_parity_with_exact(gb2, bg_o[1], bg[1] + D.sum(0), what="b2 grad")
+    assert_parity_with_exact(gw1, wg_o[0], wg[0] + DH.T @ X, what="W1 grad")
+    assert_parity_with_exact(gb1, bg_o[0], bg[0] + DH.sum(0), what="b1 grad")
+    assert_parity_with_exact(dx, want, DH @ w1.astype(F64) + resid, what="dInput + residual")
+
+
+@pytest.mark.parametrize("rows,f", [(5, 7), (64, 64), (300, 256), (1000, 1024), (33, 2048), (4, 1)])
+def test_residual_layernorm_forward_cache(rows, f):
+    a, b = synth.normal(15, (rows, f)), synth.normal(16, (rows, f))
+    g, be = synth.positive_vector(f, 17), synth.normal(18, (f,))
+    got = G.residual_layernorm_fwd(a, b, g, be)
+    want = O.residual_layernorm_forward(a, b, g, be)
+    for x, e, n in zip(got, want, ("out", "mean", "variance", "normalized", "residual")):
+        parity(x, e, f"ResidualLayerNormForward {n}")
+    assert np.array_equal(got[4], want[4])  # a + b exactly
+
+
+@pytest.mark.parametrize("rows,f,with_norm", [(5, 7, True), (64, 64, False), (300, 256, False),
+                                              (1000, 1024, False), (130, 2048, True)])
+def test_layernorm_backward(rows, f, with_norm):
+    a, b = synth.normal(19, (rows, f)), synth.normal(20, (rows, f))
+    g, be = synth.positive_vector(f, 21), synth.normal(22, (f,))
+    _, mean, var, norm, res = O.residual_layernorm_forward(a, b, g, be)
+    d1, d2 = synth.normal(23, (rows, f)), synth.normal(24, (rows, f))
+    want = O.layernorm_backward(d1 + d2, norm, g, res, mean, var)
+    got = G.layernorm_backward(d1, norm if with_norm else None, g, res, mean, var, dout2=d2)
+    G64 = (d1 + d2).astype(F64)
+    N64 = norm.astype(F64)
+    assert_parity_with_exact(got[0], want[0], want[0], what="dInput")
+    assert_parity_with_exact(got[1], want[1], (G64 * N64).sum(0), what="dGamma")
+    assert_parity_with_exact(got[2], want[2], G64.sum(0), what="dBeta")
+    acc = G.layernorm_backward(d1, None, g, res, mean, var, dout2=d2, dgamma0=np.ones(f, np.float32),
+                               dbeta0=np.full(f, 2, np.float32))
+    parity(acc[1], want[1] + 1, "dGamma accumulated")
+    parity(acc[2], want[2] + 2, "dBeta accumulated")
+
+
+@pytest.mark.parametrize("rows,v,eff,scale", [(6, 11, 4, 1.0), (64, 200, 64, 4.0), (300, 1000, 257, 1.0),
+                                              (16, 50000, 16, 2.0), (3, 7, 0, 1.0)])
+def test_cross_entropy(rows, v, eff, scale):
+    logits = synth.normal(25, (rows, v)) * np.float32(3)
+    t = (np.arange(rows) * 7919 % v).astype(np.int32)
+    loss, dl = G.cross_entropy(logits, t, eff, grad_scale=scale)
+    if eff == 0:
+        assert loss == 0 and not dl.any()
+        return
+    want_loss, want_dl = O.cross_entropy(logits, t, eff)
+    assert abs(loss - want_loss) <= 1e-5 + 1e-5 * abs(want_loss)
+    parity(dl, want_dl * np.float32(scale), "dLogits")
+    assert not dl[eff:].any()
+
+
+def test_cross_entropy_bad_target_gives_nan_loss():
+    logits = synth.normal(26, (4, 9))
+    loss, _ = G.cross_entropy(logits, np.array([1, 2, 9, 0], np.int32), 4)
+    assert np.isnan(loss)
+
+
+@pytest.mark.parametrize("rows,vocab,dim", [(12, 5, 3), (256, 200, 64), (16384, 50000, 64), (300, 7, 1024)])
+def test_embedding_grad(rows, vocab, dim):
+    ids = (np.arange(rows) * 31 % vocab).astype(np.int32)
+    if rows > 12:
+        ids[::5] = 3  # a token repeated many times
+    dx, dx2 = synth.normal(27, (rows, dim)), synth.normal(28, (rows, dim))
+    eg = synth.normal(29, (vocab, dim))
+    got = G.embedding_grad(eg, dx, ids, dx2)
+    want = O.accumulate_token_embedding_grad(eg, dx + dx2, ids)
+    assert np.array_equal(got, want)  # same rows, same order, same sums
+
+
+def test_grad_norm_clip_and_update():
+    """Global norm with the trainer's grouping, clipping and the SGD update;
+    the update is bit-exact against w - lr * g' with g' the oracle's scaled
+    gradients."""
+    shapes = [(200, 64), (64,), (64, 64), (64, 64), (64, 64), (64, 64), (64,), (64,), (128, 64), (7,)]
+    groups = [0, 1, 2, 2, 2, 2, 3, 3, 4, 5]
+    ws = [synth.normal(30 + i, s) for i, s in enumerate(shapes)]
+    gs = [synth.normal(50 + i, s) for i, s in enumerate(shapes)]
+    prescale = float(np.float32(1) / np.float32(3))
+    scaled = [g.copy() for g in gs]
+    for g in scaled:
+        O.scale_inplace(g, prescale)
+    total = np.float32(0)
+    i = 0
+    while i < len(shapes):  # groups of consecutive equal ids
+        j = i
+        s = np.float32(0)
+        while j < len(shapes) and groups[j] == groups[i]:
+            s = np.float32(s + np.float32(O.squared_norm(scaled[j])))
+            j += 1
+        total = np.float32(total + s)
+        i = j
+    norm_want = float(np.sqrt(total, dtype=np.float32))
+    for clip_on, thr in ((False, 1.0), (True, 1.0), (True, 1e6)):
+        lr = 0.05
+        norm, clip, finite, neww, after = G.norm_and_update(ws, gs, groups, lr, prescale, clip_on, thr)
+        assert finite == 1.0
+        assert norm == pytest.approx(norm_want, rel=1e-5)
+        want_clip = thr / norm if (clip_on and norm > thr) else 1.0
+        assert clip == pytest.approx(want_clip, rel=1e-6)
+        for w, g, nw, ga in zip(ws, scaled, neww, after):
+            gp = g.copy()
+            if clip != 1.0:
+                O.scale_inplace(gp, clip)
+            assert np.array_equal(ga, gp)  # the gradient left as the in-place scaling leaves it
+            wp = w.copy()
+            O.sgd_update(wp, gp, lr)
+            assert np.array_equal(nw, wp)
+    # zero_grads clears every gradient; a non-finite norm skips the update
+    bad = [g.copy() for g in gs]
+    bad[3][1, 2] = np.inf
+    _, _, finite, neww, after = G.norm_and_update(ws, bad, groups, 0.05, prescale, True, 1.0, zero_grads=True)
+    assert finite == 0.0
+    assert all(np.array_equal(a, b) for a, b in zip(neww, ws)) and not any(a.any() for a in after)
+
+
+# ------------------------------------------------------------- the trainer
+def _trainer(cfg, weights, batch_cap, seq_cap, clip=1.0, use_clip=True):
+    from cdml import host
+    H = host.module()
+    lm, _ = host.language_model(cfg, weights)
+    tc = H.TrainingConfig()
+    tc.UseGradientClipping = use_clip
+    tc.GradientClipThreshold = clip
+    return H.DeviceTrainer(lm, tc, batch_cap, seq_cap), lm
+
+
+def _oracle_named(d):
+    """oracle train_batch dicts -> the trainer's flat names."""
+    out = {"token_embedding": d["token_embedding"], "out_proj": d["out_proj"], "out_bias": d["out_bias"]}
+    for i, L in enumerate(d["layers"]):
+        for k, v in L.items():
+            k2 = {"ffn_w1": "ffn_w1", "ffn_w2": "ffn_w2", "ffn_b1": "ffn_b1", "ffn_b2": "ffn_b2"}.get(k, k)
+            out[f"layers.{i}.{k2}"] = v
+    return out
+
+
+def _compare(got: dict, want: dict, what: str):
+    w = _oracle_named(want)
+    assert set(got) == set(w), set(got) ^ set(w)
+    for k, v in got.items():
+        parity(v, np.asarray(w[k]).reshape(-1), f"{what} {k}")
+
+
+C1 = {"vocab": 200, "dim": 64, "heads": 4, "layers": 2, "ff": 128, "max_seq": 64}
+
+
+@pytest.mark.parametrize("batch,seq,use_clip", [(4, 33, True), (1, 64, False), (8, 17, True)])
+def test_device_trainer_step_matches_oracle(batch, seq, use_clip):
+    """One TrainBatchDiscrete step of the config-1 text model (segmented
+    attention for batch > 1, the single-sequence path for batch 1): loss,
+    every gradient after the 1/B and clipping scales, and every updated
+    weight against the oracle."""
+    w = synth.lm_weights(C1, 12, biased=True)
+    seqs = synth.token_ids(40 + batch, batch * seq, C1["vocab"]).reshape(batch, seq)
+    t, _ = _trainer(C1, w, batch, seq - 1, use_clip=use_clip)
+    loss = t.TrainBatch(list(seqs), 0.01)
+    want_loss, want_g, want_w = O.train_batch(C1, w, list(seqs), 0.01, use_clipping=use_clip)
+    assert abs(loss - want_loss) <= 1e-5 + 1e-5 * abs(want_loss)
+    assert t.last_norm == pytest.approx(want_g["norm"], rel=1e-4)
+    _compare(t.gradients(), want_g, "gradient")
+    _compare(t.weights(), want_w, "weight")
+
+
+def test_device_trainer_mixed_batch_and_several_steps():
+    """Buckets of two lengths, a single-sequence bucket and skipped sequences
+    in one batch, then three more steps: weights track the oracle's."""
+    w = synth.lm_weights(C1, 13, biased=True)
+    rng = np.random.default_rng(5)
+    batch = [rng.integers(0, 200, 20).astype(np.int32) for _ in range(3)]
+    batch += [rng.integers(0, 200, 12).astype(np.int32) for _ in range(2)]
+    batch += [rng.integers(0, 200, 30).astype(np.int32), np.array([7], np.int32),
+              np.array([1, 200, 3], np.int32)]
+    t, lm = _trainer(C1, w, 4, 32)
+    loss = t.TrainBatch(batch, 0.02)
+    want_loss, want_g, want_w = O.train_batch(C1, w, batch, 0.02)
+    assert abs(loss - want_loss) <= 1e-5 + 1e-5 * abs(want_loss)
+    _compare(t.gradients(), want_g, "mixed gradient")
+    _compare(t.weights(), want_w, "mixed weight")
+    ww = want_w
+    for step in range(3):
+        seqs = list(synth.token_ids(60 + step, 4 * 25, 200).reshape(4, 25))
+        t.TrainBatch(seqs, 0.02)
+        _, _, ww = O.train_batch(C1, ww, seqs, 0.02)
+    _compare(t.weights(), ww, "after 4 steps")
+    # CopyWeightsTo writes the trained weights back into the host model
+    t.CopyWeightsTo(lm)
+    got = lm.weights()
+    parity(got["out_proj"], ww["out_proj"], "CopyWeightsTo out_proj")
+    parity(got["layers"][1]["ffn_w1"], ww["layers"][1]["ffn_w1"], "CopyWeightsTo ffn_w1")
+
+
+def test_device_trainer_loss_decreases():
+    """Training on a fixed batch drives its loss down (the reference's own
+    convergence tests, MultiTypeTransformerTests, check the same)."""
+    w = synth.lm_weights(C1, 14)
+    seqs = list(synth.token_ids(70, 8 * 33, 200).reshape(8, 33))
+    t, _ = _trainer(C1, w, 8, 32)
+    losses = [t.TrainBatch(seqs, 0.05) for _ in range(40)]
+    assert all(b < a for a, b in zip(losses[:10], losses[1:11])), losses
+    assert losses[-1] < 0.8 * losses[0], losses

@@ -101,11 +101,22 @@ def _get(d, key):
 CFG = {"vocab": 12, "dim": 8, "heads": 2, "layers": 2, "ff": 16, "max_seq": 8}
 
 
+def batch_loss64(cfg, w, buckets, drop_ffn_residual=False):
+    """TrainBatchDiscrete's objective over several length buckets: the
+    bucket means weighted by their sequence counts, over the valid count."""
+    n = [b.shape[0] for b in buckets]
+    return sum(k * loss64(cfg, w, b, drop_ffn_residual) for k, b in zip(n, buckets)) / sum(n)
+
+
 def _fd_check(seqs, per_tensor=6, seed=0, drop_ffn_residual=False):
+    buckets = seqs if isinstance(seqs, list) else [seqs]
     w = synth.lm_weights(CFG, 3, biased=True)
-    loss, g, _ = O.train_step(CFG, w, seqs, 0.1, use_clipping=False)
+    flat = [s for b in buckets for s in b]
+    loss, g, _ = O.train_batch(CFG, w, flat, 0.1, use_clipping=False)
     w64 = _to64(w)
-    assert abs(loss - loss64(CFG, w64, seqs)) < 1e-5
+    lossf = lambda ww: batch_loss64(CFG, ww, buckets, drop_ffn_residual)
+    assert abs(loss - lossf(w64)) < 1e-5 or drop_ffn_residual
+    used_ids = np.unique(np.concatenate([b[:, :-1].reshape(-1) for b in buckets]))
     rng = np.random.default_rng(seed)
     eps = 1e-6
     worst = 0.0
@@ -113,16 +124,15 @@ def _fd_check(seqs, per_tensor=6, seed=0, drop_ffn_residual=False):
         flat = arr.reshape(-1)
         gr = _get(g, key).reshape(-1)
         if key == ("token_embedding",):  # rows of used tokens carry the gradient
-            used = np.unique(seqs[:, :-1])
-            cand = (used[:, None] * CFG["dim"] + np.arange(CFG["dim"])[None, :]).reshape(-1)
+            cand = (used_ids[:, None] * CFG["dim"] + np.arange(CFG["dim"])[None, :]).reshape(-1)
         else:
             cand = np.arange(flat.size)
         for e in rng.choice(cand, size=min(per_tensor, cand.size), replace=False):
             keep = flat[e]
             flat[e] = keep + eps
-            lp = loss64(CFG, w64, seqs, drop_ffn_residual)
+            lp = lossf(w64)
             flat[e] = keep - eps
-            lm = loss64(CFG, w64, seqs, drop_ffn_residual)
+            lm = lossf(w64)
             flat[e] = keep
             fd = (lp - lm) / (2 * eps)
             err = abs(gr[e] - fd) - (3e-5 + 1e-3 * abs(fd))
@@ -136,6 +146,21 @@ def _fd_check(seqs, per_tensor=6, seed=0, drop_ffn_residual=False):
 def test_train_step_gradients_against_finite_differences(batch):
     seqs = synth.token_ids(5 + batch, batch * 6, CFG["vocab"]).reshape(batch, 6)
     ok, info = _fd_check(seqs)
+    assert ok, info
+
+
+def test_mixed_length_batch_gradients_against_finite_differences():
+    """Two buckets (three sequences of 6 tokens, one of 4) plus sequences the
+    trainer skips (too short, an id outside the vocabulary): the gradients
+    accumulate over the buckets before the 1/validCount scale."""
+    a = synth.token_ids(31, 3 * 6, CFG["vocab"]).reshape(3, 6)
+    b = synth.token_ids(32, 4, CFG["vocab"]).reshape(1, 4)
+    w = synth.lm_weights(CFG, 3, biased=True)
+    skipped = [np.array([5], np.int32), np.array([1, CFG["vocab"], 2], np.int32)]
+    full = O.train_batch(CFG, w, [a[0], skipped[0], b[0], a[1], skipped[1], a[2]], 0.1, use_clipping=False)
+    ref = O.train_batch(CFG, w, [a[0], b[0], a[1], a[2]], 0.1, use_clipping=False)
+    assert full[0] == ref[0] and np.array_equal(full[1]["out_proj"], ref[1]["out_proj"])
+    ok, info = _fd_check([a, b])
     assert ok, info
 
 
