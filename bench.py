@@ -278,6 +278,28 @@ def bench_mha_backward(N, st, steps, warmup, cfg=None):
                           "for the core (no recompute counted), 4 x rows x D^2 per projection"}
 
 
+def bench_train(H, cfg, batch, seq_inputs, steps, warmup, lr=0.01):
+    """Whole TrainBatchDiscrete steps of the DeviceTrainer on one fixed bucket
+    of `batch` synthetic token sequences (seq_inputs + 1 tokens each):
+    forward with cache, cross-entropy, backward, global-norm clipping and the
+    SGD update.  Matmul FLOPs counted as 3x the forward's (forward, then dX
+    and dW of every product; the attention core's backward at 8 x head_dim
+    per causal pair, recomputation not counted)."""
+    from cdml import host, synth
+
+    lm, _ = host.language_model(cfg, synth.lm_weights(cfg, 17))
+    tc = H.TrainingConfig()
+    t = H.DeviceTrainer(lm, tc, batch, seq_inputs)
+    toks = synth.token_ids(23, batch * (seq_inputs + 1), cfg["vocab"]).reshape(batch, seq_inputs + 1)
+    ms = t.time_step(toks, lr, steps, warmup)
+    D, Hh, L, FF, V = cfg["dim"], cfg["heads"], cfg["layers"], cfg["ff"], cfg["vocab"]
+    rows = batch * seq_inputs
+    core, qkv, out = mha_flops(batch, seq_inputs, D, Hh)
+    fwd = L * (core + qkv + out + 4 * rows * D * FF) + 2 * rows * D * V
+    return {"ms": round(ms, 3), "tokens_per_s": round(rows / (ms * 1e-3), 1),
+            "tflops": round(3 * fwd / (ms * 1e-3) / 1e12, 2), "gflop_per_step": round(3 * fwd / 1e9, 1)}
+
+
 def extras(N, st):
     """End-to-end figures for the other BASELINE configs (device-resident,
     events on the engine's stream) and the PCIe-inclusive drop-in path."""
@@ -294,6 +316,15 @@ def extras(N, st):
                            "flash_ms": round(r["flash_ms"], 4)}
     log("[bench] extras: c3 MHA layer backward")
     out["c3_mha_layer_backward"] = bench_mha_backward(N, st, 5, 3)
+    log("[bench] extras: training steps")
+    out["c1_text_model_train_step"] = dict(
+        bench_train(H, {"vocab": 200, "dim": 64, "heads": 4, "layers": 2, "ff": 128, "max_seq": 64}, 4, 63, 20, 5),
+        workload="TrainBatchDiscrete on 4 sequences of 64 tokens (63 inputs), config-1 text model")
+    out["c3_shape_train_step"] = dict(
+        bench_train(H, {"vocab": 1000, "dim": 1024, "heads": 16, "layers": 12, "ff": 4096, "max_seq": 4096},
+                    4, 4095, 3, 1),
+        workload="TrainBatchDiscrete on 4 sequences of 4096 tokens, 12 decoder layers D 1024 / 16 heads / "
+                 "FF 4096 (config-3 shape) with a 1000-token vocabulary")
     log("[bench] extras: c3 12-layer decoder stack")
     # c3: 12 post-LN decoder layers (MHA + FFN 4096 + 2 LayerNorms) on N(0,1) embeddings
     cfg3 = {"dim": 1024, "heads": 16, "layers": 12, "ff": 4096, "max_seq": 4096, "discrete": False,

@@ -684,9 +684,9 @@ struct SplitPlan {
 
 SplitPlan splitk_plan(int M, int N, int K, int nprob) {
   SplitPlan sp;
-  const int nk = K / 16;
+  const int nk = K / 16;  // whole k-tiles; a ragged tail is added by a separate launch
   sp.kchunk = nk;
-  if (M <= 0 || N <= 0 || K % 16 || N % 4) return sp;
+  if (M <= 0 || N <= 0 || nk < 1 || N % 4) return sp;
   const bool big = M >= 1024;
   const int TM = big ? 256 : 128, TN = 128;
   const int tiles = ((M + TM - 1) / TM) * ((N + TN - 1) / TN) * nprob;
@@ -768,10 +768,31 @@ int launch_gemm(GemmArgs &g, bool ta, bool tb, hipStream_t stream, const char *w
     fast = fast && stage_ok(g.p[i].a, g.M, g.lda, ta, 16) && stage_ok(g.p[i].w, g.N, g.ldb, tb, 16);
   if (ta || tb) {
     int rc;
-    if (ta && tb) rc = launch_layout<true, true>(g, fast, stream);
-    else if (tb) rc = launch_layout<false, true>(g, fast, stream);
+    // A ragged K: the tiled kernel covers the whole 16-row k-tiles (it never
+    // reads past them) and the last K % 16 rows are added by a second launch
+    // (C += tail, bgrad += tail row sums) -- unless an epilogue must see the
+    // complete sum.
+    const int ktail = g.K % 16;
+    bool split_tail = tb && ktail != 0 && g.K >= 16 && !g.dz && !g.add && !g.pre && g.act == CDML_ACT_NONE;
+    for (int i = 0; split_tail && i < g.nprob; ++i)
+      split_tail = stage_ok(g.p[i].a, g.M, g.lda, ta, 16) && stage_ok(g.p[i].w, g.N, g.ldb, tb, 16);
+    if (ta && tb) rc = launch_layout<true, true>(g, fast || split_tail, stream);
+    else if (tb) rc = launch_layout<false, true>(g, fast || split_tail, stream);
     else rc = launch_layout<true, false>(g, false, stream);
     if (rc) return rc;
+    if (split_tail) {
+      const int kmain = g.K - ktail;
+      GemmArgs t = g;
+      t.K = ktail;
+      t.beta = 1;
+      t.ksplit = 1;
+      for (int i = 0; i < t.nprob; ++i) {
+        t.p[i].a += ta ? (size_t)kmain * g.lda : (size_t)kmain;
+        t.p[i].w += tb ? (size_t)kmain * g.ldb : (size_t)kmain;
+      }
+      rc = ta ? launch_layout<true, true>(t, false, stream) : launch_layout<false, true>(t, false, stream);
+      if (rc) return rc;
+    }
     return check_launch(what);
   }
   g.tiles_m = (g.M + BM - 1) / BM;

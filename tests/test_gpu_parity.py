@@ -162,6 +162,7 @@ def test_backprop_qkv_reference_case():
 @pytest.mark.parametrize("rows,ind,out", [(1024, 512, 512),   # tiled kernels (128-row tiles)
                                           (2048, 256, 1024),  # 256-row tiles for W_grad
                                           (656, 256, 256),    # split K with a short last chunk
+                                          (1000, 256, 512),   # split K plus a ragged 8-row tail
                                           (300, 1024, 96),    # K = 300 rows: generic W_grad kernel
                                           (130, 257, 129),    # ragged everywhere
                                           (1, 64, 64)])
@@ -201,7 +202,9 @@ def test_backprop_qkv_c3_shape_float64():
 
 
 @pytest.mark.parametrize("rows,ind,out", [(4, 8, 8), (16, 16, 32), (512, 256, 256), (77, 64, 130),
-                                          (4112, 128, 1024)])  # split K, 257 k-tiles
+                                          (4112, 128, 1024),   # split K, 257 k-tiles
+                                          (4100, 128, 1000),   # split K + 4-row tail; dX with K = 1000
+                                          (252, 64, 200)])     # the config-1 LM head of one training bucket
 def test_linear_backward(rows, ind, out):
     """BackpropLinearProjection (dInput accumulates) and BackpropOutputProjection
     (dX overwritten) on the shapes of AccelerationConsistencyTests.cs:633-700,
