@@ -71,6 +71,9 @@ SIGNATURES = {
     "cdml_sdpa_bwd_workspace_size": [_i, _i, _i, _i, _i, C.POINTER(_sz)],
     "cdml_sdpa_bwd": [_vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i,
                       _i, _i, _i, _i, _i, _f, _i, _vp, _vp, _sz, _vp],
+    "cdml_sdpa_fwd_lse": [_vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _f, _i, _vp, _vp],
+    "cdml_sdpa_bwd_saved": [_vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _vp, _i, _vp, _i, _vp, _i, _vp, _i,
+                            _i, _i, _i, _i, _i, _f, _i, _vp, _vp, _sz, _vp],
     "cdml_rope_table": [_vp, _i, _i, _f, _vp],
     "cdml_project_qkv_rope": [_vp] * 10 + [_i, _i, _i, _i, _vp, _i, _i, _i, _vp],
     "cdml_sdpa_fwd": [_vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, _vp],
@@ -79,6 +82,7 @@ SIGNATURES = {
     "cdml_kv_cache_append": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp],
     "cdml_residual_layernorm": [_vp, _vp, _vp, _vp, _vp, _i, _i, _f, _vp],
     "cdml_embed_tokens": [_vp, _i, _vp, _i, _i, _vp, _vp, _vp],
+    "cdml_matmul": [_vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _vp],
     "cdml_linear_preact": [_vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
     "cdml_linear_backward_act": [_vp, _i, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _i, _i,
                                  _vp, _sz, _vp],

@@ -490,10 +490,11 @@ int flash_forward(const float *q, int ldq, const float *k, int ldk, const float 
 
 }  // namespace cdml
 
-extern "C" int cdml_sdpa_fwd(const float *q, int ldq, const float *k, int ldk, const float *v,
-                             int ldv, float *o, int ldo, int batch, int lq, int lk, int dim,
-                             int num_heads, float scale, int causal, const uint8_t *mask,
-                             cdml_stream stream) {
+namespace {
+
+int sdpa_fwd_impl(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv, float *o,
+                  int ldo, float *lse, int batch, int lq, int lk, int dim, int num_heads, float scale,
+                  int causal, const uint8_t *mask, cdml_stream stream) {
   if (batch < 0 || lq < 0 || lk < 0 || dim <= 0 || num_heads <= 0)
     return fail(CDML_E_INVALID, "cdml_sdpa_fwd: bad size (batch %d, lq %d, lk %d, dim %d, heads %d)",
                 batch, lq, lk, dim, num_heads);
@@ -510,6 +511,25 @@ extern "C" int cdml_sdpa_fwd(const float *q, int ldq, const float *k, int ldk, c
   if (!q || !k || !v || !o) return fail(CDML_E_INVALID, "cdml_sdpa_fwd: NULL pointer");
   int rc = ensure_device();
   if (rc) return rc;
-  return flash_forward(q, ldq, k, ldk, v, ldv, o, ldo, nullptr, batch, lq, lk, dim, num_heads, scale,
+  return flash_forward(q, ldq, k, ldk, v, ldv, o, ldo, lse, batch, lq, lk, dim, num_heads, scale,
                        causal != 0, mask, as_hip(stream));
+}
+
+}  // namespace
+
+extern "C" int cdml_sdpa_fwd(const float *q, int ldq, const float *k, int ldk, const float *v,
+                             int ldv, float *o, int ldo, int batch, int lq, int lk, int dim,
+                             int num_heads, float scale, int causal, const uint8_t *mask,
+                             cdml_stream stream) {
+  return sdpa_fwd_impl(q, ldq, k, ldk, v, ldv, o, ldo, nullptr, batch, lq, lk, dim, num_heads, scale,
+                       causal, mask, stream);
+}
+
+extern "C" int cdml_sdpa_fwd_lse(const float *q, int ldq, const float *k, int ldk, const float *v,
+                                 int ldv, float *o, int ldo, float *lse, int batch, int lq, int lk,
+                                 int dim, int num_heads, float scale, int causal,
+                                 const uint8_t *mask, cdml_stream stream) {
+  if (!lse) return fail(CDML_E_INVALID, "cdml_sdpa_fwd_lse: lse is NULL");
+  return sdpa_fwd_impl(q, ldq, k, ldk, v, ldv, o, ldo, lse, batch, lq, lk, dim, num_heads, scale, causal,
+                       mask, stream);
 }

@@ -35,11 +35,11 @@ constexpr float kLog2e = 1.4426950408889634f;
 struct BwdArgs {
   const float *q, *k, *v, *dout;
   float *dq, *dk, *dv;
-  const float *o;      // forward output [batch * lq][dim] (row stride dim)
+  const float *o;      // forward output [batch * lq][dim] (row stride ldo)
   const float *lse;    // [batch * heads][lq]
   float *delta;        // [batch * heads][lq]
   const uint8_t *mask; // [lq][lk] or NULL
-  int ldq, ldk, ldv, lddo, lddq, lddk, lddv;
+  int ldq, ldk, ldv, lddo, lddq, lddk, lddv, ldo;
   int batch, lq, lk, dim, heads, hd;
   float scale, scale_log2;
   int n_tiles, total;
@@ -97,7 +97,7 @@ __global__ void __launch_bounds__(256) bwd_delta_kernel(const BwdArgs a) {
   const long long row = ec / d4;
   const int c4 = (int)(ec % d4);
   const vf4 x = *reinterpret_cast<const vf4 *>(a.dout + row * a.lddo + 4 * c4);
-  const vf4 y = *reinterpret_cast<const vf4 *>(a.o + row * a.dim + 4 * c4);
+  const vf4 y = *reinterpret_cast<const vf4 *>(a.o + row * a.ldo + 4 * c4);
   float s = (x[0] * y[0] + x[1] * y[1]) + (x[2] * y[2] + x[3] * y[3]);
 #pragma unroll
   for (int off = G / 2; off >= 1; off >>= 1) s += __shfl_xor(s, off);
@@ -600,22 +600,35 @@ extern "C" int cdml_sdpa_bwd_workspace_size(int batch, int lq, int lk, int dim, 
   return CDML_OK;
 }
 
-extern "C" int cdml_sdpa_bwd(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv,
-                             const float *dout, int lddo, float *dq, int lddq, float *dk, int lddk,
-                             float *dv, int lddv, int batch, int lq, int lk, int dim, int num_heads,
-                             float scale, int causal, const uint8_t *mask, void *workspace,
-                             size_t workspace_bytes, cdml_stream stream) {
+namespace cdml {
+namespace {
+
+// cdml_sdpa_bwd, and with o_saved / lse_saved the backward from the forward's
+// saved output and row statistics (cdml_sdpa_bwd_saved): no forward pass.
+int sdpa_bwd_impl(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv,
+                  const float *o_saved, int ldo_saved, const float *lse_saved, const float *dout,
+                  int lddo, float *dq, int lddq, float *dk, int lddk, float *dv, int lddv, int batch,
+                  int lq, int lk, int dim, int num_heads, float scale, int causal,
+                  const uint8_t *mask, void *workspace, size_t workspace_bytes, cdml_stream stream,
+                  const char *what) {
+  const bool saved = o_saved != nullptr;
   size_t need = 0;
   int rc = cdml_sdpa_bwd_workspace_size(batch, lq, lk, dim, num_heads, &need);
   if (rc) return rc;
+  if (saved) {
+    need = sizeof(float) * (size_t)batch * num_heads * lq;
+    if (!lse_saved || ldo_saved < dim || ldo_saved % 4 || !aligned16(o_saved))
+      return fail(CDML_E_INVALID, "%s: saved output needs the row statistics, a 16-byte aligned "
+                  "output and a row stride of at least dim (a multiple of 4)", what);
+  }
   if (ldq < dim || ldk < dim || ldv < dim || lddo < dim || lddq < dim || lddk < dim || lddv < dim)
-    return fail(CDML_E_INVALID, "cdml_sdpa_bwd: row stride smaller than dim");
+    return fail(CDML_E_INVALID, "%s: row stride smaller than dim", what);
   if ((long long)ldq * 128 > INT32_MAX || (long long)ldk * 128 > INT32_MAX ||
       (long long)ldv * 128 > INT32_MAX || (long long)lddo * 128 > INT32_MAX)
-    return fail(CDML_E_INVALID, "cdml_sdpa_bwd: row stride above %d elements", INT32_MAX / 128);
+    return fail(CDML_E_INVALID, "%s: row stride above %d elements", what, INT32_MAX / 128);
   if (batch == 0 || (lq == 0 && lk == 0)) return CDML_OK;
   if ((lq && (!dq || !q || !dout)) || (lk && (!dk || !dv || !k || !v)))
-    return fail(CDML_E_INVALID, "cdml_sdpa_bwd: NULL pointer");
+    return fail(CDML_E_INVALID, "%s: NULL pointer", what);
   rc = ensure_device();
   if (rc) return rc;
   hipStream_t st = as_hip(stream);
@@ -626,10 +639,10 @@ extern "C" int cdml_sdpa_bwd(const float *q, int ldq, const float *k, int ldk, c
     return rc;
   }
   if (!workspace || workspace_bytes < need)
-    return fail(CDML_E_INVALID, "cdml_sdpa_bwd: workspace of %zu bytes needed, %zu given", need,
+    return fail(CDML_E_INVALID, "%s: workspace of %zu bytes needed, %zu given", what, need,
                 workspace_bytes);
   if ((long long)batch * num_heads * ((std::max(lq, lk) + BW_TILE - 1) / BW_TILE) > (1LL << 30))
-    return fail(CDML_E_INVALID, "cdml_sdpa_bwd: problem too large");
+    return fail(CDML_E_INVALID, "%s: problem too large", what);
 
   BwdArgs a{};
   a.q = q;
@@ -662,24 +675,36 @@ extern "C" int cdml_sdpa_bwd(const float *q, int ldq, const float *k, int ldk, c
   float *delta = reinterpret_cast<float *>(reinterpret_cast<char *>(lse) + align256(f * bh * lq));
   float *scratch = reinterpret_cast<float *>(reinterpret_cast<char *>(delta) + align256(f * bh * lq));
   a.o = o;
+  a.ldo = dim;
   a.lse = lse;
   a.delta = delta;
+  if (saved) {  // workspace holds D only
+    a.o = o_saved;
+    a.ldo = ldo_saved;
+    a.lse = lse_saved;
+    a.delta = reinterpret_cast<float *>(ws);
+  }
 
   const int hd = a.hd;
   const bool fast = (hd == 32 || hd == 64 || hd == 128) && ldq % 4 == 0 && ldk % 4 == 0 &&
                     ldv % 4 == 0 && lddo % 4 == 0 && lddq % 4 == 0 && lddk % 4 == 0 &&
                     lddv % 4 == 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
                     aligned16(dout) && aligned16(dq) && aligned16(dk) && aligned16(dv);
+  if (!fast && saved)
+    return fail(CDML_E_INVALID, "%s: saved statistics need head dim 32, 64 or 128 and 16-byte aligned "
+                "rows; use cdml_sdpa_bwd", what);
   if (!fast) {
     const size_t smem = f * (2 * (size_t)hd + 8);
-    if (smem > 64 * 1024) return fail(CDML_E_INVALID, "cdml_sdpa_bwd: head dim %d too large", hd);
+    if (smem > 64 * 1024) return fail(CDML_E_INVALID, "%s: head dim %d too large", what, hd);
     flash_bwd_generic_kernel<<<dim3((unsigned)bh), dim3(256), smem, st>>>(a, scratch, causal ? 1 : 0);
     return check_launch("flash_bwd_generic_kernel");
   }
-  // 1. O and the row statistics
-  rc = flash_forward(q, ldq, k, ldk, v, ldv, o, dim, lse, batch, lq, lk, dim, num_heads, scale,
-                     causal != 0, mask, st);
-  if (rc) return rc;
+  // 1. O and the row statistics (unless the caller saved them)
+  if (!saved) {
+    rc = flash_forward(q, ldq, k, ldk, v, ldv, o, dim, lse, batch, lq, lk, dim, num_heads, scale,
+                       causal != 0, mask, st);
+    if (rc) return rc;
+  }
   // 2. D = rowsum(dO * O)
   {
     const long long n = (long long)batch * lq * (dim / 4);
@@ -695,4 +720,29 @@ extern "C" int cdml_sdpa_bwd(const float *q, int ldq, const float *k, int ldk, c
   else if (hd == 64) launch_bwd_hd<64, 64, 32>(a, causal != 0, st);
   else launch_bwd_hd<128, 32, 32>(a, causal != 0, st);
   return check_launch("flash_bwd_dkdv_kernel / flash_bwd_dq_kernel");
+}
+
+}  // namespace
+}  // namespace cdml
+
+extern "C" int cdml_sdpa_bwd(const float *q, int ldq, const float *k, int ldk, const float *v, int ldv,
+                             const float *dout, int lddo, float *dq, int lddq, float *dk, int lddk,
+                             float *dv, int lddv, int batch, int lq, int lk, int dim, int num_heads,
+                             float scale, int causal, const uint8_t *mask, void *workspace,
+                             size_t workspace_bytes, cdml_stream stream) {
+  return sdpa_bwd_impl(q, ldq, k, ldk, v, ldv, nullptr, 0, nullptr, dout, lddo, dq, lddq, dk, lddk, dv,
+                       lddv, batch, lq, lk, dim, num_heads, scale, causal, mask, workspace,
+                       workspace_bytes, stream, "cdml_sdpa_bwd");
+}
+
+extern "C" int cdml_sdpa_bwd_saved(const float *q, int ldq, const float *k, int ldk, const float *v,
+                                   int ldv, const float *o, int ldo, const float *lse,
+                                   const float *dout, int lddo, float *dq, int lddq, float *dk,
+                                   int lddk, float *dv, int lddv, int batch, int lq, int lk, int dim,
+                                   int num_heads, float scale, int causal, const uint8_t *mask,
+                                   void *workspace, size_t workspace_bytes, cdml_stream stream) {
+  if (!o) return fail(CDML_E_INVALID, "cdml_sdpa_bwd_saved: o is NULL");
+  return sdpa_bwd_impl(q, ldq, k, ldk, v, ldv, o, ldo, lse, dout, lddo, dq, lddq, dk, lddk, dv, lddv,
+                       batch, lq, lk, dim, num_heads, scale, causal, mask, workspace, workspace_bytes,
+                       stream, "cdml_sdpa_bwd_saved");
 }

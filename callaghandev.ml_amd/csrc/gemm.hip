@@ -1035,6 +1035,26 @@ extern "C" int cdml_linear_backward_act(const float *x, int ldx, const float *dy
                               "cdml_linear_backward_act");
 }
 
+extern "C" int cdml_matmul(const float *a, int lda, const float *b, int ldb, float *c, int ldc, int m,
+                           int k, int n, cdml_stream stream) {
+  if (m < 0 || k < 0 || n < 0) return fail(CDML_E_INVALID, "cdml_matmul: negative size");
+  if (m == 0 || n == 0) return CDML_OK;
+  if (!a || !b || !c) return fail(CDML_E_INVALID, "cdml_matmul: NULL pointer");
+  if (lda < k || ldb < n || ldc < n) return fail(CDML_E_INVALID, "cdml_matmul: row stride smaller than the row");
+  int rc = ensure_device();
+  if (rc) return rc;
+  GemmArgs g{};  // k == 0: the generic kernel stores zeros
+  g.lda = lda;
+  g.ldb = ldb;
+  g.ldc = ldc;
+  g.M = m;
+  g.N = n;
+  g.K = k;
+  g.nprob = 1;
+  g.p[0] = {a, b, nullptr, c, nullptr};
+  return launch_gemm(g, false, true, as_hip(stream), "cdml_matmul");
+}
+
 extern "C" int cdml_linear_preact(const float *x, int ldx, const float *w, const float *b, float *z,
                                   float *y, int ldy, int rows, int in_dim, int out_dim,
                                   int activation, cdml_stream stream) {

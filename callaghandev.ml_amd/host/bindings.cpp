@@ -335,6 +335,52 @@ PYBIND11_MODULE(_cdml_host, m) {
              return to_numpy(a.BackpropOutputProjection(DL.view, X.view, W.view, mat_inout(wg), vec_inout(bg),
                                                         seqLen, outputDim, embeddingDim));
            })
+      .def("MatrixMultiply",
+           [](HipAccelerationManager &a, py::object A, py::object B) {
+             auto X = mat(A), Y = mat(B);
+             return to_numpy(a.MatrixMultiply(X.view, Y.view));
+           })
+      .def("MatrixMultiplyTranspose",
+           [](HipAccelerationManager &a, py::object A, py::object B) {
+             auto X = mat(A), Y = mat(B);
+             return to_numpy(a.MatrixMultiplyTranspose(X.view, Y.view));
+           })
+      .def("ResidualLayerNormForward",
+           [](HipAccelerationManager &a, py::object x, py::object sl, py::object g, py::object b, float eps) {
+             auto X = mat(x), S = mat(sl);
+             auto G = vec(g), B = vec(b);
+             auto r = a.ResidualLayerNormForward(X.view, S.view, G.view, B.view, eps);
+             return py::make_tuple(to_numpy(std::move(std::get<0>(r))), vec_to_numpy(std::get<1>(r)),
+                                   vec_to_numpy(std::get<2>(r)), to_numpy(std::move(std::get<3>(r))),
+                                   to_numpy(std::move(std::get<4>(r))));
+           },
+           py::arg("input"), py::arg("subLayer"), py::arg("gamma"), py::arg("beta"), py::arg("epsilon") = 1e-5f)
+      .def("LayerNormBackward",
+           [](HipAccelerationManager &a, py::object d, py::object n, py::object g, py::object x, py::object m,
+              py::object v, float eps) {
+             auto D = mat(d), Nn = mat(n), X = mat(x);
+             auto G = vec(g), M = vec(m), V = vec(v);
+             auto r = a.LayerNormBackward(D.view, Nn.view, G.view, X.view, M.view, V.view, eps);
+             return py::make_tuple(to_numpy(std::move(std::get<0>(r))), vec_to_numpy(std::get<1>(r)),
+                                   vec_to_numpy(std::get<2>(r)));
+           },
+           py::arg("dOut"), py::arg("normalized"), py::arg("gamma"), py::arg("input"), py::arg("mean"),
+           py::arg("variance"), py::arg("epsilon") = 1e-5f)
+      .def("CrossEntropyLossAndGradient",
+           [](HipAccelerationManager &a, py::object logits, py::object targets, int targetStart, int effectiveLen) {
+             if (targets.is_none()) throw ArgumentNullException("targets");
+             auto L = mat(logits);
+             auto r = a.CrossEntropyLossAndGradient(L.view, ids_from(targets), targetStart, effectiveLen);
+             return py::make_tuple(r.first, to_numpy(std::move(r.second)));
+           },
+           py::arg("logits"), py::arg("targets"), py::arg("targetStart"), py::arg("effectiveLen"))
+      .def("AccumulateTokenEmbeddingGrad",
+           [](HipAccelerationManager &a, py::object eg, py::object dx, py::object ids, int tokenStart, int seqLen,
+              int dim) {
+             if (ids.is_none()) throw ArgumentNullException("tokenIds");
+             auto D = mat(dx);
+             a.AccumulateTokenEmbeddingGrad(mat_inout(eg), D.view, ids_from(ids), tokenStart, seqLen, dim);
+           })
       .def("Dispose", &HipAccelerationManager::Dispose);
 
   py::class_<TransformerConfig>(m, "TransformerConfig")

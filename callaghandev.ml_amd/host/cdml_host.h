@@ -200,6 +200,26 @@ class HipAccelerationManager {
                                   MatRef weightGrad, VecRef biasGrad, int seqLen, int outputDim,
                                   int embeddingDim);
 
+  // ---- the rest of the training step with real work per call ---------------
+  // IAccelerationManager.MatrixMultiply (:20) / MatrixMultiplyTranspose (:26)
+  Matrix MatrixMultiply(MatView A, MatView B);
+  Matrix MatrixMultiplyTranspose(MatView A, MatView B);
+  // IAccelerationManager.ResidualLayerNormForward (:138): (output, means,
+  // variances, normalized, residual)
+  std::tuple<Matrix, std::vector<float>, std::vector<float>, Matrix, Matrix>
+  ResidualLayerNormForward(MatView input, MatView subLayer, VecView gamma, VecView beta,
+                           float epsilon = 1e-5f);
+  // IAccelerationManager.LayerNormBackward (:143): (dInput, dGamma, dBeta)
+  std::tuple<Matrix, std::vector<float>, std::vector<float>>
+  LayerNormBackward(MatView dOut, MatView normalized, VecView gamma, MatView input, VecView mean,
+                    VecView variance, float epsilon = 1e-5f);
+  // IAccelerationManager.CrossEntropyLossAndGradient (:207, :209)
+  std::pair<float, Matrix> CrossEntropyLossAndGradient(MatView logits, const std::vector<int> &targets,
+                                                       int targetStart, int effectiveLen);
+  // IAccelerationManager.AccumulateTokenEmbeddingGrad (:203, :205)
+  void AccumulateTokenEmbeddingGrad(MatRef embeddingGrad, MatView dX, const std::vector<int> &tokenIds,
+                                    int tokenStart, int seqLen, int embeddingDim);
+
   // Optional decode capability (no IAccelerationManager counterpart: the
   // reference runs this inline in LanguageModel.DecoderSelfAttentionStep,
   // LanguageModel.cs:353-427).  q, k, v [1, D] are the step's projections
@@ -481,6 +501,7 @@ class DeviceTrainer {
     std::vector<int> ffrows, ffcols, ffact;
     // forward cache of the current bucket
     float *x, *q, *k, *v, *att, *r1, *n1, *m1, *v1, *r2, *m2, *v2;
+    float *lse;  // attention row statistics of the forward (NULL: the backward recomputes them)
     std::vector<float *> z, h;  // pre-activation / activation of each FFN hidden layer
   };
   float *alloc(size_t floats);

@@ -5,6 +5,7 @@
 // weight arrays, runs the kernel(s) on the manager's stream and returns host
 // arrays.  Nothing here computes on the CPU: a missing device or library is
 // an InvalidOperationException.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 
@@ -723,6 +724,224 @@ Matrix HipAccelerationManager::BackpropOutputProjection(MatView dLogits, MatView
   Matrix dX(seqLen, embeddingDim);
   linear_backward(input, dLogits, seqLen, weights, weightGrad, biasGrad, dX.ptr(), false);
   return dX;
+}
+
+// ---- MatrixMultiply / MatrixMultiplyTranspose: AccelerationCPU.cs:159-250 ----
+Matrix HipAccelerationManager::MatrixMultiply(MatView A, MatView B) {
+  if (A.null()) throw ArgumentNullException("A");
+  if (B.null()) throw ArgumentNullException("B");
+  if (A.cols != B.rows)
+    throw ArgumentException("Matrix dimensions don't match: [" + std::to_string(A.rows) + "x" +
+                            std::to_string(A.cols) + "] * [" + std::to_string(B.rows) + "x" +
+                            std::to_string(B.cols) + "]");
+  Matrix C(A.rows, B.cols);
+  if (A.rows == 0 || B.cols == 0 || A.cols == 0) return C;
+  std::lock_guard<std::mutex> lock(mu_);
+  ensure_ready();
+  const size_t ab = (size_t)A.rows * A.cols * 4, bb = (size_t)B.rows * B.cols * 4,
+               cb = (size_t)A.rows * B.cols * 4;
+  float *da = static_cast<float *>(scratch(S_X, ab));
+  float *db = static_cast<float *>(scratch(S_Q, bb));
+  float *dc = static_cast<float *>(scratch(S_O, cb));
+  upload(da, A.data, ab);
+  upload(db, B.data, bb);
+  check(cdml_matmul(da, A.cols, db, B.cols, dc, B.cols, A.rows, A.cols, B.cols, stream_), "cdml_matmul");
+  download(C.ptr(), dc, cb);
+  sync();
+  return C;
+}
+
+Matrix HipAccelerationManager::MatrixMultiplyTranspose(MatView A, MatView B) {
+  if (A.null()) throw ArgumentNullException("A");
+  if (B.null()) throw ArgumentNullException("B");
+  if (A.cols != B.cols) throw ArgumentException("Matrix dimensions don't match for A*B^T");
+  Matrix C(A.rows, B.rows);
+  if (A.rows == 0 || B.rows == 0 || A.cols == 0) return C;
+  std::lock_guard<std::mutex> lock(mu_);
+  ensure_ready();
+  const size_t ab = (size_t)A.rows * A.cols * 4, bb = (size_t)B.rows * B.cols * 4,
+               cb = (size_t)A.rows * B.rows * 4;
+  float *da = static_cast<float *>(scratch(S_X, ab));
+  float *db = static_cast<float *>(scratch(S_Q, bb));
+  float *dc = static_cast<float *>(scratch(S_O, cb));
+  upload(da, A.data, ab);
+  upload(db, B.data, bb);
+  check(cdml_linear(da, A.cols, db, nullptr, dc, B.rows, A.rows, A.cols, B.rows, CDML_ACT_NONE, stream_),
+        "cdml_linear");
+  download(C.ptr(), dc, cb);
+  sync();
+  return C;
+}
+
+// ---- ResidualLayerNormForward: AccelerationCPU.cs:1440-1514 -------------------
+std::tuple<Matrix, std::vector<float>, std::vector<float>, Matrix, Matrix>
+HipAccelerationManager::ResidualLayerNormForward(MatView input, MatView subLayer, VecView gamma,
+                                                 VecView beta, float epsilon) {
+  if (input.null()) throw ArgumentNullException("input");
+  if (subLayer.null()) throw ArgumentNullException("subLayer");
+  if (gamma.null()) throw ArgumentNullException("gamma");
+  if (beta.null()) throw ArgumentNullException("beta");
+  const int rows = input.rows, f = input.cols;
+  if (subLayer.rows != rows || subLayer.cols != f)
+    throw ArgumentException("Residual input dimensions must match.", "subLayer");
+  if (gamma.length != f || beta.length != f)
+    throw ArgumentException("Layer norm gamma/beta must match the feature dimension.");
+  if (f > 2048) throw ArgumentException("ResidualLayerNormForward supports up to 2048 features.", "input");
+  Matrix out(rows, f), norm(rows, f), res(rows, f);
+  std::vector<float> mean(rows), var(rows);
+  if (rows == 0 || f == 0) return {std::move(out), std::move(mean), std::move(var), std::move(norm), std::move(res)};
+  std::lock_guard<std::mutex> lock(mu_);
+  ensure_ready();
+  const size_t bytes = (size_t)rows * f * 4;
+  const float *dg = resident(gamma.data, 1, f), *dbt = resident(beta.data, 1, f);
+  float *da = static_cast<float *>(scratch(S_X, bytes));
+  float *dbb = static_cast<float *>(scratch(S_Q, bytes));
+  float *dy = static_cast<float *>(scratch(S_O, bytes));
+  float *dn = static_cast<float *>(scratch(S_K, bytes));
+  float *dr = static_cast<float *>(scratch(S_V, bytes));
+  float *dm = static_cast<float *>(scratch(S_DQ, (size_t)rows * 8));
+  upload(da, input.data, bytes);
+  upload(dbb, subLayer.data, bytes);
+  check(cdml_residual_layernorm_fwd(da, dbb, dg, dbt, dy, dm, dm + rows, dr, dn, rows, f, epsilon, stream_),
+        "cdml_residual_layernorm_fwd");
+  download(out.ptr(), dy, bytes);
+  download(norm.ptr(), dn, bytes);
+  download(res.ptr(), dr, bytes);
+  download(mean.data(), dm, (size_t)rows * 4);
+  download(var.data(), dm + rows, (size_t)rows * 4);
+  sync();
+  return {std::move(out), std::move(mean), std::move(var), std::move(norm), std::move(res)};
+}
+
+// ---- LayerNormBackward: AccelerationCPU.cs:1516-1564 ----------------------------
+// The reference indexes its arguments without checks; every shape is checked
+// here first (ArgumentException).
+std::tuple<Matrix, std::vector<float>, std::vector<float>>
+HipAccelerationManager::LayerNormBackward(MatView dOut, MatView normalized, VecView gamma, MatView input,
+                                          VecView mean, VecView variance, float epsilon) {
+  if (dOut.null()) throw ArgumentNullException("dOut");
+  if (normalized.null()) throw ArgumentNullException("normalized");
+  if (gamma.null()) throw ArgumentNullException("gamma");
+  if (input.null()) throw ArgumentNullException("input");
+  if (mean.null()) throw ArgumentNullException("mean");
+  if (variance.null()) throw ArgumentNullException("variance");
+  const int rows = dOut.rows, f = dOut.cols;
+  if (normalized.rows != rows || normalized.cols != f || input.rows != rows || input.cols != f)
+    throw ArgumentException("normalized and input must have dOut's shape.");
+  if (gamma.length != f) throw ArgumentException("gamma must match the feature dimension.", "gamma");
+  if (mean.length < rows || variance.length < rows)
+    throw ArgumentException("mean and variance need one entry per row.");
+  if (f > 2048) throw ArgumentException("LayerNormBackward supports up to 2048 features.", "dOut");
+  Matrix dx(rows, f);
+  std::vector<float> dg(f), db(f);
+  if (rows == 0 || f == 0) return {std::move(dx), std::move(dg), std::move(db)};
+  std::lock_guard<std::mutex> lock(mu_);
+  ensure_ready();
+  const size_t bytes = (size_t)rows * f * 4;
+  float *dd = static_cast<float *>(scratch(S_X, bytes));
+  float *dn = static_cast<float *>(scratch(S_Q, bytes));
+  float *di = static_cast<float *>(scratch(S_K, bytes));
+  float *dxo = static_cast<float *>(scratch(S_O, bytes));
+  float *dmv = static_cast<float *>(scratch(S_DQ, (size_t)rows * 8));
+  float *dgb = static_cast<float *>(scratch(S_GB0, (size_t)f * 8 + 4 * (size_t)f));
+  float *dgam = dgb + 2 * (size_t)f;
+  size_t ws = 0;
+  check(cdml_layernorm_backward_workspace_size(rows, f, &ws), "cdml_layernorm_backward_workspace_size");
+  void *dws = scratch(S_WS, ws);
+  upload(dd, dOut.data, bytes);
+  upload(dn, normalized.data, bytes);
+  upload(di, input.data, bytes);
+  upload(dmv, mean.data, (size_t)rows * 4);
+  upload(dmv + rows, variance.data, (size_t)rows * 4);
+  upload(dgam, gamma.data, (size_t)f * 4);
+  check(cdml_layernorm_backward(dd, nullptr, dn, dgam, di, dmv, dmv + rows, dxo, dgb, dgb + f, rows, f, epsilon,
+                                0, dws, ws, stream_),
+        "cdml_layernorm_backward");
+  download(dx.ptr(), dxo, bytes);
+  download(dg.data(), dgb, (size_t)f * 4);
+  download(db.data(), dgb + f, (size_t)f * 4);
+  sync();
+  return {std::move(dx), std::move(dg), std::move(db)};
+}
+
+// ---- CrossEntropyLossAndGradient: AccelerationCPU.cs:2372-2440 -----------------
+std::pair<float, Matrix> HipAccelerationManager::CrossEntropyLossAndGradient(
+    MatView logits, const std::vector<int> &targets, int targetStart, int effectiveLen) {
+  if (logits.null()) throw ArgumentNullException("logits");
+  if (targetStart < 0 || effectiveLen < 0 || (long long)targetStart + effectiveLen > (long long)targets.size())
+    throw ArgumentOutOfRangeException("targetStart");
+  const int rows = logits.rows, v = logits.cols;
+  Matrix dl(rows, v);
+  if (effectiveLen == 0) return {0.f, std::move(dl)};
+  // the reference reads row i < effectiveLen and the target's column without
+  // checks; both are checked here
+  if (effectiveLen > rows) throw ArgumentException("effectiveLen exceeds the logits rows.", "effectiveLen");
+  for (int i = 0; i < effectiveLen; ++i)
+    if ((unsigned)targets[targetStart + i] >= (unsigned)v)
+      throw ArgumentOutOfRangeException("targets", "Target out of range: " + std::to_string(targets[targetStart + i]));
+  std::lock_guard<std::mutex> lock(mu_);
+  ensure_ready();
+  const size_t bytes = (size_t)rows * v * 4;
+  float *dlog = static_cast<float *>(scratch(S_X, bytes));
+  int *dt = static_cast<int *>(scratch(S_IDS, (size_t)effectiveLen * 4));
+  float *dloss = static_cast<float *>(scratch(S_BIAS, 4));
+  size_t ws = 0;
+  check(cdml_cross_entropy_workspace_size(rows, &ws), "cdml_cross_entropy_workspace_size");
+  void *dws = scratch(S_WS, ws);
+  upload(dlog, logits.data, bytes);
+  upload(dt, targets.data() + targetStart, (size_t)effectiveLen * 4);
+  check(cdml_cross_entropy(dlog, v, dt, rows, v, effectiveLen, 1.0f, 1.0f, dloss, dlog, v, dws, ws, stream_),
+        "cdml_cross_entropy");
+  float loss = 0.f;
+  download(dl.ptr(), dlog, bytes);
+  download(&loss, dloss, 4);
+  sync();
+  return {loss, std::move(dl)};
+}
+
+// ---- AccumulateTokenEmbeddingGrad: AccelerationCPU.cs:2339-2370 ----------------
+void HipAccelerationManager::AccumulateTokenEmbeddingGrad(MatRef embeddingGrad, MatView dX,
+                                                          const std::vector<int> &tokenIds, int tokenStart,
+                                                          int seqLen, int embeddingDim) {
+  if (!embeddingGrad.data) throw ArgumentNullException("embeddingGrad");
+  if (dX.null()) throw ArgumentNullException("dX");
+  if (tokenStart < 0 || seqLen < 0 || (long long)tokenStart + seqLen > (long long)tokenIds.size())
+    throw ArgumentOutOfRangeException("tokenStart");
+  if (embeddingGrad.cols != embeddingDim || dX.cols != embeddingDim || dX.rows < seqLen)
+    throw ArgumentException("embeddingGrad and dX must be [*, embeddingDim] with seqLen rows of dX.");
+  const int vocab = embeddingGrad.rows;
+  for (int i = 0; i < seqLen; ++i)
+    if ((unsigned)tokenIds[tokenStart + i] >= (unsigned)vocab)
+      throw ArgumentOutOfRangeException("tokenIds", "Token out of range: " + std::to_string(tokenIds[tokenStart + i]));
+  if (seqLen == 0 || embeddingDim == 0) return;
+  // rows grouped by token, each group in row order (the reference's summation order)
+  std::vector<int> order(seqLen);
+  for (int i = 0; i < seqLen; ++i) order[i] = i;
+  std::stable_sort(order.begin(), order.end(),
+                   [&](int a, int b) { return tokenIds[tokenStart + a] < tokenIds[tokenStart + b]; });
+  std::vector<int> start, token;
+  for (int i = 0; i < seqLen; ++i)
+    if (i == 0 || tokenIds[tokenStart + order[i]] != tokenIds[tokenStart + order[i - 1]]) {
+      start.push_back(i);
+      token.push_back(tokenIds[tokenStart + order[i]]);
+    }
+  start.push_back(seqLen);
+  std::lock_guard<std::mutex> lock(mu_);
+  ensure_ready();
+  const size_t gb = (size_t)vocab * embeddingDim * 4, xb = (size_t)seqLen * embeddingDim * 4;
+  float *dg = static_cast<float *>(scratch(S_O, gb));
+  float *dx = static_cast<float *>(scratch(S_X, xb));
+  int *di = static_cast<int *>(scratch(S_IDS, ((size_t)seqLen * 3 + 1) * 4));
+  upload(dg, embeddingGrad.data, gb);
+  upload(dx, dX.data, xb);
+  upload(di, order.data(), (size_t)seqLen * 4);
+  upload(di + seqLen, start.data(), start.size() * 4);
+  upload(di + 2 * seqLen + 1, token.data(), token.size() * 4);
+  check(cdml_embedding_grad(dg, dx, nullptr, embeddingDim, di, di + seqLen, di + 2 * seqLen + 1,
+                            (int)token.size(), embeddingDim, stream_),
+        "cdml_embedding_grad");
+  download(embeddingGrad.data, dg, gb);
+  sync();
 }
 
 // ---- decode capability ------------------------------------------------------

@@ -194,6 +194,8 @@ DeviceTrainer::DeviceTrainer(const LanguageModel &model, const TrainingConfig &c
       Y.v1 = alloc(rows);
       Y.m2 = alloc(rows);
       Y.v2 = alloc(rows);
+      // the saved-statistics attention backward covers head dims 32, 64 and 128
+      Y.lse = (hd == 32 || hd == 64 || hd == 128) && D % 4 == 0 ? alloc((size_t)cap_b_ * H * cap_s_) : nullptr;
       layers_.push_back(std::move(Y));
     }
     xfinal_ = alloc(rows * D);
@@ -300,8 +302,13 @@ void DeviceTrainer::bucket_forward(int batch, int seqLen, float grad_scale, floa
     check(cdml_project_qkv_rope(Y.x, Y.wq, Y.bq, Y.wk, Y.bk, Y.wv, Y.bv, Y.q, Y.k, Y.v, rows, D, D, hd,
                                 rope_cs_, cap_s_, 0, seqLen, s),
           "cdml_project_qkv_rope");
-    check(cdml_sdpa_fwd(Y.q, D, Y.k, D, Y.v, D, Y.att, D, batch, seqLen, seqLen, D, H, scale, 1, nullptr, s),
-          "cdml_sdpa_fwd");
+    if (Y.lse)  // keep the row statistics: the backward then skips its forward pass
+      check(cdml_sdpa_fwd_lse(Y.q, D, Y.k, D, Y.v, D, Y.att, D, Y.lse, batch, seqLen, seqLen, D, H, scale, 1,
+                              nullptr, s),
+            "cdml_sdpa_fwd_lse");
+    else
+      check(cdml_sdpa_fwd(Y.q, D, Y.k, D, Y.v, D, Y.att, D, batch, seqLen, seqLen, D, H, scale, 1, nullptr, s),
+            "cdml_sdpa_fwd");
     check(cdml_linear(Y.att, D, Y.wo, Y.bo, tmp_, D, rows, D, D, CDML_ACT_NONE, s), "cdml_linear");
     check(cdml_residual_layernorm_fwd(Y.x, tmp_, Y.ln1g, Y.ln1b, Y.n1, Y.m1, Y.v1, Y.r1, nullptr, rows, D, eps, s),
           "cdml_residual_layernorm_fwd");
@@ -366,9 +373,14 @@ void DeviceTrainer::bucket_backward(int batch, int seqLen) {
     // attention (BackpropAttention, :933-987)
     check(cdml_linear_backward(Y.att, D, dr1_, D, Y.wo, dcat_, D, Y.gwo, Y.gbo, rows, D, D, 0, ws_, ws_bytes_, s),
           "cdml_linear_backward");
-    check(cdml_sdpa_bwd(Y.q, D, Y.k, D, Y.v, D, dcat_, D, dq_, D, dk_, D, dv_, D, batch, seqLen, seqLen, D, H,
-                        scale, 1, nullptr, ws_, ws_bytes_, s),
-          "cdml_sdpa_bwd");
+    if (Y.lse)
+      check(cdml_sdpa_bwd_saved(Y.q, D, Y.k, D, Y.v, D, Y.att, D, Y.lse, dcat_, D, dq_, D, dk_, D, dv_, D, batch,
+                                seqLen, seqLen, D, H, scale, 1, nullptr, ws_, ws_bytes_, s),
+            "cdml_sdpa_bwd_saved");
+    else
+      check(cdml_sdpa_bwd(Y.q, D, Y.k, D, Y.v, D, dcat_, D, dq_, D, dk_, D, dv_, D, batch, seqLen, seqLen, D, H,
+                          scale, 1, nullptr, ws_, ws_bytes_, s),
+            "cdml_sdpa_bwd");
     check(cdml_rope(dq_, rows, D, 0, hd, H, 10000.0f, 1, 0, seqLen, nullptr, s), "cdml_rope");
     check(cdml_rope(dk_, rows, D, 0, hd, H, 10000.0f, 1, 0, seqLen, nullptr, s), "cdml_rope");
     check(cdml_backprop_qkv(Y.x, dq_, dk_, dv_, Y.wq, Y.wk, Y.wv, Y.gwq, Y.gbq, Y.gwk, Y.gbk, Y.gwv, Y.gbv, dxa_,

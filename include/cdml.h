@@ -128,6 +128,15 @@ int cdml_linear(const float *x, int ldx, const float *w, const float *b,
                 float *y, int ldy, int rows, int in_dim, int out_dim,
                 int activation, cdml_stream stream);
 
+/* IAccelerationManager.MatrixMultiply (:20), replacing AccelerationCPU.cs:
+ * 159-214 (the FFN backward's hidden deltas and input gradient,
+ * NeuralNetwork.cs:861-881): c = a b with a [m, k] (row stride lda), b
+ * [k, n] (row stride ldb), c [m, n] (row stride ldc); fp32 MFMA.
+ * MatrixMultiplyTranspose (:26, a b^T) is cdml_linear with b as the weight
+ * and no bias. */
+int cdml_matmul(const float *a, int lda, const float *b, int ldb, float *c,
+                int ldc, int m, int k, int n, cdml_stream stream);
+
 /* IAccelerationManager.BackpropLinearProjection (:182) and
  * BackpropOutputProjection (:184), replacing AccelerationCPU.cs:2188-2270:
  *   wgrad += dy^T x,  bgrad += column sums of dy,  dx (+)= dy w
@@ -224,6 +233,15 @@ int cdml_sdpa_fwd(const float *q, int ldq, const float *k, int ldk,
                   int lq, int lk, int dim, int num_heads, float scale,
                   int causal, const uint8_t *mask, cdml_stream stream);
 
+/* cdml_sdpa_fwd that also keeps each row's softmax statistics for a later
+ * cdml_sdpa_bwd_saved: lse (device, [batch * num_heads][lq] floats, an
+ * opaque per-row normaliser).  Head dims up to 128. */
+int cdml_sdpa_fwd_lse(const float *q, int ldq, const float *k, int ldk,
+                      const float *v, int ldv, float *o, int ldo, float *lse,
+                      int batch, int lq, int lk, int dim, int num_heads,
+                      float scale, int causal, const uint8_t *mask,
+                      cdml_stream stream);
+
 /* IAccelerationManager.MultiHeadAttentionBackward, both overloads (:161,
  * :163), replacing AccelerationCPU.cs:1011-1280.  For `batch` independent
  * sequences (the segmented trainer's SegmentedMultiHeadAttentionBackward,
@@ -246,6 +264,21 @@ int cdml_sdpa_bwd(const float *q, int ldq, const float *k, int ldk,
                   int lddv, int batch, int lq, int lk, int dim, int num_heads,
                   float scale, int causal, const uint8_t *mask,
                   void *workspace, size_t workspace_bytes, cdml_stream stream);
+
+/* cdml_sdpa_bwd from the forward pass's own output o (row stride ldo) and
+ * row statistics lse, as cdml_sdpa_fwd_lse wrote them for the same q, k, v,
+ * scale, causal flag and mask: no forward pass is repeated.  This is the
+ * trainer's form (TransformerTrainer keeps the attention output in its
+ * cache, AttentionCache.cs:9-38).  Head dims 32, 64 and 128 with 16-byte
+ * aligned rows; workspace: batch * num_heads * lq floats. */
+int cdml_sdpa_bwd_saved(const float *q, int ldq, const float *k, int ldk,
+                        const float *v, int ldv, const float *o, int ldo,
+                        const float *lse, const float *dout, int lddo,
+                        float *dq, int lddq, float *dk, int lddk, float *dv,
+                        int lddv, int batch, int lq, int lk, int dim,
+                        int num_heads, float scale, int causal,
+                        const uint8_t *mask, void *workspace,
+                        size_t workspace_bytes, cdml_stream stream);
 
 /* ---- training step (TransformerTrainer.TrainBatchDiscrete,
  * Transformers/MultiTypeTransformer/TransformerTrainer.cs:217-327) -------- */

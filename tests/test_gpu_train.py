@@ -262,3 +262,46 @@ def test_device_trainer_loss_decreases():
     losses = [t.TrainBatch(seqs, 0.05) for _ in range(40)]
     assert all(b < a for a, b in zip(losses[:10], losses[1:11])), losses
     assert losses[-1] < 0.8 * losses[0], losses
+
+
+@pytest.mark.parametrize("batch,L,dim,heads", [(2, 300, 128, 2), (1, 257, 256, 2), (3, 130, 96, 3), (2, 64, 512, 4)])
+def test_sdpa_bwd_from_saved_statistics(batch, L, dim, heads):
+    """The trainer's attention backward from the forward's saved output and
+    row statistics (cdml_sdpa_fwd_lse + cdml_sdpa_bwd_saved) gives the same
+    bits as cdml_sdpa_bwd, which recomputes them, and the forward's output is
+    the same as cdml_sdpa_fwd's."""
+    import ctypes as C
+    from cdml import native as N
+    rows = batch * L
+    q, k, v, g = (synth.normal(80 + i, (rows, dim)) for i in range(4))
+    scale = float(np.float32(1) / np.sqrt(np.float32(dim // heads)))
+    bq, bk, bv, bg = (G.up(a) for a in (q, k, v, g))
+    o1, o2 = N.DeviceBuffer(rows * dim * 4), N.DeviceBuffer(rows * dim * 4)
+    lse = N.DeviceBuffer(batch * heads * L * 4)
+    s = G.stream().handle
+    lib = N.lib()
+    N.check(lib.cdml_sdpa_fwd(bq.ptr, dim, bk.ptr, dim, bv.ptr, dim, o1.ptr, dim, batch, L, L, dim, heads, scale,
+                              1, None, s))
+    N.check(lib.cdml_sdpa_fwd_lse(bq.ptr, dim, bk.ptr, dim, bv.ptr, dim, o2.ptr, dim, lse.ptr, batch, L, L, dim,
+                                  heads, scale, 1, None, s))
+    assert np.array_equal(G.down(o1, (rows, dim)), G.down(o2, (rows, dim)))
+    ws = C.c_size_t(0)
+    N.check(lib.cdml_sdpa_bwd_workspace_size(batch, L, L, dim, heads, C.byref(ws)))
+    bws = N.DeviceBuffer(ws.value)
+    outs = [[N.DeviceBuffer(rows * dim * 4) for _ in range(3)] for _ in range(2)]
+    N.check(lib.cdml_sdpa_bwd(bq.ptr, dim, bk.ptr, dim, bv.ptr, dim, bg.ptr, dim, outs[0][0].ptr, dim,
+                              outs[0][1].ptr, dim, outs[0][2].ptr, dim, batch, L, L, dim, heads, scale, 1, None,
+                              bws.ptr, ws.value, s))
+    small = batch * heads * L * 4
+    N.check(lib.cdml_sdpa_bwd_saved(bq.ptr, dim, bk.ptr, dim, bv.ptr, dim, o2.ptr, dim, lse.ptr, bg.ptr, dim,
+                                    outs[1][0].ptr, dim, outs[1][1].ptr, dim, outs[1][2].ptr, dim, batch, L, L,
+                                    dim, heads, scale, 1, None, bws.ptr, small, s))
+    for a, b, n in zip(outs[0], outs[1], "QKV"):
+        assert np.array_equal(G.down(a, (rows, dim)), G.down(b, (rows, dim))), f"d{n}"
+    want = O.mha_backward(q[:L], k[:L], v[:L], g[:L], heads, scale, use_decoder_mask=True)
+    for a, e, n in zip(outs[1], want, "QKV"):
+        parity(G.down(a, (rows, dim))[:L], e, f"saved-statistics d{n} vs oracle")
+    rc = lib.cdml_sdpa_bwd_saved(bq.ptr, dim, bk.ptr, dim, bv.ptr, dim, o2.ptr, dim, lse.ptr, bg.ptr, dim,
+                                 outs[1][0].ptr, dim, outs[1][1].ptr, dim, outs[1][2].ptr, dim, batch, L, L, dim,
+                                 heads, scale, 1, None, bws.ptr, small - 4, s)
+    assert rc == -1

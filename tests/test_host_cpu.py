@@ -185,6 +185,28 @@ def test_backward_argument_rules(mgr):
     assert [a.shape for a in r] == [(0, 8), (5, 8), (5, 8)] and not any(a.any() for a in r)
 
 
+def test_training_method_argument_rules(mgr):
+    z = np.zeros
+    with pytest.raises(H.ArgumentException, match="don't match"):
+        mgr.MatrixMultiply(M(3, 4, 1), M(5, 2, 2))
+    with pytest.raises(H.ArgumentException, match="A\\*B\\^T"):
+        mgr.MatrixMultiplyTranspose(M(3, 4, 1), M(5, 2, 2))
+    with pytest.raises(H.ArgumentException, match="Residual input dimensions"):
+        mgr.ResidualLayerNormForward(M(3, 4, 1), M(3, 5, 2), Vec(4, 3), Vec(4, 4))
+    with pytest.raises(H.ArgumentException, match="gamma"):
+        mgr.LayerNormBackward(M(3, 4, 1), M(3, 4, 2), Vec(5, 3), M(3, 4, 4), Vec(3, 5), Vec(3, 6))
+    with pytest.raises(H.ArgumentOutOfRangeException, match="targetStart"):
+        mgr.CrossEntropyLossAndGradient(M(3, 4, 1), np.array([0, 1], np.int32), 1, 2)
+    with pytest.raises(H.ArgumentOutOfRangeException, match="Target out of range"):
+        mgr.CrossEntropyLossAndGradient(M(3, 4, 1), np.array([0, 4, 1], np.int32), 0, 3)
+    loss, dl = mgr.CrossEntropyLossAndGradient(M(3, 4, 1), np.array([0, 1], np.int32), 0, 0)
+    assert loss == 0 and dl.shape == (3, 4) and not dl.any()  # no device work
+    with pytest.raises(H.ArgumentOutOfRangeException, match="tokenStart"):
+        mgr.AccumulateTokenEmbeddingGrad(z((5, 2), np.float32), M(3, 2, 1), np.array([0, 1], np.int32), 0, 3, 2)
+    with pytest.raises(H.ArgumentOutOfRangeException, match="Token out of range"):
+        mgr.AccumulateTokenEmbeddingGrad(z((5, 2), np.float32), M(2, 2, 1), np.array([0, 5], np.int32), 0, 2, 2)
+
+
 def test_no_device_means_loud_failure(mgr):
     if N.device_count() > 0:
         pytest.skip("a device is visible")

@@ -191,6 +191,42 @@ def test_manager_projection_backward(mgr):
         parity(got, e, f"BackpropOutputProjection LM head {n}")
 
 
+def test_manager_training_methods(mgr):
+    """MatrixMultiply / MatrixMultiplyTranspose, ResidualLayerNormForward,
+    LayerNormBackward, CrossEntropyLossAndGradient and
+    AccumulateTokenEmbeddingGrad against the oracle (MatrixMultiply against
+    float64 matrix algebra, the reference's textbook product)."""
+    A, B = synth.normal(1, (130, 257)), synth.normal(2, (257, 66))
+    ref = A.astype(np.float64) @ B.astype(np.float64)
+    parity(mgr.MatrixMultiply(A, B), ref, "MatrixMultiply")
+    parity(mgr.MatrixMultiplyTranspose(A, np.ascontiguousarray(B.T)), ref, "MatrixMultiplyTranspose")
+    x, sl = synth.normal(3, (40, 96)), synth.normal(4, (40, 96))
+    g, be = synth.positive_vector(96, 5), synth.normal(6, (96,))
+    got = mgr.ResidualLayerNormForward(x, sl, g, be)
+    want = O.residual_layernorm_forward(x, sl, g, be)
+    for a, e, n in zip(got, want, ("output", "means", "variances", "normalized", "residual")):
+        parity(a, e, f"ResidualLayerNormForward {n}")
+    d = synth.normal(7, (40, 96))
+    got = mgr.LayerNormBackward(d, want[3], g, want[4], want[1], want[2])
+    for a, e, n in zip(got, O.layernorm_backward(d, want[3], g, want[4], want[1], want[2]),
+                       ("dInput", "dGamma", "dBeta")):
+        parity(a, e, f"LayerNormBackward {n}")
+    logits = synth.normal(8, (12, 200)) * np.float32(2)
+    t = (np.arange(20) * 37 % 200).astype(np.int32)
+    loss, dl = mgr.CrossEntropyLossAndGradient(logits, t, 3, 10)
+    wl, wd = O.cross_entropy(logits, t, 10, target_start=3)
+    assert abs(loss - wl) <= 1e-5 + 1e-5 * abs(wl)
+    parity(dl, wd, "CrossEntropyLossAndGradient")
+    eg = synth.normal(9, (50, 16))
+    dx = synth.normal(10, (30, 16))
+    ids = (np.arange(40) * 7 % 50).astype(np.int32)
+    ids[5:15] = 4
+    want = O.accumulate_token_embedding_grad(eg, dx, ids[5:35])
+    got = eg.copy()
+    mgr.AccumulateTokenEmbeddingGrad(got, dx, ids, 5, 30, 16)
+    assert np.array_equal(got, want)
+
+
 def test_manager_decode_step_matches_prefill(mgr):
     """The decode capability over T steps reproduces causal prefill row by row
     (RoPE at the absolute position, append, attend)."""
