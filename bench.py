@@ -325,6 +325,20 @@ def extras(N, st):
                     4, 4095, 3, 1),
         workload="TrainBatchDiscrete on 4 sequences of 4096 tokens, 12 decoder layers D 1024 / 16 heads / "
                  "FF 4096 (config-3 shape) with a 1000-token vocabulary")
+    cfg5t = {"dim": 256, "heads": 8, "layers": 6, "ff": 1024, "max_seq": 512, "discrete": False, "input_dim": 5,
+             "output_dim": 1}
+    lm5t, _ = host.language_model(cfg5t, synth.continuous_lm_weights(cfg5t, 19))
+    t5 = H.DeviceTrainer(lm5t, H.TrainingConfig(), 256, 511)
+    win = synth.random_walk_windows(33, 256, 512, 5)
+    tgt = np.ascontiguousarray(win[:, :, :1])  # next-step regression of the first feature
+    ms5t = t5.time_step_continuous(win, tgt, 1e-3, 3, 1)
+    core, qkv, o = mha_flops(256, 511, 256, 8)
+    fwd5 = 6 * (core + qkv + o + 4 * 256 * 511 * 256 * 1024) + 2 * 256 * 511 * 256 * (5 + 1)
+    out["c5_time_series_train_step"] = {
+        "ms": round(ms5t, 3), "windows_per_s": round(256 / (ms5t * 1e-3), 1),
+        "tflops": round(3 * fwd5 / (ms5t * 1e-3) / 1e12, 2),
+        "workload": "TrainBatchContinuous (MSE) on 256 windows of 512 steps, config-5 model"}
+    del t5, lm5t
     log("[bench] extras: c3 12-layer decoder stack")
     # c3: 12 post-LN decoder layers (MHA + FFN 4096 + 2 LayerNorms) on N(0,1) embeddings
     cfg3 = {"dim": 1024, "heads": 16, "layers": 12, "ff": 4096, "max_seq": 4096, "discrete": False,

@@ -45,6 +45,9 @@ def config(cfg: dict, **overrides):
     c.FeedForwardDim = int(cfg["ff"])
     c.MaxSequenceLength = int(cfg["max_seq"])
     c.UsesDiscreteTokens = bool(cfg.get("discrete", True))
+    # TransformerDataType: Text 0 for token models, TimeSeriesRegression 1
+    # (or TimeSeriesClassification 2) for continuous ones
+    c.DataType = int(cfg.get("data_type", 0 if c.UsesDiscreteTokens else 1))
     c.UseDecoderOnly = bool(cfg.get("decoder_only", True))
     c.InputFeatureDim = int(cfg.get("input_dim", 1))
     c.OutputDim = int(cfg.get("output_dim", 1))

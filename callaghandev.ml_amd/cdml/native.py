@@ -91,6 +91,8 @@ SIGNATURES = {
     "cdml_layernorm_backward": [_vp] * 10 + [_i, _i, _f, _i, _vp, _sz, _vp],
     "cdml_cross_entropy_workspace_size": [_i, C.POINTER(_sz)],
     "cdml_cross_entropy": [_vp, _i, _vp, _i, _i, _i, _f, _f, _vp, _vp, _i, _vp, _sz, _vp],
+    "cdml_mse_loss": [_vp, _i, _vp, _i, _i, _i, _i, _f, _f, _vp, _vp, _i, _vp, _sz, _vp],
+    "cdml_add_inplace": [_vp, _vp, _sz, _vp],
     "cdml_embedding_grad": [_vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _i, _vp],
     "cdml_grad_norm_workspace_size": [_i, C.POINTER(_sz)],
     "cdml_grad_norm": [_vp, _i, _f, _i, _f, _vp, _vp, _sz, _vp],

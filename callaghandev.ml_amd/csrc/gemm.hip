@@ -63,6 +63,7 @@ struct GemmArgs {
   // output tiles of all problems (total = tiles * ksplit).
   int ksplit, kchunk, tiles;
   float *ws, *wsb;
+  int small;  // split-K by wgrad_small_kernel (kchunk counts rows, not k-tiles)
   // Single-problem epilogue options (store_elem): pre receives the
   // pre-activation acc + bias (forward layers whose backward needs it); dz
   // multiplies the result by act'(dz) with act = dact (the hidden deltas of
@@ -679,14 +680,90 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs args)
 // too few tiles, at least eight k-tiles (128 rows) per chunk.
 struct SplitPlan {
   int ksplit = 1, kchunk = 0;
-  size_t bytes = 0;  // workspace: ksplit * nprob * (M * N + M) floats
+  bool small = false;  // small output: wgrad_small_kernel, kchunk in rows
+  size_t bytes = 0;    // workspace: ksplit * nprob * (M * N + M) floats
 };
+
+// Weight gradients whose output is too small or too oddly shaped for the
+// tiled kernel (an input projection [D, 5], a regression head [1, D]) but
+// whose row reduction is long: block c sums rows [c * kchunk, (c + 1) *
+// kchunk) of opA^T opB (opA stored [K, M], opB [K, N]) and of opA's row
+// sums into its own partial; wgrad_small_reduce_kernel adds the partials in
+// block order.  Each thread owns up to kSmallPer outputs.
+constexpr int kSmallPer = 16;
+constexpr int kSmallOut = 256 * kSmallPer;
+
+__global__ void __launch_bounds__(256) wgrad_small_kernel(const GemmArgs args) {
+  const int chunk = blockIdx.x, prob = blockIdx.y, t = threadIdx.x;
+  const GemmProblem P = args.p[prob];
+  const int M = args.M, N = args.N, MN = M * N;
+  const int k0 = chunk * args.kchunk, k1 = min(args.K, k0 + args.kchunk);
+  float acc[kSmallPer], bacc[kSmallPer];
+  int am[kSmallPer], bn[kSmallPer];
+#pragma unroll
+  for (int i = 0; i < kSmallPer; ++i) {
+    const int e = min(t + 256 * i, MN - 1);
+    am[i] = e / N;
+    bn[i] = e % N;
+    acc[i] = bacc[i] = 0.f;
+  }
+  const bool bsum = P.bgrad != nullptr;
+  for (int k = k0; k < k1; ++k) {
+    const float *ar = P.a + (size_t)k * args.lda;
+    const float *br = P.w + (size_t)k * args.ldb;
+#pragma unroll
+    for (int i = 0; i < kSmallPer; ++i)
+      if (t + 256 * i < MN) acc[i] += ar[am[i]] * br[bn[i]];
+    if (bsum) {
+#pragma unroll
+      for (int i = 0; i < kSmallPer; ++i)
+        if (t + 256 * i < M) bacc[i] += ar[t + 256 * i];
+    }
+  }
+  float *out = args.ws + ((size_t)chunk * args.nprob + prob) * MN;
+#pragma unroll
+  for (int i = 0; i < kSmallPer; ++i)
+    if (t + 256 * i < MN) out[t + 256 * i] = acc[i];
+  if (bsum) {
+    float *ob = args.wsb + ((size_t)chunk * args.nprob + prob) * M;
+#pragma unroll
+    for (int i = 0; i < kSmallPer; ++i)
+      if (t + 256 * i < M) ob[t + 256 * i] = bacc[i];
+  }
+}
+
+__global__ void __launch_bounds__(256) wgrad_small_reduce_kernel(const GemmArgs args) {
+  const int prob = blockIdx.y;
+  const GemmProblem P = args.p[prob];
+  const int M = args.M, N = args.N, MN = M * N;
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e < MN) {
+    float s = 0.f;
+    for (int c = 0; c < args.ksplit; ++c) s += args.ws[((size_t)c * args.nprob + prob) * MN + e];
+    float *dst = P.c + (size_t)(e / N) * args.ldc + e % N;
+    *dst = args.beta ? *dst + s : s;
+  }
+  if (P.bgrad && e < M) {
+    float s = 0.f;
+    for (int c = 0; c < args.ksplit; ++c) s += args.wsb[((size_t)c * args.nprob + prob) * M + e];
+    P.bgrad[e] += s;
+  }
+}
 
 SplitPlan splitk_plan(int M, int N, int K, int nprob) {
   SplitPlan sp;
   const int nk = K / 16;  // whole k-tiles; a ragged tail is added by a separate launch
   sp.kchunk = nk;
-  if (M <= 0 || N <= 0 || nk < 1 || N % 4) return sp;
+  if (M <= 0 || N <= 0) return sp;
+  if (nk < 1 || N % 4 || M % 4) {  // not the tiled kernel's shape
+    if ((long long)M * N > kSmallOut || K < 2048) return sp;
+    sp.small = true;
+    sp.ksplit = std::min(256, K / 512);
+    sp.kchunk = (K + sp.ksplit - 1) / sp.ksplit;
+    sp.ksplit = (K + sp.kchunk - 1) / sp.kchunk;
+    sp.bytes = (size_t)sp.ksplit * nprob * ((size_t)M * N + M) * sizeof(float);
+    return sp;
+  }
   const bool big = M >= 1024;
   const int TM = big ? 256 : 128, TN = 128;
   const int tiles = ((M + TM - 1) / TM) * ((N + TN - 1) / TN) * nprob;
@@ -776,6 +853,12 @@ int launch_gemm(GemmArgs &g, bool ta, bool tb, hipStream_t stream, const char *w
     bool split_tail = tb && ktail != 0 && g.K >= 16 && !g.dz && !g.add && !g.pre && g.act == CDML_ACT_NONE;
     for (int i = 0; split_tail && i < g.nprob; ++i)
       split_tail = stage_ok(g.p[i].a, g.M, g.lda, ta, 16) && stage_ok(g.p[i].w, g.N, g.ldb, tb, 16);
+    if (ta && tb && g.small && g.ksplit > 1) {  // small output, long reduction
+      wgrad_small_kernel<<<dim3(g.ksplit, g.nprob), dim3(256), 0, stream>>>(g);
+      const int n = std::max(g.M * g.N, g.M);
+      wgrad_small_reduce_kernel<<<dim3((n + 255) / 256, g.nprob), dim3(256), 0, stream>>>(g);
+      return check_launch(what);
+    }
     if (ta && tb) rc = launch_layout<true, true>(g, fast || split_tail, stream);
     else if (tb) rc = launch_layout<false, true>(g, fast || split_tail, stream);
     else rc = launch_layout<true, false>(g, false, stream);
@@ -826,6 +909,7 @@ int attach_split(GemmArgs &g, void *workspace, size_t workspace_bytes, const cha
   if (!aligned16(workspace)) return fail(CDML_E_INVALID, "%s: workspace must be 16-byte aligned", what);
   g.ksplit = sp.ksplit;
   g.kchunk = sp.kchunk;
+  g.small = sp.small ? 1 : 0;
   g.ws = static_cast<float *>(workspace);
   g.wsb = g.ws + (size_t)sp.ksplit * g.nprob * g.M * g.N;
   return CDML_OK;

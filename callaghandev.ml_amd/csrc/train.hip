@@ -4,6 +4,7 @@
 // and gradient, the token-embedding gradient, and the global-norm clipping
 // and SGD update over every parameter.  All reductions run in a fixed order
 // (no atomics), so a step gives the same bits on every run.
+#include <algorithm>
 #include <cmath>
 
 #include "common.h"
@@ -154,22 +155,37 @@ __global__ void __launch_bounds__(256) ln_backward_kernel(
   }
 }
 
-// dGamma / dBeta: the row-block partials summed in block order; written, or
-// added to the caller's accumulators (the trainer's VectorAccumulate).
-__global__ void __launch_bounds__(256) ln_param_grad_kernel(const float *__restrict__ part_g,
-                                                            const float *__restrict__ part_b,
-                                                            float *__restrict__ dgamma,
-                                                            float *__restrict__ dbeta, int nblk,
-                                                            int f, int accumulate) {
-  const int j = blockIdx.x * 256 + threadIdx.x;
-  if (j >= f) return;
+// dGamma / dBeta: the row-block partials summed in a fixed order -- 64
+// columns per workgroup, wave w of 16 taking blocks w, w + 16, ..., the 16
+// wave sums then added in wave order -- and written, or added to the
+// caller's accumulators (the trainer's VectorAccumulate).
+__global__ void __launch_bounds__(1024) ln_param_grad_kernel(const float *__restrict__ part_g,
+                                                             const float *__restrict__ part_b,
+                                                             float *__restrict__ dgamma,
+                                                             float *__restrict__ dbeta, int nblk,
+                                                             int f, int accumulate) {
+  __shared__ float rg[16][64], rb[16][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = blockIdx.x * 64 + lane;
   float sg = 0.f, sb = 0.f;
-  for (int k = 0; k < nblk; ++k) {
-    sg += part_g[(size_t)k * f + j];
-    sb += part_b[(size_t)k * f + j];
+  if (j < f)
+    for (int k = wave; k < nblk; k += 16) {
+      sg += part_g[(size_t)k * f + j];
+      sb += part_b[(size_t)k * f + j];
+    }
+  rg[wave][lane] = sg;
+  rb[wave][lane] = sb;
+  __syncthreads();
+  if (wave == 0 && j < f) {
+    float g = 0.f, b = 0.f;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+      g += rg[w][lane];
+      b += rb[w][lane];
+    }
+    if (dgamma) dgamma[j] = accumulate ? dgamma[j] + g : g;
+    if (dbeta) dbeta[j] = accumulate ? dbeta[j] + b : b;
   }
-  if (dgamma) dgamma[j] = accumulate ? dgamma[j] + sg : sg;
-  if (dbeta) dbeta[j] = accumulate ? dbeta[j] + sb : sb;
 }
 
 // CrossEntropyLossAndGradient (AccelerationCPU.cs:2377-2440): one workgroup per
@@ -223,9 +239,45 @@ __global__ void __launch_bounds__(256) ce_row_kernel(const float *__restrict__ l
   }
 }
 
-// loss = sum of the row terms (fixed order) / effective_len, times loss_scale.
+// MSELossAndGradient (AccelerationCPU.cs:2447-2490): one thread per row; rows
+// below effective_len get d = 2 * diff / (effective_len * out_dim) (times
+// grad_scale) and their sum of diff^2 as the row term; later rows get 0.
+__global__ void __launch_bounds__(256) mse_row_kernel(const float *__restrict__ pred, int ldp,
+                                                      const float *__restrict__ targets, int ldt,
+                                                      int rows, int o, int effective_len,
+                                                      float grad_scale, float *__restrict__ d,
+                                                      int ldd, float *__restrict__ row_loss) {
+#pragma clang fp contract(off)
+  const int row = blockIdx.x * 256 + threadIdx.x;
+  if (row >= rows) return;
+  float *dr = d + (size_t)row * ldd;
+  if (row >= effective_len) {
+    for (int j = 0; j < o; ++j) dr[j] = 0.f;
+    return;
+  }
+  const float inv_len = 1.0f / (float)(effective_len * o);
+  const float *pr = pred + (size_t)row * ldp, *tr = targets + (size_t)row * ldt;
+  float s = 0.f;
+  for (int j = 0; j < o; ++j) {
+    const float diff = pr[j] - tr[j];
+    s += diff * diff;
+    dr[j] = (2.0f * diff * inv_len) * grad_scale;
+  }
+  row_loss[row] = s;
+}
+
+// target[i] += addend[i] (MatrixAddInPlace, AccelerationCPU.cs:522-546).
+__global__ void __launch_bounds__(256) add_inplace_kernel(float *__restrict__ target,
+                                                          const float *__restrict__ addend,
+                                                          long long n) {
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256)
+    target[i] += addend[i];
+}
+
+// loss = (sum of the row terms, fixed order) / divisor, times loss_scale.
 __global__ void __launch_bounds__(256) ce_loss_kernel(const float *__restrict__ row_loss, int n,
-                                                      float loss_scale, float *__restrict__ loss) {
+                                                      float divisor, float loss_scale,
+                                                      float *__restrict__ loss) {
   __shared__ float red[256];
   float s = 0.f;
   for (int i = threadIdx.x; i < n; i += 256) s += row_loss[i];
@@ -235,7 +287,7 @@ __global__ void __launch_bounds__(256) ce_loss_kernel(const float *__restrict__ 
     if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
     __syncthreads();
   }
-  if (threadIdx.x == 0) *loss = (red[0] / (float)n) * loss_scale;
+  if (threadIdx.x == 0) *loss = (red[0] / divisor) * loss_scale;
 }
 
 // AccumulateTokenEmbeddingGrad (AccelerationCPU.cs:2339-2370) as a gather: group
@@ -439,8 +491,8 @@ extern "C" int cdml_layernorm_backward(const float *dout, const float *dout2,
     if (rc) return rc;
   }
   if (dgamma || dbeta) {
-    ln_param_grad_kernel<<<dim3((features + 255) / 256), dim3(256), 0, st>>>(pg, pb, dgamma, dbeta, nblk,
-                                                                             features, accumulate);
+    ln_param_grad_kernel<<<dim3((features + 63) / 64), dim3(1024), 0, st>>>(pg, pb, dgamma, dbeta, nblk,
+                                                                            features, accumulate);
     rc = check_launch("ln_param_grad_kernel");
   }
   return rc;
@@ -475,8 +527,48 @@ extern "C" int cdml_cross_entropy(const float *logits, int ldl, const int *targe
     if (rc) return rc;
   }
   if (effective_len == 0) return cdml_zero_f32_async(loss, 1, stream);
-  ce_loss_kernel<<<dim3(1), dim3(256), 0, st>>>(row_loss, effective_len, loss_scale, loss);
+  ce_loss_kernel<<<dim3(1), dim3(256), 0, st>>>(row_loss, effective_len, (float)effective_len, loss_scale,
+                                                 loss);
   return check_launch("ce_loss_kernel");
+}
+
+extern "C" int cdml_mse_loss(const float *pred, int ldp, const float *targets, int ldt, int rows,
+                             int out_dim, int effective_len, float grad_scale, float loss_scale,
+                             float *loss, float *dout, int ldd, void *workspace,
+                             size_t workspace_bytes, cdml_stream stream) {
+  if (rows < 0 || out_dim <= 0 || effective_len < 0 || effective_len > rows)
+    return fail(CDML_E_INVALID, "cdml_mse_loss: bad size");
+  if (ldp < out_dim || ldt < out_dim || ldd < out_dim)
+    return fail(CDML_E_INVALID, "cdml_mse_loss: row stride smaller than the row");
+  if (!pred || !dout || !loss || (effective_len > 0 && !targets))
+    return fail(CDML_E_INVALID, "cdml_mse_loss: NULL pointer");
+  if (!workspace || workspace_bytes < (size_t)(rows > 0 ? rows : 1) * sizeof(float))
+    return fail(CDML_E_INVALID, "cdml_mse_loss: workspace too small");
+  int rc = ensure_device();
+  if (rc) return rc;
+  hipStream_t st = as_hip(stream);
+  float *row_loss = static_cast<float *>(workspace);
+  if (rows > 0) {
+    mse_row_kernel<<<dim3((rows + 255) / 256), dim3(256), 0, st>>>(pred, ldp, targets, ldt, rows, out_dim,
+                                                                  effective_len, grad_scale, dout, ldd,
+                                                                  row_loss);
+    rc = check_launch("mse_row_kernel");
+    if (rc) return rc;
+  }
+  if (effective_len == 0) return cdml_zero_f32_async(loss, 1, stream);
+  ce_loss_kernel<<<dim3(1), dim3(256), 0, st>>>(row_loss, effective_len, (float)(effective_len * out_dim),
+                                                 loss_scale, loss);
+  return check_launch("ce_loss_kernel");
+}
+
+extern "C" int cdml_add_inplace(float *target, const float *addend, size_t count, cdml_stream stream) {
+  if (count == 0) return CDML_OK;
+  if (!target || !addend) return fail(CDML_E_INVALID, "cdml_add_inplace: NULL pointer");
+  int rc = ensure_device();
+  if (rc) return rc;
+  const size_t blocks = std::min<size_t>((count + 255) / 256, 8192);
+  add_inplace_kernel<<<dim3((unsigned)blocks), dim3(256), 0, as_hip(stream)>>>(target, addend, (long long)count);
+  return check_launch("add_inplace_kernel");
 }
 
 extern "C" int cdml_embedding_grad(float *grad, const float *dx, const float *dx2, int ldx,

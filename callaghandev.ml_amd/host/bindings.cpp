@@ -524,6 +524,28 @@ PYBIND11_MODULE(_cdml_host, m) {
              return t.Train(b, seed);
            },
            py::arg("sequences"), py::arg("seed") = 0)
+      .def("TrainBatchContinuous",
+           [](DeviceTrainer &t, py::object inputs, py::object reg, py::object cls, float lr) {
+             std::vector<Matrix> xs, rs;
+             std::vector<std::vector<int>> cs;
+             auto mats = [](py::object o, std::vector<Matrix> &out) {
+               for (py::handle h : o) {
+                 py::object ob = py::reinterpret_borrow<py::object>(h);
+                 out.push_back(ob.is_none() ? Matrix() : from_numpy(ob));
+               }
+             };
+             mats(inputs, xs);
+             if (!reg.is_none()) mats(reg, rs);
+             if (!cls.is_none())
+               for (py::handle h : cls) {
+                 py::object ob = py::reinterpret_borrow<py::object>(h);
+                 cs.push_back(ob.is_none() ? std::vector<int>() : ids_from(ob));
+               }
+             py::gil_scoped_release nogil;
+             return t.TrainBatchContinuous(xs, rs, cs, lr);
+           },
+           py::arg("inputs"), py::arg("regressionTargets") = py::none(), py::arg("classTargets") = py::none(),
+           py::arg("learningRate") = 1e-4f)
       .def("CopyWeightsTo", &DeviceTrainer::CopyWeightsTo, py::arg("model"))
       .def("weights", [flat_dict](DeviceTrainer &t) { return flat_dict(t, t.weights_flat()); })
       .def("gradients", [flat_dict](DeviceTrainer &t) { return flat_dict(t, t.gradients_flat()); })
@@ -545,7 +567,26 @@ PYBIND11_MODULE(_cdml_host, m) {
              const auto t1 = std::chrono::steady_clock::now();
              return std::chrono::duration<double, std::milli>(t1 - t0).count() / std::max(steps, 1);
            },
-           py::arg("tokens"), py::arg("learningRate"), py::arg("steps") = 5, py::arg("warmup") = 2);
+           py::arg("tokens"), py::arg("learningRate"), py::arg("steps") = 5, py::arg("warmup") = 2)
+      .def("time_step_continuous",
+           // time_step for a regression model: inputs [batch, seqLen + 1, F],
+           // targets [batch, seqLen + 1, OutputDim]
+           [](DeviceTrainer &t, py::object inputs, py::object targets, float lr, int steps, int warmup) {
+             F32 x = F32::ensure(inputs), y = F32::ensure(targets);
+             if (!x || !y || x.ndim() != 3 || y.ndim() != 3 || x.shape(0) != y.shape(0) || x.shape(1) != y.shape(1))
+               throw ArgumentException("inputs [batch, T, F] and targets [batch, T, O] expected", "inputs");
+             py::gil_scoped_release nogil;
+             t.load_batch_continuous(x.data(), y.data(), (int)x.shape(0), (int)x.shape(1));
+             for (int i = 0; i < warmup; ++i) t.step_loaded(lr);
+             t.synchronize();
+             const auto t0 = std::chrono::steady_clock::now();
+             for (int i = 0; i < steps; ++i) t.step_loaded(lr);
+             t.synchronize();
+             const auto t1 = std::chrono::steady_clock::now();
+             return std::chrono::duration<double, std::milli>(t1 - t0).count() / std::max(steps, 1);
+           },
+           py::arg("inputs"), py::arg("targets"), py::arg("learningRate"), py::arg("steps") = 5,
+           py::arg("warmup") = 2);
 
   py::class_<DeviceLanguageModel>(m, "DeviceLanguageModel")
       .def(py::init<const LanguageModel &, int, int>(), py::arg("model"), py::arg("batch_capacity"),

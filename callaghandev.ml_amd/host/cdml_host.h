@@ -475,6 +475,15 @@ class DeviceTrainer {
   // `seed`; the reference's System.Random is not reproduced) with the
   // configured learning-rate decay; returns the last epoch's average loss.
   float Train(const std::vector<std::vector<int>> &sequences, uint64_t seed = 0);
+  // Continuous inputs (TrainBatchContinuous, :337-485): windows [T_i,
+  // InputFeatureDim]; with DataType TimeSeriesRegression (1) the targets are
+  // regTargets[i] [>= T_i, OutputDim] (MSE), with TimeSeriesClassification
+  // (2) class ids classTargets[i] (>= T_i); row t predicts step t + 1.
+  float TrainBatchContinuous(const std::vector<Matrix> &inputs, const std::vector<Matrix> &regTargets,
+                             const std::vector<std::vector<int>> &classTargets, float learningRate);
+  // TrainContinuous (:130-207): epochs of shuffled batches.
+  float TrainContinuous(const std::vector<Matrix> &inputs, const std::vector<Matrix> &regTargets,
+                        const std::vector<std::vector<int>> &classTargets, uint64_t seed = 0);
   // Writes the device weights into the model's host arrays.
   void CopyWeightsTo(LanguageModel &model);
   // Current weights / the last step's gradients (after its 1/validCount and
@@ -491,6 +500,9 @@ class DeviceTrainer {
   // (zero, forward, loss, backward, norm, update) with no read-back.
   void load_batch(const int *host_tokens, int batch, int seqLenPlus1);
   void step_loaded(float learningRate);
+  // load_batch for a regression model: inputs [batch, seqLenPlus1,
+  // InputFeatureDim] and targets [batch, seqLenPlus1, OutputDim].
+  void load_batch_continuous(const float *host_inputs, const float *host_targets, int batch, int seqLenPlus1);
   void synchronize();
 
  private:
@@ -509,6 +521,9 @@ class DeviceTrainer {
   void bucket_forward(int batch, int seqLen, float grad_scale, float *loss_dev);
   void bucket_backward(int batch, int seqLen);
   void upload_bucket(const std::vector<const std::vector<int> *> &seqs, int seqLen);
+  void upload_bucket_continuous(const std::vector<Matrix> &inputs, const std::vector<Matrix> &regTargets,
+                                const std::vector<std::vector<int>> &classTargets, const std::vector<int> &idx,
+                                int seqLen);
   void update(int validCount, float learningRate);
 
   TransformerConfig cfg_;
@@ -522,7 +537,10 @@ class DeviceTrainer {
   std::vector<std::pair<size_t, size_t>> offs_;
   void *param_table_ = nullptr;
   int param_count_ = 0;
-  float *emb_, *outproj_, *outbias_, *gemb_, *goutproj_, *goutbias_;
+  // emb_ / gemb_: the token embedding, or the input projection of a
+  // continuous model (with inbias_ / ginbias_)
+  float *emb_ = nullptr, *outproj_ = nullptr, *outbias_ = nullptr, *gemb_ = nullptr, *goutproj_ = nullptr,
+        *goutbias_ = nullptr, *inbias_ = nullptr, *ginbias_ = nullptr, *inputs_ = nullptr, *regt_ = nullptr;
   std::vector<Layer> layers_;
   float *xfinal_, *logits_, *dx_, *dxa_, *dr1_, *dr2_, *dn1_, *dcat_, *dq_, *dk_, *dv_, *tmp_;
   std::vector<float *> dh_;  // FFN hidden gradients

@@ -39,8 +39,6 @@ DeviceTrainer::DeviceTrainer(const LanguageModel &model, const TrainingConfig &c
                              int batch_capacity, int seq_capacity, int device)
     : cfg_(model.config()), tc_(config), cap_b_(batch_capacity), cap_s_(seq_capacity),
       device_(device) {
-  if (!cfg_.UsesDiscreteTokens)
-    throw InvalidOperationException("DeviceTrainer trains token models; continuous inputs use TrainContinuous.");
   if (batch_capacity <= 0) throw ArgumentOutOfRangeException("batch_capacity");
   if (seq_capacity <= 0 || seq_capacity > cfg_.MaxSequenceLength)
     throw ArgumentOutOfRangeException("seq_capacity");
@@ -49,7 +47,9 @@ DeviceTrainer::DeviceTrainer(const LanguageModel &model, const TrainingConfig &c
   check(cdml_init(device), "cdml_init");
   check(cdml_stream_create(&stream_), "cdml_stream_create");
   try {
-    const int D = cfg_.EmbeddingDim, H = cfg_.NumHeads, V = cfg_.VocabSize, hd = D / H;
+    const int D = cfg_.EmbeddingDim, H = cfg_.NumHeads, V = cfg_.EffectiveOutputDim(), hd = D / H;
+    const int F = cfg_.InputFeatureDim;
+    const bool discrete = cfg_.UsesDiscreteTokens;
     // ---- parameter layout: one buffer for the weights, one for the gradients
     struct Spec {
       std::string name;
@@ -57,7 +57,12 @@ DeviceTrainer::DeviceTrainer(const LanguageModel &model, const TrainingConfig &c
       size_t count;
     };
     std::vector<Spec> specs;
-    specs.push_back({"token_embedding", model.TokenEmbedding.ptr(), model.TokenEmbedding.data.size()});
+    if (discrete) {
+      specs.push_back({"token_embedding", model.TokenEmbedding.ptr(), model.TokenEmbedding.data.size()});
+    } else {
+      specs.push_back({"input_proj", model.InputProjection.ptr(), model.InputProjection.data.size()});
+      specs.push_back({"input_bias", model.InputProjectionBias.data(), model.InputProjectionBias.size()});
+    }
     specs.push_back({"out_proj", model.OutputProjection.ptr(), model.OutputProjection.data.size()});
     specs.push_back({"out_bias", model.OutputBias.data(), model.OutputBias.size()});
     for (size_t l = 0; l < model.Blocks.size(); ++l) {
@@ -99,10 +104,17 @@ DeviceTrainer::DeviceTrainer(const LanguageModel &model, const TrainingConfig &c
             "cdml_memcpy_h2d_async");
     auto W = [&](const std::string &n) { return params_ + offs_[at.at(n)].first; };
     auto G = [&](const std::string &n) { return grads_ + offs_[at.at(n)].first; };
-    emb_ = W("token_embedding");
+    if (discrete) {
+      emb_ = W("token_embedding");
+      gemb_ = G("token_embedding");
+    } else {
+      emb_ = W("input_proj");
+      inbias_ = W("input_bias");
+      gemb_ = G("input_proj");
+      ginbias_ = G("input_bias");
+    }
     outproj_ = W("out_proj");
     outbias_ = W("out_bias");
-    gemb_ = G("token_embedding");
     goutproj_ = G("out_proj");
     goutbias_ = G("out_bias");
 
@@ -115,7 +127,12 @@ DeviceTrainer::DeviceTrainer(const LanguageModel &model, const TrainingConfig &c
       table.push_back(cdml_param{params_ + offs_[i].first, grads_ + offs_[i].first,
                                  (long long)offs_[i].second, grp, 0});
     };
-    add("token_embedding", group++);
+    if (discrete) {
+      add("token_embedding", group++);
+    } else {  // InputProjectionGrad and its bias, two terms (:1327-1328)
+      add("input_proj", group++);
+      add("input_bias", group++);
+    }
     add("out_proj", group++);
     add("out_bias", group++);
     const int L = (int)model.Blocks.size();
@@ -203,6 +220,10 @@ DeviceTrainer::DeviceTrainer(const LanguageModel &model, const TrainingConfig &c
     for (float **p : {&dx_, &dxa_, &dr1_, &dr2_, &dn1_, &dcat_, &dq_, &dk_, &dv_, &tmp_}) *p = alloc(rows * D);
     dh_.push_back(alloc(rows * ffmax));
     dh_.push_back(alloc(rows * ffmax));
+    if (!discrete) {
+      inputs_ = alloc(rows * F);
+      regt_ = alloc(rows * (size_t)V);
+    }
     ids_ = reinterpret_cast<int *>(alloc(rows));
     targets_ = reinterpret_cast<int *>(alloc(rows));
     order_ = reinterpret_cast<int *>(alloc(rows));
@@ -221,6 +242,10 @@ DeviceTrainer::DeviceTrainer(const LanguageModel &model, const TrainingConfig &c
     need = std::max(need, n);
     check(cdml_linear_backward_workspace_size(R, D, V, &n), "workspace size");
     need = std::max(need, n);
+    if (!discrete) {
+      check(cdml_linear_backward_workspace_size(R, F, D, &n), "workspace size");
+      need = std::max(need, n);
+    }
     for (const Layer &Y : layers_)
       for (size_t i = 0; i < Y.ffrows.size(); ++i) {
         check(cdml_linear_backward_workspace_size(R, Y.ffcols[i], Y.ffrows[i], &n), "workspace size");
@@ -288,14 +313,18 @@ void DeviceTrainer::upload_bucket(const std::vector<const std::vector<int> *> &s
 // Forward with cache and the loss gradient of one bucket of `batch`
 // sequences of seqLen inputs (the loss lands in loss_dev).
 void DeviceTrainer::bucket_forward(int batch, int seqLen, float grad_scale, float *loss_dev) {
-  const int D = cfg_.EmbeddingDim, H = cfg_.NumHeads, V = cfg_.VocabSize, hd = D / H;
+  const int D = cfg_.EmbeddingDim, H = cfg_.NumHeads, V = cfg_.EffectiveOutputDim(), hd = D / H;
+  const int F = cfg_.InputFeatureDim;
   const int rows = batch * seqLen;
   const float scale = 1.0f / std::sqrt((float)hd);  // TransformerTrainer.cs:947
   cdml_stream s = stream_;
   const float eps = 1e-5f;
   // ---- forward (ForwardFromEmbeddingWithCache, :540-590)
-  check(cdml_embed_tokens(ids_, rows, emb_, V, D, layers_.empty() ? xfinal_ : layers_[0].x, nullptr, s),
-        "cdml_embed_tokens");
+  float *x0 = layers_.empty() ? xfinal_ : layers_[0].x;
+  if (cfg_.UsesDiscreteTokens)
+    check(cdml_embed_tokens(ids_, rows, emb_, cfg_.VocabSize, D, x0, nullptr, s), "cdml_embed_tokens");
+  else  // BatchDotProductAddBias(InputProjection, input, bias) (:528, :647)
+    check(cdml_linear(inputs_, F, emb_, inbias_, x0, D, rows, F, D, CDML_ACT_NONE, s), "cdml_linear");
   for (size_t l = 0; l < layers_.size(); ++l) {
     Layer &Y = layers_[l];
     float *next = l + 1 < layers_.size() ? layers_[l + 1].x : xfinal_;
@@ -327,16 +356,22 @@ void DeviceTrainer::bucket_forward(int batch, int seqLen, float grad_scale, floa
           "cdml_residual_layernorm_fwd");
   }
   check(cdml_linear(xfinal_, D, outproj_, outbias_, logits_, V, rows, D, V, CDML_ACT_NONE, s), "cdml_linear");
-  // ---- loss and its gradient, in place over the logits
-  check(cdml_cross_entropy(logits_, V, targets_, rows, V, rows, grad_scale, 1.0f, loss_dev, logits_, V, ws_,
-                           ws_bytes_, s),
-        "cdml_cross_entropy");
+  // ---- loss and its gradient, in place over the logits (:270-285, :409-438)
+  if (cfg_.UsesDiscreteTokens || cfg_.DataType != 1)
+    check(cdml_cross_entropy(logits_, V, targets_, rows, V, rows, grad_scale, 1.0f, loss_dev, logits_, V, ws_,
+                             ws_bytes_, s),
+          "cdml_cross_entropy");
+  else
+    check(cdml_mse_loss(logits_, V, regt_, V, rows, V, rows, grad_scale, 1.0f, loss_dev, logits_, V, ws_, ws_bytes_,
+                        s),
+          "cdml_mse_loss");
 }
 
 // Backward of the bucket bucket_forward left in the cache; gradients
 // accumulate into grads_.
 void DeviceTrainer::bucket_backward(int batch, int seqLen) {
-  const int D = cfg_.EmbeddingDim, H = cfg_.NumHeads, V = cfg_.VocabSize, hd = D / H;
+  const int D = cfg_.EmbeddingDim, H = cfg_.NumHeads, V = cfg_.EffectiveOutputDim(), hd = D / H;
+  const int F = cfg_.InputFeatureDim;
   const int rows = batch * seqLen;
   const float scale = 1.0f / std::sqrt((float)hd);
   cdml_stream s = stream_;
@@ -389,8 +424,16 @@ void DeviceTrainer::bucket_backward(int batch, int seqLen) {
     ga = dxa_;  // dX = dX_attn + dAttnResidual (:919)
     gb = dr1_;
   }
-  // BackpropInput (:887-896): the embedding rows of the bucket's tokens
-  check(cdml_embedding_grad(gemb_, ga, gb, D, order_, gstart_, gtoken_, ngroups_, D, s), "cdml_embedding_grad");
+  // BackpropInput (:887-896): the embedding rows of the bucket's tokens, or
+  // the input projection (BackpropInputProjection, AccelerationCPU.cs:2280-2332)
+  if (cfg_.UsesDiscreteTokens) {
+    check(cdml_embedding_grad(gemb_, ga, gb, D, order_, gstart_, gtoken_, ngroups_, D, s), "cdml_embedding_grad");
+  } else {
+    if (gb) check(cdml_add_inplace(const_cast<float *>(ga), gb, (size_t)rows * D, s), "cdml_add_inplace");
+    check(cdml_linear_backward(inputs_, F, ga, D, emb_, nullptr, F, gemb_, ginbias_, rows, F, D, 0, ws_, ws_bytes_,
+                               s),
+          "cdml_linear_backward");
+  }
 }
 
 void DeviceTrainer::update(int validCount, float learningRate) {
@@ -404,7 +447,141 @@ void DeviceTrainer::update(int validCount, float learningRate) {
         "cdml_sgd_update");
 }
 
+// Inputs and targets of one continuous bucket: window rows [0, S) are the
+// inputs, rows [1, S] the targets (BuildContinuousRegressionFlatTargets /
+// BuildContinuousClassFlatTargets, TransformerTrainer.cs:676-708).
+void DeviceTrainer::upload_bucket_continuous(const std::vector<Matrix> &inputs,
+                                             const std::vector<Matrix> &regTargets,
+                                             const std::vector<std::vector<int>> &classTargets,
+                                             const std::vector<int> &idx, int seqLen) {
+  const int F = cfg_.InputFeatureDim, O = cfg_.EffectiveOutputDim();
+  const int B = (int)idx.size(), rows = B * seqLen;
+  std::vector<float> x((size_t)rows * F);
+  for (int b = 0; b < B; ++b)
+    std::memcpy(x.data() + (size_t)b * seqLen * F, inputs[idx[b]].ptr(), (size_t)seqLen * F * sizeof(float));
+  check(cdml_memcpy_h2d_async(inputs_, x.data(), x.size() * sizeof(float), stream_), "upload inputs");
+  std::vector<float> rt;
+  std::vector<int> ct;
+  if (cfg_.DataType == 1) {
+    rt.resize((size_t)rows * O);
+    for (int b = 0; b < B; ++b)
+      std::memcpy(rt.data() + (size_t)b * seqLen * O, regTargets[idx[b]].ptr() + O, (size_t)seqLen * O * sizeof(float));
+    check(cdml_memcpy_h2d_async(regt_, rt.data(), rt.size() * sizeof(float), stream_), "upload targets");
+  } else {
+    ct.resize(rows);
+    for (int b = 0; b < B; ++b)
+      for (int t = 0; t < seqLen; ++t) ct[b * seqLen + t] = classTargets[idx[b]][t + 1];
+    check(cdml_memcpy_h2d_async(targets_, ct.data(), ct.size() * sizeof(int), stream_), "upload targets");
+  }
+  synchronize();  // the host vectors must outlive the copies
+}
+
+float DeviceTrainer::TrainBatchContinuous(const std::vector<Matrix> &inputs, const std::vector<Matrix> &regTargets,
+                                          const std::vector<std::vector<int>> &classTargets, float learningRate) {
+  if (cfg_.UsesDiscreteTokens) throw InvalidOperationException("Use TrainBatch for token models.");
+  const bool regression = cfg_.DataType == 1;
+  const int F = cfg_.InputFeatureDim, O = cfg_.EffectiveOutputDim();
+  std::vector<int> lens;
+  std::unordered_map<int, std::vector<int>> buckets;
+  for (size_t i = 0; i < inputs.size(); ++i) {  // the skips of :353-377 and :1480-1502
+    const Matrix &x = inputs[i];
+    const int T = x.rows;
+    if (T < 2 || x.cols != F) continue;
+    bool ok = std::all_of(x.data.begin(), x.data.end(), [](float v) { return std::isfinite(v); });
+    if (regression) {
+      ok = ok && i < regTargets.size() && regTargets[i].rows >= T && regTargets[i].cols == O &&
+           std::all_of(regTargets[i].data.begin(), regTargets[i].data.end(), [](float v) { return std::isfinite(v); });
+    } else {
+      ok = ok && i < classTargets.size() && (int)classTargets[i].size() >= T;
+      for (int t = 1; ok && t < T; ++t) ok = (unsigned)classTargets[i][t] < (unsigned)O;
+    }
+    if (!ok) continue;
+    if (!buckets.count(T - 1)) lens.push_back(T - 1);
+    buckets[T - 1].push_back((int)i);
+  }
+  loaded_b_ = 0;
+  zero_grads();
+  float totalLoss = 0.f;
+  int validCount = 0;
+  for (int inputLen : lens) {
+    const auto &all = buckets[inputLen];
+    if (inputLen > cap_s_) throw ArgumentOutOfRangeException("inputs", "window longer than the trainer's seq_capacity");
+    for (size_t start = 0; start < all.size(); start += cap_b_) {
+      std::vector<int> part(all.begin() + start, all.begin() + std::min(all.size(), start + cap_b_));
+      const int B = (int)part.size();
+      upload_bucket_continuous(inputs, regTargets, classTargets, part, inputLen);
+      bucket_forward(B, inputLen, B > 1 ? (float)B : 1.0f, losses_);
+      float loss = 0.f;
+      check(cdml_memcpy_d2h_async(&loss, losses_, sizeof(float), stream_), "read loss");
+      synchronize();
+      if (!std::isfinite(loss)) continue;
+      bucket_backward(B, inputLen);
+      totalLoss += loss * B;  // :451
+      validCount += B;
+    }
+  }
+  if (validCount == 0) return 0.f;
+  update(validCount, learningRate);
+  float res[3];
+  check(cdml_memcpy_d2h_async(res, result_, sizeof(res), stream_), "read norm");
+  synchronize();
+  last_norm_ = res[0];
+  return totalLoss / validCount;
+}
+
+float DeviceTrainer::TrainContinuous(const std::vector<Matrix> &inputs, const std::vector<Matrix> &regTargets,
+                                     const std::vector<std::vector<int>> &classTargets, uint64_t seed) {
+  if (cfg_.UsesDiscreteTokens) throw InvalidOperationException("Use Train(int[][]) for token models.");
+  if (tc_.BatchSize <= 0) throw ArgumentOutOfRangeException("BatchSize", "BatchSize must be positive.");
+  if (tc_.Epochs < 0) throw ArgumentOutOfRangeException("Epochs", "Epochs must be non-negative.");
+  if (cfg_.DataType == 1 && regTargets.size() != inputs.size())
+    throw ArgumentException("regressionTargets length must match inputs length.", "regressionTargets");
+  if (cfg_.DataType == 2 && classTargets.size() != inputs.size())
+    throw ArgumentException("classTargets length must match inputs length.", "classTargets");
+  std::vector<int> valid;
+  for (size_t i = 0; i < inputs.size(); ++i) {
+    if (inputs[i].rows < 2) continue;
+    if (inputs[i].cols != cfg_.InputFeatureDim)
+      throw ArgumentException("Input sequence " + std::to_string(i) + " has feature dimension " +
+                                  std::to_string(inputs[i].cols) + ", expected " +
+                                  std::to_string(cfg_.InputFeatureDim) + ".",
+                              "inputs");
+    valid.push_back((int)i);
+  }
+  if (valid.empty()) throw ArgumentException("No valid sequences. All must have at least 2 timesteps.", "inputs");
+  float lr = tc_.LearningRate, epochAvg = 0.f;
+  uint64_t state = seed;
+  auto next = [&state]() {  // SplitMix64
+    uint64_t z = (state += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+  };
+  for (int epoch = 0; epoch < tc_.Epochs; ++epoch) {
+    std::vector<int> order = valid;
+    for (size_t i = order.size(); i > 1; --i) std::swap(order[i - 1], order[next() % i]);
+    float epochLoss = 0.f;
+    int numBatches = 0;
+    for (size_t i = 0; i < order.size(); i += tc_.BatchSize) {
+      std::vector<Matrix> bx;
+      std::vector<Matrix> br;
+      std::vector<std::vector<int>> bc;
+      for (size_t j = i; j < std::min(order.size(), i + (size_t)tc_.BatchSize); ++j) {
+        bx.push_back(inputs[order[j]]);
+        if (cfg_.DataType == 1) br.push_back(regTargets[order[j]]);
+        else bc.push_back(classTargets[order[j]]);
+      }
+      epochLoss += TrainBatchContinuous(bx, br, bc, lr);
+      ++numBatches;
+    }
+    epochAvg = numBatches > 0 ? epochLoss / numBatches : 0.f;
+    if (tc_.UseLearningRateDecay) lr *= tc_.LearningRateDecay;
+  }
+  return epochAvg;
+}
+
 float DeviceTrainer::TrainBatch(const std::vector<std::vector<int>> &batch, float learningRate) {
+  if (!cfg_.UsesDiscreteTokens) throw InvalidOperationException("Use TrainBatchContinuous for continuous inputs.");
   // TokensAreValid (:1467-1478) and the length buckets (:224-248), in order of
   // first appearance
   std::vector<int> lens;
@@ -450,6 +627,7 @@ float DeviceTrainer::TrainBatch(const std::vector<std::vector<int>> &batch, floa
 }
 
 void DeviceTrainer::load_batch(const int *host_tokens, int batch, int seqLenPlus1) {
+  if (!cfg_.UsesDiscreteTokens) throw InvalidOperationException("load_batch takes token sequences.");
   if (batch <= 0 || batch > cap_b_ || seqLenPlus1 < 2 || seqLenPlus1 - 1 > cap_s_)
     throw ArgumentOutOfRangeException("batch");
   std::vector<std::vector<int>> seqs(batch);
@@ -463,6 +641,27 @@ void DeviceTrainer::load_batch(const int *host_tokens, int batch, int seqLenPlus
   loaded_s_ = seqLenPlus1 - 1;
 }
 
+void DeviceTrainer::load_batch_continuous(const float *host_inputs, const float *host_targets, int batch,
+                                          int seqLenPlus1) {
+  if (cfg_.UsesDiscreteTokens || cfg_.DataType != 1)
+    throw InvalidOperationException("load_batch_continuous takes regression windows.");
+  if (batch <= 0 || batch > cap_b_ || seqLenPlus1 < 2 || seqLenPlus1 - 1 > cap_s_)
+    throw ArgumentOutOfRangeException("batch");
+  const int F = cfg_.InputFeatureDim, O = cfg_.EffectiveOutputDim();
+  std::vector<Matrix> xs(batch), ts(batch);
+  std::vector<int> idx(batch);
+  for (int b = 0; b < batch; ++b) {
+    xs[b] = Matrix(seqLenPlus1, F);
+    ts[b] = Matrix(seqLenPlus1, O);
+    std::memcpy(xs[b].ptr(), host_inputs + (size_t)b * seqLenPlus1 * F, (size_t)seqLenPlus1 * F * sizeof(float));
+    std::memcpy(ts[b].ptr(), host_targets + (size_t)b * seqLenPlus1 * O, (size_t)seqLenPlus1 * O * sizeof(float));
+    idx[b] = b;
+  }
+  upload_bucket_continuous(xs, ts, {}, idx, seqLenPlus1 - 1);
+  loaded_b_ = batch;
+  loaded_s_ = seqLenPlus1 - 1;
+}
+
 void DeviceTrainer::step_loaded(float learningRate) {
   if (loaded_b_ <= 0) throw InvalidOperationException("load_batch first");
   zero_grads();
@@ -472,6 +671,7 @@ void DeviceTrainer::step_loaded(float learningRate) {
 }
 
 float DeviceTrainer::Train(const std::vector<std::vector<int>> &sequences, uint64_t seed) {
+  if (!cfg_.UsesDiscreteTokens) throw InvalidOperationException("Use TrainContinuous() for continuous inputs.");
   if (tc_.BatchSize <= 0) throw ArgumentOutOfRangeException("BatchSize", "BatchSize must be positive.");
   if (tc_.Epochs < 0) throw ArgumentOutOfRangeException("Epochs", "Epochs must be non-negative.");
   std::vector<const std::vector<int> *> valid;
@@ -527,7 +727,12 @@ void DeviceTrainer::CopyWeightsTo(LanguageModel &model) {
     std::memcpy(dst, w.data() + offs_[i].first, n * sizeof(float));
     ++i;
   };
-  take(model.TokenEmbedding.ptr(), model.TokenEmbedding.data.size());
+  if (cfg_.UsesDiscreteTokens) {
+    take(model.TokenEmbedding.ptr(), model.TokenEmbedding.data.size());
+  } else {
+    take(model.InputProjection.ptr(), model.InputProjection.data.size());
+    take(model.InputProjectionBias.data(), model.InputProjectionBias.size());
+  }
   take(model.OutputProjection.ptr(), model.OutputProjection.data.size());
   take(model.OutputBias.data(), model.OutputBias.size());
   for (TransformerBlock &b : model.Blocks) {

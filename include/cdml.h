@@ -354,6 +354,22 @@ int cdml_cross_entropy(const float *logits, int ldl, const int *targets,
                        float *dlogits, int lddl, void *workspace,
                        size_t workspace_bytes, cdml_stream stream);
 
+/* IAccelerationManager.MSELossAndGradient (:212-214), replacing
+ * AccelerationCPU.cs:2442-2490: rows i < effective_len of pred [rows,
+ * out_dim] against targets rows i (row strides ldp / ldt): dout = 2 (p - t) /
+ * (effective_len * out_dim) * grad_scale, *loss (device) = mean squared
+ * difference times loss_scale; rows past effective_len get 0.  workspace:
+ * rows floats. */
+int cdml_mse_loss(const float *pred, int ldp, const float *targets, int ldt,
+                  int rows, int out_dim, int effective_len, float grad_scale,
+                  float loss_scale, float *loss, float *dout, int ldd,
+                  void *workspace, size_t workspace_bytes, cdml_stream stream);
+
+/* IAccelerationManager.MatrixAddInPlace (:91; AccelerationCPU.cs:
+ * 522-546): target[i] += addend[i] for `count` floats. */
+int cdml_add_inplace(float *target, const float *addend, size_t count,
+                     cdml_stream stream);
+
 /* IAccelerationManager.AccumulateTokenEmbeddingGrad (:203-205), replacing
  * AccelerationCPU.cs:2339-2370, as a gather over groups of rows that share a
  * token: for group k, rows order[group_start[k] .. group_start[k+1]) of

@@ -73,6 +73,8 @@ def lib():
             "ref_squared_norm": (f, [_f32p, C.c_long]),
             "ref_scale_inplace": (None, [_f32p, C.c_long, f]),
             "ref_sgd_update": (None, [_f32p, _f32p, C.c_long, f]),
+            "ref_mse_loss": (i, [_f32p, i, i, _f32p, i, i, i, C.POINTER(f), _f32p]),
+            "ref_backprop_input_projection": (i, [_f32p, _f32p, i, i, i, _f32p, _f32p, i, i, i]),
             "mt_num_threads": (i, []),
             "mt_set_threads": (None, [i]),
             "mt_project_qkv": (i, [_f32p] * 10 + [i, i, i]),
@@ -409,16 +411,46 @@ def train_step(cfg: dict, weights: dict, seqs, lr: float, clip: float = 1.0, use
     return train_batch(cfg, weights, list(np.ascontiguousarray(seqs, dtype=np.int32)), lr, clip, use_clipping)
 
 
-def _bucket_forward_backward(cfg, w, g, seqs):
-    """Forward with cache, loss and backward of one bucket [B, S + 1]
-    (TransformerTrainer.cs:255-300); gradients accumulate into g.  Returns
-    the bucket's loss, or None when it is not finite (no backward)."""
-    seqs = np.ascontiguousarray(seqs, dtype=np.int32)
-    B, S = seqs.shape[0], seqs.shape[1] - 1
+def mse_loss(pred, targets, effective_len: int, target_start: int = 0):
+    """AccelerationCPU.MSELossAndGradient -> (loss, dOutput)."""
+    pred, targets = _f32(pred), _f32(targets)
+    rows, o = pred.shape
+    d = np.empty((rows, o), np.float32)
+    loss = C.c_float(0)
+    _check(lib().ref_mse_loss(pred, rows, o, targets, targets.shape[0], target_start, effective_len,
+                              C.byref(loss), d), "MSELossAndGradient")
+    return float(np.float32(loss.value)), d
+
+
+def backprop_input_projection(dx, inp, wg, bg, row_start: int = 0):
+    """AccelerationCPU.BackpropInputProjection on copies -> (weightGrad, biasGrad)."""
+    dx, inp = _f32(dx), _f32(inp)
+    wg, bg = _f32(wg).copy(), _f32(bg).copy()
+    _check(lib().ref_backprop_input_projection(dx, inp, inp.shape[0], inp.shape[1], row_start, wg, bg,
+                                               dx.shape[0], dx.shape[1], wg.shape[1]),
+           "BackpropInputProjection")
+    return wg, bg
+
+
+def _bucket_forward_backward(cfg, w, g, seqs=None, inputs=None, reg=None, cls=None):
+    """Forward with cache, loss and backward of one bucket
+    (TransformerTrainer.cs:255-300, 373-456); gradients accumulate into g.
+    Token models take seqs [B, S + 1]; continuous models take inputs
+    [B, S + 1, F] with regression targets reg [B, S + 1, O] (MSE) or class
+    targets cls [B, S + 1] (cross-entropy); row t's target is step t + 1.
+    Returns the bucket's loss, or None when it is not finite (no backward)."""
+    discrete = seqs is not None
+    if discrete:
+        seqs = np.ascontiguousarray(seqs, dtype=np.int32)
+        B, S = seqs.shape[0], seqs.shape[1] - 1
+        ids, targets = seqs[:, :S].reshape(-1), seqs[:, 1:].reshape(-1)
+    else:
+        inputs = _f32(inputs)
+        B, S = inputs.shape[0], inputs.shape[1] - 1
+        flat_in = np.ascontiguousarray(inputs[:, :S].reshape(B * S, -1))
     D, H, nl = cfg["dim"], cfg["heads"], cfg["layers"]
     hd = D // H
     act = cfg.get("ffn_activation", 3)
-    ids, targets = seqs[:, :S].reshape(-1), seqs[:, 1:].reshape(-1)
     rows = B * S
     scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
 
@@ -429,7 +461,10 @@ def _bucket_forward_backward(cfg, w, g, seqs):
         return out
 
     # forward with cache
-    x = embed_tokens(ids, w["token_embedding"])
+    if discrete:
+        x = embed_tokens(ids, w["token_embedding"])
+    else:
+        x = batch_dot_add_bias(w["input_proj"], flat_in, w["input_bias"])
     cache = []
     for L in w["layers"]:
         c = {"input": x}
@@ -447,7 +482,13 @@ def _bucket_forward_backward(cfg, w, g, seqs):
         x, c["m2"], c["v2"], c["n2"], c["r2"] = residual_layernorm_forward(n1, ff, L["ln2_g"], L["ln2_b"])
         cache.append(c)
     logits = project_output_batch(x, w["out_proj"], w["out_bias"])
-    loss, dl = cross_entropy(logits, targets, rows)
+    if discrete:
+        loss, dl = cross_entropy(logits, targets, rows)
+    elif reg is not None:
+        tg = np.ascontiguousarray(_f32(reg)[:, 1:].reshape(B * S, -1))
+        loss, dl = mse_loss(logits, tg, rows)
+    else:
+        loss, dl = cross_entropy(logits, np.ascontiguousarray(np.asarray(cls, np.int32)[:, 1:].reshape(-1)), rows)
     if not (np.isfinite(loss) and np.all(np.isfinite(dl))):
         return None
     if B > 1:
@@ -476,8 +517,12 @@ def _bucket_forward_backward(cfg, w, g, seqs):
         dxa, G["wq"], G["bq"], G["wk"], G["bk"], G["wv"], G["bv"] = backprop_qkv(
             c["input"], dq, dk, dv, L["wq"], L["wk"], L["wv"], G["wq"], G["bq"], G["wk"], G["bk"], G["wv"], G["bv"])
         dx = dxa + dr1
-    g["token_embedding"] = accumulate_token_embedding_grad(g["token_embedding"], dx, ids)
-    g.setdefault("_ids", []).append(ids)
+    if discrete:
+        g["token_embedding"] = accumulate_token_embedding_grad(g["token_embedding"], dx, ids)
+        g.setdefault("_ids", []).append(ids)
+    else:
+        g["input_proj"], g["input_bias"] = backprop_input_projection(dx, flat_in, g["input_proj"],
+                                                                      g["input_bias"])
     return loss
 
 
@@ -494,29 +539,80 @@ def train_batch(cfg: dict, weights: dict, batch, lr: float, clip: float = 1.0, u
     modified.  Returns (loss, grads, new_weights); grads are the gradients
     the update applied, keyed like weights, plus ``norm`` (the pre-clipping
     global norm, None when nothing was valid)."""
-    w = weights
-    nl = cfg["layers"]
-    z = lambda a: np.zeros_like(_f32(a))
-    g = {"token_embedding": z(w["token_embedding"]), "out_proj": z(w["out_proj"]), "out_bias": z(w["out_bias"]),
-         "layers": [{k: z(v) for k, v in L.items()} for L in w["layers"]]}
     buckets = {}
     for seq in batch:
         seq = np.asarray(seq, np.int32)
         if seq.size < 2 or seq.min() < 0 or seq.max() >= cfg["vocab"]:
             continue
         buckets.setdefault(seq.size - 1, []).append(seq)
+    work = [(len(m), {"seqs": np.stack(m)}) for m in buckets.values()]
+    return _train_core(cfg, weights, work, lr, clip, use_clipping, discrete=True)
+
+
+def train_batch_continuous(cfg: dict, weights: dict, inputs, lr: float, reg_targets=None, class_targets=None,
+                           clip: float = 1.0, use_clipping: bool = True):
+    """TransformerTrainer.TrainBatchContinuous (TransformerTrainer.cs:337-485)
+    for a continuous-input model (the continuous_lm_weights layout): window i
+    is inputs[i] [T_i, F]; with reg_targets (TimeSeriesRegression) its targets
+    are reg_targets[i] [>= T_i, O] and the loss is MSE, with class_targets
+    (TimeSeriesClassification) they are class ids class_targets[i] (>= T_i of
+    them) and the loss is cross-entropy; row t predicts step t + 1.  Windows
+    shorter than 2 steps, with non-finite values or invalid targets
+    (:1480-1502) are skipped; the rest are bucketed by length like the token
+    trainer."""
+    F, O = cfg["input_dim"], cfg["output_dim"]
+    buckets = {}
+    for i, x in enumerate(inputs):
+        if x is None:
+            continue
+        x = _f32(x)
+        T = x.shape[0]
+        if T < 2 or x.shape[1] != F or not np.all(np.isfinite(x)):
+            continue
+        if reg_targets is not None:
+            t = reg_targets[i] if i < len(reg_targets) else None
+            if t is None:
+                continue
+            t = _f32(t)
+            if t.shape[0] < T or t.shape[1] != O or not np.all(np.isfinite(t)):
+                continue
+            buckets.setdefault(T - 1, []).append((x, t[:T]))
+        else:
+            t = class_targets[i] if class_targets is not None and i < len(class_targets) else None
+            if t is None:
+                continue
+            t = np.asarray(t, np.int32)
+            if t.size < T or np.any((t[1:T] < 0) | (t[1:T] >= O)):
+                continue
+            buckets.setdefault(T - 1, []).append((x, t[:T]))
+    work = []
+    for m in buckets.values():
+        kw = {"inputs": np.stack([a for a, _ in m])}
+        if reg_targets is not None:
+            kw["reg"] = np.stack([b for _, b in m])
+        else:
+            kw["cls"] = np.stack([b for _, b in m])
+        work.append((len(m), kw))
+    return _train_core(cfg, weights, work, lr, clip, use_clipping, discrete=False)
+
+
+def _train_core(cfg, weights, work, lr, clip, use_clipping, discrete):
+    w = weights
+    first = "token_embedding" if discrete else "input_proj"
+    z = lambda a: np.zeros_like(_f32(a))
+    g = {k: z(w[k]) for k in ((first,) if discrete else ("input_proj", "input_bias"))}
+    g.update({"out_proj": z(w["out_proj"]), "out_bias": z(w["out_bias"]),
+              "layers": [{k: z(v) for k, v in L.items()} for L in w["layers"]]})
     total_loss = np.float32(0)
     valid = 0
-    for _, members in buckets.items():
-        loss = _bucket_forward_backward(cfg, w, g, np.stack(members))
+    for n, kw in work:
+        loss = _bucket_forward_backward(cfg, w, g, **kw)
         if loss is None:
             continue
-        n = len(members)
         total_loss = np.float32(total_loss + (np.float32(loss) * np.float32(n) if n > 1 else np.float32(loss)))
         valid += n
-    neww = {"token_embedding": _f32(w["token_embedding"]).copy(), "out_proj": _f32(w["out_proj"]).copy(),
-            "out_bias": _f32(w["out_bias"]).copy(), "layers": [{k: _f32(v).copy() for k, v in L.items()}
-                                                              for L in w["layers"]]}
+    neww = {k: _f32(v).copy() for k, v in w.items() if k != "layers"}
+    neww["layers"] = [{k: _f32(v).copy() for k, v in L.items()} for L in w["layers"]]
     ids = np.concatenate(g.pop("_ids")) if "_ids" in g else np.zeros(0, np.int32)
     if valid == 0:
         g["norm"] = None
@@ -524,7 +620,11 @@ def train_batch(cfg: dict, weights: dict, batch, lr: float, clip: float = 1.0, u
     loss = float(np.float32(total_loss / np.float32(valid)))
 
     def walk(d):  # every gradient / parameter array once
-        yield d["token_embedding"]
+        if discrete:
+            yield d["token_embedding"]
+        else:
+            yield d["input_proj"]
+            yield d["input_bias"]
         yield d["out_proj"]
         yield d["out_bias"]
         for L in d["layers"]:
@@ -545,12 +645,15 @@ def train_batch(cfg: dict, weights: dict, batch, lr: float, clip: float = 1.0, u
         scale_inplace(a, inv)
     # ComputeGradientNorm (TransformerTrainer.cs:1319-1352): the embedding
     # gradient over its touched rows in first-use order
-    # (SparseRowGradientTracker.SquaredNorm), then the terms in the trainer's
-    # grouping
+    # (SparseRowGradientTracker.SquaredNorm) or the input projection and its
+    # bias, then the terms in the trainer's grouping
     f32, sn = np.float32, lambda a: np.float32(squared_norm(a))
-    _, first = np.unique(ids, return_index=True)
-    touched = ids[np.sort(first)]
-    total = sn(g["token_embedding"][touched])
+    if discrete:
+        _, firsti = np.unique(ids, return_index=True)
+        total = sn(g["token_embedding"][ids[np.sort(firsti)]])
+    else:
+        total = f32(f32(0) + sn(g["input_proj"]))
+        total = f32(total + sn(g["input_bias"]))
     total = f32(total + sn(g["out_proj"]))
     total = f32(total + sn(g["out_bias"]))
     for G in g["layers"]:

@@ -142,6 +142,11 @@ int ref_accumulate_token_embedding_grad(float *eg, const float *dx, const int *i
 float ref_squared_norm(const float *x, long n);
 void ref_scale_inplace(float *x, long n, float scale);
 void ref_sgd_update(float *w, const float *g, long n, float lr);
+int ref_mse_loss(const float *pred, int rows, int out_dim, const float *targets, int target_rows,
+                 int target_start, int effective_len, float *loss, float *dout);
+int ref_backprop_input_projection(const float *dx, const float *input, int input_rows,
+                                  int input_cols, int row_start, float *wg, float *bg, int seq_len,
+                                  int emb_dim, int feat_dim);
 
 /* ---- multi-threaded restatement of AccelerationMutliThreadCPU ---------- */
 

@@ -291,3 +291,47 @@ void ref_scale_inplace(float *x, long n, float scale) {
 void ref_sgd_update(float *w, const float *g, long n, float lr) {
   for (long i = 0; i < n; i++) w[i] -= lr * g[i];
 }
+
+/* AccelerationCPU.cs:2447-2490 (MSELossAndGradient): for rows i <
+ * effective_len, diff = p[i] - t[target_start + i], loss += diff^2,
+ * dOutput = 2 * diff / (effective_len * out_dim); loss /= effective_len *
+ * out_dim.  Rows past effective_len keep a zero gradient. */
+int ref_mse_loss(const float *pred, int rows, int out_dim, const float *targets, int target_rows,
+                 int target_start, int effective_len, float *loss, float *dout) {
+  if (!pred || !targets || !loss || !dout) return REF_EINVAL;
+  if (target_start < 0 || effective_len < 0 || (long)target_start + effective_len > target_rows ||
+      effective_len > rows)
+    return REF_EINVAL;
+  memset(dout, 0, sizeof(float) * (size_t)rows * out_dim);
+  *loss = 0.0f;
+  if (effective_len == 0 || out_dim == 0) return REF_OK;
+  const float inv_len = 1.0f / (float)(effective_len * out_dim);
+  float total = 0.0f;
+  for (int i = 0; i < effective_len; i++)
+    for (int j = 0; j < out_dim; j++) {
+      const float diff = pred[(long)i * out_dim + j] - targets[(long)(target_start + i) * out_dim + j];
+      total += diff * diff;
+      dout[(long)i * out_dim + j] = 2.0f * diff * inv_len;
+    }
+  *loss = total / (float)(effective_len * out_dim);
+  return REF_OK;
+}
+
+/* AccelerationCPU.cs:2280-2332 (BackpropInputProjection): wg[e, f] +=
+ * dX[i, e] * input[row_start + i, f], bg[e] += dX[i, e], rows in order. */
+int ref_backprop_input_projection(const float *dx, const float *input, int input_rows,
+                                  int input_cols, int row_start, float *wg, float *bg, int seq_len,
+                                  int emb_dim, int feat_dim) {
+  if (!dx || !input || !wg || !bg) return REF_EINVAL;
+  if (row_start < 0 || seq_len < 0 || row_start + seq_len > input_rows || feat_dim > input_cols)
+    return REF_EINVAL;
+  for (int i = 0; i < seq_len; i++) {
+    const float *src = input + (long)(row_start + i) * input_cols;
+    for (int e = 0; e < emb_dim; e++) {
+      const float d = dx[(long)i * emb_dim + e];
+      for (int f = 0; f < feat_dim; f++) wg[(long)e * feat_dim + f] += d * src[f];
+      bg[e] += d;
+    }
+  }
+  return REF_OK;
+}

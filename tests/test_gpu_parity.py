@@ -204,7 +204,10 @@ def test_backprop_qkv_c3_shape_float64():
 @pytest.mark.parametrize("rows,ind,out", [(4, 8, 8), (16, 16, 32), (512, 256, 256), (77, 64, 130),
                                           (4112, 128, 1024),   # split K, 257 k-tiles
                                           (4100, 128, 1000),   # split K + 4-row tail; dX with K = 1000
-                                          (252, 64, 200)])     # the config-1 LM head of one training bucket
+                                          (252, 64, 200),      # the config-1 LM head of one training bucket
+                                          (8192, 5, 256),      # input projection: small output, split rows
+                                          (8200, 256, 1),      # regression head [1, D]
+                                          (5000, 7, 3)])       # both small and odd
 def test_linear_backward(rows, ind, out):
     """BackpropLinearProjection (dInput accumulates) and BackpropOutputProjection
     (dX overwritten) on the shapes of AccelerationConsistencyTests.cs:633-700,

@@ -305,3 +305,61 @@ def test_sdpa_bwd_from_saved_statistics(batch, L, dim, heads):
                                  outs[1][0].ptr, dim, outs[1][1].ptr, dim, outs[1][2].ptr, dim, batch, L, L, dim,
                                  heads, scale, 1, None, bws.ptr, small - 4, s)
     assert rc == -1
+
+
+C5S = {"dim": 64, "heads": 2, "layers": 2, "ff": 128, "max_seq": 64, "discrete": False, "input_dim": 5,
+       "output_dim": 3}
+
+
+@pytest.mark.parametrize("kind", ["regression", "classification"])
+def test_device_trainer_continuous_matches_oracle(kind):
+    """TrainBatchContinuous of a time-series model (input projection F 5 ->
+    D 64, head dim 32 on the saved-statistics attention backward): a bucket
+    of four 33-step windows, a lone 20-step window and skipped windows, then
+    two more steps; loss, gradients and weights against the oracle."""
+    cfg = dict(C5S, data_type=1 if kind == "regression" else 2)
+    w = synth.continuous_lm_weights(cfg, 15)
+    rng = np.random.default_rng(21)
+    wins = [rng.uniform(0, 1, (33, 5)).astype(np.float32) for _ in range(4)] + \
+           [rng.uniform(0, 1, (20, 5)).astype(np.float32)]
+    if kind == "regression":
+        tg = [rng.standard_normal((x.shape[0], 3)).astype(np.float32) for x in wins]
+        kw, okw = {"regressionTargets": tg + [None]}, {"reg_targets": tg + [None]}
+    else:
+        tg = [rng.integers(0, 3, x.shape[0]).astype(np.int32) for x in wins]
+        kw, okw = {"classTargets": tg + [None]}, {"class_targets": tg + [None]}
+    inputs = wins + [rng.uniform(0, 1, (33, 5)).astype(np.float32)]  # no targets: skipped
+    t, lm = _trainer(cfg, w, 4, 32)
+    loss = t.TrainBatchContinuous(inputs, learningRate=0.01, **kw)
+    want_loss, want_g, want_w = O.train_batch_continuous(cfg, w, inputs, 0.01, **okw)
+    assert abs(loss - want_loss) <= 1e-5 + 1e-5 * abs(want_loss)
+    assert t.last_norm == pytest.approx(want_g["norm"], rel=1e-4)
+    names = set(t.gradients())
+    assert "input_proj" in names and "token_embedding" not in names
+
+    def named(d):
+        out = {k: d[k] for k in ("input_proj", "input_bias", "out_proj", "out_bias")}
+        for i, L in enumerate(d["layers"]):
+            for k, v in L.items():
+                out[f"layers.{i}.{k}"] = v
+        return out
+
+    for got, want, what in ((t.gradients(), want_g, "gradient"), (t.weights(), want_w, "weight")):
+        ww = named(want)
+        for k, v in got.items():
+            parity(v, np.asarray(ww[k]).reshape(-1), f"continuous {kind} {what} {k}")
+    ww = want_w
+    for step in range(2):
+        more = [rng.uniform(0, 1, (25, 5)).astype(np.float32) for _ in range(3)]
+        if kind == "regression":
+            mt = [rng.standard_normal((25, 3)).astype(np.float32) for _ in range(3)]
+            t.TrainBatchContinuous(more, regressionTargets=mt, learningRate=0.01)
+            _, _, ww = O.train_batch_continuous(cfg, ww, more, 0.01, reg_targets=mt)
+        else:
+            mt = [rng.integers(0, 3, 25).astype(np.int32) for _ in range(3)]
+            t.TrainBatchContinuous(more, classTargets=mt, learningRate=0.01)
+            _, _, ww = O.train_batch_continuous(cfg, ww, more, 0.01, class_targets=mt)
+    got = t.weights()
+    named_w = named(ww)
+    for k in ("input_proj", "layers.1.wq", "layers.0.ffn_w2", "out_proj"):
+        parity(got[k], np.asarray(named_w[k]).reshape(-1), f"after 3 steps {k}")

@@ -79,6 +79,38 @@ def loss64(cfg, w, seqs, drop_ffn_residual=False):
     return float(np.mean(-np.log(p[np.arange(len(tg)), tg] + 1e-10)))
 
 
+def cont_loss64(cfg, w, inputs, reg=None, cls=None):
+    """TrainBatchContinuous's objective for one bucket in float64: the
+    input-projection model of loss64, MSE over rows x outputs against step
+    t + 1 (regression) or mean cross-entropy (classification)."""
+    B, S = inputs.shape[0], inputs.shape[1] - 1
+    D, H = cfg["dim"], cfg["heads"]
+    hd = D // H
+    x = inputs[:, :S].reshape(B * S, -1) @ w["input_proj"].T + w["input_bias"]
+    for L in w["layers"]:
+        q = _rope(x @ L["wq"].T + L["bq"], H, S)
+        k = _rope(x @ L["wk"].T + L["bk"], H, S)
+        v = x @ L["wv"].T + L["bv"]
+        att = np.zeros_like(q)
+        mask = np.tril(np.ones((S, S), bool))
+        for b in range(B):
+            sl = slice(b * S, (b + 1) * S)
+            for h in range(H):
+                cs = slice(h * hd, (h + 1) * hd)
+                sc = np.where(mask, q[sl, cs] @ k[sl, cs].T / np.sqrt(hd), -np.inf)
+                p = np.exp(sc - sc.max(1, keepdims=True))
+                att[sl, cs] = (p / p.sum(1, keepdims=True)) @ v[sl, cs]
+        n1 = _ln(x + att @ L["wo"].T + L["bo"], L["ln1_g"], L["ln1_b"])
+        ff = np.maximum(n1 @ L["ffn_w1"].T + L["ffn_b1"], 0) @ L["ffn_w2"].T + L["ffn_b2"]
+        x = _ln(n1 + ff, L["ln2_g"], L["ln2_b"])
+    out = x @ w["out_proj"].T + w["out_bias"]
+    if reg is not None:
+        return float(np.mean((out - reg[:, 1:S + 1].reshape(B * S, -1)) ** 2))
+    tg = cls[:, 1:S + 1].reshape(-1)
+    p = np.exp(log_softmax(out, axis=1))
+    return float(np.mean(-np.log(p[np.arange(len(tg)), tg] + 1e-10)))
+
+
 def _to64(w):
     return {k: ([{kk: vv.astype(F64) for kk, vv in L.items()} for L in v] if k == "layers" else v.astype(F64))
             for k, v in w.items()}
@@ -162,6 +194,64 @@ def test_mixed_length_batch_gradients_against_finite_differences():
     assert full[0] == ref[0] and np.array_equal(full[1]["out_proj"], ref[1]["out_proj"])
     ok, info = _fd_check([a, b])
     assert ok, info
+
+
+CCFG = {"dim": 8, "heads": 2, "layers": 2, "ff": 16, "max_seq": 8, "discrete": False, "input_dim": 5,
+        "output_dim": 3}
+
+
+@pytest.mark.parametrize("kind", ["regression", "classification"])
+def test_continuous_train_batch_against_finite_differences(kind):
+    """TrainBatchContinuous: a bucket of three 6-step windows and a lone
+    4-step window (plus windows the trainer skips), every gradient against
+    float64 finite differences of the bucket-weighted loss."""
+    rng = np.random.default_rng(11)
+    w = synth.continuous_lm_weights(CCFG, 7)
+    wins = [rng.uniform(0, 1, (6, 5)).astype(np.float32) for _ in range(3)] + \
+           [rng.uniform(0, 1, (4, 5)).astype(np.float32)]
+    if kind == "regression":
+        tg = [rng.standard_normal((t.shape[0] + 1, 3)).astype(np.float32) for t in wins]  # longer is allowed
+        bad_t = rng.standard_normal((6, 3)).astype(np.float32)
+        bad_t[2, 1] = np.nan
+        kw = {"reg_targets": tg + [bad_t, None]}
+    else:
+        tg = [rng.integers(0, 3, t.shape[0]).astype(np.int32) for t in wins]
+        kw = {"class_targets": tg + [np.array([0, 1, 7, 0, 1, 2], np.int32), None]}
+    inputs = wins + [rng.uniform(0, 1, (6, 5)).astype(np.float32), np.zeros((1, 5), np.float32)]
+    loss, g, _ = O.train_batch_continuous(CCFG, w, inputs, 0.1, use_clipping=False, **kw)
+    w64 = _to64(w)
+    a_in, b_in = np.stack(wins[:3]).astype(F64), wins[3][None].astype(F64)
+    if kind == "regression":
+        A, Bt = np.stack([t[:6] for t in tg[:3]]).astype(F64), tg[3][None, :4].astype(F64)
+        lossf = lambda ww: (3 * cont_loss64(CCFG, ww, a_in, reg=A) + cont_loss64(CCFG, ww, b_in, reg=Bt)) / 4
+    else:
+        A, Bt = np.stack(tg[:3]), tg[3][None]
+        lossf = lambda ww: (3 * cont_loss64(CCFG, ww, a_in, cls=A) + cont_loss64(CCFG, ww, b_in, cls=Bt)) / 4
+    assert abs(loss - lossf(w64)) < 1e-5
+    rng2 = np.random.default_rng(0)
+    eps = 1e-6
+    for key, arr in [(("input_proj",), w64["input_proj"]), (("input_bias",), w64["input_bias"])] + \
+            [e for e in _entries(w64) if e[0] != ("token_embedding",)]:
+        flat = arr.reshape(-1)
+        gr = _get(g, key).reshape(-1)
+        for e in rng2.choice(flat.size, size=min(5, flat.size), replace=False):
+            keep = flat[e]
+            flat[e] = keep + eps
+            lp = lossf(w64)
+            flat[e] = keep - eps
+            lm = lossf(w64)
+            flat[e] = keep
+            fd = (lp - lm) / (2 * eps)
+            assert abs(gr[e] - fd) < 3e-5 + 1e-3 * abs(fd), (key, e, gr[e], fd)
+
+
+def test_mse_loss_closed_form():
+    rng = np.random.default_rng(4)
+    p, t = rng.standard_normal((5, 3)).astype(np.float32), rng.standard_normal((7, 3)).astype(np.float32)
+    loss, d = O.mse_loss(p, t, 4, target_start=2)
+    diff = p[:4].astype(F64) - t[2:6]
+    assert loss == pytest.approx(np.mean(diff ** 2), rel=1e-6)
+    assert np.allclose(d[:4], 2 * diff / 12, atol=1e-7) and not d[4].any()
 
 
 def test_planted_mistake_fails_the_gradient_check():
