@@ -168,15 +168,25 @@ __device__ __forceinline__ float activate(float x, int act) {
 // Stores output (m, n) of problem P from z = acc + bias: pre <- z,
 // v = act(z), v *= act'(dz) and v += add when those options are set, then
 // C = v (or C + v with beta).
+// The options are a compile-time switch (EPI) so that launches without them
+// keep the plain epilogue.
+template <bool EPI>
 __device__ __forceinline__ void store_elem(const GemmArgs &args, const GemmProblem &P, int m, int n,
                                            float z, int act) {
-  if (args.pre) args.pre[(size_t)m * args.ldpre + n] = z;
-  float v = activate(z, act);
-  if (args.dz) v *= act_deriv(args.dz[(size_t)m * args.lddz + n], args.dact);
-  if (args.add) v += args.add[(size_t)m * args.ldadd + n];
+  float v;
+  if constexpr (EPI) {
+    if (args.pre) args.pre[(size_t)m * args.ldpre + n] = z;
+    v = activate(z, act);
+    if (args.dz) v *= act_deriv(args.dz[(size_t)m * args.lddz + n], args.dact);
+    if (args.add) v += args.add[(size_t)m * args.ldadd + n];
+  } else {
+    v = activate(z, act);
+  }
   float *pc = P.c + (size_t)m * args.ldc + n;
   *pc = args.beta ? *pc + v : v;
 }
+
+inline bool has_epi(const GemmArgs &g) { return g.pre || g.dz || g.add; }
 
 // Global -> register staging of one 128x32 tile of a row-major [rows, K]
 // matrix.  VEC: K % 4 == 0 and 16-byte aligned rows, four float4 per thread;
@@ -224,7 +234,7 @@ struct TileStage {
 };
 
 // Guarded fallback of the forward layout (any K, any alignment).
-template <bool VEC>
+template <bool VEC, bool EPI>
 __global__ void __launch_bounds__(NTHREADS) gemm_nt_kernel(const GemmArgs args) {
   __shared__ __attribute__((aligned(16))) float As[2][BM][LDSK];
   __shared__ __attribute__((aligned(16))) float Bs[2][BN][LDSK];
@@ -319,7 +329,7 @@ __global__ void __launch_bounds__(NTHREADS) gemm_nt_kernel(const GemmArgs args) 
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
-        if (m < M) store_elem(args, P, m, n, acc[i][j][r] + bias, args.act);
+        if (m < M) store_elem<EPI>(args, P, m, n, acc[i][j][r] + bias, args.act);
       }
     }
   }
@@ -400,7 +410,7 @@ struct OpStage {
 // weight-gradient GEMM costs no extra pass over dY.  Each thread keeps one
 // partial sum (row t % TM, a 1/(NT/TM) slice of the k-tile); the slices meet
 // in LDS at the end.
-template <int TM, int TN, int BKK, int WM, int WN, int MINB, int ACT, bool TA, bool TB>
+template <int TM, int TN, int BKK, int WM, int WN, int MINB, int ACT, bool TA, bool TB, bool EPI>
 __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const GemmArgs args) {
   constexpr int NT = 64 * WM * WN;
   constexpr int LD = BKK + 4;
@@ -578,7 +588,7 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const Gem
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + wm * (TM / WM) + i * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
-        if (m < M) store_elem(args, P, m, n, acc[i][j][r] + bias, ACT == kActRope ? CDML_ACT_NONE : ACT);
+        if (m < M) store_elem<EPI>(args, P, m, n, acc[i][j][r] + bias, ACT == kActRope ? CDML_ACT_NONE : ACT);
       }
     }
   }
@@ -588,7 +598,7 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const Gem
 // kernel's conditions): a 64 x 64 tile of C per 256-thread workgroup, 4 x 4
 // outputs per thread, K in steps of 16 through LDS with guarded loads that
 // walk each source along its contiguous dimension.
-template <bool TA, bool TB>
+template <bool TA, bool TB, bool EPI>
 __global__ void __launch_bounds__(256) gemm_any_kernel(const GemmArgs args) {
   __shared__ float As[16][65], Bs[16][65];  // [k][m], [k][n]
   const GemmProblem P = args.p[blockIdx.z];
@@ -628,7 +638,7 @@ __global__ void __launch_bounds__(256) gemm_any_kernel(const GemmArgs args) {
     for (int j = 0; j < 4; ++j) {
       const int n = n0 + tx * 4 + j;
       if (n >= N) continue;
-      store_elem(args, P, m, n, acc[i][j] + (P.bias ? P.bias[n] : 0.f), args.act);
+      store_elem<EPI>(args, P, m, n, acc[i][j] + (P.bias ? P.bias[n] : 0.f), args.act);
     }
   }
 }
@@ -781,6 +791,19 @@ SplitPlan splitk_plan(int M, int N, int K, int nprob) {
   return sp;
 }
 
+// The forward tile kernel for the launch's activation.
+template <int TM, int TN, int BKK, int WM, int WN, int MINB, bool EPI>
+void launch_tile_act(const GemmArgs &g, dim3 grid, dim3 block, hipStream_t stream) {
+  switch (g.act) {
+    case CDML_ACT_NONE: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_NONE, false, false, EPI><<<grid, block, 0, stream>>>(g); break;
+    case CDML_ACT_SIGMOID: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_SIGMOID, false, false, EPI><<<grid, block, 0, stream>>>(g); break;
+    case CDML_ACT_TANH: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_TANH, false, false, EPI><<<grid, block, 0, stream>>>(g); break;
+    case CDML_ACT_RELU: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_RELU, false, false, EPI><<<grid, block, 0, stream>>>(g); break;
+    case CDML_ACT_LEAKYRELU: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_LEAKYRELU, false, false, EPI><<<grid, block, 0, stream>>>(g); break;
+    default: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_SWISH, false, false, EPI><<<grid, block, 0, stream>>>(g); break;
+  }
+}
+
 // Two tile configurations: 256 x 128 with eight waves for M >= 1024, and
 // 128 x 128 with four waves for smaller M (decode rows, short sequences).
 template <int TM, int TN, int BKK, int WM, int WN, int MINB, bool TA, bool TB>
@@ -793,23 +816,23 @@ int launch_tile(GemmArgs g, hipStream_t stream) {
   g.padded = pad_to_xcd(g.total);
   const dim3 grid(g.padded), block(64 * WM * WN);
   if constexpr (TA || TB) {
-    gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_NONE, TA, TB><<<grid, block, 0, stream>>>(g);
+    if (has_epi(g))
+      gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_NONE, TA, TB, true><<<grid, block, 0, stream>>>(g);
+    else
+      gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_NONE, TA, TB, false><<<grid, block, 0, stream>>>(g);
     if (g.ksplit > 1) {
       const size_t n = std::max((size_t)g.M * (g.N / 4), (size_t)g.M);
       splitk_reduce_kernel<<<dim3((unsigned)((n + 255) / 256), g.nprob), dim3(256), 0, stream>>>(g);
     }
   } else {
     if (g.rope_cs) {
-      gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, kActRope, false, false><<<grid, block, 0, stream>>>(g);
+      gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, kActRope, false, false, false><<<grid, block, 0, stream>>>(g);
       return CDML_OK;
     }
-    switch (g.act) {
-      case CDML_ACT_NONE: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_NONE, false, false><<<grid, block, 0, stream>>>(g); break;
-      case CDML_ACT_SIGMOID: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_SIGMOID, false, false><<<grid, block, 0, stream>>>(g); break;
-      case CDML_ACT_TANH: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_TANH, false, false><<<grid, block, 0, stream>>>(g); break;
-      case CDML_ACT_RELU: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_RELU, false, false><<<grid, block, 0, stream>>>(g); break;
-      case CDML_ACT_LEAKYRELU: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_LEAKYRELU, false, false><<<grid, block, 0, stream>>>(g); break;
-      default: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_SWISH, false, false><<<grid, block, 0, stream>>>(g); break;
+    if (has_epi(g)) {
+      launch_tile_act<TM, TN, BKK, WM, WN, MINB, true>(g, grid, block, stream);
+    } else {
+      launch_tile_act<TM, TN, BKK, WM, WN, MINB, false>(g, grid, block, stream);
     }
   }
   return CDML_OK;
@@ -828,7 +851,8 @@ int launch_layout(GemmArgs &g, bool fast, hipStream_t stream) {
   if (fast) return g.M >= 1024 ? launch_tile<256, 128, 16, 4, 2, 2, TA, TB>(g, stream)
                                : launch_tile<128, 128, 16, 2, 2, 2, TA, TB>(g, stream);
   const dim3 grid((g.N + 63) / 64, (g.M + 63) / 64, g.nprob);
-  gemm_any_kernel<TA, TB><<<grid, dim3(256), 0, stream>>>(g);
+  if (has_epi(g)) gemm_any_kernel<TA, TB, true><<<grid, dim3(256), 0, stream>>>(g);
+  else gemm_any_kernel<TA, TB, false><<<grid, dim3(256), 0, stream>>>(g);
   bool bgrad = false;
   for (int i = 0; i < g.nprob; ++i) bgrad = bgrad || g.p[i].bgrad;
   if (bgrad && g.K > 0) op_rowsum_kernel<TA><<<dim3((g.M + 255) / 256, g.nprob), dim3(256), 0, stream>>>(g);
@@ -891,9 +915,11 @@ int launch_gemm(GemmArgs &g, bool ta, bool tb, hipStream_t stream, const char *w
     int rc = launch_tile<128, 128, 16, 2, 2, 2, false, false>(g, stream);
     if (rc) return rc;
   } else if (vec)
-    gemm_nt_kernel<true><<<dim3(g.padded), dim3(NTHREADS), 0, stream>>>(g);
+    has_epi(g) ? gemm_nt_kernel<true, true><<<dim3(g.padded), dim3(NTHREADS), 0, stream>>>(g)
+               : gemm_nt_kernel<true, false><<<dim3(g.padded), dim3(NTHREADS), 0, stream>>>(g);
   else
-    gemm_nt_kernel<false><<<dim3(g.padded), dim3(NTHREADS), 0, stream>>>(g);
+    has_epi(g) ? gemm_nt_kernel<false, true><<<dim3(g.padded), dim3(NTHREADS), 0, stream>>>(g)
+               : gemm_nt_kernel<false, false><<<dim3(g.padded), dim3(NTHREADS), 0, stream>>>(g);
   return check_launch(what);
 }
 

@@ -8,7 +8,13 @@
 namespace cdml {
 namespace {
 
-constexpr int ROW_CACHE = 32;
+// Row-cache size: the smallest power of two with 64 * RC >= features (up to
+// 32); longer rows are re-read in the second and third passes.
+inline int row_cache(int f) {
+  int rc = 1;
+  while (64 * rc < f && rc < 32) rc <<= 1;
+  return rc;
+}
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -16,6 +22,7 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+template <int ROW_CACHE>
 __global__ void __launch_bounds__(256) residual_ln_kernel(const float *__restrict__ a,
                                                           const float *__restrict__ b,
                                                           const float *__restrict__ gamma,
@@ -84,7 +91,17 @@ extern "C" int cdml_residual_layernorm(const float *a, const float *b, const flo
     return fail(CDML_E_INVALID, "cdml_residual_layernorm: NULL pointer");
   int rc = ensure_device();
   if (rc) return rc;
-  residual_ln_kernel<<<dim3((rows + 3) / 4), dim3(256), 0, as_hip(stream)>>>(a, b, gamma, beta, y,
-                                                                            rows, features, eps);
+  const dim3 grid((rows + 3) / 4), block(256);
+  hipStream_t st = as_hip(stream);
+#define CDML_RLN(RC) residual_ln_kernel<RC><<<grid, block, 0, st>>>(a, b, gamma, beta, y, rows, features, eps)
+  switch (row_cache(features)) {
+    case 1: CDML_RLN(1); break;
+    case 2: CDML_RLN(2); break;
+    case 4: CDML_RLN(4); break;
+    case 8: CDML_RLN(8); break;
+    case 16: CDML_RLN(16); break;
+    default: CDML_RLN(32); break;
+  }
+#undef CDML_RLN
   return check_launch("residual_ln_kernel");
 }

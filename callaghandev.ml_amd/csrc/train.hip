@@ -12,7 +12,15 @@
 namespace cdml {
 namespace {
 
-constexpr int kRowCache = 32;  // features kept in registers per lane (64 * 32 = 2048)
+constexpr int kRowCache = 32;  // most features kept in registers per lane (64 * 32 = 2048)
+
+// Row-cache size of the LayerNorm kernels: the smallest power of two with
+// 64 * RC >= features, so short rows keep few registers (high occupancy).
+inline int row_cache(int f) {
+  int rc = 1;
+  while (64 * rc < f) rc <<= 1;
+  return rc;
+}
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -30,6 +38,7 @@ __device__ __forceinline__ float wave_max(float v) {
 // wave: residual = a + b, mean, biased variance (two passes), out = gamma *
 // (residual - mean) * invStd + beta; mean / var / residual / normalized are
 // written when non-NULL.
+template <int RC>
 __global__ void __launch_bounds__(256) ln_forward_kernel(const float *__restrict__ a,
                                                          const float *__restrict__ b,
                                                          const float *__restrict__ gamma,
@@ -44,10 +53,10 @@ __global__ void __launch_bounds__(256) ln_forward_kernel(const float *__restrict
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
   const size_t base = (size_t)row * f;
-  float cache[kRowCache];
+  float cache[RC];
   float sum = 0.f;
 #pragma unroll
-  for (int i = 0; i < kRowCache; ++i) {
+  for (int i = 0; i < RC; ++i) {
     const int j = lane + 64 * i;
     cache[i] = j < f ? a[base + j] + b[base + j] : 0.f;
     sum += cache[i];
@@ -55,7 +64,7 @@ __global__ void __launch_bounds__(256) ln_forward_kernel(const float *__restrict
   const float mean = wave_sum(sum) / (float)f;
   float var = 0.f;
 #pragma unroll
-  for (int i = 0; i < kRowCache; ++i) {
+  for (int i = 0; i < RC; ++i) {
     const int j = lane + 64 * i;
     const float d = cache[i] - mean;
     var += j < f ? d * d : 0.f;
@@ -63,7 +72,7 @@ __global__ void __launch_bounds__(256) ln_forward_kernel(const float *__restrict
   var = wave_sum(var) / (float)f;
   const float inv_std = 1.0f / sqrtf(var + eps);
 #pragma unroll
-  for (int i = 0; i < kRowCache; ++i) {
+  for (int i = 0; i < RC; ++i) {
     const int j = lane + 64 * i;
     if (j < f) {
       const float n = (cache[i] - mean) * inv_std;
@@ -86,6 +95,7 @@ __global__ void __launch_bounds__(256) ln_forward_kernel(const float *__restrict
 // workspace for ln_param_grad_kernel.
 constexpr int kLnRowsPerBlock = 64;
 
+template <int RC>
 __global__ void __launch_bounds__(256) ln_backward_kernel(
     const float *__restrict__ dout, const float *__restrict__ dout2,
     const float *__restrict__ normalized, const float *__restrict__ gamma,
@@ -94,9 +104,9 @@ __global__ void __launch_bounds__(256) ln_backward_kernel(
     int f, float eps) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int row0 = blockIdx.x * kLnRowsPerBlock;
-  float pg[kRowCache], pb[kRowCache];
+  float pg[RC], pb[RC];
 #pragma unroll
-  for (int i = 0; i < kRowCache; ++i) pg[i] = pb[i] = 0.f;
+  for (int i = 0; i < RC; ++i) pg[i] = pb[i] = 0.f;
   for (int rr = wave; rr < kLnRowsPerBlock; rr += 4) {
     const int row = row0 + rr;
     if (row >= rows) break;
@@ -104,10 +114,10 @@ __global__ void __launch_bounds__(256) ln_backward_kernel(
     const float inv_std = 1.0f / sqrtf(var[row] + eps);
     const float inv_std3 = inv_std * inv_std * inv_std;
     const float m = mean[row];
-    float gv[kRowCache], xm[kRowCache];
+    float gv[RC], xm[RC];
     float dvar = 0.f, dmean = 0.f;
 #pragma unroll
-    for (int i = 0; i < kRowCache; ++i) {
+    for (int i = 0; i < RC; ++i) {
       const int j = lane + 64 * i;
       gv[i] = 0.f;
       xm[i] = 0.f;
@@ -131,7 +141,7 @@ __global__ void __launch_bounds__(256) ln_backward_kernel(
     const float dvar_scale = dvar * 2.0f * inv_n;
     const float dmean_scale = dmean * inv_n;
 #pragma unroll
-    for (int i = 0; i < kRowCache; ++i) {
+    for (int i = 0; i < RC; ++i) {
       const int j = lane + 64 * i;
       if (j < f) dx[base + j] = (gv[i] * gamma[j]) * inv_std + dvar_scale * xm[i] + dmean_scale;
     }
@@ -139,7 +149,7 @@ __global__ void __launch_bounds__(256) ln_backward_kernel(
   // the four waves' column partials meet in LDS, in wave order
   __shared__ float red[4][64];
 #pragma unroll
-  for (int i = 0; i < kRowCache; ++i) {
+  for (int i = 0; i < RC; ++i) {
     if (64 * i >= f) break;  // uniform
     red[wave][lane] = pg[i];
     __syncthreads();
@@ -447,8 +457,18 @@ extern "C" int cdml_residual_layernorm_fwd(const float *a, const float *b, const
     return fail(CDML_E_INVALID, "cdml_residual_layernorm_fwd: more than %d features", 64 * kRowCache);
   int rc = ensure_device();
   if (rc) return rc;
-  ln_forward_kernel<<<dim3((rows + 3) / 4), dim3(256), 0, as_hip(stream)>>>(
-      a, b, gamma, beta, out, mean, variance, residual, normalized, rows, features, eps);
+  const dim3 grid((rows + 3) / 4), block(256);
+  hipStream_t st = as_hip(stream);
+#define CDML_LN_FWD(RC) ln_forward_kernel<RC><<<grid, block, 0, st>>>(a, b, gamma, beta, out, mean, variance, residual, normalized, rows, features, eps)
+  switch (row_cache(features)) {
+    case 1: CDML_LN_FWD(1); break;
+    case 2: CDML_LN_FWD(2); break;
+    case 4: CDML_LN_FWD(4); break;
+    case 8: CDML_LN_FWD(8); break;
+    case 16: CDML_LN_FWD(16); break;
+    default: CDML_LN_FWD(32); break;
+  }
+#undef CDML_LN_FWD
   return check_launch("ln_forward_kernel");
 }
 
@@ -485,8 +505,16 @@ extern "C" int cdml_layernorm_backward(const float *dout, const float *dout2,
   const int nblk = (rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock;
   float *pg = static_cast<float *>(workspace), *pb = pg + (size_t)nblk * features;
   if (rows > 0) {
-    ln_backward_kernel<<<dim3(nblk), dim3(256), 0, st>>>(dout, dout2, normalized, gamma, input, mean,
-                                                         variance, dinput, pg, pb, rows, features, eps);
+#define CDML_LN_BWD(RC) ln_backward_kernel<RC><<<dim3(nblk), dim3(256), 0, st>>>(dout, dout2, normalized, gamma, input, mean, variance, dinput, pg, pb, rows, features, eps)
+    switch (row_cache(features)) {
+      case 1: CDML_LN_BWD(1); break;
+      case 2: CDML_LN_BWD(2); break;
+      case 4: CDML_LN_BWD(4); break;
+      case 8: CDML_LN_BWD(8); break;
+      case 16: CDML_LN_BWD(16); break;
+      default: CDML_LN_BWD(32); break;
+    }
+#undef CDML_LN_BWD
     rc = check_launch("ln_backward_kernel");
     if (rc) return rc;
   }
