@@ -93,10 +93,11 @@ __global__ void __launch_bounds__(256) ln_forward_kernel(const float *__restrict
 // residual input when not given.  Each workgroup owns kLnRowsPerBlock rows
 // and writes its partial column sums of g * normalized and g to the
 // workspace for ln_param_grad_kernel.
-constexpr int kLnRowsPerBlock = 64;
+constexpr int kLnRowsPerBlock = 64;  // rows per workgroup (16 waves x 4, or 4 waves x 16 for the longest rows)
+constexpr int ln_waves(int rc) { return rc >= 32 ? 4 : 16; }
 
-template <int RC>
-__global__ void __launch_bounds__(256) ln_backward_kernel(
+template <int RC, int WAVES = ln_waves(RC)>
+__global__ void __launch_bounds__(64 * WAVES) ln_backward_kernel(
     const float *__restrict__ dout, const float *__restrict__ dout2,
     const float *__restrict__ normalized, const float *__restrict__ gamma,
     const float *__restrict__ x, const float *__restrict__ mean, const float *__restrict__ var,
@@ -107,60 +108,84 @@ __global__ void __launch_bounds__(256) ln_backward_kernel(
   float pg[RC], pb[RC];
 #pragma unroll
   for (int i = 0; i < RC; ++i) pg[i] = pb[i] = 0.f;
-  for (int rr = wave; rr < kLnRowsPerBlock; rr += 4) {
-    const int row = row0 + rr;
-    if (row >= rows) break;
-    const size_t base = (size_t)row * f;
-    const float inv_std = 1.0f / sqrtf(var[row] + eps);
-    const float inv_std3 = inv_std * inv_std * inv_std;
-    const float m = mean[row];
-    float gv[RC], xm[RC];
-    float dvar = 0.f, dmean = 0.f;
+  // Short rows (RC <= 4): the wave's U rows are handled together so that
+  // their loads and reductions overlap; rows past the end are clamped for
+  // the loads and contribute nothing.
+  constexpr int U = RC <= 4 ? kLnRowsPerBlock / WAVES : 1;
+  const float inv_n = 1.0f / (float)f;
+  for (int rr0 = wave; rr0 < kLnRowsPerBlock; rr0 += WAVES * U) {
+    float gv[U][RC], xm[U][RC], dvar[U], dmean[U], istd[U];
+    size_t base[U];
+    bool live[U];
 #pragma unroll
-    for (int i = 0; i < RC; ++i) {
-      const int j = lane + 64 * i;
-      gv[i] = 0.f;
-      xm[i] = 0.f;
-      if (j < f) {
-        float g = dout[base + j];
-        if (dout2) g += dout2[base + j];
-        const float xmj = x[base + j] - m;
-        const float n = normalized ? normalized[base + j] : xmj * inv_std;
-        pg[i] += g * n;
-        pb[i] += g;
-        const float dnorm = g * gamma[j];
-        dvar += dnorm * xmj * (-0.5f) * inv_std3;
-        dmean += dnorm * (-inv_std);
-        gv[i] = g;
-        xm[i] = xmj;
+    for (int u = 0; u < U; ++u) {
+      const int row = row0 + rr0 + WAVES * u;
+      live[u] = row < rows;
+      const int rc = live[u] ? row : rows - 1;
+      base[u] = (size_t)rc * f;
+      const float inv_std = 1.0f / sqrtf(var[rc] + eps);
+      const float inv_std3 = inv_std * inv_std * inv_std;
+      const float m = mean[rc];
+      istd[u] = inv_std;
+      dvar[u] = dmean[u] = 0.f;
+#pragma unroll
+      for (int i = 0; i < RC; ++i) {
+        const int j = lane + 64 * i;
+        gv[u][i] = 0.f;
+        xm[u][i] = 0.f;
+        if (j < f) {
+          float g = dout[base[u] + j];
+          if (dout2) g += dout2[base[u] + j];
+          const float xmj = x[base[u] + j] - m;
+          const float n = normalized ? normalized[base[u] + j] : xmj * inv_std;
+          if (live[u]) {
+            pg[i] += g * n;
+            pb[i] += g;
+          }
+          const float dnorm = g * gamma[j];
+          dvar[u] += dnorm * xmj * (-0.5f) * inv_std3;
+          dmean[u] += dnorm * (-inv_std);
+          gv[u][i] = g;
+          xm[u][i] = xmj;
+        }
       }
     }
-    dvar = wave_sum(dvar);
-    dmean = wave_sum(dmean);
-    const float inv_n = 1.0f / (float)f;
-    const float dvar_scale = dvar * 2.0f * inv_n;
-    const float dmean_scale = dmean * inv_n;
 #pragma unroll
-    for (int i = 0; i < RC; ++i) {
-      const int j = lane + 64 * i;
-      if (j < f) dx[base + j] = (gv[i] * gamma[j]) * inv_std + dvar_scale * xm[i] + dmean_scale;
+    for (int u = 0; u < U; ++u) {
+      dvar[u] = wave_sum(dvar[u]);
+      dmean[u] = wave_sum(dmean[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (!live[u]) continue;
+      const float dvar_scale = dvar[u] * 2.0f * inv_n;
+      const float dmean_scale = dmean[u] * inv_n;
+#pragma unroll
+      for (int i = 0; i < RC; ++i) {
+        const int j = lane + 64 * i;
+        if (j < f) dx[base[u] + j] = (gv[u][i] * gamma[j]) * istd[u] + dvar_scale * xm[u][i] + dmean_scale;
+      }
     }
   }
-  // the four waves' column partials meet in LDS, in wave order
-  __shared__ float red[4][64];
+  // the waves' column partials meet in LDS, summed in wave order
+  __shared__ float rg[WAVES][64], rb[WAVES][64];
 #pragma unroll
   for (int i = 0; i < RC; ++i) {
     if (64 * i >= f) break;  // uniform
-    red[wave][lane] = pg[i];
+    rg[wave][lane] = pg[i];
+    rb[wave][lane] = pb[i];
     __syncthreads();
     const int j = lane + 64 * i;
-    if (wave == 0 && j < f)
-      part_g[(size_t)blockIdx.x * f + j] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
-    __syncthreads();
-    red[wave][lane] = pb[i];
-    __syncthreads();
-    if (wave == 0 && j < f)
-      part_b[(size_t)blockIdx.x * f + j] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+    if (wave == 0 && j < f) {
+      float sg = 0.f, sb = 0.f;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) {
+        sg += rg[w][lane];
+        sb += rb[w][lane];
+      }
+      part_g[(size_t)blockIdx.x * f + j] = sg;
+      part_b[(size_t)blockIdx.x * f + j] = sb;
+    }
     __syncthreads();
   }
 }
@@ -505,7 +530,7 @@ extern "C" int cdml_layernorm_backward(const float *dout, const float *dout2,
   const int nblk = (rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock;
   float *pg = static_cast<float *>(workspace), *pb = pg + (size_t)nblk * features;
   if (rows > 0) {
-#define CDML_LN_BWD(RC) ln_backward_kernel<RC><<<dim3(nblk), dim3(256), 0, st>>>(dout, dout2, normalized, gamma, input, mean, variance, dinput, pg, pb, rows, features, eps)
+#define CDML_LN_BWD(RC) ln_backward_kernel<RC><<<dim3(nblk), dim3(64 * ln_waves(RC)), 0, st>>>(dout, dout2, normalized, gamma, input, mean, variance, dinput, pg, pb, rows, features, eps)
     switch (row_cache(features)) {
       case 1: CDML_LN_BWD(1); break;
       case 2: CDML_LN_BWD(2); break;
