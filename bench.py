@@ -300,113 +300,136 @@ def bench_train(H, cfg, batch, seq_inputs, steps, warmup, lr=0.01):
             "tflops": round(3 * fwd / (ms * 1e-3) / 1e12, 2), "gflop_per_step": round(3 * fwd / 1e9, 1)}
 
 
-def extras(N, st):
+EXTRA_LEGS = ("c2_mha_layer", "c3_mha_layer_backward", "c1_text_model_train_step", "c3_shape_train_step",
+              "c5_time_series_train_step", "c3_decoder_stack_12_layers", "c3_mha_one_sequence_dropin_host_arrays",
+              "c5_time_series_model", "c1_text_model")
+
+
+def extras(N, st, only=None):
     """End-to-end figures for the other BASELINE configs (device-resident,
-    events on the engine's stream) and the PCIe-inclusive drop-in path."""
+    events on the engine's stream) and the PCIe-inclusive drop-in path.
+    `only` (a set of EXTRA_LEGS names) restricts the run to those legs."""
     from cdml import host, synth
 
     H = host.module()
     out = {}
-    # c2: one causal MHA layer, B 16 x L 1024, D 512, 8 heads
-    c2 = dict(batch=16, seq=1024, dim=512, heads=8)
-    r = bench_mha(N, st, 10, 5, c2)
-    core, qkv, o = mha_flops(**c2)
-    out["c2_mha_layer"] = {"ms": round(r["wall_s"] / 10 * 1e3, 4),
-                           "tflops": round((core + qkv + o) / (r["wall_s"] / 10) / 1e12, 2),
-                           "flash_ms": round(r["flash_ms"], 4)}
-    log("[bench] extras: c3 MHA layer backward")
-    out["c3_mha_layer_backward"] = bench_mha_backward(N, st, 5, 3)
-    log("[bench] extras: training steps")
-    out["c1_text_model_train_step"] = dict(
-        bench_train(H, {"vocab": 200, "dim": 64, "heads": 4, "layers": 2, "ff": 128, "max_seq": 64}, 4, 63, 20, 5),
-        workload="TrainBatchDiscrete on 4 sequences of 64 tokens (63 inputs), config-1 text model")
-    out["c3_shape_train_step"] = dict(
-        bench_train(H, {"vocab": 1000, "dim": 1024, "heads": 16, "layers": 12, "ff": 4096, "max_seq": 4096},
-                    4, 4095, 3, 1),
-        workload="TrainBatchDiscrete on 4 sequences of 4096 tokens, 12 decoder layers D 1024 / 16 heads / "
-                 "FF 4096 (config-3 shape) with a 1000-token vocabulary")
-    cfg5t = {"dim": 256, "heads": 8, "layers": 6, "ff": 1024, "max_seq": 512, "discrete": False, "input_dim": 5,
-             "output_dim": 1}
-    lm5t, _ = host.language_model(cfg5t, synth.continuous_lm_weights(cfg5t, 19))
-    t5 = H.DeviceTrainer(lm5t, H.TrainingConfig(), 256, 511)
-    win = synth.random_walk_windows(33, 256, 512, 5)
-    tgt = np.ascontiguousarray(win[:, :, :1])  # next-step regression of the first feature
-    ms5t = t5.time_step_continuous(win, tgt, 1e-3, 3, 1)
-    core, qkv, o = mha_flops(256, 511, 256, 8)
-    fwd5 = 6 * (core + qkv + o + 4 * 256 * 511 * 256 * 1024) + 2 * 256 * 511 * 256 * (5 + 1)
-    out["c5_time_series_train_step"] = {
-        "ms": round(ms5t, 3), "windows_per_s": round(256 / (ms5t * 1e-3), 1),
-        "tflops": round(3 * fwd5 / (ms5t * 1e-3) / 1e12, 2),
-        "workload": "TrainBatchContinuous (MSE) on 256 windows of 512 steps, config-5 model"}
-    del t5, lm5t
-    log("[bench] extras: c3 12-layer decoder stack")
-    # c3: 12 post-LN decoder layers (MHA + FFN 4096 + 2 LayerNorms) on N(0,1) embeddings
-    cfg3 = {"dim": 1024, "heads": 16, "layers": 12, "ff": 4096, "max_seq": 4096, "discrete": False,
-            "input_dim": 1024, "output_dim": 1}
-    lm3, mgr = host.language_model(cfg3, synth.continuous_lm_weights(cfg3, 41, biased=False))
-    dev3 = H.DeviceLanguageModel(lm3, 4)
-    x3 = np.random.default_rng(6).standard_normal((4 * 4096, 1024), dtype=np.float32)
-    ms3 = dev3.time_layers(x3, 4, 4096, steps=3, warmup=1)
-    core, qkv, o = mha_flops(**C3)
-    ffn = 4 * 4 * 4096 * 1024 * 4096
-    fl3 = 12 * (core + qkv + o + ffn)
-    out["c3_decoder_stack_12_layers"] = {"ms": round(ms3, 3), "tflops": round(fl3 / (ms3 * 1e-3) / 1e12, 2),
-                                         "frac_of_fp32_mfma_peak": round(fl3 / (ms3 * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
-                                         "tokens_per_s": round(4 * 4096 / (ms3 * 1e-3), 1),
-                                         "gflop": round(fl3 / 1e9, 1)}
-    del dev3, lm3
-    # drop-in manager path on one c3 sequence: host arrays in and out (PCIe inclusive)
-    log("[bench] extras: drop-in manager (host arrays)")
-    D, Hh, L = 1024, 16, 4096
-    xs = np.random.default_rng(7).standard_normal((L, D), dtype=np.float32)
-    wq, wk, wv, wo = (synth.xavier_uniform(60 + i, D, D) for i in range(4))
-    bz = np.zeros(D, np.float32)
+    want = (lambda name: True) if not only else (lambda name: name in only)
+    mgr = None
+    if want("c2_mha_layer"):
+        # c2: one causal MHA layer, B 16 x L 1024, D 512, 8 heads
+        c2 = dict(batch=16, seq=1024, dim=512, heads=8)
+        r = bench_mha(N, st, 10, 5, c2)
+        core, qkv, o = mha_flops(**c2)
+        out["c2_mha_layer"] = {"ms": round(r["wall_s"] / 10 * 1e3, 4),
+                               "tflops": round((core + qkv + o) / (r["wall_s"] / 10) / 1e12, 2),
+                               "flash_ms": round(r["flash_ms"], 4)}
+    if want("c3_mha_layer_backward"):
+        log("[bench] extras: c3 MHA layer backward")
+        out["c3_mha_layer_backward"] = bench_mha_backward(N, st, 5, 3)
+    if want("c1_text_model_train_step"):
+        log("[bench] extras: c1 train step")
+        out["c1_text_model_train_step"] = dict(
+            bench_train(H, {"vocab": 200, "dim": 64, "heads": 4, "layers": 2, "ff": 128, "max_seq": 64},
+                        4, 63, 20, 5),
+            workload="TrainBatchDiscrete on 4 sequences of 64 tokens (63 inputs), config-1 text model")
+    if want("c3_shape_train_step"):
+        log("[bench] extras: c3-shape train step")
+        out["c3_shape_train_step"] = dict(
+            bench_train(H, {"vocab": 1000, "dim": 1024, "heads": 16, "layers": 12, "ff": 4096, "max_seq": 4096},
+                        4, 4095, 3, 1),
+            workload="TrainBatchDiscrete on 4 sequences of 4096 tokens, 12 decoder layers D 1024 / 16 heads / "
+                     "FF 4096 (config-3 shape) with a 1000-token vocabulary")
+    if want("c5_time_series_train_step"):
+        log("[bench] extras: c5 train step")
+        cfg5t = {"dim": 256, "heads": 8, "layers": 6, "ff": 1024, "max_seq": 512, "discrete": False,
+                 "input_dim": 5, "output_dim": 1}
+        lm5t, _ = host.language_model(cfg5t, synth.continuous_lm_weights(cfg5t, 19))
+        t5 = H.DeviceTrainer(lm5t, H.TrainingConfig(), 256, 511)
+        win = synth.random_walk_windows(33, 256, 512, 5)
+        tgt = np.ascontiguousarray(win[:, :, :1])  # next-step regression of the first feature
+        ms5t = t5.time_step_continuous(win, tgt, 1e-3, 3, 1)
+        core, qkv, o = mha_flops(256, 511, 256, 8)
+        fwd5 = 6 * (core + qkv + o + 4 * 256 * 511 * 256 * 1024) + 2 * 256 * 511 * 256 * (5 + 1)
+        out["c5_time_series_train_step"] = {
+            "ms": round(ms5t, 3), "windows_per_s": round(256 / (ms5t * 1e-3), 1),
+            "tflops": round(3 * fwd5 / (ms5t * 1e-3) / 1e12, 2),
+            "workload": "TrainBatchContinuous (MSE) on 256 windows of 512 steps, config-5 model"}
+        del t5, lm5t
+    if want("c3_decoder_stack_12_layers"):
+        log("[bench] extras: c3 12-layer decoder stack")
+        # c3: 12 post-LN decoder layers (MHA + FFN 4096 + 2 LayerNorms) on N(0,1) embeddings
+        cfg3 = {"dim": 1024, "heads": 16, "layers": 12, "ff": 4096, "max_seq": 4096, "discrete": False,
+                "input_dim": 1024, "output_dim": 1}
+        lm3, mgr = host.language_model(cfg3, synth.continuous_lm_weights(cfg3, 41, biased=False))
+        dev3 = H.DeviceLanguageModel(lm3, 4)
+        x3 = np.random.default_rng(6).standard_normal((4 * 4096, 1024), dtype=np.float32)
+        ms3 = dev3.time_layers(x3, 4, 4096, steps=3, warmup=1)
+        core, qkv, o = mha_flops(**C3)
+        ffn = 4 * 4 * 4096 * 1024 * 4096
+        fl3 = 12 * (core + qkv + o + ffn)
+        out["c3_decoder_stack_12_layers"] = {
+            "ms": round(ms3, 3), "tflops": round(fl3 / (ms3 * 1e-3) / 1e12, 2),
+            "frac_of_fp32_mfma_peak": round(fl3 / (ms3 * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
+            "tokens_per_s": round(4 * 4096 / (ms3 * 1e-3), 1), "gflop": round(fl3 / 1e9, 1)}
+        del dev3, lm3
+    if mgr is None and any(want(n) for n in EXTRA_LEGS[6:]):
+        mgr = H.HipAccelerationManager(0)
+    if want("c3_mha_one_sequence_dropin_host_arrays"):
+        # drop-in manager path on one c3 sequence: host arrays in and out (PCIe inclusive)
+        log("[bench] extras: drop-in manager (host arrays)")
+        D, Hh, L = 1024, 16, 4096
+        xs = np.random.default_rng(7).standard_normal((L, D), dtype=np.float32)
+        wq, wk, wv, wo = (synth.xavier_uniform(60 + i, D, D) for i in range(4))
+        bz = np.zeros(D, np.float32)
 
-    def mha_host():
-        q, k, v = mgr.ProjectQKV(xs, wq, bz, wk, bz, wv, bz)
-        mgr.ApplyRotaryPositionEmbeddingInPlace(q, Hh, 10000.0, False)
-        mgr.ApplyRotaryPositionEmbeddingInPlace(k, Hh, 10000.0, False)
-        a = mgr.ScaledDotProductAttention(q, k, v, Hh, None, True)
-        return mgr.ProjectOutputBatch(a, wo, bz, L, D)
+        def mha_host():
+            q, k, v = mgr.ProjectQKV(xs, wq, bz, wk, bz, wv, bz)
+            mgr.ApplyRotaryPositionEmbeddingInPlace(q, Hh, 10000.0, False)
+            mgr.ApplyRotaryPositionEmbeddingInPlace(k, Hh, 10000.0, False)
+            a = mgr.ScaledDotProductAttention(q, k, v, Hh, None, True)
+            return mgr.ProjectOutputBatch(a, wo, bz, L, D)
 
-    mha_host()
-    t0 = time.perf_counter()
-    for _ in range(3):
         mha_host()
-    dt = (time.perf_counter() - t0) / 3
-    core, qkv, o = mha_flops(1, L, D, Hh)
-    out["c3_mha_one_sequence_dropin_host_arrays"] = {
-        "ms": round(dt * 1e3, 3), "tflops": round((core + qkv + o) / dt / 1e12, 3),
-        "note": "HipAccelerationManager with float[,]-style host arrays: every call uploads its "
-                "activations and downloads its result (PCIe included); weights stay resident"}
-    # c5: time-series regression transformer, full forward, B 256 x L 512
-    log("[bench] extras: c5 time-series model")
-    cfg5 = {"dim": 256, "heads": 8, "layers": 6, "ff": 1024, "max_seq": 512, "discrete": False,
-            "input_dim": 5, "output_dim": 1}
-    lm5, _ = host.language_model(cfg5, synth.continuous_lm_weights(cfg5, 21), mgr)
-    dev5 = H.DeviceLanguageModel(lm5, 256)
-    x5 = synth.random_walk_windows(31, 256, 512, 5).reshape(256 * 512, 5)
-    ms5 = dev5.time_forward(x5, 256, 512, steps=5, warmup=2, continuous=True)
-    core, qkv, o = mha_flops(256, 512, 256, 8)
-    fl5 = 6 * (core + qkv + o + 4 * 256 * 512 * 256 * 1024) + 2 * 256 * 512 * 256 * (5 + 1)
-    out["c5_time_series_model"] = {"ms": round(ms5, 3), "tflops": round(fl5 / (ms5 * 1e-3) / 1e12, 2),
-                                   "windows_per_s": round(256 / (ms5 * 1e-3), 1)}
-    del dev5, lm5
-    # c1: README text model, forward of 4 x 64 tokens and greedy generation of 20 tokens
-    log("[bench] extras: c1 text model")
-    cfg1 = {"vocab": 200, "dim": 64, "heads": 4, "layers": 2, "ff": 128, "max_seq": 64}
-    lm1, _ = host.language_model(cfg1, synth.lm_weights(cfg1, 7), mgr)
-    dev1 = H.DeviceLanguageModel(lm1, 4)
-    ids = synth.token_ids(11, 4 * 64, 200).reshape(4, 64)
-    ms1 = dev1.time_forward(ids, 4, 64, steps=50, warmup=5)
-    dev1.GenerateGreedy(ids[:, :32], 20)
-    t0 = time.perf_counter()
-    for _ in range(5):
+        t0 = time.perf_counter()
+        for _ in range(3):
+            mha_host()
+        dt = (time.perf_counter() - t0) / 3
+        core, qkv, o = mha_flops(1, L, D, Hh)
+        out["c3_mha_one_sequence_dropin_host_arrays"] = {
+            "ms": round(dt * 1e3, 3), "tflops": round((core + qkv + o) / dt / 1e12, 3),
+            "note": "HipAccelerationManager with float[,]-style host arrays: every call uploads its "
+                    "activations and downloads its result (PCIe included); weights stay resident"}
+    if want("c5_time_series_model"):
+        # c5: time-series regression transformer, full forward, B 256 x L 512
+        log("[bench] extras: c5 time-series model")
+        cfg5 = {"dim": 256, "heads": 8, "layers": 6, "ff": 1024, "max_seq": 512, "discrete": False,
+                "input_dim": 5, "output_dim": 1}
+        lm5, _ = host.language_model(cfg5, synth.continuous_lm_weights(cfg5, 21), mgr)
+        dev5 = H.DeviceLanguageModel(lm5, 256)
+        x5 = synth.random_walk_windows(31, 256, 512, 5).reshape(256 * 512, 5)
+        ms5 = dev5.time_forward(x5, 256, 512, steps=5, warmup=2, continuous=True)
+        core, qkv, o = mha_flops(256, 512, 256, 8)
+        fl5 = 6 * (core + qkv + o + 4 * 256 * 512 * 256 * 1024) + 2 * 256 * 512 * 256 * (5 + 1)
+        out["c5_time_series_model"] = {"ms": round(ms5, 3), "tflops": round(fl5 / (ms5 * 1e-3) / 1e12, 2),
+                                       "windows_per_s": round(256 / (ms5 * 1e-3), 1)}
+        del dev5, lm5
+    if want("c1_text_model"):
+        # c1: README text model, forward of 4 x 64 tokens and greedy generation of 20 tokens
+        log("[bench] extras: c1 text model")
+        cfg1 = {"vocab": 200, "dim": 64, "heads": 4, "layers": 2, "ff": 128, "max_seq": 64}
+        lm1, _ = host.language_model(cfg1, synth.lm_weights(cfg1, 7), mgr)
+        dev1 = H.DeviceLanguageModel(lm1, 4)
+        ids = synth.token_ids(11, 4 * 64, 200).reshape(4, 64)
+        ms1 = dev1.time_forward(ids, 4, 64, steps=50, warmup=5)
         dev1.GenerateGreedy(ids[:, :32], 20)
-    gen_ms = (time.perf_counter() - t0) / 5 * 1e3
-    out["c1_text_model"] = {"forward_ms": round(ms1, 4), "forward_tokens_per_s": round(256 / (ms1 * 1e-3), 1),
-                            "generate_20_tokens_batch4_ms": round(gen_ms, 3),
-                            "generated_tokens_per_s": round(80 / (gen_ms * 1e-3), 1)}
+        t0 = time.perf_counter()
+        for _ in range(5):
+            dev1.GenerateGreedy(ids[:, :32], 20)
+        gen_ms = (time.perf_counter() - t0) / 5 * 1e3
+        out["c1_text_model"] = {"forward_ms": round(ms1, 4),
+                                "forward_tokens_per_s": round(256 / (ms1 * 1e-3), 1),
+                                "generate_20_tokens_batch4_ms": round(gen_ms, 3),
+                                "generated_tokens_per_s": round(80 / (gen_ms * 1e-3), 1)}
     return out
 
 
@@ -449,7 +472,13 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--only", default="",
+                    help="run only these comma-separated legs of " + ", ".join(EXTRA_LEGS) +
+                         " and print their figures (no headline metric line); for kernel traces")
     args = ap.parse_args()
+    only = {n for n in args.only.split(",") if n}
+    if only - set(EXTRA_LEGS):
+        ap.error(f"--only: unknown legs {sorted(only - set(EXTRA_LEGS))}")
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the attention path is single-device by design "
               "(batch x head shards need no exchange); run with --gpus 1", file=sys.stderr)
@@ -462,6 +491,10 @@ def main():
     log(f"[bench] device {info['name']} {info['arch']} CUs {info['compute_units']} "
         f"sclk {info['max_clock_mhz']} MHz")
     st = N.Stream()
+    if only:
+        # profiling mode: the selected legs alone, so a kernel trace holds only their launches
+        print(json.dumps({"other_configs": extras(N, st, only)}), flush=True)
+        return
 
     mha = bench_mha(N, st, args.steps, args.warmup)
     core, qkv, out = mha_flops(**C3)
@@ -510,7 +543,7 @@ def main():
                                       "algorithmic_per_launch": nbytes}}
     if not args.no_extras:
         log("[bench] extras")
-        res["other_configs"] = extras(N, st)
+        res["other_configs"] = extras(N, st, only)
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (multi-threaded restatement)")
         cb = cpu_baseline()

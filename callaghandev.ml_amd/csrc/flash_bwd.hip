@@ -20,9 +20,12 @@
 //      and dP^T = V dO^T put one query per lane, dS^T is consumed in place by
 //      dQ^T += K^T dS^T.
 // Every output element is written by one lane of one workgroup: no atomics,
-// and the result is the same on every run.  Head dims other than 32, 64 and
-// 128 (or unaligned strides) take flash_bwd_generic_kernel, which follows the
-// reference's per-row loops.
+// and the result is the same on every run.  Head dims below 128 other than
+// 32 and 64, or rows that are not 16-byte aligned, run the same kernels at the
+// next of 32 / 64 / 128 with zero-filled scalar loads (VEC false) and
+// predicated stores; zero columns of Q, K, V and dO leave S, dP and every
+// stored gradient column unchanged.  Head dims above 128 take
+// flash_bwd_generic_kernel, which follows the reference's per-row loops.
 #include "common.h"
 
 namespace cdml {
@@ -52,8 +55,9 @@ __device__ __forceinline__ constexpr int acc_row(int r) { return 8 * (r >> 2) + 
 // One ROWS x HD tile of a row-major matrix (rows [row0, row0 + ROWS) of the
 // head's column block), global -> registers -> LDS.  Each thread's offsets
 // inside a tile are fixed; rows past `nrows` are clamped to the last row
-// (their contributions are masked or never stored).
-template <int HD, int ROWS>
+// (their contributions are masked or never stored).  Without VEC, columns at
+// or past the head dim `hd` read as zero and the rest are scalar loads.
+template <int HD, int ROWS, bool VEC>
 struct RowStage {
   static constexpr int F4 = HD / 4;
   static constexpr int RPP = BW_THREADS / F4;
@@ -69,11 +73,20 @@ struct RowStage {
 #pragma unroll
     for (int i = 0; i < NV; ++i) off[i] = (uint32_t)((t / F4 + RPP * i) * ld + col);
   }
-  __device__ __forceinline__ void load(const float *__restrict__ base, int ld, int row0, int nrows) {
+  __device__ __forceinline__ void load(const float *__restrict__ base, int ld, int row0, int nrows,
+                                       int hd) {
     const float *tile = base + (size_t)row0 * ld;
     const uint32_t lim = (uint32_t)(min(nrows - 1 - row0, ROWS - 1) * ld) + col;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) r[i] = *reinterpret_cast<const vf4 *>(tile + min(off[i], lim));
+    for (int i = 0; i < NV; ++i) {
+      if constexpr (VEC) {
+        r[i] = *reinterpret_cast<const vf4 *>(tile + min(off[i], lim));
+      } else {
+        const float *p = tile + min(off[i], lim);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) r[i][c] = col + c < hd ? p[c] : 0.f;
+      }
+    }
   }
   __device__ __forceinline__ void store(float (*lds)[HD + 4]) const {
     const int t = threadIdx.x;
@@ -108,10 +121,24 @@ __global__ void __launch_bounds__(256) bwd_delta_kernel(const BwdArgs a) {
   }
 }
 
+// D for any head dim and stride: thread e owns (row e / heads, head e % heads).
+__global__ void __launch_bounds__(256) bwd_delta_scalar_kernel(const BwdArgs a) {
+  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (e >= (long long)a.batch * a.lq * a.heads) return;
+  const long long row = e / a.heads;
+  const int h = (int)(e % a.heads);
+  const float *x = a.dout + row * a.lddo + h * a.hd;
+  const float *y = a.o + row * a.ldo + h * a.hd;
+  float s = 0.f;
+  for (int d = 0; d < a.hd; ++d) s += x[d] * y[d];
+  const int b = (int)(row / a.lq), i = (int)(row % a.lq);
+  a.delta[((size_t)b * a.heads + h) * a.lq + i] = s;
+}
+
 // dK and dV.  Workgroup i takes (sequence, head) i % n_bh and key tile
 // i / n_bh: under the causal rule the first key tiles are seen by the most
 // queries, so the heaviest tiles go out first on every XCD.
-template <int HD, int BQ, bool CAUSAL, bool HAS_MASK>
+template <int HD, int BQ, bool CAUSAL, bool HAS_MASK, bool VEC>
 __global__ void __launch_bounds__(BW_THREADS, HD <= 64 ? 2 : 1) flash_bwd_dkdv_kernel(const BwdArgs a) {
   constexpr int NQB = BQ / 32;  // 32-query sub-blocks per tile
   constexpr int NDB = HD / 32;  // 32-wide head-dim blocks of dK^T / dV^T
@@ -131,7 +158,7 @@ __global__ void __launch_bounds__(BW_THREADS, HD <= 64 ? 2 : 1) flash_bwd_dkdv_k
   const int k0 = kt * BW_TILE;
   const int kw0 = k0 + wave * 32;  // first key of this wave
   const int key = kw0 + li;        // this lane's key
-  const int col0 = h * HD;
+  const int col0 = h * (VEC ? HD : a.hd);
 
   // B operands of S = Q K^T and dP = dO V^T: register 4u + r holds
   // K[key][8u + 4*hf + r] (and likewise V), fixed for the whole loop.
@@ -142,12 +169,21 @@ __global__ void __launch_bounds__(BW_THREADS, HD <= 64 ? 2 : 1) flash_bwd_dkdv_k
     const float *vrow = a.v + ((size_t)b * a.lk + kr) * a.ldv + col0;
 #pragma unroll
     for (int u = 0; u < NKG; ++u) {
-      const vf4 x = *reinterpret_cast<const vf4 *>(krow + 8 * u + 4 * hf);
-      const vf4 y = *reinterpret_cast<const vf4 *>(vrow + 8 * u + 4 * hf);
+      const int d = 8 * u + 4 * hf;
+      if constexpr (VEC) {
+        const vf4 x = *reinterpret_cast<const vf4 *>(krow + d);
+        const vf4 y = *reinterpret_cast<const vf4 *>(vrow + d);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        kreg[4 * u + r] = x[r];
-        vreg[4 * u + r] = y[r];
+        for (int r = 0; r < 4; ++r) {
+          kreg[4 * u + r] = x[r];
+          vreg[4 * u + r] = y[r];
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          kreg[4 * u + r] = d + r < a.hd ? krow[d + r] : 0.f;
+          vreg[4 * u + r] = d + r < a.hd ? vrow[d + r] : 0.f;
+        }
       }
     }
   }
@@ -166,13 +202,13 @@ __global__ void __launch_bounds__(BW_THREADS, HD <= 64 ? 2 : 1) flash_bwd_dkdv_k
     for (int r = 0; r < 16; ++r) dk[db][r] = dv[db][r] = 0.f;
   const floatx16 zero = {};
 
-  RowStage<HD, BQ> sq, sg;
+  RowStage<HD, BQ, VEC> sq, sg;
   sq.init(a.ldq);
   sg.init(a.lddo);
   float lreg = 0.f, dreg = 0.f;
   if (n_it > 0) {
-    sq.load(qbase, a.ldq, q_begin, a.lq);
-    sg.load(gbase, a.lddo, q_begin, a.lq);
+    sq.load(qbase, a.ldq, q_begin, a.lq, a.hd);
+    sg.load(gbase, a.lddo, q_begin, a.lq, a.hd);
     if (t < BQ) {
       const int qq = min(q_begin + t, a.lq - 1);
       lreg = lse[qq];
@@ -194,8 +230,8 @@ __global__ void __launch_bounds__(BW_THREADS, HD <= 64 ? 2 : 1) flash_bwd_dkdv_k
     // into the idle buffer (an unconditional stage keeps the registers out
     // of scratch memory).
     const int nxt = it + 1 < n_it ? qt0 + BQ : qt0;
-    sq.load(qbase, a.ldq, nxt, a.lq);
-    sg.load(gbase, a.lddo, nxt, a.lq);
+    sq.load(qbase, a.ldq, nxt, a.lq, a.hd);
+    sg.load(gbase, a.lddo, nxt, a.lq, a.hd);
     if (t < BQ) {
       const int qq = min(nxt + t, a.lq - 1);
       lreg = lse[qq];
@@ -295,15 +331,24 @@ __global__ void __launch_bounds__(BW_THREADS, HD <= 64 ? 2 : 1) flash_bwd_dkdv_k
           x[c] = dk[db][4 * g + c] * a.scale;
           y[c] = dv[db][4 * g + c];
         }
-        *reinterpret_cast<vf4 *>(dkrow + d) = x;
-        *reinterpret_cast<vf4 *>(dvrow + d) = y;
+        if constexpr (VEC) {
+          *reinterpret_cast<vf4 *>(dkrow + d) = x;
+          *reinterpret_cast<vf4 *>(dvrow + d) = y;
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (d + c < a.hd) {
+              dkrow[d + c] = x[c];
+              dvrow[d + c] = y[c];
+            }
+        }
       }
     }
   }
 }
 
 // dQ.  Query-tile major with the heaviest causal tiles first, as the forward.
-template <int HD, int BN, bool CAUSAL, bool HAS_MASK>
+template <int HD, int BN, bool CAUSAL, bool HAS_MASK, bool VEC>
 __global__ void __launch_bounds__(BW_THREADS, 2) flash_bwd_dq_kernel(const BwdArgs a) {
   constexpr int NKB = BN / 32;
   constexpr int NDB = HD / 32;
@@ -324,7 +369,7 @@ __global__ void __launch_bounds__(BW_THREADS, 2) flash_bwd_dq_kernel(const BwdAr
   const int qw0 = q0 + wave * 32;
   const int qi = qw0 + li;
   const int qc = min(qi, a.lq - 1);
-  const int col0 = h * HD;
+  const int col0 = h * (VEC ? HD : a.hd);
 
   // B operands of S^T = K Q^T and dP^T = V dO^T: register 4u + r holds
   // Q[qi][8u + 4*hf + r] (and likewise dO).
@@ -334,12 +379,21 @@ __global__ void __launch_bounds__(BW_THREADS, 2) flash_bwd_dq_kernel(const BwdAr
     const float *grow = a.dout + ((size_t)b * a.lq + qc) * a.lddo + col0;
 #pragma unroll
     for (int u = 0; u < NKG; ++u) {
-      const vf4 x = *reinterpret_cast<const vf4 *>(qrow + 8 * u + 4 * hf);
-      const vf4 y = *reinterpret_cast<const vf4 *>(grow + 8 * u + 4 * hf);
+      const int d = 8 * u + 4 * hf;
+      if constexpr (VEC) {
+        const vf4 x = *reinterpret_cast<const vf4 *>(qrow + d);
+        const vf4 y = *reinterpret_cast<const vf4 *>(grow + d);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        qreg[4 * u + r] = x[r];
-        greg[4 * u + r] = y[r];
+        for (int r = 0; r < 4; ++r) {
+          qreg[4 * u + r] = x[r];
+          greg[4 * u + r] = y[r];
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          qreg[4 * u + r] = d + r < a.hd ? qrow[d + r] : 0.f;
+          greg[4 * u + r] = d + r < a.hd ? grow[d + r] : 0.f;
+        }
       }
     }
   }
@@ -360,11 +414,11 @@ __global__ void __launch_bounds__(BW_THREADS, 2) flash_bwd_dq_kernel(const BwdAr
     for (int r = 0; r < 16; ++r) dq[db][r] = 0.f;
   const floatx16 zero = {};
 
-  RowStage<HD, BN> sk, sv;
+  RowStage<HD, BN, VEC> sk, sv;
   sk.init(a.ldk);
   sv.init(a.ldv);
-  sk.load(kbase, a.ldk, 0, a.lk);
-  sv.load(vbase, a.ldv, 0, a.lk);
+  sk.load(kbase, a.ldk, 0, a.lk, a.hd);
+  sv.load(vbase, a.ldv, 0, a.lk, a.hd);
   sk.store(Ks[0]);
   sv.store(Vs[0]);
   __syncthreads();
@@ -373,8 +427,8 @@ __global__ void __launch_bounds__(BW_THREADS, 2) flash_bwd_dq_kernel(const BwdAr
     const int cur = kt & 1;
     const int k0 = kt * BN;
     const int nxt = kt + 1 < n_kt ? k0 + BN : k0;
-    sk.load(kbase, a.ldk, nxt, a.lk);
-    sv.load(vbase, a.ldv, nxt, a.lk);
+    sk.load(kbase, a.ldk, nxt, a.lk, a.hd);
+    sv.load(vbase, a.ldv, nxt, a.lk, a.hd);
 
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
@@ -439,10 +493,17 @@ __global__ void __launch_bounds__(BW_THREADS, 2) flash_bwd_dq_kernel(const BwdAr
     for (int db = 0; db < NDB; ++db) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
+        const int d = db * 32 + 8 * g + 4 * hf;
         vf4 x;
 #pragma unroll
         for (int c = 0; c < 4; ++c) x[c] = dq[db][4 * g + c] * a.scale;
-        *reinterpret_cast<vf4 *>(dqrow + db * 32 + 8 * g + 4 * hf) = x;
+        if constexpr (VEC) {
+          *reinterpret_cast<vf4 *>(dqrow + d) = x;
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (d + c < a.hd) dqrow[d + c] = x[c];
+        }
       }
     }
   }
@@ -564,24 +625,30 @@ int zero_rows(float *p, long long rows, int cols, int ld, hipStream_t st) {
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
-template <int HD, int BQ, int BN, bool CAUSAL, bool HAS_MASK>
+template <int HD, int BQ, int BN, bool CAUSAL, bool HAS_MASK, bool VEC>
 void launch_bwd(BwdArgs &a, hipStream_t st) {
   const int n_bh = a.batch * a.heads;
   const int kt = (a.lk + BW_TILE - 1) / BW_TILE;
-  flash_bwd_dkdv_kernel<HD, BQ, CAUSAL, HAS_MASK><<<dim3(n_bh * kt), dim3(BW_THREADS), 0, st>>>(a);
+  flash_bwd_dkdv_kernel<HD, BQ, CAUSAL, HAS_MASK, VEC><<<dim3(n_bh * kt), dim3(BW_THREADS), 0, st>>>(a);
   a.n_tiles = (a.lq + BW_TILE - 1) / BW_TILE;
-  flash_bwd_dq_kernel<HD, BN, CAUSAL, HAS_MASK><<<dim3(n_bh * a.n_tiles), dim3(BW_THREADS), 0, st>>>(a);
+  flash_bwd_dq_kernel<HD, BN, CAUSAL, HAS_MASK, VEC><<<dim3(n_bh * a.n_tiles), dim3(BW_THREADS), 0, st>>>(a);
+}
+
+template <int HD, int BQ, int BN, bool VEC>
+void launch_bwd_mode(BwdArgs &a, bool causal, hipStream_t st) {
+  if (causal) {
+    if (a.mask) launch_bwd<HD, BQ, BN, true, true, VEC>(a, st);
+    else launch_bwd<HD, BQ, BN, true, false, VEC>(a, st);
+  } else {
+    if (a.mask) launch_bwd<HD, BQ, BN, false, true, VEC>(a, st);
+    else launch_bwd<HD, BQ, BN, false, false, VEC>(a, st);
+  }
 }
 
 template <int HD, int BQ, int BN>
-void launch_bwd_hd(BwdArgs &a, bool causal, hipStream_t st) {
-  if (causal) {
-    if (a.mask) launch_bwd<HD, BQ, BN, true, true>(a, st);
-    else launch_bwd<HD, BQ, BN, true, false>(a, st);
-  } else {
-    if (a.mask) launch_bwd<HD, BQ, BN, false, true>(a, st);
-    else launch_bwd<HD, BQ, BN, false, false>(a, st);
-  }
+void launch_bwd_hd(BwdArgs &a, bool causal, bool vec, hipStream_t st) {
+  if (vec) launch_bwd_mode<HD, BQ, BN, true>(a, causal, st);
+  else launch_bwd_mode<HD, BQ, BN, false>(a, causal, st);
 }
 
 }  // namespace
@@ -617,9 +684,9 @@ int sdpa_bwd_impl(const float *q, int ldq, const float *k, int ldk, const float 
   if (rc) return rc;
   if (saved) {
     need = sizeof(float) * (size_t)batch * num_heads * lq;
-    if (!lse_saved || ldo_saved < dim || ldo_saved % 4 || !aligned16(o_saved))
-      return fail(CDML_E_INVALID, "%s: saved output needs the row statistics, a 16-byte aligned "
-                  "output and a row stride of at least dim (a multiple of 4)", what);
+    if (!lse_saved || ldo_saved < dim)
+      return fail(CDML_E_INVALID, "%s: saved output needs the row statistics and a row stride of at "
+                  "least dim", what);
   }
   if (ldq < dim || ldk < dim || ldv < dim || lddo < dim || lddq < dim || lddk < dim || lddv < dim)
     return fail(CDML_E_INVALID, "%s: row stride smaller than dim", what);
@@ -686,14 +753,9 @@ int sdpa_bwd_impl(const float *q, int ldq, const float *k, int ldk, const float 
   }
 
   const int hd = a.hd;
-  const bool fast = (hd == 32 || hd == 64 || hd == 128) && ldq % 4 == 0 && ldk % 4 == 0 &&
-                    ldv % 4 == 0 && lddo % 4 == 0 && lddq % 4 == 0 && lddk % 4 == 0 &&
-                    lddv % 4 == 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
-                    aligned16(dout) && aligned16(dq) && aligned16(dk) && aligned16(dv);
-  if (!fast && saved)
-    return fail(CDML_E_INVALID, "%s: saved statistics need head dim 32, 64 or 128 and 16-byte aligned "
-                "rows; use cdml_sdpa_bwd", what);
-  if (!fast) {
+  if (hd > 128 && saved)
+    return fail(CDML_E_INVALID, "%s: saved statistics need head dim <= 128; use cdml_sdpa_bwd", what);
+  if (hd > 128) {
     const size_t smem = f * (2 * (size_t)hd + 8);
     if (smem > 64 * 1024) return fail(CDML_E_INVALID, "%s: head dim %d too large", what, hd);
     flash_bwd_generic_kernel<<<dim3((unsigned)bh), dim3(256), smem, st>>>(a, scratch, causal ? 1 : 0);
@@ -706,19 +768,26 @@ int sdpa_bwd_impl(const float *q, int ldq, const float *k, int ldk, const float 
     if (rc) return rc;
   }
   // 2. D = rowsum(dO * O)
-  {
+  const int hd_pad = hd <= 32 ? 32 : (hd <= 64 ? 64 : 128);
+  const bool vec = hd == hd_pad && ldq % 4 == 0 && ldk % 4 == 0 && ldv % 4 == 0 && lddo % 4 == 0 &&
+                   lddq % 4 == 0 && lddk % 4 == 0 && lddv % 4 == 0 && aligned16(q) && aligned16(k) &&
+                   aligned16(v) && aligned16(dout) && aligned16(dq) && aligned16(dk) && aligned16(dv);
+  if (vec && a.ldo % 4 == 0 && aligned16(a.o)) {
     const long long n = (long long)batch * lq * (dim / 4);
     const dim3 grid((unsigned)((n + 255) / 256));
     if (hd == 32) bwd_delta_kernel<32><<<grid, dim3(256), 0, st>>>(a);
     else if (hd == 64) bwd_delta_kernel<64><<<grid, dim3(256), 0, st>>>(a);
     else bwd_delta_kernel<128><<<grid, dim3(256), 0, st>>>(a);
-    rc = check_launch("bwd_delta_kernel");
-    if (rc) return rc;
+  } else {
+    const long long n = (long long)batch * lq * num_heads;
+    bwd_delta_scalar_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a);
   }
+  rc = check_launch("bwd_delta_kernel");
+  if (rc) return rc;
   // 3. dK, dV and 4. dQ
-  if (hd == 32) launch_bwd_hd<32, 64, 64>(a, causal != 0, st);
-  else if (hd == 64) launch_bwd_hd<64, 64, 32>(a, causal != 0, st);
-  else launch_bwd_hd<128, 32, 32>(a, causal != 0, st);
+  if (hd_pad == 32) launch_bwd_hd<32, 64, 64>(a, causal != 0, vec, st);
+  else if (hd_pad == 64) launch_bwd_hd<64, 64, 32>(a, causal != 0, vec, st);
+  else launch_bwd_hd<128, 32, 32>(a, causal != 0, vec, st);
   return check_launch("flash_bwd_dkdv_kernel / flash_bwd_dq_kernel");
 }
 

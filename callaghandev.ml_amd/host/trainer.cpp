@@ -211,8 +211,8 @@ DeviceTrainer::DeviceTrainer(const LanguageModel &model, const TrainingConfig &c
       Y.v1 = alloc(rows);
       Y.m2 = alloc(rows);
       Y.v2 = alloc(rows);
-      // the saved-statistics attention backward covers head dims 32, 64 and 128
-      Y.lse = (hd == 32 || hd == 64 || hd == 128) && D % 4 == 0 ? alloc((size_t)cap_b_ * H * cap_s_) : nullptr;
+      // the saved-statistics attention backward covers head dims up to 128
+      Y.lse = hd <= 128 ? alloc((size_t)cap_b_ * H * cap_s_) : nullptr;
       layers_.push_back(std::move(Y));
     }
     xfinal_ = alloc(rows * D);

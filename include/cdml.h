@@ -253,9 +253,10 @@ int cdml_sdpa_fwd_lse(const float *q, int ldq, const float *k, int ldk,
  * (the bool[,] overload).  scale is used as passed (the attention scores are
  * q.k * scale).  A query with no visible key contributes nothing.
  * `workspace`: device memory of cdml_sdpa_bwd_workspace_size() bytes.  Head
- * dims 32, 64 and 128 with 16-byte aligned rows run on fp32 MFMA (a forward
- * pass with row statistics, then dK/dV and dQ kernels, no atomics); other
- * shapes run a per-row kernel. */
+ * dims up to 128 run on fp32 MFMA (a forward pass with row statistics, then
+ * dK/dV and dQ kernels, no atomics; head dims other than 32, 64 and 128, and
+ * rows that are not 16-byte aligned, take zero-padded scalar loads); larger
+ * head dims run a per-row kernel. */
 int cdml_sdpa_bwd_workspace_size(int batch, int lq, int lk, int dim,
                                  int num_heads, size_t *bytes);
 int cdml_sdpa_bwd(const float *q, int ldq, const float *k, int ldk,
@@ -269,8 +270,8 @@ int cdml_sdpa_bwd(const float *q, int ldq, const float *k, int ldk,
  * row statistics lse, as cdml_sdpa_fwd_lse wrote them for the same q, k, v,
  * scale, causal flag and mask: no forward pass is repeated.  This is the
  * trainer's form (TransformerTrainer keeps the attention output in its
- * cache, AttentionCache.cs:9-38).  Head dims 32, 64 and 128 with 16-byte
- * aligned rows; workspace: batch * num_heads * lq floats. */
+ * cache, AttentionCache.cs:9-38).  Head dims up to 128; workspace:
+ * batch * num_heads * lq floats. */
 int cdml_sdpa_bwd_saved(const float *q, int ldq, const float *k, int ldk,
                         const float *v, int ldv, const float *o, int ldo,
                         const float *lse, const float *dout, int lddo,

@@ -291,8 +291,11 @@ def test_sdpa_bwd_reference_cases(case):
     (1, 257, 257, 128, 2, False, True),    # explicit mask
     (1, 200, 200, 128, 2, True, True),     # mask and decoder rule together
     (1, 300, 300, 256, 2, True, False),    # head dim 128
-    (3, 64, 64, 64, 4, True, False),       # segments (head dim 16: per-row kernel)
-    (1, 130, 130, 96, 2, True, False),     # head dim 48: per-row kernel
+    (3, 64, 64, 64, 4, True, False),       # segments, head dim 16 (zero-padded to 32)
+    (1, 130, 130, 96, 2, True, False),     # head dim 48 (zero-padded to 64)
+    (2, 70, 90, 36, 2, False, True),       # head dim 18: rows not 16-byte aligned, scalar loads
+    (1, 77, 77, 200, 2, True, False),      # head dim 100 (zero-padded to 128)
+    (1, 40, 40, 272, 2, True, False),      # head dim 136: per-row kernel
 ])
 def test_sdpa_bwd_shapes(b, lq, lk, dim, heads, causal, masked):
     hd = dim // heads
