@@ -374,6 +374,14 @@ PYBIND11_MODULE(_cdml_host, m) {
              return py::make_tuple(r.first, to_numpy(std::move(r.second)));
            },
            py::arg("logits"), py::arg("targets"), py::arg("targetStart"), py::arg("effectiveLen"))
+      .def("MSELossAndGradient",
+           [](HipAccelerationManager &a, py::object pred, py::object targets, int targetStart, int effectiveLen) {
+             auto P = mat(pred);
+             auto T = mat(targets);
+             auto r = a.MSELossAndGradient(P.view, T.view, targetStart, effectiveLen);
+             return py::make_tuple(r.first, to_numpy(std::move(r.second)));
+           },
+           py::arg("predictions"), py::arg("targets"), py::arg("targetStart"), py::arg("effectiveLen"))
       .def("AccumulateTokenEmbeddingGrad",
            [](HipAccelerationManager &a, py::object eg, py::object dx, py::object ids, int tokenStart, int seqLen,
               int dim) {
@@ -497,6 +505,24 @@ PYBIND11_MODULE(_cdml_host, m) {
     }
     return out;
   };
+  // Windows [len, F], regression targets [len, O] and class-id arrays; None
+  // entries become empty (the trainer skips those windows).
+  auto cont_from = [](const py::object &inputs, const py::object &reg, const py::object &cls,
+                      std::vector<Matrix> &xs, std::vector<Matrix> &rs, std::vector<std::vector<int>> &cs) {
+    auto mats = [](const py::object &o, std::vector<Matrix> &out) {
+      for (py::handle h : o) {
+        py::object ob = py::reinterpret_borrow<py::object>(h);
+        out.push_back(ob.is_none() ? Matrix() : from_numpy(ob));
+      }
+    };
+    mats(inputs, xs);
+    if (!reg.is_none()) mats(reg, rs);
+    if (!cls.is_none())
+      for (py::handle h : cls) {
+        py::object ob = py::reinterpret_borrow<py::object>(h);
+        cs.push_back(ob.is_none() ? std::vector<int>() : ids_from(ob));
+      }
+  };
   auto flat_dict = [](DeviceTrainer &t, const std::vector<float> &flat) {
     py::dict d;
     for (size_t i = 0; i < t.names().size(); ++i) {
@@ -525,27 +551,25 @@ PYBIND11_MODULE(_cdml_host, m) {
            },
            py::arg("sequences"), py::arg("seed") = 0)
       .def("TrainBatchContinuous",
-           [](DeviceTrainer &t, py::object inputs, py::object reg, py::object cls, float lr) {
+           [cont_from](DeviceTrainer &t, py::object inputs, py::object reg, py::object cls, float lr) {
              std::vector<Matrix> xs, rs;
              std::vector<std::vector<int>> cs;
-             auto mats = [](py::object o, std::vector<Matrix> &out) {
-               for (py::handle h : o) {
-                 py::object ob = py::reinterpret_borrow<py::object>(h);
-                 out.push_back(ob.is_none() ? Matrix() : from_numpy(ob));
-               }
-             };
-             mats(inputs, xs);
-             if (!reg.is_none()) mats(reg, rs);
-             if (!cls.is_none())
-               for (py::handle h : cls) {
-                 py::object ob = py::reinterpret_borrow<py::object>(h);
-                 cs.push_back(ob.is_none() ? std::vector<int>() : ids_from(ob));
-               }
+             cont_from(inputs, reg, cls, xs, rs, cs);
              py::gil_scoped_release nogil;
              return t.TrainBatchContinuous(xs, rs, cs, lr);
            },
            py::arg("inputs"), py::arg("regressionTargets") = py::none(), py::arg("classTargets") = py::none(),
            py::arg("learningRate") = 1e-4f)
+      .def("TrainContinuous",
+           [cont_from](DeviceTrainer &t, py::object inputs, py::object reg, py::object cls, uint64_t seed) {
+             std::vector<Matrix> xs, rs;
+             std::vector<std::vector<int>> cs;
+             cont_from(inputs, reg, cls, xs, rs, cs);
+             py::gil_scoped_release nogil;
+             return t.TrainContinuous(xs, rs, cs, seed);
+           },
+           py::arg("inputs"), py::arg("regressionTargets") = py::none(), py::arg("classTargets") = py::none(),
+           py::arg("seed") = 0)
       .def("CopyWeightsTo", &DeviceTrainer::CopyWeightsTo, py::arg("model"))
       .def("weights", [flat_dict](DeviceTrainer &t) { return flat_dict(t, t.weights_flat()); })
       .def("gradients", [flat_dict](DeviceTrainer &t) { return flat_dict(t, t.gradients_flat()); })

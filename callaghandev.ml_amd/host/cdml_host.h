@@ -216,6 +216,9 @@ class HipAccelerationManager {
   // IAccelerationManager.CrossEntropyLossAndGradient (:207, :209)
   std::pair<float, Matrix> CrossEntropyLossAndGradient(MatView logits, const std::vector<int> &targets,
                                                        int targetStart, int effectiveLen);
+  // IAccelerationManager.MSELossAndGradient (:212, :214)
+  std::pair<float, Matrix> MSELossAndGradient(MatView predictions, MatView targets, int targetStart,
+                                              int effectiveLen);
   // IAccelerationManager.AccumulateTokenEmbeddingGrad (:203, :205)
   void AccumulateTokenEmbeddingGrad(MatRef embeddingGrad, MatView dX, const std::vector<int> &tokenIds,
                                     int tokenStart, int seqLen, int embeddingDim);

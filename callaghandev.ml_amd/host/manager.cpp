@@ -899,6 +899,38 @@ std::pair<float, Matrix> HipAccelerationManager::CrossEntropyLossAndGradient(
   return {loss, std::move(dl)};
 }
 
+// ---- MSELossAndGradient: AccelerationCPU.cs:2442-2490 -------------------------
+std::pair<float, Matrix> HipAccelerationManager::MSELossAndGradient(MatView predictions, MatView targets,
+                                                                    int targetStart, int effectiveLen) {
+  if (predictions.null()) throw ArgumentNullException("predictions");
+  if (targets.null()) throw ArgumentNullException("targets");
+  const int rows = predictions.rows, o = predictions.cols;
+  if (targetStart < 0 || effectiveLen < 0 || (long long)targetStart + effectiveLen > targets.rows || targets.cols != o)
+    throw ArgumentException("Target shape must match predictions for the effective length and target offset.",
+                            "targets");
+  Matrix d(rows, o);
+  if (effectiveLen == 0 || o == 0) return {0.f, std::move(d)};
+  // the reference reads prediction rows i < effectiveLen without a check
+  if (effectiveLen > rows) throw ArgumentException("effectiveLen exceeds the prediction rows.", "effectiveLen");
+  std::lock_guard<std::mutex> lock(mu_);
+  ensure_ready();
+  const size_t pbytes = (size_t)rows * o * 4, tbytes = (size_t)effectiveLen * o * 4;
+  float *dp = static_cast<float *>(scratch(S_X, pbytes));
+  float *dt = static_cast<float *>(scratch(S_Q, tbytes));
+  float *dd = static_cast<float *>(scratch(S_K, pbytes));
+  float *dloss = static_cast<float *>(scratch(S_BIAS, 4));
+  void *dws = scratch(S_WS, (size_t)rows * 4);
+  upload(dp, predictions.data, pbytes);
+  upload(dt, targets.data + (size_t)targetStart * o, tbytes);
+  check(cdml_mse_loss(dp, o, dt, o, rows, o, effectiveLen, 1.0f, 1.0f, dloss, dd, o, dws, (size_t)rows * 4, stream_),
+        "cdml_mse_loss");
+  float loss = 0.f;
+  download(d.ptr(), dd, pbytes);
+  download(&loss, dloss, 4);
+  sync();
+  return {loss, std::move(d)};
+}
+
 // ---- AccumulateTokenEmbeddingGrad: AccelerationCPU.cs:2339-2370 ----------------
 void HipAccelerationManager::AccumulateTokenEmbeddingGrad(MatRef embeddingGrad, MatView dX,
                                                           const std::vector<int> &tokenIds, int tokenStart,

@@ -364,3 +364,73 @@ def test_device_trainer_continuous_matches_oracle(kind):
     named_w = named(ww)
     for k in ("input_proj", "layers.1.wq", "layers.0.ffn_w2", "out_proj"):
         parity(got[k], np.asarray(named_w[k]).reshape(-1), f"after 3 steps {k}")
+
+
+def _splitmix_order(n, seed, epochs):
+    """The epoch orders of DeviceTrainer.Train / TrainContinuous: a
+    Fisher-Yates shuffle per epoch driven by SplitMix64 from `seed`."""
+    m = (1 << 64) - 1
+    state = seed
+    orders = []
+    for _ in range(epochs):
+        order = list(range(n))
+        for i in range(n, 1, -1):
+            state = (state + 0x9E3779B97F4A7C15) & m
+            z = state
+            z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & m
+            z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & m
+            z ^= z >> 31
+            j = z % i
+            order[i - 1], order[j] = order[j], order[i - 1]
+        orders.append(order)
+    return orders
+
+
+@pytest.mark.parametrize("kind", ["tokens", "regression"])
+def test_device_trainer_epochs_equal_batch_steps(kind):
+    """Train / TrainContinuous (TransformerTrainer.cs:43-215): epochs of
+    shuffled batches of BatchSize with learning-rate decay give the same bits
+    as TrainBatch / TrainBatchContinuous called in that order; sequences
+    shorter than 2 are dropped first, and the result is the last epoch's mean
+    batch loss."""
+    from cdml import host
+    H = host.module()
+    epochs, bs, lr0, decay = 3, 3, 0.02, 0.8
+    if kind == "tokens":
+        cfg, w = C1, synth.lm_weights(C1, 31)
+        rng = np.random.default_rng(5)
+        data = [rng.integers(0, 200, int(n)).astype(np.int32) for n in (17, 17, 9, 1, 17, 12, 9, 17)]
+        valid = [d for d in data if d.shape[0] >= 2]
+    else:
+        cfg = dict(C5S, data_type=1)
+        w = synth.continuous_lm_weights(cfg, 33)
+        rng = np.random.default_rng(6)
+        data = [rng.uniform(0, 1, (int(n), 5)).astype(np.float32) for n in (21, 21, 13, 1, 21, 8, 13)]
+        targets = [rng.standard_normal((x.shape[0], 3)).astype(np.float32) for x in data]
+        keep = [i for i, d in enumerate(data) if d.shape[0] >= 2]
+        valid, vt = [data[i] for i in keep], [targets[i] for i in keep]
+    trainers = []
+    for _ in range(2):
+        lm, _ = host.language_model(cfg, w)
+        tc = H.TrainingConfig()
+        tc.BatchSize, tc.Epochs, tc.LearningRate = bs, epochs, lr0
+        tc.UseLearningRateDecay, tc.LearningRateDecay = True, decay
+        trainers.append(H.DeviceTrainer(lm, tc, 4, 32))
+    a, b = trainers
+    got = a.Train(data, seed=9) if kind == "tokens" else a.TrainContinuous(data, regressionTargets=targets, seed=9)
+    lr = np.float32(lr0)
+    for order in _splitmix_order(len(valid), 9, epochs):
+        losses = []
+        for i in range(0, len(order), bs):
+            idx = order[i:i + bs]
+            if kind == "tokens":
+                losses.append(b.TrainBatch([valid[j] for j in idx], float(lr)))
+            else:
+                losses.append(b.TrainBatchContinuous([valid[j] for j in idx], regressionTargets=[vt[j] for j in idx],
+                                                     learningRate=float(lr)))
+        lr = np.float32(lr * np.float32(decay))
+    want = float(np.float32(sum(np.float32(x) for x in losses)) / np.float32(len(losses)))
+    assert got == pytest.approx(want, rel=1e-6)
+    wa, wb = a.weights(), b.weights()
+    for k in wa:
+        assert np.array_equal(wa[k], wb[k]), k

@@ -201,6 +201,14 @@ def test_training_method_argument_rules(mgr):
         mgr.CrossEntropyLossAndGradient(M(3, 4, 1), np.array([0, 4, 1], np.int32), 0, 3)
     loss, dl = mgr.CrossEntropyLossAndGradient(M(3, 4, 1), np.array([0, 1], np.int32), 0, 0)
     assert loss == 0 and dl.shape == (3, 4) and not dl.any()  # no device work
+    with pytest.raises(H.ArgumentException, match="Target shape"):
+        mgr.MSELossAndGradient(M(3, 2, 1), M(3, 3, 2), 0, 2)
+    with pytest.raises(H.ArgumentException, match="Target shape"):
+        mgr.MSELossAndGradient(M(3, 2, 1), M(3, 2, 2), 2, 2)
+    with pytest.raises(H.ArgumentException, match="effectiveLen exceeds"):
+        mgr.MSELossAndGradient(M(3, 2, 1), M(5, 2, 2), 0, 4)
+    loss, dp = mgr.MSELossAndGradient(M(3, 2, 1), M(3, 2, 2), 1, 0)
+    assert loss == 0 and dp.shape == (3, 2) and not dp.any()  # no device work
     with pytest.raises(H.ArgumentOutOfRangeException, match="tokenStart"):
         mgr.AccumulateTokenEmbeddingGrad(z((5, 2), np.float32), M(3, 2, 1), np.array([0, 1], np.int32), 0, 3, 2)
     with pytest.raises(H.ArgumentOutOfRangeException, match="Token out of range"):

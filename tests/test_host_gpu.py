@@ -193,7 +193,7 @@ def test_manager_projection_backward(mgr):
 
 def test_manager_training_methods(mgr):
     """MatrixMultiply / MatrixMultiplyTranspose, ResidualLayerNormForward,
-    LayerNormBackward, CrossEntropyLossAndGradient and
+    LayerNormBackward, CrossEntropyLossAndGradient, MSELossAndGradient and
     AccumulateTokenEmbeddingGrad against the oracle (MatrixMultiply against
     float64 matrix algebra, the reference's textbook product)."""
     A, B = synth.normal(1, (130, 257)), synth.normal(2, (257, 66))
@@ -217,6 +217,12 @@ def test_manager_training_methods(mgr):
     wl, wd = O.cross_entropy(logits, t, 10, target_start=3)
     assert abs(loss - wl) <= 1e-5 + 1e-5 * abs(wl)
     parity(dl, wd, "CrossEntropyLossAndGradient")
+    pred, tgt = synth.normal(11, (12, 3)), synth.normal(12, (20, 3))
+    loss, dp = mgr.MSELossAndGradient(pred, tgt, 4, 9)
+    wl, wd = O.mse_loss(pred, tgt, 9, target_start=4)
+    assert abs(loss - wl) <= 1e-5 + 1e-5 * abs(wl)
+    parity(dp, wd, "MSELossAndGradient")
+    assert not dp[9:].any()
     eg = synth.normal(9, (50, 16))
     dx = synth.normal(10, (30, 16))
     ids = (np.arange(40) * 7 % 50).astype(np.int32)
