@@ -41,6 +41,8 @@ struct BwdArgs {
   const float *o;      // forward output [batch * lq][dim] (row stride ldo)
   const float *lse;    // [batch * heads][lq]
   float *delta;        // [batch * heads][lq]
+  float *ds;           // stored dS blocks (causal, lq == lk) or NULL
+  long long ds_bh;     // floats of ds per (sequence, head)
   const uint8_t *mask; // [lq][lk] or NULL
   int ldq, ldk, ldv, lddo, lddq, lddk, lddv, ldo;
   int batch, lq, lk, dim, heads, hd;
@@ -138,7 +140,14 @@ __global__ void __launch_bounds__(256) bwd_delta_scalar_kernel(const BwdArgs a) 
 // dK and dV.  Workgroup i takes (sequence, head) i % n_bh and key tile
 // i / n_bh: under the causal rule the first key tiles are seen by the most
 // queries, so the heaviest tiles go out first on every XCD.
-template <int HD, int BQ, bool CAUSAL, bool HAS_MASK, bool VEC>
+//
+// With STORE_DS (causal, lq == lk) the kernel also writes every dS sub-block
+// it forms, for flash_bwd_dq_ds_kernel: block (query block i, key block j),
+// j <= i, holds 32 x 32 floats at ds + bh * ds_bh + (i (i + 1) / 2 + j) * 1024,
+// query row r of the block at [32 r, 32 r + 32) with key 2s + c at 16 c + s,
+// which is the A operand order of the dQ product (16 contiguous floats per
+// lane).
+template <int HD, int BQ, bool CAUSAL, bool HAS_MASK, bool VEC, bool STORE_DS>
 __global__ void __launch_bounds__(BW_THREADS, HD <= 64 ? 2 : 1) flash_bwd_dkdv_kernel(const BwdArgs a) {
   constexpr int NQB = BQ / 32;  // 32-query sub-blocks per tile
   constexpr int NDB = HD / 32;  // 32-wide head-dim blocks of dK^T / dV^T
@@ -290,6 +299,13 @@ __global__ void __launch_bounds__(BW_THREADS, HD <= 64 ? 2 : 1) flash_bwd_dkdv_k
           s[r] = p;
           dp[r] = p * (dp[r] - d4[c]);
         }
+      }
+      if constexpr (STORE_DS) {
+        const int qi = qb0 >> 5, kj = kw0 >> 5;
+        float *blk = a.ds + (size_t)bh * a.ds_bh + ((size_t)qi * (qi + 1) / 2 + kj) * 1024 +
+                     4 * hf * 32 + (li & 1) * 16 + (li >> 1);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) blk[acc_row(r) * 32] = dp[r];
       }
 
       // dV^T += dO^T P and dK^T += Q^T dS: MFMA step st pairs query rows
@@ -509,6 +525,94 @@ __global__ void __launch_bounds__(BW_THREADS, 2) flash_bwd_dq_kernel(const BwdAr
   }
 }
 
+// dQ from the dS blocks that flash_bwd_dkdv_kernel stored (causal, lq == lk,
+// 16-byte aligned rows): dQ = scale dS K, one product instead of recomputing
+// S and dP.  Query-tile major with the heaviest tiles first, as the forward.
+// Wave w owns query block i = q0 / 32 + w; for its key blocks j <= i the A
+// operand (dS[q][2s + c] in lane (q, c) for step s) is 16 contiguous floats
+// per lane, loaded one block ahead, and K streams through double-buffered LDS
+// as the B operand.  Lane d of the accumulator holds dQ[q][d] for the 16
+// query rows acc_row(r) + 4 c.
+template <int HD, int BN>
+__global__ void __launch_bounds__(BW_THREADS, 2) flash_bwd_dq_ds_kernel(const BwdArgs a) {
+  constexpr int NKB = BN / 32;
+  constexpr int NDB = HD / 32;
+  __shared__ __attribute__((aligned(16))) float Ks[2][BN][HD + 4];
+
+  const int n_bh = a.batch * a.heads;
+  const int bh = blockIdx.x % n_bh;
+  const int qt = a.n_tiles - 1 - (int)(blockIdx.x / n_bh);
+  const int b = bh / a.heads, h = bh % a.heads;
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int li = lane & 31, hf = lane >> 5;
+  const int q0 = qt * BW_TILE;
+  const int qw0 = q0 + wave * 32;
+  const int qi = qw0 >> 5;                    // this wave's query block
+  const int last = qw0 < a.lq ? qi : -1;      // its last key block (none past the end)
+  const int col0 = h * HD;
+  const float *__restrict__ kbase = a.k + (size_t)b * a.lk * a.ldk + col0;
+  const float *__restrict__ dsw = a.ds + (size_t)bh * a.ds_bh + (size_t)qi * (qi + 1) / 2 * 1024 + li * 32 + hf * 16;
+
+  floatx16 dq[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[db][r] = 0.f;
+
+  const int kend = min(q0 + BW_TILE, a.lk);
+  const int n_kt = (kend + BN - 1) / BN;
+  RowStage<HD, BN, true> sk;
+  sk.init(a.ldk);
+  sk.load(kbase, a.ldk, 0, a.lk, HD);
+  sk.store(Ks[0]);
+  vf4 cur[4], nxt[4];
+  if (last >= 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cur[i] = *reinterpret_cast<const vf4 *>(dsw + 4 * i);
+  }
+  __syncthreads();
+
+  for (int kt = 0; kt < n_kt; ++kt) {
+    const int buf = kt & 1;
+    const int k0 = kt * BN;
+    sk.load(kbase, a.ldk, kt + 1 < n_kt ? k0 + BN : k0, a.lk, HD);
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const int j = kt * NKB + kb;  // key block
+      if (j > last) continue;
+      if (j + 1 <= last) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) nxt[i] = *reinterpret_cast<const vf4 *>(dsw + (size_t)(j + 1) * 1024 + 4 * i);
+      }
+      const float(*krow)[HD + 4] = &Ks[buf][kb * 32];
+#pragma unroll
+      for (int st = 0; st < 16; ++st) {
+        const float av = cur[st >> 2][st & 3];
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) dq[db] = mfma32x32x2(av, krow[2 * st + hf][db * 32 + li], dq[db]);
+      }
+      if (j + 1 <= last) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cur[i] = nxt[i];
+      }
+    }
+    sk.store(Ks[buf ^ 1]);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int q = qw0 + acc_row(r) + 4 * hf;
+    if (q < a.lq) {
+      float *dqrow = a.dq + ((size_t)b * a.lq + q) * a.lddq + col0;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) dqrow[db * 32 + li] = dq[db][r] * a.scale;
+    }
+  }
+}
+
 // Any head dim, any strides: one workgroup per (sequence, head) walks the
 // queries in order, as AccelerationCPU.cs:1092-1268 does per head, with the
 // keys spread over the threads.  scratch holds two floats per key.
@@ -629,8 +733,15 @@ template <int HD, int BQ, int BN, bool CAUSAL, bool HAS_MASK, bool VEC>
 void launch_bwd(BwdArgs &a, hipStream_t st) {
   const int n_bh = a.batch * a.heads;
   const int kt = (a.lk + BW_TILE - 1) / BW_TILE;
-  flash_bwd_dkdv_kernel<HD, BQ, CAUSAL, HAS_MASK, VEC><<<dim3(n_bh * kt), dim3(BW_THREADS), 0, st>>>(a);
   a.n_tiles = (a.lq + BW_TILE - 1) / BW_TILE;
+  if constexpr (CAUSAL && !HAS_MASK && VEC && HD <= 64) {
+    if (a.ds) {  // dQ from the stored dS blocks
+      flash_bwd_dkdv_kernel<HD, BQ, true, false, true, true><<<dim3(n_bh * kt), dim3(BW_THREADS), 0, st>>>(a);
+      flash_bwd_dq_ds_kernel<HD, 64><<<dim3(n_bh * a.n_tiles), dim3(BW_THREADS), 0, st>>>(a);
+      return;
+    }
+  }
+  flash_bwd_dkdv_kernel<HD, BQ, CAUSAL, HAS_MASK, VEC, false><<<dim3(n_bh * kt), dim3(BW_THREADS), 0, st>>>(a);
   flash_bwd_dq_kernel<HD, BN, CAUSAL, HAS_MASK, VEC><<<dim3(n_bh * a.n_tiles), dim3(BW_THREADS), 0, st>>>(a);
 }
 
@@ -664,6 +775,32 @@ extern "C" int cdml_sdpa_bwd_workspace_size(int batch, int lq, int lk, int dim, 
   const size_t f = sizeof(float), bh = (size_t)batch * num_heads;
   // O | lse | D | two floats per key for the generic kernel
   *bytes = align256(f * (size_t)batch * lq * dim) + 2 * align256(f * bh * lq) + align256(f * 2 * bh * lk);
+  return CDML_OK;
+}
+
+namespace cdml {
+namespace {
+
+// Bytes of the stored-dS workspace of cdml_sdpa_bwd_saved (after D), or 0 when
+// the shape does not take that path: causal, lq == lk, head dim 32 or 64.
+size_t ds_bytes(int batch, int lq, int lk, int dim, int num_heads, bool causal) {
+  const int hd = dim / num_heads;
+  if (!causal || lq != lk || (hd != 32 && hd != 64) || lq == 0) return 0;
+  const size_t nb = ((size_t)lq + 31) / 32;
+  return (size_t)batch * num_heads * (nb * (nb + 1) / 2) * 1024 * sizeof(float);
+}
+
+}  // namespace
+}  // namespace cdml
+
+extern "C" int cdml_sdpa_bwd_saved_workspace_size(int batch, int lq, int lk, int dim, int num_heads,
+                                                  int causal, size_t *bytes) {
+  if (!bytes) return fail(CDML_E_INVALID, "cdml_sdpa_bwd_saved_workspace_size: bytes is NULL");
+  if (batch < 0 || lq < 0 || lk < 0 || dim <= 0 || num_heads <= 0 || dim % num_heads)
+    return fail(CDML_E_INVALID, "cdml_sdpa_bwd_saved_workspace_size: bad size");
+  const size_t d = sizeof(float) * (size_t)batch * num_heads * lq;
+  const size_t extra = ds_bytes(batch, lq, lk, dim, num_heads, causal != 0);
+  *bytes = extra ? align256(d) + extra : d;
   return CDML_OK;
 }
 
@@ -784,7 +921,16 @@ int sdpa_bwd_impl(const float *q, int ldq, const float *k, int ldk, const float 
   }
   rc = check_launch("bwd_delta_kernel");
   if (rc) return rc;
-  // 3. dK, dV and 4. dQ
+  // 3. dK, dV and 4. dQ; from saved statistics with room for the dS blocks,
+  // dQ is one product over them
+  if (saved && vec && !mask) {
+    const size_t extra = ds_bytes(batch, lq, lk, dim, num_heads, causal != 0);
+    const size_t off = align256(sizeof(float) * bh * lq);
+    if (extra && workspace_bytes >= off + extra) {
+      a.ds = reinterpret_cast<float *>(ws + off);
+      a.ds_bh = (long long)(extra / sizeof(float) / bh);
+    }
+  }
   if (hd_pad == 32) launch_bwd_hd<32, 64, 64>(a, causal != 0, vec, st);
   else if (hd_pad == 64) launch_bwd_hd<64, 64, 32>(a, causal != 0, vec, st);
   else launch_bwd_hd<128, 32, 32>(a, causal != 0, vec, st);

@@ -238,6 +238,10 @@ DeviceTrainer::DeviceTrainer(const LanguageModel &model, const TrainingConfig &c
     const int R = (int)rows;
     check(cdml_sdpa_bwd_workspace_size(cap_b_, cap_s_, cap_s_, D, H, &n), "workspace size");
     need = std::max(need, n);
+    // room for the stored dS blocks (2 * seq^2 bytes per sequence and head),
+    // so that the attention backward forms dQ as one product
+    check(cdml_sdpa_bwd_saved_workspace_size(cap_b_, cap_s_, cap_s_, D, H, 1, &n), "workspace size");
+    need = std::max(need, n);
     check(cdml_backprop_qkv_workspace_size(R, D, D, &n), "workspace size");
     need = std::max(need, n);
     check(cdml_linear_backward_workspace_size(R, D, V, &n), "workspace size");

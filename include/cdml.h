@@ -270,8 +270,15 @@ int cdml_sdpa_bwd(const float *q, int ldq, const float *k, int ldk,
  * row statistics lse, as cdml_sdpa_fwd_lse wrote them for the same q, k, v,
  * scale, causal flag and mask: no forward pass is repeated.  This is the
  * trainer's form (TransformerTrainer keeps the attention output in its
- * cache, AttentionCache.cs:9-38).  Head dims up to 128; workspace:
- * batch * num_heads * lq floats. */
+ * cache, AttentionCache.cs:9-38).  Head dims up to 128; workspace: at least
+ * batch * num_heads * lq floats.  With cdml_sdpa_bwd_saved_workspace_size()
+ * bytes (causal without a mask, lq == lk, head dim 32 or 64, 16-byte aligned
+ * rows) the dK/dV pass also stores dS, 2 * lq^2 bytes per (sequence, head),
+ * and dQ becomes one product over it instead of recomputing the scores; the
+ * result meets the same bar but need not match the smaller workspace's bits. */
+int cdml_sdpa_bwd_saved_workspace_size(int batch, int lq, int lk, int dim,
+                                       int num_heads, int causal,
+                                       size_t *bytes);
 int cdml_sdpa_bwd_saved(const float *q, int ldq, const float *k, int ldk,
                         const float *v, int ldv, const float *o, int ldo,
                         const float *lse, const float *dout, int lddo,

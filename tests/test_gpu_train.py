@@ -306,6 +306,57 @@ def test_sdpa_bwd_from_saved_statistics(batch, L, dim, heads):
                                  outs[1][0].ptr, dim, outs[1][1].ptr, dim, outs[1][2].ptr, dim, batch, L, L, dim,
                                  heads, scale, 1, None, bws.ptr, small - 4, s)
     assert rc == -1
+    # with room for the stored dS blocks (head dims 32 and 64): dK and dV are
+    # the same bits, dQ is one product over the stored blocks
+    big = C.c_size_t(0)
+    N.check(lib.cdml_sdpa_bwd_saved_workspace_size(batch, L, L, dim, heads, 1, C.byref(big)))
+    hd = dim // heads
+    assert (big.value > small) == (hd in (32, 64))
+    bbig = N.DeviceBuffer(big.value)
+    out3 = [N.DeviceBuffer(rows * dim * 4) for _ in range(3)]
+    N.check(lib.cdml_sdpa_bwd_saved(bq.ptr, dim, bk.ptr, dim, bv.ptr, dim, o2.ptr, dim, lse.ptr, bg.ptr, dim,
+                                    out3[0].ptr, dim, out3[1].ptr, dim, out3[2].ptr, dim, batch, L, L,
+                                    dim, heads, scale, 1, None, bbig.ptr, big.value, s))
+    for a, b, n in zip(outs[1][1:], out3[1:], "KV"):
+        assert np.array_equal(G.down(a, (rows, dim)), G.down(b, (rows, dim))), f"stored-dS d{n}"
+    dq3 = G.down(out3[0], (rows, dim))
+    for sq in range(batch):
+        r = slice(sq * L, (sq + 1) * L)
+        want = O.mha_backward(q[r], k[r], v[r], g[r], heads, scale, use_decoder_mask=True)
+        parity(dq3[r], want[0], f"stored-dS dQ, sequence {sq}")
+
+
+def test_sdpa_bwd_stored_scores_c3_shape():
+    """The c3 shape (4 x 4096, 16 heads of 64, causal) through
+    cdml_sdpa_fwd_lse + cdml_sdpa_bwd_saved with the stored-dS workspace
+    (2.1 GB of dS blocks); two (sequence, head) pairs against float64."""
+    import ctypes as C
+    from cdml import native as N
+    from test_gpu_parity import _attention_bwd64
+    B, L, D, H = 4, 4096, 1024, 16
+    hd = D // H
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    q, k, v, g = (synth.normal(20 + i, (B * L, D)) for i in range(4))
+    bq, bk, bv, bg = (G.up(a) for a in (q, k, v, g))
+    o, lse = N.DeviceBuffer(B * L * D * 4), N.DeviceBuffer(B * H * L * 4)
+    s = G.stream().handle
+    lib = N.lib()
+    N.check(lib.cdml_sdpa_fwd_lse(bq.ptr, D, bk.ptr, D, bv.ptr, D, o.ptr, D, lse.ptr, B, L, L, D, H, scale, 1,
+                                  None, s))
+    ws = C.c_size_t(0)
+    N.check(lib.cdml_sdpa_bwd_saved_workspace_size(B, L, L, D, H, 1, C.byref(ws)))
+    assert ws.value > 2 * L * L * B * H
+    bws = N.DeviceBuffer(ws.value)
+    outs = [N.DeviceBuffer(B * L * D * 4) for _ in range(3)]
+    N.check(lib.cdml_sdpa_bwd_saved(bq.ptr, D, bk.ptr, D, bv.ptr, D, o.ptr, D, lse.ptr, bg.ptr, D, outs[0].ptr, D,
+                                    outs[1].ptr, D, outs[2].ptr, D, B, L, L, D, H, scale, 1, None, bws.ptr,
+                                    ws.value, s))
+    dq, dk, dv = (G.down(x, (B * L, D)) for x in outs)
+    for b, h in [(0, 0), (3, 13)]:
+        rows, cols = slice(b * L, (b + 1) * L), slice(h * hd, (h + 1) * hd)
+        want = _attention_bwd64(*(t[rows, cols].astype(np.float64) for t in (q, k, v, g)), scale)
+        for a, e, n in zip((dq, dk, dv), want, "QKV"):
+            parity(a[rows, cols], e, f"c3 stored-dS (b {b}, h {h}) d{n}")
 
 
 C5S = {"dim": 64, "heads": 2, "layers": 2, "ff": 128, "max_seq": 64, "discrete": False, "input_dim": 5,
