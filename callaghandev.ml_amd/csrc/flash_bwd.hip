@@ -530,7 +530,7 @@ __global__ void __launch_bounds__(BW_THREADS, 2) flash_bwd_dq_kernel(const BwdAr
 // S and dP.  Query-tile major with the heaviest tiles first, as the forward.
 // Wave w owns query block i = q0 / 32 + w; for its key blocks j <= i the A
 // operand (dS[q][2s + c] in lane (q, c) for step s) is 16 contiguous floats
-// per lane, loaded one block ahead, and K streams through double-buffered LDS
+// per lane, loaded two blocks ahead, and K streams through double-buffered LDS
 // as the B operand.  Lane d of the accumulator holds dQ[q][d] for the 16
 // query rows acc_row(r) + 4 c.
 template <int HD, int BN>
@@ -567,10 +567,15 @@ __global__ void __launch_bounds__(BW_THREADS, 2) flash_bwd_dq_ds_kernel(const Bw
   sk.init(a.ldk);
   sk.load(kbase, a.ldk, 0, a.lk, HD);
   sk.store(Ks[0]);
-  vf4 cur[4], nxt[4];
+  // dS operands two blocks ahead: cur (block j), n1 (j + 1), n2 (j + 2)
+  vf4 cur[4], n1[4], n2[4];
   if (last >= 0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) cur[i] = *reinterpret_cast<const vf4 *>(dsw + 4 * i);
+  }
+  if (last >= 1) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) n1[i] = *reinterpret_cast<const vf4 *>(dsw + 1024 + 4 * i);
   }
   __syncthreads();
 
@@ -582,9 +587,9 @@ __global__ void __launch_bounds__(BW_THREADS, 2) flash_bwd_dq_ds_kernel(const Bw
     for (int kb = 0; kb < NKB; ++kb) {
       const int j = kt * NKB + kb;  // key block
       if (j > last) continue;
-      if (j + 1 <= last) {
+      if (j + 2 <= last) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) nxt[i] = *reinterpret_cast<const vf4 *>(dsw + (size_t)(j + 1) * 1024 + 4 * i);
+        for (int i = 0; i < 4; ++i) n2[i] = *reinterpret_cast<const vf4 *>(dsw + (size_t)(j + 2) * 1024 + 4 * i);
       }
       const float(*krow)[HD + 4] = &Ks[buf][kb * 32];
 #pragma unroll
@@ -593,9 +598,10 @@ __global__ void __launch_bounds__(BW_THREADS, 2) flash_bwd_dq_ds_kernel(const Bw
 #pragma unroll
         for (int db = 0; db < NDB; ++db) dq[db] = mfma32x32x2(av, krow[2 * st + hf][db * 32 + li], dq[db]);
       }
-      if (j + 1 <= last) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) cur[i] = nxt[i];
+      for (int i = 0; i < 4; ++i) {
+        cur[i] = n1[i];
+        n1[i] = n2[i];
       }
     }
     sk.store(Ks[buf ^ 1]);

@@ -160,6 +160,11 @@ def main():
     f["mha128_nomask"] = t_attention(qg, kg, vg, 4, 1.0 / np.sqrt(16.0))
     f["mha128_causal"] = t_attention(qg, kg, vg, 4, 1.0 / np.sqrt(16.0), causal=True)
 
+    # One c2-sized head slice: config 2 (B 16 x L 1024, D 512, 8 heads) is 128
+    # independent causal (sequence, head) problems of L 1024 x d_h 64.
+    qh, kh, vh = (synth.normal(900 + i, (1024, 64)) for i in range(3))
+    f["c2_head_causal"] = t_attention(qh, kh, vh, 1, 1.0 / 8.0, causal=True)
+
     # ProjectQKV (:461-500) and the GPU-size case (:1203-1218).
     x = M(6, 5, 124)
     f["qkv_small_q"] = t_linear(x, M(8, 5, 125), Vec(8, 128))

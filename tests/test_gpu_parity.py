@@ -378,6 +378,19 @@ def test_mha_forward_reference_cases(ops_golden):
     parity(G.sdpa(qg, kg, vg, 4, causal=True), O.sdpa(qg, kg, vg, 4, causal=True), "SDPA 128 causal")
 
 
+def test_sdpa_c2_batch_head_slice_golden(ops_golden):
+    """Config 2 (16 sequences x 1024, D 512, 8 heads, causal) in one launch;
+    the golden head slice (float64 textbook attention) sits at sequence 5,
+    head 3, among N(0,1) data."""
+    B, L, D, H = 16, 1024, 512, 8
+    q, k, v = (synth.normal(40 + i, (B * L, D)) for i in range(3))
+    rows, cols = slice(5 * L, 6 * L), slice(3 * 64, 4 * 64)
+    for i, t in enumerate((q, k, v)):
+        t[rows, cols] = synth.normal(900 + i, (L, 64))
+    got = G.sdpa(q, k, v, H, causal=True, batch=B)
+    parity(got[rows, cols], ops_golden["c2_head_causal"], "c2 head slice vs float64 golden")
+
+
 @pytest.mark.parametrize("L,D,H", [(64, 64, 4), (1, 64, 4), (33, 96, 3), (130, 512, 8), (257, 256, 8),
                                    (300, 128, 1), (200, 160, 1), (77, 80, 5), (96, 1024, 64)])
 def test_sdpa_causal_shapes(L, D, H):

@@ -116,6 +116,8 @@ def test_mha_golden(ops_golden):
     qg, kg, vg = M(128, 64, 110), M(128, 64, 111), M(128, 64, 112)
     close(O.mha_forward(qg, kg, vg, 4, 0.25), g["mha128_nomask"], what="mha128")
     close(O.sdpa(qg, kg, vg, 4, causal=True), g["mha128_causal"], what="sdpa128 causal")
+    qh, kh, vh = (synth.normal(900 + i, (1024, 64)) for i in range(3))
+    close(O.sdpa(qh, kh, vh, 1, causal=True), g["c2_head_causal"], what="c2 head slice, causal")
 
 
 def test_causal_flag_equals_explicit_mask():
