@@ -46,6 +46,10 @@ SIGNATURES = {
     "cdml_stream_create": [C.POINTER(_vp)],
     "cdml_stream_destroy": [_vp],
     "cdml_stream_synchronize": [_vp],
+    "cdml_graph_capture_begin": [_vp],
+    "cdml_graph_capture_end": [_vp, C.POINTER(_vp)],
+    "cdml_graph_launch": [_vp, _vp],
+    "cdml_graph_destroy": [_vp],
     "cdml_event_create": [C.POINTER(_vp)],
     "cdml_event_destroy": [_vp],
     "cdml_event_record": [_vp, _vp],

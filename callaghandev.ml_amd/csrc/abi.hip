@@ -205,6 +205,55 @@ int cdml_stream_create(cdml_stream *stream) {
   return CDML_OK;
 }
 
+struct cdml_graph_s {
+  hipGraphExec_t exec;
+};
+
+int cdml_graph_capture_begin(cdml_stream stream) {
+  if (!stream) return fail(CDML_E_INVALID, "cdml_graph_capture_begin: recording needs a created stream");
+  int rc = ensure_device();
+  if (rc) return rc;
+  hipError_t e = hipStreamBeginCapture(as_hip(stream), hipStreamCaptureModeThreadLocal);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamBeginCapture");
+  return CDML_OK;
+}
+
+int cdml_graph_capture_end(cdml_stream stream, cdml_graph *graph) {
+  if (!graph) return fail(CDML_E_INVALID, "cdml_graph_capture_end: graph is NULL");
+  *graph = nullptr;
+  if (!stream) return fail(CDML_E_INVALID, "cdml_graph_capture_end: recording needs a created stream");
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(as_hip(stream), &g);
+  (void)hipGetLastError();  // a failed recording also leaves the error state set
+  if (e != hipSuccess || !g) {
+    if (g) (void)hipGraphDestroy(g);
+    return hip_fail(e != hipSuccess ? e : hipErrorStreamCaptureInvalidated, "hipStreamEndCapture");
+  }
+  hipGraphExec_t exec = nullptr;
+  e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+  *graph = new cdml_graph_s{exec};
+  return CDML_OK;
+}
+
+int cdml_graph_launch(cdml_graph graph, cdml_stream stream) {
+  if (!graph) return fail(CDML_E_INVALID, "cdml_graph_launch: graph is NULL");
+  int rc = ensure_device();
+  if (rc) return rc;
+  hipError_t e = hipGraphLaunch(graph->exec, as_hip(stream));
+  if (e != hipSuccess) return hip_fail(e, "hipGraphLaunch");
+  return CDML_OK;
+}
+
+int cdml_graph_destroy(cdml_graph graph) {
+  if (!graph) return CDML_OK;
+  hipError_t e = hipGraphExecDestroy(graph->exec);
+  delete graph;
+  if (e != hipSuccess) return hip_fail(e, "hipGraphExecDestroy");
+  return CDML_OK;
+}
+
 int cdml_stream_destroy(cdml_stream stream) {
   if (!stream) return CDML_OK;
   hipError_t e = hipStreamDestroy(as_hip(stream));

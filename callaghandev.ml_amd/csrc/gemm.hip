@@ -594,6 +594,73 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const Gem
   }
 }
 
+// Few rows (decode steps, short batches: M <= MR), non-transposed operands,
+// 16-byte aligned rows with K % 4 == 0.  One wave per pair of output columns
+// (n, n + 1): its lanes stride over K in float4 steps, each keeping 2 x MR
+// partial dot products, which xor-shuffle sums then complete in every lane.
+// The kernel is short (no LDS, no MFMA tiles), so a launch costs little more
+// than the bytes of W it streams; the pair is also the rotation pair of the
+// fused RoPE epilogue (head dims are even).
+template <int MR, bool EPI>
+__global__ void __launch_bounds__(256) gemm_rows_kernel(const GemmArgs args) {
+  const int prob = blockIdx.y;
+  const GemmProblem P = args.p[prob];
+  const int M = args.M, N = args.N, K = args.K;
+  const int lane = threadIdx.x & 63;
+  const int n0 = 2 * (blockIdx.x * 4 + (threadIdx.x >> 6));
+  if (n0 >= N) return;
+  const int n1 = min(n0 + 1, N - 1);
+  const float *__restrict__ w0 = P.w + (size_t)n0 * args.ldb;
+  const float *__restrict__ w1 = P.w + (size_t)n1 * args.ldb;
+  float s0[MR], s1[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) s0[m] = s1[m] = 0.f;
+  for (int k = 4 * lane; k < K; k += 256) {
+    const float4 a = *reinterpret_cast<const float4 *>(w0 + k);
+    const float4 b = *reinterpret_cast<const float4 *>(w1 + k);
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      if (m < M) {
+        const float4 x = *reinterpret_cast<const float4 *>(P.a + (size_t)m * args.lda + k);
+        s0[m] += (x.x * a.x + x.y * a.y) + (x.z * a.z + x.w * a.w);
+        s1[m] += (x.x * b.x + x.y * b.y) + (x.z * b.z + x.w * b.w);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      s0[m] += __shfl_xor(s0[m], off);
+      s1[m] += __shfl_xor(s1[m], off);
+    }
+  }
+  // lane m stores row m
+  float z0 = 0.f, z1 = 0.f;
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+    if (lane == m) {
+      z0 = s0[m];
+      z1 = s1[m];
+    }
+  if (lane >= M) return;
+  const int m = lane;
+  const bool has1 = n0 + 1 < N;
+  z0 += P.bias ? P.bias[n0] : 0.f;
+  if (has1) z1 += P.bias ? P.bias[n0 + 1] : 0.f;
+  if (args.rope_cs && prob < 2) {  // AccelerationCPU.cs:4947-4975 on the pair (n0, n0 + 1)
+    int pos = args.rope_pos0 + (args.rope_seg > 0 ? m % args.rope_seg : m);
+    pos = min(pos, args.rope_npos - 1);
+    const float2 t = args.rope_cs[(size_t)pos * (args.rope_hd >> 1) + ((n0 % args.rope_hd) >> 1)];
+    float *c = P.c + (size_t)m * args.ldc + n0;
+    c[0] = z0 * t.x - z1 * t.y;
+    if (has1) c[1] = z1 * t.x + z0 * t.y;
+    return;
+  }
+  store_elem<EPI>(args, P, m, n0, z0, args.act);
+  if (has1) store_elem<EPI>(args, P, m, n0 + 1, z1, args.act);
+}
+
 // Any layout, any shape (the gradient GEMMs whose sizes miss the tiled
 // kernel's conditions): a 64 x 64 tile of C per 256-thread workgroup, 4 x 4
 // outputs per thread, K in steps of 16 through LDS with guarded loads that
@@ -908,6 +975,17 @@ int launch_gemm(GemmArgs &g, bool ta, bool tb, hipStream_t stream, const char *w
   g.padded = pad_to_xcd(g.total);
   bool vec = (g.K % 4 == 0) && (g.lda % 4 == 0) && (g.ldb % 4 == 0);
   for (int i = 0; i < g.nprob; ++i) vec = vec && aligned16(g.p[i].a) && aligned16(g.p[i].w);
+  if (vec && g.M <= 16 && g.K > 0 && (g.rope_cs == nullptr || g.rope_hd % 2 == 0)) {
+    const dim3 grid((unsigned)((g.N + 7) / 8), (unsigned)g.nprob), block(256);
+    const bool epi = has_epi(g);
+    if (g.M <= 4)
+      epi ? gemm_rows_kernel<4, true><<<grid, block, 0, stream>>>(g)
+          : gemm_rows_kernel<4, false><<<grid, block, 0, stream>>>(g);
+    else
+      epi ? gemm_rows_kernel<16, true><<<grid, block, 0, stream>>>(g)
+          : gemm_rows_kernel<16, false><<<grid, block, 0, stream>>>(g);
+    return check_launch(what);
+  }
   if (fast && g.M >= 1024) {
     int rc = launch_tile<256, 128, 16, 4, 2, 2, false, false>(g, stream);
     if (rc) return rc;

@@ -627,6 +627,7 @@ PYBIND11_MODULE(_cdml_host, m) {
              auto X = mat(x);
              return to_numpy(d.ForwardContinuous(X.view, batch, seqLen));
            })
+      .def_readwrite("use_graphs", &DeviceLanguageModel::use_graphs)
       .def("GenerateGreedy",
            [](DeviceLanguageModel &d, py::object prompts, int maxNew) {
              I32 a = I32::ensure(prompts);

@@ -24,6 +24,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <map>
 #include <memory>
 #include <mutex>
 #include <stdexcept>
@@ -409,6 +410,10 @@ class DeviceLanguageModel {
   int output_dim() const { return cfg_.EffectiveOutputDim(); }
   int batch_capacity() const { return cap_; }
   void synchronize();
+  // GenerateGreedy records its device work (prefill, every decode step,
+  // the token choices) once per (batch, promptLen, n) and replays it as one
+  // graph launch; off, every kernel is launched from the host.
+  bool use_graphs = true;
 
  private:
   struct Layer {
@@ -422,6 +427,7 @@ class DeviceLanguageModel {
   float *upload(const float *host, size_t floats);
   void hidden_pass(float *x, int batch, int seqLen, bool fill_cache);
   void decode_step(const int *dev_tok, int batch, int pos, float *x);
+  void generate_device(int batch, int promptLen, int n);
 
   TransformerConfig cfg_;
   int cap_, device_;
@@ -437,6 +443,7 @@ class DeviceLanguageModel {
   void *ws_ = nullptr;
   size_t ws_bytes_ = 0;
   int ff_max_ = 0;
+  std::map<std::tuple<int, int, int>, cdml_graph> graphs_;  // (batch, promptLen, n)
 };
 
 // ---- device-resident training --------------------------------------------

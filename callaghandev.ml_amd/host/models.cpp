@@ -419,6 +419,7 @@ DeviceLanguageModel::DeviceLanguageModel(const LanguageModel &model, int batch_c
 
 DeviceLanguageModel::~DeviceLanguageModel() {
   cdml_stream_synchronize(stream_);
+  for (auto &kv : graphs_) cdml_graph_destroy(kv.second);
   for (void *p : allocs_) cdml_free(p);
   cdml_stream_destroy(stream_);
 }
@@ -553,6 +554,27 @@ void DeviceLanguageModel::decode_step(const int *dev_tok, int batch, int pos, fl
   }
 }
 
+// The device work of one greedy generation after the prompt ids are in
+// ids_: the prompt prefilled in one pass, then n - 1 decode steps; token s of
+// every sequence lands in gen_[s * batch + b].  Only enqueue calls, so the
+// sequence can be recorded as a graph.
+void DeviceLanguageModel::generate_device(int batch, int promptLen, int n) {
+  const int D = cfg_.EmbeddingDim, V = cfg_.VocabSize;
+  check(cdml_embed_tokens(ids_, batch * promptLen, emb_, V, D, x_, nullptr, stream_), "embed");
+  hidden_pass(x_, batch, promptLen, true);
+  // logits of each sequence's last prompt position: rows (P-1), stride P*D
+  check(cdml_linear(x_ + (size_t)(promptLen - 1) * D, promptLen * D, outproj_, outbias_, logits_, V,
+                    batch, D, V, CDML_ACT_NONE, stream_),
+        "output projection");
+  check(cdml_argmax_rows(logits_, batch, V, V, gen_, 1, stream_), "argmax");
+  for (int s = 1; s < n; ++s) {
+    decode_step(gen_ + (size_t)(s - 1) * batch, batch, promptLen + s - 1, x_);
+    check(cdml_linear(x_, D, outproj_, outbias_, logits_, V, batch, D, V, CDML_ACT_NONE, stream_),
+          "output projection");
+    check(cdml_argmax_rows(logits_, batch, V, V, gen_ + (size_t)s * batch, 1, stream_), "argmax");
+  }
+}
+
 // LanguageModel.Generate (:482-537) for a batch of equal-length prompts with
 // greedy selection: the prompt is prefilled in one pass (instead of one token
 // at a time), then every new token runs one decode step per sequence; token
@@ -582,18 +604,30 @@ std::vector<int> DeviceLanguageModel::GenerateGreedy(const std::vector<int> &pro
 
   check(cdml_memcpy_h2d_async(ids_, prompts.data(), prompts.size() * sizeof(int), stream_), "upload ids");
   if (cfg_.UseDecoderOnly) {
-    check(cdml_embed_tokens(ids_, batch * promptLen, emb_, V, D, x_, nullptr, stream_), "embed");
-    hidden_pass(x_, batch, promptLen, true);
-    // logits of each sequence's last prompt position: rows (P-1), stride P*D
-    check(cdml_linear(x_ + (size_t)(promptLen - 1) * D, promptLen * D, outproj_, outbias_, logits_, V,
-                      batch, D, V, CDML_ACT_NONE, stream_),
-          "output projection");
-    check(cdml_argmax_rows(logits_, batch, V, V, gen_, 1, stream_), "argmax");
-    for (int s = 1; s < n; ++s) {
-      decode_step(gen_ + (size_t)(s - 1) * batch, batch, promptLen + s - 1, x_);
-      check(cdml_linear(x_, D, outproj_, outbias_, logits_, V, batch, D, V, CDML_ACT_NONE, stream_),
-            "output projection");
-      check(cdml_argmax_rows(logits_, batch, V, V, gen_ + (size_t)s * batch, 1, stream_), "argmax");
+    if (use_graphs) {
+      const auto key = std::make_tuple(batch, promptLen, n);
+      auto it = graphs_.find(key);
+      if (it == graphs_.end()) {
+        if (graphs_.size() >= 16) {  // a bounded cache: drop every recording
+          synchronize();
+          for (auto &kv : graphs_) cdml_graph_destroy(kv.second);
+          graphs_.clear();
+        }
+        check(cdml_graph_capture_begin(stream_), "cdml_graph_capture_begin");
+        cdml_graph g = nullptr;
+        try {
+          generate_device(batch, promptLen, n);
+        } catch (...) {
+          cdml_graph_capture_end(stream_, &g);  // discards the partial recording
+          cdml_graph_destroy(g);
+          throw;
+        }
+        check(cdml_graph_capture_end(stream_, &g), "cdml_graph_capture_end");
+        it = graphs_.emplace(key, g).first;
+      }
+      check(cdml_graph_launch(it->second, stream_), "cdml_graph_launch");
+    } else {
+      generate_device(batch, promptLen, n);
     }
     std::vector<int> gen((size_t)n * batch);
     check(cdml_memcpy_d2h_async(gen.data(), gen_, gen.size() * sizeof(int), stream_), "download");

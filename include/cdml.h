@@ -93,6 +93,22 @@ int cdml_host_free_pinned(void *ptr);
 int cdml_memcpy_h2d_async(void *dst, const void *src, size_t bytes, cdml_stream stream);
 int cdml_memcpy_d2h_async(void *dst, const void *src, size_t bytes, cdml_stream stream);
 int cdml_memcpy_d2d_async(void *dst, const void *src, size_t bytes, cdml_stream stream);
+/* ---- recorded launch sequences (no counterpart in the reference, whose
+ * managers launch every kernel from the host).  A caller that repeats one
+ * sequence of enqueue calls on a stream (a generation loop, a training step
+ * of fixed shape) records it once between cdml_graph_capture_begin and
+ * cdml_graph_capture_end, then replays it with cdml_graph_launch: one host
+ * call instead of one per kernel, with the recorded arguments and pointers.
+ * While recording, only enqueue calls on that stream are legal (no
+ * synchronisation, no copies from pageable host memory); a failed call
+ * leaves the recording open, and cdml_graph_capture_end then discards it
+ * (graph NULL). */
+typedef struct cdml_graph_s *cdml_graph;
+int cdml_graph_capture_begin(cdml_stream stream);
+int cdml_graph_capture_end(cdml_stream stream, cdml_graph *graph);
+int cdml_graph_launch(cdml_graph graph, cdml_stream stream);
+int cdml_graph_destroy(cdml_graph graph);
+
 /* Zero `count` floats with a fill kernel (safe under stream capture). */
 int cdml_zero_f32_async(float *dst, size_t count, cdml_stream stream);
 /* dst[i] = value for i < count, a fill kernel (safe under stream capture). */

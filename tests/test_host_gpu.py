@@ -327,6 +327,31 @@ def test_device_language_model_c1_batch():
     assert np.array_equal(full, ids)
 
 
+def test_generate_graph_replays_match_eager():
+    """GenerateGreedy's recorded graph (one per batch x prompt length x new
+    tokens) against the same model launching every kernel from the host:
+    replays with new prompt ids of the recorded shape, a second recorded
+    shape beside the first, and eager work and synchronisations between the
+    replays, every result compared."""
+    Hm = host.module()
+    cfg = {"vocab": 200, "dim": 64, "heads": 4, "layers": 2, "ff": 128, "max_seq": 64}
+    lm, _ = host.language_model(cfg, synth.lm_weights(cfg, 8))
+    dev, eager = Hm.DeviceLanguageModel(lm, 4), Hm.DeviceLanguageModel(lm, 4)
+    eager.use_graphs = False
+    assert dev.use_graphs
+    for rep in range(4):
+        ids = synth.token_ids(50 + rep, 4 * 64, 200).reshape(4, 64)
+        for plen, n in ((32, 20), (40, 9)):
+            got = dev.GenerateGreedy(ids[:, :plen], n)
+            want = eager.GenerateGreedy(ids[:, :plen], n)
+            assert np.array_equal(got, want), f"replay {rep}, prompt {plen}, {n} tokens"
+        # eager work on the same model between replays
+        dev.use_graphs = False
+        assert np.array_equal(dev.GenerateGreedy(ids[:2, :10], 3), eager.GenerateGreedy(ids[:2, :10], 3))
+        dev.Forward(ids)
+        dev.use_graphs = True
+
+
 def _oracle_continuous(cfg, w, x):
     """LanguageModel.Forward(float[,]) from oracle functions: input projection,
     post-LN blocks, output projection."""
