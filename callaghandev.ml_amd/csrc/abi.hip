@@ -46,6 +46,19 @@ int ensure_device() {
   return CDML_OK;
 }
 
+int num_cus() {
+  static std::atomic<int> cus{0};
+  int n = cus.load(std::memory_order_relaxed);
+  if (n == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cus.store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
 int check_launch(const char *what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, what);

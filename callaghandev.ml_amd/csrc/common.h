@@ -19,6 +19,9 @@ int fail(int code, const char *fmt, ...);
 // Makes the library's device current on the calling thread.
 int ensure_device();
 
+// Compute units of the current device (queried once; 256 on MI355X).
+int num_cus();
+
 // Checks the launch that was just enqueued.
 int check_launch(const char *what);
 

@@ -42,7 +42,7 @@ struct FlashArgs {
   int ldq, ldk, ldv, ldo;
   int lq, lk, heads, hd;
   float scale_log2;
-  int n_qt, total, padded;
+  int n_qt, n_bh, total, padded;
 };
 
 // Stages one BN x HD tile of K or V (rows [k0, k0+BN) of head column block
@@ -134,7 +134,7 @@ constexpr float kRescaleThreshold = 8.0f;
 // lane of half-wave h: 8 * (r / 4) + 4 * h + r % 4 (the 32x32 MFMA D layout).
 __device__ __forceinline__ constexpr int acc_key(int r) { return 8 * (r >> 2) + (r & 3); }
 
-template <int HD, int BN, bool CAUSAL, bool HAS_MASK, bool VEC>
+template <int HD, int BN, bool CAUSAL, bool HAS_MASK, bool VEC, bool PAIR>
 __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArgs a) {
   constexpr int NKB = BN / 32;   // 32-key sub-blocks per tile
   constexpr int NDB = HD / 32;   // 32-wide head-dim blocks of O^T
@@ -144,18 +144,28 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArg
   __shared__ __attribute__((aligned(16))) float Ks[2][BN][HD + 4];
   __shared__ __attribute__((aligned(16))) float Vs[2][BN][HD + 4];
 
-  // Query-tile-major order: workgroup i takes (sequence, head) i % n_bh and
-  // query tile i / n_bh, counted from the last (longest under causal
-  // masking) tile down.  Every XCD therefore receives the heaviest tiles
-  // first and the lightest last (a near-optimal greedy schedule), and since
-  // workgroup i runs on XCD i % 8, all tiles of one (sequence, head) share an
-  // XCD and its L2 whenever n_bh is a multiple of 8.
+  // Workgroup i takes (sequence, head) i % n_bh, so with workgroup i on XCD
+  // i % 8 all tiles of one (sequence, head) share an XCD and its L2 whenever
+  // n_bh is a multiple of 8.  Under the causal rule query tile t sees t + 1
+  // key tiles:
+  //  * slot p = i / n_bh is tile n_qt - 1 - p, counted from the longest row
+  //    down, so every XCD receives the heaviest tiles first and the lightest
+  //    last (a near-optimal greedy schedule when the launch spans several
+  //    rounds of resident workgroups);
+  //  * with PAIR (a launch that fits in one round), slot p runs the pair of
+  //    tiles n_qt - 1 - p and p one after the other, so every workgroup has
+  //    the same work (n_qt + 1 key tiles; the middle tile of an odd count
+  //    runs alone) and the round finishes together.
+  // Without the causal rule slot p is tile p.
   const int lid = blockIdx.x;
-  const int n_bh = a.total / a.n_qt;
+  const int n_bh = a.n_bh;
   const int bh = lid % n_bh;
-  int qt = lid / n_bh;
-  if (CAUSAL) qt = a.n_qt - 1 - qt;
+  const int slot = lid / n_bh;
+  const int npass = (PAIR && 2 * slot + 1 != a.n_qt) ? 2 : 1;
   const int b = bh / a.heads, h = bh % a.heads;
+  for (int pass = 0; pass < npass; ++pass) {
+  if (pass > 0) __syncthreads();  // the LDS tiles of the first pass are done with
+  const int qt = CAUSAL ? (pass == 0 ? a.n_qt - 1 - slot : slot) : slot;
   const int q0 = qt * FA_BM;
 
   const int lane = threadIdx.x & 63;
@@ -353,6 +363,7 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArg
       }
     }
   }
+  }  // pass
 }
 
 // Head dims above 128: one workgroup per (sequence, head, query), keys in
@@ -417,11 +428,23 @@ __global__ void __launch_bounds__(256) flash_generic_kernel(const FlashArgs a, i
 }
 
 template <int HD, int BN, bool CAUSAL, bool HAS_MASK>
-void launch_tpl(const FlashArgs &a, bool vec, hipStream_t st) {
+void launch_tpl(FlashArgs a, bool vec, hipStream_t st) {
+  // Pairs of causal tiles when one tile per workgroup would fit in a single
+  // round of resident workgroups (four per CU): then the round lasts as long
+  // as its longest tile.
+  const bool pair = CAUSAL && a.n_qt > 1 && (long long)a.n_bh * a.n_qt <= 4LL * num_cus();
+  a.total = pair ? a.n_bh * ((a.n_qt + 1) / 2) : a.n_bh * a.n_qt;
+  if constexpr (CAUSAL) {
+    if (pair) {
+      if (vec) flash_fwd_kernel<HD, BN, true, HAS_MASK, true, true><<<dim3(a.total), dim3(FA_THREADS), 0, st>>>(a);
+      else flash_fwd_kernel<HD, BN, true, HAS_MASK, false, true><<<dim3(a.total), dim3(FA_THREADS), 0, st>>>(a);
+      return;
+    }
+  }
   if (vec)
-    flash_fwd_kernel<HD, BN, CAUSAL, HAS_MASK, true><<<dim3(a.total), dim3(FA_THREADS), 0, st>>>(a);
+    flash_fwd_kernel<HD, BN, CAUSAL, HAS_MASK, true, false><<<dim3(a.total), dim3(FA_THREADS), 0, st>>>(a);
   else
-    flash_fwd_kernel<HD, BN, CAUSAL, HAS_MASK, false><<<dim3(a.total), dim3(FA_THREADS), 0, st>>>(a);
+    flash_fwd_kernel<HD, BN, CAUSAL, HAS_MASK, false, false><<<dim3(a.total), dim3(FA_THREADS), 0, st>>>(a);
 }
 
 template <int HD, int BN>
@@ -478,6 +501,7 @@ int flash_forward(const float *q, int ldq, const float *k, int ldk, const float 
   const bool vec = hd == hd_pad && ldq % 4 == 0 && ldk % 4 == 0 && ldv % 4 == 0 && ldo % 4 == 0 &&
                    aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
   a.n_qt = (lq + FA_BM - 1) / FA_BM;
+  a.n_bh = batch * num_heads;
   long long total = (long long)batch * num_heads * a.n_qt;
   if (total > (1LL << 30)) return fail(CDML_E_INVALID, "cdml_sdpa_fwd: problem too large");
   a.total = (int)total;
