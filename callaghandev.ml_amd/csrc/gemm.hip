@@ -721,34 +721,51 @@ __global__ void __launch_bounds__(256) op_rowsum_kernel(const GemmArgs args) {
   P.bgrad[m] += s;
 }
 
-// Sum of the split-K partials in chunk order: C (+)= sum_c ws[c], bgrad +=
-// sum_c wsb[c].  N % 4 == 0 (the tiled path's transposed staging of opB needs
-// it), so each thread owns four consecutive columns.
+// Sum of the split-K partials: C (+)= sum_c ws[c], bgrad += sum_c wsb[c].
+// N % 4 == 0 (the tiled path's transposed staging of opB needs it), so an
+// output is four consecutive columns.  Eight consecutive lanes share an
+// output: lane g adds chunks g, g + 8, g + 16, ... in order, and a fixed
+// xor-shuffle tree joins the eight sums, so the order of every addition is
+// fixed (the same bits on every run) while the chunk loads of eight lanes
+// are in flight together.  The group of output e also sums bias row e.
+constexpr int kReduceLanes = 8;
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs args) {
   const int prob = blockIdx.y;
   const GemmProblem P = args.p[prob];
   const int M = args.M, N = args.N, n4 = N >> 2;
   const size_t plane = (size_t)args.nprob * M * N;
-  const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (e < (size_t)M * n4) {
+  const size_t e = ((size_t)blockIdx.x * 256 + threadIdx.x) / kReduceLanes;
+  const int g = threadIdx.x % kReduceLanes;
+  const size_t n_out = (size_t)M * n4;
+  if (e < n_out) {
     const int m = (int)(e / n4), n = (int)(e % n4) * 4;
     const float *src = args.ws + (size_t)prob * M * N + (size_t)m * N + n;
-    vf4 s = *reinterpret_cast<const vf4 *>(src);
-    for (int c = 1; c < args.ksplit; ++c) {
+    vf4 s = {0.f, 0.f, 0.f, 0.f};
+    for (int c = g; c < args.ksplit; c += kReduceLanes) {
       const vf4 x = *reinterpret_cast<const vf4 *>(src + c * plane);
       s[0] += x[0];
       s[1] += x[1];
       s[2] += x[2];
       s[3] += x[3];
     }
-    float *dst = P.c + (size_t)m * args.ldc + n;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) dst[q] = args.beta ? dst[q] + s[q] : s[q];
+    for (int off = kReduceLanes / 2; off > 0; off >>= 1)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) s[q] += __shfl_xor(s[q], off);
+    if (g == 0) {
+      float *dst = P.c + (size_t)m * args.ldc + n;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) dst[q] = args.beta ? dst[q] + s[q] : s[q];
+    }
   }
+  // every lane of a group runs the shuffles together (e is uniform in a group)
   if (P.bgrad && e < (size_t)M) {
     float s = 0.f;
-    for (int c = 0; c < args.ksplit; ++c) s += args.wsb[((size_t)c * args.nprob + prob) * M + e];
-    P.bgrad[e] += s;
+    for (int c = g; c < args.ksplit; c += kReduceLanes)
+      s += args.wsb[((size_t)c * args.nprob + prob) * M + e];
+#pragma unroll
+    for (int off = kReduceLanes / 2; off > 0; off >>= 1) s += __shfl_xor(s, off);
+    if (g == 0) P.bgrad[e] += s;
   }
 }
 
@@ -809,21 +826,100 @@ __global__ void __launch_bounds__(256) wgrad_small_kernel(const GemmArgs args) {
   }
 }
 
+// The same weight gradients when one side is narrow (at most kNarrow): the
+// input projection [D, F] (F = 5) and a regression head [O, D] (O <= 16).
+// Threads run along the wide side, so each row of that operand is one
+// coalesced load and the narrow side's few values of the row are broadcast
+// loads; a thread keeps the narrow side's sums (and the bias row sums) in
+// registers over its chunk of rows, in row order, four rows per iteration.
+// OVER_M: the output rows m are wide (thread m, columns n < N narrow);
+// otherwise the columns n are wide and the rows m < M narrow.
+constexpr int kNarrow = 16;
+template <bool OVER_M>
+__global__ void __launch_bounds__(256) wgrad_narrow_kernel(const GemmArgs args) {
+  const int chunk = blockIdx.x, prob = blockIdx.z;
+  const GemmProblem P = args.p[prob];
+  const int M = args.M, N = args.N, MN = M * N;
+  const int wide = OVER_M ? M : N, narrow = OVER_M ? N : M;
+  const int i = blockIdx.y * 256 + threadIdx.x;
+  const int ic = min(i, wide - 1);
+  const int k0 = chunk * args.kchunk, k1 = min(args.K, k0 + args.kchunk);
+  const bool bsum = P.bgrad != nullptr;
+  float acc[kNarrow], bacc[kNarrow];
+#pragma unroll
+  for (int j = 0; j < kNarrow; ++j) acc[j] = bacc[j] = 0.f;
+  auto row = [&](int k) {
+    const float *ar = P.a + (size_t)k * args.lda;
+    const float *br = P.w + (size_t)k * args.ldb;
+    if constexpr (OVER_M) {
+      const float x = ar[ic];
+#pragma unroll
+      for (int j = 0; j < kNarrow; ++j)
+        if (j < narrow) acc[j] += x * br[j];
+      bacc[0] += x;
+    } else {
+      const float y = br[ic];
+#pragma unroll
+      for (int j = 0; j < kNarrow; ++j)
+        if (j < narrow) {
+          const float x = ar[j];
+          acc[j] += x * y;
+          bacc[j] += x;
+        }
+    }
+  };
+  int k = k0;
+  for (; k + 4 <= k1; k += 4) {
+    row(k);
+    row(k + 1);
+    row(k + 2);
+    row(k + 3);
+  }
+  for (; k < k1; ++k) row(k);
+  if (i >= wide) return;
+  float *out = args.ws + ((size_t)chunk * args.nprob + prob) * MN;
+#pragma unroll
+  for (int j = 0; j < kNarrow; ++j)
+    if (j < narrow) out[OVER_M ? (size_t)i * N + j : (size_t)j * N + i] = acc[j];
+  if (bsum) {
+    float *ob = args.wsb + ((size_t)chunk * args.nprob + prob) * M;
+    if constexpr (OVER_M) {
+      ob[i] = bacc[0];
+    } else if (i == 0) {
+#pragma unroll
+      for (int j = 0; j < kNarrow; ++j)
+        if (j < narrow) ob[j] = bacc[j];
+    }
+  }
+}
+
+// Sum of the small-output partials, kSmallLanes lanes per output: lane g adds
+// chunks g, g + kSmallLanes, ... in order and a fixed xor-shuffle tree joins
+// them (the same bits on every run); the group of output e also sums bias
+// row e.
+constexpr int kSmallLanes = 64;
 __global__ void __launch_bounds__(256) wgrad_small_reduce_kernel(const GemmArgs args) {
   const int prob = blockIdx.y;
   const GemmProblem P = args.p[prob];
   const int M = args.M, N = args.N, MN = M * N;
-  const int e = blockIdx.x * 256 + threadIdx.x;
+  const int e = (blockIdx.x * 256 + threadIdx.x) / kSmallLanes;
+  const int g = threadIdx.x % kSmallLanes;
   if (e < MN) {
     float s = 0.f;
-    for (int c = 0; c < args.ksplit; ++c) s += args.ws[((size_t)c * args.nprob + prob) * MN + e];
-    float *dst = P.c + (size_t)(e / N) * args.ldc + e % N;
-    *dst = args.beta ? *dst + s : s;
+    for (int c = g; c < args.ksplit; c += kSmallLanes) s += args.ws[((size_t)c * args.nprob + prob) * MN + e];
+#pragma unroll
+    for (int off = kSmallLanes / 2; off > 0; off >>= 1) s += __shfl_xor(s, off);
+    if (g == 0) {
+      float *dst = P.c + (size_t)(e / N) * args.ldc + e % N;
+      *dst = args.beta ? *dst + s : s;
+    }
   }
   if (P.bgrad && e < M) {
     float s = 0.f;
-    for (int c = 0; c < args.ksplit; ++c) s += args.wsb[((size_t)c * args.nprob + prob) * M + e];
-    P.bgrad[e] += s;
+    for (int c = g; c < args.ksplit; c += kSmallLanes) s += args.wsb[((size_t)c * args.nprob + prob) * M + e];
+#pragma unroll
+    for (int off = kSmallLanes / 2; off > 0; off >>= 1) s += __shfl_xor(s, off);
+    if (g == 0) P.bgrad[e] += s;
   }
 }
 
@@ -835,7 +931,9 @@ SplitPlan splitk_plan(int M, int N, int K, int nprob) {
   if (nk < 1 || N % 4 || M % 4) {  // not the tiled kernel's shape
     if ((long long)M * N > kSmallOut || K < 2048) return sp;
     sp.small = true;
-    sp.ksplit = std::min(256, K / 512);
+    // chunks of 64 rows (at most 4096 chunks): each workgroup's row loop is
+    // short, so the launch is not bound by one loop's load latency
+    sp.ksplit = std::min(4096, (K + 63) / 64);
     sp.kchunk = (K + sp.ksplit - 1) / sp.ksplit;
     sp.ksplit = (K + sp.kchunk - 1) / sp.kchunk;
     sp.bytes = (size_t)sp.ksplit * nprob * ((size_t)M * N + M) * sizeof(float);
@@ -888,7 +986,7 @@ int launch_tile(GemmArgs g, hipStream_t stream) {
     else
       gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_NONE, TA, TB, false><<<grid, block, 0, stream>>>(g);
     if (g.ksplit > 1) {
-      const size_t n = std::max((size_t)g.M * (g.N / 4), (size_t)g.M);
+      const size_t n = std::max((size_t)g.M * (g.N / 4), (size_t)g.M) * kReduceLanes;
       splitk_reduce_kernel<<<dim3((unsigned)((n + 255) / 256), g.nprob), dim3(256), 0, stream>>>(g);
     }
   } else {
@@ -945,8 +1043,13 @@ int launch_gemm(GemmArgs &g, bool ta, bool tb, hipStream_t stream, const char *w
     for (int i = 0; split_tail && i < g.nprob; ++i)
       split_tail = stage_ok(g.p[i].a, g.M, g.lda, ta, 16) && stage_ok(g.p[i].w, g.N, g.ldb, tb, 16);
     if (ta && tb && g.small && g.ksplit > 1) {  // small output, long reduction
-      wgrad_small_kernel<<<dim3(g.ksplit, g.nprob), dim3(256), 0, stream>>>(g);
-      const int n = std::max(g.M * g.N, g.M);
+      if (g.N <= kNarrow)
+        wgrad_narrow_kernel<true><<<dim3(g.ksplit, (g.M + 255) / 256, g.nprob), dim3(256), 0, stream>>>(g);
+      else if (g.M <= kNarrow)
+        wgrad_narrow_kernel<false><<<dim3(g.ksplit, (g.N + 255) / 256, g.nprob), dim3(256), 0, stream>>>(g);
+      else
+        wgrad_small_kernel<<<dim3(g.ksplit, g.nprob), dim3(256), 0, stream>>>(g);
+      const int n = std::max(g.M * g.N, g.M) * kSmallLanes;
       wgrad_small_reduce_kernel<<<dim3((n + 255) / 256, g.nprob), dim3(256), 0, stream>>>(g);
       return check_launch(what);
     }

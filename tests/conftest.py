@@ -59,10 +59,13 @@ def assert_parity_with_exact(actual, oracle, exact, atol=1e-4, rtol=1e-3, what="
     elements that cancel to near zero its own rounding can exceed the bar: a
     2048-row gradient sum of O(1) products drifts by up to 3e-4 from exact
     arithmetic.  So the result must meet the bar against the float64 value
-    everywhere, and against the oracle wherever the oracle itself meets the
-    bar against the float64 value."""
+    everywhere, and against the oracle wherever the oracle is within half the
+    bar of the float64 value.  (With the full bar as the selection, an
+    element where the oracle is off by 0.9 of the bar fails even when the
+    result is off by 0.15 of it in the other direction: a 4100-row sum
+    measured exactly that.)"""
     e64 = np.asarray(exact, np.float64)
     o = np.asarray(oracle, np.float64)
     assert_parity(actual, e64, atol, rtol, what + " (vs float64)")
-    ok = np.abs(o - e64) <= atol + rtol * np.abs(e64)
+    ok = np.abs(o - e64) <= 0.5 * (atol + rtol * np.abs(e64))
     assert_parity(np.asarray(actual)[ok], o[ok], atol, rtol, what + " (vs oracle)")

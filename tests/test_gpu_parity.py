@@ -207,7 +207,9 @@ def test_backprop_qkv_c3_shape_float64():
                                           (252, 64, 200),      # the config-1 LM head of one training bucket
                                           (8192, 5, 256),      # input projection: small output, split rows
                                           (8200, 256, 1),      # regression head [1, D]
-                                          (5000, 7, 3)])       # both small and odd
+                                          (5000, 7, 3),        # both small and odd
+                                          (6000, 3, 600),      # narrow input side, 600 output rows
+                                          (4096, 18, 36)])     # small output, neither side narrow
 def test_linear_backward(rows, ind, out):
     """BackpropLinearProjection (dInput accumulates) and BackpropOutputProjection
     (dX overwritten) on the shapes of AccelerationConsistencyTests.cs:633-700,
