@@ -37,8 +37,10 @@ __device__ __forceinline__ float wave_max(float v) {
 // ResidualLayerNormForward (AccelerationCPU.cs:1440-1514) for one row per
 // wave: residual = a + b, mean, biased variance (two passes), out = gamma *
 // (residual - mean) * invStd + beta; mean / var / residual / normalized are
-// written when non-NULL.
-template <int RC>
+// written when non-NULL.  Element i of a lane's row cache is column
+// lane + 64 i, or with V4 (features % 4 == 0, 16-byte aligned rows, RC >= 4)
+// column 256 (i / 4) + 4 lane + i % 4, so that each access moves a float4.
+template <int RC, bool V4>
 __global__ void __launch_bounds__(256) ln_forward_kernel(const float *__restrict__ a,
                                                          const float *__restrict__ b,
                                                          const float *__restrict__ gamma,
@@ -55,30 +57,63 @@ __global__ void __launch_bounds__(256) ln_forward_kernel(const float *__restrict
   const size_t base = (size_t)row * f;
   float cache[RC];
   float sum = 0.f;
+  if constexpr (V4) {
 #pragma unroll
-  for (int i = 0; i < RC; ++i) {
-    const int j = lane + 64 * i;
-    cache[i] = j < f ? a[base + j] + b[base + j] : 0.f;
-    sum += cache[i];
+    for (int i4 = 0; i4 < RC / 4; ++i4) {
+      const int j = 256 * i4 + 4 * lane;
+      vf4 v = {0.f, 0.f, 0.f, 0.f};
+      if (j < f) v = *reinterpret_cast<const vf4 *>(a + base + j) + *reinterpret_cast<const vf4 *>(b + base + j);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        cache[4 * i4 + c] = v[c];
+        sum += v[c];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < RC; ++i) {
+      const int j = lane + 64 * i;
+      cache[i] = j < f ? a[base + j] + b[base + j] : 0.f;
+      sum += cache[i];
+    }
   }
   const float mean = wave_sum(sum) / (float)f;
   float var = 0.f;
 #pragma unroll
   for (int i = 0; i < RC; ++i) {
-    const int j = lane + 64 * i;
+    const int j = V4 ? 256 * (i >> 2) + 4 * lane + (i & 3) : lane + 64 * i;
     const float d = cache[i] - mean;
     var += j < f ? d * d : 0.f;
   }
   var = wave_sum(var) / (float)f;
   const float inv_std = 1.0f / sqrtf(var + eps);
+  if constexpr (V4) {
 #pragma unroll
-  for (int i = 0; i < RC; ++i) {
-    const int j = lane + 64 * i;
-    if (j < f) {
-      const float n = (cache[i] - mean) * inv_std;
-      out[base + j] = gamma[j] * n + beta[j];
-      if (res_out) res_out[base + j] = cache[i];
-      if (norm_out) norm_out[base + j] = n;
+    for (int i4 = 0; i4 < RC / 4; ++i4) {
+      const int j = 256 * i4 + 4 * lane;
+      if (j >= f) continue;
+      const vf4 g = *reinterpret_cast<const vf4 *>(gamma + j), be = *reinterpret_cast<const vf4 *>(beta + j);
+      vf4 n, y, r;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        r[c] = cache[4 * i4 + c];
+        n[c] = (r[c] - mean) * inv_std;
+        y[c] = g[c] * n[c] + be[c];
+      }
+      *reinterpret_cast<vf4 *>(out + base + j) = y;
+      if (res_out) *reinterpret_cast<vf4 *>(res_out + base + j) = r;
+      if (norm_out) *reinterpret_cast<vf4 *>(norm_out + base + j) = n;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < RC; ++i) {
+      const int j = lane + 64 * i;
+      if (j < f) {
+        const float n = (cache[i] - mean) * inv_std;
+        out[base + j] = gamma[j] * n + beta[j];
+        if (res_out) res_out[base + j] = cache[i];
+        if (norm_out) norm_out[base + j] = n;
+      }
     }
   }
   if (lane == 0) {
@@ -185,6 +220,113 @@ __global__ void __launch_bounds__(64 * WAVES) ln_backward_kernel(
       }
       part_g[(size_t)blockIdx.x * f + j] = sg;
       part_b[(size_t)blockIdx.x * f + j] = sb;
+    }
+    __syncthreads();
+  }
+}
+
+// The same with float4 columns (features % 4 == 0, 16-byte aligned rows, at
+// least 256 features of row cache): lane l owns columns 256 i + 4 l .. + 3,
+// so every load and store moves a float4.  The column partials of the
+// waves meet in LDS 256 columns at a time and two waves add them, in wave
+// order, for the workspace.
+template <int R4, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) ln_backward_vec_kernel(
+    const float *__restrict__ dout, const float *__restrict__ dout2,
+    const float *__restrict__ normalized, const float *__restrict__ gamma,
+    const float *__restrict__ x, const float *__restrict__ mean, const float *__restrict__ var,
+    float *__restrict__ dx, float *__restrict__ part_g, float *__restrict__ part_b, int rows,
+    int f, float eps) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row0 = blockIdx.x * kLnRowsPerBlock;
+  constexpr int U = R4 == 1 ? kLnRowsPerBlock / WAVES : 1;
+  const float inv_n = 1.0f / (float)f;
+  vf4 pg[R4], pb[R4], gm[R4];
+  bool colok[R4];
+#pragma unroll
+  for (int i = 0; i < R4; ++i) {
+    const int col = 256 * i + 4 * lane;
+    colok[i] = col < f;
+    gm[i] = colok[i] ? *reinterpret_cast<const vf4 *>(gamma + col) : vf4{0.f, 0.f, 0.f, 0.f};
+    pg[i] = pb[i] = vf4{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int rr0 = wave; rr0 < kLnRowsPerBlock; rr0 += WAVES * U) {
+    vf4 gv[U][R4], xm[U][R4];
+    float dvar[U], dmean[U], istd[U];
+    size_t base[U];
+    bool live[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int row = row0 + rr0 + WAVES * u;
+      live[u] = row < rows;
+      const int rc = live[u] ? row : rows - 1;
+      base[u] = (size_t)rc * f;
+      const float inv_std = 1.0f / sqrtf(var[rc] + eps);
+      const float inv_std3 = inv_std * inv_std * inv_std;
+      const float m = mean[rc];
+      istd[u] = inv_std;
+      dvar[u] = dmean[u] = 0.f;
+#pragma unroll
+      for (int i = 0; i < R4; ++i) {
+        gv[u][i] = xm[u][i] = vf4{0.f, 0.f, 0.f, 0.f};
+        if (!colok[i]) continue;
+        const size_t o = base[u] + 256 * i + 4 * lane;
+        vf4 g = *reinterpret_cast<const vf4 *>(dout + o);
+        if (dout2) g += *reinterpret_cast<const vf4 *>(dout2 + o);
+        const vf4 xv = *reinterpret_cast<const vf4 *>(x + o);
+        vf4 n;
+        if (normalized) n = *reinterpret_cast<const vf4 *>(normalized + o);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float xmj = xv[c] - m;
+          const float nj = normalized ? n[c] : xmj * inv_std;
+          if (live[u]) {
+            pg[i][c] += g[c] * nj;
+            pb[i][c] += g[c];
+          }
+          const float dnorm = g[c] * gm[i][c];
+          dvar[u] += dnorm * xmj * (-0.5f) * inv_std3;
+          dmean[u] += dnorm * (-inv_std);
+          xm[u][i][c] = xmj;
+        }
+        gv[u][i] = g;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      dvar[u] = wave_sum(dvar[u]);
+      dmean[u] = wave_sum(dmean[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (!live[u]) continue;
+      const float dvar_scale = dvar[u] * 2.0f * inv_n;
+      const float dmean_scale = dmean[u] * inv_n;
+#pragma unroll
+      for (int i = 0; i < R4; ++i) {
+        if (!colok[i]) continue;
+        vf4 y;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) y[c] = (gv[u][i][c] * gm[i][c]) * istd[u] + dvar_scale * xm[u][i][c] + dmean_scale;
+        *reinterpret_cast<vf4 *>(dx + base[u] + 256 * i + 4 * lane) = y;
+      }
+    }
+  }
+  __shared__ vf4 rg[WAVES][64], rb[WAVES][64];
+#pragma unroll
+  for (int i = 0; i < R4; ++i) {
+    if (256 * i >= f) break;  // uniform
+    rg[wave][lane] = pg[i];
+    rb[wave][lane] = pb[i];
+    __syncthreads();
+    if (threadIdx.x < 128) {
+      const int l = threadIdx.x & 63;
+      const bool isb = threadIdx.x >= 64;
+      vf4 sum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) sum += isb ? rb[w][l] : rg[w][l];
+      const int col = 256 * i + 4 * l;
+      if (col < f) *reinterpret_cast<vf4 *>((isb ? part_b : part_g) + (size_t)blockIdx.x * f + col) = sum;
     }
     __syncthreads();
   }
@@ -484,14 +626,27 @@ extern "C" int cdml_residual_layernorm_fwd(const float *a, const float *b, const
   if (rc) return rc;
   const dim3 grid((rows + 3) / 4), block(256);
   hipStream_t st = as_hip(stream);
-#define CDML_LN_FWD(RC) ln_forward_kernel<RC><<<grid, block, 0, st>>>(a, b, gamma, beta, out, mean, variance, residual, normalized, rows, features, eps)
-  switch (row_cache(features)) {
-    case 1: CDML_LN_FWD(1); break;
-    case 2: CDML_LN_FWD(2); break;
-    case 4: CDML_LN_FWD(4); break;
-    case 8: CDML_LN_FWD(8); break;
-    case 16: CDML_LN_FWD(16); break;
-    default: CDML_LN_FWD(32); break;
+  const int rcache = row_cache(features);
+  const bool v4 = rcache >= 4 && features % 4 == 0 && aligned16(a) && aligned16(b) && aligned16(gamma) &&
+                  aligned16(beta) && aligned16(out) && (!residual || aligned16(residual)) &&
+                  (!normalized || aligned16(normalized));
+#define CDML_LN_FWD(RC, V) ln_forward_kernel<RC, V><<<grid, block, 0, st>>>(a, b, gamma, beta, out, mean, variance, residual, normalized, rows, features, eps)
+  if (v4) {
+    switch (rcache) {
+      case 4: CDML_LN_FWD(4, true); break;
+      case 8: CDML_LN_FWD(8, true); break;
+      case 16: CDML_LN_FWD(16, true); break;
+      default: CDML_LN_FWD(32, true); break;
+    }
+  } else {
+    switch (rcache) {
+      case 1: CDML_LN_FWD(1, false); break;
+      case 2: CDML_LN_FWD(2, false); break;
+      case 4: CDML_LN_FWD(4, false); break;
+      case 8: CDML_LN_FWD(8, false); break;
+      case 16: CDML_LN_FWD(16, false); break;
+      default: CDML_LN_FWD(32, false); break;
+    }
   }
 #undef CDML_LN_FWD
   return check_launch("ln_forward_kernel");
@@ -529,9 +684,24 @@ extern "C" int cdml_layernorm_backward(const float *dout, const float *dout2,
   hipStream_t st = as_hip(stream);
   const int nblk = (rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock;
   float *pg = static_cast<float *>(workspace), *pb = pg + (size_t)nblk * features;
-  if (rows > 0) {
+  const int rcache = row_cache(features);
+  const bool vec = rcache >= 4 && features % 4 == 0 && aligned16(dout) && (!dout2 || aligned16(dout2)) &&
+                   (!normalized || aligned16(normalized)) && aligned16(gamma) && aligned16(input) &&
+                   aligned16(dinput) && aligned16(pg);
+  if (rows > 0 && vec) {
+#define CDML_LN_BWDV(RC) ln_backward_vec_kernel<RC / 4, ln_waves(RC)><<<dim3(nblk), dim3(64 * ln_waves(RC)), 0, st>>>(dout, dout2, normalized, gamma, input, mean, variance, dinput, pg, pb, rows, features, eps)
+    switch (rcache) {
+      case 4: CDML_LN_BWDV(4); break;
+      case 8: CDML_LN_BWDV(8); break;
+      case 16: CDML_LN_BWDV(16); break;
+      default: CDML_LN_BWDV(32); break;
+    }
+#undef CDML_LN_BWDV
+    rc = check_launch("ln_backward_vec_kernel");
+    if (rc) return rc;
+  } else if (rows > 0) {
 #define CDML_LN_BWD(RC) ln_backward_kernel<RC><<<dim3(nblk), dim3(64 * ln_waves(RC)), 0, st>>>(dout, dout2, normalized, gamma, input, mean, variance, dinput, pg, pb, rows, features, eps)
-    switch (row_cache(features)) {
+    switch (rcache) {
       case 1: CDML_LN_BWD(1); break;
       case 2: CDML_LN_BWD(2); break;
       case 4: CDML_LN_BWD(4); break;
