@@ -661,6 +661,27 @@ __global__ void __launch_bounds__(256) gemm_rows_kernel(const GemmArgs args) {
   if (has1) store_elem<EPI>(args, P, m, n0 + 1, z1, args.act);
 }
 
+// A short reduction (K <= 16: the input projection of a time-series model,
+// F features -> D), non-transposed operands: one output per thread, so the
+// stores, which are nearly all of the traffic, are coalesced along N; the
+// K values of the row and of W's row are read in k order.
+template <bool EPI>
+__global__ void __launch_bounds__(256) gemm_smallk_kernel(const GemmArgs args) {
+  const int prob = blockIdx.y;
+  const GemmProblem P = args.p[prob];
+  const int M = args.M, N = args.N, K = args.K;
+  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (e >= (long long)M * N) return;
+  const int m = (int)(e / N), n = (int)(e % N);
+  const float *__restrict__ x = P.a + (size_t)m * args.lda;
+  const float *__restrict__ w = P.w + (size_t)n * args.ldb;
+  float z = 0.f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k)
+    if (k < K) z += x[k] * w[k];
+  store_elem<EPI>(args, P, m, n, z + (P.bias ? P.bias[n] : 0.f), args.act);
+}
+
 // Any layout, any shape (the gradient GEMMs whose sizes miss the tiled
 // kernel's conditions): a 64 x 64 tile of C per 256-thread workgroup, 4 x 4
 // outputs per thread, K in steps of 16 through LDS with guarded loads that
@@ -923,6 +944,11 @@ __global__ void __launch_bounds__(256) wgrad_small_reduce_kernel(const GemmArgs 
   }
 }
 
+// The 256 x 128 eight-wave tiles for M >= 1024, and for weight gradients
+// (both operands transposed, a long row reduction split over chunks) whose
+// M is a multiple of 256; 128 x 128 four-wave tiles otherwise.
+inline bool big_tiles(int M, bool wgrad) { return M >= 1024 || (wgrad && M % 256 == 0); }
+
 SplitPlan splitk_plan(int M, int N, int K, int nprob) {
   SplitPlan sp;
   const int nk = K / 16;  // whole k-tiles; a ragged tail is added by a separate launch
@@ -939,7 +965,7 @@ SplitPlan splitk_plan(int M, int N, int K, int nprob) {
     sp.bytes = (size_t)sp.ksplit * nprob * ((size_t)M * N + M) * sizeof(float);
     return sp;
   }
-  const bool big = M >= 1024;
+  const bool big = big_tiles(M, true);
   const int TM = big ? 256 : 128, TN = 128;
   const int tiles = ((M + TM - 1) / TM) * ((N + TN - 1) / TN) * nprob;
   const int slots = big ? 512 : 1024;
@@ -1013,8 +1039,8 @@ bool stage_ok(const float *p, int rows, int ld, bool T, int bkk) {
 
 template <bool TA, bool TB>
 int launch_layout(GemmArgs &g, bool fast, hipStream_t stream) {
-  if (fast) return g.M >= 1024 ? launch_tile<256, 128, 16, 4, 2, 2, TA, TB>(g, stream)
-                               : launch_tile<128, 128, 16, 2, 2, 2, TA, TB>(g, stream);
+  if (fast) return big_tiles(g.M, TA && TB) ? launch_tile<256, 128, 16, 4, 2, 2, TA, TB>(g, stream)
+                                            : launch_tile<128, 128, 16, 2, 2, 2, TA, TB>(g, stream);
   const dim3 grid((g.N + 63) / 64, (g.M + 63) / 64, g.nprob);
   if (has_epi(g)) gemm_any_kernel<TA, TB, true><<<grid, dim3(256), 0, stream>>>(g);
   else gemm_any_kernel<TA, TB, false><<<grid, dim3(256), 0, stream>>>(g);
@@ -1078,6 +1104,13 @@ int launch_gemm(GemmArgs &g, bool ta, bool tb, hipStream_t stream, const char *w
   g.padded = pad_to_xcd(g.total);
   bool vec = (g.K % 4 == 0) && (g.lda % 4 == 0) && (g.ldb % 4 == 0);
   for (int i = 0; i < g.nprob; ++i) vec = vec && aligned16(g.p[i].a) && aligned16(g.p[i].w);
+  if (g.K <= 16 && g.K > 0 && g.M > 16 && !g.rope_cs && (long long)g.M * g.N <= (1LL << 38)) {
+    const long long n = (long long)g.M * g.N;
+    const dim3 grid((unsigned)((n + 255) / 256), (unsigned)g.nprob), block(256);
+    has_epi(g) ? gemm_smallk_kernel<true><<<grid, block, 0, stream>>>(g)
+               : gemm_smallk_kernel<false><<<grid, block, 0, stream>>>(g);
+    return check_launch(what);
+  }
   if (vec && g.M <= 16 && g.K > 0 && (g.rope_cs == nullptr || g.rope_hd % 2 == 0)) {
     const dim3 grid((unsigned)((g.N + 7) / 8), (unsigned)g.nprob), block(256);
     const bool epi = has_epi(g);

@@ -452,19 +452,30 @@ __global__ void __launch_bounds__(256) add_inplace_kernel(float *__restrict__ ta
 }
 
 // loss = (sum of the row terms, fixed order) / divisor, times loss_scale.
-__global__ void __launch_bounds__(256) ce_loss_kernel(const float *__restrict__ row_loss, int n,
-                                                      float divisor, float loss_scale,
-                                                      float *__restrict__ loss) {
-  __shared__ float red[256];
-  float s = 0.f;
-  for (int i = threadIdx.x; i < n; i += 256) s += row_loss[i];
-  red[threadIdx.x] = s;
+// One workgroup of 1024 threads; thread t keeps four running sums (rows
+// t + 1024 (4q + r) into sum r), so four loads per thread are in flight, and
+// the sums meet in a fixed tree.
+__global__ void __launch_bounds__(1024) ce_loss_kernel(const float *__restrict__ row_loss, int n,
+                                                       float divisor, float loss_scale,
+                                                       float *__restrict__ loss) {
+  __shared__ float red[1024];
+  const int t = threadIdx.x;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  int i = t;
+  for (; i + 3 * 1024 < n; i += 4 * 1024) {
+    s0 += row_loss[i];
+    s1 += row_loss[i + 1024];
+    s2 += row_loss[i + 2048];
+    s3 += row_loss[i + 3072];
+  }
+  for (; i < n; i += 1024) s0 += row_loss[i];
+  red[t] = (s0 + s1) + (s2 + s3);
   __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+  for (int w = 512; w > 0; w >>= 1) {
+    if (t < w) red[t] += red[t + w];
     __syncthreads();
   }
-  if (threadIdx.x == 0) *loss = (red[0] / divisor) * loss_scale;
+  if (t == 0) *loss = (red[0] / divisor) * loss_scale;
 }
 
 // AccumulateTokenEmbeddingGrad (AccelerationCPU.cs:2339-2370) as a gather: group
@@ -750,7 +761,7 @@ extern "C" int cdml_cross_entropy(const float *logits, int ldl, const int *targe
     if (rc) return rc;
   }
   if (effective_len == 0) return cdml_zero_f32_async(loss, 1, stream);
-  ce_loss_kernel<<<dim3(1), dim3(256), 0, st>>>(row_loss, effective_len, (float)effective_len, loss_scale,
+  ce_loss_kernel<<<dim3(1), dim3(1024), 0, st>>>(row_loss, effective_len, (float)effective_len, loss_scale,
                                                  loss);
   return check_launch("ce_loss_kernel");
 }
@@ -779,7 +790,7 @@ extern "C" int cdml_mse_loss(const float *pred, int ldp, const float *targets, i
     if (rc) return rc;
   }
   if (effective_len == 0) return cdml_zero_f32_async(loss, 1, stream);
-  ce_loss_kernel<<<dim3(1), dim3(256), 0, st>>>(row_loss, effective_len, (float)(effective_len * out_dim),
+  ce_loss_kernel<<<dim3(1), dim3(1024), 0, st>>>(row_loss, effective_len, (float)(effective_len * out_dim),
                                                  loss_scale, loss);
   return check_launch("ce_loss_kernel");
 }

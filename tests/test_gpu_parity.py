@@ -60,12 +60,15 @@ def test_project_qkv_shapes(rows, ind, out):
 
 
 @pytest.mark.parametrize("act", [0, 1, 2, 3, 4, 5])
-def test_linear_with_activation(act):
-    x = synth.normal(3, (77, 64))
-    w = synth.xavier_uniform(4, 130, 64)
-    b = synth.normal(5, (130,))
+@pytest.mark.parametrize("rows,ind,out", [(77, 64, 130), (300, 5, 256), (40, 16, 33), (3, 5, 7), (9, 12, 70)])
+def test_linear_with_activation(act, rows, ind, out):
+    """BatchDotProductAddBias + activation on the tiled shape, a short
+    reduction (the input projection of F 5 features, K 16) and few rows."""
+    x = synth.normal(3, (rows, ind))
+    w = synth.xavier_uniform(4, out, ind)
+    b = synth.normal(5, (out,))
     want = O.activation(O.batch_dot_add_bias(w, x, b), act)
-    parity(G.linear(x, w, b, act), want, f"linear act={act}")
+    parity(G.linear(x, w, b, act), want, f"linear {rows}x{ind}->{out} act={act}")
 
 
 def test_project_output_batch_reference_case():
