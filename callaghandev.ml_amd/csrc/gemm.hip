@@ -662,24 +662,51 @@ __global__ void __launch_bounds__(256) gemm_rows_kernel(const GemmArgs args) {
 }
 
 // A short reduction (K <= 16: the input projection of a time-series model,
-// F features -> D), non-transposed operands: one output per thread, so the
-// stores, which are nearly all of the traffic, are coalesced along N; the
-// K values of the row and of W's row are read in k order.
+// F features -> D), non-transposed operands, N * K <= kSmallKW: W is staged
+// in LDS as [K][N], and each thread computes four consecutive outputs of one
+// row -- the row's K values are the same for the 64 lanes of a wave that
+// share it (broadcast loads), W's four columns come from LDS, and the four
+// results leave as one float4 when the row layout allows it.  Every output
+// sums its K products in k order.
+constexpr int kSmallKW = 8192;
 template <bool EPI>
 __global__ void __launch_bounds__(256) gemm_smallk_kernel(const GemmArgs args) {
+  __shared__ float ws[kSmallKW];
   const int prob = blockIdx.y;
   const GemmProblem P = args.p[prob];
   const int M = args.M, N = args.N, K = args.K;
-  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (e >= (long long)M * N) return;
-  const int m = (int)(e / N), n = (int)(e % N);
-  const float *__restrict__ x = P.a + (size_t)m * args.lda;
-  const float *__restrict__ w = P.w + (size_t)n * args.ldb;
-  float z = 0.f;
+  for (int i = threadIdx.x; i < N * K; i += 256) {
+    const int n = i / K, k = i % K;
+    ws[k * N + n] = P.w[(size_t)n * args.ldb + k];
+  }
+  __syncthreads();
+  const int n4 = (N + 3) / 4;
+  const long long total = (long long)M * n4;
+  // grid-stride over the outputs, so W is staged once per workgroup
+  for (long long e = (long long)blockIdx.x * 256 + threadIdx.x; e < total; e += (long long)gridDim.x * 256) {
+    const int m = (int)(e / n4), n0 = (int)(e % n4) * 4;
+    const float *__restrict__ x = P.a + (size_t)m * args.lda;
+    float z[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int k = 0; k < 16; ++k)
-    if (k < K) z += x[k] * w[k];
-  store_elem<EPI>(args, P, m, n, z + (P.bias ? P.bias[n] : 0.f), args.act);
+    for (int k = 0; k < 16; ++k) {
+      if (k < K) {
+        const float xv = x[k];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) z[c] += xv * ws[k * N + min(n0 + c, N - 1)];
+      }
+    }
+    float *crow = P.c + (size_t)m * args.ldc;
+    if (!EPI && !args.beta && n0 + 3 < N && ((reinterpret_cast<uintptr_t>(crow + n0) & 15) == 0)) {
+      vf4 y;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) y[c] = activate(z[c] + (P.bias ? P.bias[n0 + c] : 0.f), args.act);
+      *reinterpret_cast<vf4 *>(crow + n0) = y;
+      continue;
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (n0 + c < N) store_elem<EPI>(args, P, m, n0 + c, z[c] + (P.bias ? P.bias[n0 + c] : 0.f), args.act);
+  }
 }
 
 // Any layout, any shape (the gradient GEMMs whose sizes miss the tiled
@@ -744,13 +771,15 @@ __global__ void __launch_bounds__(256) op_rowsum_kernel(const GemmArgs args) {
 
 // Sum of the split-K partials: C (+)= sum_c ws[c], bgrad += sum_c wsb[c].
 // N % 4 == 0 (the tiled path's transposed staging of opB needs it), so an
-// output is four consecutive columns.  Eight consecutive lanes share an
-// output: lane g adds chunks g, g + 8, g + 16, ... in order, and a fixed
-// xor-shuffle tree joins the eight sums, so the order of every addition is
-// fixed (the same bits on every run) while the chunk loads of eight lanes
-// are in flight together.  The group of output e also sums bias row e.
-constexpr int kReduceLanes = 8;
+// output is four consecutive columns.  LANES consecutive lanes share an
+// output: lane g adds chunks g, g + LANES, ... in order, and a fixed
+// xor-shuffle tree joins the sums, so the order of every addition is fixed
+// (the same bits on every run) while the chunk loads of the group are in
+// flight together.  The group of output e also sums bias row e.  Eight
+// lanes pay off from 32 chunks on; below that one lane walks the chunks.
+template <int LANES>
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs args) {
+  constexpr int kReduceLanes = LANES;
   const int prob = blockIdx.y;
   const GemmProblem P = args.p[prob];
   const int M = args.M, N = args.N, n4 = N >> 2;
@@ -1012,8 +1041,11 @@ int launch_tile(GemmArgs g, hipStream_t stream) {
     else
       gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_NONE, TA, TB, false><<<grid, block, 0, stream>>>(g);
     if (g.ksplit > 1) {
-      const size_t n = std::max((size_t)g.M * (g.N / 4), (size_t)g.M) * kReduceLanes;
-      splitk_reduce_kernel<<<dim3((unsigned)((n + 255) / 256), g.nprob), dim3(256), 0, stream>>>(g);
+      const size_t outs = std::max((size_t)g.M * (g.N / 4), (size_t)g.M);
+      if (g.ksplit >= 32)
+        splitk_reduce_kernel<8><<<dim3((unsigned)((outs * 8 + 255) / 256), g.nprob), dim3(256), 0, stream>>>(g);
+      else
+        splitk_reduce_kernel<1><<<dim3((unsigned)((outs + 255) / 256), g.nprob), dim3(256), 0, stream>>>(g);
     }
   } else {
     if (g.rope_cs) {
@@ -1104,9 +1136,10 @@ int launch_gemm(GemmArgs &g, bool ta, bool tb, hipStream_t stream, const char *w
   g.padded = pad_to_xcd(g.total);
   bool vec = (g.K % 4 == 0) && (g.lda % 4 == 0) && (g.ldb % 4 == 0);
   for (int i = 0; i < g.nprob; ++i) vec = vec && aligned16(g.p[i].a) && aligned16(g.p[i].w);
-  if (g.K <= 16 && g.K > 0 && g.M > 16 && !g.rope_cs && (long long)g.M * g.N <= (1LL << 38)) {
-    const long long n = (long long)g.M * g.N;
-    const dim3 grid((unsigned)((n + 255) / 256), (unsigned)g.nprob), block(256);
+  if (g.K <= 16 && g.K > 0 && g.M > 16 && !g.rope_cs && g.N * g.K <= kSmallKW &&
+      (long long)g.M * g.N <= (1LL << 38)) {
+    const long long n = (long long)g.M * ((g.N + 3) / 4);
+    const dim3 grid((unsigned)std::min<long long>((n + 255) / 256, 2048), (unsigned)g.nprob), block(256);
     has_epi(g) ? gemm_smallk_kernel<true><<<grid, block, 0, stream>>>(g)
                : gemm_smallk_kernel<false><<<grid, block, 0, stream>>>(g);
     return check_launch(what);
