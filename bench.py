@@ -52,7 +52,7 @@ HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, AMD published
 # HBM bytes per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded in
 # profiles/mha_c3_decode_c4_hbm_traffic.md (FETCH_SIZE scaled by 1.99918, the factor a
 # 64 MiB device copy reads on that counter; WRITE_SIZE by 1.0).
-TRAFFIC_BYTES = {"flash_c3": 977267744, "decode_c4": 8643184928}
+TRAFFIC_BYTES = {"flash_c3": 1047999283, "decode_c4": 8643213076}
 
 # c3: one MHA layer of the long-context stack
 C3 = dict(batch=4, seq=4096, dim=1024, heads=16)
