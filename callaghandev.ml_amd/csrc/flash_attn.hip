@@ -430,9 +430,12 @@ __global__ void __launch_bounds__(256) flash_generic_kernel(const FlashArgs a, i
 template <int HD, int BN, bool CAUSAL, bool HAS_MASK>
 void launch_tpl(FlashArgs a, bool vec, hipStream_t st) {
   // Pairs of causal tiles when one tile per workgroup would fit in a single
-  // round of resident workgroups (four per CU): then the round lasts as long
-  // as its longest tile.
-  const bool pair = CAUSAL && a.n_qt > 1 && (long long)a.n_bh * a.n_qt <= 4LL * num_cus();
+  // round of resident workgroups (four per CU), so that the round lasts as
+  // long as its longest tile, and the pairs still give every CU two
+  // workgroups (fewer would leave SIMDs with a single wave).
+  const long long cus = num_cus();
+  const bool pair = CAUSAL && a.n_qt > 1 && (long long)a.n_bh * a.n_qt <= 4 * cus &&
+                    (long long)a.n_bh * ((a.n_qt + 1) / 2) >= 2 * cus;
   a.total = pair ? a.n_bh * ((a.n_qt + 1) / 2) : a.n_bh * a.n_qt;
   if constexpr (CAUSAL) {
     if (pair) {
