@@ -486,3 +486,24 @@ def test_device_trainer_epochs_equal_batch_steps(kind):
     wa, wb = a.weights(), b.weights()
     for k in wa:
         assert np.array_equal(wa[k], wb[k]), k
+
+
+def test_device_trainer_steps_are_deterministic():
+    """Every reduction in the training step runs in a fixed order and no
+    kernel uses atomics, so two trainers from the same weights on the same
+    batches end with the same bits.  The shape takes split-K weight gradients
+    with a ragged tail (2 x 1023 rows), the stored-dS attention backward
+    (head dim 64) and vectorised LayerNorm (D 256)."""
+    cfg = {"vocab": 300, "dim": 256, "heads": 4, "layers": 2, "ff": 512, "max_seq": 1024}
+    w = synth.lm_weights(cfg, 77)
+    seqs = list(synth.token_ids(78, 2 * 1024, 300).reshape(2, 1024))
+    short = list(synth.token_ids(79, 3 * 300, 300).reshape(3, 300))
+    runs = []
+    for _ in range(2):
+        t, _ = _trainer(cfg, w, 3, 1023)
+        losses = [t.TrainBatch(seqs, 0.01), t.TrainBatch(short, 0.01), t.TrainBatch(seqs, 0.01)]
+        runs.append((losses, t.weights(), t.last_norm))
+    (la, wa, na), (lb, wb, nb) = runs
+    assert la == lb and na == nb
+    for k in wa:
+        assert np.array_equal(wa[k], wb[k]), k
