@@ -580,7 +580,7 @@ __global__ void __launch_bounds__(BW_THREADS, 2) flash_bwd_dq_ds_kernel(const Bw
   __syncthreads();
 
   for (int kt = 0; kt < n_kt; ++kt) {
-    const int buf = kt & 1;
+    const int lbuf = kt & 1;
     const int k0 = kt * BN;
     sk.load(kbase, a.ldk, kt + 1 < n_kt ? k0 + BN : k0, a.lk, HD);
 #pragma unroll
@@ -591,7 +591,7 @@ __global__ void __launch_bounds__(BW_THREADS, 2) flash_bwd_dq_ds_kernel(const Bw
 #pragma unroll
         for (int i = 0; i < 4; ++i) n2[i] = *reinterpret_cast<const vf4 *>(dsw + (size_t)(j + 2) * 1024 + 4 * i);
       }
-      const float(*krow)[HD + 4] = &Ks[buf][kb * 32];
+      const float(*krow)[HD + 4] = &Ks[lbuf][kb * 32];
 #pragma unroll
       for (int st = 0; st < 16; ++st) {
         const float av = cur[st >> 2][st & 3];
@@ -604,7 +604,7 @@ __global__ void __launch_bounds__(BW_THREADS, 2) flash_bwd_dq_ds_kernel(const Bw
         n1[i] = n2[i];
       }
     }
-    sk.store(Ks[buf ^ 1]);
+    sk.store(Ks[lbuf ^ 1]);
     __syncthreads();
   }
 
@@ -615,6 +615,93 @@ __global__ void __launch_bounds__(BW_THREADS, 2) flash_bwd_dq_ds_kernel(const Bw
       float *dqrow = a.dq + ((size_t)b * a.lq + q) * a.lddq + col0;
 #pragma unroll
       for (int db = 0; db < NDB; ++db) dqrow[db * 32 + li] = dq[db][r] * a.scale;
+    }
+  }
+}
+
+// dQ from the stored dS blocks for short sequences (lq <= 32 * MAXQB): one
+// workgroup per (sequence, head) stages the head's whole K in LDS once; wave
+// w owns query blocks w and nqb - 1 - w, so every wave has nqb + 1 key
+// blocks of work (the middle block of an odd count alone) and no barrier
+// follows the staging.  Operand order and the per-block product are those
+// of flash_bwd_dq_ds_kernel, with the dS operands four blocks ahead (a block
+// is about a thousand MFMA cycles at head dim 32, short of the load latency).
+template <int HD, int MAXQB>
+__global__ void __launch_bounds__(64 * (MAXQB / 2)) flash_bwd_dq_ds_short_kernel(const BwdArgs a) {
+  constexpr int NDB = HD / 32;
+  __shared__ __attribute__((aligned(16))) float Ks[32 * MAXQB][HD + 4];
+  const int bh = blockIdx.x;
+  const int b = bh / a.heads, h = bh % a.heads;
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int li = lane & 31, hf = lane >> 5;
+  const int nqb = (a.lq + 31) >> 5;
+  const int col0 = h * HD;
+  // K rows [0, 32 nqb) of the head, rows past lk clamped (their dS is 0)
+  {
+    const float *kbase = a.k + (size_t)b * a.lk * a.ldk + col0;
+    constexpr int F4 = HD / 4;
+    for (int e = t; e < 32 * nqb * F4; e += blockDim.x) {
+      const int r = e / F4, c = (e % F4) * 4;
+      *reinterpret_cast<vf4 *>(&Ks[r][c]) =
+          *reinterpret_cast<const vf4 *>(kbase + (size_t)min(r, a.lk - 1) * a.ldk + c);
+    }
+  }
+  __syncthreads();
+  const float *__restrict__ dsbh = a.ds + (size_t)bh * a.ds_bh + li * 32 + hf * 16;
+  for (int pass = 0; pass < 2; ++pass) {
+    const int qi = pass == 0 ? nqb - 1 - wave : wave;
+    if (pass == 1 && qi >= nqb - 1 - wave) break;  // the middle block ran in pass 0
+    const float *dsw = dsbh + (size_t)qi * (qi + 1) / 2 * 1024;
+    floatx16 dq[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dq[db][r] = 0.f;
+    // dS operands PF blocks ahead in a ring: block j lives in buf[j % PF]
+    // (the loop is unrolled by PF, so every index is a constant and no
+    // in-flight load is ever copied), and the load of block j + PF goes into
+    // the buffer block j has just left.
+    // dS operands PF blocks ahead in a ring: block j lives in buf[j % PF]
+    // (the loop is unrolled by PF, so every index is a constant and no
+    // in-flight load is ever copied), and the load of block j + PF goes into
+    // the buffer block j has just left.
+    constexpr int PF = 4;
+    vf4 buf[PF][4];
+#pragma unroll
+    for (int p = 0; p < PF; ++p)
+      if (p <= qi) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) buf[p][i] = *reinterpret_cast<const vf4 *>(dsw + (size_t)p * 1024 + 4 * i);
+      }
+    for (int j0 = 0; j0 <= qi; j0 += PF) {
+#pragma unroll
+      for (int u = 0; u < PF; ++u) {
+        const int j = j0 + u;
+        if (j > qi) break;
+        const float(*krow)[HD + 4] = &Ks[j * 32];
+#pragma unroll
+        for (int st = 0; st < 16; ++st) {
+          const float av = buf[u][st >> 2][st & 3];
+#pragma unroll
+          for (int db = 0; db < NDB; ++db) dq[db] = mfma32x32x2(av, krow[2 * st + hf][db * 32 + li], dq[db]);
+        }
+        if (j + PF <= qi) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            buf[u][i] = *reinterpret_cast<const vf4 *>(dsw + (size_t)(j + PF) * 1024 + 4 * i);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int q = qi * 32 + acc_row(r) + 4 * hf;
+      if (q < a.lq) {
+        float *dqrow = a.dq + ((size_t)b * a.lq + q) * a.lddq + col0;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) dqrow[db * 32 + li] = dq[db][r] * a.scale;
+      }
     }
   }
 }
@@ -743,7 +830,12 @@ void launch_bwd(BwdArgs &a, hipStream_t st) {
   if constexpr (CAUSAL && !HAS_MASK && VEC && HD <= 64) {
     if (a.ds) {  // dQ from the stored dS blocks
       flash_bwd_dkdv_kernel<HD, BQ, true, false, true, true><<<dim3(n_bh * kt), dim3(BW_THREADS), 0, st>>>(a);
-      flash_bwd_dq_ds_kernel<HD, 64><<<dim3(n_bh * a.n_tiles), dim3(BW_THREADS), 0, st>>>(a);
+      constexpr int kShortQB = HD <= 32 ? 16 : 8;  // the whole K of a head in LDS: 72 KB at most
+      const int nqb = (a.lq + 31) / 32;
+      if (nqb <= kShortQB)
+        flash_bwd_dq_ds_short_kernel<HD, kShortQB><<<dim3(n_bh), dim3(64 * ((nqb + 1) / 2)), 0, st>>>(a);
+      else
+        flash_bwd_dq_ds_kernel<HD, 64><<<dim3(n_bh * a.n_tiles), dim3(BW_THREADS), 0, st>>>(a);
       return;
     }
   }

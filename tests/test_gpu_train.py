@@ -266,7 +266,8 @@ def test_device_trainer_loss_decreases():
 
 
 @pytest.mark.parametrize("batch,L,dim,heads", [(2, 300, 128, 2), (1, 257, 256, 2), (3, 130, 96, 3), (2, 64, 512, 4),
-                                               (4, 63, 64, 4), (2, 100, 96, 2)])
+                                               (4, 63, 64, 4), (2, 100, 96, 2), (2, 200, 128, 2), (1, 512, 256, 8),
+                                               (3, 33, 64, 2)])
 def test_sdpa_bwd_from_saved_statistics(batch, L, dim, heads):
     """The trainer's attention backward from the forward's saved output and
     row statistics (cdml_sdpa_fwd_lse + cdml_sdpa_bwd_saved) gives the same
