@@ -516,3 +516,55 @@ def test_embed_tokens_exact():
     assert bad == 0 and np.array_equal(out, O.embed_tokens(ids, t2))
     out, bad = G.embed([1, 200, -1], t2)
     assert bad == 2 and np.all(out[1:] == 0) and np.array_equal(out[0], t2[1])
+
+
+def test_graph_capture_replays_the_recorded_launches():
+    """cdml_graph_capture_begin / _end / _launch: a recorded sequence of
+    launches (a linear layer with ReLU, a fill, a second linear layer into
+    another buffer) replays with the recorded pointers, so new inputs
+    uploaded between replays give new results; every replay, with eager
+    launches and synchronisations between them, matches the eager result.
+    Recording on the default stream is refused, and a graph handle of NULL is
+    an argument error."""
+    import ctypes as C
+    lib = N.lib()
+    st = N.Stream()  # a stream of its own: capture must not see the helpers' stream
+    s = st.handle
+    rows, ind, hid, out = 40, 64, 96, 24
+    w1, w2 = synth.xavier_uniform(1, hid, ind), synth.xavier_uniform(2, out, hid)
+    b1, b2 = synth.normal(3, (hid,)), synth.normal(4, (out,))
+    dw1, dw2, db1, db2 = (N.DeviceBuffer.from_array(a, st) for a in (w1, w2, b1, b2))
+    dx, dh, dy = N.DeviceBuffer(rows * ind * 4), N.DeviceBuffer(rows * hid * 4), N.DeviceBuffer(rows * out * 4)
+    dcount = N.DeviceBuffer(64 * 4)
+
+    def enqueue():
+        N.check(lib.cdml_linear(dx.ptr, ind, dw1.ptr, db1.ptr, dh.ptr, hid, rows, ind, hid, 3, s))
+        N.check(lib.cdml_fill_i32_async(dcount.ptr, 64, 7, s))
+        N.check(lib.cdml_linear(dh.ptr, hid, dw2.ptr, db2.ptr, dy.ptr, out, rows, hid, out, 0, s))
+
+    def expected(x):
+        h = O.activation(O.batch_dot_add_bias(w1, x, b1), 3)
+        return O.batch_dot_add_bias(w2, h, b2)
+
+    N.check(lib.cdml_graph_capture_begin(s))
+    enqueue()
+    g = C.c_void_p()
+    N.check(lib.cdml_graph_capture_end(s, C.byref(g)))
+    assert g.value
+    try:
+        for rep in range(4):
+            x = synth.normal(10 + rep, (rows, ind))
+            dx.upload(x, st)
+            N.check(lib.cdml_graph_launch(g, s))
+            st.synchronize()
+            got = dy.download((rows, out), np.float32, st)
+            parity(got, expected(x), f"replay {rep}")
+            assert np.all(dcount.download((64,), np.int32, st) == 7)
+            # eager work on the same buffers between replays
+            enqueue()
+            st.synchronize()
+            assert np.array_equal(dy.download((rows, out), np.float32, st), got)
+    finally:
+        N.check(lib.cdml_graph_destroy(g))
+    assert lib.cdml_graph_launch(None, s) == N.E_INVALID
+    assert lib.cdml_graph_capture_begin(None) == N.E_INVALID
