@@ -50,6 +50,8 @@ SIGNATURES = {
     "cdml_graph_capture_end": [_vp, C.POINTER(_vp)],
     "cdml_graph_launch": [_vp, _vp],
     "cdml_graph_destroy": [_vp],
+    "cdml_tiny_layer_check": [_vp, _i],
+    "cdml_tiny_decode": [_vp, _vp, _i, _i, _i, _vp],
     "cdml_event_create": [C.POINTER(_vp)],
     "cdml_event_destroy": [_vp],
     "cdml_event_record": [_vp, _vp],

@@ -628,6 +628,8 @@ PYBIND11_MODULE(_cdml_host, m) {
              return to_numpy(d.ForwardContinuous(X.view, batch, seqLen));
            })
       .def_readwrite("use_graphs", &DeviceLanguageModel::use_graphs)
+      .def_readwrite("use_fused_decode", &DeviceLanguageModel::use_fused_decode)
+      .def_property_readonly("fused_decode_available", &DeviceLanguageModel::fused_decode_available)
       .def("GenerateGreedy",
            [](DeviceLanguageModel &d, py::object prompts, int maxNew) {
              I32 a = I32::ensure(prompts);

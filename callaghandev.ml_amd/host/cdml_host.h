@@ -414,6 +414,10 @@ class DeviceLanguageModel {
   // the token choices) once per (batch, promptLen, n) and replays it as one
   // graph launch; off, every kernel is launched from the host.
   bool use_graphs = true;
+  // Decode steps of a small model (cdml_tiny_decode's limits) run in one
+  // fused launch; off, each step runs the per-kernel path.
+  bool use_fused_decode = true;
+  bool fused_decode_available() const { return tiny_ok_; }
 
  private:
   struct Layer {
@@ -444,6 +448,8 @@ class DeviceLanguageModel {
   size_t ws_bytes_ = 0;
   int ff_max_ = 0;
   std::map<std::tuple<int, int, int>, cdml_graph> graphs_;  // (batch, promptLen, n)
+  cdml_tiny_model tiny_{};  // descriptors for cdml_tiny_decode (layers in device memory)
+  bool tiny_ok_ = false;
 };
 
 // ---- device-resident training --------------------------------------------

@@ -409,6 +409,53 @@ DeviceLanguageModel::DeviceLanguageModel(const LanguageModel &model, int batch_c
     // (cos, sin) of every position the model can see, shared by all layers
     rope_cs_ = alloc((size_t)S * (D / cfg_.NumHeads));
     check(cdml_rope_table(rope_cs_, S, D / cfg_.NumHeads, 10000.0f, stream_), "cdml_rope_table");
+    // descriptors of the fused decode path, when the model is within its limits
+    if (cfg_.UsesDiscreteTokens && cfg_.UseDecoderOnly && D <= 256 && (D / cfg_.NumHeads) % 4 == 0 &&
+        (long long)cfg_.NumHeads * S <= 4096) {
+      std::vector<cdml_tiny_layer> tl(layers_.size());
+      bool ok = true;
+      for (size_t i = 0; i < layers_.size() && ok; ++i) {
+        const Layer &L = layers_[i];
+        cdml_tiny_layer &T = tl[i];
+        T.wq = L.wq; T.bq = L.bq; T.wk = L.wk; T.bk = L.bk; T.wv = L.wv; T.bv = L.bv; T.wo = L.wo; T.bo = L.bo;
+        T.ln1g = L.ln1g; T.ln1b = L.ln1b; T.ln2g = L.ln2g; T.ln2b = L.ln2b;
+        T.n_ff = (int)L.ffw.size();
+        if (T.n_ff > CDML_TINY_MAX_FF) {
+          ok = false;
+          break;
+        }
+        for (int f = 0; f < T.n_ff; ++f) {
+          T.ffw[f] = L.ffw[f];
+          T.ffb[f] = L.ffb[f];
+          T.ffrows[f] = L.ffrows[f];
+          T.ffcols[f] = L.ffcols[f];
+          T.ffact[f] = L.ffact[f];
+        }
+        T.kcache = L.kcache;
+        T.vcache = L.vcache;
+        ok = cdml_tiny_layer_check(&T, D) == CDML_OK;
+      }
+      if (ok) {
+        void *dev = nullptr;
+        if (!tl.empty()) {
+          check(cdml_malloc(&dev, tl.size() * sizeof(cdml_tiny_layer)), "cdml_malloc");
+          allocs_.push_back(dev);
+          check(cdml_memcpy_h2d_async(dev, tl.data(), tl.size() * sizeof(cdml_tiny_layer), stream_), "upload");
+        }
+        tiny_.embedding = emb_;
+        tiny_.out_w = outproj_;
+        tiny_.out_b = outbias_;
+        tiny_.rope_cs = rope_cs_;
+        tiny_.layers = static_cast<const cdml_tiny_layer *>(dev);
+        tiny_.n_layers = (int)tl.size();
+        tiny_.dim = D;
+        tiny_.heads = cfg_.NumHeads;
+        tiny_.vocab = cfg_.VocabSize;
+        tiny_.max_seq = S;
+        tiny_.eps = 1e-5f;
+        tiny_ok_ = true;
+      }
+    }
     synchronize();
   } catch (...) {
     for (void *p : allocs_) cdml_free(p);
@@ -567,6 +614,10 @@ void DeviceLanguageModel::generate_device(int batch, int promptLen, int n) {
                     batch, D, V, CDML_ACT_NONE, stream_),
         "output projection");
   check(cdml_argmax_rows(logits_, batch, V, V, gen_, 1, stream_), "argmax");
+  if (use_fused_decode && tiny_ok_ && n > 1) {  // every later step in one launch
+    check(cdml_tiny_decode(&tiny_, gen_, batch, promptLen, n - 1, stream_), "cdml_tiny_decode");
+    return;
+  }
   for (int s = 1; s < n; ++s) {
     decode_step(gen_ + (size_t)(s - 1) * batch, batch, promptLen + s - 1, x_);
     check(cdml_linear(x_, D, outproj_, outbias_, logits_, V, batch, D, V, CDML_ACT_NONE, stream_),

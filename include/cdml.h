@@ -487,6 +487,53 @@ int cdml_embed_tokens(const int *ids, int count, const float *table, int vocab,
 int cdml_argmax_rows(const float *x, int rows, int cols, int ld, int *out,
                      int out_stride, cdml_stream stream);
 
+/* ---- whole greedy decode steps of a small decoder-only model in one launch.
+ * LanguageModel.Generate's per-token loop (LanguageModel.cs:482-537) runs
+ * DecoderSelfAttentionStep (:334-430) in every post-LN block
+ * (TransformerBlock.cs:35-44), then the LM head and the token choice.  For a
+ * model of D <= 256 that is two dozen launches of microseconds each per
+ * token; here one workgroup per sequence runs every step in one launch.
+ *
+ * Step s = 1 .. n_steps feeds token tokens[(s - 1) * batch + b] of sequence
+ * b at position pos0 + s - 1. It goes through every layer:
+ *   - Q/K/V with RoPE from rope_cs (as cdml_rope_table writes it);
+ *   - K and V appended as row pos0 + s - 1 of the layer's caches
+ *     ([batch, max_seq, dim]);
+ *   - attention over the pos0 + s keys so far, scale 1 / sqrt(dim / heads);
+ *   - output projection, residual LayerNorm (eps), the FFN layers, residual
+ *     LayerNorm.
+ * The LM head's argmax (lowest index on ties, 0 when every logit is NaN,
+ * as cdml_argmax_rows) goes to tokens[s * batch + b].
+ *
+ * Limits: dim <= 256 with a head dim that is a multiple of 4, FFN widths
+ * <= 1024 and multiples of 4, heads * max_seq <= 4096, pos0 + n_steps <=
+ * max_seq; every weight row 16-byte aligned.  `layers` is a device array of
+ * n_layers descriptors; every pointer in it is device memory, and each layer
+ * is first checked with cdml_tiny_layer_check on the host copy.  No
+ * counterpart in the reference's interface: it is the device engine's
+ * generation loop. */
+#define CDML_TINY_MAX_FF 4
+typedef struct {
+  const float *wq, *bq, *wk, *bk, *wv, *bv, *wo, *bo;  /* [dim, dim], [dim] */
+  const float *ln1g, *ln1b, *ln2g, *ln2b;              /* [dim] */
+  const float *ffw[CDML_TINY_MAX_FF];  /* [ffrows[f], ffcols[f]] */
+  const float *ffb[CDML_TINY_MAX_FF];  /* [ffrows[f]] */
+  int ffrows[CDML_TINY_MAX_FF], ffcols[CDML_TINY_MAX_FF], ffact[CDML_TINY_MAX_FF];
+  int n_ff;
+  float *kcache, *vcache;  /* [batch capacity, max_seq, dim] */
+} cdml_tiny_layer;
+typedef struct {
+  const float *embedding;      /* [vocab, dim] */
+  const float *out_w, *out_b;  /* [vocab, dim], [vocab] */
+  const float *rope_cs;        /* [max_seq, dim / heads / 2] (cos, sin) pairs */
+  const cdml_tiny_layer *layers;
+  int n_layers, dim, heads, vocab, max_seq;
+  float eps;
+} cdml_tiny_model;
+int cdml_tiny_layer_check(const cdml_tiny_layer *layer, int dim);
+int cdml_tiny_decode(const cdml_tiny_model *model, int *tokens, int batch,
+                     int pos0, int n_steps, cdml_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

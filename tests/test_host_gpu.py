@@ -352,6 +352,30 @@ def test_generate_graph_replays_match_eager():
         dev.use_graphs = True
 
 
+@pytest.mark.parametrize("name", ["c1", "deep_ffn"])
+def test_generate_fused_decode_matches_per_kernel_path(name):
+    """The fused decode launch (every step after the prefill in one kernel)
+    against the per-kernel decode steps of the same model: identical greedy
+    tokens for several prompt lengths, up to the MaxSequenceLength cap, and
+    the same KV caches' effect on later tokens."""
+    Hm = host.module()
+    if name == "c1":
+        cfg = {"vocab": 200, "dim": 64, "heads": 4, "layers": 2, "ff": 128, "max_seq": 64}
+    else:
+        cfg = {"vocab": 97, "dim": 32, "heads": 2, "layers": 3, "ff": 48, "max_seq": 40}
+    lm, _ = host.language_model(cfg, synth.lm_weights(cfg, 12, biased=True))
+    fused, plain = Hm.DeviceLanguageModel(lm, 4), Hm.DeviceLanguageModel(lm, 4)
+    assert fused.fused_decode_available
+    plain.use_fused_decode = False
+    S = cfg["max_seq"]
+    ids = synth.token_ids(13, 4 * S, cfg["vocab"]).reshape(4, S)
+    for plen, n in ((1, 10), (5, 20), (S // 2, 30), (S - 3, 20)):
+        got = fused.GenerateGreedy(ids[:, :plen], n)
+        want = plain.GenerateGreedy(ids[:, :plen], n)
+        assert got.shape == want.shape == (4, min(S, plen + n))
+        assert np.array_equal(got, want), f"prompt {plen}, {n} tokens"
+
+
 def _oracle_continuous(cfg, w, x):
     """LanguageModel.Forward(float[,]) from oracle functions: input projection,
     post-LN blocks, output projection."""
