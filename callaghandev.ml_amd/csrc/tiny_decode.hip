@@ -272,6 +272,8 @@ extern "C" int cdml_tiny_decode(const cdml_tiny_model *model, int *tokens, int b
     return fail(CDML_E_INVALID, "cdml_tiny_decode: positions past MaxSequenceLength");
   if (!m.embedding || !m.out_w || !m.out_b || !m.rope_cs || (m.n_layers > 0 && !m.layers))
     return fail(CDML_E_INVALID, "cdml_tiny_decode: NULL model pointer");
+  if (!aligned16(m.embedding) || !aligned16(m.out_w))
+    return fail(CDML_E_INVALID, "cdml_tiny_decode: embedding and LM head must be 16-byte aligned");
   int rc = ensure_device();
   if (rc) return rc;
   tiny_decode_kernel<<<dim3((unsigned)batch), dim3(kTinyThreads), 0, as_hip(stream)>>>(m, tokens, batch, pos0,
@@ -284,10 +286,21 @@ extern "C" int cdml_tiny_layer_check(const cdml_tiny_layer *layer, int dim) {
   const cdml_tiny_layer &L = *layer;
   if (L.n_ff < 1 || L.n_ff > CDML_TINY_MAX_FF)
     return fail(CDML_E_INVALID, "cdml_tiny_layer_check: %d FFN layers (1 to %d)", L.n_ff, CDML_TINY_MAX_FF);
+  // Weight rows and cache rows are read as float4.
+  const float *vec4[] = {L.wq, L.wk, L.wv, L.wo, L.kcache, L.vcache};
+  for (const float *p : vec4)
+    if (!p || !aligned16(p))
+      return fail(CDML_E_INVALID, "cdml_tiny_layer_check: NULL or unaligned weight or cache pointer");
+  if (!L.ln1g || !L.ln1b || !L.ln2g || !L.ln2b)  // biases may be NULL (zero)
+    return fail(CDML_E_INVALID, "cdml_tiny_layer_check: NULL LayerNorm pointer");
   int width = dim;
   for (int f = 0; f < L.n_ff; ++f) {
     if (L.ffcols[f] != width || L.ffrows[f] <= 0 || L.ffrows[f] > kTinyMaxFF || L.ffrows[f] % 4)
       return fail(CDML_E_INVALID, "cdml_tiny_layer_check: FFN layer %d is %d x %d", f, L.ffrows[f], L.ffcols[f]);
+    if (!L.ffw[f] || !aligned16(L.ffw[f]))
+      return fail(CDML_E_INVALID, "cdml_tiny_layer_check: FFN layer %d has a NULL or unaligned pointer", f);
+    if (L.ffact[f] < CDML_ACT_NONE || L.ffact[f] > CDML_ACT_SWISH)
+      return fail(CDML_E_INVALID, "cdml_tiny_layer_check: FFN layer %d activation %d", f, L.ffact[f]);
     width = L.ffrows[f];
   }
   if (width != dim) return fail(CDML_E_INVALID, "cdml_tiny_layer_check: FFN output width %d != dim %d", width, dim);

@@ -72,3 +72,71 @@ def test_no_device_is_reported_not_faked():
     assert N.lib().cdml_init(0) == N.E_NODEVICE
     with pytest.raises(N.CdmlError):
         N.DeviceBuffer(1024)
+
+
+class _TinyLayer(C.Structure):
+    """ctypes mirror of cdml_tiny_layer (include/cdml.h)."""
+    _fields_ = [(n, C.c_void_p) for n in ("wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo",
+                                           "ln1g", "ln1b", "ln2g", "ln2b")] + [
+        ("ffw", C.c_void_p * 4), ("ffb", C.c_void_p * 4), ("ffrows", C.c_int * 4),
+        ("ffcols", C.c_int * 4), ("ffact", C.c_int * 4), ("n_ff", C.c_int),
+        ("kcache", C.c_void_p), ("vcache", C.c_void_p)]
+
+
+class _TinyModel(C.Structure):
+    """ctypes mirror of cdml_tiny_model (include/cdml.h)."""
+    _fields_ = [("embedding", C.c_void_p), ("out_w", C.c_void_p), ("out_b", C.c_void_p),
+                ("rope_cs", C.c_void_p), ("layers", C.c_void_p), ("n_layers", C.c_int),
+                ("dim", C.c_int), ("heads", C.c_int), ("vocab", C.c_int), ("max_seq", C.c_int),
+                ("eps", C.c_float)]
+
+
+def _tiny_layer(dim=64, widths=(128, 64), acts=(3, 0)):
+    # Addresses are never dereferenced: the checks read only the descriptor.
+    L = _TinyLayer()
+    for i, n in enumerate(("wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo",
+                           "ln1g", "ln1b", "ln2g", "ln2b", "kcache", "vcache")):
+        setattr(L, n, 0x10000 + 256 * i)
+    cols = dim
+    for f, (w, a) in enumerate(zip(widths, acts)):
+        L.ffw[f], L.ffb[f] = 0x20000 + 256 * f, 0x30000 + 256 * f
+        L.ffrows[f], L.ffcols[f], L.ffact[f] = w, cols, a
+        cols = w
+    L.n_ff = len(widths)
+    return L
+
+
+def test_tiny_decode_descriptor_checks():
+    lib = N.lib()
+    check = lambda L, dim=64: lib.cdml_tiny_layer_check(C.byref(L), dim)
+    assert check(_tiny_layer()) == N.OK
+    assert check(_tiny_layer(), 32) == N.E_INVALID                       # first FFN width != dim
+    assert check(_tiny_layer(widths=(128, 32))) == N.E_INVALID           # last width != dim
+    assert check(_tiny_layer(widths=(130, 64))) == N.E_INVALID           # width not a multiple of 4
+    assert check(_tiny_layer(widths=(2048, 64))) == N.E_INVALID          # width past 1024
+    assert check(_tiny_layer(acts=(9, 0))) == N.E_INVALID                # activation code
+    assert check(_tiny_layer(widths=(), acts=())) == N.E_INVALID         # no FFN layer
+    L = _tiny_layer(); L.wk = 0x10004
+    assert check(L) == N.E_INVALID                                       # unaligned weight
+    L = _tiny_layer(); L.vcache = None
+    assert check(L) == N.E_INVALID                                       # no cache
+    L = _tiny_layer(); L.ln2b = None
+    assert check(L) == N.E_INVALID                                       # no LayerNorm shift
+    L = _tiny_layer(); L.bq = L.ffb[0] = None
+    assert check(L) == N.OK                                              # biases may be zero
+    L = _tiny_layer(); L.ffw[1] = 0x20108
+    assert check(L) == N.E_INVALID                                       # unaligned FFN weight
+
+    tok = (C.c_int * 8)()
+    M = _TinyModel(0x40000, 0x50000, 0x60000, 0x70000, 0x80000, 2, 64, 4, 200, 64, 1e-5)
+    decode = lambda M, batch=4, pos0=0, n=4: lib.cdml_tiny_decode(C.byref(M), tok, batch, pos0, n, None)
+    assert decode(M, n=0) == N.OK                                        # empty work
+    assert decode(M, pos0=62, n=3) == N.E_INVALID                        # past max_seq
+    assert decode(M, batch=-1) == N.E_INVALID
+    for field, value in (("dim", 512), ("heads", 3), ("max_seq", 2048), ("dim", 72)):
+        bad = _TinyModel.from_buffer_copy(M); setattr(bad, field, value)
+        assert decode(bad) == N.E_INVALID, field                         # outside the limits
+    bad = _TinyModel.from_buffer_copy(M); bad.out_w = 0x50008
+    assert decode(bad) == N.E_INVALID                                    # unaligned LM head
+    bad = _TinyModel.from_buffer_copy(M); bad.layers = None
+    assert decode(bad) == N.E_INVALID
