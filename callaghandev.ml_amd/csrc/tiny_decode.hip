@@ -8,9 +8,14 @@
 // argmax itself: sequences never exchange data, so no step needs another
 // workgroup.
 //
-// Products y = act(W x + b) run one thread per output with float4 loads,
-// four in flight; attention runs one thread per (head, key) for the scores,
-// one wave per head for the softmax, one thread per output column for P V.
+// Every phase of a step is latency-bound (a few hundred outputs whose
+// operands sit in L2), so the layout is chosen for the fewest dependent
+// memory round trips: each dot product (projections, scores, LM head) is
+// spread over G adjacent lanes, G the smallest power of two that leaves a
+// lane at most 8 float4 loads, all issued before the first is used, and
+// the G partial sums meet in a butterfly of shuffles; P V splits the keys
+// over 256 / D thread groups, each with 8 V loads in flight.  The softmax
+// is one wave per head.
 #include "common.h"
 
 namespace cdml {
@@ -51,36 +56,61 @@ __device__ __forceinline__ float tiny_wave_max(float v) {
   return v;
 }
 
-// sum_k row[k] x[k] for K % 4 == 0 (16-byte aligned row, x in LDS): four
-// float4 loads in flight per iteration, one running sum per float4 lane.
-__device__ __forceinline__ float tiny_dot(const float *__restrict__ row, const float *x, int K) {
+constexpr int kTinyLoads = 8;  // float4 loads in flight per lane of a dot product
+
+// Lanes per dot product of length K (K % 4 == 0, K <= 1024): the smallest
+// power of two G with K / 4 <= 8 G.
+__device__ __forceinline__ int tiny_group(int K) {
+  int g = 1;
+  while (g < 64 && K / 4 > kTinyLoads * g) g <<= 1;
+  return g;
+}
+
+// Lane `sub`'s share of row . x over float4 groups sub, sub + G, ... (16-byte
+// aligned row; x in LDS); every load is issued before the first product.
+__device__ __forceinline__ float tiny_dot_part(const float *__restrict__ row, const float *x, int nf4, int sub,
+                                               int G) {
   const float4 *r4 = reinterpret_cast<const float4 *>(row);
   const float4 *x4 = reinterpret_cast<const float4 *>(x);
-  float4 acc = {0.f, 0.f, 0.f, 0.f};
-  int i = 0;
-  for (; i + 4 <= K / 4; i += 4) {
-    const float4 a0 = r4[i], a1 = r4[i + 1], a2 = r4[i + 2], a3 = r4[i + 3];
-    const float4 b0 = x4[i], b1 = x4[i + 1], b2 = x4[i + 2], b3 = x4[i + 3];
-    acc.x += a0.x * b0.x + a1.x * b1.x + a2.x * b2.x + a3.x * b3.x;
-    acc.y += a0.y * b0.y + a1.y * b1.y + a2.y * b2.y + a3.y * b3.y;
-    acc.z += a0.z * b0.z + a1.z * b1.z + a2.z * b2.z + a3.z * b3.z;
-    acc.w += a0.w * b0.w + a1.w * b1.w + a2.w * b2.w + a3.w * b3.w;
+  float4 a[kTinyLoads];
+#pragma unroll
+  for (int i = 0; i < kTinyLoads; ++i) {
+    const int idx = sub + G * i;
+    a[i] = idx < nf4 ? r4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  for (; i < K / 4; ++i) {
-    const float4 a0 = r4[i], b0 = x4[i];
-    acc.x += a0.x * b0.x;
-    acc.y += a0.y * b0.y;
-    acc.z += a0.z * b0.z;
-    acc.w += a0.w * b0.w;
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < kTinyLoads; ++i) {
+    const int idx = sub + G * i;
+    if (idx < nf4) {
+      const float4 b = x4[idx];
+      acc += (a[i].x * b.x + a[i].y * b.y) + (a[i].z * b.z + a[i].w * b.w);
+    }
   }
-  return (acc.x + acc.y) + (acc.z + acc.w);
+  return acc;
+}
+
+// For every o < count: emit(o, row(o) . x(o)), K-long dot products spread
+// over G lanes each.  Every thread runs the same passes (the shuffles need
+// whole waves); emit runs on the group's first lane.
+template <class Row, class X, class Emit>
+__device__ __forceinline__ void tiny_dots(int count, int K, Row row, X x, Emit emit) {
+  const int G = tiny_group(K), per = kTinyThreads / G, nf4 = K / 4;
+  const int sub = threadIdx.x % G, slot = threadIdx.x / G;
+  for (int base = 0; base < count; base += per) {
+    const int o = base + slot;
+    float acc = o < count ? tiny_dot_part(row(o), x(o), nf4, sub, G) : 0.f;
+    for (int off = G >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+    if (sub == 0 && o < count) emit(o, acc);
+  }
 }
 
 // y[n] = act(b[n] + w[n] . x) for n < N (x and y in LDS).
 __device__ __forceinline__ void tiny_linear(const float *__restrict__ w, const float *__restrict__ b,
                                             const float *x, int K, int N, float *y, int act) {
-  for (int n = threadIdx.x; n < N; n += kTinyThreads)
-    y[n] = tiny_act(tiny_dot(w + (size_t)n * K, x, K) + (b ? b[n] : 0.f), act);
+  tiny_dots(
+      N, K, [&](int n) { return w + (size_t)n * K; }, [&](int) { return x; },
+      [&](int n, float v) { y[n] = tiny_act(v + (b ? b[n] : 0.f), act); });
 }
 
 // out = LayerNorm(a + c) with the biased variance in two passes (the
@@ -120,6 +150,7 @@ __global__ void __launch_bounds__(kTinyThreads) tiny_decode_kernel(const cdml_ti
       att[kTinyMaxDim], h[kTinyMaxDim];
   __shared__ __attribute__((aligned(16))) float ff[2][kTinyMaxFF];
   __shared__ float sc[kTinyMaxScores];
+  __shared__ float part[kTinyThreads];  // P V partial sums of the key groups
   __shared__ float best_v[kTinyThreads / 64];
   __shared__ int best_i[kTinyThreads / 64];
   __shared__ int tok;
@@ -136,9 +167,19 @@ __global__ void __launch_bounds__(kTinyThreads) tiny_decode_kernel(const cdml_ti
     __syncthreads();
     for (int l = 0; l < m.n_layers; ++l) {
       const cdml_tiny_layer &L = m.layers[l];
-      tiny_linear(L.wq, L.bq, x, D, D, q, CDML_ACT_NONE);
-      tiny_linear(L.wk, L.bk, x, D, D, kv[0], CDML_ACT_NONE);
-      tiny_linear(L.wv, L.bv, x, D, D, kv[1], CDML_ACT_NONE);
+      // Q, K and V as one set of 3 D dot products
+      tiny_dots(
+          3 * D, D,
+          [&](int o) {
+            const int n = o % D;
+            return (o < D ? L.wq : o < 2 * D ? L.wk : L.wv) + (size_t)n * D;
+          },
+          [&](int) { return x; },
+          [&](int o, float v) {
+            const int n = o % D;
+            const float *bias = o < D ? L.bq : o < 2 * D ? L.bk : L.bv;
+            (o < D ? q : o < 2 * D ? kv[0] : kv[1])[n] = v + (bias ? bias[n] : 0.f);
+          });
       __syncthreads();
       // RoPE of q and k at `pos` (AccelerationCPU.cs:4947-4975): pair p of a
       // head is columns 2p and 2p + 1, (cos, sin) from the model's table
@@ -161,10 +202,9 @@ __global__ void __launch_bounds__(kTinyThreads) tiny_decode_kernel(const cdml_ti
       __threadfence_block();  // the appended row is read back below
       __syncthreads();
       // scores of every head against the nk cached keys
-      for (int i = t; i < H * nk; i += kTinyThreads) {
-        const int hh = i / nk, j = i % nk;
-        sc[hh * S + j] = tiny_dot(kc + (size_t)j * D + hh * hd, q + hh * hd, hd) * scale;
-      }
+      tiny_dots(
+          H * nk, hd, [&](int i) { return kc + (size_t)(i % nk) * D + (i / nk) * hd; },
+          [&](int i) { return q + (i / nk) * hd; }, [&](int i, float v) { sc[(i / nk) * S + i % nk] = v * scale; });
       __syncthreads();
       // softmax per head: wave w takes heads w, w + 4, ...
       for (int hh = wave; hh < H; hh += kTinyThreads / 64) {
@@ -182,19 +222,34 @@ __global__ void __launch_bounds__(kTinyThreads) tiny_decode_kernel(const cdml_ti
         for (int j = lane; j < nk; j += 64) sc[hh * S + j] *= inv;
       }
       __syncthreads();
-      // att[e] = sum_j p[head(e)][j] v_j[e]
-      for (int e = t; e < D; e += kTinyThreads) {
-        const float *p = sc + (e / hd) * S;
-        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-        int j = 0;
-        for (; j + 4 <= nk; j += 4) {  // four V loads in flight
-          a0 += p[j] * vc[(size_t)j * D + e];
-          a1 += p[j + 1] * vc[(size_t)(j + 1) * D + e];
-          a2 += p[j + 2] * vc[(size_t)(j + 2) * D + e];
-          a3 += p[j + 3] * vc[(size_t)(j + 3) * D + e];
+      // att[e] = sum_j p[head(e)][j] v_j[e]: group g of the 256 / D thread
+      // groups takes keys g, g + groups, ..., 8 V loads in flight per lane
+      {
+        const int groups = kTinyThreads / D, g = t / D, e = t % D;
+        if (g < groups) {
+          const float *p = sc + (e / hd) * S;
+          float acc = 0.f;
+          for (int j0 = g; j0 < nk; j0 += kTinyLoads * groups) {
+            float vv[kTinyLoads];
+#pragma unroll
+            for (int i = 0; i < kTinyLoads; ++i) {
+              const int j = j0 + i * groups;
+              vv[i] = j < nk ? vc[(size_t)j * D + e] : 0.f;
+            }
+#pragma unroll
+            for (int i = 0; i < kTinyLoads; ++i) {
+              const int j = j0 + i * groups;
+              if (j < nk) acc += p[j] * vv[i];
+            }
+          }
+          part[t] = acc;
         }
-        for (; j < nk; ++j) a0 += p[j] * vc[(size_t)j * D + e];
-        att[e] = (a0 + a1) + (a2 + a3);
+        __syncthreads();
+        for (int d = t; d < D; d += kTinyThreads) {
+          float v = 0.f;
+          for (int gg = 0; gg < groups; ++gg) v += part[gg * D + d];
+          att[d] = v;
+        }
       }
       __syncthreads();
       tiny_linear(L.wo, L.bo, att, D, D, q, CDML_ACT_NONE);  // q is free again: the projection
@@ -216,13 +271,15 @@ __global__ void __launch_bounds__(kTinyThreads) tiny_decode_kernel(const cdml_ti
     // LM head and greedy choice: the lowest index among the largest logits
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int n = t; n < m.vocab; n += kTinyThreads) {
-      const float v = tiny_dot(m.out_w + (size_t)n * D, x, D) + m.out_b[n];
-      if (v > bv || (v == bv && n < bi)) {
-        bv = v;
-        bi = n;
-      }
-    }
+    tiny_dots(
+        m.vocab, D, [&](int n) { return m.out_w + (size_t)n * D; }, [&](int) { return x; },
+        [&](int n, float v) {
+          v += m.out_b[n];
+          if (v > bv || (v == bv && n < bi)) {
+            bv = v;
+            bi = n;
+          }
+        });
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
       const float ov = __shfl_xor(bv, off);

@@ -352,7 +352,7 @@ def test_generate_graph_replays_match_eager():
         dev.use_graphs = True
 
 
-@pytest.mark.parametrize("name", ["c1", "deep_ffn"])
+@pytest.mark.parametrize("name", ["c1", "deep_ffn", "odd_width", "widest"])
 def test_generate_fused_decode_matches_per_kernel_path(name):
     """The fused decode launch (every step after the prefill in one kernel)
     against the per-kernel decode steps of the same model: identical greedy
@@ -361,8 +361,12 @@ def test_generate_fused_decode_matches_per_kernel_path(name):
     Hm = host.module()
     if name == "c1":
         cfg = {"vocab": 200, "dim": 64, "heads": 4, "layers": 2, "ff": 128, "max_seq": 64}
-    else:
+    elif name == "deep_ffn":
         cfg = {"vocab": 97, "dim": 32, "heads": 2, "layers": 3, "ff": 48, "max_seq": 40}
+    elif name == "odd_width":  # 256 / D leaves threads without a key group
+        cfg = {"vocab": 301, "dim": 96, "heads": 3, "layers": 1, "ff": 200, "max_seq": 40}
+    else:  # the fused path's largest model width and FFN width
+        cfg = {"vocab": 500, "dim": 256, "heads": 4, "layers": 2, "ff": 1024, "max_seq": 64}
     lm, _ = host.language_model(cfg, synth.lm_weights(cfg, 12, biased=True))
     fused, plain = Hm.DeviceLanguageModel(lm, 4), Hm.DeviceLanguageModel(lm, 4)
     assert fused.fused_decode_available
