@@ -229,7 +229,7 @@ def bench_mha_backward(N, st, steps, warmup, cfg=None):
     gb = [N.DeviceBuffer.from_array(np.zeros(D, np.float32), st) for _ in range(4)]
     dcat, dq, dk, dv, dxin = (N.DeviceBuffer(rows * D * 4) for _ in range(5))
     wsz, wsl, wsq = C.c_size_t(0), C.c_size_t(0), C.c_size_t(0)
-    N.check(lib.cdml_sdpa_bwd_workspace_size(B, L, L, D, H, C.byref(wsz)))
+    N.check(lib.cdml_sdpa_bwd_stored_ds_workspace_size(B, L, L, D, H, 1, C.byref(wsz)))
     N.check(lib.cdml_linear_backward_workspace_size(rows, D, D, C.byref(wsl)))
     N.check(lib.cdml_backprop_qkv_workspace_size(rows, D, D, C.byref(wsq)))
     dws = N.DeviceBuffer(max(16, wsz.value))

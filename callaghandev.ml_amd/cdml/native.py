@@ -76,6 +76,7 @@ SIGNATURES = {
     "cdml_backprop_qkv": [_vp] * 14 + [_i, _i, _i, _vp, _sz, _vp],
     "cdml_sdpa_bwd_workspace_size": [_i, _i, _i, _i, _i, C.POINTER(_sz)],
     "cdml_sdpa_bwd_saved_workspace_size": [_i, _i, _i, _i, _i, _i, C.POINTER(_sz)],
+    "cdml_sdpa_bwd_stored_ds_workspace_size": [_i, _i, _i, _i, _i, _i, C.POINTER(_sz)],
     "cdml_sdpa_bwd": [_vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i,
                       _i, _i, _i, _i, _i, _f, _i, _vp, _vp, _sz, _vp],
     "cdml_sdpa_fwd_lse": [_vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _f, _i, _vp, _vp],

@@ -891,6 +891,14 @@ size_t ds_bytes(int batch, int lq, int lk, int dim, int num_heads, bool causal) 
 }  // namespace
 }  // namespace cdml
 
+extern "C" int cdml_sdpa_bwd_stored_ds_workspace_size(int batch, int lq, int lk, int dim, int num_heads,
+                                                      int causal, size_t *bytes) {
+  int rc = cdml_sdpa_bwd_workspace_size(batch, lq, lk, dim, num_heads, bytes);
+  if (rc) return rc;
+  *bytes = align256(*bytes) + ds_bytes(batch, lq, lk, dim, num_heads, causal != 0);
+  return CDML_OK;
+}
+
 extern "C" int cdml_sdpa_bwd_saved_workspace_size(int batch, int lq, int lk, int dim, int num_heads,
                                                   int causal, size_t *bytes) {
   if (!bytes) return fail(CDML_E_INVALID, "cdml_sdpa_bwd_saved_workspace_size: bytes is NULL");
@@ -1019,11 +1027,11 @@ int sdpa_bwd_impl(const float *q, int ldq, const float *k, int ldk, const float 
   }
   rc = check_launch("bwd_delta_kernel");
   if (rc) return rc;
-  // 3. dK, dV and 4. dQ; from saved statistics with room for the dS blocks,
-  // dQ is one product over them
-  if (saved && vec && !mask) {
+  // 3. dK, dV and 4. dQ; with room for the dS blocks after the required
+  // workspace, dQ is one product over them
+  if (vec && !mask) {
     const size_t extra = ds_bytes(batch, lq, lk, dim, num_heads, causal != 0);
-    const size_t off = align256(sizeof(float) * bh * lq);
+    const size_t off = align256(need);  // the dS blocks follow the required workspace
     if (extra && workspace_bytes >= off + extra) {
       a.ds = reinterpret_cast<float *>(ws + off);
       a.ds_bh = (long long)(extra / sizeof(float) / bh);

@@ -529,7 +529,9 @@ std::tuple<Matrix, Matrix, Matrix> HipAccelerationManager::attention_backward(
   float *gk = static_cast<float *>(scratch(S_DK, kb));
   float *gv = static_cast<float *>(scratch(S_DV, kb));
   size_t ws = 0;
-  check(cdml_sdpa_bwd_workspace_size(1, lq, lk, dim, numHeads, &ws), "cdml_sdpa_bwd_workspace_size");
+  // with room for the dS blocks when the shape can use them (dQ as one product)
+  check(cdml_sdpa_bwd_stored_ds_workspace_size(1, lq, lk, dim, numHeads, causal && mask.null() ? 1 : 0, &ws),
+        "cdml_sdpa_bwd_stored_ds_workspace_size");
   void *dws = scratch(S_WS, ws);
   upload(dq_in, Q.data, qb);
   upload(dk_in, K.data, kb);

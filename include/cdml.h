@@ -275,6 +275,15 @@ int cdml_sdpa_fwd_lse(const float *q, int ldq, const float *k, int ldk,
  * head dims run a per-row kernel. */
 int cdml_sdpa_bwd_workspace_size(int batch, int lq, int lk, int dim,
                                  int num_heads, size_t *bytes);
+/* A larger workspace for cdml_sdpa_bwd: the required bytes plus room for the
+ * dS blocks, 2 * lq^2 bytes per (sequence, head), when the shape can use them
+ * (causal without a mask, lq == lk, head dim 32 or 64, 16-byte aligned rows).
+ * With it the dK/dV pass stores dS and dQ is one product over it instead of
+ * recomputing the scores; the result meets the same bar but need not match
+ * the smaller workspace's bits.  Other shapes leave the extra bytes unused. */
+int cdml_sdpa_bwd_stored_ds_workspace_size(int batch, int lq, int lk, int dim,
+                                           int num_heads, int causal,
+                                           size_t *bytes);
 int cdml_sdpa_bwd(const float *q, int ldq, const float *k, int ldk,
                   const float *v, int ldv, const float *dout, int lddo,
                   float *dq, int lddq, float *dk, int lddk, float *dv,

@@ -321,6 +321,18 @@ def test_sdpa_bwd_from_saved_statistics(batch, L, dim, heads):
                                     dim, heads, scale, 1, None, bbig.ptr, big.value, s))
     for a, b, n in zip(outs[1][1:], out3[1:], "KV"):
         assert np.array_equal(G.down(a, (rows, dim)), G.down(b, (rows, dim))), f"stored-dS d{n}"
+    # the drop-in form with its own larger workspace takes the same path: the
+    # recomputed forward gives the saved output's bits, so all three agree
+    bigd = C.c_size_t(0)
+    N.check(lib.cdml_sdpa_bwd_stored_ds_workspace_size(batch, L, L, dim, heads, 1, C.byref(bigd)))
+    assert (bigd.value > ws.value) == (hd in (32, 64))
+    bbigd = N.DeviceBuffer(bigd.value)
+    out4 = [N.DeviceBuffer(rows * dim * 4) for _ in range(3)]
+    N.check(lib.cdml_sdpa_bwd(bq.ptr, dim, bk.ptr, dim, bv.ptr, dim, bg.ptr, dim, out4[0].ptr, dim,
+                              out4[1].ptr, dim, out4[2].ptr, dim, batch, L, L, dim, heads, scale, 1, None,
+                              bbigd.ptr, bigd.value, s))
+    for a, b, n in zip(out3, out4, "QKV"):
+        assert np.array_equal(G.down(a, (rows, dim)), G.down(b, (rows, dim))), f"drop-in stored-dS d{n}"
     dq3 = G.down(out3[0], (rows, dim))
     for sq in range(batch):
         r = slice(sq * L, (sq + 1) * L)
