@@ -140,3 +140,32 @@ def test_tiny_decode_descriptor_checks():
     assert decode(bad) == N.E_INVALID                                    # unaligned LM head
     bad = _TinyModel.from_buffer_copy(M); bad.layers = None
     assert decode(bad) == N.E_INVALID
+
+
+def test_sdpa_bwd_workspace_sizes():
+    """The drop-in backward's larger workspace is the required one plus the
+    stored dS blocks (32 x 32 floats per block of the causal triangle) exactly
+    when the shape can use them: causal, lq == lk, head dim 32 or 64."""
+    lib = N.lib()
+
+    def size(fn, *args):
+        out = C.c_size_t(0)
+        assert fn(*args, C.byref(out)) == N.OK
+        return out.value
+
+    def align(n):
+        return (n + 255) // 256 * 256
+
+    for batch, L, dim, heads, causal in ((4, 4096, 1024, 16, 1), (3, 300, 256, 8, 1), (2, 100, 96, 3, 1),
+                                         (2, 100, 256, 4, 0), (2, 100, 48, 1, 1)):
+        base = size(lib.cdml_sdpa_bwd_workspace_size, batch, L, L, dim, heads)
+        big = size(lib.cdml_sdpa_bwd_stored_ds_workspace_size, batch, L, L, dim, heads, causal)
+        hd, nb = dim // heads, (L + 31) // 32
+        ds = batch * heads * nb * (nb + 1) // 2 * 1024 * 4 if causal and hd in (32, 64) else 0
+        assert big == align(base) + ds, (batch, L, dim, heads, causal)
+    # different query and key lengths never store dS
+    assert (size(lib.cdml_sdpa_bwd_stored_ds_workspace_size, 2, 64, 128, 256, 4, 1)
+            == align(size(lib.cdml_sdpa_bwd_workspace_size, 2, 64, 128, 256, 4)))
+    bad = C.c_size_t(0)
+    assert lib.cdml_sdpa_bwd_stored_ds_workspace_size(1, 8, 8, 10, 3, 1, C.byref(bad)) == N.E_INVALID
+    assert lib.cdml_sdpa_bwd_stored_ds_workspace_size(1, 8, 8, 12, 3, 1, None) == N.E_INVALID
