@@ -128,8 +128,8 @@ def test_manager_attention_backward(mgr):
     closed-form case (AccelerationManagerParityTests.cs:355-382: 4x6, 2 heads,
     scale 1/sqrt 3, decoder flag and explicit causal mask), the consistency
     suite's 6x8 no-mask / decoder and 5x8 cross cases
-    (AccelerationConsistencyTests.cs:962-1020), and a 300x128 causal case on
-    the MFMA kernels (head dim 64)."""
+    (AccelerationConsistencyTests.cs:962-1020), and causal cases on the MFMA
+    kernels: 300x128 (head dim 64) by flag and by mask, 237x128 (head dim 32)."""
     q, k, v, d = M(4, 6, 31), M(4, 6, 32), M(4, 6, 33), M(4, 6, 34)
     scale = float(np.float32(1) / np.sqrt(np.float32(3)))
     causal = np.tril(np.ones((4, 4), bool))
@@ -150,6 +150,17 @@ def test_manager_attention_backward(mgr):
     want = O.mha_backward(q, k, v, d, Hh, s, use_decoder_mask=True)
     for got, w, n in zip(mgr.MultiHeadAttentionBackward(q, k, v, d, Hh, s, True), want, ("dQ", "dK", "dV")):
         parity(got, w, f"MHA backward 300x128 causal {n}")
+    # the same case through the bool[,] overload (no stored dS with a mask),
+    # and head dim 32 with a ragged last block (stored dS, the short dQ kernel)
+    tri = np.tril(np.ones((L, L), bool))
+    for got, w, n in zip(mgr.MultiHeadAttentionBackward(q, k, v, d, Hh, s, tri), want, ("dQ", "dK", "dV")):
+        parity(got, w, f"MHA backward 300x128 mask {n}")
+    L, Hh = 237, 4
+    q, k, v, d = (synth.normal(70 + i, (L, D)) for i in range(4))
+    s = float(np.float32(1) / np.sqrt(np.float32(32)))
+    want = O.mha_backward(q, k, v, d, Hh, s, use_decoder_mask=True)
+    for got, w, n in zip(mgr.MultiHeadAttentionBackward(q, k, v, d, Hh, s, True), want, ("dQ", "dK", "dV")):
+        parity(got, w, f"MHA backward 237x128 head dim 32 causal {n}")
 
 
 def test_manager_projection_backward(mgr):
