@@ -433,6 +433,40 @@ def extras(N, st, only=None):
     return out
 
 
+def host_cpu_info():
+    """The host's processor count as .NET's Environment.ProcessorCount reads it
+    on Linux (the CPUs in the process's affinity mask, lowered to the cgroup
+    CPU quota when one is set), which AccelerationMutliThreadCPU uses as its
+    degree of parallelism (AccelerationMutliThreadCPU.cs:61-69), plus nproc and
+    the CPU model.  The threads used are that count, capped at this box's CPU
+    share for one GPU when the box announces one through OMP_NUM_THREADS."""
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = os.cpu_count() or 1
+    quota = None
+    try:
+        q, p = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if q != "max":
+            quota = max(1, -(-int(q) // int(p)))
+    except (OSError, ValueError):
+        pass
+    proc_count = min(affinity, quota) if quota else affinity
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    share = int(share) if share.isdigit() and int(share) > 0 else None
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    used = min(proc_count, share) if share else proc_count
+    return {"processor_count": proc_count, "nproc": affinity, "os_cpu_count": os.cpu_count(),
+            "cgroup_cpu_quota": quota, "box_cpu_share": share, "threads_used": used, "cpu_model": model}
+
+
 def cpu_baseline(sample_seqs=3):
     """The multi-threaded CPU restatement of AccelerationMutliThreadCPU's
     ProjectQKV / RoPE / ScaledDotProductAttention / ProjectOutputBatch
@@ -441,7 +475,8 @@ def cpu_baseline(sample_seqs=3):
     from oracle import oracle as O
     from cdml import synth
 
-    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16") or 16))
+    host = host_cpu_info()
+    threads = host["threads_used"]
     O.set_threads(threads)
     L, D, H = C3["seq"], C3["dim"], C3["heads"]
     rng = np.random.default_rng(5)
@@ -458,10 +493,12 @@ def cpu_baseline(sample_seqs=3):
     dt = time.perf_counter() - t0
     core, qkv, out = mha_flops(sample_seqs, L, D, H)
     return dict(value=(core + qkv + out) / dt / 1e12, unit="TFLOP/s", cores=threads, kind="port",
-                seconds=dt,
+                seconds=dt, host=host,
                 sample=f"{sample_seqs} of the 4 c3 sequences (L 4096, D 1024, H 16), full MHA forward "
                        f"through the C restatement of AccelerationMutliThreadCPU (-O2, no fast-math), "
-                       f"{threads} threads, {dt:.1f} s")
+                       f"{threads} threads (Environment.ProcessorCount equivalent {host['processor_count']}, "
+                       f"nproc {host['nproc']}, box share {host['box_cpu_share']}) on {host['cpu_model']}, "
+                       f"{dt:.1f} s")
 
 
 def main():

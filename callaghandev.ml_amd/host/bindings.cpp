@@ -190,6 +190,20 @@ PYBIND11_MODULE(_cdml_host, m) {
   py::register_exception<InvalidOperationException>(m, "InvalidOperationException", PyExc_RuntimeError);
   py::register_exception<FileNotFoundException>(m, "FileNotFoundException", PyExc_FileNotFoundError);
 
+  m.def("sdpa_backward_workspace_choice",
+        // the drop-in attention backward's workspace size for one sequence
+        // (MultiHeadAttentionBackward): the C ABI's two sizes and the choice
+        [](int lq, int lk, int dim, int numHeads, bool causal, size_t extra_cap) {
+          size_t base = 0, stored = 0;
+          if (cdml_sdpa_bwd_workspace_size(1, lq, lk, dim, numHeads, &base) != CDML_OK ||
+              cdml_sdpa_bwd_stored_ds_workspace_size(1, lq, lk, dim, numHeads, causal ? 1 : 0, &stored) != CDML_OK)
+            throw ArgumentException(cdml_last_error());
+          return py::make_tuple(base, stored, SdpaBackwardWorkspaceChoice(base, stored, extra_cap));
+        },
+        py::arg("lq"), py::arg("lk"), py::arg("dim"), py::arg("numHeads"), py::arg("causal"),
+        py::arg("extra_cap") = kStoredDsExtraBytesCap);
+  m.attr("STORED_DS_EXTRA_BYTES_CAP") = kStoredDsExtraBytesCap;
+
   py::class_<HipAccelerationManager>(m, "HipAccelerationManager")
       .def(py::init<int>(), py::arg("device") = 0)
       .def("ProjectQKV",
@@ -627,6 +641,36 @@ PYBIND11_MODULE(_cdml_host, m) {
              auto X = mat(x);
              return to_numpy(d.ForwardContinuous(X.view, batch, seqLen));
            })
+      .def("Layers",
+           // The decoder blocks alone on embeddings x [batch * seqLen, D]
+           // (the c3 stack's input): uploads x, runs every block in place on
+           // the device and returns the result.
+           [](DeviceLanguageModel &d, py::object x, int batch, int seqLen) {
+             auto X = mat(x);
+             if (X.view.null() || (long long)X.view.rows != (long long)batch * seqLen)
+               throw ArgumentException("x must be [batch * seqLen, D]", "x");
+             if (batch <= 0 || batch > d.batch_capacity()) throw ArgumentOutOfRangeException("batch");
+             auto chk = [](int rc) {
+               if (rc != CDML_OK) throw InvalidOperationException(cdml_last_error());
+             };
+             Matrix out(X.view.rows, X.view.cols);
+             void *dx = nullptr;
+             const size_t bytes = (size_t)X.view.rows * X.view.cols * sizeof(float);
+             chk(cdml_malloc(&dx, bytes));
+             try {
+               py::gil_scoped_release nogil;
+               chk(cdml_memcpy_h2d_async(dx, X.view.data, bytes, d.stream()));
+               d.layers_device(static_cast<float *>(dx), batch, seqLen);
+               chk(cdml_memcpy_d2h_async(out.ptr(), dx, bytes, d.stream()));
+               d.synchronize();
+             } catch (...) {
+               cdml_free(dx);
+               throw;
+             }
+             cdml_free(dx);
+             return to_numpy(std::move(out));
+           },
+           py::arg("x"), py::arg("batch"), py::arg("seqLen"))
       .def_readwrite("use_graphs", &DeviceLanguageModel::use_graphs)
       .def_readwrite("use_fused_decode", &DeviceLanguageModel::use_fused_decode)
       .def_property_readonly("fused_decode_available", &DeviceLanguageModel::fused_decode_available)

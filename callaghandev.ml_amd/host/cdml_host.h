@@ -129,6 +129,13 @@ struct FeedForwardNetwork {
   int output_size() const { return weights.empty() ? 0 : weights.back().rows; }
 };
 
+// The attention backward's workspace: the stored-dS size (the causal 32 x 32
+// fp32 dS blocks, about 2 L^2 bytes per head: gigabytes at long context)
+// when its extra bytes over the base size are at most `extra_cap`, else the
+// base size.
+size_t SdpaBackwardWorkspaceChoice(size_t base_bytes, size_t stored_ds_bytes, size_t extra_cap);
+constexpr size_t kStoredDsExtraBytesCap = size_t(1) << 30;
+
 // ---- the manager -----------------------------------------------------------
 class HipAccelerationManager {
  public:
@@ -259,6 +266,7 @@ class HipAccelerationManager {
 
   void ensure_ready();
   void *scratch(int slot, size_t bytes);
+  void *try_scratch(int slot, size_t bytes);
   const float *resident(const float *host, int rows, int cols);
   void upload(void *dev, const void *host, size_t bytes);
   void download(void *host, const void *dev, size_t bytes);
@@ -447,7 +455,7 @@ class DeviceLanguageModel {
   void *ws_ = nullptr;
   size_t ws_bytes_ = 0;
   int ff_max_ = 0;
-  std::map<std::tuple<int, int, int>, cdml_graph> graphs_;  // (batch, promptLen, n)
+  std::map<std::tuple<int, int, int, bool>, cdml_graph> graphs_;  // (batch, promptLen, n, fused decode)
   cdml_tiny_model tiny_{};  // descriptors for cdml_tiny_decode (layers in device memory)
   bool tiny_ok_ = false;
 };
@@ -566,6 +574,10 @@ class DeviceTrainer {
   void *ws_ = nullptr;
   size_t ws_bytes_ = 0;
   float last_norm_ = 0.f;
+  // Every public method holds it: the trainer's device buffers and host
+  // state are shared by all its calls (Train calls TrainBatch, hence
+  // recursive).
+  std::recursive_mutex mu_;
 };
 
 }  // namespace cdml_host

@@ -88,6 +88,28 @@ void *HipAccelerationManager::scratch(int slot, size_t bytes) {
   return b.p;
 }
 
+// Like scratch(), but a failed allocation returns NULL (the slot is left
+// empty) instead of throwing.
+void *HipAccelerationManager::try_scratch(int slot, size_t bytes) {
+  DeviceBuf &b = scratch_[slot];
+  if (bytes == 0) bytes = 4;
+  if (b.bytes >= bytes) return b.p;
+  check(cdml_stream_synchronize(stream_), "cdml_stream_synchronize");
+  check(cdml_free(b.p), "cdml_free");
+  b.p = nullptr;
+  b.bytes = 0;
+  void *p = nullptr;
+  if (cdml_malloc(&p, bytes) != CDML_OK) return nullptr;
+  b.p = p;
+  b.bytes = bytes;
+  return p;
+}
+
+size_t SdpaBackwardWorkspaceChoice(size_t base_bytes, size_t stored_ds_bytes, size_t extra_cap) {
+  if (stored_ds_bytes <= base_bytes) return base_bytes;
+  return stored_ds_bytes - base_bytes <= extra_cap ? stored_ds_bytes : base_bytes;
+}
+
 void HipAccelerationManager::upload(void *dev, const void *host, size_t bytes) {
   check(cdml_memcpy_h2d_async(dev, host, bytes, stream_), "cdml_memcpy_h2d_async");
 }
@@ -528,11 +550,19 @@ std::tuple<Matrix, Matrix, Matrix> HipAccelerationManager::attention_backward(
   float *gq = static_cast<float *>(scratch(S_DQ, qb));
   float *gk = static_cast<float *>(scratch(S_DK, kb));
   float *gv = static_cast<float *>(scratch(S_DV, kb));
-  size_t ws = 0;
-  // with room for the dS blocks when the shape can use them (dQ as one product)
-  check(cdml_sdpa_bwd_stored_ds_workspace_size(1, lq, lk, dim, numHeads, causal && mask.null() ? 1 : 0, &ws),
+  size_t base_ws = 0, stored_ws = 0;
+  check(cdml_sdpa_bwd_workspace_size(1, lq, lk, dim, numHeads, &base_ws), "cdml_sdpa_bwd_workspace_size");
+  // with room for the dS blocks when the shape can use them (dQ as one
+  // product), as long as the extra bytes stay under the cap and allocate
+  check(cdml_sdpa_bwd_stored_ds_workspace_size(1, lq, lk, dim, numHeads, causal && mask.null() ? 1 : 0,
+                                               &stored_ws),
         "cdml_sdpa_bwd_stored_ds_workspace_size");
-  void *dws = scratch(S_WS, ws);
+  size_t ws = SdpaBackwardWorkspaceChoice(base_ws, stored_ws, kStoredDsExtraBytesCap);
+  void *dws = ws > base_ws ? try_scratch(S_WS, ws) : nullptr;
+  if (!dws) {
+    ws = base_ws;
+    dws = scratch(S_WS, ws);
+  }
   upload(dq_in, Q.data, qb);
   upload(dk_in, K.data, kb);
   upload(dv_in, V.data, kb);

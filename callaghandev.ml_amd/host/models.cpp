@@ -656,7 +656,10 @@ std::vector<int> DeviceLanguageModel::GenerateGreedy(const std::vector<int> &pro
   check(cdml_memcpy_h2d_async(ids_, prompts.data(), prompts.size() * sizeof(int), stream_), "upload ids");
   if (cfg_.UseDecoderOnly) {
     if (use_graphs) {
-      const auto key = std::make_tuple(batch, promptLen, n);
+      // the recording holds the decode path chosen at capture time, so the
+      // path's switch is part of the key
+      const bool fused = use_fused_decode && tiny_ok_ && n > 1;
+      const auto key = std::make_tuple(batch, promptLen, n, fused);
       auto it = graphs_.find(key);
       if (it == graphs_.end()) {
         if (graphs_.size() >= 16) {  // a bounded cache: drop every recording

@@ -278,7 +278,10 @@ DeviceTrainer::~DeviceTrainer() {
   cdml_stream_destroy(stream_);
 }
 
-void DeviceTrainer::synchronize() { check(cdml_stream_synchronize(stream_), "cdml_stream_synchronize"); }
+void DeviceTrainer::synchronize() {
+  std::lock_guard<std::recursive_mutex> lock(mu_);
+  check(cdml_stream_synchronize(stream_), "cdml_stream_synchronize");
+}
 
 void DeviceTrainer::zero_grads() {
   check(cdml_zero_f32_async(grads_, nparams_, stream_), "cdml_zero_f32_async");
@@ -482,6 +485,7 @@ void DeviceTrainer::upload_bucket_continuous(const std::vector<Matrix> &inputs,
 
 float DeviceTrainer::TrainBatchContinuous(const std::vector<Matrix> &inputs, const std::vector<Matrix> &regTargets,
                                           const std::vector<std::vector<int>> &classTargets, float learningRate) {
+  std::lock_guard<std::recursive_mutex> lock(mu_);
   if (cfg_.UsesDiscreteTokens) throw InvalidOperationException("Use TrainBatch for token models.");
   const bool regression = cfg_.DataType == 1;
   const int F = cfg_.InputFeatureDim, O = cfg_.EffectiveOutputDim();
@@ -535,6 +539,7 @@ float DeviceTrainer::TrainBatchContinuous(const std::vector<Matrix> &inputs, con
 
 float DeviceTrainer::TrainContinuous(const std::vector<Matrix> &inputs, const std::vector<Matrix> &regTargets,
                                      const std::vector<std::vector<int>> &classTargets, uint64_t seed) {
+  std::lock_guard<std::recursive_mutex> lock(mu_);
   if (cfg_.UsesDiscreteTokens) throw InvalidOperationException("Use Train(int[][]) for token models.");
   if (tc_.BatchSize <= 0) throw ArgumentOutOfRangeException("BatchSize", "BatchSize must be positive.");
   if (tc_.Epochs < 0) throw ArgumentOutOfRangeException("Epochs", "Epochs must be non-negative.");
@@ -585,6 +590,7 @@ float DeviceTrainer::TrainContinuous(const std::vector<Matrix> &inputs, const st
 }
 
 float DeviceTrainer::TrainBatch(const std::vector<std::vector<int>> &batch, float learningRate) {
+  std::lock_guard<std::recursive_mutex> lock(mu_);
   if (!cfg_.UsesDiscreteTokens) throw InvalidOperationException("Use TrainBatchContinuous for continuous inputs.");
   // TokensAreValid (:1467-1478) and the length buckets (:224-248), in order of
   // first appearance
@@ -631,6 +637,7 @@ float DeviceTrainer::TrainBatch(const std::vector<std::vector<int>> &batch, floa
 }
 
 void DeviceTrainer::load_batch(const int *host_tokens, int batch, int seqLenPlus1) {
+  std::lock_guard<std::recursive_mutex> lock(mu_);
   if (!cfg_.UsesDiscreteTokens) throw InvalidOperationException("load_batch takes token sequences.");
   if (batch <= 0 || batch > cap_b_ || seqLenPlus1 < 2 || seqLenPlus1 - 1 > cap_s_)
     throw ArgumentOutOfRangeException("batch");
@@ -647,6 +654,7 @@ void DeviceTrainer::load_batch(const int *host_tokens, int batch, int seqLenPlus
 
 void DeviceTrainer::load_batch_continuous(const float *host_inputs, const float *host_targets, int batch,
                                           int seqLenPlus1) {
+  std::lock_guard<std::recursive_mutex> lock(mu_);
   if (cfg_.UsesDiscreteTokens || cfg_.DataType != 1)
     throw InvalidOperationException("load_batch_continuous takes regression windows.");
   if (batch <= 0 || batch > cap_b_ || seqLenPlus1 < 2 || seqLenPlus1 - 1 > cap_s_)
@@ -667,6 +675,7 @@ void DeviceTrainer::load_batch_continuous(const float *host_inputs, const float 
 }
 
 void DeviceTrainer::step_loaded(float learningRate) {
+  std::lock_guard<std::recursive_mutex> lock(mu_);
   if (loaded_b_ <= 0) throw InvalidOperationException("load_batch first");
   zero_grads();
   bucket_forward(loaded_b_, loaded_s_, loaded_b_ > 1 ? (float)loaded_b_ : 1.0f, losses_);
@@ -675,6 +684,7 @@ void DeviceTrainer::step_loaded(float learningRate) {
 }
 
 float DeviceTrainer::Train(const std::vector<std::vector<int>> &sequences, uint64_t seed) {
+  std::lock_guard<std::recursive_mutex> lock(mu_);
   if (!cfg_.UsesDiscreteTokens) throw InvalidOperationException("Use TrainContinuous() for continuous inputs.");
   if (tc_.BatchSize <= 0) throw ArgumentOutOfRangeException("BatchSize", "BatchSize must be positive.");
   if (tc_.Epochs < 0) throw ArgumentOutOfRangeException("Epochs", "Epochs must be non-negative.");
@@ -710,6 +720,7 @@ float DeviceTrainer::Train(const std::vector<std::vector<int>> &sequences, uint6
 }
 
 std::vector<float> DeviceTrainer::weights_flat() {
+  std::lock_guard<std::recursive_mutex> lock(mu_);
   std::vector<float> h(nparams_);
   check(cdml_memcpy_d2h_async(h.data(), params_, nparams_ * sizeof(float), stream_), "download");
   synchronize();
@@ -717,6 +728,7 @@ std::vector<float> DeviceTrainer::weights_flat() {
 }
 
 std::vector<float> DeviceTrainer::gradients_flat() {
+  std::lock_guard<std::recursive_mutex> lock(mu_);
   std::vector<float> h(nparams_);
   check(cdml_memcpy_d2h_async(h.data(), grads_, nparams_ * sizeof(float), stream_), "download");
   synchronize();
@@ -724,6 +736,7 @@ std::vector<float> DeviceTrainer::gradients_flat() {
 }
 
 void DeviceTrainer::CopyWeightsTo(LanguageModel &model) {
+  std::lock_guard<std::recursive_mutex> lock(mu_);
   const std::vector<float> w = weights_flat();
   size_t i = 0;
   auto take = [&](float *dst, size_t n) {

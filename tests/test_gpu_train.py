@@ -265,9 +265,14 @@ def test_device_trainer_loss_decreases():
     assert losses[-1] < 0.8 * losses[0], losses
 
 
+# (1, 700, 64, 2) and (2, 1000, 256, 8): head dim 32 past 512 rows, where the
+# stored-dS dQ takes flash_bwd_dq_ds_kernel<32, 64> instead of the short
+# kernel; (1, 256, 128, 2) / (1, 257, 128, 2): head dim 64 at the short
+# kernel's last length and one past it.
 @pytest.mark.parametrize("batch,L,dim,heads", [(2, 300, 128, 2), (1, 257, 256, 2), (3, 130, 96, 3), (2, 64, 512, 4),
                                                (4, 63, 64, 4), (2, 100, 96, 2), (2, 200, 128, 2), (1, 512, 256, 8),
-                                               (3, 33, 64, 2)])
+                                               (3, 33, 64, 2), (1, 700, 64, 2), (2, 1000, 256, 8),
+                                               (1, 256, 128, 2), (1, 257, 128, 2)])
 def test_sdpa_bwd_from_saved_statistics(batch, L, dim, heads):
     """The trainer's attention backward from the forward's saved output and
     row statistics (cdml_sdpa_fwd_lse + cdml_sdpa_bwd_saved) gives the same

@@ -220,3 +220,26 @@ def test_no_device_means_loud_failure(mgr):
         pytest.skip("a device is visible")
     with pytest.raises(H.InvalidOperationException, match="no HIP device"):
         mgr.ScaledDotProductAttention(M(4, 8, 1), M(4, 8, 2), M(4, 8, 3), 2)
+
+
+def test_attention_backward_workspace_choice():
+    """MultiHeadAttentionBackward asks for the stored-dS workspace (the causal
+    32 x 32 fp32 dS blocks of every head, about 2 L^2 bytes per head) only
+    while its extra bytes stay under the cap; beyond it (long contexts) the
+    O(L) base workspace is used."""
+    cap = H.STORED_DS_EXTRA_BYTES_CAP
+    assert cap == 1 << 30
+    # c3 sequence: 16 heads x (128 x 129 / 2) blocks x 4 KiB = 541 MB -> stored dS
+    base, stored, pick = H.sdpa_backward_workspace_choice(4096, 4096, 1024, 16, True)
+    assert stored - base - 16 * (128 * 129 // 2) * 32 * 32 * 4 in range(0, 256)
+    assert pick == stored
+    # 16384 keys: 8.6 GB of dS blocks -> the base size
+    base, stored, pick = H.sdpa_backward_workspace_choice(16384, 16384, 1024, 16, True)
+    assert stored - base > cap and pick == base
+    # a smaller cap moves the c3 case to the base size too
+    base, stored, pick = H.sdpa_backward_workspace_choice(4096, 4096, 1024, 16, True, extra_cap=1 << 20)
+    assert pick == base
+    # shapes that cannot use stored dS (no causal flag, head dim 16) never ask for it
+    for args in ((512, 512, 512, 8, False), (512, 512, 256, 16, True)):
+        base, stored, pick = H.sdpa_backward_workspace_choice(*args)
+        assert stored == base and pick == base

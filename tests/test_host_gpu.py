@@ -129,7 +129,8 @@ def test_manager_attention_backward(mgr):
     scale 1/sqrt 3, decoder flag and explicit causal mask), the consistency
     suite's 6x8 no-mask / decoder and 5x8 cross cases
     (AccelerationConsistencyTests.cs:962-1020), and causal cases on the MFMA
-    kernels: 300x128 (head dim 64) by flag and by mask, 237x128 (head dim 32)."""
+    kernels: 300x128 (head dim 64) by flag and by mask, 237x128 and 700x128
+    (head dim 32, either side of the short stored-dS kernel's 512 rows)."""
     q, k, v, d = M(4, 6, 31), M(4, 6, 32), M(4, 6, 33), M(4, 6, 34)
     scale = float(np.float32(1) / np.sqrt(np.float32(3)))
     causal = np.tril(np.ones((4, 4), bool))
@@ -161,6 +162,12 @@ def test_manager_attention_backward(mgr):
     want = O.mha_backward(q, k, v, d, Hh, s, use_decoder_mask=True)
     for got, w, n in zip(mgr.MultiHeadAttentionBackward(q, k, v, d, Hh, s, True), want, ("dQ", "dK", "dV")):
         parity(got, w, f"MHA backward 237x128 head dim 32 causal {n}")
+    # head dim 32 past 512 rows: the stored-dS dQ of the long-sequence kernel
+    L = 700
+    q, k, v, d = (synth.normal(90 + i, (L, D)) for i in range(4))
+    want = O.mha_backward(q, k, v, d, Hh, s, use_decoder_mask=True)
+    for got, w, n in zip(mgr.MultiHeadAttentionBackward(q, k, v, d, Hh, s, True), want, ("dQ", "dK", "dV")):
+        parity(got, w, f"MHA backward 700x128 head dim 32 causal {n}")
 
 
 def test_manager_projection_backward(mgr):
