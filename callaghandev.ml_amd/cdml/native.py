@@ -87,6 +87,7 @@ SIGNATURES = {
     "cdml_sdpa_fwd": [_vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, _vp],
     "cdml_decode_attn_workspace_size": [_i, _i, _i, _i, C.POINTER(_sz)],
     "cdml_decode_attn": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp, _sz, _vp],
+    "cdml_decode_attn_noalloc": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp],
     "cdml_kv_cache_append": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp],
     "cdml_residual_layernorm": [_vp, _vp, _vp, _vp, _vp, _i, _i, _f, _vp],
     "cdml_embed_tokens": [_vp, _i, _vp, _i, _i, _vp, _vp, _vp],

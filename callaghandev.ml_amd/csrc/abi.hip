@@ -181,6 +181,9 @@ int cdml_init(int device) {
     return fail(CDML_E_INVALID, "cdml_init: device %d out of range [0, %d)", device, n);
   hipError_t e = hipSetDevice(device);
   if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+  // A failure here leaves the library usable; the no-allocation entry points
+  // then report it.
+  (void)noalloc_scratch_setup(device);
   g_device.store(device, std::memory_order_release);
   return CDML_OK;
 }

@@ -19,6 +19,11 @@ int fail(int code, const char *fmt, ...);
 // Makes the library's device current on the calling thread.
 int ensure_device();
 
+// Finds this device's copy of the static scratch behind the no-allocation
+// entry points (hipGetSymbolAddress); called by cdml_init with `device`
+// current.
+int noalloc_scratch_setup(int device);
+
 // Compute units of the current device (queried once; 256 on MI355X).
 int num_cus();
 

@@ -14,6 +14,8 @@
 // running sum, running output), so no workgroup barrier separates the K and V
 // streams.  The eight groups of a wave and then the four waves are merged with
 // the (max, sum) rescaling; a combine kernel merges the chunks.
+#include <mutex>
+
 #include "common.h"
 
 namespace cdml {
@@ -294,7 +296,41 @@ __global__ void __launch_bounds__(256) decode_split_generic_kernel(const DecodeA
 
 bool fast_hd(int hd) { return hd == 16 || hd == 32 || hd == 64 || hd == 128 || hd == 256; }
 
+
+// Partials of cdml_decode_attn_noalloc: a file-scope device array, one copy
+// per GPU, that lives until the process ends.  Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in for the
+// symbol); it uses the address hipGetSymbolAddress returned for the device.
+constexpr int kScratchMaxDevices = 64;
+static __device__ __align__(256) float scratch[CDML_DECODE_NOALLOC_MAX_BYTES / sizeof(float)];
+static std::mutex g_scratch_mu;
+static float *g_scratch_ptr[kScratchMaxDevices];
+
 }  // namespace
+
+// Looks up this device's copy of `scratch` once (the device is current).
+int noalloc_scratch_setup(int device) {
+  if (device < 0 || device >= kScratchMaxDevices)
+    return fail(CDML_E_INVALID, "device %d is beyond the %d devices the no-allocation entry points track",
+                device, kScratchMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[device]) return CDML_OK;
+  void *p = nullptr;
+  hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p) {
+    (void)hipGetLastError();
+    return fail(CDML_E_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
+  }
+  g_scratch_ptr[device] = static_cast<float *>(p);
+  return CDML_OK;
+}
+
+static float *noalloc_scratch_ptr(int device) {
+  if (device < 0 || device >= kScratchMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  return g_scratch_ptr[device];
+}
+
 }  // namespace cdml
 
 using namespace cdml;
@@ -310,38 +346,25 @@ extern "C" int cdml_decode_attn_workspace_size(int batch, int t_max, int dim, in
   return CDML_OK;
 }
 
-extern "C" int cdml_decode_attn(const float *q, const float *kcache, const float *vcache,
-                                const int *kv_len, float *o, int batch, int t_max, int dim,
-                                int num_heads, float scale, void *workspace,
-                                size_t workspace_bytes, cdml_stream stream) {
-  size_t need = 0;
-  int rc = cdml_decode_attn_workspace_size(batch, t_max, dim, num_heads, &need);
-  if (rc) return rc;
-  if (batch == 0) return CDML_OK;
-  if (t_max == 0) return cdml_zero_f32_async(o, (size_t)batch * dim, stream);
-  if (!q || !kcache || !vcache || !kv_len || !o)
-    return fail(CDML_E_INVALID, "cdml_decode_attn: NULL pointer");
-  if (!workspace || workspace_bytes < need)
-    return fail(CDML_E_INVALID, "cdml_decode_attn: workspace of %zu bytes needed, %zu given", need,
-                workspace_bytes);
-  if (batch > 65535 || num_heads > 65535)
-    return fail(CDML_E_INVALID, "cdml_decode_attn: batch and heads must be <= 65535");
-  rc = ensure_device();
-  if (rc) return rc;
+// Validated launch of the split and combine kernels over the partials buffer
+// `part` (at least cdml_decode_attn_workspace_size() bytes; every split
+// writes its whole slot, so the buffer needs no clearing).
+static int decode_launch(const float *q, const float *kcache, const float *vcache,
+                         const int *kv_len, float *o, int batch, int t_max, int dim,
+                         int num_heads, float scale, float *part, hipStream_t st) {
   DecodeArgs a{};
   a.q = q;
   a.kc = kcache;
   a.vc = vcache;
   a.kv_len = kv_len;
   a.o = o;
-  a.part = static_cast<float *>(workspace);
+  a.part = part;
   a.t_max = t_max;
   a.dim = dim;
   a.heads = num_heads;
   a.hd = dim / num_heads;
   a.nsplit = (t_max + DC_CHUNK - 1) / DC_CHUNK;
   a.scale_log2 = scale * 1.4426950408889634f;
-  hipStream_t st = as_hip(stream);
   dim3 grid(a.nsplit, num_heads, batch);
   const bool vec = fast_hd(a.hd) && dim % 4 == 0 && aligned16(q) && aligned16(kcache) &&
                    aligned16(vcache);
@@ -372,8 +395,62 @@ extern "C" int cdml_decode_attn(const float *q, const float *kcache, const float
     return check_launch("decode_split_kernel/decode_combine_vec_kernel");
   }
   decode_split_generic_kernel<<<grid, 256, sizeof(float) * (256 + 8), st>>>(a);
-  rc = check_launch("decode_split_generic_kernel");
+  int rc = check_launch("decode_split_generic_kernel");
   if (rc) return rc;
   decode_combine_kernel<<<dim3(num_heads, batch), dim3(a.hd < 256 ? 128 : 256), 0, st>>>(a);
   return check_launch("decode_combine_kernel");
+}
+
+extern "C" int cdml_decode_attn(const float *q, const float *kcache, const float *vcache,
+                                const int *kv_len, float *o, int batch, int t_max, int dim,
+                                int num_heads, float scale, void *workspace,
+                                size_t workspace_bytes, cdml_stream stream) {
+  size_t need = 0;
+  int rc = cdml_decode_attn_workspace_size(batch, t_max, dim, num_heads, &need);
+  if (rc) return rc;
+  if (batch == 0) return CDML_OK;
+  if (t_max == 0) return cdml_zero_f32_async(o, (size_t)batch * dim, stream);
+  if (!q || !kcache || !vcache || !kv_len || !o)
+    return fail(CDML_E_INVALID, "cdml_decode_attn: NULL pointer");
+  if (!workspace || workspace_bytes < need)
+    return fail(CDML_E_INVALID, "cdml_decode_attn: workspace of %zu bytes needed, %zu given", need,
+                workspace_bytes);
+  if (batch > 65535 || num_heads > 65535)
+    return fail(CDML_E_INVALID, "cdml_decode_attn: batch and heads must be <= 65535");
+  rc = ensure_device();
+  if (rc) return rc;
+  return decode_launch(q, kcache, vcache, kv_len, o, batch, t_max, dim, num_heads, scale,
+                       static_cast<float *>(workspace), as_hip(stream));
+}
+
+extern "C" int cdml_decode_attn_noalloc(const float *q, const float *kcache, const float *vcache,
+                                        const int *kv_len, float *o, int batch, int t_max, int dim,
+                                        int num_heads, float scale, cdml_stream stream) {
+  size_t need = 0;
+  int rc = cdml_decode_attn_workspace_size(batch, t_max, dim, num_heads, &need);
+  if (rc) return rc;
+  if (batch == 0) return CDML_OK;
+  if (t_max == 0) return cdml_zero_f32_async(o, (size_t)batch * dim, stream);
+  if (!q || !kcache || !vcache || !kv_len || !o)
+    return fail(CDML_E_INVALID, "cdml_decode_attn_noalloc: NULL pointer");
+  if (need > (size_t)CDML_DECODE_NOALLOC_MAX_BYTES)
+    return fail(CDML_E_INVALID,
+                "cdml_decode_attn_noalloc: the shape needs %zu bytes of partials, more than the %zu "
+                "bytes of the library's static scratch; call cdml_decode_attn with a workspace",
+                need, (size_t)CDML_DECODE_NOALLOC_MAX_BYTES);
+  if (batch > 65535 || num_heads > 65535)
+    return fail(CDML_E_INVALID, "cdml_decode_attn_noalloc: batch and heads must be <= 65535");
+  rc = ensure_device();
+  if (rc) return rc;
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(CDML_E_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  float *part = noalloc_scratch_ptr(dev);
+  if (!part) {  // cdml_init sets it up; a device made current some other way gets it here
+    rc = noalloc_scratch_setup(dev);
+    if (rc) return rc;
+    part = noalloc_scratch_ptr(dev);
+  }
+  return decode_launch(q, kcache, vcache, kv_len, o, batch, t_max, dim, num_heads, scale, part,
+                       as_hip(stream));
 }

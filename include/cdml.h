@@ -466,6 +466,22 @@ int cdml_decode_attn(const float *q, const float *kcache, const float *vcache,
                      int dim, int num_heads, float scale, void *workspace,
                      size_t workspace_bytes, cdml_stream stream);
 
+/* cdml_decode_attn without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * split-K partials live in a static device array of the library, one per
+ * GPU, of CDML_DECODE_NOALLOC_MAX_BYTES; shapes whose partials
+ * (cdml_decode_attn_workspace_size) exceed it fail with CDML_E_INVALID.
+ * Allocates nothing and frees nothing.  Every call on one GPU shares that
+ * array: calls that overlap on one GPU (two streams, two threads) race, so
+ * such callers must order them.  Results are identical to cdml_decode_attn's
+ * (same kernels). */
+#define CDML_DECODE_NOALLOC_MAX_BYTES (32u << 20)
+int cdml_decode_attn_noalloc(const float *q, const float *kcache,
+                             const float *vcache, const int *kv_len, float *o,
+                             int batch, int t_max, int dim, int num_heads,
+                             float scale, cdml_stream stream);
+
 /* Appends one K row and one V row per sequence to the decode cache, as
  * LanguageModel.cs:356-363 does: kcache[b, positions[b], :] = k_new[b, :]
  * (same for V).  positions is device int32[batch], each in [0, t_max). */
