@@ -390,15 +390,25 @@ def extras(N, st, only=None):
             return mgr.ProjectOutputBatch(a, wo, bz, L, D)
 
         mha_host()
+        s0 = mgr.transfer_stats()
+        reps = 5
         t0 = time.perf_counter()
-        for _ in range(3):
+        for _ in range(reps):
             mha_host()
-        dt = (time.perf_counter() - t0) / 3
+        dt = (time.perf_counter() - t0) / reps
+        s1 = mgr.transfer_stats()
         core, qkv, o = mha_flops(1, L, D, Hh)
+        pcie = pinned_pcie_bandwidth(N, st)
         out["c3_mha_one_sequence_dropin_host_arrays"] = {
             "ms": round(dt * 1e3, 3), "tflops": round((core + qkv + o) / dt / 1e12, 3),
-            "note": "HipAccelerationManager with float[,]-style host arrays: every call uploads its "
-                    "activations and downloads its result (PCIe included); weights stay resident"}
+            "h2d_mib_per_sequence": round((s1["h2d_bytes"] - s0["h2d_bytes"]) / reps / 2**20, 2),
+            "d2h_mib_per_sequence": round((s1["d2h_bytes"] - s0["d2h_bytes"]) / reps / 2**20, 2),
+            "h2d_mib_saved_per_sequence": round((s1["h2d_skipped_bytes"] - s0["h2d_skipped_bytes"]) / reps / 2**20, 2),
+            "pinned_pcie_gbs": pcie, "host_copy_threads": H.host_copy_threads(),
+            "note": "HipAccelerationManager with float[,]-style host arrays (PCIe included): each call "
+                    "stages its transfers through pinned memory; returned activations stay on the device "
+                    "and are uploaded again only when the shadow compare finds a host change; weights "
+                    "stay resident"}
     if want("c5_time_series_model"):
         # c5: time-series regression transformer, full forward, B 256 x L 512
         log("[bench] extras: c5 time-series model")
@@ -465,6 +475,33 @@ def host_cpu_info():
     used = min(proc_count, share) if share else proc_count
     return {"processor_count": proc_count, "nproc": affinity, "os_cpu_count": os.cpu_count(),
             "cgroup_cpu_quota": quota, "box_cpu_share": share, "threads_used": used, "cpu_model": model}
+
+
+def pinned_pcie_bandwidth(N, st, mib=256, reps=5):
+    """Host<->device copy rate between pinned host memory and HBM (GB/s), the
+    bound of the drop-in manager's staged transfers."""
+    lib = N.lib()
+    nbytes = mib << 20
+    hp = C.c_void_p()
+    N.check(lib.cdml_host_alloc_pinned(C.byref(hp), nbytes))
+    d = N.DeviceBuffer(nbytes)
+    res = {}
+    try:
+        for name, fn, args in (("h2d", lib.cdml_memcpy_h2d_async, (d.ptr, hp.value)),
+                               ("d2h", lib.cdml_memcpy_d2h_async, (hp.value, d.ptr))):
+            N.check(fn(*args, nbytes, st.handle))
+            st.synchronize()
+            e0, e1 = N.Event(), N.Event()
+            e0.record(st)
+            for _ in range(reps):
+                N.check(fn(*args, nbytes, st.handle))
+            e1.record(st)
+            ms = e0.elapsed_ms(e1) / reps
+            res[name] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+    finally:
+        d.free()
+        lib.cdml_host_free_pinned(hp.value)
+    return res
 
 
 def cpu_baseline(sample_seqs=3):

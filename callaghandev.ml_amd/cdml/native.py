@@ -55,6 +55,7 @@ SIGNATURES = {
     "cdml_event_create": [C.POINTER(_vp)],
     "cdml_event_destroy": [_vp],
     "cdml_event_record": [_vp, _vp],
+    "cdml_event_synchronize": [_vp],
     "cdml_event_elapsed_ms": [_vp, _vp, C.POINTER(_f)],
     "cdml_malloc": [C.POINTER(_vp), _sz],
     "cdml_free": [_vp],

@@ -310,6 +310,13 @@ int cdml_event_record(cdml_event event, cdml_stream stream) {
   return CDML_OK;
 }
 
+int cdml_event_synchronize(cdml_event event) {
+  if (!event) return fail(CDML_E_INVALID, "cdml_event_synchronize: event is NULL");
+  hipError_t e = hipEventSynchronize(reinterpret_cast<hipEvent_t>(event));
+  if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+  return CDML_OK;
+}
+
 int cdml_event_elapsed_ms(cdml_event start, cdml_event stop, float *ms) {
   if (!start || !stop || !ms) return fail(CDML_E_INVALID, "cdml_event_elapsed_ms: NULL argument");
   hipError_t e = hipEventSynchronize(reinterpret_cast<hipEvent_t>(stop));

@@ -94,8 +94,8 @@ VecRef vec_inout(const py::object &o) {
 }
 
 py::array_t<float> to_numpy(Matrix &&m) {
-  auto *v = new std::vector<float>(std::move(m.data));
-  py::capsule owner(v, [](void *p) { delete static_cast<std::vector<float> *>(p); });
+  auto *v = new FloatBuf(std::move(m.data));
+  py::capsule owner(v, [](void *p) { delete static_cast<FloatBuf *>(p); });
   return py::array_t<float>({(py::ssize_t)m.rows, (py::ssize_t)m.cols},
                             {(py::ssize_t)(m.cols * sizeof(float)), (py::ssize_t)sizeof(float)}, v->data(),
                             owner);
@@ -179,6 +179,15 @@ std::vector<int> ids_from(const py::object &o) {
   return std::vector<int>(a.data(), a.data() + a.size());
 }
 
+// Runs f with the GIL released: the manager's methods only touch C++ data
+// and the numpy buffers that the argument holders keep alive, so other
+// Python threads (other managers) run meanwhile.
+template <class F>
+auto nogil(F &&f) -> decltype(f()) {
+  py::gil_scoped_release release;
+  return f();
+}
+
 }  // namespace
 
 PYBIND11_MODULE(_cdml_host, m) {
@@ -211,7 +220,7 @@ PYBIND11_MODULE(_cdml_host, m) {
               py::object bk, py::object wv, py::object bv) {
              auto X = mat(x), WQ = mat(wq), WK = mat(wk), WV = mat(wv);
              auto BQ = vec(bq), BK = vec(bk), BV = vec(bv);
-             auto r = a.ProjectQKV(X.view, WQ.view, BQ.view, WK.view, BK.view, WV.view, BV.view);
+             auto r = nogil([&] { return a.ProjectQKV(X.view, WQ.view, BQ.view, WK.view, BK.view, WV.view, BV.view); });
              return py::make_tuple(to_numpy(std::move(std::get<0>(r))), to_numpy(std::move(std::get<1>(r))),
                                    to_numpy(std::move(std::get<2>(r))));
            })
@@ -220,7 +229,7 @@ PYBIND11_MODULE(_cdml_host, m) {
               py::object msk, bool causal) {
              auto Q = mat(q), K = mat(k), V = mat(v);
              auto M = mask(msk);
-             return to_numpy(a.ScaledDotProductAttention(Q.view, K.view, V.view, numHeads, M.view, causal));
+             return to_numpy(nogil([&] { return a.ScaledDotProductAttention(Q.view, K.view, V.view, numHeads, M.view, causal); }));
            },
            py::arg("q"), py::arg("k"), py::arg("v"), py::arg("numHeads"), py::arg("mask") = py::none(),
            py::arg("causal") = false)
@@ -229,7 +238,7 @@ PYBIND11_MODULE(_cdml_host, m) {
               float scale, py::object msk) {
              auto Q = mat(q), K = mat(k), V = mat(v);
              auto M = mask(msk);
-             return to_numpy(a.MultiHeadAttentionForward(Q.view, K.view, V.view, numHeads, scale, M.view));
+             return to_numpy(nogil([&] { return a.MultiHeadAttentionForward(Q.view, K.view, V.view, numHeads, scale, M.view); }));
            },
            py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("numHeads"), py::arg("scale"),
            py::arg("mask") = py::none())
@@ -237,51 +246,55 @@ PYBIND11_MODULE(_cdml_host, m) {
            [](HipAccelerationManager &a, py::object h, py::object w, py::object b, int seqLen, int outputDim) {
              auto Hh = mat(h), W = mat(w);
              auto B = vec(b);
-             return to_numpy(a.ProjectOutputBatch(Hh.view, W.view, B.view, seqLen, outputDim));
+             return to_numpy(nogil([&] { return a.ProjectOutputBatch(Hh.view, W.view, B.view, seqLen, outputDim); }));
            })
       .def("BatchDotProductAddBias",
            [](HipAccelerationManager &a, py::object w, py::object x, py::object b) {
              auto W = mat(w), X = mat(x);
              auto B = vec(b);
-             return to_numpy(a.BatchDotProductAddBias(W.view, X.view, B.view));
+             return to_numpy(nogil([&] { return a.BatchDotProductAddBias(W.view, X.view, B.view); }));
            })
       .def("BatchDotProductAddBias",
            [](HipAccelerationManager &a, py::object w, py::object x, int rowStart, int rowCount, py::object b) {
              auto W = mat(w), X = mat(x);
              auto B = vec(b);
-             return to_numpy(a.BatchDotProductAddBias(W.view, X.view, rowStart, rowCount, B.view));
+             return to_numpy(nogil([&] { return a.BatchDotProductAddBias(W.view, X.view, rowStart, rowCount, B.view); }));
            })
       .def("ApplyRotaryPositionEmbeddingInPlace",
            [](HipAccelerationManager &a, py::object mtx, int numHeads, float baseTheta, bool inverse) {
              if (mtx.is_none()) throw ArgumentNullException("matrix");
              py::array arr = mtx;
-             a.ApplyRotaryPositionEmbeddingInPlace(mat_inplace(arr), numHeads, baseTheta, inverse);
+             MatRef m = mat_inplace(arr);
+             nogil([&] { a.ApplyRotaryPositionEmbeddingInPlace(m, numHeads, baseTheta, inverse); });
            })
       .def("ApplyRotaryPositionEmbeddingHeadInPlace",
            [](HipAccelerationManager &a, py::object mtx, int startCol, int headDim, float baseTheta,
               bool inverse) {
              if (mtx.is_none()) throw ArgumentNullException("matrix");
              py::array arr = mtx;
-             a.ApplyRotaryPositionEmbeddingHeadInPlace(mat_inplace(arr), startCol, headDim, baseTheta, inverse);
+             MatRef m = mat_inplace(arr);
+             nogil([&] { a.ApplyRotaryPositionEmbeddingHeadInPlace(m, startCol, headDim, baseTheta, inverse); });
            })
       .def("ResidualLayerNorm",
            [](HipAccelerationManager &a, py::object x, py::object s, py::object g, py::object b, float eps) {
              auto X = mat(x), S = mat(s);
              auto G = vec(g), B = vec(b);
-             return to_numpy(a.ResidualLayerNorm(X.view, S.view, G.view, B.view, eps));
+             return to_numpy(nogil([&] { return a.ResidualLayerNorm(X.view, S.view, G.view, B.view, eps); }));
            },
            py::arg("input"), py::arg("subLayer"), py::arg("gamma"), py::arg("beta"), py::arg("epsilon") = 1e-5f)
       .def("EmbedTokenIds",
            [](HipAccelerationManager &a, py::object ids, py::object emb, int dim) {
              if (ids.is_none()) throw ArgumentNullException("tokenIds");
              auto E = mat(emb);
-             return to_numpy(a.EmbedTokenIds(ids_from(ids), E.view, dim));
+             std::vector<int> I = ids_from(ids);
+             return to_numpy(nogil([&] { return a.EmbedTokenIds(I, E.view, dim); }));
            })
       .def("EmbedTokenIds",
            [](HipAccelerationManager &a, py::object ids, int start, int count, py::object emb, int dim) {
              if (ids.is_none()) throw ArgumentNullException("tokenIds");
              auto E = mat(emb);
-             return to_numpy(a.EmbedTokenIds(ids_from(ids), start, count, E.view, dim));
+             std::vector<int> I = ids_from(ids);
+             return to_numpy(nogil([&] { return a.EmbedTokenIds(I, start, count, E.view, dim); }));
            })
       .def("CreateCausalMask",
            [](HipAccelerationManager &a, int n) {
@@ -300,26 +313,27 @@ PYBIND11_MODULE(_cdml_host, m) {
              ffn.activations = acts;
              if (ffn.biases.size() != ffn.weights.size() || ffn.activations.size() != ffn.weights.size())
                throw ArgumentException("FFN weights, biases and activations must have equal counts");
-             return to_numpy(a.FFNForwardBatch(X.view, seqLen, outputDim, ffn));
+             return to_numpy(nogil([&] { return a.FFNForwardBatch(X.view, seqLen, outputDim, ffn); }));
            })
       .def("DecodeSelfAttention",
            [](HipAccelerationManager &a, py::array q, py::array k, py::object v, py::array keys,
               py::array values, int pos, int numHeads) {
              auto V = mat(v);
-             return to_numpy(a.DecodeSelfAttention(mat_inplace(q), mat_inplace(k), V.view, mat_inplace(keys),
-                                                   mat_inplace(values), pos, numHeads));
+             MatRef Q = mat_inplace(q), K = mat_inplace(k), KS = mat_inplace(keys), VS = mat_inplace(values);
+             return to_numpy(nogil([&] { return a.DecodeSelfAttention(Q, K, V.view, KS, VS, pos, numHeads); }));
            })
       .def("MultiHeadAttentionBackward",
            [](HipAccelerationManager &a, py::object q, py::object k, py::object v, py::object dout,
               int numHeads, float scale, py::object maskOrDecoder) {
              auto Q = mat(q), K = mat(k), V = mat(v), D = mat(dout);
              std::tuple<Matrix, Matrix, Matrix> r;
-             if (py::isinstance<py::bool_>(maskOrDecoder))  // the useDecoderMask overload
-               r = a.MultiHeadAttentionBackward(Q.view, K.view, V.view, D.view, numHeads, scale,
-                                                maskOrDecoder.cast<bool>());
+             if (py::isinstance<py::bool_>(maskOrDecoder)) {  // the useDecoderMask overload
+               const bool dec = maskOrDecoder.cast<bool>();
+               r = nogil([&] { return a.MultiHeadAttentionBackward(Q.view, K.view, V.view, D.view, numHeads, scale, dec); });
+             }
              else {
                auto M = mask(maskOrDecoder);
-               r = a.MultiHeadAttentionBackward(Q.view, K.view, V.view, D.view, numHeads, scale, M.view);
+               r = nogil([&] { return a.MultiHeadAttentionBackward(Q.view, K.view, V.view, D.view, numHeads, scale, M.view); });
              }
              return py::make_tuple(to_numpy(std::move(std::get<0>(r))), to_numpy(std::move(std::get<1>(r))),
                                    to_numpy(std::move(std::get<2>(r))));
@@ -332,38 +346,45 @@ PYBIND11_MODULE(_cdml_host, m) {
               py::object bkg, py::object wvg, py::object bvg) {
              auto X = mat(x), DQ = mat(dq), DK = mat(dk), DV = mat(dv), WQ = mat(wq), WK = mat(wk),
                   WV = mat(wv);
-             return to_numpy(a.BackpropQKV(X.view, DQ.view, DK.view, DV.view, WQ.view, WK.view, WV.view,
-                                           mat_inout(wqg), vec_inout(bqg), mat_inout(wkg), vec_inout(bkg),
-                                           mat_inout(wvg), vec_inout(bvg)));
+             MatRef GQ = mat_inout(wqg), GK = mat_inout(wkg), GV = mat_inout(wvg);
+             VecRef BQ = vec_inout(bqg), BK = vec_inout(bkg), BV = vec_inout(bvg);
+             return to_numpy(nogil([&] {
+               return a.BackpropQKV(X.view, DQ.view, DK.view, DV.view, WQ.view, WK.view, WV.view, GQ, BQ, GK, BK, GV, BV);
+             }));
            })
       .def("BackpropLinearProjection",
            [](HipAccelerationManager &a, py::object x, py::object dy, py::object w, py::object wg,
               py::object bg, py::object dx) {
              auto X = mat(x), DY = mat(dy), W = mat(w);
-             a.BackpropLinearProjection(X.view, DY.view, W.view, mat_inout(wg), vec_inout(bg), mat_inout(dx));
+             MatRef WG = mat_inout(wg), DX = mat_inout(dx);
+             VecRef BG = vec_inout(bg);
+             nogil([&] { a.BackpropLinearProjection(X.view, DY.view, W.view, WG, BG, DX); });
            })
       .def("BackpropOutputProjection",
            [](HipAccelerationManager &a, py::object dl, py::object x, py::object w, py::object wg,
               py::object bg, int seqLen, int outputDim, int embeddingDim) {
              auto DL = mat(dl), X = mat(x), W = mat(w);
-             return to_numpy(a.BackpropOutputProjection(DL.view, X.view, W.view, mat_inout(wg), vec_inout(bg),
-                                                        seqLen, outputDim, embeddingDim));
+             MatRef WG = mat_inout(wg);
+             VecRef BG = vec_inout(bg);
+             return to_numpy(nogil([&] {
+               return a.BackpropOutputProjection(DL.view, X.view, W.view, WG, BG, seqLen, outputDim, embeddingDim);
+             }));
            })
       .def("MatrixMultiply",
            [](HipAccelerationManager &a, py::object A, py::object B) {
              auto X = mat(A), Y = mat(B);
-             return to_numpy(a.MatrixMultiply(X.view, Y.view));
+             return to_numpy(nogil([&] { return a.MatrixMultiply(X.view, Y.view); }));
            })
       .def("MatrixMultiplyTranspose",
            [](HipAccelerationManager &a, py::object A, py::object B) {
              auto X = mat(A), Y = mat(B);
-             return to_numpy(a.MatrixMultiplyTranspose(X.view, Y.view));
+             return to_numpy(nogil([&] { return a.MatrixMultiplyTranspose(X.view, Y.view); }));
            })
       .def("ResidualLayerNormForward",
            [](HipAccelerationManager &a, py::object x, py::object sl, py::object g, py::object b, float eps) {
              auto X = mat(x), S = mat(sl);
              auto G = vec(g), B = vec(b);
-             auto r = a.ResidualLayerNormForward(X.view, S.view, G.view, B.view, eps);
+             auto r = nogil([&] { return a.ResidualLayerNormForward(X.view, S.view, G.view, B.view, eps); });
              return py::make_tuple(to_numpy(std::move(std::get<0>(r))), vec_to_numpy(std::get<1>(r)),
                                    vec_to_numpy(std::get<2>(r)), to_numpy(std::move(std::get<3>(r))),
                                    to_numpy(std::move(std::get<4>(r))));
@@ -374,7 +395,7 @@ PYBIND11_MODULE(_cdml_host, m) {
               py::object v, float eps) {
              auto D = mat(d), Nn = mat(n), X = mat(x);
              auto G = vec(g), M = vec(m), V = vec(v);
-             auto r = a.LayerNormBackward(D.view, Nn.view, G.view, X.view, M.view, V.view, eps);
+             auto r = nogil([&] { return a.LayerNormBackward(D.view, Nn.view, G.view, X.view, M.view, V.view, eps); });
              return py::make_tuple(to_numpy(std::move(std::get<0>(r))), vec_to_numpy(std::get<1>(r)),
                                    vec_to_numpy(std::get<2>(r)));
            },
@@ -384,7 +405,8 @@ PYBIND11_MODULE(_cdml_host, m) {
            [](HipAccelerationManager &a, py::object logits, py::object targets, int targetStart, int effectiveLen) {
              if (targets.is_none()) throw ArgumentNullException("targets");
              auto L = mat(logits);
-             auto r = a.CrossEntropyLossAndGradient(L.view, ids_from(targets), targetStart, effectiveLen);
+             std::vector<int> T = ids_from(targets);
+             auto r = nogil([&] { return a.CrossEntropyLossAndGradient(L.view, T, targetStart, effectiveLen); });
              return py::make_tuple(r.first, to_numpy(std::move(r.second)));
            },
            py::arg("logits"), py::arg("targets"), py::arg("targetStart"), py::arg("effectiveLen"))
@@ -392,7 +414,7 @@ PYBIND11_MODULE(_cdml_host, m) {
            [](HipAccelerationManager &a, py::object pred, py::object targets, int targetStart, int effectiveLen) {
              auto P = mat(pred);
              auto T = mat(targets);
-             auto r = a.MSELossAndGradient(P.view, T.view, targetStart, effectiveLen);
+             auto r = nogil([&] { return a.MSELossAndGradient(P.view, T.view, targetStart, effectiveLen); });
              return py::make_tuple(r.first, to_numpy(std::move(r.second)));
            },
            py::arg("predictions"), py::arg("targets"), py::arg("targetStart"), py::arg("effectiveLen"))
@@ -401,9 +423,35 @@ PYBIND11_MODULE(_cdml_host, m) {
               int dim) {
              if (ids.is_none()) throw ArgumentNullException("tokenIds");
              auto D = mat(dx);
-             a.AccumulateTokenEmbeddingGrad(mat_inout(eg), D.view, ids_from(ids), tokenStart, seqLen, dim);
+             MatRef EG = mat_inout(eg);
+             std::vector<int> I = ids_from(ids);
+             nogil([&] { a.AccumulateTokenEmbeddingGrad(EG, D.view, I, tokenStart, seqLen, dim); });
+           })
+      .def("SetActivationCacheLimit", &HipAccelerationManager::SetActivationCacheLimit, py::arg("bytes"))
+      .def_property_readonly("activation_cache_limit", &HipAccelerationManager::activation_cache_limit)
+      .def_property_readonly("activation_cache_entries", &HipAccelerationManager::activation_cache_entries)
+      .def("transfer_stats",
+           [](HipAccelerationManager &a) {
+             auto t = a.transfer_stats();
+             py::dict d;
+             d["h2d_bytes"] = t.h2d_bytes;
+             d["d2h_bytes"] = t.d2h_bytes;
+             d["h2d_skipped_bytes"] = t.h2d_skipped_bytes;
+             return d;
            })
       .def("Dispose", &HipAccelerationManager::Dispose);
+  m.def("host_copy_threads", &HostCopyThreads);
+  // The host copy engine on byte arrays (for tests of its slicing).
+  m.def("_parallel_copy", [](py::array_t<uint8_t, py::array::c_style | py::array::forcecast> a) {
+    py::array_t<uint8_t> out(a.size());
+    ParallelMemcpy(out.mutable_data(), a.data(), (size_t)a.size());
+    return out;
+  });
+  m.def("_parallel_equal", [](py::array_t<uint8_t, py::array::c_style | py::array::forcecast> a,
+                              py::array_t<uint8_t, py::array::c_style | py::array::forcecast> b) {
+    if (a.size() != b.size()) return false;
+    return ParallelEqual(a.data(), b.data(), (size_t)a.size());
+  });
 
   py::class_<TransformerConfig>(m, "TransformerConfig")
       .def(py::init<>())

@@ -31,6 +31,7 @@
 #include <string>
 #include <tuple>
 #include <unordered_map>
+#include <utility>
 #include <vector>
 
 #include "cdml.h"
@@ -61,11 +62,53 @@ struct FileNotFoundException : std::runtime_error {  // System.IO.FileNotFoundEx
 };
 
 // ---- host arrays (row-major, the float[,] layout) ------------------------
+// Storage of large host arrays (staging.cpp): blocks of 1 MiB and more are
+// recycled through a process-wide cache (up to 1 GiB of idle blocks) instead
+// of going back to the OS, so a result array of the same size as an earlier
+// one lands in memory that is already mapped (a freshly mapped block costs a
+// page fault per 4 KiB on its first write).  .NET's large-object heap keeps
+// its segments the same way.
+void *HostArrayAlloc(size_t bytes);
+void HostArrayFree(void *p, size_t bytes);
+
+// An allocator that leaves new elements uninitialised, for result arrays
+// that a device download overwrites completely (their zero fill would cost a
+// pass over the memory), on the recycled storage above.
+template <class T>
+struct DefaultInitAllocator : std::allocator<T> {
+  template <class U>
+  struct rebind {
+    using other = DefaultInitAllocator<U>;
+  };
+  DefaultInitAllocator() = default;
+  template <class U>
+  DefaultInitAllocator(const DefaultInitAllocator<U> &) noexcept {}  // NOLINT
+  T *allocate(size_t n) { return static_cast<T *>(HostArrayAlloc(n * sizeof(T))); }
+  void deallocate(T *p, size_t n) noexcept { HostArrayFree(p, n * sizeof(T)); }
+  template <class U>
+  void construct(U *p) noexcept {
+    ::new (static_cast<void *>(p)) U;
+  }
+  template <class U, class... A>
+  void construct(U *p, A &&...args) {
+    ::new (static_cast<void *>(p)) U(std::forward<A>(args)...);
+  }
+};
+using FloatBuf = std::vector<float, DefaultInitAllocator<float>>;
+
 struct Matrix {
   int rows = 0, cols = 0;
-  std::vector<float> data;
+  FloatBuf data;
   Matrix() = default;
   Matrix(int r, int c) : rows(r), cols(c), data((size_t)r * c, 0.f) {}
+  // Storage without the zero fill; every element must be written.
+  static Matrix Uninit(int r, int c) {
+    Matrix m;
+    m.rows = r;
+    m.cols = c;
+    m.data.resize((size_t)r * c);
+    return m;
+  }
   float *ptr() { return data.data(); }
   const float *ptr() const { return data.data(); }
   float &at(int r, int c) { return data[(size_t)r * cols + c]; }
@@ -128,6 +171,14 @@ struct FeedForwardNetwork {
   int input_size() const { return weights.empty() ? 0 : weights.front().cols; }
   int output_size() const { return weights.empty() ? 0 : weights.back().rows; }
 };
+
+// ---- host copies (staging.cpp) ---------------------------------------------
+// memcpy / memcmp split over a process-wide pool of host threads for large
+// sizes (the pool has min(12, 3/4 of the CPUs) threads beside the caller, or
+// CDML_HOST_COPY_THREADS).
+void ParallelMemcpy(void *dst, const void *src, size_t bytes);
+bool ParallelEqual(const void *a, const void *b, size_t bytes);
+int HostCopyThreads();
 
 // The attention backward's workspace: the stored-dS size (the causal 32 x 32
 // fp32 dS blocks, about 2 L^2 bytes per head: gigabytes at long context)
@@ -249,6 +300,25 @@ class HipAccelerationManager {
   bool disposed() const { return disposed_; }
   cdml_stream stream();  // the manager's own stream (created on first use)
 
+  // Resident activations: every activation array a method reads or returns
+  // keeps a device copy keyed by the host array's address, with the pinned
+  // staging buffer of its last transfer as the shadow of its contents (the
+  // resident cache of AccelerationManagers/GPU/DeviceResidentCache.cs:44-120,
+  // extended from weights to activations).  A later call that receives the
+  // same array compares it with the shadow and uploads it only when the
+  // host side changed.  The least recently used entries are dropped beyond
+  // `bytes` of device memory (and as much pinned memory); 0 turns the cache
+  // off, so every activation crosses PCIe on every call.
+  void SetActivationCacheLimit(size_t bytes);
+  size_t activation_cache_limit() const { return act_limit_; }
+  int activation_cache_entries();
+  // Host<->device bytes this manager has moved (uploads, downloads) and how
+  // many activation uploads the shadow compare saved.
+  struct TransferStats {
+    uint64_t h2d_bytes = 0, d2h_bytes = 0, h2d_skipped_bytes = 0;
+  };
+  TransferStats transfer_stats();
+
  private:
   struct Resident {
     int rows = 0, cols = 0;
@@ -264,6 +334,50 @@ class HipAccelerationManager {
     int rows = 0, cols = 0, uploaded = 0;
   };
 
+  struct ActEntry {
+    int rows = 0, cols = 0;
+    void *dev = nullptr, *pin = nullptr;
+    size_t cap = 0;
+    uint64_t last = 0, busy = 0;
+  };
+  struct Xfer {  // one host<->device transfer staged through pinned memory
+    void *host;
+    void *dev;
+    size_t bytes;
+    void *pin;
+  };
+  // Deferred shadow compares: while defer_ is set, act_in and resident hand
+  // out the device copy of a known array at once and record the compare;
+  // settle() runs the compares after the kernel was launched (so they
+  // overlap its execution), uploads what changed and returns false when
+  // anything did, in which case the caller launches again.  Only methods
+  // whose kernels write nothing but their results use it.
+  struct Pending {
+    const void *host;
+    void *shadow;  // pinned shadow of an activation, or a weight's host shadow
+    void *dev;
+    size_t bytes;
+    bool weight;
+  };
+  bool settle();
+  void begin_call();
+  void *stage_region(size_t bytes);
+  void stage_upload(void *dev, const void *host, size_t bytes, void *pin);
+  void download_all(const std::vector<Xfer> &xs);
+  const float *act_in(MatView m, int slot);
+  float *act_inplace(MatRef m, int slot);
+  float *act_out(float *host, int rows, int cols, int slot);
+  float *act_out(Matrix &out, int slot) { return act_out(out.ptr(), out.rows, out.cols, slot); }
+  struct Out {  // a result: host array and the device buffer it is downloaded from
+    float *host;
+    size_t floats;
+    const float *dev;
+  };
+  static Out out_of(Matrix &m, const float *dev) { return Out{m.ptr(), m.data.size(), dev}; }
+  void act_done(std::initializer_list<Out> outs);
+  ActEntry act_acquire(size_t bytes);
+  void act_release(const ActEntry &e);
+  void act_drop(const float *key);
   void ensure_ready();
   void *scratch(int slot, size_t bytes);
   void *try_scratch(int slot, size_t bytes);
@@ -287,6 +401,18 @@ class HipAccelerationManager {
   std::unordered_map<const float *, Resident> resident_;
   std::vector<DeviceBuf> scratch_;
   std::unordered_map<const float *, DecodeMirror> decode_;
+  // pinned staging: a grow-only buffer handed out front to back within a call
+  void *stage_ = nullptr;
+  size_t stage_cap_ = 0, stage_off_ = 0;
+  std::vector<cdml_event> events_;
+  bool dirty_ = false;  // work enqueued since the last synchronisation
+  bool defer_ = false;
+  std::vector<Pending> pending_;
+  std::unordered_map<const float *, ActEntry> acts_;
+  std::multimap<size_t, ActEntry> act_free_;
+  size_t act_held_ = 0, act_limit_ = size_t(1) << 30;
+  uint64_t tick_ = 0, call_ = 0;
+  TransferStats stats_;
 };
 
 // ---- the MultiTypeTransformer classes on the manager ----------------------

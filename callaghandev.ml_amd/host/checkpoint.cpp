@@ -270,7 +270,7 @@ FfnLayer read_ffn_layer(JsonReader &r) {
       });
       L.w.rows = rows;
       L.w.cols = cols < 0 ? 0 : cols;
-      L.w.data = std::move(flat);
+      L.w.data.assign(flat.begin(), flat.end());
     } else if (k == "Biases") {
       if (r.null()) return;
       L.has_b = true;

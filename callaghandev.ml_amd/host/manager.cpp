@@ -7,6 +7,7 @@
 // an InvalidOperationException.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 
 #include "cdml_host.h"
@@ -54,17 +55,64 @@ void HipAccelerationManager::Dispose() {
     cdml_free(kv.second.v);
   }
   decode_.clear();
+  for (auto &kv : acts_) act_release(kv.second);
+  acts_.clear();
+  for (auto &kv : act_free_) {
+    cdml_free(kv.second.dev);
+    cdml_host_free_pinned(kv.second.pin);
+  }
+  act_free_.clear();
+  act_held_ = 0;
+  cdml_host_free_pinned(stage_);
+  stage_ = nullptr;
+  stage_cap_ = stage_off_ = 0;
+  for (cdml_event e : events_) cdml_event_destroy(e);
+  events_.clear();
   cdml_stream_destroy(stream_);
   stream_ = nullptr;
 }
 
 void HipAccelerationManager::ensure_ready() {
   if (disposed_) throw InvalidOperationException("HipAccelerationManager has been disposed.");
-  if (ready_) return;
-  check(cdml_init(device_), "cdml_init");
-  check(cdml_stream_create(&stream_), "cdml_stream_create");
-  scratch_.assign(S_COUNT, DeviceBuf{});
-  ready_ = true;
+  if (!ready_) {
+    check(cdml_init(device_), "cdml_init");
+    check(cdml_stream_create(&stream_), "cdml_stream_create");
+    scratch_.assign(S_COUNT, DeviceBuf{});
+    ready_ = true;
+  }
+  begin_call();
+}
+
+// Every public method that touches the device starts here (through
+// ensure_ready, with mu_ held): the staging buffer is handed out from its
+// start again, and the call gets a new id that marks the activation entries
+// it uses as not evictable.
+void HipAccelerationManager::begin_call() {
+  if (dirty_) sync();  // an earlier call that threw may have left transfers in flight
+  stage_off_ = 0;
+  ++call_;
+  defer_ = false;
+  pending_.clear();
+}
+
+bool HipAccelerationManager::settle() {
+  defer_ = false;
+  bool current = true;
+  for (const Pending &p : pending_) {
+    if (ParallelEqual(p.host, p.shadow, p.bytes)) {
+      if (!p.weight) stats_.h2d_skipped_bytes += p.bytes;
+      continue;
+    }
+    current = false;
+    if (p.weight) {
+      ParallelMemcpy(p.shadow, p.host, p.bytes);
+      upload(p.dev, p.shadow, p.bytes);
+    } else {
+      stage_upload(p.dev, p.host, p.bytes, p.shadow);
+    }
+  }
+  pending_.clear();
+  return current;
 }
 
 cdml_stream HipAccelerationManager::stream() {
@@ -77,7 +125,7 @@ void *HipAccelerationManager::scratch(int slot, size_t bytes) {
   DeviceBuf &b = scratch_[slot];
   if (bytes == 0) bytes = 4;
   if (b.bytes < bytes) {
-    check(cdml_stream_synchronize(stream_), "cdml_stream_synchronize");
+    sync();
     check(cdml_free(b.p), "cdml_free");
     b.p = nullptr;
     b.bytes = 0;
@@ -94,7 +142,7 @@ void *HipAccelerationManager::try_scratch(int slot, size_t bytes) {
   DeviceBuf &b = scratch_[slot];
   if (bytes == 0) bytes = 4;
   if (b.bytes >= bytes) return b.p;
-  check(cdml_stream_synchronize(stream_), "cdml_stream_synchronize");
+  sync();
   check(cdml_free(b.p), "cdml_free");
   b.p = nullptr;
   b.bytes = 0;
@@ -110,15 +158,261 @@ size_t SdpaBackwardWorkspaceChoice(size_t base_bytes, size_t stored_ds_bytes, si
   return stored_ds_bytes - base_bytes <= extra_cap ? stored_ds_bytes : base_bytes;
 }
 
+// ---- pinned staging ----------------------------------------------------------
+// Every host<->device copy of the manager goes through pinned memory: either
+// the shadow buffer of a resident activation, or a region of the grow-only
+// staging buffer.  Regions are handed out front to back within one call, so
+// no region is reused while a transfer from it may still be in flight.
+namespace {
+// Bytes per DMA of a staged transfer (CDML_STAGE_CHUNK_MB, default 8): a
+// chunk's host copy overlaps the next chunk's DMA.
+size_t stage_chunk() {
+  static const size_t c = [] {
+    const char *e = std::getenv("CDML_STAGE_CHUNK_MB");
+    const int mb = e ? std::atoi(e) : 0;
+    return size_t(mb > 0 && mb <= 256 ? mb : 8) << 20;
+  }();
+  return c;
+}
+size_t round_up(size_t n, size_t a) { return (n + a - 1) / a * a; }
+}  // namespace
+
+void *HipAccelerationManager::stage_region(size_t bytes) {
+  bytes = round_up(std::max<size_t>(bytes, 1), 256);
+  if (stage_off_ + bytes > stage_cap_) {
+    sync();  // transfers that still read the current buffer finish first
+    const size_t cap = std::max(round_up(bytes, size_t(1) << 20), std::max(stage_cap_ * 2, size_t(4) << 20));
+    check(cdml_host_free_pinned(stage_), "cdml_host_free_pinned");
+    stage_ = nullptr;
+    stage_cap_ = 0;
+    check(cdml_host_alloc_pinned(&stage_, cap), "cdml_host_alloc_pinned");
+    stage_cap_ = cap;
+    stage_off_ = 0;
+  }
+  void *p = static_cast<char *>(stage_) + stage_off_;
+  stage_off_ += bytes;
+  return p;
+}
+
+// Host -> pinned -> device in chunks: the host copy of chunk i + 1 runs
+// while the DMA of chunk i is in flight.
+void HipAccelerationManager::stage_upload(void *dev, const void *host, size_t bytes, void *pin) {
+  const size_t kChunk = stage_chunk();
+  for (size_t off = 0; off < bytes; off += kChunk) {
+    const size_t n = std::min(kChunk, bytes - off);
+    ParallelMemcpy(static_cast<char *>(pin) + off, static_cast<const char *>(host) + off, n);
+    check(cdml_memcpy_h2d_async(static_cast<char *>(dev) + off, static_cast<char *>(pin) + off, n, stream_),
+          "cdml_memcpy_h2d_async");
+    dirty_ = true;
+  }
+  stats_.h2d_bytes += bytes;
+}
+
+// Device -> pinned -> host for a group of transfers: every chunk's DMA is
+// enqueued first, each followed by an event, then each chunk is copied out as
+// soon as its event has completed, while the later chunks are still moving.
+void HipAccelerationManager::download_all(const std::vector<Xfer> &xs) {
+  const size_t kChunk = stage_chunk();
+  size_t chunks = 0;
+  for (const Xfer &x : xs) chunks += (x.bytes + kChunk - 1) / kChunk;
+  while (events_.size() < chunks) {
+    cdml_event e = nullptr;
+    check(cdml_event_create(&e), "cdml_event_create");
+    events_.push_back(e);
+  }
+  size_t c = 0;
+  for (const Xfer &x : xs)
+    for (size_t off = 0; off < x.bytes; off += kChunk, ++c) {
+      const size_t n = std::min(kChunk, x.bytes - off);
+      check(cdml_memcpy_d2h_async(static_cast<char *>(x.pin) + off, static_cast<const char *>(x.dev) + off, n,
+                                  stream_),
+            "cdml_memcpy_d2h_async");
+      check(cdml_event_record(events_[c], stream_), "cdml_event_record");
+      dirty_ = true;
+    }
+  c = 0;
+  for (const Xfer &x : xs) {
+    for (size_t off = 0; off < x.bytes; off += kChunk, ++c) {
+      const size_t n = std::min(kChunk, x.bytes - off);
+      check(cdml_event_synchronize(events_[c]), "cdml_event_synchronize");
+      ParallelMemcpy(static_cast<char *>(x.host) + off, static_cast<const char *>(x.pin) + off, n);
+    }
+    stats_.d2h_bytes += x.bytes;
+  }
+}
+
 void HipAccelerationManager::upload(void *dev, const void *host, size_t bytes) {
-  check(cdml_memcpy_h2d_async(dev, host, bytes, stream_), "cdml_memcpy_h2d_async");
+  if (bytes == 0) return;
+  stage_upload(dev, host, bytes, stage_region(bytes));
 }
 
 void HipAccelerationManager::download(void *host, const void *dev, size_t bytes) {
-  check(cdml_memcpy_d2h_async(host, dev, bytes, stream_), "cdml_memcpy_d2h_async");
+  if (bytes == 0) return;
+  download_all({Xfer{host, const_cast<void *>(dev), bytes, stage_region(bytes)}});
 }
 
-void HipAccelerationManager::sync() { check(cdml_stream_synchronize(stream_), "cdml_stream_synchronize"); }
+void HipAccelerationManager::sync() {
+  check(cdml_stream_synchronize(stream_), "cdml_stream_synchronize");
+  dirty_ = false;
+}
+
+// ---- resident activations ------------------------------------------------------
+// An entry pairs a device buffer with a pinned buffer of the same capacity;
+// the pinned one holds exactly the bits of the device one (it was the staging
+// buffer of the last transfer in either direction), so comparing the host
+// array with it tells whether the device copy is still current.
+HipAccelerationManager::ActEntry HipAccelerationManager::act_acquire(size_t bytes) {
+  const size_t cap = round_up(std::max<size_t>(bytes, 1), size_t(64) << 10);
+  auto fit = act_free_.lower_bound(cap);
+  if (fit != act_free_.end() && fit->first <= 2 * cap) {
+    ActEntry e = fit->second;
+    act_free_.erase(fit);
+    return e;
+  }
+  // make room: idle buffers first, then the least recently used entries that
+  // this call does not use
+  while (act_held_ + cap > act_limit_) {
+    if (!act_free_.empty()) {
+      auto it = std::prev(act_free_.end());
+      cdml_free(it->second.dev);
+      cdml_host_free_pinned(it->second.pin);
+      act_held_ -= it->first;
+      act_free_.erase(it);
+      continue;
+    }
+    auto lru = acts_.end();
+    for (auto it = acts_.begin(); it != acts_.end(); ++it)
+      if (it->second.busy != call_ && (lru == acts_.end() || it->second.last < lru->second.last)) lru = it;
+    if (lru == acts_.end()) break;  // everything left is in use by this call
+    const ActEntry old = lru->second;
+    acts_.erase(lru);
+    cdml_free(old.dev);
+    cdml_host_free_pinned(old.pin);
+    act_held_ -= old.cap;
+  }
+  ActEntry e;
+  e.cap = cap;
+  check(cdml_malloc(&e.dev, cap), "cdml_malloc");
+  if (cdml_host_alloc_pinned(&e.pin, cap) != CDML_OK) {
+    cdml_free(e.dev);
+    throw InvalidOperationException(std::string("cdml_host_alloc_pinned: ") + cdml_last_error());
+  }
+  act_held_ += cap;
+  return e;
+}
+
+void HipAccelerationManager::act_release(const ActEntry &e) {
+  ActEntry idle;
+  idle.dev = e.dev;
+  idle.pin = e.pin;
+  idle.cap = e.cap;
+  act_free_.emplace(e.cap, idle);
+}
+
+void HipAccelerationManager::act_drop(const float *key) {
+  auto it = acts_.find(key);
+  if (it == acts_.end()) return;
+  if (it->second.busy == call_) sync();  // work of this call may still use its buffer
+  act_release(it->second);
+  acts_.erase(it);
+}
+
+// The device copy of activation `m` (uploaded only when it is new or its
+// host contents changed since the last transfer).  With the cache off, `m`
+// is uploaded into scratch slot `slot`.
+const float *HipAccelerationManager::act_in(MatView m, int slot) {
+  const size_t bytes = (size_t)m.rows * m.cols * sizeof(float);
+  if (act_limit_ == 0 || bytes == 0) {
+    void *d = scratch(slot, bytes);
+    upload(d, m.data, bytes);
+    return static_cast<const float *>(d);
+  }
+  auto it = acts_.find(m.data);
+  if (it != acts_.end() && it->second.rows == m.rows && it->second.cols == m.cols) {
+    ActEntry &e = it->second;
+    e.last = ++tick_;
+    if (e.busy != call_ && defer_) {
+      pending_.push_back(Pending{m.data, e.pin, e.dev, bytes, false});
+    } else if (e.busy != call_ && ParallelEqual(m.data, e.pin, bytes)) {
+      stats_.h2d_skipped_bytes += bytes;
+    } else if (e.busy != call_) {
+      stage_upload(e.dev, m.data, bytes, e.pin);
+    }
+    e.busy = call_;
+    return static_cast<const float *>(e.dev);
+  }
+  act_drop(m.data);
+  ActEntry e = act_acquire(bytes);
+  e.rows = m.rows;
+  e.cols = m.cols;
+  e.last = ++tick_;
+  e.busy = call_;
+  stage_upload(e.dev, m.data, bytes, e.pin);
+  acts_[m.data] = e;
+  return static_cast<const float *>(e.dev);
+}
+
+// The device copy of an array that the method changes in place (RoPE,
+// gradient accumulators): as act_in, and the caller writes the result back
+// with act_done, which refreshes the shadow.  A failure in between must drop
+// the entry (act_drop), since the device copy may then differ from both.
+float *HipAccelerationManager::act_inplace(MatRef m, int slot) {
+  return const_cast<float *>(act_in(MatView(m.data, m.rows, m.cols), slot));
+}
+
+// A device buffer for a result whose host storage `host` [rows, cols] this
+// call allocated (or the caller keeps); its entry is keyed by that storage.
+float *HipAccelerationManager::act_out(float *host, int rows, int cols, int slot) {
+  const size_t bytes = (size_t)rows * cols * sizeof(float);
+  if (act_limit_ == 0 || bytes == 0) return static_cast<float *>(scratch(slot, bytes));
+  act_drop(host);  // an entry left by a freed array at the same address
+  ActEntry e = act_acquire(bytes);
+  e.rows = rows;
+  e.cols = cols;
+  e.last = ++tick_;
+  e.busy = call_;
+  acts_[host] = e;
+  return static_cast<float *>(e.dev);
+}
+
+// Downloads each result from its device buffer, through its entry's shadow
+// when the buffer belongs to one (the shadow then matches the host again).
+void HipAccelerationManager::act_done(std::initializer_list<Out> outs) {
+  std::vector<Xfer> xs;
+  for (const Out &o : outs) {
+    const size_t bytes = o.floats * sizeof(float);
+    if (bytes == 0) continue;
+    auto it = acts_.find(o.host);
+    void *pin = (it != acts_.end() && it->second.dev == o.dev) ? it->second.pin : stage_region(bytes);
+    xs.push_back(Xfer{o.host, const_cast<float *>(o.dev), bytes, pin});
+  }
+  download_all(xs);
+}
+
+void HipAccelerationManager::SetActivationCacheLimit(size_t bytes) {
+  std::lock_guard<std::mutex> lock(mu_);
+  act_limit_ = bytes;
+  if (!ready_) return;
+  sync();
+  for (auto &kv : acts_) act_release(kv.second);
+  acts_.clear();
+  for (auto &kv : act_free_) {
+    cdml_free(kv.second.dev);
+    cdml_host_free_pinned(kv.second.pin);
+  }
+  act_free_.clear();
+  act_held_ = 0;
+}
+
+int HipAccelerationManager::activation_cache_entries() {
+  std::lock_guard<std::mutex> lock(mu_);
+  return (int)acts_.size();
+}
+
+HipAccelerationManager::TransferStats HipAccelerationManager::transfer_stats() {
+  std::lock_guard<std::mutex> lock(mu_);
+  return stats_;
+}
 
 // Identity-keyed resident copy with a shadow compare
 // (AccelerationManagers/GPU/DeviceResidentCache.cs:44-120): the first call
@@ -143,9 +437,10 @@ const float *HipAccelerationManager::resident(const float *host, int rows, int c
     return static_cast<const float *>(res.first->second.dev);
   }
   Resident &r = it->second;
-  if (n && std::memcmp(r.shadow.data(), host, n * sizeof(float)) != 0) {
-    sync();  // an earlier enqueued copy may still read the shadow
-    std::memcpy(r.shadow.data(), host, n * sizeof(float));
+  if (defer_ && n) {
+    pending_.push_back(Pending{host, r.shadow.data(), r.dev, n * sizeof(float), true});
+  } else if (n && !ParallelEqual(r.shadow.data(), host, n * sizeof(float))) {
+    ParallelMemcpy(r.shadow.data(), host, n * sizeof(float));
     upload(r.dev, r.shadow.data(), n * sizeof(float));
   }
   return static_cast<const float *>(r.dev);
@@ -173,25 +468,25 @@ std::tuple<Matrix, Matrix, Matrix> HipAccelerationManager::ProjectQKV(MatView in
   if (biasV.length != vDim) throw ArgumentException("biasV length does not match WV output dimension.", "biasV");
   if (qDim != kDim || qDim != vDim) throw ArgumentException("Q, K and V output dimensions must match.");
 
-  Matrix Q(rows, qDim), K(rows, kDim), V(rows, vDim);
-  if (rows == 0 || qDim == 0) return {Q, K, V};
+  if (rows == 0 || qDim == 0) return {Matrix(rows, qDim), Matrix(rows, kDim), Matrix(rows, vDim)};
   std::lock_guard<std::mutex> lock(mu_);
   ensure_ready();
+  defer_ = true;
   const float *wq = resident(WQ.data, qDim, inputDim), *wk = resident(WK.data, kDim, inputDim),
               *wv = resident(WV.data, vDim, inputDim);
   const float *bq = resident(biasQ.data, 1, qDim), *bk = resident(biasK.data, 1, kDim),
               *bv = resident(biasV.data, 1, vDim);
-  const size_t out_bytes = (size_t)rows * qDim * sizeof(float);
-  float *dx = static_cast<float *>(scratch(S_X, (size_t)rows * inputDim * sizeof(float)));
-  float *dq = static_cast<float *>(scratch(S_Q, out_bytes));
-  float *dk = static_cast<float *>(scratch(S_K, out_bytes));
-  float *dv = static_cast<float *>(scratch(S_V, out_bytes));
-  upload(dx, input.data, (size_t)rows * inputDim * sizeof(float));
-  check(cdml_project_qkv(dx, wq, bq, wk, bk, wv, bv, dq, dk, dv, rows, inputDim, qDim, stream_),
-        "cdml_project_qkv");
-  download(Q.ptr(), dq, out_bytes);
-  download(K.ptr(), dk, out_bytes);
-  download(V.ptr(), dv, out_bytes);
+  const float *dx = act_in(input, S_X);
+  defer_ = false;
+  Matrix Q = Matrix::Uninit(rows, qDim), K = Matrix::Uninit(rows, kDim), V = Matrix::Uninit(rows, vDim);
+  float *dq = act_out(Q, S_Q), *dk = act_out(K, S_K), *dv = act_out(V, S_V);
+  auto launch = [&] {
+    check(cdml_project_qkv(dx, wq, bq, wk, bk, wv, bv, dq, dk, dv, rows, inputDim, qDim, stream_),
+          "cdml_project_qkv");
+  };
+  launch();
+  if (!settle()) launch();
+  act_done({out_of(Q, dq), out_of(K, dk), out_of(V, dv)});
   sync();
   return {std::move(Q), std::move(K), std::move(V)};
 }
@@ -200,28 +495,28 @@ std::tuple<Matrix, Matrix, Matrix> HipAccelerationManager::ProjectQKV(MatView in
 Matrix HipAccelerationManager::attention(MatView q, MatView k, MatView v, int numHeads,
                                          float scale, MaskView mask, bool causal) {
   const int lq = q.rows, lk = k.rows, dim = q.cols;
-  Matrix out(lq, dim);
-  if (lq == 0 || lk == 0 || dim == 0) return out;
+  if (lq == 0 || lk == 0 || dim == 0) return Matrix(lq, dim);
   std::lock_guard<std::mutex> lock(mu_);
   ensure_ready();
-  const size_t qb = (size_t)lq * dim * sizeof(float), kb = (size_t)lk * dim * sizeof(float);
-  float *dq = static_cast<float *>(scratch(S_Q, qb));
-  float *dk = static_cast<float *>(scratch(S_K, kb));
-  float *dv = static_cast<float *>(scratch(S_V, kb));
-  float *dout = static_cast<float *>(scratch(S_O, qb));
-  upload(dq, q.data, qb);
-  upload(dk, k.data, kb);
-  upload(dv, v.data, kb);
+  defer_ = true;
+  const float *dq = act_in(q, S_Q), *dk = act_in(k, S_K), *dv = act_in(v, S_V);
+  defer_ = false;
+  Matrix out = Matrix::Uninit(lq, dim);
+  float *dout = act_out(out, S_O);
   const uint8_t *dm = nullptr;
   if (!mask.null()) {
     void *m = scratch(S_MASK, (size_t)lq * lk);
     upload(m, mask.data, (size_t)lq * lk);
     dm = static_cast<const uint8_t *>(m);
   }
-  check(cdml_sdpa_fwd(dq, dim, dk, dim, dv, dim, dout, dim, 1, lq, lk, dim, numHeads, scale,
-                      causal ? 1 : 0, dm, stream_),
-        "cdml_sdpa_fwd");
-  download(out.ptr(), dout, qb);
+  auto launch = [&] {
+    check(cdml_sdpa_fwd(dq, dim, dk, dim, dv, dim, dout, dim, 1, lq, lk, dim, numHeads, scale,
+                        causal ? 1 : 0, dm, stream_),
+          "cdml_sdpa_fwd");
+  };
+  launch();
+  if (!settle()) launch();
+  act_done({out_of(out, dout)});
   sync();
   return out;
 }
@@ -278,18 +573,30 @@ Matrix HipAccelerationManager::MultiHeadAttentionForward(MatView Q, MatView K, M
 Matrix HipAccelerationManager::linear(MatView x, int rowStart, int rowCount, MatView w, VecView b,
                                       int act) {
   const int in = w.cols, out = w.rows;
-  Matrix y(rowCount, out);
-  if (rowCount == 0 || out == 0) return y;
+  if (rowCount == 0 || out == 0) return Matrix(rowCount, out);
   std::lock_guard<std::mutex> lock(mu_);
   ensure_ready();
+  defer_ = true;
   const float *dw = resident(w.data, out, in);
   const float *db = resident(b.data, 1, out);
-  const size_t xb = (size_t)rowCount * in * sizeof(float), yb = (size_t)rowCount * out * sizeof(float);
-  float *dx = static_cast<float *>(scratch(S_X, xb));
-  float *dy = static_cast<float *>(scratch(S_O, yb));
-  upload(dx, x.data + (size_t)rowStart * x.cols, xb);
-  check(cdml_linear(dx, in, dw, db, dy, out, rowCount, in, out, act, stream_), "cdml_linear");
-  download(y.ptr(), dy, yb);
+  const float *dx;
+  if (rowStart == 0 && rowCount == x.rows) {
+    dx = act_in(x, S_X);
+  } else {  // a row range of a larger array: staged on its own
+    const size_t xb = (size_t)rowCount * in * sizeof(float);
+    float *d = static_cast<float *>(scratch(S_X, xb));
+    upload(d, x.data + (size_t)rowStart * x.cols, xb);
+    dx = d;
+  }
+  defer_ = false;
+  Matrix y = Matrix::Uninit(rowCount, out);
+  float *dy = act_out(y, S_O);
+  auto launch = [&] {
+    check(cdml_linear(dx, in, dw, db, dy, out, rowCount, in, out, act, stream_), "cdml_linear");
+  };
+  launch();
+  if (!settle()) launch();
+  act_done({out_of(y, dy)});
   sync();
   return y;
 }
@@ -355,14 +662,17 @@ void HipAccelerationManager::ApplyRotaryPositionEmbeddingInPlace(MatRef matrix, 
   if (matrix.rows == 0 || headDim == 0) return;
   std::lock_guard<std::mutex> lock(mu_);
   ensure_ready();
-  const size_t bytes = (size_t)matrix.rows * dim * sizeof(float);
-  float *dx = static_cast<float *>(scratch(S_X, bytes));
-  upload(dx, matrix.data, bytes);
-  check(cdml_rope(dx, matrix.rows, dim, 0, headDim, numHeads, baseTheta, inverse ? 1 : 0, 0, 0,
-                  nullptr, stream_),
-        "cdml_rope");
-  download(matrix.data, dx, bytes);
-  sync();
+  float *dx = act_inplace(matrix, S_X);
+  try {
+    check(cdml_rope(dx, matrix.rows, dim, 0, headDim, numHeads, baseTheta, inverse ? 1 : 0, 0, 0,
+                    nullptr, stream_),
+          "cdml_rope");
+    act_done({Out{matrix.data, (size_t)matrix.rows * dim, dx}});
+    sync();
+  } catch (...) {
+    act_drop(matrix.data);
+    throw;
+  }
 }
 
 void HipAccelerationManager::ApplyRotaryPositionEmbeddingHeadInPlace(MatRef matrix, int startCol,
@@ -378,14 +688,17 @@ void HipAccelerationManager::ApplyRotaryPositionEmbeddingHeadInPlace(MatRef matr
   if (matrix.rows == 0 || headDim == 0) return;
   std::lock_guard<std::mutex> lock(mu_);
   ensure_ready();
-  const size_t bytes = (size_t)matrix.rows * matrix.cols * sizeof(float);
-  float *dx = static_cast<float *>(scratch(S_X, bytes));
-  upload(dx, matrix.data, bytes);
-  check(cdml_rope(dx, matrix.rows, matrix.cols, startCol, headDim, 1, baseTheta, inverse ? 1 : 0,
-                  0, 0, nullptr, stream_),
-        "cdml_rope");
-  download(matrix.data, dx, bytes);
-  sync();
+  float *dx = act_inplace(matrix, S_X);
+  try {
+    check(cdml_rope(dx, matrix.rows, matrix.cols, startCol, headDim, 1, baseTheta, inverse ? 1 : 0,
+                    0, 0, nullptr, stream_),
+          "cdml_rope");
+    act_done({Out{matrix.data, (size_t)matrix.rows * matrix.cols, dx}});
+    sync();
+  } catch (...) {
+    act_drop(matrix.data);
+    throw;
+  }
 }
 
 // ---- ResidualLayerNorm: AccelerationCPU.cs:1376-1438 ----------------------
@@ -400,20 +713,22 @@ Matrix HipAccelerationManager::ResidualLayerNorm(MatView input, MatView subLayer
     throw ArgumentException("Residual input dimensions must match.", "subLayer");
   if (gamma.length != f || beta.length != f)
     throw ArgumentException("Layer norm gamma/beta must match the feature dimension.");
-  Matrix out(rows, f);
-  if (rows == 0 || f == 0) return out;
+  if (rows == 0 || f == 0) return Matrix(rows, f);
   std::lock_guard<std::mutex> lock(mu_);
   ensure_ready();
-  const size_t bytes = (size_t)rows * f * sizeof(float);
+  defer_ = true;
   const float *dg = resident(gamma.data, 1, f), *db = resident(beta.data, 1, f);
-  float *da = static_cast<float *>(scratch(S_X, bytes));
-  float *dbb = static_cast<float *>(scratch(S_Q, bytes));
-  float *dy = static_cast<float *>(scratch(S_O, bytes));
-  upload(da, input.data, bytes);
-  upload(dbb, subLayer.data, bytes);
-  check(cdml_residual_layernorm(da, dbb, dg, db, dy, rows, f, epsilon, stream_),
-        "cdml_residual_layernorm");
-  download(out.ptr(), dy, bytes);
+  const float *da = act_in(input, S_X), *dbb = act_in(subLayer, S_Q);
+  defer_ = false;
+  Matrix out = Matrix::Uninit(rows, f);
+  float *dy = act_out(out, S_O);
+  auto launch = [&] {
+    check(cdml_residual_layernorm(da, dbb, dg, db, dy, rows, f, epsilon, stream_),
+          "cdml_residual_layernorm");
+  };
+  launch();
+  if (!settle()) launch();
+  act_done({out_of(out, dy)});
   sync();
   return out;
 }
@@ -438,17 +753,17 @@ Matrix HipAccelerationManager::EmbedTokenIds(const std::vector<int> &tokenIds, i
     if ((unsigned)t >= (unsigned)vocab)
       throw ArgumentOutOfRangeException("tokenIds", "Token out of range: " + std::to_string(t));
   }
-  Matrix out(tokenCount, embeddingDim);
-  if (embeddingDim == 0) return out;
+  if (embeddingDim == 0) return Matrix(tokenCount, embeddingDim);
   std::lock_guard<std::mutex> lock(mu_);
   ensure_ready();
   const float *dt = resident(embedding.data, vocab, embeddingDim);
   int *dids = static_cast<int *>(scratch(S_IDS, (size_t)tokenCount * sizeof(int)));
-  float *dout = static_cast<float *>(scratch(S_O, (size_t)tokenCount * embeddingDim * sizeof(float)));
   upload(dids, tokenIds.data() + tokenStart, (size_t)tokenCount * sizeof(int));
+  Matrix out = Matrix::Uninit(tokenCount, embeddingDim);
+  float *dout = act_out(out, S_O);
   check(cdml_embed_tokens(dids, tokenCount, dt, vocab, embeddingDim, dout, nullptr, stream_),
         "cdml_embed_tokens");
-  download(out.ptr(), dout, (size_t)tokenCount * embeddingDim * sizeof(float));
+  act_done({out_of(out, dout)});
   sync();
   return out;
 }
@@ -477,27 +792,57 @@ Matrix HipAccelerationManager::FFNForwardBatch(MatView input, int seqLen, int ou
                                 std::to_string(ffn.input_size()) + ").",
                             "input");
   (void)outputDim;  // the reference's batched route returns the network's own output width
+  {
+    int w_in = input.cols;
+    for (size_t l = 0; l < ffn.weights.size(); ++l) {
+      const Matrix &w = ffn.weights[l];
+      if (w.cols != w_in) throw ArgumentException("FFN layer widths do not chain.", "ffn");
+      if ((int)ffn.biases[l].size() != w.rows) throw ArgumentException("FFN bias length mismatch.", "ffn");
+      w_in = w.rows;
+    }
+  }
   std::lock_guard<std::mutex> lock(mu_);
   ensure_ready();
   int width = input.cols;
   size_t maxw = width;
   for (auto &w : ffn.weights) maxw = std::max(maxw, (size_t)w.rows);
-  float *a = static_cast<float *>(scratch(S_X, (size_t)seqLen * maxw * sizeof(float)));
-  float *b = static_cast<float *>(scratch(S_O, (size_t)seqLen * maxw * sizeof(float)));
-  upload(a, input.data, (size_t)seqLen * width * sizeof(float));
+  defer_ = true;
+  const float *in0;
+  if (seqLen == input.rows) {
+    in0 = act_in(input, S_X);
+  } else {
+    float *d = static_cast<float *>(scratch(S_X, (size_t)seqLen * width * sizeof(float)));
+    upload(d, input.data, (size_t)seqLen * width * sizeof(float));
+    in0 = d;
+  }
+  std::vector<const float *> dws(ffn.weights.size()), dbs(ffn.weights.size());
   for (size_t l = 0; l < ffn.weights.size(); ++l) {
     const Matrix &w = ffn.weights[l];
-    if (w.cols != width) throw ArgumentException("FFN layer widths do not chain.", "ffn");
-    if ((int)ffn.biases[l].size() != w.rows) throw ArgumentException("FFN bias length mismatch.", "ffn");
-    const float *dw = resident(w.ptr(), w.rows, w.cols);
-    const float *db = resident(ffn.biases[l].data(), 1, w.rows);
-    check(cdml_linear(a, width, dw, db, b, w.rows, seqLen, width, w.rows, ffn.activations[l], stream_),
-          "cdml_linear");
-    std::swap(a, b);
-    width = w.rows;
+    dws[l] = resident(w.ptr(), w.rows, w.cols);
+    dbs[l] = resident(ffn.biases[l].data(), 1, w.rows);
   }
-  Matrix out(seqLen, width);
-  download(out.ptr(), a, (size_t)seqLen * width * sizeof(float));
+  defer_ = false;
+  // hidden layers alternate between two scratch buffers; the last layer
+  // writes the result's own buffer
+  float *tmp[2] = {static_cast<float *>(scratch(S_Q, (size_t)seqLen * maxw * sizeof(float))),
+                   static_cast<float *>(scratch(S_K, (size_t)seqLen * maxw * sizeof(float)))};
+  Matrix out = Matrix::Uninit(seqLen, ffn.output_size());
+  float *dout = act_out(out, S_O);
+  auto launch = [&] {
+    const float *cur = in0;
+    int wdt = input.cols;
+    for (size_t l = 0; l < ffn.weights.size(); ++l) {
+      const Matrix &w = ffn.weights[l];
+      float *dst = l + 1 == ffn.weights.size() ? dout : tmp[l & 1];
+      check(cdml_linear(cur, wdt, dws[l], dbs[l], dst, w.rows, seqLen, wdt, w.rows, ffn.activations[l], stream_),
+            "cdml_linear");
+      cur = dst;
+      wdt = w.rows;
+    }
+  };
+  launch();
+  if (!settle()) launch();
+  act_done({out_of(out, dout)});
   sync();
   return out;
 }
@@ -538,18 +883,9 @@ std::tuple<Matrix, Matrix, Matrix> HipAccelerationManager::attention_backward(
                                 "], got [" + std::to_string(mask.rows) + "," +
                                 std::to_string(mask.cols) + "].",
                             "mask");
-  Matrix dQ(lq, dim), dK(lk, dim), dV(lk, dim);
-  if (lq == 0 || lk == 0 || dim == 0) return {std::move(dQ), std::move(dK), std::move(dV)};
+  if (lq == 0 || lk == 0 || dim == 0) return {Matrix(lq, dim), Matrix(lk, dim), Matrix(lk, dim)};
   std::lock_guard<std::mutex> lock(mu_);
   ensure_ready();
-  const size_t qb = (size_t)lq * dim * sizeof(float), kb = (size_t)lk * dim * sizeof(float);
-  float *dq_in = static_cast<float *>(scratch(S_Q, qb));
-  float *dk_in = static_cast<float *>(scratch(S_K, kb));
-  float *dv_in = static_cast<float *>(scratch(S_V, kb));
-  float *ddo = static_cast<float *>(scratch(S_O, qb));
-  float *gq = static_cast<float *>(scratch(S_DQ, qb));
-  float *gk = static_cast<float *>(scratch(S_DK, kb));
-  float *gv = static_cast<float *>(scratch(S_DV, kb));
   size_t base_ws = 0, stored_ws = 0;
   check(cdml_sdpa_bwd_workspace_size(1, lq, lk, dim, numHeads, &base_ws), "cdml_sdpa_bwd_workspace_size");
   // with room for the dS blocks when the shape can use them (dQ as one
@@ -563,22 +899,26 @@ std::tuple<Matrix, Matrix, Matrix> HipAccelerationManager::attention_backward(
     ws = base_ws;
     dws = scratch(S_WS, ws);
   }
-  upload(dq_in, Q.data, qb);
-  upload(dk_in, K.data, kb);
-  upload(dv_in, V.data, kb);
-  upload(ddo, dO.data, qb);
+  defer_ = true;
+  const float *dq_in = act_in(Q, S_Q), *dk_in = act_in(K, S_K), *dv_in = act_in(V, S_V);
+  const float *ddo = act_in(dO, S_O);
+  defer_ = false;
+  Matrix dQ = Matrix::Uninit(lq, dim), dK = Matrix::Uninit(lk, dim), dV = Matrix::Uninit(lk, dim);
+  float *gq = act_out(dQ, S_DQ), *gk = act_out(dK, S_DK), *gv = act_out(dV, S_DV);
   const uint8_t *dm = nullptr;
   if (!mask.null()) {
     void *m = scratch(S_MASK, (size_t)lq * lk);
     upload(m, mask.data, (size_t)lq * lk);
     dm = static_cast<const uint8_t *>(m);
   }
-  check(cdml_sdpa_bwd(dq_in, dim, dk_in, dim, dv_in, dim, ddo, dim, gq, dim, gk, dim, gv, dim, 1,
-                      lq, lk, dim, numHeads, scale, causal ? 1 : 0, dm, dws, ws, stream_),
-        "cdml_sdpa_bwd");
-  download(dQ.ptr(), gq, qb);
-  download(dK.ptr(), gk, kb);
-  download(dV.ptr(), gv, kb);
+  auto launch = [&] {
+    check(cdml_sdpa_bwd(dq_in, dim, dk_in, dim, dv_in, dim, ddo, dim, gq, dim, gk, dim, gv, dim, 1,
+                        lq, lk, dim, numHeads, scale, causal ? 1 : 0, dm, dws, ws, stream_),
+          "cdml_sdpa_bwd");
+  };
+  launch();
+  if (!settle()) launch();
+  act_done({out_of(dQ, gq), out_of(dK, gk), out_of(dV, gv)});
   sync();
   return {std::move(dQ), std::move(dK), std::move(dV)};
 }
@@ -619,30 +959,22 @@ Matrix HipAccelerationManager::BackpropQKV(MatView input, MatView dQ, MatView dK
     throw ArgumentException("WVGrad shape mismatch.", "WVGrad");
   if (biasQGrad.length != outputDim || biasKGrad.length != outputDim || biasVGrad.length != outputDim)
     throw ArgumentException("Q/K/V bias gradient lengths must match output dimension.");
-  Matrix dInput(rows, inputDim);
-  if (rows == 0 || inputDim == 0 || outputDim == 0) return dInput;
+  if (rows == 0 || inputDim == 0 || outputDim == 0) return Matrix(rows, inputDim);
   std::lock_guard<std::mutex> lock(mu_);
   ensure_ready();
-  const size_t xb = (size_t)rows * inputDim * sizeof(float);
-  const size_t db = (size_t)rows * outputDim * sizeof(float);
   const size_t wb = (size_t)outputDim * inputDim * sizeof(float), bb = (size_t)outputDim * sizeof(float);
   const float *wq = resident(WQ.data, outputDim, inputDim), *wk = resident(WK.data, outputDim, inputDim),
               *wv = resident(WV.data, outputDim, inputDim);
-  float *dx_in = static_cast<float *>(scratch(S_X, xb));
-  float *ddq = static_cast<float *>(scratch(S_DQ, db));
-  float *ddk = static_cast<float *>(scratch(S_DK, db));
-  float *ddv = static_cast<float *>(scratch(S_DV, db));
-  float *ddx = static_cast<float *>(scratch(S_O, xb));
+  const float *dx_in = act_in(input, S_X);
+  const float *ddq = act_in(dQ, S_DQ), *ddk = act_in(dK, S_DK), *ddv = act_in(dV, S_DV);
+  Matrix dInput = Matrix::Uninit(rows, inputDim);
+  float *ddx = act_out(dInput, S_O);
   float *gw[3] = {static_cast<float *>(scratch(S_GW0, wb)), static_cast<float *>(scratch(S_GW1, wb)),
                   static_cast<float *>(scratch(S_GW2, wb))};
   float *gb[3] = {static_cast<float *>(scratch(S_GB0, bb)), static_cast<float *>(scratch(S_GB1, bb)),
                   static_cast<float *>(scratch(S_GB2, bb))};
   MatRef hw[3] = {WQGrad, WKGrad, WVGrad};
   VecRef hb[3] = {biasQGrad, biasKGrad, biasVGrad};
-  upload(dx_in, input.data, xb);
-  upload(ddq, dQ.data, db);
-  upload(ddk, dK.data, db);
-  upload(ddv, dV.data, db);
   for (int i = 0; i < 3; ++i) {
     upload(gw[i], hw[i].data, wb);
     upload(gb[i], hb[i].data, bb);
@@ -654,11 +986,9 @@ Matrix HipAccelerationManager::BackpropQKV(MatView input, MatView dQ, MatView dK
   check(cdml_backprop_qkv(dx_in, ddq, ddk, ddv, wq, wk, wv, gw[0], gb[0], gw[1], gb[1], gw[2], gb[2],
                           ddx, rows, inputDim, outputDim, dws, ws, stream_),
         "cdml_backprop_qkv");
-  download(dInput.ptr(), ddx, xb);
-  for (int i = 0; i < 3; ++i) {
-    download(hw[i].data, gw[i], wb);
-    download(hb[i].data, gb[i], bb);
-  }
+  act_done({out_of(dInput, ddx), Out{hw[0].data, wb / 4, gw[0]}, Out{hb[0].data, bb / 4, gb[0]},
+            Out{hw[1].data, wb / 4, gw[1]}, Out{hb[1].data, bb / 4, gb[1]}, Out{hw[2].data, wb / 4, gw[2]},
+            Out{hb[2].data, bb / 4, gb[2]}});
   sync();
   return dInput;
 }
@@ -673,21 +1003,28 @@ void HipAccelerationManager::linear_backward(MatView x, MatView dy, int rows, Ma
   if (rows == 0 || in == 0) return;
   std::lock_guard<std::mutex> lock(mu_);
   ensure_ready();
-  const size_t xb = (size_t)rows * in * sizeof(float), yb = (size_t)rows * out * sizeof(float);
+  const size_t xb = (size_t)rows * in * sizeof(float);
   const size_t wb = (size_t)out * in * sizeof(float), bb = (size_t)out * sizeof(float);
   const float *dw = resident(w.data, out, in);
-  float *dxin = static_cast<float *>(scratch(S_X, xb));
-  float *ddy = static_cast<float *>(scratch(S_Q, yb > 0 ? yb : 4));
-  float *ddx = static_cast<float *>(scratch(S_O, xb));
+  // x and dy are whole arrays when `rows` covers them, else row prefixes
+  auto rows_of = [&](MatView m, int slot) -> const float * {
+    if (m.rows == rows) return act_in(m, slot);
+    const size_t b = (size_t)rows * m.cols * sizeof(float);
+    float *d = static_cast<float *>(scratch(slot, b));
+    upload(d, m.data, b);
+    return d;
+  };
+  const float *dxin = rows_of(x, S_X);
+  const float *ddy = out > 0 ? rows_of(dy, S_Q) : nullptr;
   float *gw = static_cast<float *>(scratch(S_GW0, wb > 0 ? wb : 4));
   float *gb = static_cast<float *>(scratch(S_GB0, bb > 0 ? bb : 4));
-  upload(dxin, x.data, xb);
   if (out > 0) {
-    upload(ddy, dy.data, yb);
     upload(gw, wgrad.data, wb);
     upload(gb, bgrad.data, bb);
   }
-  if (accumulate_dx) upload(ddx, dx_host, xb);
+  // dX: accumulated in place into the caller's array, or a new result
+  float *ddx = accumulate_dx ? act_inplace(MatRef(dx_host, rows, in), S_O) : act_out(dx_host, rows, in, S_O);
+  try {
   if (out > 0) {
     size_t ws = 0;
     check(cdml_linear_backward_workspace_size(rows, in, out, &ws),
@@ -699,12 +1036,15 @@ void HipAccelerationManager::linear_backward(MatView x, MatView dy, int rows, Ma
   } else if (!accumulate_dx) {
     check(cdml_zero_f32_async(ddx, (size_t)rows * in, stream_), "cdml_zero_f32_async");
   }
-  download(dx_host, ddx, xb);
-  if (out > 0) {
-    download(wgrad.data, gw, wb);
-    download(bgrad.data, gb, bb);
-  }
+  if (out > 0)
+    act_done({Out{dx_host, xb / 4, ddx}, Out{wgrad.data, wb / 4, gw}, Out{bgrad.data, bb / 4, gb}});
+  else
+    act_done({Out{dx_host, xb / 4, ddx}});
   sync();
+  } catch (...) {
+    act_drop(dx_host);
+    throw;
+  }
 }
 
 // ---- BackpropLinearProjection: AccelerationCPU.cs:2188-2227 -----------------
@@ -766,43 +1106,33 @@ Matrix HipAccelerationManager::MatrixMultiply(MatView A, MatView B) {
     throw ArgumentException("Matrix dimensions don't match: [" + std::to_string(A.rows) + "x" +
                             std::to_string(A.cols) + "] * [" + std::to_string(B.rows) + "x" +
                             std::to_string(B.cols) + "]");
-  Matrix C(A.rows, B.cols);
-  if (A.rows == 0 || B.cols == 0 || A.cols == 0) return C;
+  if (A.rows == 0 || B.cols == 0 || A.cols == 0) return Matrix(A.rows, B.cols);
   std::lock_guard<std::mutex> lock(mu_);
   ensure_ready();
-  const size_t ab = (size_t)A.rows * A.cols * 4, bb = (size_t)B.rows * B.cols * 4,
-               cb = (size_t)A.rows * B.cols * 4;
-  float *da = static_cast<float *>(scratch(S_X, ab));
-  float *db = static_cast<float *>(scratch(S_Q, bb));
-  float *dc = static_cast<float *>(scratch(S_O, cb));
-  upload(da, A.data, ab);
-  upload(db, B.data, bb);
+  const float *da = act_in(A, S_X), *db = act_in(B, S_Q);
+  Matrix Cm = Matrix::Uninit(A.rows, B.cols);
+  float *dc = act_out(Cm, S_O);
   check(cdml_matmul(da, A.cols, db, B.cols, dc, B.cols, A.rows, A.cols, B.cols, stream_), "cdml_matmul");
-  download(C.ptr(), dc, cb);
+  act_done({out_of(Cm, dc)});
   sync();
-  return C;
+  return Cm;
 }
 
 Matrix HipAccelerationManager::MatrixMultiplyTranspose(MatView A, MatView B) {
   if (A.null()) throw ArgumentNullException("A");
   if (B.null()) throw ArgumentNullException("B");
   if (A.cols != B.cols) throw ArgumentException("Matrix dimensions don't match for A*B^T");
-  Matrix C(A.rows, B.rows);
-  if (A.rows == 0 || B.rows == 0 || A.cols == 0) return C;
+  if (A.rows == 0 || B.rows == 0 || A.cols == 0) return Matrix(A.rows, B.rows);
   std::lock_guard<std::mutex> lock(mu_);
   ensure_ready();
-  const size_t ab = (size_t)A.rows * A.cols * 4, bb = (size_t)B.rows * B.cols * 4,
-               cb = (size_t)A.rows * B.rows * 4;
-  float *da = static_cast<float *>(scratch(S_X, ab));
-  float *db = static_cast<float *>(scratch(S_Q, bb));
-  float *dc = static_cast<float *>(scratch(S_O, cb));
-  upload(da, A.data, ab);
-  upload(db, B.data, bb);
+  const float *da = act_in(A, S_X), *db = act_in(B, S_Q);
+  Matrix Cm = Matrix::Uninit(A.rows, B.rows);
+  float *dc = act_out(Cm, S_O);
   check(cdml_linear(da, A.cols, db, nullptr, dc, B.rows, A.rows, A.cols, B.rows, CDML_ACT_NONE, stream_),
         "cdml_linear");
-  download(C.ptr(), dc, cb);
+  act_done({out_of(Cm, dc)});
   sync();
-  return C;
+  return Cm;
 }
 
 // ---- ResidualLayerNormForward: AccelerationCPU.cs:1440-1514 -------------------
@@ -819,28 +1149,20 @@ HipAccelerationManager::ResidualLayerNormForward(MatView input, MatView subLayer
   if (gamma.length != f || beta.length != f)
     throw ArgumentException("Layer norm gamma/beta must match the feature dimension.");
   if (f > 2048) throw ArgumentException("ResidualLayerNormForward supports up to 2048 features.", "input");
-  Matrix out(rows, f), norm(rows, f), res(rows, f);
   std::vector<float> mean(rows), var(rows);
-  if (rows == 0 || f == 0) return {std::move(out), std::move(mean), std::move(var), std::move(norm), std::move(res)};
+  if (rows == 0 || f == 0)
+    return {Matrix(rows, f), std::move(mean), std::move(var), Matrix(rows, f), Matrix(rows, f)};
   std::lock_guard<std::mutex> lock(mu_);
   ensure_ready();
-  const size_t bytes = (size_t)rows * f * 4;
   const float *dg = resident(gamma.data, 1, f), *dbt = resident(beta.data, 1, f);
-  float *da = static_cast<float *>(scratch(S_X, bytes));
-  float *dbb = static_cast<float *>(scratch(S_Q, bytes));
-  float *dy = static_cast<float *>(scratch(S_O, bytes));
-  float *dn = static_cast<float *>(scratch(S_K, bytes));
-  float *dr = static_cast<float *>(scratch(S_V, bytes));
+  const float *da = act_in(input, S_X), *dbb = act_in(subLayer, S_Q);
+  Matrix out = Matrix::Uninit(rows, f), norm = Matrix::Uninit(rows, f), res = Matrix::Uninit(rows, f);
+  float *dy = act_out(out, S_O), *dn = act_out(norm, S_K), *dr = act_out(res, S_V);
   float *dm = static_cast<float *>(scratch(S_DQ, (size_t)rows * 8));
-  upload(da, input.data, bytes);
-  upload(dbb, subLayer.data, bytes);
   check(cdml_residual_layernorm_fwd(da, dbb, dg, dbt, dy, dm, dm + rows, dr, dn, rows, f, epsilon, stream_),
         "cdml_residual_layernorm_fwd");
-  download(out.ptr(), dy, bytes);
-  download(norm.ptr(), dn, bytes);
-  download(res.ptr(), dr, bytes);
-  download(mean.data(), dm, (size_t)rows * 4);
-  download(var.data(), dm + rows, (size_t)rows * 4);
+  act_done({out_of(out, dy), out_of(norm, dn), out_of(res, dr), Out{mean.data(), (size_t)rows, dm},
+            Out{var.data(), (size_t)rows, dm + rows}});
   sync();
   return {std::move(out), std::move(mean), std::move(var), std::move(norm), std::move(res)};
 }
@@ -864,34 +1186,26 @@ HipAccelerationManager::LayerNormBackward(MatView dOut, MatView normalized, VecV
   if (mean.length < rows || variance.length < rows)
     throw ArgumentException("mean and variance need one entry per row.");
   if (f > 2048) throw ArgumentException("LayerNormBackward supports up to 2048 features.", "dOut");
-  Matrix dx(rows, f);
   std::vector<float> dg(f), db(f);
-  if (rows == 0 || f == 0) return {std::move(dx), std::move(dg), std::move(db)};
+  if (rows == 0 || f == 0) return {Matrix(rows, f), std::move(dg), std::move(db)};
   std::lock_guard<std::mutex> lock(mu_);
   ensure_ready();
-  const size_t bytes = (size_t)rows * f * 4;
-  float *dd = static_cast<float *>(scratch(S_X, bytes));
-  float *dn = static_cast<float *>(scratch(S_Q, bytes));
-  float *di = static_cast<float *>(scratch(S_K, bytes));
-  float *dxo = static_cast<float *>(scratch(S_O, bytes));
+  const float *dd = act_in(dOut, S_X), *dn = act_in(normalized, S_Q), *di = act_in(input, S_K);
+  Matrix dx = Matrix::Uninit(rows, f);
+  float *dxo = act_out(dx, S_O);
   float *dmv = static_cast<float *>(scratch(S_DQ, (size_t)rows * 8));
   float *dgb = static_cast<float *>(scratch(S_GB0, (size_t)f * 8 + 4 * (size_t)f));
   float *dgam = dgb + 2 * (size_t)f;
   size_t ws = 0;
   check(cdml_layernorm_backward_workspace_size(rows, f, &ws), "cdml_layernorm_backward_workspace_size");
   void *dws = scratch(S_WS, ws);
-  upload(dd, dOut.data, bytes);
-  upload(dn, normalized.data, bytes);
-  upload(di, input.data, bytes);
   upload(dmv, mean.data, (size_t)rows * 4);
   upload(dmv + rows, variance.data, (size_t)rows * 4);
   upload(dgam, gamma.data, (size_t)f * 4);
   check(cdml_layernorm_backward(dd, nullptr, dn, dgam, di, dmv, dmv + rows, dxo, dgb, dgb + f, rows, f, epsilon,
                                 0, dws, ws, stream_),
         "cdml_layernorm_backward");
-  download(dx.ptr(), dxo, bytes);
-  download(dg.data(), dgb, (size_t)f * 4);
-  download(db.data(), dgb + f, (size_t)f * 4);
+  act_done({out_of(dx, dxo), Out{dg.data(), (size_t)f, dgb}, Out{db.data(), (size_t)f, dgb + f}});
   sync();
   return {std::move(dx), std::move(dg), std::move(db)};
 }
@@ -903,8 +1217,7 @@ std::pair<float, Matrix> HipAccelerationManager::CrossEntropyLossAndGradient(
   if (targetStart < 0 || effectiveLen < 0 || (long long)targetStart + effectiveLen > (long long)targets.size())
     throw ArgumentOutOfRangeException("targetStart");
   const int rows = logits.rows, v = logits.cols;
-  Matrix dl(rows, v);
-  if (effectiveLen == 0) return {0.f, std::move(dl)};
+  if (effectiveLen == 0) return {0.f, Matrix(rows, v)};
   // the reference reads row i < effectiveLen and the target's column without
   // checks; both are checked here
   if (effectiveLen > rows) throw ArgumentException("effectiveLen exceeds the logits rows.", "effectiveLen");
@@ -913,20 +1226,19 @@ std::pair<float, Matrix> HipAccelerationManager::CrossEntropyLossAndGradient(
       throw ArgumentOutOfRangeException("targets", "Target out of range: " + std::to_string(targets[targetStart + i]));
   std::lock_guard<std::mutex> lock(mu_);
   ensure_ready();
-  const size_t bytes = (size_t)rows * v * 4;
-  float *dlog = static_cast<float *>(scratch(S_X, bytes));
+  const float *dlog = act_in(logits, S_X);
   int *dt = static_cast<int *>(scratch(S_IDS, (size_t)effectiveLen * 4));
   float *dloss = static_cast<float *>(scratch(S_BIAS, 4));
   size_t ws = 0;
   check(cdml_cross_entropy_workspace_size(rows, &ws), "cdml_cross_entropy_workspace_size");
   void *dws = scratch(S_WS, ws);
-  upload(dlog, logits.data, bytes);
   upload(dt, targets.data() + targetStart, (size_t)effectiveLen * 4);
-  check(cdml_cross_entropy(dlog, v, dt, rows, v, effectiveLen, 1.0f, 1.0f, dloss, dlog, v, dws, ws, stream_),
+  Matrix dl = Matrix::Uninit(rows, v);
+  float *dgrad = act_out(dl, S_O);
+  check(cdml_cross_entropy(dlog, v, dt, rows, v, effectiveLen, 1.0f, 1.0f, dloss, dgrad, v, dws, ws, stream_),
         "cdml_cross_entropy");
   float loss = 0.f;
-  download(dl.ptr(), dlog, bytes);
-  download(&loss, dloss, 4);
+  act_done({out_of(dl, dgrad), Out{&loss, 1, dloss}});
   sync();
   return {loss, std::move(dl)};
 }
@@ -940,25 +1252,23 @@ std::pair<float, Matrix> HipAccelerationManager::MSELossAndGradient(MatView pred
   if (targetStart < 0 || effectiveLen < 0 || (long long)targetStart + effectiveLen > targets.rows || targets.cols != o)
     throw ArgumentException("Target shape must match predictions for the effective length and target offset.",
                             "targets");
-  Matrix d(rows, o);
-  if (effectiveLen == 0 || o == 0) return {0.f, std::move(d)};
+  if (effectiveLen == 0 || o == 0) return {0.f, Matrix(rows, o)};
   // the reference reads prediction rows i < effectiveLen without a check
   if (effectiveLen > rows) throw ArgumentException("effectiveLen exceeds the prediction rows.", "effectiveLen");
   std::lock_guard<std::mutex> lock(mu_);
   ensure_ready();
-  const size_t pbytes = (size_t)rows * o * 4, tbytes = (size_t)effectiveLen * o * 4;
-  float *dp = static_cast<float *>(scratch(S_X, pbytes));
+  const size_t tbytes = (size_t)effectiveLen * o * 4;
+  const float *dp = act_in(predictions, S_X);
   float *dt = static_cast<float *>(scratch(S_Q, tbytes));
-  float *dd = static_cast<float *>(scratch(S_K, pbytes));
   float *dloss = static_cast<float *>(scratch(S_BIAS, 4));
   void *dws = scratch(S_WS, (size_t)rows * 4);
-  upload(dp, predictions.data, pbytes);
   upload(dt, targets.data + (size_t)targetStart * o, tbytes);
+  Matrix d = Matrix::Uninit(rows, o);
+  float *dd = act_out(d, S_K);
   check(cdml_mse_loss(dp, o, dt, o, rows, o, effectiveLen, 1.0f, 1.0f, dloss, dd, o, dws, (size_t)rows * 4, stream_),
         "cdml_mse_loss");
   float loss = 0.f;
-  download(d.ptr(), dd, pbytes);
-  download(&loss, dloss, 4);
+  act_done({out_of(d, dd), Out{&loss, 1, dloss}});
   sync();
   return {loss, std::move(d)};
 }
@@ -992,20 +1302,30 @@ void HipAccelerationManager::AccumulateTokenEmbeddingGrad(MatRef embeddingGrad, 
   start.push_back(seqLen);
   std::lock_guard<std::mutex> lock(mu_);
   ensure_ready();
-  const size_t gb = (size_t)vocab * embeddingDim * 4, xb = (size_t)seqLen * embeddingDim * 4;
-  float *dg = static_cast<float *>(scratch(S_O, gb));
-  float *dx = static_cast<float *>(scratch(S_X, xb));
+  float *dg = act_inplace(embeddingGrad, S_O);
+  const float *dx;
+  if (dX.rows == seqLen) {
+    dx = act_in(dX, S_X);
+  } else {
+    const size_t xb = (size_t)seqLen * embeddingDim * 4;
+    float *d = static_cast<float *>(scratch(S_X, xb));
+    upload(d, dX.data, xb);
+    dx = d;
+  }
   int *di = static_cast<int *>(scratch(S_IDS, ((size_t)seqLen * 3 + 1) * 4));
-  upload(dg, embeddingGrad.data, gb);
-  upload(dx, dX.data, xb);
   upload(di, order.data(), (size_t)seqLen * 4);
   upload(di + seqLen, start.data(), start.size() * 4);
   upload(di + 2 * seqLen + 1, token.data(), token.size() * 4);
-  check(cdml_embedding_grad(dg, dx, nullptr, embeddingDim, di, di + seqLen, di + 2 * seqLen + 1,
-                            (int)token.size(), embeddingDim, stream_),
-        "cdml_embedding_grad");
-  download(embeddingGrad.data, dg, gb);
-  sync();
+  try {
+    check(cdml_embedding_grad(dg, dx, nullptr, embeddingDim, di, di + seqLen, di + 2 * seqLen + 1,
+                              (int)token.size(), embeddingDim, stream_),
+          "cdml_embedding_grad");
+    act_done({Out{embeddingGrad.data, (size_t)vocab * embeddingDim, dg}});
+    sync();
+  } catch (...) {
+    act_drop(embeddingGrad.data);
+    throw;
+  }
 }
 
 // ---- decode capability ------------------------------------------------------

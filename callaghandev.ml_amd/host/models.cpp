@@ -219,7 +219,7 @@ std::vector<float> LanguageModel::ProjectLastTokenOnly(const Matrix &hidden) {
   if (hidden.rows <= 0) throw ArgumentException("Hidden states must contain at least one row.", "hidden");
   MatView last(hidden.ptr() + (size_t)(hidden.rows - 1) * hidden.cols, 1, hidden.cols);
   Matrix logits = accel_->ProjectOutputBatch(last, OutputProjection, OutputBias, 1, cfg_.EffectiveOutputDim());
-  return logits.data;
+  return std::vector<float>(logits.data.begin(), logits.data.end());
 }
 
 // :602-612 (PredictNext)

@@ -80,6 +80,10 @@ int cdml_stream_synchronize(cdml_stream stream);
 int cdml_event_create(cdml_event *event);
 int cdml_event_destroy(cdml_event event);
 int cdml_event_record(cdml_event event, cdml_stream stream);
+/* Blocks until the work recorded before `event` has finished (a host that
+ * stages a download in chunks copies chunk i out of pinned memory while the
+ * later chunks are still in flight). */
+int cdml_event_synchronize(cdml_event event);
 /* Waits for `stop`, then returns the time between the two events. */
 int cdml_event_elapsed_ms(cdml_event start, cdml_event stop, float *ms);
 

@@ -243,3 +243,20 @@ def test_attention_backward_workspace_choice():
     for args in ((512, 512, 512, 8, False), (512, 512, 256, 16, True)):
         base, stored, pick = H.sdpa_backward_workspace_choice(*args)
         assert stored == base and pick == base
+
+
+def test_parallel_host_copy_and_compare():
+    """The manager's host copy engine: copies of sizes around its slice and
+    threshold sizes are exact, and a single differing byte anywhere is found."""
+    assert H.host_copy_threads() >= 1
+    rng = np.random.default_rng(3)
+    for n in (0, 1, 1000, (2 << 20) - 4, 2 << 20, (9 << 20) + 12, 40 << 20):
+        a = rng.integers(0, 255, size=n, dtype=np.uint8)
+        b = H._parallel_copy(a)
+        assert b.dtype == np.uint8 and np.array_equal(a, b)
+        assert H._parallel_equal(a, b)
+        if n:
+            for pos in (0, n // 2, n - 1):
+                c = b.copy()
+                c[pos] ^= 1
+                assert not H._parallel_equal(a, c)

@@ -1,0 +1,145 @@
+"""The drop-in manager's boundary contract on the GPU.
+
+* Threads: calls on distinct HipAccelerationManager instances from different
+  threads are safe.  RotaryPositionEmbeddingTests.cs:304-322 builds 32
+  instances inside Parallel.For, and every FFN builds a manager of its own;
+  here 32 managers on 32 threads run the MultiHeadAttention.Forward sequence
+  (MultiHeadAttention.cs:108-111) at the same time.
+* Resident activations: an array the manager returned stays on the device,
+  and the next call that receives it uploads it only when its host contents
+  changed (the shadow compare of DeviceResidentCache.cs:44-60 extended from
+  weights to activations).  Host edits between calls must be seen, and the
+  cache must give the same bits as a manager without it.
+
+Bar: |got - want| <= 1e-4 + 1e-3 |want| per element against the oracle.
+"""
+from __future__ import annotations
+
+import threading
+
+import numpy as np
+import pytest
+
+from cdml import host, synth
+from conftest import assert_parity
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _mha_inputs(seed, L, D):
+    x = synth.normal(seed, (L, D))
+    w = [synth.xavier_uniform(seed + 10 + j, D, D) for j in range(4)]
+    b = [np.float32(0.1) * synth.normal(seed + 20 + j, (D,)) for j in range(4)]
+    return x, w, b
+
+
+def _mha_manager(m, x, w, b, heads):
+    """MultiHeadAttention.Forward's calls on one manager."""
+    L, D = x.shape
+    q, k, v = m.ProjectQKV(x, w[0], b[0], w[1], b[1], w[2], b[2])
+    m.ApplyRotaryPositionEmbeddingInPlace(q, heads, 10000.0, False)
+    m.ApplyRotaryPositionEmbeddingInPlace(k, heads, 10000.0, False)
+    a = m.ScaledDotProductAttention(q, k, v, heads, None, True)
+    return m.ProjectOutputBatch(a, w[3], b[3], L, D)
+
+
+def _mha_oracle(x, w, b, heads):
+    q, k, v = O.project_qkv(x, w[0], b[0], w[1], b[1], w[2], b[2])
+    a = O.sdpa(O.rope(q, heads), O.rope(k, heads), v, heads, causal=True)
+    return O.project_output_batch(a, w[3], b[3])
+
+
+def test_32_managers_on_32_threads():
+    Hm = host.module()
+    n, L, D, heads = 32, 96, 64, 4
+    results = [None] * n
+    barrier = threading.Barrier(n, timeout=60)
+
+    def work(i):
+        try:
+            m = Hm.HipAccelerationManager(0)
+            x, w, b = _mha_inputs(1000 + 40 * i, L + i, D)
+            barrier.wait()  # every manager exists before any computes
+            ys = [_mha_manager(m, x, w, b, heads) for _ in range(3)]
+            m.Dispose()
+            results[i] = (x, w, b, ys)
+        except BaseException as e:  # reported by the main thread
+            results[i] = e
+
+    print("[boundary] 32 managers on 32 threads", flush=True)
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(n)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=100)
+    assert not any(t.is_alive() for t in threads), "a manager thread did not finish"
+    for i, r in enumerate(results):
+        assert not isinstance(r, BaseException), f"thread {i}: {r!r}"
+        x, w, b, ys = r
+        want = _mha_oracle(x, w, b, heads)
+        for rep, y in enumerate(ys):
+            assert_parity(y, want, what=f"manager {i} (L {L + i}) call {rep}")
+        # repeated calls on one manager: the same bits
+        assert all(np.array_equal(ys[0], y) for y in ys[1:])
+
+
+def test_returned_arrays_stay_resident_and_follow_host_edits():
+    Hm = host.module()
+    m = Hm.HipAccelerationManager(0)
+    L, D, heads = 300, 128, 4
+    x, w, b = _mha_inputs(77, L, D)
+    nbytes = L * D * 4
+    q, k, v = m.ProjectQKV(x, w[0], b[0], w[1], b[1], w[2], b[2])
+    s0 = m.transfer_stats()
+    m.ApplyRotaryPositionEmbeddingInPlace(q, heads, 10000.0, False)
+    m.ApplyRotaryPositionEmbeddingInPlace(k, heads, 10000.0, False)
+    s1 = m.transfer_stats()
+    # Q and K were on the device already: nothing uploaded, both compared
+    assert s1["h2d_bytes"] == s0["h2d_bytes"]
+    assert s1["h2d_skipped_bytes"] - s0["h2d_skipped_bytes"] == 2 * nbytes
+    qo, ko, vo = O.project_qkv(x, w[0], b[0], w[1], b[1], w[2], b[2])
+    assert_parity(q, O.rope(qo, heads), what="RoPE of the resident Q")
+    # host edits of returned arrays between calls
+    q[5, 3] += np.float32(1.0)
+    v[7, :] *= np.float32(-1.0)
+    a = m.ScaledDotProductAttention(q, k, v, heads, None, True)
+    s2 = m.transfer_stats()
+    assert s2["h2d_bytes"] - s1["h2d_bytes"] == 2 * nbytes  # Q and V again, K skipped
+    assert_parity(a, O.sdpa(q, k, v, heads, causal=True), what="SDPA after host edits of Q and V")
+    # a write that leaves the contents as they were costs no upload
+    q[9, :] = q[9, :].copy()
+    a2 = m.ScaledDotProductAttention(q, k, v, heads, None, True)
+    assert m.transfer_stats()["h2d_bytes"] == s2["h2d_bytes"]
+    assert np.array_equal(a, a2)
+    # an edit of the result before it goes back in
+    a[0, :] = np.float32(2.0)
+    y = m.ProjectOutputBatch(a, w[3], b[3], L, D)
+    assert_parity(y, O.project_output_batch(a, w[3], b[3]), what="out-proj after an edit of its input")
+    # the same sequence with the cache off gives the same bits
+    m0 = Hm.HipAccelerationManager(0)
+    m0.SetActivationCacheLimit(0)
+    assert m0.activation_cache_limit == 0
+    y_cached = _mha_manager(m, x, w, b, heads)
+    y_plain = _mha_manager(m0, x, w, b, heads)
+    assert m0.activation_cache_entries == 0
+    assert np.array_equal(y_cached, y_plain)
+    m0.Dispose()
+    m.Dispose()
+
+
+def test_small_activation_cache_evicts_and_stays_correct():
+    """A limit of three arrays: every call evicts the least recently used
+    entries it does not itself use, and the results still match the oracle."""
+    Hm = host.module()
+    L, D, heads = 257, 64, 2
+    m = Hm.HipAccelerationManager(0)
+    m.SetActivationCacheLimit(3 * L * D * 4)
+    x, w, b = _mha_inputs(91, L, D)
+    want = _mha_oracle(x, w, b, heads)
+    for rep in range(3):
+        assert_parity(_mha_manager(m, x, w, b, heads), want, what=f"limited cache, call {rep}")
+    m.SetActivationCacheLimit(1 << 30)
+    for rep in range(2):
+        assert_parity(_mha_manager(m, x, w, b, heads), want, what=f"cache back on, call {rep}")
+    m.Dispose()
