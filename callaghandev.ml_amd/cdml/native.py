@@ -103,6 +103,10 @@ SIGNATURES = {
     "cdml_cross_entropy": [_vp, _i, _vp, _i, _i, _i, _f, _f, _vp, _vp, _i, _vp, _sz, _vp],
     "cdml_mse_loss": [_vp, _i, _vp, _i, _i, _i, _i, _f, _f, _vp, _vp, _i, _vp, _sz, _vp],
     "cdml_add_inplace": [_vp, _vp, _sz, _vp],
+    "cdml_update_f32": [_vp, _vp, _f, _sz, _vp],
+    "cdml_scale_f32": [_vp, _f, _sz, _vp],
+    "cdml_sum_squares_workspace_size": [C.POINTER(_sz)],
+    "cdml_sum_squares": [_vp, _sz, _vp, _vp, _sz, _vp],
     "cdml_embedding_grad": [_vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _i, _vp],
     "cdml_grad_norm_workspace_size": [_i, C.POINTER(_sz)],
     "cdml_grad_norm": [_vp, _i, _f, _i, _f, _vp, _vp, _sz, _vp],

@@ -616,10 +616,94 @@ __global__ void __launch_bounds__(256) sgd_kernel(const cdml_param *__restrict__
   }
 }
 
+// MatrixUpdate / VectorUpdate (AccelerationCPU.cs:2548-2597): w -= lr * g,
+// the product and the difference rounded separately as in the reference.
+__global__ void __launch_bounds__(256) update_kernel(float *__restrict__ w, const float *__restrict__ g,
+                                                     float lr, long long n) {
+#pragma clang fp contract(off)
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256)
+    w[i] -= lr * g[i];
+}
+
+// MatrixScaleInPlace / VectorScaleInPlace (AccelerationCPU.cs:2514-2546).
+__global__ void __launch_bounds__(256) scale_kernel(float *__restrict__ x, float a, long long n) {
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256)
+    x[i] *= a;
+}
+
+// MatrixSquaredNorm / VectorSquaredNorm (AccelerationCPU.cs:2493-2512): block
+// b sums the squares of elements b * 256 + t + k * kNormBlocks * 256 into a
+// partial; one wave then adds the partials in block order.
+__global__ void __launch_bounds__(256) sq_partial_kernel(const float *__restrict__ x, long long n,
+                                                         float *__restrict__ partial) {
+  __shared__ float red[4];
+  float s = 0.f;
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)kNormBlocks * 256)
+    s += x[i] * x[i];
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) partial[blockIdx.x] = ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+__global__ void __launch_bounds__(64) sq_final_kernel(const float *__restrict__ partial,
+                                                      float *__restrict__ out) {
+  float s = 0.f;
+  for (int b = threadIdx.x; b < kNormBlocks; b += 64) s += partial[b];
+  s = wave_sum(s);
+  if (threadIdx.x == 0) out[0] = s;
+}
+
 }  // namespace
 }  // namespace cdml
 
 using namespace cdml;
+
+extern "C" int cdml_update_f32(float *weights, const float *gradients, float learning_rate, size_t count,
+                               cdml_stream stream) {
+  if (count == 0) return CDML_OK;
+  if (!weights || !gradients) return fail(CDML_E_INVALID, "cdml_update_f32: NULL pointer");
+  int rc = ensure_device();
+  if (rc) return rc;
+  const size_t blocks = std::min<size_t>((count + 255) / 256, 8192);
+  update_kernel<<<dim3((unsigned)blocks), dim3(256), 0, as_hip(stream)>>>(weights, gradients, learning_rate,
+                                                                         (long long)count);
+  return check_launch("update_kernel");
+}
+
+extern "C" int cdml_scale_f32(float *x, float scale, size_t count, cdml_stream stream) {
+  if (count == 0) return CDML_OK;
+  if (!x) return fail(CDML_E_INVALID, "cdml_scale_f32: NULL pointer");
+  int rc = ensure_device();
+  if (rc) return rc;
+  const size_t blocks = std::min<size_t>((count + 255) / 256, 8192);
+  scale_kernel<<<dim3((unsigned)blocks), dim3(256), 0, as_hip(stream)>>>(x, scale, (long long)count);
+  return check_launch("scale_kernel");
+}
+
+extern "C" int cdml_sum_squares_workspace_size(size_t *bytes) {
+  if (!bytes) return fail(CDML_E_INVALID, "cdml_sum_squares_workspace_size: bytes is NULL");
+  *bytes = (size_t)kNormBlocks * sizeof(float);
+  return CDML_OK;
+}
+
+extern "C" int cdml_sum_squares(const float *x, size_t count, float *out, void *workspace,
+                                size_t workspace_bytes, cdml_stream stream) {
+  if (!out) return fail(CDML_E_INVALID, "cdml_sum_squares: out is NULL");
+  if (count > 0 && !x) return fail(CDML_E_INVALID, "cdml_sum_squares: x is NULL");
+  if (!workspace || workspace_bytes < (size_t)kNormBlocks * sizeof(float))
+    return fail(CDML_E_INVALID, "cdml_sum_squares: workspace of %zu bytes needed",
+                (size_t)kNormBlocks * sizeof(float));
+  int rc = ensure_device();
+  if (rc) return rc;
+  hipStream_t st = as_hip(stream);
+  float *partial = static_cast<float *>(workspace);
+  sq_partial_kernel<<<dim3(kNormBlocks), dim3(256), 0, st>>>(x, (long long)count, partial);
+  rc = check_launch("sq_partial_kernel");
+  if (rc) return rc;
+  sq_final_kernel<<<dim3(1), dim3(64), 0, st>>>(partial, out);
+  return check_launch("sq_final_kernel");
+}
 
 extern "C" int cdml_residual_layernorm_fwd(const float *a, const float *b, const float *gamma,
                                            const float *beta, float *out, float *mean,

@@ -427,6 +427,103 @@ PYBIND11_MODULE(_cdml_host, m) {
              std::vector<int> I = ids_from(ids);
              nogil([&] { a.AccumulateTokenEmbeddingGrad(EG, D.view, I, tokenStart, seqLen, dim); });
            })
+      .def("ZeroMatrix",
+           [](HipAccelerationManager &a, py::object m) {
+             if (m.is_none()) throw ArgumentNullException("matrix");
+             MatRef M = mat_inout(m);
+             nogil([&] { a.ZeroMatrix(M); });
+           })
+      .def("ZeroVector",
+           [](HipAccelerationManager &a, py::object v) {
+             if (v.is_none()) throw ArgumentNullException("vector");
+             VecRef Vv = vec_inout(v);
+             nogil([&] { a.ZeroVector(Vv); });
+           })
+      .def("MatrixAddInPlace",
+           [](HipAccelerationManager &a, py::object t, py::object x) {
+             MatRef T = mat_inout(t);
+             auto X = mat(x);
+             nogil([&] { a.MatrixAddInPlace(T, X.view); });
+           })
+      .def("VectorAccumulate",
+           [](HipAccelerationManager &a, py::object t, py::object x) {
+             VecRef T = vec_inout(t);
+             auto X = vec(x);
+             nogil([&] { a.VectorAccumulate(T, X.view); });
+           })
+      .def("MatrixSquaredNorm",
+           [](HipAccelerationManager &a, py::object m) {
+             auto M = mat(m);
+             return nogil([&] { return a.MatrixSquaredNorm(M.view); });
+           })
+      .def("VectorSquaredNorm",
+           [](HipAccelerationManager &a, py::object v) {
+             auto Vv = vec(v);
+             return nogil([&] { return a.VectorSquaredNorm(Vv.view); });
+           })
+      .def("MatrixScaleInPlace",
+           [](HipAccelerationManager &a, py::object m, float scale) {
+             MatRef M = mat_inout(m);
+             nogil([&] { a.MatrixScaleInPlace(M, scale); });
+           })
+      .def("VectorScaleInPlace",
+           [](HipAccelerationManager &a, py::object v, float scale) {
+             VecRef Vv = vec_inout(v);
+             nogil([&] { a.VectorScaleInPlace(Vv, scale); });
+           })
+      .def("MatrixUpdate",
+           [](HipAccelerationManager &a, py::object w, py::object g, float lr) {
+             MatRef W = mat_inout(w);
+             auto G = mat(g);
+             nogil([&] { a.MatrixUpdate(W, G.view, lr); });
+           })
+      .def("VectorUpdate",
+           [](HipAccelerationManager &a, py::object w, py::object g, float lr) {
+             VecRef W = vec_inout(w);
+             auto G = vec(g);
+             nogil([&] { a.VectorUpdate(W, G.view, lr); });
+           })
+      .def("SegmentedAttentionForward",
+           [](HipAccelerationManager &a, py::object q, py::object k, py::object v, int numHeads, int segLen,
+              int segCount, bool causal) {
+             auto Q = mat(q), K = mat(k), V = mat(v);
+             return to_numpy(nogil([&] {
+               return a.SegmentedAttentionForward(Q.view, K.view, V.view, numHeads, segLen, segCount, causal);
+             }));
+           })
+      .def("SegmentedMultiHeadAttentionBackward",
+           [](HipAccelerationManager &a, py::object q, py::object k, py::object v, py::object d, int numHeads,
+              float scale, int segLen, int segCount, bool causal) {
+             auto Q = mat(q), K = mat(k), V = mat(v), Dd = mat(d);
+             auto r = nogil([&] {
+               return a.SegmentedMultiHeadAttentionBackward(Q.view, K.view, V.view, Dd.view, numHeads, scale, segLen,
+                                                            segCount, causal);
+             });
+             return py::make_tuple(to_numpy(std::move(std::get<0>(r))), to_numpy(std::move(std::get<1>(r))),
+                                   to_numpy(std::move(std::get<2>(r))));
+           })
+      .def("ApplySegmentedRotaryInPlace",
+           [](HipAccelerationManager &a, py::object q, py::object k, int numHeads, int segLen, bool inverse) {
+             MatRef Q = mat_inout(q), K = mat_inout(k);
+             if (!Q.data || !K.data) throw ArgumentNullException(!Q.data ? "q" : "k");
+             nogil([&] { a.ApplySegmentedRotaryInPlace(Q, K, numHeads, segLen, inverse); });
+           })
+      .def("FFNInputGradientBatch",
+           [](HipAccelerationManager &a, py::object x, py::object dy, py::list ws, py::list bs, std::vector<int> acts,
+              py::list wgs, py::list bgs) {
+             auto X = mat(x), DY = mat(dy);
+             FeedForwardNetwork ffn;
+             for (auto w : ws) ffn.weights.push_back(from_numpy(py::reinterpret_borrow<py::object>(w)));
+             for (auto b : bs) ffn.biases.push_back(vec_from_numpy(py::reinterpret_borrow<py::object>(b)));
+             ffn.activations = acts;
+             if (ffn.biases.size() != ffn.weights.size() || ffn.activations.size() != ffn.weights.size())
+               throw ArgumentException("FFN weights, biases and activations must have equal counts");
+             std::vector<MatRef> WG;
+             std::vector<VecRef> BG;
+             for (auto w : wgs) WG.push_back(mat_inout(py::reinterpret_borrow<py::object>(w)));
+             for (auto b : bgs) BG.push_back(vec_inout(py::reinterpret_borrow<py::object>(b)));
+             return to_numpy(nogil([&] { return a.FFNInputGradientBatch(X.view, DY.view, ffn, WG, BG); }));
+           })
       .def("SetActivationCacheLimit", &HipAccelerationManager::SetActivationCacheLimit, py::arg("bytes"))
       .def_property_readonly("activation_cache_limit", &HipAccelerationManager::activation_cache_limit)
       .def_property_readonly("activation_cache_entries", &HipAccelerationManager::activation_cache_entries)
@@ -437,6 +534,7 @@ PYBIND11_MODULE(_cdml_host, m) {
              d["h2d_bytes"] = t.h2d_bytes;
              d["d2h_bytes"] = t.d2h_bytes;
              d["h2d_skipped_bytes"] = t.h2d_skipped_bytes;
+             d["backward_from_saved"] = t.backward_from_saved;
              return d;
            })
       .def("Dispose", &HipAccelerationManager::Dispose);
@@ -595,6 +693,56 @@ PYBIND11_MODULE(_cdml_host, m) {
     }
     return d;
   };
+  py::class_<TransformerTrainer>(m, "TransformerTrainer")
+      .def(py::init<LanguageModel &, const TrainingConfig &>(), py::arg("model"), py::arg("config"),
+           py::keep_alive<1, 2>())
+      .def("TrainBatch",
+           [seqs_from](TransformerTrainer &t, py::object batch, float lr) {
+             auto b = seqs_from(batch);
+             return nogil([&] { return t.TrainBatch(b, lr); });
+           },
+           py::arg("batch"), py::arg("learningRate"))
+      .def("Train",
+           [seqs_from](TransformerTrainer &t, py::object seqs, uint64_t seed) {
+             auto b = seqs_from(seqs);
+             return nogil([&] { return t.Train(b, seed); });
+           },
+           py::arg("sequences"), py::arg("seed") = 0)
+      .def_property_readonly("last_norm", &TransformerTrainer::last_norm)
+      .def("gradients",
+           // the gradients the last update applied (after the 1/validCount and
+           // clipping scales), flat names as DeviceTrainer.gradients()
+           [](const TransformerTrainer &t) {
+             const auto &g = t.gradients();
+             py::dict d;
+             d["token_embedding"] = to_numpy(g.TokenEmbeddingGrad);
+             d["out_proj"] = to_numpy(g.OutputProjectionGrad);
+             d["out_bias"] = vec_to_numpy(g.OutputBiasGrad);
+             for (size_t i = 0; i < g.AttentionGrads.size(); ++i) {
+               const auto &a = g.AttentionGrads[i];
+               const std::string p = "layers." + std::to_string(i) + ".";
+               d[py::str(p + "wq")] = to_numpy(a.WQ_Grad);
+               d[py::str(p + "wk")] = to_numpy(a.WK_Grad);
+               d[py::str(p + "wv")] = to_numpy(a.WV_Grad);
+               d[py::str(p + "wo")] = to_numpy(a.WO_Grad);
+               d[py::str(p + "bq")] = vec_to_numpy(a.BiasQ_Grad);
+               d[py::str(p + "bk")] = vec_to_numpy(a.BiasK_Grad);
+               d[py::str(p + "bv")] = vec_to_numpy(a.BiasV_Grad);
+               d[py::str(p + "bo")] = vec_to_numpy(a.BiasO_Grad);
+               d[py::str(p + "ln1_g")] = vec_to_numpy(g.LN1Grads[i].GammaGrad);
+               d[py::str(p + "ln1_b")] = vec_to_numpy(g.LN1Grads[i].BetaGrad);
+               d[py::str(p + "ln2_g")] = vec_to_numpy(g.LN2Grads[i].GammaGrad);
+               d[py::str(p + "ln2_b")] = vec_to_numpy(g.LN2Grads[i].BetaGrad);
+               const auto &fw = t.ffn_weight_gradients()[i];
+               const auto &fb = t.ffn_bias_gradients()[i];
+               for (size_t l = 0; l < fw.size(); ++l) {
+                 d[py::str(p + "ffn_w" + std::to_string(l + 1))] = to_numpy(fw[l]);
+                 d[py::str(p + "ffn_b" + std::to_string(l + 1))] = vec_to_numpy(fb[l]);
+               }
+             }
+             return d;
+           });
+
   py::class_<DeviceTrainer>(m, "DeviceTrainer")
       .def(py::init<const LanguageModel &, const TrainingConfig &, int, int, int>(), py::arg("model"),
            py::arg("config"), py::arg("batch_capacity"), py::arg("seq_capacity"), py::arg("device") = 0)

@@ -178,6 +178,7 @@ struct FeedForwardNetwork {
 // CDML_HOST_COPY_THREADS).
 void ParallelMemcpy(void *dst, const void *src, size_t bytes);
 bool ParallelEqual(const void *a, const void *b, size_t bytes);
+void ParallelZero(void *dst, size_t bytes);
 int HostCopyThreads();
 
 // The attention backward's workspace: the stored-dS size (the causal 32 x 32
@@ -282,6 +283,48 @@ class HipAccelerationManager {
   void AccumulateTokenEmbeddingGrad(MatRef embeddingGrad, MatView dX, const std::vector<int> &tokenIds,
                                     int tokenStart, int seqLen, int embeddingDim);
 
+  // ---- the elementwise methods the trainer calls (IAccelerationManager.cs:
+  // 80-97, 221-248; AccelerationCPU.cs:507-570, 2493-2597).  The in-place
+  // ones update the array's device copy and write the result back to it.
+  void ZeroMatrix(MatRef matrix);
+  void ZeroVector(VecRef vector);
+  void MatrixAddInPlace(MatRef target, MatView addend);
+  void VectorAccumulate(VecRef target, VecView source);
+  float MatrixSquaredNorm(MatView matrix);
+  float VectorSquaredNorm(VecView vector);
+  void MatrixScaleInPlace(MatRef matrix, float scale);
+  void VectorScaleInPlace(VecRef vector, float scale);
+  void MatrixUpdate(MatRef weights, MatView gradients, float learningRate);
+  void VectorUpdate(VecRef weights, VecView gradients, float learningRate);
+
+  // ---- capabilities with no IAccelerationManager slot: code the reference
+  // runs inline on the host in TransformerTrainer and NeuralNetwork, which a
+  // HIP-aware caller reaches through an optional interface (as decode).
+  // TransformerTrainer.SegmentedAttentionForwardWithCache's attention
+  // (TransformerTrainer.cs:747-796): segmentCount independent sequences of
+  // segmentLength rows in q, k, v [segmentCount * segmentLength, D], scale
+  // 1/sqrt(d_h), keys j <= i when causal.
+  Matrix SegmentedAttentionForward(MatView q, MatView k, MatView v, int numHeads, int segmentLength,
+                                   int segmentCount, bool causal);
+  // SegmentedMultiHeadAttentionBackward (TransformerTrainer.cs:989-1120).
+  std::tuple<Matrix, Matrix, Matrix> SegmentedMultiHeadAttentionBackward(MatView Q, MatView K, MatView V,
+                                                                         MatView dConcatenated, int numHeads,
+                                                                         float scale, int segmentLength,
+                                                                         int segmentCount, bool causal);
+  // ApplySegmentedRotaryInPlace (TransformerTrainer.cs:811-848): RoPE of q and
+  // k at position row % segmentLength.
+  void ApplySegmentedRotaryInPlace(MatRef q, MatRef k, int numHeads, int segmentLength, bool inverse);
+  // NeuralNetwork.ComputeInputGradientBatch with gradient storage
+  // (NeuralNetwork.cs:773-882, AccumulateGradientsBatch :946-985): the
+  // forward recomputed with its pre-activations, the deltas through every
+  // layer (act' of FillActivationAndDerivative), wgrads[i] += delta^T x and
+  // bgrads[i] += column sums of delta; returns the input gradient.  The
+  // network's output layer must have activation None (the transformer FFN's
+  // [None, act, None], TransformerBlock.cs:101-123).
+  Matrix FFNInputGradientBatch(MatView input, MatView dOutput, const FeedForwardNetwork &ffn,
+                               const std::vector<MatRef> &weightGradients,
+                               const std::vector<VecRef> &biasGradients);
+
   // Optional decode capability (no IAccelerationManager counterpart: the
   // reference runs this inline in LanguageModel.DecoderSelfAttentionStep,
   // LanguageModel.cs:353-427).  q, k, v [1, D] are the step's projections
@@ -316,6 +359,7 @@ class HipAccelerationManager {
   // many activation uploads the shadow compare saved.
   struct TransferStats {
     uint64_t h2d_bytes = 0, d2h_bytes = 0, h2d_skipped_bytes = 0;
+    uint64_t backward_from_saved = 0;  // attention backwards that reused a forward's statistics
   };
   TransferStats transfer_stats();
 
@@ -339,7 +383,28 @@ class HipAccelerationManager {
     void *dev = nullptr, *pin = nullptr;
     size_t cap = 0;
     uint64_t last = 0, busy = 0;
+    uint64_t ver = 0;  // changes whenever the device contents may have changed
   };
+  // Row statistics of an attention forward (cdml_sdpa_fwd_lse) kept for a
+  // later MultiHeadAttentionBackward on the same arrays: valid while the q,
+  // k, v and output entries still hold the versions they had.
+  struct LseRecord {
+    const float *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
+    void *qd = nullptr, *kd = nullptr, *vd = nullptr, *od = nullptr;
+    uint64_t qv = 0, kv = 0, vv = 0, ov = 0, last = 0;
+    int batch = 0, lq = 0, lk = 0, dim = 0, heads = 0;
+    float scale = 0.f;
+    bool causal = false;
+    void *lse = nullptr;
+    size_t lse_bytes = 0;
+  };
+  float *lse_slot(size_t bytes);
+  void lse_record(const LseRecord &r);
+  const LseRecord *lse_find(const float *q, const float *k, const float *v, int batch, int lq, int lk, int dim,
+                            int heads, float scale, bool causal);
+  float *inplace_begin(float *host, int rows, int cols, int slot);
+  void inplace_end(float *host, int rows, int cols, const float *dev);
+  void inplace_fail(float *host);
   struct Xfer {  // one host<->device transfer staged through pinned memory
     void *host;
     void *dev;
@@ -386,11 +451,13 @@ class HipAccelerationManager {
   void download(void *host, const void *dev, size_t bytes);
   void sync();
   Matrix attention(MatView q, MatView k, MatView v, int numHeads, float scale, MaskView mask,
-                   bool causal);
+                   bool causal, int batch = 1);
   Matrix linear(MatView x, int rowStart, int rowCount, MatView w, VecView b, int act);
   std::tuple<Matrix, Matrix, Matrix> attention_backward(MatView Q, MatView K, MatView V,
                                                         MatView dO, int numHeads, float scale,
-                                                        MaskView mask, bool causal);
+                                                        MaskView mask, bool causal, int batch = 1);
+  float elementwise_norm(const float *host, int rows, int cols);
+  void elementwise_inplace(float *host, int rows, int cols, const float *src, int op, float a);
   void linear_backward(MatView x, MatView dy, int rows, MatView w, MatRef wgrad, VecRef bgrad,
                        float *dx_host, bool accumulate_dx);
 
@@ -411,8 +478,12 @@ class HipAccelerationManager {
   std::unordered_map<const float *, ActEntry> acts_;
   std::multimap<size_t, ActEntry> act_free_;
   size_t act_held_ = 0, act_limit_ = size_t(1) << 30;
-  uint64_t tick_ = 0, call_ = 0;
+  uint64_t tick_ = 0, call_ = 0, ver_ = 0;
   TransferStats stats_;
+  std::vector<LseRecord> lse_;  // at most kLseRecords, least recently used replaced
+  void *lse_spare_ = nullptr;   // the buffer the next record will take
+  size_t lse_spare_bytes_ = 0;
+  std::vector<DeviceBuf> ffn_scratch_;  // FFNInputGradientBatch's per-layer buffers
 };
 
 // ---- the MultiTypeTransformer classes on the manager ----------------------
@@ -486,6 +557,7 @@ class LanguageModel {
                             float temperature = 1.0f, bool greedy = true, uint64_t seed = 0);
   std::vector<float> PredictNext(MatView inputSequence);
   const TransformerConfig &config() const { return cfg_; }
+  HipAccelerationManager *AccelerationManager() const { return accel_; }  // LanguageModel.cs:17
   // LanguageModel.Save / Load (LanguageModel.cs:706-839): config.json,
   // weights.bin and ffn/ffn_layer_<i>.json in the reference's formats.
   void Save(const std::string &directory) const;
@@ -584,6 +656,101 @@ class DeviceLanguageModel {
   std::map<std::tuple<int, int, int, bool>, cdml_graph> graphs_;  // (batch, promptLen, n, fused decode)
   cdml_tiny_model tiny_{};  // descriptors for cdml_tiny_decode (layers in device memory)
   bool tiny_ok_ = false;
+};
+
+// ---- the reference's trainer on the manager -------------------------------
+// TrainingConfig (Transformers/Configuration/SharedConfigs.cs:24-60) is below.
+struct TrainingConfig;
+
+// Transformers/MultiTypeTransformer/TransformerTrainer.cs restated for
+// decoder token models on HipAccelerationManager, call for call: every
+// `_accel.X(...)` of the reference is the manager's X with host arrays in and
+// out (resident on the device between calls), the trainer's own host loops
+// (the sparse row tracker of the token-embedding gradient, ScaleMatrixLocal,
+// MatrixAllFinite, TransformerGradients.Zero) stay host loops as in the
+// reference, and the three pieces the reference runs inline on the host
+// (segmented attention forward and backward, segmented RoPE) and the FFN's
+// NeuralNetwork.ComputeInputGradientBatch go to the manager's capability
+// methods.  The model's host arrays are updated in place, as the reference's
+// are.
+class TransformerTrainer {
+ public:
+  TransformerTrainer(LanguageModel &model, const TrainingConfig &config);
+  ~TransformerTrainer();
+  // TrainBatchDiscrete(batch, 0, batch.Length, learningRate) (:217-327).
+  float TrainBatch(const std::vector<std::vector<int>> &batch, float learningRate);
+  // Train (:43-128) with the SplitMix64 shuffle seeded by `seed`.
+  float Train(const std::vector<std::vector<int>> &sequences, uint64_t seed = 0);
+  float last_norm() const { return last_norm_; }
+
+  struct AttentionGradients {  // AttentionGradients.cs:9-60
+    Matrix WQ_Grad, WK_Grad, WV_Grad, WO_Grad;
+    std::vector<float> BiasQ_Grad, BiasK_Grad, BiasV_Grad, BiasO_Grad;
+  };
+  struct LayerNormGradients {  // LayerNormGradients.cs:10-40
+    std::vector<float> GammaGrad, BetaGrad;
+  };
+  // TransformerGradients.cs:11-160 with its SparseRowGradientTracker
+  // (Transformers/Utils/SparseRowGradientTracker.cs): touched embedding rows
+  // in first-use order (a HashSet without removals enumerates that way).
+  struct Gradients {
+    Matrix TokenEmbeddingGrad, OutputProjectionGrad;
+    std::vector<float> OutputBiasGrad;
+    std::vector<AttentionGradients> AttentionGrads;
+    std::vector<LayerNormGradients> LN1Grads, LN2Grads;
+    std::vector<int> rows;
+    std::vector<uint8_t> marked;
+  };
+  const Gradients &gradients() const { return grads_; }
+  const std::vector<std::vector<Matrix>> &ffn_weight_gradients() const { return ffnWeightGrads_; }
+  const std::vector<std::vector<std::vector<float>>> &ffn_bias_gradients() const { return ffnBiasGrads_; }
+
+ private:
+  using MatPtr = std::shared_ptr<Matrix>;
+  struct AttentionCache {  // AttentionCache.cs
+    MatPtr Input, Q, K, V, AttentionOutput;
+    bool IsSegmented = false, Causal = false;
+    int SegmentLength = 0, SegmentCount = 1;
+  };
+  struct LayerNormCache {
+    MatPtr Input, Normalized;
+    std::vector<float> Mean, Variance;
+  };
+  struct ForwardCache {  // ForwardCache.cs
+    std::vector<AttentionCache> AttentionCaches;
+    std::vector<LayerNormCache> LN1Caches, LN2Caches;
+    std::vector<MatPtr> LayerInputs, FFNInputs, FFNOutputs;
+    MatPtr EmbeddedInput, FinalHiddenStates;
+    std::vector<int> TokenIds;
+    int TokenStart = 0, TokenCount = 0;
+  };
+  Matrix ForwardWithCacheDiscrete(const std::vector<int> &tokenIds, int tokenStart, int tokenCount,
+                                  ForwardCache &cache);
+  Matrix ForwardWithCacheDiscreteBatch(const std::vector<std::vector<int>> &sequences,
+                                       const std::vector<int> &offsets, int inputLen, ForwardCache &cache);
+  Matrix ForwardFromEmbeddingWithCache(MatPtr embedded, int seqLen, ForwardCache &cache, int segmentLength = 0,
+                                       int segmentCount = 1);
+  MatPtr AttentionForwardWithCache(MultiHeadAttention &attention, const MatPtr &input, bool causal,
+                                   AttentionCache &cache);
+  MatPtr SegmentedAttentionForwardWithCache(MultiHeadAttention &attention, const MatPtr &input, int segmentLength,
+                                            int segmentCount, bool causal, AttentionCache &cache);
+  void BackpropFromOutput(Matrix &dOutput, ForwardCache &cache);
+  Matrix BackpropBlock(int layer, Matrix &dOut, ForwardCache &cache);
+  Matrix BackpropAttention(int layer, Matrix &dOut, AttentionCache &cache);
+  void ZeroAllGradients();
+  void ScaleGradients(float scale);
+  float ComputeGradientNorm();
+  void ClipGradients(float threshold, float totalNorm);
+  void UpdateParameters(float learningRate);
+
+  LanguageModel &model_;
+  TransformerConfig cfg_;
+  std::unique_ptr<TrainingConfig> tc_;
+  HipAccelerationManager *accel_;
+  Gradients grads_;
+  std::vector<std::vector<Matrix>> ffnWeightGrads_;
+  std::vector<std::vector<std::vector<float>>> ffnBiasGrads_;
+  float last_norm_ = 0.f;
 };
 
 // ---- device-resident training --------------------------------------------

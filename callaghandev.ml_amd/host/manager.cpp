@@ -66,6 +66,13 @@ void HipAccelerationManager::Dispose() {
   cdml_host_free_pinned(stage_);
   stage_ = nullptr;
   stage_cap_ = stage_off_ = 0;
+  for (LseRecord &r : lse_) cdml_free(r.lse);
+  lse_.clear();
+  cdml_free(lse_spare_);
+  lse_spare_ = nullptr;
+  lse_spare_bytes_ = 0;
+  for (DeviceBuf &b : ffn_scratch_) cdml_free(b.p);
+  ffn_scratch_.clear();
   for (cdml_event e : events_) cdml_event_destroy(e);
   events_.clear();
   cdml_stream_destroy(stream_);
@@ -109,6 +116,8 @@ bool HipAccelerationManager::settle() {
       upload(p.dev, p.shadow, p.bytes);
     } else {
       stage_upload(p.dev, p.host, p.bytes, p.shadow);
+      auto it = acts_.find(static_cast<const float *>(p.host));
+      if (it != acts_.end() && it->second.dev == p.dev) it->second.ver = ++ver_;
     }
   }
   pending_.clear();
@@ -337,6 +346,7 @@ const float *HipAccelerationManager::act_in(MatView m, int slot) {
       stats_.h2d_skipped_bytes += bytes;
     } else if (e.busy != call_) {
       stage_upload(e.dev, m.data, bytes, e.pin);
+      e.ver = ++ver_;
     }
     e.busy = call_;
     return static_cast<const float *>(e.dev);
@@ -347,6 +357,7 @@ const float *HipAccelerationManager::act_in(MatView m, int slot) {
   e.cols = m.cols;
   e.last = ++tick_;
   e.busy = call_;
+  e.ver = ++ver_;
   stage_upload(e.dev, m.data, bytes, e.pin);
   acts_[m.data] = e;
   return static_cast<const float *>(e.dev);
@@ -357,7 +368,10 @@ const float *HipAccelerationManager::act_in(MatView m, int slot) {
 // with act_done, which refreshes the shadow.  A failure in between must drop
 // the entry (act_drop), since the device copy may then differ from both.
 float *HipAccelerationManager::act_inplace(MatRef m, int slot) {
-  return const_cast<float *>(act_in(MatView(m.data, m.rows, m.cols), slot));
+  float *d = const_cast<float *>(act_in(MatView(m.data, m.rows, m.cols), slot));
+  auto it = acts_.find(m.data);
+  if (it != acts_.end() && it->second.dev == d) it->second.ver = ++ver_;
+  return d;
 }
 
 // A device buffer for a result whose host storage `host` [rows, cols] this
@@ -371,6 +385,7 @@ float *HipAccelerationManager::act_out(float *host, int rows, int cols, int slot
   e.cols = cols;
   e.last = ++tick_;
   e.busy = call_;
+  e.ver = ++ver_;
   acts_[host] = e;
   return static_cast<float *>(e.dev);
 }
@@ -387,6 +402,108 @@ void HipAccelerationManager::act_done(std::initializer_list<Out> outs) {
     xs.push_back(Xfer{o.host, const_cast<float *>(o.dev), bytes, pin});
   }
   download_all(xs);
+}
+
+// ---- attention row statistics kept for the backward --------------------------
+namespace {
+constexpr size_t kLseRecords = 64;
+}  // namespace
+
+// A buffer of at least `bytes` for the next record's statistics.
+float *HipAccelerationManager::lse_slot(size_t bytes) {
+  if (lse_spare_bytes_ < bytes) {
+    sync();
+    cdml_free(lse_spare_);
+    lse_spare_ = nullptr;
+    lse_spare_bytes_ = 0;
+    check(cdml_malloc(&lse_spare_, bytes), "cdml_malloc");
+    lse_spare_bytes_ = bytes;
+  }
+  return static_cast<float *>(lse_spare_);
+}
+
+// Files `r` (whose lse is the spare buffer): it replaces a record of the same
+// arrays, or the least recently used one when all slots are taken; the
+// replaced record's buffer becomes the spare.
+void HipAccelerationManager::lse_record(const LseRecord &r) {
+  LseRecord *slot = nullptr;
+  for (LseRecord &x : lse_)
+    if (x.q == r.q && x.k == r.k && x.v == r.v) slot = &x;
+  if (!slot && lse_.size() < kLseRecords) {
+    lse_.push_back(LseRecord{});
+    slot = &lse_.back();
+  }
+  if (!slot) {
+    slot = &lse_.front();
+    for (LseRecord &x : lse_)
+      if (x.last < slot->last) slot = &x;
+  }
+  void *old = slot->lse;
+  const size_t old_bytes = slot->lse_bytes;
+  *slot = r;
+  slot->lse = lse_spare_;
+  slot->lse_bytes = lse_spare_bytes_;
+  slot->last = ++tick_;
+  lse_spare_ = old;
+  lse_spare_bytes_ = old ? old_bytes : 0;
+}
+
+// The record of a forward on exactly these arrays, if every array's device
+// copy is still the one (and the version) the forward saw.
+const HipAccelerationManager::LseRecord *HipAccelerationManager::lse_find(
+    const float *q, const float *k, const float *v, int batch, int lq, int lk, int dim, int heads, float scale,
+    bool causal) {
+  auto same = [&](const float *key, void *dev, uint64_t ver) {
+    auto it = acts_.find(key);
+    return it != acts_.end() && it->second.dev == dev && it->second.ver == ver;
+  };
+  for (LseRecord &r : lse_) {
+    if (r.q != q || r.k != k || r.v != v || r.batch != batch || r.lq != lq || r.lk != lk || r.dim != dim ||
+        r.heads != heads || r.scale != scale || r.causal != causal)
+      continue;
+    if (same(r.q, r.qd, r.qv) && same(r.k, r.kd, r.kv) && same(r.v, r.vd, r.vv) && same(r.o, r.od, r.ov)) {
+      r.last = ++tick_;
+      return &r;
+    }
+  }
+  return nullptr;
+}
+
+// ---- arrays the manager changes in place ---------------------------------------
+// A resident weight (MatrixUpdate on a model's weights) is updated in its
+// resident copy, whose shadow then follows the new host contents; any other
+// array takes the activation path.
+float *HipAccelerationManager::inplace_begin(float *host, int rows, int cols, int slot) {
+  auto it = resident_.find(host);
+  if (it != resident_.end() && it->second.rows == rows && it->second.cols == cols) {
+    Resident &r = it->second;
+    const size_t bytes = (size_t)rows * cols * sizeof(float);
+    if (bytes && !ParallelEqual(r.shadow.data(), host, bytes)) {
+      ParallelMemcpy(r.shadow.data(), host, bytes);
+      upload(r.dev, r.shadow.data(), bytes);
+    }
+    return static_cast<float *>(r.dev);
+  }
+  return act_inplace(MatRef(host, rows, cols), slot);
+}
+
+void HipAccelerationManager::inplace_end(float *host, int rows, int cols, const float *dev) {
+  const size_t n = (size_t)rows * cols;
+  act_done({Out{host, n, dev}});
+  auto it = resident_.find(host);
+  if (it != resident_.end() && it->second.dev == dev) ParallelMemcpy(it->second.shadow.data(), host, n * sizeof(float));
+}
+
+// After a failure between inplace_begin and inplace_end the device copy may
+// differ from the host array and its shadow alike: forget it.
+void HipAccelerationManager::inplace_fail(float *host) {
+  act_drop(host);
+  auto it = resident_.find(host);
+  if (it != resident_.end()) {
+    cdml_stream_synchronize(stream_);
+    cdml_free(it->second.dev);
+    resident_.erase(it);
+  }
 }
 
 void HipAccelerationManager::SetActivationCacheLimit(size_t bytes) {
@@ -492,16 +609,21 @@ std::tuple<Matrix, Matrix, Matrix> HipAccelerationManager::ProjectQKV(MatView in
 }
 
 // ---- attention core shared by SDPA and MultiHeadAttentionForward -----------
+// `batch` independent sequences: q [batch * lq, D], k and v [batch * lk, D].
+// Without a mask (head dims up to 128) the forward keeps each row's softmax
+// statistics, so a MultiHeadAttentionBackward on the same arrays can start
+// from them instead of repeating this pass.
 Matrix HipAccelerationManager::attention(MatView q, MatView k, MatView v, int numHeads,
-                                         float scale, MaskView mask, bool causal) {
-  const int lq = q.rows, lk = k.rows, dim = q.cols;
-  if (lq == 0 || lk == 0 || dim == 0) return Matrix(lq, dim);
+                                         float scale, MaskView mask, bool causal, int batch) {
+  const int rq = q.rows, rk = k.rows, dim = q.cols;
+  if (rq == 0 || rk == 0 || dim == 0) return Matrix(rq, dim);
+  const int lq = rq / batch, lk = rk / batch;
   std::lock_guard<std::mutex> lock(mu_);
   ensure_ready();
   defer_ = true;
   const float *dq = act_in(q, S_Q), *dk = act_in(k, S_K), *dv = act_in(v, S_V);
   defer_ = false;
-  Matrix out = Matrix::Uninit(lq, dim);
+  Matrix out = Matrix::Uninit(rq, dim);
   float *dout = act_out(out, S_O);
   const uint8_t *dm = nullptr;
   if (!mask.null()) {
@@ -509,13 +631,46 @@ Matrix HipAccelerationManager::attention(MatView q, MatView k, MatView v, int nu
     upload(m, mask.data, (size_t)lq * lk);
     dm = static_cast<const uint8_t *>(m);
   }
+  const bool keep = act_limit_ > 0 && mask.null() && dim / numHeads <= 128;
+  float *lse = keep ? lse_slot((size_t)batch * numHeads * lq * sizeof(float)) : nullptr;
   auto launch = [&] {
-    check(cdml_sdpa_fwd(dq, dim, dk, dim, dv, dim, dout, dim, 1, lq, lk, dim, numHeads, scale,
-                        causal ? 1 : 0, dm, stream_),
-          "cdml_sdpa_fwd");
+    if (lse)
+      check(cdml_sdpa_fwd_lse(dq, dim, dk, dim, dv, dim, dout, dim, lse, batch, lq, lk, dim, numHeads, scale,
+                              causal ? 1 : 0, nullptr, stream_),
+            "cdml_sdpa_fwd_lse");
+    else
+      check(cdml_sdpa_fwd(dq, dim, dk, dim, dv, dim, dout, dim, batch, lq, lk, dim, numHeads, scale,
+                          causal ? 1 : 0, dm, stream_),
+            "cdml_sdpa_fwd");
   };
   launch();
   if (!settle()) launch();
+  if (lse) {
+    auto eq = acts_.find(q.data), ek = acts_.find(k.data), ev = acts_.find(v.data), eo = acts_.find(out.ptr());
+    if (eq != acts_.end() && ek != acts_.end() && ev != acts_.end() && eo != acts_.end()) {
+      LseRecord r;
+      r.q = q.data;
+      r.k = k.data;
+      r.v = v.data;
+      r.o = out.ptr();
+      r.qd = eq->second.dev;
+      r.kd = ek->second.dev;
+      r.vd = ev->second.dev;
+      r.od = eo->second.dev;
+      r.qv = eq->second.ver;
+      r.kv = ek->second.ver;
+      r.vv = ev->second.ver;
+      r.ov = eo->second.ver;
+      r.batch = batch;
+      r.lq = lq;
+      r.lk = lk;
+      r.dim = dim;
+      r.heads = numHeads;
+      r.scale = scale;
+      r.causal = causal;
+      lse_record(r);
+    }
+  }
   act_done({out_of(out, dout)});
   sync();
   return out;
@@ -864,7 +1019,7 @@ std::tuple<Matrix, Matrix, Matrix> HipAccelerationManager::MultiHeadAttentionBac
 // order, then cdml_sdpa_bwd on the manager's stream.
 std::tuple<Matrix, Matrix, Matrix> HipAccelerationManager::attention_backward(
     MatView Q, MatView K, MatView V, MatView dO, int numHeads, float scale, MaskView mask,
-    bool causal) {
+    bool causal, int batch) {
   if (Q.null()) throw ArgumentNullException("Q");
   if (K.null()) throw ArgumentNullException("K");
   if (V.null()) throw ArgumentNullException("V");
@@ -886,18 +1041,26 @@ std::tuple<Matrix, Matrix, Matrix> HipAccelerationManager::attention_backward(
   if (lq == 0 || lk == 0 || dim == 0) return {Matrix(lq, dim), Matrix(lk, dim), Matrix(lk, dim)};
   std::lock_guard<std::mutex> lock(mu_);
   ensure_ready();
-  size_t base_ws = 0, stored_ws = 0;
-  check(cdml_sdpa_bwd_workspace_size(1, lq, lk, dim, numHeads, &base_ws), "cdml_sdpa_bwd_workspace_size");
+  const int sq = lq / batch, sk = lk / batch;  // rows per sequence
+  const int cflag = causal && mask.null() ? 1 : 0;
+  // Workspaces of both forms: recomputing the forward (cdml_sdpa_bwd) and
+  // starting from the forward's saved statistics (cdml_sdpa_bwd_saved); each
   // with room for the dS blocks when the shape can use them (dQ as one
-  // product), as long as the extra bytes stay under the cap and allocate
-  check(cdml_sdpa_bwd_stored_ds_workspace_size(1, lq, lk, dim, numHeads, causal && mask.null() ? 1 : 0,
-                                               &stored_ws),
+  // product), as long as the extra bytes stay under the cap and allocate.
+  size_t base_ws = 0, stored_ws = 0, saved_stored_ws = 0;
+  check(cdml_sdpa_bwd_workspace_size(batch, sq, sk, dim, numHeads, &base_ws), "cdml_sdpa_bwd_workspace_size");
+  check(cdml_sdpa_bwd_stored_ds_workspace_size(batch, sq, sk, dim, numHeads, cflag, &stored_ws),
         "cdml_sdpa_bwd_stored_ds_workspace_size");
+  check(cdml_sdpa_bwd_saved_workspace_size(batch, sq, sk, dim, numHeads, cflag, &saved_stored_ws),
+        "cdml_sdpa_bwd_saved_workspace_size");
+  const size_t saved_base_ws = (size_t)batch * numHeads * sq * sizeof(float);
   size_t ws = SdpaBackwardWorkspaceChoice(base_ws, stored_ws, kStoredDsExtraBytesCap);
-  void *dws = ws > base_ws ? try_scratch(S_WS, ws) : nullptr;
+  size_t ws_saved = SdpaBackwardWorkspaceChoice(saved_base_ws, saved_stored_ws, kStoredDsExtraBytesCap);
+  void *dws = try_scratch(S_WS, std::max(ws, ws_saved));
   if (!dws) {
     ws = base_ws;
-    dws = scratch(S_WS, ws);
+    ws_saved = saved_base_ws;
+    dws = scratch(S_WS, std::max(ws, ws_saved));
   }
   defer_ = true;
   const float *dq_in = act_in(Q, S_Q), *dk_in = act_in(K, S_K), *dv_in = act_in(V, S_V);
@@ -911,13 +1074,28 @@ std::tuple<Matrix, Matrix, Matrix> HipAccelerationManager::attention_backward(
     upload(m, mask.data, (size_t)lq * lk);
     dm = static_cast<const uint8_t *>(m);
   }
-  auto launch = [&] {
-    check(cdml_sdpa_bwd(dq_in, dim, dk_in, dim, dv_in, dim, ddo, dim, gq, dim, gk, dim, gv, dim, 1,
-                        lq, lk, dim, numHeads, scale, causal ? 1 : 0, dm, dws, ws, stream_),
-          "cdml_sdpa_bwd");
+  // the forward's statistics, when it ran on these very arrays (no mask)
+  auto saved = [&]() -> const LseRecord * {
+    return mask.null() ? lse_find(Q.data, K.data, V.data, batch, sq, sk, dim, numHeads, scale, causal) : nullptr;
   };
-  launch();
-  if (!settle()) launch();
+  auto launch = [&](const LseRecord *r) {
+    if (r)
+      check(cdml_sdpa_bwd_saved(dq_in, dim, dk_in, dim, dv_in, dim, static_cast<const float *>(r->od), dim,
+                                static_cast<const float *>(r->lse), ddo, dim, gq, dim, gk, dim, gv, dim, batch, sq,
+                                sk, dim, numHeads, scale, cflag, nullptr, dws, ws_saved, stream_),
+            "cdml_sdpa_bwd_saved");
+    else
+      check(cdml_sdpa_bwd(dq_in, dim, dk_in, dim, dv_in, dim, ddo, dim, gq, dim, gk, dim, gv, dim, batch, sq, sk,
+                          dim, numHeads, scale, causal ? 1 : 0, dm, dws, ws, stream_),
+            "cdml_sdpa_bwd");
+  };
+  const LseRecord *rec = saved();
+  launch(rec);
+  if (!settle()) {  // an input changed on the host: its record, if any, no longer holds
+    rec = saved();
+    launch(rec);
+  }
+  if (rec) ++stats_.backward_from_saved;
   act_done({out_of(dQ, gq), out_of(dK, gk), out_of(dV, gv)});
   sync();
   return {std::move(dQ), std::move(dK), std::move(dV)};
@@ -1326,6 +1504,293 @@ void HipAccelerationManager::AccumulateTokenEmbeddingGrad(MatRef embeddingGrad, 
     act_drop(embeddingGrad.data);
     throw;
   }
+}
+
+// ---- elementwise methods of the training step ----------------------------------
+namespace {
+enum ElemOp { OP_ZERO, OP_ADD, OP_SCALE, OP_UPDATE };
+}  // namespace
+
+// One in-place elementwise operation on host array `host` [rows, cols]:
+// zero, += src, *= a, or -= a * src (MatrixUpdate), on its device copy, with
+// the result written back to the host array.
+void HipAccelerationManager::elementwise_inplace(float *host, int rows, int cols, const float *src, int op,
+                                                 float a) {
+  const size_t n = (size_t)rows * cols;
+  if (n == 0) return;
+  std::lock_guard<std::mutex> lock(mu_);
+  ensure_ready();
+  float *d = nullptr;
+  if (op == OP_ZERO) {  // the old contents do not matter: no compare, no upload
+    auto it = resident_.find(host);
+    d = (it != resident_.end() && it->second.rows == rows && it->second.cols == cols)
+            ? static_cast<float *>(it->second.dev)
+            : act_out(host, rows, cols, S_O);
+  } else {
+    d = inplace_begin(host, rows, cols, S_O);
+  }
+  try {
+    const float *ds = src ? act_in(MatView(src, rows, cols), S_X) : nullptr;
+    switch (op) {
+      case OP_ZERO: check(cdml_zero_f32_async(d, n, stream_), "cdml_zero_f32_async"); break;
+      case OP_ADD: check(cdml_add_inplace(d, ds, n, stream_), "cdml_add_inplace"); break;
+      case OP_SCALE: check(cdml_scale_f32(d, a, n, stream_), "cdml_scale_f32"); break;
+      default: check(cdml_update_f32(d, ds, a, n, stream_), "cdml_update_f32"); break;
+    }
+    inplace_end(host, rows, cols, d);
+    sync();
+  } catch (...) {
+    inplace_fail(host);
+    throw;
+  }
+}
+
+float HipAccelerationManager::elementwise_norm(const float *host, int rows, int cols) {
+  const size_t n = (size_t)rows * cols;
+  if (n == 0) return 0.f;
+  std::lock_guard<std::mutex> lock(mu_);
+  ensure_ready();
+  const float *d = act_in(MatView(host, rows, cols), S_X);
+  size_t ws = 0;
+  check(cdml_sum_squares_workspace_size(&ws), "cdml_sum_squares_workspace_size");
+  float *dws = static_cast<float *>(scratch(S_WS, ws + sizeof(float)));
+  check(cdml_sum_squares(d, n, dws + ws / sizeof(float), dws, ws, stream_), "cdml_sum_squares");
+  float out = 0.f;
+  act_done({Out{&out, 1, dws + ws / sizeof(float)}});
+  sync();
+  return out;
+}
+
+// ZeroMatrix / ZeroVector: AccelerationCPU.cs:507-520
+void HipAccelerationManager::ZeroMatrix(MatRef matrix) {
+  if (!matrix.data) throw ArgumentNullException("matrix");
+  elementwise_inplace(matrix.data, matrix.rows, matrix.cols, nullptr, OP_ZERO, 0.f);
+}
+void HipAccelerationManager::ZeroVector(VecRef vector) {
+  if (vector.null()) throw ArgumentNullException("vector");
+  elementwise_inplace(vector.data, 1, vector.length, nullptr, OP_ZERO, 0.f);
+}
+// MatrixAddInPlace: AccelerationCPU.cs:522-546
+void HipAccelerationManager::MatrixAddInPlace(MatRef target, MatView addend) {
+  if (!target.data) throw ArgumentNullException("target");
+  if (addend.null()) throw ArgumentNullException("addend");
+  if (addend.rows != target.rows || addend.cols != target.cols)
+    throw ArgumentException("Matrix dimensions must match.", "addend");
+  elementwise_inplace(target.data, target.rows, target.cols, addend.data, OP_ADD, 0.f);
+}
+// VectorAccumulate: AccelerationCPU.cs:548-568 (the reference reads
+// source[j] for every j < target.Length; a shorter source is rejected here)
+void HipAccelerationManager::VectorAccumulate(VecRef target, VecView source) {
+  if (target.null()) throw ArgumentNullException("target");
+  if (source.null()) throw ArgumentNullException("source");
+  if (source.length < target.length) throw ArgumentException("source is shorter than target.", "source");
+  elementwise_inplace(target.data, 1, target.length, source.data, OP_ADD, 0.f);
+}
+// MatrixSquaredNorm / VectorSquaredNorm: AccelerationCPU.cs:2493-2512
+float HipAccelerationManager::MatrixSquaredNorm(MatView matrix) {
+  if (matrix.null()) throw ArgumentNullException("matrix");
+  return elementwise_norm(matrix.data, matrix.rows, matrix.cols);
+}
+float HipAccelerationManager::VectorSquaredNorm(VecView vector) {
+  if (vector.null()) throw ArgumentNullException("vector");
+  return elementwise_norm(vector.data, 1, vector.length);
+}
+// MatrixScaleInPlace / VectorScaleInPlace: AccelerationCPU.cs:2514-2546
+void HipAccelerationManager::MatrixScaleInPlace(MatRef matrix, float scale) {
+  if (!matrix.data) throw ArgumentNullException("matrix");
+  elementwise_inplace(matrix.data, matrix.rows, matrix.cols, nullptr, OP_SCALE, scale);
+}
+void HipAccelerationManager::VectorScaleInPlace(VecRef vector, float scale) {
+  if (vector.null()) throw ArgumentNullException("vector");
+  elementwise_inplace(vector.data, 1, vector.length, nullptr, OP_SCALE, scale);
+}
+// MatrixUpdate / VectorUpdate: AccelerationCPU.cs:2548-2597
+void HipAccelerationManager::MatrixUpdate(MatRef weights, MatView gradients, float learningRate) {
+  if (!weights.data) throw ArgumentNullException("weights");
+  if (gradients.null()) throw ArgumentNullException("gradients");
+  if (gradients.rows != weights.rows || gradients.cols != weights.cols)
+    throw ArgumentException("Matrix dimensions must match.", "gradients");
+  elementwise_inplace(weights.data, weights.rows, weights.cols, gradients.data, OP_UPDATE, learningRate);
+}
+void HipAccelerationManager::VectorUpdate(VecRef weights, VecView gradients, float learningRate) {
+  if (weights.null()) throw ArgumentNullException("weights");
+  if (gradients.null()) throw ArgumentNullException("gradients");
+  if (gradients.length < weights.length) throw ArgumentException("gradients is shorter than weights.", "gradients");
+  elementwise_inplace(weights.data, 1, weights.length, gradients.data, OP_UPDATE, learningRate);
+}
+
+// ---- capabilities the reference's trainer runs inline ----------------------------
+Matrix HipAccelerationManager::SegmentedAttentionForward(MatView q, MatView k, MatView v, int numHeads,
+                                                         int segmentLength, int segmentCount, bool causal) {
+  if (q.null()) throw ArgumentNullException("q");
+  if (k.null()) throw ArgumentNullException("k");
+  if (v.null()) throw ArgumentNullException("v");
+  if (numHeads <= 0) throw ArgumentOutOfRangeException("numHeads");
+  const int totalRows = q.rows, dim = q.cols;
+  // TransformerTrainer.cs:726-731
+  if (segmentLength <= 0 || segmentCount <= 0 || (long long)totalRows != (long long)segmentLength * segmentCount)
+    throw ArgumentException("Invalid segmented attention shape.");
+  if (k.rows != totalRows || v.rows != totalRows || k.cols != dim || v.cols != dim)
+    throw ArgumentException("Q, K and V must have the same shape.");
+  if (dim % numHeads != 0) throw ArgumentException("Embedding dimension must be divisible by numHeads.", "numHeads");
+  const float scale = 1.0f / std::sqrt((float)(dim / numHeads));  // :734
+  return attention(q, k, v, numHeads, scale, MaskView{}, causal, segmentCount);
+}
+
+std::tuple<Matrix, Matrix, Matrix> HipAccelerationManager::SegmentedMultiHeadAttentionBackward(
+    MatView Q, MatView K, MatView V, MatView dConcatenated, int numHeads, float scale, int segmentLength,
+    int segmentCount, bool causal) {
+  if (Q.null()) throw ArgumentNullException("Q");
+  if (numHeads <= 0) throw ArgumentOutOfRangeException("numHeads");
+  // TransformerTrainer.cs:1000-1006
+  if (segmentLength <= 0 || segmentCount <= 0 || (long long)Q.rows != (long long)segmentLength * segmentCount)
+    throw ArgumentException("Invalid segmented attention backward shape.");
+  return attention_backward(Q, K, V, dConcatenated, numHeads, scale, MaskView{}, causal, segmentCount);
+}
+
+void HipAccelerationManager::ApplySegmentedRotaryInPlace(MatRef q, MatRef k, int numHeads, int segmentLength,
+                                                         bool inverse) {
+  if (!q.data) throw ArgumentNullException("q");
+  if (!k.data) throw ArgumentNullException("k");
+  if (numHeads <= 0) throw ArgumentOutOfRangeException("numHeads");
+  if (segmentLength <= 0) throw ArgumentOutOfRangeException("segmentLength");
+  if (k.rows != q.rows || k.cols != q.cols) throw ArgumentException("Q and K must have the same shape.");
+  const int dim = q.cols;
+  if (dim % numHeads != 0)
+    throw ArgumentException("Embedding dimension must be divisible by number of heads.");
+  const int headDim = dim / numHeads;
+  if (headDim & 1) throw ArgumentException("RoPE requires an even per-head dimension.");
+  if (q.rows == 0 || headDim == 0) return;
+  std::lock_guard<std::mutex> lock(mu_);
+  ensure_ready();
+  float *dq = act_inplace(q, S_Q);
+  float *dk = act_inplace(k, S_K);
+  try {
+    for (float *d : {dq, dk})
+      check(cdml_rope(d, q.rows, dim, 0, headDim, numHeads, 10000.0f, inverse ? 1 : 0, 0, segmentLength, nullptr,
+                      stream_),
+            "cdml_rope");
+    act_done({Out{q.data, (size_t)q.rows * dim, dq}, Out{k.data, (size_t)k.rows * dim, dk}});
+    sync();
+  } catch (...) {
+    act_drop(q.data);
+    act_drop(k.data);
+    throw;
+  }
+}
+
+// NeuralNetwork.ComputeInputGradientBatch: NeuralNetwork.cs:773-882
+Matrix HipAccelerationManager::FFNInputGradientBatch(MatView input, MatView dOutput, const FeedForwardNetwork &ffn,
+                                                     const std::vector<MatRef> &weightGradients,
+                                                     const std::vector<VecRef> &biasGradients) {
+  if (input.null()) throw ArgumentNullException("input");
+  if (dOutput.null()) throw ArgumentNullException("dOutput");
+  if (ffn.weights.empty()) throw InvalidOperationException("Neural network must have at least input and output layers.");
+  const int rows = input.rows, inputDim = input.cols, outputDim = dOutput.cols;
+  const int nl = (int)ffn.weights.size();
+  if (dOutput.rows != rows) throw ArgumentException("dOutput row count must match input row count.", "dOutput");
+  if (inputDim != ffn.input_size())
+    throw ArgumentException("Input matrix column count (" + std::to_string(inputDim) +
+                                ") must match network input size (" + std::to_string(ffn.input_size()) + ").",
+                            "input");
+  if (outputDim != ffn.output_size())
+    throw ArgumentException("dOutput column count (" + std::to_string(outputDim) +
+                                ") must match network output size (" + std::to_string(ffn.output_size()) + ").",
+                            "dOutput");
+  if ((int)weightGradients.size() != nl || (int)biasGradients.size() != nl)
+    throw ArgumentException("Gradient storage must contain one entry per non-input layer.");
+  for (int l = 0; l < nl; ++l) {
+    const Matrix &w = ffn.weights[l];
+    if (l > 0 && w.cols != ffn.weights[l - 1].rows) throw ArgumentException("FFN layer widths do not chain.", "ffn");
+    if ((int)ffn.biases[l].size() != w.rows) throw ArgumentException("FFN bias length mismatch.", "ffn");
+    if (!weightGradients[l].data || weightGradients[l].rows != w.rows || weightGradients[l].cols != w.cols)
+      throw ArgumentException("Weight gradient shape does not match layer shape.", "weightGradients");
+    if (biasGradients[l].null() || biasGradients[l].length != w.rows)
+      throw ArgumentException("Bias gradient length does not match layer size.", "biasGradients");
+  }
+  if (ffn.activations.back() != None)
+    throw ArgumentException("FFNInputGradientBatch takes networks whose output layer has no activation.", "ffn");
+  if (rows == 0) return Matrix(0, inputDim);
+  std::lock_guard<std::mutex> lock(mu_);
+  ensure_ready();
+  // forward with pre-activations for the hidden layers (the output layer's
+  // own values are not needed: its derivative is 1)
+  if ((int)ffn_scratch_.size() < 2 * nl + 2) ffn_scratch_.resize(2 * nl + 2);
+  auto buf = [&](int i, size_t bytes) -> float * {
+    DeviceBuf &b = ffn_scratch_[i];
+    if (b.bytes < bytes) {
+      sync();
+      check(cdml_free(b.p), "cdml_free");
+      b.p = nullptr;
+      b.bytes = 0;
+      check(cdml_malloc(&b.p, bytes), "cdml_malloc");
+      b.bytes = bytes;
+    }
+    return static_cast<float *>(b.p);
+  };
+  const float *x0 = act_in(input, S_X);
+  const float *dy = act_in(dOutput, S_Q);
+  std::vector<const float *> dw(nl), db(nl), xin(nl);
+  std::vector<float *> z(nl, nullptr);
+  xin[0] = x0;
+  for (int l = 0; l < nl; ++l) {
+    const Matrix &w = ffn.weights[l];
+    dw[l] = resident(w.ptr(), w.rows, w.cols);
+    db[l] = resident(ffn.biases[l].data(), 1, w.rows);
+    if (l + 1 < nl) {
+      z[l] = buf(2 * l, (size_t)rows * w.rows * sizeof(float));
+      float *y = buf(2 * l + 1, (size_t)rows * w.rows * sizeof(float));
+      check(cdml_linear_preact(xin[l], w.cols, dw[l], db[l], z[l], y, w.rows, rows, w.cols, w.rows,
+                               ffn.activations[l], stream_),
+            "cdml_linear_preact");
+      xin[l + 1] = y;
+    }
+  }
+  std::vector<float *> gw(nl), gb(nl);
+  size_t ws = 0;
+  for (int l = 0; l < nl; ++l) {
+    size_t w1 = 0;
+    check(cdml_linear_backward_workspace_size(rows, ffn.weights[l].cols, ffn.weights[l].rows, &w1),
+          "cdml_linear_backward_workspace_size");
+    ws = std::max(ws, w1);
+  }
+  void *dws = ws ? scratch(S_WS, ws) : nullptr;
+  Matrix dInput = Matrix::Uninit(rows, inputDim);
+  float *dxo = act_out(dInput, S_O);
+  int started = 0;
+  try {
+    for (int l = 0; l < nl; ++l, ++started) {
+      gw[l] = inplace_begin(weightGradients[l].data, weightGradients[l].rows, weightGradients[l].cols, S_GW0);
+      gb[l] = inplace_begin(biasGradients[l].data, 1, biasGradients[l].length, S_GB0);
+    }
+    // deltas from the output layer down (currentDeltas = dOutput for an
+    // output layer without activation); layer l's input gradient carries
+    // act'(z of layer l - 1) into the next delta
+    const float *delta = dy;
+    for (int l = nl - 1; l >= 0; --l) {
+      const Matrix &w = ffn.weights[l];
+      float *dxl = l > 0 ? buf(2 * nl + (l & 1), (size_t)rows * w.cols * sizeof(float)) : dxo;
+      check(cdml_linear_backward_act(xin[l], w.cols, delta, w.rows, dw[l], l > 0 ? z[l - 1] : nullptr,
+                                     l > 0 ? ffn.activations[l - 1] : CDML_ACT_NONE, nullptr, dxl, w.cols, gw[l],
+                                     gb[l], rows, w.cols, w.rows, dws, ws, stream_),
+            "cdml_linear_backward_act");
+      delta = dxl;
+    }
+    std::vector<Xfer> xs;
+    act_done({out_of(dInput, dxo)});
+    for (int l = 0; l < nl; ++l) {
+      inplace_end(weightGradients[l].data, weightGradients[l].rows, weightGradients[l].cols, gw[l]);
+      inplace_end(biasGradients[l].data, 1, biasGradients[l].length, gb[l]);
+    }
+    sync();
+  } catch (...) {
+    for (int l = 0; l < started; ++l) {
+      inplace_fail(weightGradients[l].data);
+      inplace_fail(biasGradients[l].data);
+    }
+    throw;
+  }
+  return dInput;
 }
 
 // ---- decode capability ------------------------------------------------------

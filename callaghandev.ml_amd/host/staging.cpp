@@ -191,6 +191,19 @@ void ParallelMemcpy(void *dst, const void *src, size_t bytes) {
   });
 }
 
+void ParallelZero(void *dst, size_t bytes) {
+  if (bytes < kParallelMin) {
+    if (bytes) std::memset(dst, 0, bytes);
+    return;
+  }
+  const int n = slices(bytes);
+  const size_t per = ((bytes + n - 1) / n + 63) & ~size_t(63);
+  pool().run(n, [&](int i) {
+    const size_t off = (size_t)i * per;
+    if (off < bytes) std::memset(static_cast<char *>(dst) + off, 0, std::min(per, bytes - off));
+  });
+}
+
 bool ParallelEqual(const void *a, const void *b, size_t bytes) {
   if (bytes < kParallelMin) return bytes == 0 || std::memcmp(a, b, bytes) == 0;
   const int n = slices(bytes);

@@ -407,6 +407,24 @@ int cdml_mse_loss(const float *pred, int ldp, const float *targets, int ldt,
 int cdml_add_inplace(float *target, const float *addend, size_t count,
                      cdml_stream stream);
 
+/* IAccelerationManager.MatrixUpdate / VectorUpdate (:246, :248), replacing
+ * AccelerationCPU.cs:2548-2597: weights[i] -= learning_rate * gradients[i]
+ * (product and difference rounded separately) for `count` floats. */
+int cdml_update_f32(float *weights, const float *gradients,
+                    float learning_rate, size_t count, cdml_stream stream);
+
+/* IAccelerationManager.MatrixScaleInPlace / VectorScaleInPlace (:235, :240),
+ * replacing AccelerationCPU.cs:2514-2546: x[i] *= scale. */
+int cdml_scale_f32(float *x, float scale, size_t count, cdml_stream stream);
+
+/* IAccelerationManager.MatrixSquaredNorm / VectorSquaredNorm (:221, :226),
+ * replacing AccelerationCPU.cs:2493-2512: out[0] (device) = sum of x[i]^2,
+ * in a fixed order (512 block partials, then their sum).  workspace:
+ * cdml_sum_squares_workspace_size bytes. */
+int cdml_sum_squares_workspace_size(size_t *bytes);
+int cdml_sum_squares(const float *x, size_t count, float *out, void *workspace,
+                     size_t workspace_bytes, cdml_stream stream);
+
 /* IAccelerationManager.AccumulateTokenEmbeddingGrad (:203-205), replacing
  * AccelerationCPU.cs:2339-2370, as a gather over groups of rows that share a
  * token: for group k, rows order[group_start[k] .. group_start[k+1]) of
