@@ -57,7 +57,7 @@ struct KvStage {
   static constexpr int ROWS_PER_PASS = FA_THREADS / F4_ROW;
   static constexpr int NV = BN / ROWS_PER_PASS;
   static constexpr int NS = BN * HD / FA_THREADS;
-  float4 r[VEC ? NV : 1];
+  vf4 r[VEC ? NV : 1];  // a native vector, so the prefetch stays a register load issued at the loop top
   float s[VEC ? 1 : NS];
   uint32_t off[VEC ? NV : 1];  // element offsets of this thread's rows in a tile
   int col;
@@ -77,7 +77,7 @@ struct KvStage {
       const float *tile = base + (size_t)k0 * ld;  // wave-uniform
       const uint32_t lim = (uint32_t)(min(lk - 1 - k0, BN - 1) * ld) + col;
 #pragma unroll
-      for (int i = 0; i < NV; ++i) r[i] = *reinterpret_cast<const float4 *>(tile + min(off[i], lim));
+      for (int i = 0; i < NV; ++i) r[i] = *reinterpret_cast<const vf4 *>(tile + min(off[i], lim));
     } else {
       const int t = threadIdx.x;
 #pragma unroll
@@ -95,7 +95,7 @@ struct KvStage {
     if constexpr (VEC) {
 #pragma unroll
       for (int i = 0; i < NV; ++i)
-        *reinterpret_cast<float4 *>(&lds[t / F4_ROW + ROWS_PER_PASS * i][col]) = r[i];
+        *reinterpret_cast<vf4 *>(&lds[t / F4_ROW + ROWS_PER_PASS * i][col]) = r[i];
     } else {
 #pragma unroll
       for (int i = 0; i < NS; ++i) {
@@ -111,7 +111,7 @@ struct KvStage {
 // l % 32 + 32.
 __device__ __forceinline__ float halves_max(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float halves_sum(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -197,6 +197,9 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArg
         for (int r = 0; r < 4; ++r) qreg[4 * u + r] = (qok && d + r < a.hd) ? qrow[d + r] : 0.f;
       }
     }
+    // Q in the exp2 domain: the scores leave the MFMA as s * scale * log2(e)
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) qreg[i] *= a.scale_log2;
   }
 
   const int kend = CAUSAL ? min(q0 + FA_BM, a.lk) : a.lk;
@@ -216,14 +219,14 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArg
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
-  // Scores enter the exp2 domain as s * c.  For c > 0 the tile max is taken
-  // on the raw scores and p = exp2(fma(s, c, -m)); otherwise the scores are
-  // scaled first and c becomes 1.
-  const bool pos_scale = a.scale_log2 > 0.f;
-  const float c = pos_scale ? a.scale_log2 : 1.0f;
-  float m_run = -INFINITY;   // reference max of this lane's query (exp2 domain)
+  // The reference max of this lane's query (exp2 domain) is subtracted by
+  // the MFMA itself: the first step of every S^T block starts from negm,
+  // -m_run in all 16 entries (0 until the first visible key sets m_run), so
+  // the scores come out relative to the reference and p = exp2(score).
+  float m_run = -INFINITY;
+  float thr = -INFINITY;  // rescale threshold: any visible key until m_run is set
   float l_a = 0.f, l_b = 0.f;  // running sums over this half-wave's keys
-  const floatx16 zero = {};
+  floatx16 negm = {};
   // Last key this lane may attend (the causal diagonal and the sequence end).
   const int key_last = CAUSAL ? min(qi, a.lk - 1) : a.lk - 1;
 
@@ -255,7 +258,7 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArg
       for (int u = 0; u < NKG; ++u) {
         float4 knext;
         if (u + 1 < NKG) knext = *reinterpret_cast<const float4 *>(&krow[li][8 * (u + 1) + 4 * hf]);
-        sacc = mfma32x32x2(kcur.x, qreg[4 * u + 0], u == 0 ? zero : sacc);
+        sacc = mfma32x32x2(kcur.x, qreg[4 * u + 0], u == 0 ? negm : sacc);
         sacc = mfma32x32x2(kcur.y, qreg[4 * u + 1], sacc);
         sacc = mfma32x32x2(kcur.z, qreg[4 * u + 2], sacc);
         sacc = mfma32x32x2(kcur.w, qreg[4 * u + 3], sacc);
@@ -268,16 +271,12 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArg
 #pragma unroll
         for (int db = 0; db < NDB; ++db) vr[st][db] = vrow[acc_key(st) + 4 * hf][db * 32 + li];
 
-      if (!pos_scale) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[r] *= a.scale_log2;
-      }
       // Masking (wave-uniform decision): the diagonal, the sequence end, a mask.
       if (HAS_MASK || kb0 + 31 > (CAUSAL ? min(qw0, a.lk - 1) : a.lk - 1)) {
-        const int thr = key_last - kb0 - 4 * hf;  // last visible offset for this lane
+        const int last_vis = key_last - kb0 - 4 * hf;  // last visible offset for this lane
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          bool ok = acc_key(r) <= thr;
+          bool ok = acc_key(r) <= last_vis;
           if (HAS_MASK) {
             const int key = min(kb0 + acc_key(r) + 4 * hf, a.lk - 1);
             ok = ok && qi < a.lq && mrow[key] != 0;
@@ -285,30 +284,38 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArg
           sacc[r] = ok ? sacc[r] : -INFINITY;
         }
       }
+      // tile max relative to the reference (-inf: no visible key)
       float smax = max3_scores(sacc[0], sacc[1], sacc[2]);
 #pragma unroll
       for (int r = 3; r < 15; r += 2) smax = max3_scores(smax, sacc[r], sacc[r + 1]);
       smax = max3_scores(smax, sacc[15], -INFINITY);
       smax = halves_max(smax);
-      const float m_tile = smax * c;  // exact max of fl(s * c) for c > 0
 
-      // Lazy rescale: only when this lane's max grew by more than the threshold.
-      const float m_new = fmaxf(m_run, m_tile);
-      const bool need = m_new > m_run + kRescaleThreshold;
+      // Lazy rescale: the first visible key sets the reference, later only a
+      // rise of more than the threshold moves it (the scores shift with it).
+      const bool need = smax > thr;
       if (__builtin_amdgcn_ballot_w64(need)) {
-        const float alpha = need ? fast_exp2(m_run - m_new) : 1.0f;
-        m_run = need ? m_new : m_run;
+        const bool first = m_run == -INFINITY;
+        const float shift = need ? smax : 0.f;
+        const float alpha = (need && !first) ? fast_exp2(-smax) : 1.0f;  // o and l are 0 before the first key
+        m_run = need ? (first ? smax : m_run + smax) : m_run;
+        thr = m_run == -INFINITY ? -INFINITY : kRescaleThreshold;
         l_a *= alpha;
         l_b *= alpha;
+        const float nref = m_run == -INFINITY ? 0.f : -m_run;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          sacc[r] -= shift;
+          negm[r] = nref;
+        }
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
           for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
       }
-      const float nm = m_run == -INFINITY ? 0.f : -m_run;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(fmaf(sacc[r], c, nm));
+        const float p = fast_exp2(sacc[r]);
         sacc[r] = p;
         if (r & 1) l_b += p;
         else l_a += p;
