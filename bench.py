@@ -33,8 +33,10 @@ from __future__ import annotations
 
 import argparse
 import ctypes as C
+import hashlib
 import json
 import os
+import re
 import sys
 import time
 
@@ -49,10 +51,45 @@ METRIC = "attn fwd TFLOP/s (% fp32 MFMA peak) @seq4096; decode HBM GB/s @KV8192"
 FP32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense fp32 matrix, AMD published
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, AMD published
 
-# HBM bytes per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded in
-# profiles/mha_c3_decode_c4_hbm_traffic.md (FETCH_SIZE scaled by 1.99918, the factor a
-# 64 MiB device copy reads on that counter; WRITE_SIZE by 1.0).
-TRAFFIC_BYTES = {"flash_c3": 1047999283, "decode_c4": 8643213076}
+# HBM bytes per launch come from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes that
+# profile_bench.py records in this profile, together with a digest of the kernel
+# sources they were measured on; a record measured on other sources is not used.
+TRAFFIC_PROFILE = os.path.join("profiles", "mha_c3_decode_c4_hbm_traffic.md")
+TRAFFIC_SOURCES = {
+    "flash_c3": ("callaghandev.ml_amd/csrc/flash_attn.hip", "callaghandev.ml_amd/csrc/common.h"),
+    "decode_c4": ("callaghandev.ml_amd/csrc/decode_attn.hip", "callaghandev.ml_amd/csrc/common.h"),
+}
+
+
+def source_digest(paths):
+    """sha256 (first 16 hex digits) of the named files' bytes, in order."""
+    h = hashlib.sha256()
+    for p in paths:
+        with open(os.path.join(ROOT, p), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic(name):
+    """(HBM bytes per launch or None, provenance) for kernel `name` from the
+    traffic profile; None when the profile was measured on other sources."""
+    prov = {"profile": TRAFFIC_PROFILE, "current_sources": source_digest(TRAFFIC_SOURCES[name])}
+    try:
+        with open(os.path.join(ROOT, TRAFFIC_PROFILE)) as f:
+            m = re.search(r"<!-- traffic-record (\{.*?\}) -->", f.read(), re.S)
+        rec = json.loads(m.group(1)) if m else None
+    except OSError:
+        rec = None
+    if not rec or name not in rec.get("bytes", {}):
+        prov["status"] = "no record"
+        return None, prov
+    prov["measured_on_sources"] = rec["sources"][name]
+    prov["measured"] = rec.get("date")
+    if rec["sources"][name] != prov["current_sources"]:
+        prov["status"] = "stale: the kernel sources changed since the profile (rerun profile_bench.py)"
+        return None, prov
+    prov["status"] = "current"
+    return int(rec["bytes"][name]), prov
 
 # c3 (BASELINE.json configs[2]): one MHA layer of the long-context stack
 C3 = dict(batch=4, seq=4096, dim=1024, heads=16)
@@ -162,7 +199,41 @@ def bench_mha(N, st, steps, warmup, cfg=None):
     flash_ms, qkv_ms, out_ms = (float(np.mean(t.ms())) for t in (tf, tq, to))
     y = dy.download((rows, D), stream=st)
     assert np.all(np.isfinite(y)), "non-finite MHA output"
-    return dict(wall_s=wall, dev_ms=dev_ms, flash_ms=flash_ms, qkv_ms=qkv_ms, out_ms=out_ms)
+    err = float64_prefix_check(x[:64], ws, y[:64], H)
+    return dict(wall_s=wall, dev_ms=dev_ms, flash_ms=flash_ms, qkv_ms=qkv_ms, out_ms=out_ms,
+                selfcheck_max_abs_err=err)
+
+
+def float64_prefix_check(x, ws, y, heads, atol=1e-4, rtol=1e-3):
+    """The first rows of sequence 0 depend only on its first rows (causal), so
+    they are recomputed here in float64 numpy from the same inputs (Q/K/V
+    projections, interleaved RoPE with base 10000, causal softmax attention,
+    output projection; zero biases) and the timed kernels' output must meet
+    the parity bar against them.  Returns the largest absolute difference."""
+    n, D = x.shape
+    hd = D // heads
+    xd = x.astype(np.float64)
+    q, k, v = (xd @ w.astype(np.float64).T for w in ws[:3])
+    pos = np.arange(n, dtype=np.float64)[:, None]
+    theta = pos / (10000.0 ** (2.0 * np.arange(hd // 2) / hd))[None, :]   # [n, hd/2]
+    c, s_ = np.tile(np.cos(theta), heads), np.tile(np.sin(theta), heads)   # [n, D/2]
+    for t in (q, k):
+        a, b = t[:, 0::2].copy(), t[:, 1::2].copy()
+        t[:, 0::2], t[:, 1::2] = a * c - b * s_, a * s_ + b * c
+    att = np.empty_like(q)
+    scale = 1.0 / np.sqrt(hd)
+    mask = np.triu(np.ones((n, n), bool), 1)
+    for h in range(heads):
+        cols = slice(h * hd, (h + 1) * hd)
+        sc = q[:, cols] @ k[:, cols].T * scale
+        sc[mask] = -np.inf
+        p = np.exp(sc - sc.max(axis=1, keepdims=True))
+        att[:, cols] = (p / p.sum(axis=1, keepdims=True)) @ v[:, cols]
+    want = att @ ws[3].astype(np.float64).T
+    diff = np.abs(y.astype(np.float64) - want)
+    if not np.all(diff <= atol + rtol * np.abs(want)):
+        raise AssertionError(f"bench self-check: MHA output rows differ from float64 by up to {diff.max():.3g}")
+    return float(diff.max())
 
 
 def bench_decode(N, st, steps, warmup):
@@ -213,7 +284,16 @@ def bench_mha_backward(N, st, steps, warmup, cfg=None):
     (TransformerTrainer.cs:933-987): BackpropLinearProjection of the output
     projection, MultiHeadAttentionBackward with the decoder mask, the inverse
     RoPE of dQ and dK, BackpropQKV.  Events around the attention-core kernels
-    (cdml_sdpa_bwd) and around the whole chain."""
+    and around the whole chain.
+
+    Two forms of the attention core are timed:
+      * from the forward's saved output and row statistics
+        (cdml_sdpa_bwd_saved; the forward with statistics, cdml_sdpa_fwd_lse,
+        runs once before timing, as in the training step).  The device trainer
+        always takes it, and the drop-in manager takes it whenever it still
+        holds the statistics of the forward call on the same arrays;
+      * recomputing the row statistics (cdml_sdpa_bwd): the drop-in manager's
+        form when no forward on those arrays preceded the call."""
     lib = N.lib()
     cfg = cfg or C3
     B, L, D, H = cfg["batch"], cfg["seq"], cfg["dim"], cfg["heads"]
@@ -228,23 +308,37 @@ def bench_mha_backward(N, st, steps, warmup, cfg=None):
     gw = [N.DeviceBuffer.from_array(np.zeros((D, D), np.float32), st) for _ in range(4)]
     gb = [N.DeviceBuffer.from_array(np.zeros(D, np.float32), st) for _ in range(4)]
     dcat, dq, dk, dv, dxin = (N.DeviceBuffer(rows * D * 4) for _ in range(5))
-    wsz, wsl, wsq = C.c_size_t(0), C.c_size_t(0), C.c_size_t(0)
+    wsz, wss, wsl, wsq = C.c_size_t(0), C.c_size_t(0), C.c_size_t(0), C.c_size_t(0)
     N.check(lib.cdml_sdpa_bwd_stored_ds_workspace_size(B, L, L, D, H, 1, C.byref(wsz)))
+    N.check(lib.cdml_sdpa_bwd_saved_workspace_size(B, L, L, D, H, 1, C.byref(wss)))
     N.check(lib.cdml_linear_backward_workspace_size(rows, D, D, C.byref(wsl)))
     N.check(lib.cdml_backprop_qkv_workspace_size(rows, D, D, C.byref(wsq)))
     dws = N.DeviceBuffer(max(16, wsz.value))
+    dwss = N.DeviceBuffer(max(16, wss.value))
     dwsg = N.DeviceBuffer(max(16, wsl.value, wsq.value))
     s = st.handle
     scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
     b = bufs
+    # the forward's saved output and row statistics (untimed, as in the training step)
+    osv, lse = N.DeviceBuffer(rows * D * 4), N.DeviceBuffer(B * H * L * 4)
+    N.check(lib.cdml_sdpa_fwd_lse(b["q"].ptr, D, b["k"].ptr, D, b["v"].ptr, D, osv.ptr, D, lse.ptr,
+                                  B, L, L, D, H, scale, 1, None, s))
 
-    def step(t_core=None):
+    def core(saved):
+        if saved:
+            N.check(lib.cdml_sdpa_bwd_saved(b["q"].ptr, D, b["k"].ptr, D, b["v"].ptr, D, osv.ptr, D, lse.ptr,
+                                            dcat.ptr, D, dq.ptr, D, dk.ptr, D, dv.ptr, D, B, L, L, D, H, scale,
+                                            1, None, dwss.ptr, wss.value, s))
+        else:
+            N.check(lib.cdml_sdpa_bwd(b["q"].ptr, D, b["k"].ptr, D, b["v"].ptr, D, dcat.ptr, D, dq.ptr, D,
+                                      dk.ptr, D, dv.ptr, D, B, L, L, D, H, scale, 1, None, dws.ptr, wsz.value, s))
+
+    def step(saved, t_core=None):
         N.check(lib.cdml_linear_backward(b["att"].ptr, D, b["dy"].ptr, D, dw[3].ptr, dcat.ptr, D, gw[3].ptr,
                                          gb[3].ptr, rows, D, D, 0, dwsg.ptr, wsl.value, s))
         if t_core:
             t_core.start(st)
-        N.check(lib.cdml_sdpa_bwd(b["q"].ptr, D, b["k"].ptr, D, b["v"].ptr, D, dcat.ptr, D, dq.ptr, D,
-                                  dk.ptr, D, dv.ptr, D, B, L, L, D, H, scale, 1, None, dws.ptr, wsz.value, s))
+        core(saved)
         if t_core:
             t_core.stop(st)
         for t in (dq, dk):
@@ -253,27 +347,41 @@ def bench_mha_backward(N, st, steps, warmup, cfg=None):
                                       gw[0].ptr, gb[0].ptr, gw[1].ptr, gb[1].ptr, gw[2].ptr, gb[2].ptr,
                                       dxin.ptr, rows, D, D, dwsg.ptr, wsq.value, s))
 
-    for _ in range(warmup):
-        step()
-    st.synchronize()
-    tc = Timer(N, steps)
-    e0, e1 = N.Event(), N.Event()
-    e0.record(st)
-    for _ in range(steps):
-        step(tc)
-    e1.record(st)
-    st.synchronize()
-    g = dxin.download((rows, D), stream=st)
-    assert np.all(np.isfinite(g)), "non-finite MHA backward output"
-    core_ms = float(np.mean(tc.ms()))
-    step_ms = e0.elapsed_ms(e1) / steps
+    def timed(saved):
+        for _ in range(warmup):
+            step(saved)
+        st.synchronize()
+        tc = Timer(N, steps)
+        e0, e1 = N.Event(), N.Event()
+        e0.record(st)
+        for _ in range(steps):
+            step(saved, tc)
+        e1.record(st)
+        st.synchronize()
+        g = dxin.download((rows, D), stream=st)
+        assert np.all(np.isfinite(g)), "non-finite MHA backward output"
+        return e0.elapsed_ms(e1) / steps, float(np.mean(tc.ms()))
+
+    step_ms, core_ms = timed(True)
+    step_rc, core_rc = timed(False)
     pairs = L * (L + 1) // 2
     core_fl = 8 * B * H * hd * pairs          # dV = P^T dO, dP = dO V^T, dQ = dS K, dK = dS^T Q
     proj_fl = 16 * rows * D * D               # out-proj dX + dW, and Q/K/V dX + dW
-    return {"ms": round(step_ms, 4), "tflops": round((core_fl + proj_fl) / (step_ms * 1e-3) / 1e12, 2),
+
+    def tf(fl, ms):
+        return fl / (ms * 1e-3) / 1e12
+
+    return {"ms": round(step_ms, 4), "tflops": round(tf(core_fl + proj_fl, step_ms), 2),
             "attention_core_ms": round(core_ms, 4),
-            "attention_core_tflops": round(core_fl / (core_ms * 1e-3) / 1e12, 2),
-            "attention_core_frac_of_fp32_mfma_peak": round(core_fl / (core_ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
+            "attention_core_tflops": round(tf(core_fl, core_ms), 2),
+            "attention_core_frac_of_fp32_mfma_peak": round(tf(core_fl, core_ms) / FP32_MFMA_PEAK_TFLOPS, 4),
+            "attention_core_form": "cdml_sdpa_bwd_saved: from the forward's saved output and row statistics",
+            "recomputing_statistics": {
+                "ms": round(step_rc, 4), "tflops": round(tf(core_fl + proj_fl, step_rc), 2),
+                "attention_core_ms": round(core_rc, 4),
+                "attention_core_tflops": round(tf(core_fl, core_rc), 2),
+                "attention_core_frac_of_fp32_mfma_peak": round(tf(core_fl, core_rc) / FP32_MFMA_PEAK_TFLOPS, 4),
+                "form": "cdml_sdpa_bwd: the row statistics are recomputed by a forward pass inside the call"},
             "flop_count": "matmul FLOPs of the gradients only: 8 x head_dim per causal (query, key) pair "
                           "for the core (no recompute counted), 4 x rows x D^2 per projection"}
 
@@ -420,9 +528,17 @@ def extras(N, st, only=None):
         ms5 = dev5.time_forward(x5, 256, 512, steps=5, warmup=2, continuous=True)
         core, qkv, o = mha_flops(256, 512, 256, 8)
         fl5 = 6 * (core + qkv + o + 4 * 256 * 512 * 256 * 1024) + 2 * 256 * 512 * 256 * (5 + 1)
-        out["c5_time_series_model"] = {"ms": round(ms5, 3), "tflops": round(fl5 / (ms5 * 1e-3) / 1e12, 2),
-                                       "windows_per_s": round(256 / (ms5 * 1e-3), 1)}
         del dev5, lm5
+        # the model's attention shape alone (d_h 32): flash kernel by events
+        r5 = bench_mha(N, st, 10, 5, dict(batch=256, seq=512, dim=256, heads=8))
+        core5 = mha_flops(256, 512, 256, 8)[0]
+        fa5 = core5 / (r5["flash_ms"] * 1e-3) / 1e12
+        out["c5_time_series_model"] = {"ms": round(ms5, 3), "tflops": round(fl5 / (ms5 * 1e-3) / 1e12, 2),
+                                       "windows_per_s": round(256 / (ms5 * 1e-3), 1),
+                                       "attention_kernel_ms": round(r5["flash_ms"], 4),
+                                       "attention_kernel_tflops": round(fa5, 2),
+                                       "attention_kernel_frac_of_fp32_mfma_peak":
+                                           round(fa5 / FP32_MFMA_PEAK_TFLOPS, 4)}
     if want("c1_text_model"):
         # c1: README text model, forward of 4 x 64 tokens and greedy generation of 20 tokens
         log("[bench] extras: c1 text model")
@@ -576,6 +692,7 @@ def main():
     ms_per_step = mha["wall_s"] / args.steps * 1e3
     value = total / (ms_per_step * 1e-3) / 1e12
     flash_tflops = core / (mha["flash_ms"] * 1e-3) / 1e12
+    traffic_c3, prov_c3 = measured_traffic("flash_c3")
     res = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -593,13 +710,15 @@ def main():
                    "batch": C3["batch"], "seq_len": C3["seq"], "d_model": C3["dim"],
                    "heads": C3["heads"], "head_dim": C3["dim"] // C3["heads"], "parallelism": "none"},
         "frac_of_fp32_mfma_peak": round(value / FP32_MFMA_PEAK_TFLOPS, 4),
+        "selfcheck": {"rows": "sequence 0, rows 0-63, against float64 numpy", "tolerance": "1e-4 + 1e-3 |ref|",
+                      "max_abs_err": mha["selfcheck_max_abs_err"]},
         "tokens_per_s": round(C3["batch"] * C3["seq"] / (ms_per_step * 1e-3), 1),
         "kernels_ms": {"project_qkv_rope": round(mha["qkv_ms"], 4), "flash_sdpa": round(mha["flash_ms"], 4),
                        "out_proj": round(mha["out_ms"], 4), "step_events": round(mha["dev_ms"], 4)},
         "roofline": {"kernel": "flash_fwd_kernel (cdml_sdpa_fwd, c3)", "bound": "mfma",
                      "achieved": round(flash_tflops, 3), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(flash_tflops / FP32_MFMA_PEAK_TFLOPS, 4),
-                     "traffic": TRAFFIC_BYTES["flash_c3"],
+                     "traffic": traffic_c3, "traffic_provenance": prov_c3,
                      "algorithmic_per_launch": core},
         "device": {k: info[k] for k in ("name", "arch", "compute_units", "max_clock_mhz")},
     }
@@ -608,12 +727,13 @@ def main():
         dec = bench_decode(N, st, max(args.steps, 10), args.warmup)
         nbytes = decode_bytes(C4["batch"], C4["t"], C4["dim"])
         gbs = nbytes / (dec["ms"] * 1e-3) / 1e9
+        traffic_c4, prov_c4 = measured_traffic("decode_c4")
         res["decode"] = {"workload": "c4 decode step (B 64, KV 8192, 16 heads x 128)",
                          "ms": round(dec["ms"], 4), "tokens_per_s": round(C4["batch"] / (dec["ms"] * 1e-3), 1),
                          "roofline": {"kernel": "decode_split_kernel + decode_combine_vec_kernel", "bound": "hbm",
                                       "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                       "frac": round(gbs / HBM_PEAK_GBS, 4),
-                                      "traffic": TRAFFIC_BYTES["decode_c4"],
+                                      "traffic": traffic_c4, "traffic_provenance": prov_c4,
                                       "algorithmic_per_launch": nbytes}}
     if not args.no_extras:
         log("[bench] extras")

@@ -59,20 +59,42 @@ def build_hip(verbose: bool = False) -> str:
     return LIB
 
 
-def build_host(verbose: bool = False) -> str:
+# Host-code-only sanitizer build (g++; no GPU code is built with it): the
+# checked variant of the host module that tests load from _build/asan/.
+SANITIZE_FLAGS = ["-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined",
+                  "-fno-sanitize-recover=undefined"]
+SANITIZE_OUT = os.path.join(OUT, "asan")
+
+
+def build_host(verbose: bool = False, sanitize: bool = False) -> str:
+    """The pybind11 host module; with sanitize, an ASan + UBSan build of the
+    same sources into _build/asan/ (it needs libasan preloaded to import)."""
     import pybind11
 
     srcs = sorted(glob.glob(os.path.join(HOST, "*.cpp")))
     if not srcs:
         return ""
     ext = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
-    out = os.path.join(OUT, "_cdml_host" + ext)
+    out_dir = SANITIZE_OUT if sanitize else OUT
+    os.makedirs(out_dir, exist_ok=True)
+    out = os.path.join(out_dir, "_cdml_host" + ext)
     tmp = out + ".tmp"
-    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
-           "-I" + INCLUDE, "-I" + HOST, "-I" + pybind11.get_include(),
-           "-I" + sysconfig.get_paths()["include"], *srcs, "-o", tmp,
-           "-L" + OUT, "-lcdml_hip", "-Wl,-rpath,$ORIGIN"]
-    _run(cmd)
+    opt = SANITIZE_FLAGS if sanitize else ["-O2"]
+    rpath = "-Wl,-rpath,$ORIGIN/.." if sanitize else "-Wl,-rpath,$ORIGIN"
+    if sanitize:
+        # one object per source in parallel: the sanitized compile is slow
+        objs = [os.path.join(out_dir, os.path.basename(s)[:-4] + ".o") for s in srcs]
+        base = ["g++", *opt, "-std=c++17", "-fPIC", "-fvisibility=hidden", "-I" + INCLUDE, "-I" + HOST,
+                "-I" + pybind11.get_include(), "-I" + sysconfig.get_paths()["include"]]
+        with cf.ThreadPoolExecutor(min(len(srcs), os.cpu_count() or 4)) as ex:
+            for f in [ex.submit(_run, base + ["-c", s, "-o", o]) for s, o in zip(srcs, objs)]:
+                f.result()
+        _run(["g++", *opt, "-shared", *objs, "-o", tmp, "-L" + OUT, "-lcdml_hip", rpath])
+    else:
+        _run(["g++", *opt, "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
+              "-I" + INCLUDE, "-I" + HOST, "-I" + pybind11.get_include(),
+              "-I" + sysconfig.get_paths()["include"], *srcs, "-o", tmp,
+              "-L" + OUT, "-lcdml_hip", rpath])
     os.replace(tmp, out)
     if verbose:
         print("built", out)

@@ -14,7 +14,9 @@ import os
 import sys
 
 PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-BUILD = os.path.join(PKG, "_build")
+# CDML_HOST_BUILD selects another build directory of the same module (the
+# sanitizer build in _build/asan, which tests load under libasan).
+BUILD = os.environ.get("CDML_HOST_BUILD") or os.path.join(PKG, "_build")
 
 _mod = None
 

@@ -18,7 +18,9 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "_build", "librefcpu.so")
+# CDML_ORACLE_LIB selects another build of the same sources (the sanitizer
+# build, `make asan`, which tests load under libasan).
+_LIB_PATH = os.environ.get("CDML_ORACLE_LIB") or os.path.join(_HERE, "_build", "librefcpu.so")
 _lib = None
 
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
