@@ -13,11 +13,12 @@
 //                   softmax row reductions are in-lane plus one swap between
 //                   the two half-waves.
 //   online softmax  running max / sum per query in the exp2 domain
-//                   (scale * log2 e folded into one FMA), masked keys -inf.
+//                   (scale * log2 e folded into Q), masked keys -inf.
 //   O^T += V^T P^T  the probabilities stay in the S accumulator registers:
 //                   accumulator r of a lane holds key 8*(r/4) + 4*h + r%4,
 //                   exactly the key the B operand of MFMA step r needs, so
-//                   P is consumed in place; V^T comes from LDS (b32 reads).
+//                   P is consumed in place; V is staged transposed in LDS,
+//                   so one 16-byte read feeds four MFMA steps.
 //
 // Causal: tiles entirely above the diagonal are never loaded; a wave skips
 // MFMA work for its 32-key sub-blocks that lie wholly in its future; heavy
@@ -42,7 +43,7 @@ struct FlashArgs {
   int ldq, ldk, ldv, ldo;
   int lq, lk, heads, hd;
   float scale_log2;
-  int n_qt, n_bh, total, padded;
+  int n_qt, n_bh, n_items;  // query tiles per sequence, (sequence, head) pairs, n_bh * n_qt
 };
 
 // Stages one BN x HD tile of K or V (rows [k0, k0+BN) of head column block
@@ -59,7 +60,7 @@ struct KvStage {
   static constexpr int NS = BN * HD / FA_THREADS;
   vf4 r[VEC ? NV : 1];  // a native vector, so the prefetch stays a register load issued at the loop top
   float s[VEC ? 1 : NS];
-  uint32_t off[VEC ? NV : 1];  // element offsets of this thread's rows in a tile
+  uint32_t off[VEC ? NV : 1];  // byte offsets of this thread's rows in a tile
   int col;
 
   __device__ __forceinline__ void init(int ld) {
@@ -67,15 +68,17 @@ struct KvStage {
       const int t = threadIdx.x;
       col = (t % F4_ROW) * 4;
 #pragma unroll
-      for (int i = 0; i < NV; ++i) off[i] = (uint32_t)((t / F4_ROW + ROWS_PER_PASS * i) * ld + col);
+      for (int i = 0; i < NV; ++i) off[i] = 4u * (uint32_t)((t / F4_ROW + ROWS_PER_PASS * i) * ld + col);
     }
   }
 
   __device__ __forceinline__ void load(const float *__restrict__ base, int ld, int k0, int lk,
                                        int hd) {
     if constexpr (VEC) {
-      const float *tile = base + (size_t)k0 * ld;  // wave-uniform
-      const uint32_t lim = (uint32_t)(min(lk - 1 - k0, BN - 1) * ld) + col;
+      // wave-uniform tile base plus a 32-bit per-lane byte offset (one
+      // scalar-base global load per row, no 64-bit address arithmetic)
+      const char *tile = reinterpret_cast<const char *>(base + (size_t)k0 * ld);
+      const uint32_t lim = 4u * ((uint32_t)(min(lk - 1 - k0, BN - 1) * ld) + col);
 #pragma unroll
       for (int i = 0; i < NV; ++i) r[i] = *reinterpret_cast<const vf4 *>(tile + min(off[i], lim));
     } else {
@@ -106,12 +109,89 @@ struct KvStage {
   }
 };
 
+// Stages one BN x HD tile of V transposed into LDS, Vt[d][key] with row pitch
+// BN + 4, so that the P.V step reads the four consecutive keys of one V^T
+// column it needs for four MFMA steps in a single 16-byte read.  A thread
+// takes two consecutive keys of a 4-wide column group (two 16-byte global
+// loads of adjacent lanes' contiguous row slices) and writes them as four
+// 8-byte pairs Vt[c + j][2p .. 2p + 1].  Rows past lk are clamped as in
+// KvStage.
+template <int HD, int BN, bool VEC>
+struct VtStage {
+  static constexpr int NCG = HD / 4;               // 4-wide column groups
+  static constexpr int NU = BN / 2 * NCG / FA_THREADS;  // (key pair, column group) units per thread
+  static constexpr int NS = BN * HD / FA_THREADS;
+  static_assert(BN / 2 * NCG % FA_THREADS == 0, "V tile units must divide the workgroup");
+  vf4 r[VEC ? 2 * NU : 1];
+  float s[VEC ? 1 : NS];
+  uint32_t off[VEC ? NU : 1];  // byte offset of each unit's first row in a tile
+  int col[VEC ? NU : 1];
+
+  __device__ __forceinline__ void init(int ld) {
+    if constexpr (VEC) {
+#pragma unroll
+      for (int i = 0; i < NU; ++i) {
+        const int u = threadIdx.x + FA_THREADS * i;
+        col[i] = (u % NCG) * 4;
+        off[i] = 4u * (uint32_t)(2 * (u / NCG) * ld + col[i]);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void load(const float *__restrict__ base, int ld, int k0, int lk,
+                                       int hd) {
+    if constexpr (VEC) {
+      const char *tile = reinterpret_cast<const char *>(base + (size_t)k0 * ld);
+      const uint32_t last = (uint32_t)min(lk - 1 - k0, BN - 1) * (uint32_t)ld;
+      const uint32_t row = 4u * (uint32_t)ld;
+#pragma unroll
+      for (int i = 0; i < NU; ++i) {
+        const uint32_t lim = 4u * (last + col[i]);
+        r[2 * i] = *reinterpret_cast<const vf4 *>(tile + min(off[i], lim));
+        r[2 * i + 1] = *reinterpret_cast<const vf4 *>(tile + min(off[i] + row, lim));
+      }
+    } else {
+      const int t = threadIdx.x;
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        const int e = t + FA_THREADS * i;
+        const int rw = e / HD, c = e % HD;
+        const int key = k0 + rw;
+        s[i] = (key < lk && c < hd) ? base[(size_t)key * ld + c] : 0.f;
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(float (*lds)[BN + 4]) {
+    if constexpr (VEC) {
+#pragma unroll
+      for (int i = 0; i < NU; ++i) {
+        const int u = threadIdx.x + FA_THREADS * i;
+        const int kp = 2 * (u / NCG);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          typedef float vf2 __attribute__((ext_vector_type(2)));
+          *reinterpret_cast<vf2 *>(&lds[col[i] + j][kp]) = vf2{r[2 * i][j], r[2 * i + 1][j]};
+        }
+      }
+    } else {
+      const int t = threadIdx.x;
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        const int e = t + FA_THREADS * i;
+        lds[e % HD][e / HD] = s[i];
+      }
+    }
+  }
+};
+
 // max / sum of a value over the two half-waves (lanes l and l ^ 32) with
 // v_permlane32_swap: both results hold the value of lane l % 32 and of lane
 // l % 32 + 32.
 __device__ __forceinline__ float halves_max(float x) {
+#pragma float_control(precise, off)
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));  // scores: no signalling NaN
 }
 __device__ __forceinline__ float halves_sum(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -134,243 +214,303 @@ constexpr float kRescaleThreshold = 8.0f;
 // lane of half-wave h: 8 * (r / 4) + 4 * h + r % 4 (the 32x32 MFMA D layout).
 __device__ __forceinline__ constexpr int acc_key(int r) { return 8 * (r >> 2) + (r & 3); }
 
-template <int HD, int BN, bool CAUSAL, bool HAS_MASK, bool VEC, bool PAIR>
+// Which query tiles a workgroup runs, one after the other.  Item i of a
+// launch is (sequence, head) i % n_bh and, under the causal rule, query tile
+// n_qt - 1 - i / n_bh (heaviest rows first), else tile i / n_bh.
+//  * kOne: workgroup i runs item i.  With workgroup i on XCD i % 8, all tiles
+//    of one (sequence, head) share an XCD and its L2 whenever n_bh is a
+//    multiple of 8, and every XCD receives the heaviest tiles first (a
+//    near-optimal greedy schedule for a launch of several rounds).
+//  * kPair (causal launches that fit in one round): workgroup i runs tiles
+//    n_qt - 1 - p and p of its (sequence, head), p = i / n_bh, so every
+//    workgroup has the same work (n_qt + 1 key tiles; the middle tile of an
+//    odd count runs alone) and the round finishes together.
+// The last key tile of a workgroup's first item prefetches the first key tile
+// and the Q rows of the second.
+enum { kOne = 0, kPair = 1 };
+
+struct Item {
+  int bh, qt;
+};
+
+template <bool CAUSAL, int SCHED>
+__device__ __forceinline__ bool item_at(const FlashArgs &a, int k, Item &it) {
+  const int i = blockIdx.x;
+  if (SCHED == kPair) {
+    const int slot = i / a.n_bh;
+    it.bh = i % a.n_bh;
+    if (k == 0) it.qt = a.n_qt - 1 - slot;
+    else if (k == 1 && 2 * slot + 1 != a.n_qt) it.qt = slot;
+    else return false;
+    return true;
+  } else if (k > 0) {
+    return false;
+  }
+  it.bh = i % a.n_bh;
+  const int slot = i / a.n_bh;
+  it.qt = CAUSAL ? a.n_qt - 1 - slot : slot;
+  return true;
+}
+
+// Q^T operand of a wave: register 4u + r holds q[qi][8u + 4*hf + r] (rows
+// past lq read as 0), not yet scaled.
+template <int HD, bool VEC>
+__device__ __forceinline__ void load_q(float (&qreg)[HD / 2], const FlashArgs &a, int b, int col0, int qi,
+                                       int hf) {
+  const float *qrow = a.q + ((size_t)b * a.lq + min(qi, a.lq - 1)) * a.ldq + col0;
+  const bool qok = qi < a.lq;
+#pragma unroll
+  for (int u = 0; u < HD / 8; ++u) {
+    const int d = 8 * u + 4 * hf;
+    if constexpr (VEC) {
+      const vf4 t4 = *reinterpret_cast<const vf4 *>(qrow + d);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) qreg[4 * u + r] = qok ? t4[r] : 0.f;
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) qreg[4 * u + r] = (qok && d + r < a.hd) ? qrow[d + r] : 0.f;
+    }
+  }
+}
+
+template <int HD, int BN, bool CAUSAL, bool HAS_MASK, bool VEC, int SCHED>
 __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArgs a) {
   constexpr int NKB = BN / 32;   // 32-key sub-blocks per tile
   constexpr int NDB = HD / 32;   // 32-wide head-dim blocks of O^T
   constexpr int NQ = HD / 2;     // MFMA k-steps of Q.K
   constexpr int NKG = HD / 8;    // float4 groups of a K row slice
   constexpr int VCH = HD <= 32 ? 16 : 8;  // P.V steps whose V operands are read at once
+  constexpr int NVG = VCH / 4;            // 16-byte V^T reads per chunk and head-dim block
   __shared__ __attribute__((aligned(16))) float Ks[2][BN][HD + 4];
-  __shared__ __attribute__((aligned(16))) float Vs[2][BN][HD + 4];
-
-  // Workgroup i takes (sequence, head) i % n_bh, so with workgroup i on XCD
-  // i % 8 all tiles of one (sequence, head) share an XCD and its L2 whenever
-  // n_bh is a multiple of 8.  Under the causal rule query tile t sees t + 1
-  // key tiles:
-  //  * slot p = i / n_bh is tile n_qt - 1 - p, counted from the longest row
-  //    down, so every XCD receives the heaviest tiles first and the lightest
-  //    last (a near-optimal greedy schedule when the launch spans several
-  //    rounds of resident workgroups);
-  //  * with PAIR (a launch that fits in one round), slot p runs the pair of
-  //    tiles n_qt - 1 - p and p one after the other, so every workgroup has
-  //    the same work (n_qt + 1 key tiles; the middle tile of an odd count
-  //    runs alone) and the round finishes together.
-  // Without the causal rule slot p is tile p.
-  const int lid = blockIdx.x;
-  const int n_bh = a.n_bh;
-  const int bh = lid % n_bh;
-  const int slot = lid / n_bh;
-  const int npass = (PAIR && 2 * slot + 1 != a.n_qt) ? 2 : 1;
-  const int b = bh / a.heads, h = bh % a.heads;
-  for (int pass = 0; pass < npass; ++pass) {
-  if (pass > 0) __syncthreads();  // the LDS tiles of the first pass are done with
-  const int qt = CAUSAL ? (pass == 0 ? a.n_qt - 1 - slot : slot) : slot;
-  const int q0 = qt * FA_BM;
+  __shared__ __attribute__((aligned(16))) float Vt[2][HD][BN + 4];  // V transposed
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = lane & 31, hf = lane >> 5;
-  const int qw0 = q0 + wave * 32;   // first query of this wave (wave-uniform)
-  const int qi = qw0 + li;          // this lane's query
-  const int col0 = h * a.hd;
 
-  const float *__restrict__ kbase = a.k + (size_t)b * a.lk * a.ldk + col0;
-  const float *__restrict__ vbase = a.v + (size_t)b * a.lk * a.ldv + col0;
+  KvStage<HD, BN, VEC> sk;
+  VtStage<HD, BN, VEC> sv;
+  sk.init(a.ldk);
+  sv.init(a.ldv);
 
-  // Q^T operand: register 4u + r holds q[qi][8u + 4*hf + r].
+  // The first item: its Q rows and first key tile.
+  Item it;
+  item_at<CAUSAL, SCHED>(a, 0, it);
   float qreg[NQ];
   {
-    const float *qrow = a.q + ((size_t)b * a.lq + min(qi, a.lq - 1)) * a.ldq + col0;
-    const bool qok = qi < a.lq;
-#pragma unroll
-    for (int u = 0; u < HD / 8; ++u) {
-      const int d = 8 * u + 4 * hf;
-      if constexpr (VEC) {
-        float4 t4 = *reinterpret_cast<const float4 *>(qrow + d);
-        qreg[4 * u + 0] = qok ? t4.x : 0.f;
-        qreg[4 * u + 1] = qok ? t4.y : 0.f;
-        qreg[4 * u + 2] = qok ? t4.z : 0.f;
-        qreg[4 * u + 3] = qok ? t4.w : 0.f;
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) qreg[4 * u + r] = (qok && d + r < a.hd) ? qrow[d + r] : 0.f;
-      }
-    }
+    const int b = it.bh / a.heads, col0 = (it.bh % a.heads) * a.hd;
+    load_q<HD, VEC>(qreg, a, b, col0, it.qt * FA_BM + wave * 32 + li, hf);
+    sk.load(a.k + (size_t)b * a.lk * a.ldk + col0, a.ldk, 0, a.lk, a.hd);
+    sv.load(a.v + (size_t)b * a.lk * a.ldv + col0, a.ldv, 0, a.lk, a.hd);
+  }
+  sk.store(Ks[0]);
+  sv.store(Vt[0]);
+  __syncthreads();
+  int buf = 0;  // LDS buffer holding the current key tile
+
+  for (int k = 0;; ++k) {
+    const int b = it.bh / a.heads, h = it.bh % a.heads;
+    const int q0 = it.qt * FA_BM;
+    const int qw0 = q0 + wave * 32;   // first query of this wave (wave-uniform)
+    const int qi = qw0 + li;          // this lane's query
+    const int col0 = h * a.hd;
+    const float *__restrict__ kbase = a.k + (size_t)b * a.lk * a.ldk + col0;
+    const float *__restrict__ vbase = a.v + (size_t)b * a.lk * a.ldv + col0;
+
     // Q in the exp2 domain: the scores leave the MFMA as s * scale * log2(e)
 #pragma unroll
     for (int i = 0; i < NQ; ++i) qreg[i] *= a.scale_log2;
-  }
 
-  const int kend = CAUSAL ? min(q0 + FA_BM, a.lk) : a.lk;
-  const int n_kt = (kend + BN - 1) / BN;
+    Item nx = it;
+    const bool has_next = item_at<CAUSAL, SCHED>(a, k + 1, nx);
+    const int nb = nx.bh / a.heads, ncol0 = (nx.bh % a.heads) * a.hd;  // used only with has_next
 
-  KvStage<HD, BN, VEC> sk, sv;
-  sk.init(a.ldk);
-  sv.init(a.ldv);
-  sk.load(kbase, a.ldk, 0, a.lk, a.hd);
-  sv.load(vbase, a.ldv, 0, a.lk, a.hd);
-  sk.store(Ks[0]);
-  sv.store(Vs[0]);
-  __syncthreads();
+    const int kend = CAUSAL ? min(q0 + FA_BM, a.lk) : a.lk;
+    const int n_kt = (kend + BN - 1) / BN;
 
-  floatx16 oacc[NDB];
+    floatx16 oacc[NDB];
 #pragma unroll
-  for (int db = 0; db < NDB; ++db)
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
-  // The reference max of this lane's query (exp2 domain) is subtracted by
-  // the MFMA itself: the first step of every S^T block starts from negm,
-  // -m_run in all 16 entries (0 until the first visible key sets m_run), so
-  // the scores come out relative to the reference and p = exp2(score).
-  float m_run = -INFINITY;
-  float thr = -INFINITY;  // rescale threshold: any visible key until m_run is set
-  float l_a = 0.f, l_b = 0.f;  // running sums over this half-wave's keys
-  floatx16 negm = {};
-  // Last key this lane may attend (the causal diagonal and the sequence end).
-  const int key_last = CAUSAL ? min(qi, a.lk - 1) : a.lk - 1;
+      for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
+    // The reference max of this lane's query (exp2 domain) is subtracted by
+    // the MFMA itself: the first step of every S^T block starts from negm,
+    // -m_run in all 16 entries (0 until the first visible key sets m_run), so
+    // the scores come out relative to the reference and p = exp2(score).
+    float m_run = -INFINITY;
+    float thr = -INFINITY;  // rescale threshold: any visible key until m_run is set
+    float l_a = 0.f, l_b = 0.f;  // running sums over this half-wave's keys
+    floatx16 negm = {};
+    // Last key this lane may attend (the causal diagonal and the sequence end).
+    const int key_last = CAUSAL ? min(qi, a.lk - 1) : a.lk - 1;
 
-  const uint8_t *mrow = HAS_MASK ? a.mask + (size_t)min(qi, a.lq - 1) * a.lk : nullptr;
+    const uint8_t *mrow = HAS_MASK ? a.mask + (size_t)min(qi, a.lq - 1) * a.lk : nullptr;
 
-  for (int kt = 0; kt < n_kt; ++kt) {
-    const int cur = kt & 1;
-    const int k0 = kt * BN;
-    const bool more = kt + 1 < n_kt;
-    // Next tile into registers.  The last iteration re-stages its own tile
-    // into the idle buffer (nobody reads it again): an unconditional stage
-    // keeps the staging registers out of scratch memory.
-    sk.load(kbase, a.ldk, more ? k0 + BN : k0, a.lk, a.hd);
-    sv.load(vbase, a.ldv, more ? k0 + BN : k0, a.lk, a.hd);
-
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-      const int kb0 = k0 + kb * 32;
-      // A sub-block wholly past the sequence end or in this wave's future
-      // contributes nothing (every probability would be 0): skip it.
-      if (kb0 >= a.lk || (CAUSAL && kb0 > qw0 + 31)) continue;
-      const float(*krow)[HD + 4] = &Ks[cur][kb * 32];
-      const float(*vrow)[HD + 4] = &Vs[cur][kb * 32];
-
-      // S^T = K Q^T; the K operand group u + 1 is read while group u multiplies.
-      floatx16 sacc;
-      float4 kcur = *reinterpret_cast<const float4 *>(&krow[li][4 * hf]);
-#pragma unroll
-      for (int u = 0; u < NKG; ++u) {
-        float4 knext;
-        if (u + 1 < NKG) knext = *reinterpret_cast<const float4 *>(&krow[li][8 * (u + 1) + 4 * hf]);
-        sacc = mfma32x32x2(kcur.x, qreg[4 * u + 0], u == 0 ? negm : sacc);
-        sacc = mfma32x32x2(kcur.y, qreg[4 * u + 1], sacc);
-        sacc = mfma32x32x2(kcur.z, qreg[4 * u + 2], sacc);
-        sacc = mfma32x32x2(kcur.w, qreg[4 * u + 3], sacc);
-        if (u + 1 < NKG) kcur = knext;
+    for (int kt = 0; kt < n_kt; ++kt) {
+      const int cur = buf;
+      const int k0 = kt * BN;
+      const bool last = kt + 1 == n_kt;
+      // Next tile into registers: this item's next tile, else the next
+      // item's first tile.  Without a next item the last iteration re-stages
+      // its own tile into the idle buffer (nobody reads it again): an
+      // unconditional stage keeps the staging registers out of scratch memory.
+      {
+        const bool to_next = last && has_next;
+        const int ks = !last ? k0 + BN : (has_next ? 0 : k0);
+        sk.load(to_next ? a.k + (size_t)nb * a.lk * a.ldk + ncol0 : kbase, a.ldk, ks, a.lk, a.hd);
+        sv.load(to_next ? a.v + (size_t)nb * a.lk * a.ldv + ncol0 : vbase, a.ldv, ks, a.lk, a.hd);
       }
-      // V^T operands of the first P.V chunk, in flight during the softmax.
-      float vr[VCH][NDB];
-#pragma unroll
-      for (int st = 0; st < VCH; ++st)
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) vr[st][db] = vrow[acc_key(st) + 4 * hf][db * 32 + li];
+      bool q_next = false;  // the next item's Q rows are loading
 
-      // Masking (wave-uniform decision): the diagonal, the sequence end, a mask.
-      if (HAS_MASK || kb0 + 31 > (CAUSAL ? min(qw0, a.lk - 1) : a.lk - 1)) {
-        const int last_vis = key_last - kb0 - 4 * hf;  // last visible offset for this lane
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          bool ok = acc_key(r) <= last_vis;
-          if (HAS_MASK) {
-            const int key = min(kb0 + acc_key(r) + 4 * hf, a.lk - 1);
-            ok = ok && qi < a.lq && mrow[key] != 0;
+      for (int kb = 0; kb < NKB; ++kb) {
+        const int kb0 = k0 + kb * 32;
+        // A sub-block wholly past the sequence end or in this wave's future
+        // contributes nothing (every probability would be 0): skip it.
+        if (kb0 >= a.lk || (CAUSAL && kb0 > qw0 + 31)) continue;
+        const float(*krow)[HD + 4] = &Ks[cur][kb * 32];
+        const float(*vtc)[BN + 4] = Vt[cur];  // this sub-block's keys start at column kb * 32
+
+        // S^T = K Q^T; the K operand group u + 1 is read while group u multiplies.
+        floatx16 sacc;
+        float4 kcur = *reinterpret_cast<const float4 *>(&krow[li][4 * hf]);
+#pragma unroll
+        for (int u = 0; u < NKG; ++u) {
+          float4 knext;
+          if (u + 1 < NKG) knext = *reinterpret_cast<const float4 *>(&krow[li][8 * (u + 1) + 4 * hf]);
+          sacc = mfma32x32x2(kcur.x, qreg[4 * u + 0], u == 0 ? negm : sacc);
+          sacc = mfma32x32x2(kcur.y, qreg[4 * u + 1], sacc);
+          sacc = mfma32x32x2(kcur.z, qreg[4 * u + 2], sacc);
+          sacc = mfma32x32x2(kcur.w, qreg[4 * u + 3], sacc);
+          if (u + 1 < NKG) kcur = knext;
+        }
+        // Q is last read by the final sub-block of the last tile: the next
+        // item's Q rows load while this sub-block's softmax and P.V run.
+        if (kb == NKB - 1 && last && has_next) {
+          load_q<HD, VEC>(qreg, a, nb, ncol0, nx.qt * FA_BM + wave * 32 + li, hf);
+          q_next = true;
+        }
+        // V^T operands of the first P.V chunk, in flight during the softmax: steps
+        // 4g .. 4g + 3 take keys 8g + 4h .. 8g + 4h + 3 of column db * 32 + li.
+        vf4 vr[NVG][NDB];
+#pragma unroll
+        for (int g = 0; g < NVG; ++g)
+#pragma unroll
+          for (int db = 0; db < NDB; ++db)
+            vr[g][db] = *reinterpret_cast<const vf4 *>(&vtc[db * 32 + li][kb * 32 + 8 * g + 4 * hf]);
+
+        // Masking (wave-uniform decision): the diagonal, the sequence end, a mask.
+        if (HAS_MASK || kb0 + 31 > (CAUSAL ? min(qw0, a.lk - 1) : a.lk - 1)) {
+          const int last_vis = key_last - kb0 - 4 * hf;  // last visible offset for this lane
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            bool ok = acc_key(r) <= last_vis;
+            if (HAS_MASK) {
+              const int key = min(kb0 + acc_key(r) + 4 * hf, a.lk - 1);
+              ok = ok && qi < a.lq && mrow[key] != 0;
+            }
+            sacc[r] = ok ? sacc[r] : -INFINITY;
           }
-          sacc[r] = ok ? sacc[r] : -INFINITY;
         }
-      }
-      // tile max relative to the reference (-inf: no visible key)
-      float smax = max3_scores(sacc[0], sacc[1], sacc[2]);
-#pragma unroll
-      for (int r = 3; r < 15; r += 2) smax = max3_scores(smax, sacc[r], sacc[r + 1]);
-      smax = max3_scores(smax, sacc[15], -INFINITY);
-      smax = halves_max(smax);
+        // tile max relative to the reference (-inf: no visible key)
+        // (a tree of depth 3: eight v_max3 whose inputs do not wait on each other)
+        const float m0 = max3_scores(sacc[0], sacc[1], sacc[2]);
+        const float m1 = max3_scores(sacc[3], sacc[4], sacc[5]);
+        const float m2 = max3_scores(sacc[6], sacc[7], sacc[8]);
+        const float m3 = max3_scores(sacc[9], sacc[10], sacc[11]);
+        const float m4 = max3_scores(sacc[12], sacc[13], sacc[14]);
+        float smax = max3_scores(max3_scores(m0, m1, m2), max3_scores(m3, m4, sacc[15]), -INFINITY);
+        smax = halves_max(smax);
 
-      // Lazy rescale: the first visible key sets the reference, later only a
-      // rise of more than the threshold moves it (the scores shift with it).
-      const bool need = smax > thr;
-      if (__builtin_amdgcn_ballot_w64(need)) {
-        const bool first = m_run == -INFINITY;
-        const float shift = need ? smax : 0.f;
-        const float alpha = (need && !first) ? fast_exp2(-smax) : 1.0f;  // o and l are 0 before the first key
-        m_run = need ? (first ? smax : m_run + smax) : m_run;
-        thr = m_run == -INFINITY ? -INFINITY : kRescaleThreshold;
-        l_a *= alpha;
-        l_b *= alpha;
-        const float nref = m_run == -INFINITY ? 0.f : -m_run;
+        // Lazy rescale: the first visible key sets the reference, later only a
+        // rise of more than the threshold moves it (the scores shift with it).
+        const bool need = smax > thr;
+        if (__builtin_amdgcn_ballot_w64(need)) {
+          const bool first = m_run == -INFINITY;
+          const float shift = need ? smax : 0.f;
+          const float alpha = (need && !first) ? fast_exp2(-smax) : 1.0f;  // o and l are 0 before the first key
+          m_run = need ? (first ? smax : m_run + smax) : m_run;
+          thr = m_run == -INFINITY ? -INFINITY : kRescaleThreshold;
+          const float nref = m_run == -INFINITY ? 0.f : -m_run;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            sacc[r] -= shift;
+            negm[r] = nref;
+          }
+          if (__builtin_amdgcn_ballot_w64(need && !first)) {  // not at a row's first visible key
+            l_a *= alpha;
+            l_b *= alpha;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+          }
+        }
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          sacc[r] -= shift;
-          negm[r] = nref;
+          const float p = fast_exp2(sacc[r]);
+          sacc[r] = p;
+          if (r & 1) l_b += p;
+          else l_a += p;
         }
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(sacc[r]);
-        sacc[r] = p;
-        if (r & 1) l_b += p;
-        else l_a += p;
-      }
 
-      // O^T += V^T P^T: accumulator r of the lane holds the probability of
-      // key acc_key(r) + 4*hf, the key B-operand slot of MFMA step r needs.
+        // O^T += V^T P^T: accumulator r of the lane holds the probability of
+        // key acc_key(r) + 4*hf, the key B-operand slot of MFMA step r needs.
 #pragma unroll
-      for (int ch = 0; ch < 16 / VCH; ++ch) {
-        if (ch > 0) {
+        for (int ch = 0; ch < 16 / VCH; ++ch) {
+          if (ch > 0) {
+#pragma unroll
+            for (int g = 0; g < NVG; ++g)
+#pragma unroll
+              for (int db = 0; db < NDB; ++db)
+                vr[g][db] = *reinterpret_cast<const vf4 *>(
+                    &vtc[db * 32 + li][kb * 32 + 8 * (ch * NVG + g) + 4 * hf]);
+          }
 #pragma unroll
           for (int st = 0; st < VCH; ++st)
 #pragma unroll
             for (int db = 0; db < NDB; ++db)
-              vr[st][db] = vrow[acc_key(ch * VCH + st) + 4 * hf][db * 32 + li];
-        }
-#pragma unroll
-        for (int st = 0; st < VCH; ++st)
-#pragma unroll
-          for (int db = 0; db < NDB; ++db) oacc[db] = mfma32x32x2(vr[st][db], sacc[ch * VCH + st], oacc[db]);
-      }
-    }
-
-    sk.store(Ks[cur ^ 1]);
-    sv.store(Vs[cur ^ 1]);
-    __syncthreads();
-  }
-
-  // Normalise and store: lane holds query qi, dims db*32 + 8*(r/4) + 4*hf + r%4.
-  const float l_tot = halves_sum(l_a + l_b);
-  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-  // For the backward pass: p = exp2(s * scale * log2(e) - lse) recovers every
-  // probability (+inf for a row with no visible key, whose p are all 0).
-  if (a.lse && hf == 0 && qi < a.lq)
-    a.lse[(size_t)bh * a.lq + qi] = l_tot > 0.f ? m_run + __log2f(l_tot) : INFINITY;
-  if (qi < a.lq) {
-    float *orow = a.o + ((size_t)b * a.lq + qi) * a.ldo + col0;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d = db * 32 + 8 * g + 4 * hf;
-        if constexpr (VEC) {
-          *reinterpret_cast<float4 *>(orow + d) =
-              make_float4(oacc[db][4 * g] * inv, oacc[db][4 * g + 1] * inv,
-                          oacc[db][4 * g + 2] * inv, oacc[db][4 * g + 3] * inv);
-        } else {
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (d + r < a.hd) orow[d + r] = oacc[db][4 * g + r] * inv;
+              oacc[db] = mfma32x32x2(vr[st / 4][db][st % 4], sacc[ch * VCH + st], oacc[db]);
         }
       }
+      // a wave that skipped the final sub-block loads the next Q rows here
+      if (last && has_next && !q_next) load_q<HD, VEC>(qreg, a, nb, ncol0, nx.qt * FA_BM + wave * 32 + li, hf);
+
+      sk.store(Ks[cur ^ 1]);
+      sv.store(Vt[cur ^ 1]);
+      __syncthreads();
+      buf = cur ^ 1;
     }
+
+    // Normalise and store: lane holds query qi, dims db*32 + 8*(r/4) + 4*hf + r%4.
+    const float l_tot = halves_sum(l_a + l_b);
+    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+    // For the backward pass: p = exp2(s * scale * log2(e) - lse) recovers every
+    // probability (+inf for a row with no visible key, whose p are all 0).
+    if (a.lse && hf == 0 && qi < a.lq)
+      a.lse[(size_t)it.bh * a.lq + qi] = l_tot > 0.f ? m_run + __log2f(l_tot) : INFINITY;
+    if (qi < a.lq) {
+      float *orow = a.o + ((size_t)b * a.lq + qi) * a.ldo + col0;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d = db * 32 + 8 * g + 4 * hf;
+          if constexpr (VEC) {
+            *reinterpret_cast<float4 *>(orow + d) =
+                make_float4(oacc[db][4 * g] * inv, oacc[db][4 * g + 1] * inv,
+                            oacc[db][4 * g + 2] * inv, oacc[db][4 * g + 3] * inv);
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (d + r < a.hd) orow[d + r] = oacc[db][4 * g + r] * inv;
+          }
+        }
+      }
+    }
+    if (!has_next) break;
+    it = nx;
   }
-  }  // pass
 }
 
 // Head dims above 128: one workgroup per (sequence, head, query), keys in
@@ -434,27 +574,27 @@ __global__ void __launch_bounds__(256) flash_generic_kernel(const FlashArgs a, i
   for (int d = t; d < a.hd; d += 256) orow[d] = ov[d] * inv;
 }
 
-template <int HD, int BN, bool CAUSAL, bool HAS_MASK>
-void launch_tpl(FlashArgs a, bool vec, hipStream_t st) {
+template <int HD, int BN, bool CAUSAL, bool HAS_MASK, bool VEC>
+void launch_sched(const FlashArgs &a, hipStream_t st) {
   // Pairs of causal tiles when one tile per workgroup would fit in a single
   // round of resident workgroups (four per CU), so that the round lasts as
   // long as its longest tile, and the pairs still give every CU two
   // workgroups (fewer would leave SIMDs with a single wave).
-  const long long cus = num_cus();
-  const bool pair = CAUSAL && a.n_qt > 1 && (long long)a.n_bh * a.n_qt <= 4 * cus &&
-                    (long long)a.n_bh * ((a.n_qt + 1) / 2) >= 2 * cus;
-  a.total = pair ? a.n_bh * ((a.n_qt + 1) / 2) : a.n_bh * a.n_qt;
   if constexpr (CAUSAL) {
-    if (pair) {
-      if (vec) flash_fwd_kernel<HD, BN, true, HAS_MASK, true, true><<<dim3(a.total), dim3(FA_THREADS), 0, st>>>(a);
-      else flash_fwd_kernel<HD, BN, true, HAS_MASK, false, true><<<dim3(a.total), dim3(FA_THREADS), 0, st>>>(a);
+    const long long cus = num_cus();
+    if (a.n_qt > 1 && (long long)a.n_items <= 4 * cus && (long long)a.n_bh * ((a.n_qt + 1) / 2) >= 2 * cus) {
+      flash_fwd_kernel<HD, BN, CAUSAL, HAS_MASK, VEC, kPair>
+          <<<dim3(a.n_bh * ((a.n_qt + 1) / 2)), dim3(FA_THREADS), 0, st>>>(a);
       return;
     }
   }
-  if (vec)
-    flash_fwd_kernel<HD, BN, CAUSAL, HAS_MASK, true, false><<<dim3(a.total), dim3(FA_THREADS), 0, st>>>(a);
-  else
-    flash_fwd_kernel<HD, BN, CAUSAL, HAS_MASK, false, false><<<dim3(a.total), dim3(FA_THREADS), 0, st>>>(a);
+  flash_fwd_kernel<HD, BN, CAUSAL, HAS_MASK, VEC, kOne><<<dim3(a.n_items), dim3(FA_THREADS), 0, st>>>(a);
+}
+
+template <int HD, int BN, bool CAUSAL, bool HAS_MASK>
+void launch_tpl(const FlashArgs &a, bool vec, hipStream_t st) {
+  if (vec) launch_sched<HD, BN, CAUSAL, HAS_MASK, true>(a, st);
+  else launch_sched<HD, BN, CAUSAL, HAS_MASK, false>(a, st);
 }
 
 template <int HD, int BN>
@@ -514,8 +654,7 @@ int flash_forward(const float *q, int ldq, const float *k, int ldk, const float 
   a.n_bh = batch * num_heads;
   long long total = (long long)batch * num_heads * a.n_qt;
   if (total > (1LL << 30)) return fail(CDML_E_INVALID, "cdml_sdpa_fwd: problem too large");
-  a.total = (int)total;
-  a.padded = pad_to_xcd(a.total);
+  a.n_items = (int)total;
   if (hd_pad == 32) launch_hd<32, 64>(a, causal, vec, st);
   else if (hd_pad == 64) launch_hd<64, 32>(a, causal, vec, st);
   else launch_hd<128, 32>(a, causal, vec, st);

@@ -3,6 +3,7 @@ come from.  Run on the GPU box from the repository root, after the library is
 built:
 
     python3 profile_bench.py [--passes trace,traffic,counters,backward,probe] [--out DIR]
+                             [--profiles-dir DIR]
 
 Each pass runs `rocprofv3 ... -- python3 bench.py ...` (or the probe) as a
 child process under `timeout -s KILL`; the first pass that fails ends the
@@ -293,10 +294,15 @@ def pass_probe(out):
 
 
 def main():
+    global PROFILES
     ap = argparse.ArgumentParser()
     ap.add_argument("--passes", default=",".join(PASSES))
     ap.add_argument("--out", default=os.path.join(ROOT, "gpurun_out", "profile_bench"))
+    ap.add_argument("--profiles-dir", default=PROFILES,
+                    help="where the summaries go (default profiles/)")
     a = ap.parse_args()
+    PROFILES = os.path.abspath(a.profiles_dir)
+    os.makedirs(PROFILES, exist_ok=True)
     passes = [p for p in a.passes.split(",") if p]
     bad = set(passes) - set(PASSES)
     if bad:

@@ -432,6 +432,54 @@ def test_sdpa_baseline_configs_sampled(name, B, L, D, H):
         parity(got[s], O.sdpa(q[s], k[s], v[s], H, causal=True, mt=True), f"{name} seq {b}")
 
 
+@pytest.mark.parametrize("B,L,D,H,causal,masked", [
+    (64, 300, 256, 8, True, False),   # d_h 32: 3 ragged query tiles, 1536 workgroups
+    (64, 200, 256, 8, False, True),   # d_h 32, explicit mask, no causal rule
+    (40, 257, 512, 8, True, False),   # d_h 64, 960 tiles: paired (3 tiles: the middle one alone)
+    (32, 512, 256, 8, True, False),   # d_h 32, 1024 tiles: paired, two per workgroup
+    (600, 64, 96, 3, True, False),    # d_h 32, one tile per sequence
+])
+def test_sdpa_every_sequence_of_large_launches(B, L, D, H, causal, masked):
+    """Launches of many query tiles, every sequence checked against the oracle.
+    The paired cases run two causal tiles per workgroup, the second's Q rows
+    and first key tile prefetched during the first's last key tile.  The row
+    statistics of cdml_sdpa_fwd_lse (log2 of each row's softmax normaliser in
+    the exp2(s * scale * log2 e) domain) are checked against float64, and its
+    output must equal cdml_sdpa_fwd's bit for bit."""
+    hd = D // H
+    q, k, v = (synth.normal(B + L + i, (B * L, D)) for i in range(3))
+    mask = synth.periodic_mask(L, L) if masked else None
+    got = G.sdpa(q, k, v, H, mask=mask, causal=causal, batch=B)
+    for b in range(B):
+        s = slice(b * L, (b + 1) * L)
+        parity(got[s], O.sdpa(q[s], k[s], v[s], H, mask=mask, causal=causal, mt=True), f"sequence {b}")
+    # the same launch with row statistics
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    bq, bk, bv = G.up(q), G.up(k), G.up(v)
+    bo, bl = N.DeviceBuffer(B * L * D * 4), N.DeviceBuffer(B * H * L * 4)
+    bm = G.up(mask, np.uint8) if masked else None
+    N.check(N.lib().cdml_sdpa_fwd_lse(bq.ptr, D, bk.ptr, D, bv.ptr, D, bo.ptr, D, bl.ptr, B, L, L, D, H, scale,
+                                      int(causal), bm.ptr if bm else None, G.stream().handle))
+    assert np.array_equal(G.down(bo, (B * L, D)), got), "cdml_sdpa_fwd_lse output differs from cdml_sdpa_fwd"
+    lse = G.down(bl, (B, H, L))
+    for b in (0, B // 2, B - 1):
+        for h in (0, H - 1):
+            cols = slice(h * hd, (h + 1) * hd)
+            sc = (q[b * L:(b + 1) * L, cols].astype(np.float64) @ k[b * L:(b + 1) * L, cols].astype(np.float64).T
+                  ) * scale * math.log2(math.e)
+            vis = np.ones((L, L), bool)
+            if causal:
+                vis &= np.tril(vis)
+            if masked:
+                vis &= mask.astype(bool)
+            sc = np.where(vis, sc, -np.inf)
+            m = sc.max(axis=1, keepdims=True)
+            want = (m + np.log2(np.exp2(sc - m).sum(axis=1, keepdims=True)))[:, 0]
+            ok = np.isfinite(want)
+            assert np.all(np.isinf(lse[b, h][~ok])), "rows with no visible key must have lse +inf"
+            parity(lse[b, h][ok], want[ok], f"lse sequence {b} head {h}")
+
+
 def test_sdpa_c3_long_context_sampled():
     """c3 shape (B 4, L 4096, D 1024, H 16): one full sequence's sampled heads vs the
     oracle, plus the causal-prefix property on the whole batch."""
