@@ -18,6 +18,9 @@ to --out (default gpurun_out/profile_bench); the summaries go to profiles/:
             launch plus a digest of the kernel sources they were measured on)
   counters  two SQ counter passes over the c5 model and c2 layer legs
                                         -> flash_c5_c2_counters.md
+            and over the headline step -> mha_c3_counters.md
+  trainc5   SQ counters and HBM bytes of the c5 training step's attention
+            kernels                     -> flash_bwd_c5_counters.md
   backward  kernel trace + stats of the c3 MHA layer backward leg
                                         -> mha_backward_c3_kernel_stats.md
   probe     builds and runs csrc/probes/issue_rates.hip
@@ -41,7 +44,7 @@ sys.path.insert(0, ROOT)
 import bench  # noqa: E402  (TRAFFIC_SOURCES, source_digest)
 
 PROFILES = os.path.join(ROOT, "profiles")
-PASSES = ("trace", "traffic", "counters", "backward", "probe")
+PASSES = ("trace", "traffic", "counters", "trainc5", "backward", "probe")
 COUNTERS_A = ("GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES SQ_INSTS_VALU_MFMA_F32 "
               "SQ_INSTS_VALU SQ_INSTS_VALU_TRANS_F32 SQ_INSTS_LDS SQ_LDS_BANK_CONFLICT")
 COUNTERS_B = ("GRBM_GUI_ACTIVE SQ_WAVES SQ_WAVE_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_ACTIVE_INST_VALU "
@@ -214,22 +217,31 @@ the digest of the listed kernel sources matches the tree's.
                  "Two counter passes (one counter each, KiB per dispatch).") + "\n" + body)
 
 
-def pass_counters(out):
-    args = ["--only", "c5_time_series_model,c2_mha_layer"]
-    cmds, got = [], []
-    for tag, cs in (("a", COUNTERS_A), ("b", COUNTERS_B)):
-        d = os.path.join(out, "counters_" + tag)
-        _, cmd = rocprof(["--pmc"] + cs.split(), d, args, 300, os.path.join(out, f"counters_{tag}.log"))
+def counter_table(out, tag, bench_args, keep, with_traffic=False):
+    """Counter passes A and B (and FETCH_SIZE / WRITE_SIZE when with_traffic) over
+    `bench.py bench_args`; one table row per kernel (and grid) whose name starts
+    with one of `keep`.  Returns (commands, markdown rows)."""
+    sets = [("a", COUNTERS_A), ("b", COUNTERS_B)]
+    if with_traffic:
+        sets += [("fetch", "FETCH_SIZE"), ("write", "WRITE_SIZE")]
+    cmds, got = [], {}
+    for sub, cs in sets:
+        d = os.path.join(out, f"{tag}_{sub}")
+        _, cmd = rocprof(["--pmc"] + cs.split(), d, bench_args, 600, os.path.join(out, f"{tag}_{sub}.log"))
         cmds.append(cmd)
-        got.append(read_counters(d))
-    a, b = got
-    rows = ["| kernel | grid | dispatches | active cycles per XCC | MFMA busy / active | MFMA instr | "
+        got[sub] = read_counters(d)
+    a, b = got["a"], got["b"]
+    head = ("| kernel | grid | dispatches | active cycles per XCC | MFMA busy / active | MFMA instr | "
             "other VALU per MFMA | of which transcendental | LDS instr per MFMA | LDS bank conflicts | "
-            "waves | wave cycles waiting on dependencies | duration us |",
-            "|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
+            "waves | wave cycles waiting to issue | duration us |")
+    sep = "|---|---|---|---|---|---|---|---|---|---|---|---|---|"
+    if with_traffic:
+        head += " HBM MB read | HBM MB written |"
+        sep += "---|---|"
+    rows = [head, sep]
     for key in sorted(a):
         name, grid = key
-        if not name.startswith("flash_"):
+        if not name.startswith(tuple(keep)):
             continue
         ca, cb = a[key], b.get(key, {})
         act = mean(ca["GRBM_GUI_ACTIVE"]) / N_XCC
@@ -239,19 +251,54 @@ def pass_counters(out):
         trans = mean(ca["SQ_INSTS_VALU_TRANS_F32"])
         lds = mean(ca["SQ_INSTS_LDS"])
         wait = (mean(cb["SQ_WAIT_INST_ANY"]) / mean(cb["SQ_WAVE_CYCLES"])) if cb else float("nan")
-        rows.append(f"| `{name}` | {grid} | {len(ca['GRBM_GUI_ACTIVE'])} | {act / 1e6:.3f} M | "
-                    f"**{busy / act:.1%}** | {mf:,.0f} | {valu / mf:.2f} | {trans / mf:.2f} | {lds / mf:.2f} | "
-                    f"{mean(ca['SQ_LDS_BANK_CONFLICT']):,.0f} | {mean(cb.get('SQ_WAVES', [float('nan')])):,.0f} | "
-                    f"{wait:.1%} | {mean(ca['_ns']) / 1e3:.1f} |")
+        per = lambda x: f"{x / mf:.2f}" if mf else "-"
+        row = (f"| `{name}` | {grid} | {len(ca['GRBM_GUI_ACTIVE'])} | {act / 1e6:.3f} M | "
+               f"**{busy / act:.1%}** | {mf:,.0f} | {per(valu)} | {per(trans)} | {per(lds)} | "
+               f"{mean(ca['SQ_LDS_BANK_CONFLICT']):,.0f} | {mean(cb.get('SQ_WAVES', [float('nan')])):,.0f} | "
+               f"{wait:.1%} | {mean(ca['_ns']) / 1e3:.1f} |")
+        if with_traffic:
+            # the calibration of the traffic pass: FETCH_SIZE counts half of a 64 MiB copy's reads
+            rd = mean(got["fetch"].get(key, {}).get("FETCH_SIZE", [float("nan")])) * 2 * 1024 / 1e6
+            wr = mean(got["write"].get(key, {}).get("WRITE_SIZE", [float("nan")])) * 1024 / 1e6
+            row += f" {rd:.1f} | {wr:.1f} |"
+        rows.append(row)
+    return cmds, rows
+
+
+COUNTER_NOTE = ("`GRBM_GUI_ACTIVE` is summed over the 8 XCCs (divided by 8); `SQ_VALU_MFMA_BUSY_CYCLES` is "
+                "summed over the 1024 SIMDs (divided by 1024) and reads 64 cycles per "
+                "`v_mfma_f32_32x32x2_f32`; `SQ_INSTS_VALU` includes the MFMAs, which are subtracted; "
+                "`SQ_WAIT_INST_ANY` / `SQ_WAVE_CYCLES` is the share of a wave's life spent with an "
+                "instruction waiting to issue (other waves hold the SIMD, or a dependency).  Durations are "
+                "under counter collection, which lengthens them.")
+
+
+def pass_counters(out):
+    cmds, rows = counter_table(out, "counters", ["--only", "c5_time_series_model,c2_mha_layer"], ["flash_"])
     note = ("Per dispatch of each flash-attention launch in the c5 model leg (6 layers, 256 windows x 512, "
-            "8 heads x 32, causal) and the c2 layer leg (16 x 1024, 8 heads x 64, causal).  "
-            "`GRBM_GUI_ACTIVE` is summed over the 8 XCCs (divided by 8); `SQ_VALU_MFMA_BUSY_CYCLES` is "
-            "summed over the 1024 SIMDs (divided by 1024) and reads 64 cycles per "
-            "`v_mfma_f32_32x32x2_f32`; `SQ_INSTS_VALU` includes the MFMAs, which are subtracted.  "
-            "Durations are under counter collection, which lengthens them.")
+            "8 heads x 32, causal) and the c2 layer leg (16 x 1024, 8 heads x 64, causal).  " + COUNTER_NOTE)
     write("flash_c5_c2_counters.md",
           header("Flash attention counters: c5 (d_h 32) and c2 (d_h 64)", cmds, note) + "\n" +
           "\n".join(rows) + "\n")
+    cmds, rows = counter_table(out, "c3counters", ["--steps", "3", "--warmup", "1", "--no-cpu-baseline",
+                                                   "--no-extras", "--no-decode"], ["flash_", "gemm_"])
+    note = ("Per dispatch of the three kernels of the headline step (c3: 4 x 4096, D 1024, 16 heads x 64): "
+            "the flash kernel, the Q/K/V GEMM with the RoPE epilogue and the output projection.  " +
+            COUNTER_NOTE)
+    write("mha_c3_counters.md",
+          header("Counters of the c3 MHA forward kernels", cmds, note) + "\n" + "\n".join(rows) + "\n")
+
+
+def pass_trainc5(out):
+    cmds, rows = counter_table(out, "trainc5", ["--only", "c5_time_series_train_step"],
+                               ["flash_bwd", "bwd_delta", "flash_fwd"], with_traffic=True)
+    note = ("Per dispatch of the attention kernels of the c5 training step leg (256 windows x 512, "
+            "6 layers, 8 heads x 32): the forward with row statistics, D = rowsum(dO o O), dK/dV with "
+            "the dS blocks stored, and dQ over the stored blocks.  HBM bytes are FETCH_SIZE x 2 and "
+            "WRITE_SIZE x 1 (KiB), the factors a 64 MiB device copy reads on those counters.  " +
+            COUNTER_NOTE)
+    write("flash_bwd_c5_counters.md",
+          header("Attention backward counters: c5 training step", cmds, note) + "\n" + "\n".join(rows) + "\n")
 
 
 def pass_backward(out):
