@@ -273,14 +273,183 @@ __device__ __forceinline__ void load_q(float (&qreg)[HD / 2], const FlashArgs &a
   }
 }
 
+// The online softmax of one wave's 32 query rows (one per lane % 32) over
+// 32-key sub-blocks.
+template <int HD, bool HAS_MASK>
+struct OnlineRows {
+  static constexpr int NDB = HD / 32;     // 32-wide head-dim blocks of O^T
+  static constexpr int NQ = HD / 2;       // MFMA k-steps of Q.K
+  static constexpr int NKG = HD / 8;      // float4 groups of a K row slice
+  static constexpr int VCH = HD <= 32 ? 16 : 8;  // P.V steps whose V operands are read at once
+  static constexpr int NVG = VCH / 4;            // 16-byte V^T reads per chunk and head-dim block
+  floatx16 oacc[NDB];
+  // The reference max of this lane's query (exp2 domain) is subtracted by
+  // the MFMA itself: the first step of every S^T block starts from negm,
+  // -m_run in all 16 entries (0 until the first visible key sets m_run), so
+  // the scores come out relative to the reference and p = exp2(score).
+  floatx16 negm;
+  float m_run, thr;  // thr: rescale threshold, any visible key until m_run is set
+  float l_a, l_b;    // running sums over this half-wave's keys
+
+  __device__ __forceinline__ void init() {
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) negm[r] = 0.f;
+    m_run = -INFINITY;
+    thr = -INFINITY;
+    l_a = l_b = 0.f;
+  }
+
+  // S^T = K Q^T for the 32 keys whose rows start at krow; the K operand group
+  // u + 1 is read while group u multiplies.
+  template <int KP>
+  __device__ __forceinline__ floatx16 scores(const float (*krow)[KP], const float (&qreg)[NQ], int li,
+                                             int hf) const {
+    floatx16 sacc;
+    float4 kcur = *reinterpret_cast<const float4 *>(&krow[li][4 * hf]);
+#pragma unroll
+    for (int u = 0; u < NKG; ++u) {
+      float4 knext;
+      if (u + 1 < NKG) knext = *reinterpret_cast<const float4 *>(&krow[li][8 * (u + 1) + 4 * hf]);
+      sacc = mfma32x32x2(kcur.x, qreg[4 * u + 0], u == 0 ? negm : sacc);
+      sacc = mfma32x32x2(kcur.y, qreg[4 * u + 1], sacc);
+      sacc = mfma32x32x2(kcur.z, qreg[4 * u + 2], sacc);
+      sacc = mfma32x32x2(kcur.w, qreg[4 * u + 3], sacc);
+      if (u + 1 < NKG) kcur = knext;
+    }
+    return sacc;
+  }
+
+  // Softmax of one sub-block's scores and O^T += V^T P^T.  vt: V^T rows
+  // (pitch VP) whose columns key0 .. key0 + 31 are this sub-block's keys.
+  // masked (wave-uniform): some key of the sub-block may be invisible, then
+  // keys past last_vis (offset within the sub-block for this lane's half,
+  // from key0 + 4 hf) are masked, and with HAS_MASK also keys whose mask byte
+  // mrow[min(kb0 + offset, key_cap)] is 0 or any key when !row_ok.
+  template <int VP>
+  __device__ __forceinline__ void consume(floatx16 sacc, const float (*vt)[VP], int key0, int li, int hf,
+                                          bool masked, int last_vis, const uint8_t *mrow, int kb0,
+                                          int key_cap, bool row_ok) {
+    // V^T operands of the first P.V chunk, in flight during the softmax: steps
+    // 4g .. 4g + 3 take keys 8g + 4h .. 8g + 4h + 3 of column db * 32 + li.
+    vf4 vr[NVG][NDB];
+#pragma unroll
+    for (int g = 0; g < NVG; ++g)
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+        vr[g][db] = *reinterpret_cast<const vf4 *>(&vt[db * 32 + li][key0 + 8 * g + 4 * hf]);
+
+    if (HAS_MASK || masked) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        bool ok = acc_key(r) <= last_vis;
+        if (HAS_MASK) {
+          const int key = min(kb0 + acc_key(r) + 4 * hf, key_cap);
+          ok = ok && row_ok && mrow[key] != 0;
+        }
+        sacc[r] = ok ? sacc[r] : -INFINITY;
+      }
+    }
+    // tile max relative to the reference (-inf: no visible key)
+    // (a tree of depth 3: eight v_max3 whose inputs do not wait on each other)
+    const float m0 = max3_scores(sacc[0], sacc[1], sacc[2]);
+    const float m1 = max3_scores(sacc[3], sacc[4], sacc[5]);
+    const float m2 = max3_scores(sacc[6], sacc[7], sacc[8]);
+    const float m3 = max3_scores(sacc[9], sacc[10], sacc[11]);
+    const float m4 = max3_scores(sacc[12], sacc[13], sacc[14]);
+    float smax = max3_scores(max3_scores(m0, m1, m2), max3_scores(m3, m4, sacc[15]), -INFINITY);
+    smax = halves_max(smax);
+
+    // Lazy rescale: the first visible key sets the reference, later only a
+    // rise of more than the threshold moves it (the scores shift with it).
+    const bool need = smax > thr;
+    if (__builtin_amdgcn_ballot_w64(need)) {
+      const bool first = m_run == -INFINITY;
+      const float shift = need ? smax : 0.f;
+      const float alpha = (need && !first) ? fast_exp2(-smax) : 1.0f;  // o and l are 0 before the first key
+      m_run = need ? (first ? smax : m_run + smax) : m_run;
+      thr = m_run == -INFINITY ? -INFINITY : kRescaleThreshold;
+      const float nref = m_run == -INFINITY ? 0.f : -m_run;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        sacc[r] -= shift;
+        negm[r] = nref;
+      }
+      if (__builtin_amdgcn_ballot_w64(need && !first)) {  // not at a row's first visible key
+        l_a *= alpha;
+        l_b *= alpha;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = fast_exp2(sacc[r]);
+      sacc[r] = p;
+      if (r & 1) l_b += p;
+      else l_a += p;
+    }
+
+    // O^T += V^T P^T: accumulator r of the lane holds the probability of
+    // key acc_key(r) + 4*hf, the key B-operand slot of MFMA step r needs.
+#pragma unroll
+    for (int ch = 0; ch < 16 / VCH; ++ch) {
+      if (ch > 0) {
+#pragma unroll
+        for (int g = 0; g < NVG; ++g)
+#pragma unroll
+          for (int db = 0; db < NDB; ++db)
+            vr[g][db] = *reinterpret_cast<const vf4 *>(&vt[db * 32 + li][key0 + 8 * (ch * NVG + g) + 4 * hf]);
+      }
+#pragma unroll
+      for (int st = 0; st < VCH; ++st)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+          oacc[db] = mfma32x32x2(vr[st / 4][db][st % 4], sacc[ch * VCH + st], oacc[db]);
+    }
+  }
+
+  // Normalise and store row qi of (sequence b, head bh): the lane holds dims
+  // db*32 + 8*(r/4) + 4*hf + r%4.  For the backward pass the row statistic
+  // lse = m + log2(l) recovers every probability as exp2(s * scale * log2 e
+  // - lse) (+inf for a row with no visible key, whose p are all 0).
+  template <bool VEC>
+  __device__ __forceinline__ void store(const FlashArgs &a, int bh, int b, int qi, int col0, int hf) const {
+    const float l_tot = halves_sum(l_a + l_b);
+    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+    if (a.lse && hf == 0 && qi < a.lq)
+      a.lse[(size_t)bh * a.lq + qi] = l_tot > 0.f ? m_run + __log2f(l_tot) : INFINITY;
+    if (qi < a.lq) {
+      float *orow = a.o + ((size_t)b * a.lq + qi) * a.ldo + col0;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d = db * 32 + 8 * g + 4 * hf;
+          if constexpr (VEC) {
+            *reinterpret_cast<float4 *>(orow + d) =
+                make_float4(oacc[db][4 * g] * inv, oacc[db][4 * g + 1] * inv,
+                            oacc[db][4 * g + 2] * inv, oacc[db][4 * g + 3] * inv);
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (d + r < a.hd) orow[d + r] = oacc[db][4 * g + r] * inv;
+          }
+        }
+      }
+    }
+  }
+};
+
 template <int HD, int BN, bool CAUSAL, bool HAS_MASK, bool VEC, int SCHED>
 __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArgs a) {
   constexpr int NKB = BN / 32;   // 32-key sub-blocks per tile
-  constexpr int NDB = HD / 32;   // 32-wide head-dim blocks of O^T
   constexpr int NQ = HD / 2;     // MFMA k-steps of Q.K
-  constexpr int NKG = HD / 8;    // float4 groups of a K row slice
-  constexpr int VCH = HD <= 32 ? 16 : 8;  // P.V steps whose V operands are read at once
-  constexpr int NVG = VCH / 4;            // 16-byte V^T reads per chunk and head-dim block
   __shared__ __attribute__((aligned(16))) float Ks[2][BN][HD + 4];
   __shared__ __attribute__((aligned(16))) float Vt[2][HD][BN + 4];  // V transposed
 
@@ -328,22 +497,10 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArg
     const int kend = CAUSAL ? min(q0 + FA_BM, a.lk) : a.lk;
     const int n_kt = (kend + BN - 1) / BN;
 
-    floatx16 oacc[NDB];
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
-    // The reference max of this lane's query (exp2 domain) is subtracted by
-    // the MFMA itself: the first step of every S^T block starts from negm,
-    // -m_run in all 16 entries (0 until the first visible key sets m_run), so
-    // the scores come out relative to the reference and p = exp2(score).
-    float m_run = -INFINITY;
-    float thr = -INFINITY;  // rescale threshold: any visible key until m_run is set
-    float l_a = 0.f, l_b = 0.f;  // running sums over this half-wave's keys
-    floatx16 negm = {};
+    OnlineRows<HD, HAS_MASK> rows;
+    rows.init();
     // Last key this lane may attend (the causal diagonal and the sequence end).
     const int key_last = CAUSAL ? min(qi, a.lk - 1) : a.lk - 1;
-
     const uint8_t *mrow = HAS_MASK ? a.mask + (size_t)min(qi, a.lq - 1) * a.lk : nullptr;
 
     for (int kt = 0; kt < n_kt; ++kt) {
@@ -366,112 +523,21 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArg
       for (int kb = 0; kb < NKB; ++kb) {
         const int kb0 = k0 + kb * 32;
         // A sub-block wholly past the sequence end or in this wave's future
-        // contributes nothing (every probability would be 0): skip it.
-        if (kb0 >= a.lk || (CAUSAL && kb0 > qw0 + 31)) continue;
-        const float(*krow)[HD + 4] = &Ks[cur][kb * 32];
-        const float(*vtc)[BN + 4] = Vt[cur];  // this sub-block's keys start at column kb * 32
-
-        // S^T = K Q^T; the K operand group u + 1 is read while group u multiplies.
-        floatx16 sacc;
-        float4 kcur = *reinterpret_cast<const float4 *>(&krow[li][4 * hf]);
-#pragma unroll
-        for (int u = 0; u < NKG; ++u) {
-          float4 knext;
-          if (u + 1 < NKG) knext = *reinterpret_cast<const float4 *>(&krow[li][8 * (u + 1) + 4 * hf]);
-          sacc = mfma32x32x2(kcur.x, qreg[4 * u + 0], u == 0 ? negm : sacc);
-          sacc = mfma32x32x2(kcur.y, qreg[4 * u + 1], sacc);
-          sacc = mfma32x32x2(kcur.z, qreg[4 * u + 2], sacc);
-          sacc = mfma32x32x2(kcur.w, qreg[4 * u + 3], sacc);
-          if (u + 1 < NKG) kcur = knext;
-        }
+        // contributes nothing (every probability would be 0), and a wave
+        // whose rows all lie past lq (the last tile of a ragged length) has
+        // nothing to compute: skip.
+        if (kb0 >= a.lk || qw0 >= a.lq || (CAUSAL && kb0 > qw0 + 31)) continue;
+        const floatx16 sacc = rows.scores(&Ks[cur][kb * 32], qreg, li, hf);
         // Q is last read by the final sub-block of the last tile: the next
         // item's Q rows load while this sub-block's softmax and P.V run.
         if (kb == NKB - 1 && last && has_next) {
           load_q<HD, VEC>(qreg, a, nb, ncol0, nx.qt * FA_BM + wave * 32 + li, hf);
           q_next = true;
         }
-        // V^T operands of the first P.V chunk, in flight during the softmax: steps
-        // 4g .. 4g + 3 take keys 8g + 4h .. 8g + 4h + 3 of column db * 32 + li.
-        vf4 vr[NVG][NDB];
-#pragma unroll
-        for (int g = 0; g < NVG; ++g)
-#pragma unroll
-          for (int db = 0; db < NDB; ++db)
-            vr[g][db] = *reinterpret_cast<const vf4 *>(&vtc[db * 32 + li][kb * 32 + 8 * g + 4 * hf]);
-
-        // Masking (wave-uniform decision): the diagonal, the sequence end, a mask.
-        if (HAS_MASK || kb0 + 31 > (CAUSAL ? min(qw0, a.lk - 1) : a.lk - 1)) {
-          const int last_vis = key_last - kb0 - 4 * hf;  // last visible offset for this lane
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            bool ok = acc_key(r) <= last_vis;
-            if (HAS_MASK) {
-              const int key = min(kb0 + acc_key(r) + 4 * hf, a.lk - 1);
-              ok = ok && qi < a.lq && mrow[key] != 0;
-            }
-            sacc[r] = ok ? sacc[r] : -INFINITY;
-          }
-        }
-        // tile max relative to the reference (-inf: no visible key)
-        // (a tree of depth 3: eight v_max3 whose inputs do not wait on each other)
-        const float m0 = max3_scores(sacc[0], sacc[1], sacc[2]);
-        const float m1 = max3_scores(sacc[3], sacc[4], sacc[5]);
-        const float m2 = max3_scores(sacc[6], sacc[7], sacc[8]);
-        const float m3 = max3_scores(sacc[9], sacc[10], sacc[11]);
-        const float m4 = max3_scores(sacc[12], sacc[13], sacc[14]);
-        float smax = max3_scores(max3_scores(m0, m1, m2), max3_scores(m3, m4, sacc[15]), -INFINITY);
-        smax = halves_max(smax);
-
-        // Lazy rescale: the first visible key sets the reference, later only a
-        // rise of more than the threshold moves it (the scores shift with it).
-        const bool need = smax > thr;
-        if (__builtin_amdgcn_ballot_w64(need)) {
-          const bool first = m_run == -INFINITY;
-          const float shift = need ? smax : 0.f;
-          const float alpha = (need && !first) ? fast_exp2(-smax) : 1.0f;  // o and l are 0 before the first key
-          m_run = need ? (first ? smax : m_run + smax) : m_run;
-          thr = m_run == -INFINITY ? -INFINITY : kRescaleThreshold;
-          const float nref = m_run == -INFINITY ? 0.f : -m_run;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            sacc[r] -= shift;
-            negm[r] = nref;
-          }
-          if (__builtin_amdgcn_ballot_w64(need && !first)) {  // not at a row's first visible key
-            l_a *= alpha;
-            l_b *= alpha;
-#pragma unroll
-            for (int db = 0; db < NDB; ++db)
-#pragma unroll
-              for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
-          }
-        }
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = fast_exp2(sacc[r]);
-          sacc[r] = p;
-          if (r & 1) l_b += p;
-          else l_a += p;
-        }
-
-        // O^T += V^T P^T: accumulator r of the lane holds the probability of
-        // key acc_key(r) + 4*hf, the key B-operand slot of MFMA step r needs.
-#pragma unroll
-        for (int ch = 0; ch < 16 / VCH; ++ch) {
-          if (ch > 0) {
-#pragma unroll
-            for (int g = 0; g < NVG; ++g)
-#pragma unroll
-              for (int db = 0; db < NDB; ++db)
-                vr[g][db] = *reinterpret_cast<const vf4 *>(
-                    &vtc[db * 32 + li][kb * 32 + 8 * (ch * NVG + g) + 4 * hf]);
-          }
-#pragma unroll
-          for (int st = 0; st < VCH; ++st)
-#pragma unroll
-            for (int db = 0; db < NDB; ++db)
-              oacc[db] = mfma32x32x2(vr[st / 4][db][st % 4], sacc[ch * VCH + st], oacc[db]);
-        }
+        // masking is needed on the diagonal and at the sequence end (wave-uniform)
+        const bool masked = kb0 + 31 > (CAUSAL ? min(qw0, a.lk - 1) : a.lk - 1);
+        rows.consume(sacc, Vt[cur], kb * 32, li, hf, masked, key_last - kb0 - 4 * hf, mrow, kb0, a.lk - 1,
+                     qi < a.lq);
       }
       // a wave that skipped the final sub-block loads the next Q rows here
       if (last && has_next && !q_next) load_q<HD, VEC>(qreg, a, nb, ncol0, nx.qt * FA_BM + wave * 32 + li, hf);
@@ -481,33 +547,7 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArg
       __syncthreads();
       buf = cur ^ 1;
     }
-
-    // Normalise and store: lane holds query qi, dims db*32 + 8*(r/4) + 4*hf + r%4.
-    const float l_tot = halves_sum(l_a + l_b);
-    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-    // For the backward pass: p = exp2(s * scale * log2(e) - lse) recovers every
-    // probability (+inf for a row with no visible key, whose p are all 0).
-    if (a.lse && hf == 0 && qi < a.lq)
-      a.lse[(size_t)it.bh * a.lq + qi] = l_tot > 0.f ? m_run + __log2f(l_tot) : INFINITY;
-    if (qi < a.lq) {
-      float *orow = a.o + ((size_t)b * a.lq + qi) * a.ldo + col0;
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int d = db * 32 + 8 * g + 4 * hf;
-          if constexpr (VEC) {
-            *reinterpret_cast<float4 *>(orow + d) =
-                make_float4(oacc[db][4 * g] * inv, oacc[db][4 * g + 1] * inv,
-                            oacc[db][4 * g + 2] * inv, oacc[db][4 * g + 3] * inv);
-          } else {
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              if (d + r < a.hd) orow[d + r] = oacc[db][4 * g + r] * inv;
-          }
-        }
-      }
-    }
+    rows.template store<VEC>(a, it.bh, b, qi, col0, hf);
     if (!has_next) break;
     it = nx;
   }
@@ -650,8 +690,8 @@ int flash_forward(const float *q, int ldq, const float *k, int ldk, const float 
   const int hd_pad = hd <= 32 ? 32 : (hd <= 64 ? 64 : 128);
   const bool vec = hd == hd_pad && ldq % 4 == 0 && ldk % 4 == 0 && ldv % 4 == 0 && ldo % 4 == 0 &&
                    aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
-  a.n_qt = (lq + FA_BM - 1) / FA_BM;
   a.n_bh = batch * num_heads;
+  a.n_qt = (lq + FA_BM - 1) / FA_BM;
   long long total = (long long)batch * num_heads * a.n_qt;
   if (total > (1LL << 30)) return fail(CDML_E_INVALID, "cdml_sdpa_fwd: problem too large");
   a.n_items = (int)total;
