@@ -251,8 +251,8 @@ __global__ void __launch_bounds__(BW_THREADS, HD <= 64 ? 2 : 1) flash_bwd_dkdv_k
     for (int qb = 0; qb < NQB; ++qb) {
       const int qb0 = qt0 + qb * 32;
       // Sub-blocks past the sequence end or wholly before this wave's keys
-      // contribute nothing.
-      if (qb0 >= a.lq || (CAUSAL && qb0 + 31 < kw0)) continue;
+      // contribute nothing, and neither does a wave whose keys all lie past lk.
+      if (qb0 >= a.lq || kw0 >= a.lk || (CAUSAL && qb0 + 31 < kw0)) continue;
       const float(*qrow)[HD + 4] = &Qs[cur][qb * 32];
       const float(*grow)[HD + 4] = &Gs[cur][qb * 32];
 
@@ -449,7 +449,7 @@ __global__ void __launch_bounds__(BW_THREADS, 2) flash_bwd_dq_kernel(const BwdAr
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
       const int kb0 = k0 + kb * 32;
-      if (kb0 >= a.lk || (CAUSAL && kb0 > qw0 + 31)) continue;
+      if (kb0 >= a.lk || qw0 >= a.lq || (CAUSAL && kb0 > qw0 + 31)) continue;  // nothing to add
       const float(*krow)[HD + 4] = &Ks[cur][kb * 32];
       const float(*vrow)[HD + 4] = &Vs[cur][kb * 32];
 
