@@ -262,6 +262,29 @@ int cdml_sdpa_fwd_lse(const float *q, int ldq, const float *k, int ldk,
                       float scale, int causal, const uint8_t *mask,
                       cdml_stream stream);
 
+/* MultiHeadAttention.Forward (self-attention, MultiHeadAttention.cs:96-111
+ * and AttentionCore :146-155) for one layer on device buffers: ProjectQKV,
+ * the rotary embedding of Q and K, ScaledDotProductAttention (scale
+ * 1/sqrt(head_dim), causal or masked) and ProjectOutputBatch, as one call:
+ *   x [batch * seq_len, dim] -> y [batch * seq_len, dim]
+ * for `batch` sequences of seq_len rows (row r at position r % seq_len).
+ * Weights [dim, dim] as the reference stores them, biases [dim] or NULL.
+ * rope_cs: a cdml_rope_table of at least seq_len positions, or NULL to build
+ * one (base rope_base) in the workspace.  workspace: 256-byte aligned, at
+ * least cdml_mha_layer_fwd_workspace_size bytes (Q, K, V and the attention
+ * output, each rows * dim floats, and the table).  The same results as the
+ * three entries cdml_project_qkv_rope, cdml_sdpa_fwd and cdml_linear. */
+int cdml_mha_layer_fwd_workspace_size(int batch, int seq_len, int dim,
+                                      int num_heads, size_t *bytes);
+int cdml_mha_layer_fwd(const float *x, const float *wq, const float *bq,
+                       const float *wk, const float *bk, const float *wv,
+                       const float *bv, const float *wo, const float *bo,
+                       float *y, int batch, int seq_len, int dim,
+                       int num_heads, float rope_base, int causal,
+                       const uint8_t *mask, const float *rope_cs,
+                       void *workspace, size_t workspace_bytes,
+                       cdml_stream stream);
+
 /* IAccelerationManager.MultiHeadAttentionBackward, both overloads (:161,
  * :163), replacing AccelerationCPU.cs:1011-1280.  For `batch` independent
  * sequences (the segmented trainer's SegmentedMultiHeadAttentionBackward,

@@ -169,3 +169,27 @@ def test_sdpa_bwd_workspace_sizes():
     bad = C.c_size_t(0)
     assert lib.cdml_sdpa_bwd_stored_ds_workspace_size(1, 8, 8, 10, 3, 1, C.byref(bad)) == N.E_INVALID
     assert lib.cdml_sdpa_bwd_stored_ds_workspace_size(1, 8, 8, 12, 3, 1, None) == N.E_INVALID
+
+
+def test_mha_layer_fwd_argument_checks():
+    """cdml_mha_layer_fwd rejects its arguments before any device work: a head dim that
+    does not divide D, an odd head dim (RoPE pairs), NULL buffers and a short workspace;
+    the workspace size covers Q, K, V, the attention output and the RoPE table."""
+    lib = N.lib()
+    sz = C.c_size_t(0)
+    assert lib.cdml_mha_layer_fwd_workspace_size(2, 100, 64, 4, C.byref(sz)) == N.OK
+    act = (2 * 100 * 64 * 4 + 255) // 256 * 256
+    assert sz.value == 4 * act + (100 * 16 * 4 + 255) // 256 * 256
+    assert lib.cdml_mha_layer_fwd_workspace_size(2, 100, 64, 3, C.byref(sz)) == N.E_INVALID
+    fake = C.c_void_p(0x1000)
+    w = [fake] * 9
+
+    def call(dim, heads, ws=fake, wsb=1 << 30, x=fake):
+        return lib.cdml_mha_layer_fwd(x, *w[:8], fake, 2, 16, dim, heads, 10000.0, 1, None, None, ws, wsb, None)
+
+    assert call(64, 3) == N.E_INVALID                  # 64 % 3
+    assert call(66, 2) == N.E_INVALID                  # head dim 33 is odd
+    assert call(64, 4, x=None) == N.E_INVALID          # NULL input
+    assert call(64, 4, wsb=1024) == N.E_INVALID        # workspace too small
+    assert call(64, 4, ws=None) == N.E_INVALID         # no workspace
+    assert b"workspace" in lib.cdml_last_error()

@@ -8,6 +8,7 @@ with Lq != Lk, head dims 3 .. 160).
 """
 from __future__ import annotations
 
+import ctypes as C
 import math
 
 import numpy as np
@@ -478,6 +479,60 @@ def test_sdpa_every_sequence_of_large_launches(B, L, D, H, causal, masked):
             ok = np.isfinite(want)
             assert np.all(np.isinf(lse[b, h][~ok])), "rows with no visible key must have lse +inf"
             parity(lse[b, h][ok], want[ok], f"lse sequence {b} head {h}")
+
+
+def _mha_layer(x, ws, bs, batch, seq_len, heads, causal=True, mask=None, base=10000.0, table=False):
+    """cdml_mha_layer_fwd on host arrays; ws = (wq, wk, wv, wo), bs likewise."""
+    rows, dim = x.shape
+    lib, st = N.lib(), G.stream()
+    size = C.c_size_t(0)
+    N.check(lib.cdml_mha_layer_fwd_workspace_size(batch, seq_len, dim, heads, C.byref(size)))
+    bx, by = G.up(x), N.DeviceBuffer(rows * dim * 4)
+    bw, bb = [G.up(w) for w in ws], [G.up(b) for b in bs]
+    ws_buf = N.DeviceBuffer(size.value)
+    bm = G.up(mask, np.uint8) if mask is not None else None
+    cs = None
+    if table:
+        cs = N.DeviceBuffer(seq_len * (dim // heads) * 4)
+        N.check(lib.cdml_rope_table(cs.ptr, seq_len, dim // heads, base, st.handle))
+    N.check(lib.cdml_mha_layer_fwd(bx.ptr, bw[0].ptr, bb[0].ptr, bw[1].ptr, bb[1].ptr, bw[2].ptr, bb[2].ptr,
+                                   bw[3].ptr, bb[3].ptr, by.ptr, batch, seq_len, dim, heads, base, int(causal),
+                                   bm.ptr if bm else None, cs.ptr if cs else None, ws_buf.ptr, size.value,
+                                   st.handle))
+    return G.down(by, (rows, dim))
+
+
+@pytest.mark.parametrize("batch,L,D,H,causal,masked", [
+    (1, 64, 64, 4, True, False), (3, 77, 96, 3, True, False), (2, 50, 64, 2, False, True),
+    (2, 130, 256, 8, True, False)])
+def test_mha_layer_fwd_matches_the_reference_sequence(batch, L, D, H, causal, masked):
+    """cdml_mha_layer_fwd = MultiHeadAttention.Forward (MultiHeadAttention.cs:96-155):
+    ProjectQKV, RoPE of Q and K per sequence, ScaledDotProductAttention, ProjectOutputBatch,
+    each sequence of the batch against the oracle's composition; biases non-zero."""
+    x = synth.normal(L + D, (batch * L, D))
+    ws = [synth.xavier_uniform(300 + i, D, D) for i in range(4)]
+    bs = [np.float32(0.1) * synth.normal(310 + i, (D,)) for i in range(4)]
+    mask = synth.periodic_mask(L, L) if masked else None
+    got = _mha_layer(x, ws, bs, batch, L, H, causal=causal, mask=mask)
+    for b in range(batch):
+        s = slice(b * L, (b + 1) * L)
+        q, k, v = O.project_qkv(x[s], ws[0], bs[0], ws[1], bs[1], ws[2], bs[2])
+        a = O.sdpa(O.rope(q, H), O.rope(k, H), v, H, mask=mask, causal=causal)
+        parity(got[s], O.project_output_batch(a, ws[3], bs[3]), f"sequence {b}")
+
+
+def test_mha_layer_fwd_equals_the_three_entries():
+    """The fused entry runs the same kernels as cdml_project_qkv_rope, cdml_sdpa_fwd and
+    cdml_linear chained by the host: the same bits, with its own table or a caller's."""
+    batch, L, D, H = 2, 300, 256, 8
+    hd = D // H
+    x = synth.normal(5, (batch * L, D))
+    ws = [synth.xavier_uniform(320 + i, D, D) for i in range(4)]
+    bs = [np.float32(0.1) * synth.normal(330 + i, (D,)) for i in range(4)]
+    q, k, v = G.project_qkv_rope(x, ws[0], bs[0], ws[1], bs[1], ws[2], bs[2], hd, n_pos=L, seg_len=L)
+    want = G.linear(G.sdpa(q, k, v, H, causal=True, batch=batch), ws[3], bs[3])
+    assert np.array_equal(_mha_layer(x, ws, bs, batch, L, H), want)
+    assert np.array_equal(_mha_layer(x, ws, bs, batch, L, H, table=True), want)
 
 
 def test_sdpa_c3_long_context_sampled():
