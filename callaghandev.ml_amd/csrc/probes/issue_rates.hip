@@ -79,6 +79,31 @@ __global__ void __launch_bounds__(256) valu_mix(float *out, int iters, float x) 
   out[blockIdx.x * 256 + threadIdx.x] = s;
 }
 
+// A softmax-like mix: a dependent chain of 16 MFMAs, then a burst of 48
+// independent adds (BURST), or the MFMAs alone (MFMA_ONLY), or the adds alone.
+template <bool MFMA, bool ADDS>
+__global__ void __launch_bounds__(256) burst(float *out, int iters, float x) {
+  floatx16 acc;
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+  const float a = x + threadIdx.x, b = x * 2.f, c = x * 0.25f;
+  float v[8];
+  for (int i = 0; i < 8; ++i) v[i] = x + i * threadIdx.x;
+  for (int it = 0; it < iters; ++it) {
+    if (MFMA) {
+#pragma unroll
+      for (int s = 0; s < 16; ++s) acc = mf(a, b, acc);
+    }
+    if (ADDS) {
+#pragma unroll
+      for (int j = 0; j < 48; ++j) v[j & 7] = v[j & 7] + c;
+    }
+  }
+  float s = 0.f;
+  for (int r = 0; r < 16; ++r) s += acc[r];
+  for (int i = 0; i < 8; ++i) s += v[i];
+  out[blockIdx.x * 256 + threadIdx.x] = s;
+}
+
 // MFMA A operands read from LDS one group of four ahead: KIND 0 one 16-byte
 // read of four consecutive keys of a column (a transposed tile), KIND 1 four
 // 4-byte reads of four rows, KIND 2 registers only.
@@ -166,6 +191,15 @@ int main() {
   MIX(2, 8, true, "v_max3_f32");
   MIX(3, 8, true, "v_fma_f32");
 #undef MIX
+  for (int wgs : {256, 512, 1024}) {
+    const int it = 200;
+    std::printf("16_mfma_then_48_adds waves_per_simd=%d %.1f\n", wgs / 256,
+                cycles(time_ms([&] { burst<true, true><<<wgs, 256>>>(out, it, 1e-3f); }), wgs, it));
+    std::printf("16_mfma_only waves_per_simd=%d %.1f\n", wgs / 256,
+                cycles(time_ms([&] { burst<true, false><<<wgs, 256>>>(out, it, 1e-3f); }), wgs, it));
+    std::printf("48_adds_only waves_per_simd=%d %.1f\n", wgs / 256,
+                cycles(time_ms([&] { burst<false, true><<<wgs, 256>>>(out, it, 1e-3f); }), wgs, it));
+  }
   const char *lds_names[] = {"lds_b128_transposed", "lds_b32_rows", "registers"};
   for (int k = 0; k < 3; ++k) {
     double ms = 0;

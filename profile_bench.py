@@ -332,8 +332,11 @@ def pass_probe(out):
             rows.append(f"| `{parts[0]}` | {parts[1]} |")
     note = ("Cycles per step per SIMD at the 2.4 GHz peak clock, from event time.  A step is one "
             "`v_mfma_f32_32x32x2_f32` (64 cycles at full rate) plus what the case names; `mfma=0` "
-            "cases have no MFMA.  With 4 waves per SIMD, the cycles a VALU instruction adds next to an "
-            "MFMA equal what it costs alone: on gfx950 the fp32 MFMA and the VALU do not overlap.")
+            "cases have no MFMA.  The `16_mfma`/`48_adds` cases count one iteration of a dependent "
+            "chain of 16 MFMAs followed by a burst of 48 independent adds, the shape of a softmax "
+            "between two MFMA chains.  The cycles the VALU instructions add next to the MFMAs are at "
+            "least what they cost alone: on gfx950 the fp32 MFMA and the VALU do not overlap, and a "
+            "single wave issues VALU at about half the rate of several.")
     write("gfx950_issue_rates.md",
           header("gfx950 issue rates: fp32 MFMA against VALU and LDS operands",
                  [" ".join(build[:1] + ["..."] + build[-3:]), os.path.relpath(exe, ROOT)], note) +
