@@ -23,6 +23,8 @@ to --out (default gpurun_out/profile_bench); the summaries go to profiles/:
             kernels                     -> flash_bwd_c5_counters.md
   backward  kernel trace + stats of the c3 MHA layer backward leg
                                         -> mha_backward_c3_kernel_stats.md
+  train     kernel traces of the three training-step legs
+                                        -> train_step_{c1,c3_shape,c5}_kernel_stats.md
   probe     builds and runs csrc/probes/issue_rates.hip
                                         -> gfx950_issue_rates.md
 """
@@ -44,7 +46,7 @@ sys.path.insert(0, ROOT)
 import bench  # noqa: E402  (TRAFFIC_SOURCES, source_digest)
 
 PROFILES = os.path.join(ROOT, "profiles")
-PASSES = ("trace", "traffic", "counters", "trainc5", "backward", "probe")
+PASSES = ("trace", "traffic", "counters", "trainc5", "backward", "train", "probe")
 COUNTERS_A = ("GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES SQ_INSTS_VALU_MFMA_F32 "
               "SQ_INSTS_VALU SQ_INSTS_VALU_TRANS_F32 SQ_INSTS_LDS SQ_LDS_BANK_CONFLICT")
 COUNTERS_B = ("GRBM_GUI_ACTIVE SQ_WAVES SQ_WAVE_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_ACTIVE_INST_VALU "
@@ -315,6 +317,39 @@ def pass_backward(out):
             f"and {rc.get('ms')} ms.")
     write("mha_backward_c3_kernel_stats.md",
           header("Kernel durations: c3 MHA layer backward", [cmd], note) + "\n" + stats_table(read_stats(d)) + "\n")
+
+
+TRAIN_LEGS = {
+    "c1_text_model_train_step": ("train_step_c1_kernel_stats.md", "training step, config-1 text model "
+                                 "(TrainBatchDiscrete, 4 sequences of 64 tokens)"),
+    "c3_shape_train_step": ("train_step_c3_shape_kernel_stats.md", "training step, c3 shape "
+                            "(TrainBatchDiscrete, 12 layers, 4 sequences of 4096 tokens)"),
+    "c5_time_series_train_step": ("train_step_c5_kernel_stats.md", "training step, config 5 "
+                                  "(TrainBatchContinuous, 256 windows x 512 steps)"),
+}
+
+
+def pass_train(out):
+    for leg, (name, what) in TRAIN_LEGS.items():
+        d = os.path.join(out, "train_" + leg)
+        so, cmd = rocprof(["--kernel-trace", "--stats"], d, ["--only", leg], 900, os.path.join(out, leg + ".log"))
+        b = bench_line(so).get("other_configs", {}).get(leg, {})
+        rows = read_stats(d)
+        # timed + warm-up steps the leg runs (bench.py extras)
+        steps = {"c1_text_model_train_step": 20 + 5, "c3_shape_train_step": 3 + 1,
+                 "c5_time_series_train_step": 3 + 1}[leg]
+        total = sum(float(r["TotalDurationNs"]) for r in rows) / 1e6
+        lines = ["| kernel | calls | calls/step | avg us | min us | max us | ms/step |",
+                 "|---|---|---|---|---|---|---|"]
+        for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
+            c = int(r["Calls"])
+            lines.append(f"| `{short_name(r['Name'])}` | {c} | {c / steps:g} | {float(r['AverageNs']) / 1e3:.1f} | "
+                         f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | "
+                         f"{float(r['TotalDurationNs']) / 1e6 / steps:.2f} |")
+        note = (f"The `{leg}` leg alone ({steps} steps in the trace, warm-up included).  The bench line of "
+                f"the same run: {b.get('ms')} ms per step, {b.get('tflops')} TFLOP/s by its count.  Kernel "
+                f"time summed over the trace: {total / steps:.2f} ms per step.")
+        write(name, header(f"Kernel durations: {what}", [cmd], note) + "\n" + "\n".join(lines) + "\n")
 
 
 def pass_probe(out):
