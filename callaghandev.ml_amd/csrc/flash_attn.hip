@@ -35,6 +35,23 @@ constexpr int FA_THREADS = 256;
 constexpr int FA_BM = 128;  // queries per workgroup (32 per wave)
 constexpr float kLog2e = 1.4426950408889634f;
 
+// Division by a launch-constant divisor d >= 1 for dividends 0 <= x < 2^31:
+// x / d = (x * m) >> l with l = 31 + ceil(log2 d) and m = ceil(2^l / d) < 2^32
+// (the error m * d - 2^l is below d, so x * error < 2^l for every such x).
+// Block-uniform dividends keep the division on the scalar unit.
+struct UDiv {
+  uint32_t m;
+  int l;
+  static UDiv make(uint32_t d) {
+    if (d == 0) d = 1;  // no launch divides by it
+    int s = 0;
+    while ((1ull << s) < d) ++s;
+    const int l = 31 + s;
+    return {(uint32_t)(((1ull << l) + d - 1) / d), l};
+  }
+  __device__ __forceinline__ int div(int x) const { return (int)(((uint64_t)(uint32_t)x * m) >> l); }
+};
+
 struct FlashArgs {
   const float *q, *k, *v;
   float *o;
@@ -44,6 +61,8 @@ struct FlashArgs {
   int lq, lk, heads, hd;
   float scale_log2;
   int n_qt, n_bh, n_items;  // query tiles per sequence, (sequence, head) pairs, n_bh * n_qt
+  UDiv by_bh, by_heads;     // division by n_bh and by heads
+  int fast;                 // sub-blocks may skip their maximum (see try_fast)
 };
 
 // Stages one BN x HD tile of K or V (rows [k0, k0+BN) of head column block
@@ -214,6 +233,11 @@ constexpr float kRescaleThreshold = 8.0f;
 // lane of half-wave h: 8 * (r / 4) + 4 * h + r % 4 (the 32x32 MFMA D layout).
 __device__ __forceinline__ constexpr int acc_key(int r) { return 8 * (r >> 2) + (r & 3); }
 
+// A sub-block whose per-lane probability sum stays at or below this bound is
+// accumulated without looking at its maximum: no probability exceeds it, so
+// nothing overflows (the running sums stay below 2^32 times the key count).
+constexpr float kFastSumLimit = 4294967296.0f;  // 2^32
+
 // Which query tiles a workgroup runs, one after the other.  Item i of a
 // launch is (sequence, head) i % n_bh and, under the causal rule, query tile
 // n_qt - 1 - i / n_bh (heaviest rows first), else tile i / n_bh.
@@ -237,8 +261,8 @@ template <bool CAUSAL, int SCHED>
 __device__ __forceinline__ bool item_at(const FlashArgs &a, int k, Item &it) {
   const int i = blockIdx.x;
   if (SCHED == kPair) {
-    const int slot = i / a.n_bh;
-    it.bh = i % a.n_bh;
+    const int slot = a.by_bh.div(i);
+    it.bh = i - slot * a.n_bh;
     if (k == 0) it.qt = a.n_qt - 1 - slot;
     else if (k == 1 && 2 * slot + 1 != a.n_qt) it.qt = slot;
     else return false;
@@ -246,29 +270,28 @@ __device__ __forceinline__ bool item_at(const FlashArgs &a, int k, Item &it) {
   } else if (k > 0) {
     return false;
   }
-  it.bh = i % a.n_bh;
-  const int slot = i / a.n_bh;
+  const int slot = a.by_bh.div(i);
+  it.bh = i - slot * a.n_bh;
   it.qt = CAUSAL ? a.n_qt - 1 - slot : slot;
   return true;
 }
 
-// Q^T operand of a wave: register 4u + r holds q[qi][8u + 4*hf + r] (rows
-// past lq read as 0), not yet scaled.
+// Q^T operand of a wave: register 4u + r holds q[qi][8u + 4*hf + r], not yet
+// scaled.  Rows past lq read row lq - 1: they are computed but never stored.
 template <int HD, bool VEC>
 __device__ __forceinline__ void load_q(float (&qreg)[HD / 2], const FlashArgs &a, int b, int col0, int qi,
                                        int hf) {
   const float *qrow = a.q + ((size_t)b * a.lq + min(qi, a.lq - 1)) * a.ldq + col0;
-  const bool qok = qi < a.lq;
 #pragma unroll
   for (int u = 0; u < HD / 8; ++u) {
     const int d = 8 * u + 4 * hf;
     if constexpr (VEC) {
       const vf4 t4 = *reinterpret_cast<const vf4 *>(qrow + d);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) qreg[4 * u + r] = qok ? t4[r] : 0.f;
+      for (int r = 0; r < 4; ++r) qreg[4 * u + r] = t4[r];
     } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) qreg[4 * u + r] = (qok && d + r < a.hd) ? qrow[d + r] : 0.f;
+      for (int r = 0; r < 4; ++r) qreg[4 * u + r] = d + r < a.hd ? qrow[d + r] : 0.f;
     }
   }
 }
@@ -290,6 +313,7 @@ struct OnlineRows {
   floatx16 negm;
   float m_run, thr;  // thr: rescale threshold, any visible key until m_run is set
   float l_a, l_b;    // running sums over this half-wave's keys
+  bool warm;         // every lane of the wave has its reference (wave-uniform)
 
   __device__ __forceinline__ void init() {
 #pragma unroll
@@ -301,6 +325,76 @@ struct OnlineRows {
     m_run = -INFINITY;
     thr = -INFINITY;
     l_a = l_b = 0.f;
+    warm = false;
+  }
+
+  // Sets the scores of keys this lane may not attend to -inf: keys past
+  // last_vis (offset within the sub-block for this lane's half), and with
+  // HAS_MASK also keys whose mask byte mrow[min(kb0 + offset, key_cap)] is 0
+  // or any key when !row_ok.
+  __device__ __forceinline__ void apply_mask(floatx16 &sacc, int hf, int last_vis, const uint8_t *mrow, int kb0,
+                                             int key_cap, bool row_ok) const {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      bool ok = acc_key(r) <= last_vis;
+      if (HAS_MASK) {
+        const int key = min(kb0 + acc_key(r) + 4 * hf, key_cap);
+        ok = ok && row_ok && mrow[key] != 0;
+      }
+      sacc[r] = ok ? sacc[r] : -INFINITY;
+    }
+  }
+
+  // O^T += V^T P^T: accumulator r of the lane holds the probability of key
+  // acc_key(r) + 4*hf, the key B-operand slot of MFMA step r needs.  vr holds
+  // the first chunk's V^T operands.
+  template <int VP>
+  __device__ __forceinline__ void accumulate_pv(const floatx16 &p, vf4 (&vr)[NVG][NDB], const float (*vt)[VP],
+                                                int key0, int li, int hf) {
+#pragma unroll
+    for (int ch = 0; ch < 16 / VCH; ++ch) {
+      if (ch > 0) {
+#pragma unroll
+        for (int g = 0; g < NVG; ++g)
+#pragma unroll
+          for (int db = 0; db < NDB; ++db)
+            vr[g][db] = *reinterpret_cast<const vf4 *>(&vt[db * 32 + li][key0 + 8 * (ch * NVG + g) + 4 * hf]);
+      }
+#pragma unroll
+      for (int st = 0; st < VCH; ++st)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+          oacc[db] = mfma32x32x2(vr[st / 4][db][st % 4], p[ch * VCH + st], oacc[db]);
+    }
+  }
+
+  // The common sub-block once every row has its reference: probabilities and
+  // their per-lane sum first, and only if some lane's sum is above 2^32 (a
+  // score far above the reference) or NaN does the caller take the full path
+  // (consume) on recomputed scores.  sacc is turned into probabilities in
+  // place; on false the running state is unchanged and sacc is garbage.
+  template <int VP>
+  __device__ __forceinline__ bool try_fast(floatx16 &sacc, const float (*vt)[VP], int key0, int li, int hf,
+                                           bool masked, int last_vis, const uint8_t *mrow, int kb0, int key_cap,
+                                           bool row_ok) {
+    vf4 vr[NVG][NDB];
+#pragma unroll
+    for (int g = 0; g < NVG; ++g)
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+        vr[g][db] = *reinterpret_cast<const vf4 *>(&vt[db * 32 + li][key0 + 8 * g + 4 * hf]);
+    if (HAS_MASK || masked) apply_mask(sacc, hf, last_vis, mrow, kb0, key_cap, row_ok);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sacc[r] = fast_exp2(sacc[r]);
+    // pairwise sum (a tree of depth 4)
+    float s8[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s8[i] = sacc[2 * i] + sacc[2 * i + 1];
+    const float ps = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
+    if (__builtin_amdgcn_ballot_w64(!(ps <= kFastSumLimit))) return false;
+    l_a += ps;
+    accumulate_pv(sacc, vr, vt, key0, li, hf);
+    return true;
   }
 
   // S^T = K Q^T for the 32 keys whose rows start at krow; the K operand group
@@ -325,10 +419,8 @@ struct OnlineRows {
 
   // Softmax of one sub-block's scores and O^T += V^T P^T.  vt: V^T rows
   // (pitch VP) whose columns key0 .. key0 + 31 are this sub-block's keys.
-  // masked (wave-uniform): some key of the sub-block may be invisible, then
-  // keys past last_vis (offset within the sub-block for this lane's half,
-  // from key0 + 4 hf) are masked, and with HAS_MASK also keys whose mask byte
-  // mrow[min(kb0 + offset, key_cap)] is 0 or any key when !row_ok.
+  // masked (wave-uniform): some key of the sub-block may be invisible (see
+  // apply_mask).
   template <int VP>
   __device__ __forceinline__ void consume(floatx16 sacc, const float (*vt)[VP], int key0, int li, int hf,
                                           bool masked, int last_vis, const uint8_t *mrow, int kb0,
@@ -342,17 +434,7 @@ struct OnlineRows {
       for (int db = 0; db < NDB; ++db)
         vr[g][db] = *reinterpret_cast<const vf4 *>(&vt[db * 32 + li][key0 + 8 * g + 4 * hf]);
 
-    if (HAS_MASK || masked) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        bool ok = acc_key(r) <= last_vis;
-        if (HAS_MASK) {
-          const int key = min(kb0 + acc_key(r) + 4 * hf, key_cap);
-          ok = ok && row_ok && mrow[key] != 0;
-        }
-        sacc[r] = ok ? sacc[r] : -INFINITY;
-      }
-    }
+    if (HAS_MASK || masked) apply_mask(sacc, hf, last_vis, mrow, kb0, key_cap, row_ok);
     // tile max relative to the reference (-inf: no visible key)
     // (a tree of depth 3: eight v_max3 whose inputs do not wait on each other)
     const float m0 = max3_scores(sacc[0], sacc[1], sacc[2]);
@@ -394,24 +476,8 @@ struct OnlineRows {
       if (r & 1) l_b += p;
       else l_a += p;
     }
-
-    // O^T += V^T P^T: accumulator r of the lane holds the probability of
-    // key acc_key(r) + 4*hf, the key B-operand slot of MFMA step r needs.
-#pragma unroll
-    for (int ch = 0; ch < 16 / VCH; ++ch) {
-      if (ch > 0) {
-#pragma unroll
-        for (int g = 0; g < NVG; ++g)
-#pragma unroll
-          for (int db = 0; db < NDB; ++db)
-            vr[g][db] = *reinterpret_cast<const vf4 *>(&vt[db * 32 + li][key0 + 8 * (ch * NVG + g) + 4 * hf]);
-      }
-#pragma unroll
-      for (int st = 0; st < VCH; ++st)
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-          oacc[db] = mfma32x32x2(vr[st / 4][db][st % 4], sacc[ch * VCH + st], oacc[db]);
-    }
+    warm = !__builtin_amdgcn_ballot_w64(m_run == -INFINITY);
+    accumulate_pv(sacc, vr, vt, key0, li, hf);
   }
 
   // Normalise and store row qi of (sequence b, head bh): the lane holds dims
@@ -467,7 +533,7 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArg
   item_at<CAUSAL, SCHED>(a, 0, it);
   float qreg[NQ];
   {
-    const int b = it.bh / a.heads, col0 = (it.bh % a.heads) * a.hd;
+    const int b = a.by_heads.div(it.bh), col0 = (it.bh - b * a.heads) * a.hd;
     load_q<HD, VEC>(qreg, a, b, col0, it.qt * FA_BM + wave * 32 + li, hf);
     sk.load(a.k + (size_t)b * a.lk * a.ldk + col0, a.ldk, 0, a.lk, a.hd);
     sv.load(a.v + (size_t)b * a.lk * a.ldv + col0, a.ldv, 0, a.lk, a.hd);
@@ -478,7 +544,7 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArg
   int buf = 0;  // LDS buffer holding the current key tile
 
   for (int k = 0;; ++k) {
-    const int b = it.bh / a.heads, h = it.bh % a.heads;
+    const int b = a.by_heads.div(it.bh), h = it.bh - b * a.heads;
     const int q0 = it.qt * FA_BM;
     const int qw0 = q0 + wave * 32;   // first query of this wave (wave-uniform)
     const int qi = qw0 + li;          // this lane's query
@@ -492,7 +558,7 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArg
 
     Item nx = it;
     const bool has_next = item_at<CAUSAL, SCHED>(a, k + 1, nx);
-    const int nb = nx.bh / a.heads, ncol0 = (nx.bh % a.heads) * a.hd;  // used only with has_next
+    const int nb = a.by_heads.div(nx.bh), ncol0 = (nx.bh - nb * a.heads) * a.hd;  // used only with has_next
 
     const int kend = CAUSAL ? min(q0 + FA_BM, a.lk) : a.lk;
     const int n_kt = (kend + BN - 1) / BN;
@@ -527,7 +593,7 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArg
         // whose rows all lie past lq (the last tile of a ragged length) has
         // nothing to compute: skip.
         if (kb0 >= a.lk || qw0 >= a.lq || (CAUSAL && kb0 > qw0 + 31)) continue;
-        const floatx16 sacc = rows.scores(&Ks[cur][kb * 32], qreg, li, hf);
+        floatx16 sacc = rows.scores(&Ks[cur][kb * 32], qreg, li, hf);
         // Q is last read by the final sub-block of the last tile: the next
         // item's Q rows load while this sub-block's softmax and P.V run.
         if (kb == NKB - 1 && last && has_next) {
@@ -536,8 +602,27 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(const FlashArg
         }
         // masking is needed on the diagonal and at the sequence end (wave-uniform)
         const bool masked = kb0 + 31 > (CAUSAL ? min(qw0, a.lk - 1) : a.lk - 1);
-        rows.consume(sacc, Vt[cur], kb * 32, li, hf, masked, key_last - kb0 - 4 * hf, mrow, kb0, a.lk - 1,
-                     qi < a.lq);
+        const int last_vis = key_last - kb0 - 4 * hf;
+        // Once every row has its reference, a sub-block is accumulated without
+        // its maximum unless its probabilities come out unbounded; then its
+        // scores are recomputed (K is still in LDS and Q in registers: a kOne
+        // workgroup loads no further Q rows) for the full path.  Explicit
+        // masks keep the full path (the mask reads in both paths would cost
+        // the registers of a fourth wave per SIMD), and so do launches of
+        // fewer than three workgroups per CU, whose waves cannot hide the wait
+        // of the check before the P.V step (every paired launch is one).
+        bool done = false;
+        if (!HAS_MASK && SCHED == kOne && a.fast && rows.warm) {
+          done = rows.try_fast(sacc, Vt[cur], kb * 32, li, hf, masked, last_vis, mrow, kb0, a.lk - 1, qi < a.lq);
+          if (!done) {
+            // K is read from LDS again (the compiler may not keep the first
+            // scores, which would hold them live through the fast path)
+            asm volatile("" ::: "memory");
+            sacc = rows.scores(&Ks[cur][kb * 32], qreg, li, hf);
+          }
+        }
+        if (!done)
+          rows.consume(sacc, Vt[cur], kb * 32, li, hf, masked, last_vis, mrow, kb0, a.lk - 1, qi < a.lq);
       }
       // a wave that skipped the final sub-block loads the next Q rows here
       if (last && has_next && !q_next) load_q<HD, VEC>(qreg, a, nb, ncol0, nx.qt * FA_BM + wave * 32 + li, hf);
@@ -620,15 +705,18 @@ void launch_sched(const FlashArgs &a, hipStream_t st) {
   // round of resident workgroups (four per CU), so that the round lasts as
   // long as its longest tile, and the pairs still give every CU two
   // workgroups (fewer would leave SIMDs with a single wave).
+  const long long cus = num_cus();
+  FlashArgs b = a;
   if constexpr (CAUSAL) {
-    const long long cus = num_cus();
-    if (a.n_qt > 1 && (long long)a.n_items <= 4 * cus && (long long)a.n_bh * ((a.n_qt + 1) / 2) >= 2 * cus) {
-      flash_fwd_kernel<HD, BN, CAUSAL, HAS_MASK, VEC, kPair>
-          <<<dim3(a.n_bh * ((a.n_qt + 1) / 2)), dim3(FA_THREADS), 0, st>>>(a);
+    const long long pairs = (long long)a.n_bh * ((a.n_qt + 1) / 2);
+    if (a.n_qt > 1 && (long long)a.n_items <= 4 * cus && pairs >= 2 * cus) {
+      b.fast = 0;
+      flash_fwd_kernel<HD, BN, CAUSAL, HAS_MASK, VEC, kPair><<<dim3((unsigned)pairs), dim3(FA_THREADS), 0, st>>>(b);
       return;
     }
   }
-  flash_fwd_kernel<HD, BN, CAUSAL, HAS_MASK, VEC, kOne><<<dim3(a.n_items), dim3(FA_THREADS), 0, st>>>(a);
+  b.fast = (long long)a.n_items >= 3 * cus;
+  flash_fwd_kernel<HD, BN, CAUSAL, HAS_MASK, VEC, kOne><<<dim3(a.n_items), dim3(FA_THREADS), 0, st>>>(b);
 }
 
 template <int HD, int BN, bool CAUSAL, bool HAS_MASK>
@@ -692,6 +780,8 @@ int flash_forward(const float *q, int ldq, const float *k, int ldk, const float 
                    aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
   a.n_bh = batch * num_heads;
   a.n_qt = (lq + FA_BM - 1) / FA_BM;
+  a.by_bh = UDiv::make((uint32_t)a.n_bh);
+  a.by_heads = UDiv::make((uint32_t)num_heads);
   long long total = (long long)batch * num_heads * a.n_qt;
   if (total > (1LL << 30)) return fail(CDML_E_INVALID, "cdml_sdpa_fwd: problem too large");
   a.n_items = (int)total;

@@ -481,6 +481,44 @@ def test_sdpa_every_sequence_of_large_launches(B, L, D, H, causal, masked):
             parity(lse[b, h][ok], want[ok], f"lse sequence {b} head {h}")
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_sdpa_score_jumps_in_large_launches(causal):
+    """Launches of at least three workgroups per CU accumulate a sub-block
+    without its maximum once every row has its reference, and fall back to the
+    full rescaling path when a lane's probabilities sum above 2^32.  Keys from
+    position 100 on carry K rows 12 times larger (scores about 50 log2 units
+    above the first sub-block's), keys from 200 on 12 times smaller,
+    so both the fallback and the plain path run in one launch; sampled
+    sequences against the oracle, row statistics against float64."""
+    B, L, D, H = 128, 256, 256, 8
+    hd = D // H
+    q, k, v = (synth.normal(7 + i, (B * L, D)) for i in range(3))
+    pos = np.arange(B * L) % L
+    k = np.where((pos >= 100)[:, None], k * 12, k).astype(np.float32)
+    k = np.where((pos >= 200)[:, None], k / 144, k).astype(np.float32)
+    got = G.sdpa(q, k, v, H, causal=causal, batch=B)
+    assert np.isfinite(got).all()
+    for b in (0, 37, B - 1):
+        s = slice(b * L, (b + 1) * L)
+        parity(got[s], O.sdpa(q[s], k[s], v[s], H, causal=causal, mt=True), f"sequence {b}")
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    bq, bk, bv = G.up(q), G.up(k), G.up(v)
+    bo, bl = N.DeviceBuffer(B * L * D * 4), N.DeviceBuffer(B * H * L * 4)
+    N.check(N.lib().cdml_sdpa_fwd_lse(bq.ptr, D, bk.ptr, D, bv.ptr, D, bo.ptr, D, bl.ptr, B, L, L, D, H, scale,
+                                      int(causal), None, G.stream().handle))
+    assert np.array_equal(G.down(bo, (B * L, D)), got), "cdml_sdpa_fwd_lse output differs from cdml_sdpa_fwd"
+    lse = G.down(bl, (B, H, L))
+    for b, h in ((0, 0), (B - 1, H - 1)):
+        cols = slice(h * hd, (h + 1) * hd)
+        sc = (q[b * L:(b + 1) * L, cols].astype(np.float64) @ k[b * L:(b + 1) * L, cols].astype(np.float64).T
+              ) * scale * math.log2(math.e)
+        if causal:
+            sc = np.where(np.tril(np.ones((L, L), bool)), sc, -np.inf)
+        m = sc.max(axis=1, keepdims=True)
+        want = (m + np.log2(np.exp2(sc - m).sum(axis=1, keepdims=True)))[:, 0]
+        parity(lse[b, h], want, f"lse sequence {b} head {h}")
+
+
 def _mha_layer(x, ws, bs, batch, seq_len, heads, causal=True, mask=None, base=10000.0, table=False):
     """cdml_mha_layer_fwd on host arrays; ws = (wq, wk, wv, wo), bs likewise."""
     rows, dim = x.shape
