@@ -303,7 +303,9 @@ struct OnlineRows {
   static constexpr int NDB = HD / 32;     // 32-wide head-dim blocks of O^T
   static constexpr int NQ = HD / 2;       // MFMA k-steps of Q.K
   static constexpr int NKG = HD / 8;      // float4 groups of a K row slice
-  static constexpr int VCH = HD <= 32 ? 16 : 8;  // P.V steps whose V operands are read at once
+  // P.V steps whose V operands are read at once (8: at head dim 32 every
+  // variant but the masked ones keeps four waves per SIMD)
+  static constexpr int VCH = 8;
   static constexpr int NVG = VCH / 4;            // 16-byte V^T reads per chunk and head-dim block
   floatx16 oacc[NDB];
   // The reference max of this lane's query (exp2 domain) is subtracted by

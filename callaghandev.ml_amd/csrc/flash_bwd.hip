@@ -148,7 +148,7 @@ __global__ void __launch_bounds__(256) bwd_delta_scalar_kernel(const BwdArgs a) 
 // which is the A operand order of the dQ product (16 contiguous floats per
 // lane).
 template <int HD, int BQ, bool CAUSAL, bool HAS_MASK, bool VEC, bool STORE_DS>
-__global__ void __launch_bounds__(BW_THREADS, HD <= 64 ? 2 : 1) flash_bwd_dkdv_kernel(const BwdArgs a) {
+__global__ void __launch_bounds__(BW_THREADS, (HD <= 32 && !HAS_MASK) ? 3 : (HD <= 64 ? 2 : 1)) flash_bwd_dkdv_kernel(const BwdArgs a) {
   constexpr int NQB = BQ / 32;  // 32-query sub-blocks per tile
   constexpr int NDB = HD / 32;  // 32-wide head-dim blocks of dK^T / dV^T
   constexpr int NKG = HD / 8;   // 8-dim groups of the Q.K and dO.V products
@@ -215,6 +215,8 @@ __global__ void __launch_bounds__(BW_THREADS, HD <= 64 ? 2 : 1) flash_bwd_dkdv_k
   sq.init(a.ldq);
   sg.init(a.lddo);
   float lreg = 0.f, dreg = 0.f;
+  // byte offset of this lane's dS entries in a stored block (row 4 hf + acc_row(r), key li)
+  const uint32_t ds_lane = 4u * (uint32_t)(4 * hf * 32 + (li & 1) * 16 + (li >> 1));
   if (n_it > 0) {
     sq.load(qbase, a.ldq, q_begin, a.lq, a.hd);
     sg.load(gbase, a.lddo, q_begin, a.lq, a.hd);
@@ -280,32 +282,46 @@ __global__ void __launch_bounds__(BW_THREADS, HD <= 64 ? 2 : 1) flash_bwd_dkdv_k
 
       // P = exp2(S * scale * log2 e - lse) and dS = P (dP - D), per query row
       // 8g + 4*hf + c of the sub-block (registers 4g + c).
+      // (the masked and the unmasked forms are separate branches: a select
+      // per element would run the mask arithmetic on every sub-block)
       const bool need = HAS_MASK || (CAUSAL && qb0 < kw0 + 31) || qb0 + 31 >= a.lq;
+      if (need) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const vf4 l4 = *reinterpret_cast<const vf4 *>(&Ls[cur][qb * 32 + 8 * g + 4 * hf]);
-        const vf4 d4 = *reinterpret_cast<const vf4 *>(&Ds[cur][qb * 32 + 8 * g + 4 * hf]);
+        for (int g = 0; g < 4; ++g) {
+          const vf4 l4 = *reinterpret_cast<const vf4 *>(&Ls[cur][qb * 32 + 8 * g + 4 * hf]);
+          const vf4 d4 = *reinterpret_cast<const vf4 *>(&Ds[cur][qb * 32 + 8 * g + 4 * hf]);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const int r = 4 * g + c;
-          float p = fast_exp2(fmaf(s[r], a.scale_log2, -l4[c]));
-          if (need) {
+          for (int c = 0; c < 4; ++c) {
+            const int r = 4 * g + c;
             const int qq = qb0 + 8 * g + 4 * hf + c;
             bool ok = qq < a.lq;
             if (CAUSAL) ok = ok && key <= qq;
             if (HAS_MASK) ok = ok && key < a.lk && a.mask[(size_t)min(qq, a.lq - 1) * a.lk + min(key, a.lk - 1)];
-            p = ok ? p : 0.f;
+            const float p = ok ? fast_exp2(fmaf(s[r], a.scale_log2, -l4[c])) : 0.f;
+            s[r] = p;
+            dp[r] = p * (dp[r] - d4[c]);
           }
-          s[r] = p;
-          dp[r] = p * (dp[r] - d4[c]);
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const vf4 l4 = *reinterpret_cast<const vf4 *>(&Ls[cur][qb * 32 + 8 * g + 4 * hf]);
+          const vf4 d4 = *reinterpret_cast<const vf4 *>(&Ds[cur][qb * 32 + 8 * g + 4 * hf]);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const int r = 4 * g + c;
+            const float p = fast_exp2(fmaf(s[r], a.scale_log2, -l4[c]));
+            s[r] = p;
+            dp[r] = p * (dp[r] - d4[c]);
+          }
         }
       }
       if constexpr (STORE_DS) {
+        // wave-uniform block base plus this lane's fixed 32-bit byte offset
         const int qi = qb0 >> 5, kj = kw0 >> 5;
-        float *blk = a.ds + (size_t)bh * a.ds_bh + ((size_t)qi * (qi + 1) / 2 + kj) * 1024 +
-                     4 * hf * 32 + (li & 1) * 16 + (li >> 1);
+        char *blk = reinterpret_cast<char *>(a.ds + (size_t)bh * a.ds_bh + ((size_t)qi * (qi + 1) / 2 + kj) * 1024);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) blk[acc_row(r) * 32] = dp[r];
+        for (int r = 0; r < 16; ++r) *reinterpret_cast<float *>(blk + ds_lane + 128 * acc_row(r)) = dp[r];
       }
 
       // dV^T += dO^T P and dK^T += Q^T dS: MFMA step st pairs query rows
@@ -478,15 +494,20 @@ __global__ void __launch_bounds__(BW_THREADS, 2) flash_bwd_dq_kernel(const BwdAr
       // dS^T = P^T (dP^T - D); register r holds key kb0 + acc_row(r) + 4*hf.
       const bool need = HAS_MASK || kb0 + 31 > (CAUSAL ? min(qw0, a.lk - 1) : a.lk - 1);
       const int thr = key_last - kb0 - 4 * hf;
+      if (need) {  // separate branches, as in the dK/dV kernel
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float p = fast_exp2(fmaf(s[r], a.scale_log2, -lse_q));
-        if (need) {
+        for (int r = 0; r < 16; ++r) {
           bool ok = acc_row(r) <= thr;
           if (HAS_MASK) ok = ok && mrow[min(kb0 + acc_row(r) + 4 * hf, a.lk - 1)] != 0;
-          p = ok ? p : 0.f;
+          const float p = ok ? fast_exp2(fmaf(s[r], a.scale_log2, -lse_q)) : 0.f;
+          dp[r] = p * (dp[r] - d_q);
         }
-        dp[r] = p * (dp[r] - d_q);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = fast_exp2(fmaf(s[r], a.scale_log2, -lse_q));
+          dp[r] = p * (dp[r] - d_q);
+        }
       }
 
       // dQ^T += K^T dS^T
