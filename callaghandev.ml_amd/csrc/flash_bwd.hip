@@ -33,6 +33,7 @@ namespace {
 
 constexpr int BW_THREADS = 256;
 constexpr int BW_TILE = 128;  // keys (dK/dV) or queries (dQ) per workgroup
+constexpr int kBufferWord3 = 0x00020000;  // gfx9 buffer resource word 3: raw 32-bit dwords
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct BwdArgs {
@@ -215,8 +216,12 @@ __global__ void __launch_bounds__(BW_THREADS, (HD <= 32 && !HAS_MASK) ? 3 : (HD 
   sq.init(a.ldq);
   sg.init(a.lddo);
   float lreg = 0.f, dreg = 0.f;
-  // byte offset of this lane's dS entries in a stored block (row 4 hf + acc_row(r), key li)
-  const uint32_t ds_lane = 4u * (uint32_t)(4 * hf * 32 + (li & 1) * 16 + (li >> 1));
+  // The stored dS blocks of this (sequence, head) as a buffer resource (the
+  // launch keeps ds_bh * 4 bytes within 2^31), and the byte offset of this
+  // lane's entries in a block (row 4 hf + acc_row(r), key li).
+  const __amdgpu_buffer_rsrc_t ds_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      STORE_DS ? a.ds + (size_t)bh * a.ds_bh : nullptr, (short)0, STORE_DS ? (int)(a.ds_bh * 4) : 0, kBufferWord3);
+  const int ds_lane = 4 * (4 * hf * 32 + (li & 1) * 16 + (li >> 1));
   if (n_it > 0) {
     sq.load(qbase, a.ldq, q_begin, a.lq, a.hd);
     sg.load(gbase, a.lddo, q_begin, a.lq, a.hd);
@@ -317,11 +322,13 @@ __global__ void __launch_bounds__(BW_THREADS, (HD <= 32 && !HAS_MASK) ? 3 : (HD 
         }
       }
       if constexpr (STORE_DS) {
-        // wave-uniform block base plus this lane's fixed 32-bit byte offset
+        // buffer stores: the block's byte offset in a scalar register, this
+        // lane's fixed offset plus the row's immediate (one VGPR of address)
         const int qi = qb0 >> 5, kj = kw0 >> 5;
-        char *blk = reinterpret_cast<char *>(a.ds + (size_t)bh * a.ds_bh + ((size_t)qi * (qi + 1) / 2 + kj) * 1024);
+        const int boff = (qi * (qi + 1) / 2 + kj) * 4096;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) *reinterpret_cast<float *>(blk + ds_lane + 128 * acc_row(r)) = dp[r];
+        for (int r = 0; r < 16; ++r)
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(dp[r]), ds_rsrc, ds_lane + 128 * acc_row(r), boff, 0);
       }
 
       // dV^T += dO^T P and dK^T += Q^T dS: MFMA step st pairs query rows
@@ -1053,7 +1060,8 @@ int sdpa_bwd_impl(const float *q, int ldq, const float *k, int ldk, const float 
   if (vec && !mask) {
     const size_t extra = ds_bytes(batch, lq, lk, dim, num_heads, causal != 0);
     const size_t off = align256(need);  // the dS blocks follow the required workspace
-    if (extra && workspace_bytes >= off + extra) {
+    // (a (sequence, head)'s blocks must fit a buffer resource's 31-bit range)
+    if (extra && workspace_bytes >= off + extra && extra / bh <= (size_t)INT32_MAX) {
       a.ds = reinterpret_cast<float *>(ws + off);
       a.ds_bh = (long long)(extra / sizeof(float) / bh);
     }
