@@ -74,6 +74,11 @@ struct GemmArgs {
   int ldpre, lddz, ldadd, dact;
 };
 
+// The value of lane l ^ 1 (a DPP quad permutation [1, 0, 3, 2]).
+__device__ __forceinline__ float swap_pair(float y) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(y), 0xB1, 0xF, 0xF, false));
+}
+
 // Epilogue of both forward GEMM kernels with the rotary embedding of
 // AccelerationCPU.cs:4947-4975 folded in.  A lane holds column n of rows
 // mrow0 + 32 i + 8 (r / 4) + 4 hf + r % 4, so the pair partner of column n
@@ -96,22 +101,57 @@ __device__ __forceinline__ void store_rope(const GemmArgs &args, const GemmProbl
     odd[j] = c & 1;
     bias[j] = (P.bias && n[j] < args.N) ? P.bias[n[j]] : 0.f;
   }
-#pragma unroll
-  for (int i = 0; i < BI; ++i) {
+  // rows of block i: mb + dr(r), dr = 8 (r / 4) + 4 hf + r % 4
+  auto block = [&](int i, int mb, auto position) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int m = mrow0 + i * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
-      int pos = args.rope_pos0 + (args.rope_seg > 0 ? m % args.rope_seg : m);
-      pos = min(pos, args.rope_npos - 1);  // rows past M are never stored
+      const int dr = 8 * (r >> 2) + 4 * hf + (r & 3);
+      const int m = mb + dr;
+      const int pos = min(position(m, dr), args.rope_npos - 1);  // rows past M are never stored
       const float2 *cs = args.rope_cs + (size_t)pos * pairs;
 #pragma unroll
       for (int j = 0; j < BJ; ++j) {
         const float y = acc[i][j][r] + bias[j];
-        const float yp = __shfl_xor(y, 1);
+        const float yp = swap_pair(y);
         const float2 t = cs[pidx[j]];
         const float out = odd[j] ? yp * t.y + y * t.x : y * t.x - yp * t.y;
         if (m < args.M && n[j] < args.N) P.c[(size_t)m * args.ldc + n[j]] = out;
       }
+    }
+  };
+  const int seg = args.rope_seg;
+  // every row and column of this wave's blocks exists (wave-uniform)
+  const bool full = mrow0 + 32 * BI <= args.M && ncol0 + 32 * BJ <= args.N;
+#pragma unroll
+  for (int i = 0; i < BI; ++i) {
+    const int mb = mrow0 + i * 32;             // wave-uniform
+    const int pb = seg > 0 ? mb % seg : mb;    // position of row mb in its segment
+    if (seg <= 0 || pb + 31 < seg) {
+      if (full) {
+        // A whole block inside one segment: positions pos0 + pb + dr (every
+        // one inside the table, which the entry point checks), no predicates,
+        // and per row only wave-uniform offsets from the lane's bases.
+        const float2 *csb = args.rope_cs + (size_t)(args.rope_pos0 + pb + 4 * hf) * pairs;
+        float *cb = P.c + (size_t)(mb + 4 * hf) * args.ldc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int d = 8 * (r >> 2) + (r & 3);
+          const float2 *cs = csb + d * pairs;
+          float *c = cb + (size_t)d * args.ldc;
+#pragma unroll
+          for (int j = 0; j < BJ; ++j) {
+            const float y = acc[i][j][r] + bias[j];
+            const float yp = swap_pair(y);
+            const float2 t = cs[pidx[j]];
+            c[n[j]] = odd[j] ? yp * t.y + y * t.x : y * t.x - yp * t.y;
+          }
+        }
+      } else {
+        block(i, mb, [&](int, int dr) { return args.rope_pos0 + pb + dr; });
+      }
+    } else {
+      // a block across a segment boundary divides per row
+      block(i, mb, [&](int m, int) { return args.rope_pos0 + m % seg; });
     }
   }
 }
@@ -578,6 +618,27 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const Gem
   }
   // Epilogue: D[i][j] of block (bi, bj) sits at row 8*(r/4) + 4*hf + r%4,
   // column li; 32 lanes store 32 consecutive columns of one row.
+  if constexpr (!EPI) {
+    const int mw = m0 + wm * (TM / WM), nw = n0 + wn * (TN / WN);
+    if (!args.beta && mw + TM / WM <= M && nw + TN / WN <= N) {
+      // every row and column of this wave's blocks exists: no predicates, and
+      // per row only a wave-uniform offset from the lane's base
+      float bias[BJ];
+#pragma unroll
+      for (int j = 0; j < BJ; ++j) bias[j] = P.bias ? P.bias[nw + j * 32 + li] : 0.f;
+      float *cb = P.c + (size_t)(mw + 4 * hf) * args.ldc + nw + li;
+#pragma unroll
+      for (int i = 0; i < BI; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float *c = cb + (size_t)(i * 32 + 8 * (r >> 2) + (r & 3)) * args.ldc;
+#pragma unroll
+          for (int j = 0; j < BJ; ++j)
+            c[j * 32] = activate(acc[i][j][r] + bias[j], ACT == kActRope ? CDML_ACT_NONE : ACT);
+        }
+      return;
+    }
+  }
 #pragma unroll
   for (int j = 0; j < BJ; ++j) {
     const int n = n0 + wn * (TN / WN) + j * 32 + li;

@@ -61,7 +61,9 @@ def test_project_qkv_shapes(rows, ind, out):
 
 
 @pytest.mark.parametrize("act", [0, 1, 2, 3, 4, 5])
-@pytest.mark.parametrize("rows,ind,out", [(77, 64, 130), (300, 5, 256), (40, 16, 33), (3, 5, 7), (9, 12, 70)])
+@pytest.mark.parametrize("rows,ind,out", [(77, 64, 130), (300, 5, 256), (40, 16, 33), (3, 5, 7), (9, 12, 70),
+                                          (1024, 64, 256),   # 256x128 tiles, every wave block full
+                                          (300, 128, 256)])  # 128x128 tiles, full and ragged wave blocks
 def test_linear_with_activation(act, rows, ind, out):
     """BatchDotProductAddBias + activation on the tiled shape, a short
     reduction (the input projection of F 5 features, K 16) and few rows."""
@@ -126,6 +128,9 @@ def test_rope_table_values():
     (1024, 512, 512, 64, 0, 0),    # 256x128 tiles
     (300, 1024, 1024, 64, 0, 0),   # 128x128 tiles, ragged rows
     (150, 64, 64, 16, 50, 0),      # segmented positions (row % 50)
+    (1024, 256, 256, 32, 256, 0),  # segments of whole 32-row blocks, full tiles (unpredicated epilogue)
+    (1000, 128, 384, 64, 96, 5),   # block-aligned segments, ragged last tile, position offset
+    (600, 64, 128, 32, 40, 0),     # 128x128 tiles, blocks across segment boundaries
     (40, 96, 192, 32, 0, 17),      # position offset
     (33, 130, 36, 12, 0, 0),       # generic kernel (K not a multiple of 4)
 ])
@@ -138,12 +143,13 @@ def test_project_qkv_rope(rows, ind, out, hd, seg, off):
     wq, wk, wv = O.project_qkv(x, *args, mt=True)
     heads = out // hd
 
+    def at_offset(t):  # positions off, off + 1, ... (the reference rotates positions 0, 1, ...)
+        return O.rope(np.vstack([np.zeros((off, out), np.float32), t]), heads)[off:] if off else O.rope(t, heads)
+
     def rotated(t):
-        if seg:
-            return np.concatenate([O.rope(t[i:i + seg], heads) for i in range(0, rows, seg)])
-        if off:
-            return O.rope(np.vstack([np.zeros((off, out), np.float32), t]), heads)[off:]
-        return O.rope(t, heads)
+        if seg:  # positions off + (row % seg)
+            return np.concatenate([at_offset(t[i:i + seg]) for i in range(0, rows, seg)])
+        return at_offset(t)
 
     parity(q, rotated(wq), f"QKV+RoPE {rows}x{ind}->{out} Q")
     parity(k, rotated(wk), f"QKV+RoPE {rows}x{ind}->{out} K")
