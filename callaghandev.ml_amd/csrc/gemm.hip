@@ -131,19 +131,30 @@ __device__ __forceinline__ void store_rope(const GemmArgs &args, const GemmProbl
         // A whole block inside one segment: positions pos0 + pb + dr (every
         // one inside the table, which the entry point checks), no predicates,
         // and per row only wave-uniform offsets from the lane's bases.
-        const float2 *csb = args.rope_cs + (size_t)(args.rope_pos0 + pb + 4 * hf) * pairs;
-        float *cb = P.c + (size_t)(mb + 4 * hf) * args.ldc;
+        // The table entries of four rows are loaded before any of their
+        // stores: a load issued after a store waits for it (the memory
+        // counter covers both), which serialised one round trip per element.
+        // (Loading a group ahead, or eight rows at once, takes the kernel past
+        // 128 VGPRs and one of its two workgroups per CU.)
+        const float2 *__restrict__ csb = args.rope_cs + (size_t)(args.rope_pos0 + pb + 4 * hf) * pairs;
+        float *__restrict__ cb = P.c + (size_t)(mb + 4 * hf) * args.ldc;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int d = 8 * (r >> 2) + (r & 3);
-          const float2 *cs = csb + d * pairs;
-          float *c = cb + (size_t)d * args.ldc;
+        for (int g = 0; g < 4; ++g) {
+          float2 t[4][BJ];
 #pragma unroll
-          for (int j = 0; j < BJ; ++j) {
-            const float y = acc[i][j][r] + bias[j];
-            const float yp = swap_pair(y);
-            const float2 t = cs[pidx[j]];
-            c[n[j]] = odd[j] ? yp * t.y + y * t.x : y * t.x - yp * t.y;
+          for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+            for (int j = 0; j < BJ; ++j) t[rr][j] = csb[(8 * g + rr) * pairs + pidx[j]];
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            const int r = 4 * g + rr;
+            float *c = cb + (size_t)(8 * g + rr) * args.ldc;
+#pragma unroll
+            for (int j = 0; j < BJ; ++j) {
+              const float y = acc[i][j][r] + bias[j];
+              const float yp = swap_pair(y);
+              c[n[j]] = odd[j] ? yp * t[rr][j].y + y * t[rr][j].x : y * t[rr][j].x - yp * t[rr][j].y;
+            }
           }
         }
       } else {
@@ -635,6 +646,55 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const Gem
 #pragma unroll
           for (int j = 0; j < BJ; ++j)
             c[j * 32] = activate(acc[i][j][r] + bias[j], ACT == kActRope ? CDML_ACT_NONE : ACT);
+        }
+      return;
+    }
+  } else if constexpr (!TA) {
+    const int mw = m0 + wm * (TM / WM), nw = n0 + wn * (TN / WN);
+    if (!args.beta && mw + TM / WM <= M && nw + TN / WN <= N) {
+      // The training epilogue on a whole wave block: the dz and add operands
+      // of four rows are loaded before any of their stores (a load issued
+      // after a store waits for it), and every address is a lane base plus a
+      // wave-uniform row offset.
+      float bias[BJ];
+#pragma unroll
+      for (int j = 0; j < BJ; ++j) bias[j] = P.bias ? P.bias[nw + j * 32 + li] : 0.f;
+      const size_t lane_c = (size_t)(mw + 4 * hf) * args.ldc + nw + li;
+      const size_t lane_pre = (size_t)(mw + 4 * hf) * args.ldpre + nw + li;
+      const size_t lane_dz = (size_t)(mw + 4 * hf) * args.lddz + nw + li;
+      const size_t lane_add = (size_t)(mw + 4 * hf) * args.ldadd + nw + li;
+#pragma unroll
+      for (int i = 0; i < BI; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float zv[4][BJ], av[4][BJ];
+          if (args.dz) {
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+              for (int j = 0; j < BJ; ++j)
+                zv[rr][j] = args.dz[lane_dz + (size_t)(i * 32 + 8 * g + rr) * args.lddz + j * 32];
+          }
+          if (args.add) {
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+              for (int j = 0; j < BJ; ++j)
+                av[rr][j] = args.add[lane_add + (size_t)(i * 32 + 8 * g + rr) * args.ldadd + j * 32];
+          }
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            const int r = 4 * g + rr, d = i * 32 + 8 * g + rr;
+#pragma unroll
+            for (int j = 0; j < BJ; ++j) {
+              const float z = acc[i][j][r] + bias[j];
+              if (args.pre) args.pre[lane_pre + (size_t)d * args.ldpre + j * 32] = z;
+              float v = activate(z, ACT == kActRope ? CDML_ACT_NONE : ACT);
+              if (args.dz) v *= act_deriv(zv[rr][j], args.dact);
+              if (args.add) v += av[rr][j];
+              P.c[lane_c + (size_t)d * args.ldc + j * 32] = v;
+            }
+          }
         }
       return;
     }
