@@ -74,6 +74,25 @@ def test_linear_with_activation(act, rows, ind, out):
     parity(G.linear(x, w, b, act), want, f"linear {rows}x{ind}->{out} act={act}")
 
 
+@pytest.mark.parametrize("rows,ind,out,act", [(1024, 128, 256, 3), (300, 64, 160, 5), (2048, 256, 384, 0)])
+def test_linear_row_strides(rows, ind, out, act):
+    """cdml_linear with row strides above the widths (ldx = in + 8, ldy = out + 12):
+    the full wave blocks of the unpredicated epilogue and the ragged ones give
+    the oracle's result, and the stride padding of y keeps its sentinel."""
+    ldx, ldy = ind + 8, out + 12
+    x = synth.normal(31, (rows, ind))
+    w = synth.xavier_uniform(32, out, ind)
+    b = synth.normal(33, (out,))
+    xp = np.zeros((rows, ldx), np.float32)
+    xp[:, :ind] = x
+    yp = np.full((rows, ldy), 7.5, np.float32)
+    bx, bw, bb, by = G.up(xp), G.up(w), G.up(b), G.up(yp)
+    N.check(N.lib().cdml_linear(bx.ptr, ldx, bw.ptr, bb.ptr, by.ptr, ldy, rows, ind, out, act, G.stream().handle))
+    got = G.down(by, (rows, ldy))
+    assert np.all(got[:, out:] == 7.5), "cdml_linear wrote into the row stride padding"
+    parity(got[:, :out], O.activation(O.batch_dot_add_bias(w, x, b), act), f"strided linear {rows}x{ind}->{out}")
+
+
 def test_project_output_batch_reference_case():
     parity(G.linear(M(4, 6, 56), M(3, 6, 57), Vec(3, 58)),
            O.project_output_batch(M(4, 6, 56), M(3, 6, 57), Vec(3, 58)), "ProjectOutputBatch")
