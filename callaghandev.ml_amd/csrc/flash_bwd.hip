@@ -691,10 +691,6 @@ __global__ void __launch_bounds__(64 * (MAXQB / 2)) flash_bwd_dq_ds_short_kernel
     // (the loop is unrolled by PF, so every index is a constant and no
     // in-flight load is ever copied), and the load of block j + PF goes into
     // the buffer block j has just left.
-    // dS operands PF blocks ahead in a ring: block j lives in buf[j % PF]
-    // (the loop is unrolled by PF, so every index is a constant and no
-    // in-flight load is ever copied), and the load of block j + PF goes into
-    // the buffer block j has just left.
     constexpr int PF = 4;
     vf4 buf[PF][4];
 #pragma unroll
