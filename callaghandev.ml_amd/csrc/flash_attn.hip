@@ -706,12 +706,17 @@ void launch_sched(const FlashArgs &a, hipStream_t st) {
   // Pairs of causal tiles when one tile per workgroup would fit in a single
   // round of resident workgroups (four per CU), so that the round lasts as
   // long as its longest tile, and the pairs still give every CU two
-  // workgroups (fewer would leave SIMDs with a single wave).
+  // workgroups (fewer would leave SIMDs with a single wave).  Only for
+  // sequences of at most four query tiles: with more, one workgroup per tile
+  // (which keeps the no-maximum sub-block path) measured 3-6% faster
+  // (c2, 16 x 1024 with 8 heads of 64: 161-167 against 172-175 us; 8 x 2048
+  // heads of 64: 294-296 against 310 us), while 32 x 512 heads of 64 still
+  // gain 4-6% from pairs.
   const long long cus = num_cus();
   FlashArgs b = a;
   if constexpr (CAUSAL) {
     const long long pairs = (long long)a.n_bh * ((a.n_qt + 1) / 2);
-    if (a.n_qt > 1 && (long long)a.n_items <= 4 * cus && pairs >= 2 * cus) {
+    if (a.n_qt > 1 && a.n_qt <= 4 && (long long)a.n_items <= 4 * cus && pairs >= 2 * cus) {
       b.fast = 0;
       flash_fwd_kernel<HD, BN, CAUSAL, HAS_MASK, VEC, kPair><<<dim3((unsigned)pairs), dim3(FA_THREADS), 0, st>>>(b);
       return;
