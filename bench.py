@@ -430,8 +430,11 @@ def extras(N, st, only=None):
         # milliseconds of load, as for the headline leg
         r = bench_mha(N, st, 50, 40, c2)
         core, qkv, o = mha_flops(**c2)
+        tf2 = (core + qkv + o) / (r["wall_s"] / 50) / 1e12
         out["c2_mha_layer"] = {"ms": round(r["wall_s"] / 50 * 1e3, 4),
-                               "tflops": round((core + qkv + o) / (r["wall_s"] / 50) / 1e12, 2),
+                               "tflops": round(tf2, 2),
+                               "frac_of_fp32_mfma_peak": round(tf2 / FP32_MFMA_PEAK_TFLOPS, 4),
+                               "tokens_per_s": round(16 * 1024 / (r["wall_s"] / 50), 1),
                                "flash_ms": round(r["flash_ms"], 4)}
     if want("c3_mha_layer_backward"):
         log("[bench] extras: c3 MHA layer backward")
@@ -536,11 +539,14 @@ def extras(N, st, only=None):
         fl5 = 6 * (core + qkv + o + 4 * 256 * 512 * 256 * 1024) + 2 * 256 * 512 * 256 * (5 + 1)
         del dev5, lm5
         # the model's attention shape alone (d_h 32): flash kernel by events
-        r5 = bench_mha(N, st, 10, 5, dict(batch=256, seq=512, dim=256, heads=8))
+        r5 = bench_mha(N, st, 10, 20, dict(batch=256, seq=512, dim=256, heads=8))
         core5 = mha_flops(256, 512, 256, 8)[0]
         fa5 = core5 / (r5["flash_ms"] * 1e-3) / 1e12
-        out["c5_time_series_model"] = {"ms": round(ms5, 3), "tflops": round(fl5 / (ms5 * 1e-3) / 1e12, 2),
+        tf5 = fl5 / (ms5 * 1e-3) / 1e12
+        out["c5_time_series_model"] = {"ms": round(ms5, 3), "tflops": round(tf5, 2),
+                                       "frac_of_fp32_mfma_peak": round(tf5 / FP32_MFMA_PEAK_TFLOPS, 4),
                                        "windows_per_s": round(256 / (ms5 * 1e-3), 1),
+                                       "tokens_per_s": round(256 * 512 / (ms5 * 1e-3), 1),
                                        "attention_kernel_ms": round(r5["flash_ms"], 4),
                                        "attention_kernel_tflops": round(fa5, 2),
                                        "attention_kernel_frac_of_fp32_mfma_peak":
@@ -558,8 +564,15 @@ def extras(N, st, only=None):
         for _ in range(5):
             dev1.GenerateGreedy(ids[:, :32], 20)
         gen_ms = (time.perf_counter() - t0) / 5 * 1e3
+        # forward matmul FLOPs: 2 layers of MHA and FFN 64 -> 128 -> 64, and the LM head
+        core1, qkv1, o1 = mha_flops(4, 64, 64, 4)
+        fl1 = 2 * (core1 + qkv1 + o1 + 4 * 256 * 64 * 128) + 2 * 256 * 64 * 200
+        tf1 = fl1 / (ms1 * 1e-3) / 1e12
         out["c1_text_model"] = {"forward_ms": round(ms1, 4),
                                 "forward_tokens_per_s": round(256 / (ms1 * 1e-3), 1),
+                                "forward_tflops": round(tf1, 3),
+                                "forward_frac_of_fp32_mfma_peak": round(tf1 / FP32_MFMA_PEAK_TFLOPS, 5),
+                                "note": "latency-bound (44 MFLOP per forward)",
                                 "generate_20_tokens_batch4_ms": round(gen_ms, 3),
                                 "generated_tokens_per_s": round(80 / (gen_ms * 1e-3), 1)}
     return out
