@@ -14,14 +14,17 @@
 // spread over G adjacent lanes, G the smallest power of two that leaves a
 // lane at most 8 float4 loads, all issued before the first is used, and
 // the G partial sums meet in a butterfly of shuffles; P V splits the keys
-// over 256 / D thread groups, each with 8 V loads in flight.  The softmax
-// is one wave per head.
+// over kTinyThreads / D thread groups, each with 8 V loads in flight.  The
+// softmax is one wave per head.
 #include "common.h"
 
 namespace cdml {
 namespace {
 
-constexpr int kTinyThreads = 256;
+// 512 threads per sequence: c1 generation 0.69 -> 0.64 ms against 256 (the
+// projections and the LM head take one pass of dot products instead of two);
+// 1024 measured 0.68 ms (the barriers cost more than the passes save)
+constexpr int kTinyThreads = 512;
 constexpr int kTinyMaxDim = 256;
 constexpr int kTinyMaxFF = 1024;
 constexpr int kTinyMaxScores = 4096;  // heads * MaxSequenceLength
@@ -222,7 +225,7 @@ __global__ void __launch_bounds__(kTinyThreads) tiny_decode_kernel(const cdml_ti
         for (int j = lane; j < nk; j += 64) sc[hh * S + j] *= inv;
       }
       __syncthreads();
-      // att[e] = sum_j p[head(e)][j] v_j[e]: group g of the 256 / D thread
+      // att[e] = sum_j p[head(e)][j] v_j[e]: group g of the kTinyThreads / D thread
       // groups takes keys g, g + groups, ..., 8 V loads in flight per lane
       {
         const int groups = kTinyThreads / D, g = t / D, e = t % D;
