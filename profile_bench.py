@@ -25,6 +25,8 @@ to --out (default gpurun_out/profile_bench); the summaries go to profiles/:
                                         -> mha_backward_c3_kernel_stats.md
   train     kernel traces of the three training-step legs
                                         -> train_step_{c1,c3_shape,c5}_kernel_stats.md
+  c1        kernel trace + stats of the config-1 text model leg (forward and
+            greedy generation)          -> c1_text_model_generate_kernel_stats.md
   probe     builds and runs csrc/probes/issue_rates.hip
                                         -> gfx950_issue_rates.md
 """
@@ -46,7 +48,7 @@ sys.path.insert(0, ROOT)
 import bench  # noqa: E402  (TRAFFIC_SOURCES, source_digest)
 
 PROFILES = os.path.join(ROOT, "profiles")
-PASSES = ("trace", "traffic", "counters", "trainc5", "backward", "train", "probe")
+PASSES = ("trace", "traffic", "counters", "trainc5", "backward", "train", "c1", "probe")
 COUNTERS_A = ("GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES SQ_INSTS_VALU_MFMA_F32 "
               "SQ_INSTS_VALU SQ_INSTS_VALU_TRANS_F32 SQ_INSTS_LDS SQ_LDS_BANK_CONFLICT")
 COUNTERS_B = ("GRBM_GUI_ACTIVE SQ_WAVES SQ_WAVE_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_ACTIVE_INST_VALU "
@@ -350,6 +352,22 @@ def pass_train(out):
                 f"the same run: {b.get('ms')} ms per step, {b.get('tflops')} TFLOP/s by its count.  Kernel "
                 f"time summed over the trace: {total / steps:.2f} ms per step.")
         write(name, header(f"Kernel durations: {what}", [cmd], note) + "\n" + "\n".join(lines) + "\n")
+
+
+def pass_c1(out):
+    d = os.path.join(out, "c1")
+    so, cmd = rocprof(["--kernel-trace", "--stats"], d, ["--only", "c1_text_model"], 300, os.path.join(out, "c1.log"))
+    leg = bench_line(so).get("other_configs", {}).get("c1_text_model", {})
+    note = ("`bench.py --only c1_text_model` builds the config-1 model (vocabulary 200, D 64, 4 heads, 2 layers, "
+            "FF 128, MaxSeq 64) as a `DeviceLanguageModel` for 4 sequences and runs 100 forwards of 4 x 64 tokens "
+            "(50 warm-up + 50 timed), then 6 `GenerateGreedy` calls (1 warm-up + 5 timed), each a 32-token prompt "
+            "and 20 new tokens: the batched prompt prefill (embedding, 2 layers, LM head on each sequence's last "
+            "row, argmax), then the other 19 greedy steps of all 4 sequences in one `tiny_decode_kernel` launch.  "
+            f"The bench line of the same run: forward {leg.get('forward_ms')} ms, generation "
+            f"{leg.get('generate_20_tokens_batch4_ms')} ms.")
+    write("c1_text_model_generate_kernel_stats.md",
+          header("Kernel durations: config-1 text model, forward and greedy generation", [cmd], note) + "\n" +
+          stats_table(read_stats(d)) + "\n")
 
 
 def pass_probe(out):
