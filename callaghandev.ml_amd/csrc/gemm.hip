@@ -1276,7 +1276,11 @@ int launch_gemm(GemmArgs &g, bool ta, bool tb, hipStream_t stream, const char *w
           : gemm_rows_kernel<16, false><<<grid, block, 0, stream>>>(g);
     return check_launch(what);
   }
-  if (fast && g.M >= 1024) {
+  // 256 x 128 tiles unless they would not fill one round of two workgroups
+  // per CU: then 128 x 128 tiles spread the same work over twice as many
+  // workgroups (16384 x 512 -> 512: 81 -> 78 us, same bits).
+  const long long big_tiles_fwd = (long long)((g.M + 255) / 256) * ((g.N + 127) / 128) * g.nprob;
+  if (fast && g.M >= 1024 && big_tiles_fwd >= 2 * num_cus()) {
     int rc = launch_tile<256, 128, 16, 4, 2, 2, false, false>(g, stream);
     if (rc) return rc;
   } else if (fast) {
