@@ -673,6 +673,52 @@ def cpu_baseline(sample_seqs=3):
                        f"{dt:.1f} s")
 
 
+def cpu_baseline_other_configs(threads):
+    """The same restatement on bounded samples of the other MFMA configs (c2,
+    c5: the MHA forward of one layer per sequence, as LanguageModel.Forward
+    calls it) and on the c4 decode step, whose reference
+    (LanguageModel.DecoderSelfAttentionStep) is inline and single-threaded:
+    timed sequentially over the batch as the reference runs it, and with the
+    batch spread over the threads (labelled).  Timed, not checked."""
+    from oracle import oracle as O
+    from cdml import synth
+
+    out = {}
+    rng = np.random.default_rng(6)
+    for name, (B, L, D, H, n) in (("c2", (16, 1024, 512, 8, 4)), ("c5", (256, 512, 256, 8, 64))):
+        ws = [synth.xavier_uniform(40 + i, D, D) for i in range(4)]
+        bz = np.zeros(D, np.float32)
+        xs = [rng.standard_normal((L, D), dtype=np.float32) for _ in range(n)]
+        t0 = time.perf_counter()
+        for x in xs:
+            q, k, v = O.project_qkv(x, ws[0], bz, ws[1], bz, ws[2], bz, mt=True)
+            q, k = O.rope(q, H, mt=True), O.rope(k, H, mt=True)
+            a = O.sdpa(q, k, v, H, causal=True, mt=True)
+            O.project_output_batch(a, ws[3], bz, mt=True)
+        dt = time.perf_counter() - t0
+        core, qkv, o = mha_flops(n, L, D, H)
+        out[name] = {"value": round((core + qkv + o) / dt / 1e12, 6), "unit": "TFLOP/s", "seconds": round(dt, 3),
+                     "sample": f"{n} of the {B} sequences (L {L}, D {D}, H {H}), MHA layer forward, {threads} threads"}
+    B, T, D, H = 8, C4["t"], C4["dim"], C4["heads"]
+    q = rng.standard_normal((B, D), dtype=np.float32)
+    kc = rng.standard_normal((B, T, D), dtype=np.float32)
+    vc = rng.standard_normal((B, T, D), dtype=np.float32)
+    lens = np.full(B, T, np.int32)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D // H)))
+    nbytes = decode_bytes(B, T, D)
+    dec = {}
+    for label, parallel in (("sequential", False), ("parallel_over_batch", True)):
+        O.decode_attention_batch(q[:1], kc[:1, :64], vc[:1, :64], lens[:1] * 0 + 64, H, scale, parallel)
+        t0 = time.perf_counter()
+        O.decode_attention_batch(q, kc, vc, lens, H, scale, parallel)
+        dt = time.perf_counter() - t0
+        dec[label] = {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "ms_per_step_of_64": round(dt / B * 64 * 1e3, 3)}
+    dec["sample"] = (f"{B} of the 64 decode rows (KV {T}, D {D}, H {H}); the sequential form runs one thread as "
+                     f"the reference's inline step does, the parallel one spreads the rows over {threads} threads")
+    out["c4_decode"] = dec
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -761,6 +807,7 @@ def main():
         log("[bench] CPU baseline (multi-threaded restatement)")
         cb = cpu_baseline()
         res["cpu_baseline"] = {k: (round(v, 6) if isinstance(v, float) else v) for k, v in cb.items()}
+        res["cpu_baseline"]["other_configs"] = cpu_baseline_other_configs(cb["cores"])
     print(json.dumps(res), flush=True)
 
 
