@@ -8,7 +8,8 @@ built:
 Each pass runs `rocprofv3 ... -- python3 bench.py ...` (or the probe) as a
 child process under `timeout -s KILL`; the first pass that fails ends the
 script, so no further GPU work follows a failure.  Raw rocprofv3 output goes
-to --out (default gpurun_out/profile_bench); the summaries go to profiles/:
+to --out (a scratch folder, never committed); the summaries go to profiles/
+(or --profiles-dir):
 
   trace     kernel trace + stats of bench.py's headline (c3) and decode (c4)
             legs                        -> mha_c3_decode_c4_kernel_stats.md
