@@ -62,19 +62,22 @@ def test_project_qkv_shapes(rows, ind, out):
 
 @pytest.mark.parametrize("act", [0, 1, 2, 3, 4, 5])
 @pytest.mark.parametrize("rows,ind,out", [(77, 64, 130), (300, 5, 256), (40, 16, 33), (3, 5, 7), (9, 12, 70),
-                                          (1024, 64, 256),   # 256x128 tiles, every wave block full
-                                          (300, 128, 256)])  # 128x128 tiles, full and ragged wave blocks
+                                          (1024, 64, 256),    # 128x128 tiles (256x128 would not fill a round)
+                                          (300, 128, 256),    # 128x128 tiles, full and ragged wave blocks
+                                          (16384, 64, 1024),  # 512 tiles of 256x128, every wave block full
+                                          (16484, 64, 1000)])  # 256x128 tiles, ragged last row and column tiles
 def test_linear_with_activation(act, rows, ind, out):
-    """BatchDotProductAddBias + activation on the tiled shape, a short
-    reduction (the input projection of F 5 features, K 16) and few rows."""
+    """BatchDotProductAddBias + activation on both tile configurations, a
+    short reduction (the input projection of F 5 features, K 16) and few rows."""
     x = synth.normal(3, (rows, ind))
     w = synth.xavier_uniform(4, out, ind)
     b = synth.normal(5, (out,))
-    want = O.activation(O.batch_dot_add_bias(w, x, b), act)
+    want = O.activation(O.batch_dot_add_bias(w, x, b, mt=rows > 4096), act)
     parity(G.linear(x, w, b, act), want, f"linear {rows}x{ind}->{out} act={act}")
 
 
-@pytest.mark.parametrize("rows,ind,out,act", [(1024, 128, 256, 3), (300, 64, 160, 5), (2048, 256, 384, 0)])
+@pytest.mark.parametrize("rows,ind,out,act", [(1024, 128, 256, 3), (300, 64, 160, 5), (2048, 256, 384, 0),
+                                              (16384, 64, 1024, 3)])  # 256x128 tiles
 def test_linear_row_strides(rows, ind, out, act):
     """cdml_linear with row strides above the widths (ldx = in + 8, ldy = out + 12):
     the full wave blocks of the unpredicated epilogue and the ragged ones give
@@ -90,7 +93,8 @@ def test_linear_row_strides(rows, ind, out, act):
     N.check(N.lib().cdml_linear(bx.ptr, ldx, bw.ptr, bb.ptr, by.ptr, ldy, rows, ind, out, act, G.stream().handle))
     got = G.down(by, (rows, ldy))
     assert np.all(got[:, out:] == 7.5), "cdml_linear wrote into the row stride padding"
-    parity(got[:, :out], O.activation(O.batch_dot_add_bias(w, x, b), act), f"strided linear {rows}x{ind}->{out}")
+    parity(got[:, :out], O.activation(O.batch_dot_add_bias(w, x, b, mt=rows > 4096), act),
+           f"strided linear {rows}x{ind}->{out}")
 
 
 def test_project_output_batch_reference_case():
@@ -144,7 +148,9 @@ def test_rope_table_values():
 
 
 @pytest.mark.parametrize("rows,ind,out,hd,seg,off", [
-    (1024, 512, 512, 64, 0, 0),    # 256x128 tiles
+    (1024, 512, 512, 64, 0, 0),    # 128x128 tiles (256x128 would not fill a round)
+    (16384, 64, 384, 64, 1024, 0),  # 576 tiles of 256x128 over 1024-row sequences, full wave blocks
+    (16484, 64, 384, 32, 0, 3),    # 256x128 tiles, ragged last row tile, position offset
     (300, 1024, 1024, 64, 0, 0),   # 128x128 tiles, ragged rows
     (150, 64, 64, 16, 50, 0),      # segmented positions (row % 50)
     (1024, 256, 256, 32, 256, 0),  # segments of whole 32-row blocks, full tiles (unpredicated epilogue)
