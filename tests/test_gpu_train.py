@@ -24,12 +24,14 @@ def parity(a, e, what=""):
 
 
 @pytest.mark.parametrize("rows,ind,out,act", [(64, 64, 128, 3), (300, 256, 1024, 3), (77, 130, 33, 1),
-                                              (1024, 512, 2048, 5), (40, 32, 64, 2)])
+                                              (1024, 512, 2048, 5), (40, 32, 64, 2),
+                                              (16384, 64, 1024, 3),   # 256x128 tiles, full wave blocks
+                                              (16484, 64, 1000, 1)])  # 256x128 tiles, ragged row and column tiles
 def test_linear_preact(rows, ind, out, act):
     """The FFN hidden layer with its cache: z = x W^T + b, y = act(z)."""
     x, w, b = synth.normal(1, (rows, ind)), synth.xavier_uniform(2, out, ind), synth.normal(3, (out,))
     z, y = G.linear_preact(x, w, b, act)
-    zw = O.batch_dot_add_bias(w, x, b)
+    zw = O.batch_dot_add_bias(w, x, b, mt=rows > 4096)
     parity(z, zw, "pre-activation")
     parity(y, O.activation(zw, act), "activation")
     assert np.array_equal(y, O.activation(z, act)) if act == 3 else True  # ReLU of the stored z, exactly
