@@ -22,9 +22,8 @@ namespace cdml {
 namespace {
 
 constexpr int DC_THREADS = 256;
-constexpr int DC_CHUNK = 256;                // keys per workgroup
-constexpr int DC_KITER = DC_CHUNK / 4 / 8;   // steps of 8 keys per wave
-static_assert(DC_KITER % 2 == 0, "the key loop alternates two register sets");
+constexpr int DC_CHUNK = 256;       // keys per workgroup (the partials are sized for it)
+constexpr int DC_CHUNK_WIDE = 512;  // keys per workgroup when the grid stays wide
 
 struct DecodeArgs {
   const float *q, *kc, *vc;
@@ -71,8 +70,10 @@ __device__ __forceinline__ void merge_state(float &m, float &l, float (&o)[EPL],
   m = mn;
 }
 
-template <int HD>
+template <int HD, int CHUNK>
 __global__ void __launch_bounds__(DC_THREADS) decode_split_kernel(const DecodeArgs a) {
+  constexpr int KITER = CHUNK / 4 / 8;  // steps of 8 keys per wave
+  static_assert(KITER % 2 == 0, "the key loop alternates two register sets");
   constexpr int VW = HD >= 32 ? 4 : 2;  // floats per vector load
   constexpr int NV = HD / (8 * VW);     // vector loads per lane per row
   constexpr int EPL = VW * NV;          // head dims per lane (= HD / 8)
@@ -83,7 +84,7 @@ __global__ void __launch_bounds__(DC_THREADS) decode_split_kernel(const DecodeAr
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 3, e = lane & 7;
   const int len = min(max(a.kv_len[b], 0), a.t_max);
-  const int chunk0 = split * DC_CHUNK;
+  const int chunk0 = split * CHUNK;
   float *part = a.part + ((size_t)(b * a.heads + h) * a.nsplit + split) * (HD + 2);
 
   if (chunk0 >= len) {
@@ -97,7 +98,7 @@ __global__ void __launch_bounds__(DC_THREADS) decode_split_kernel(const DecodeAr
 
   const float *kb = a.kc + (size_t)b * a.t_max * a.dim + col;
   const float *vb = a.vc + (size_t)b * a.t_max * a.dim + col;
-  const int key0 = chunk0 + wave * (DC_KITER * 8) + g;
+  const int key0 = chunk0 + wave * (KITER * 8) + g;
 
   float m = -INFINITY, l = 0.f;
   float o[EPL];
@@ -132,12 +133,12 @@ __global__ void __launch_bounds__(DC_THREADS) decode_split_kernel(const DecodeAr
   load_slice<VW, NV>(kb + (size_t)min(key0, last) * a.dim, k0r);
   load_slice<VW, NV>(vb + (size_t)min(key0, last) * a.dim, v0r);
 #pragma unroll
-  for (int it = 0; it < DC_KITER; it += 2) {
+  for (int it = 0; it < KITER; it += 2) {
     const int k1 = min(key0 + (it + 1) * 8, last);
     load_slice<VW, NV>(kb + (size_t)k1 * a.dim, k1r);
     load_slice<VW, NV>(vb + (size_t)k1 * a.dim, v1r);
     step(it, k0r, v0r);
-    if (it + 2 < DC_KITER) {
+    if (it + 2 < KITER) {
       const int k2 = min(key0 + (it + 2) * 8, last);
       load_slice<VW, NV>(kb + (size_t)k2 * a.dim, k0r);
       load_slice<VW, NV>(vb + (size_t)k2 * a.dim, v0r);
@@ -369,29 +370,33 @@ static int decode_launch(const float *q, const float *kcache, const float *vcach
   const bool vec = fast_hd(a.hd) && dim % 4 == 0 && aligned16(q) && aligned16(kcache) &&
                    aligned16(vcache);
   if (vec) {
-    const dim3 cgrid(num_heads, batch);
-    switch (a.hd) {
-      case 16:
-        decode_split_kernel<16><<<grid, DC_THREADS, 0, st>>>(a);
-        decode_combine_vec_kernel<16><<<cgrid, DC_THREADS, 0, st>>>(a);
-        break;
-      case 32:
-        decode_split_kernel<32><<<grid, DC_THREADS, 0, st>>>(a);
-        decode_combine_vec_kernel<32><<<cgrid, DC_THREADS, 0, st>>>(a);
-        break;
-      case 64:
-        decode_split_kernel<64><<<grid, DC_THREADS, 0, st>>>(a);
-        decode_combine_vec_kernel<64><<<cgrid, DC_THREADS, 0, st>>>(a);
-        break;
-      case 128:
-        decode_split_kernel<128><<<grid, DC_THREADS, 0, st>>>(a);
-        decode_combine_vec_kernel<128><<<cgrid, DC_THREADS, 0, st>>>(a);
-        break;
-      default:
-        decode_split_kernel<256><<<grid, DC_THREADS, 0, st>>>(a);
-        decode_combine_vec_kernel<256><<<cgrid, DC_THREADS, 0, st>>>(a);
-        break;
+    // 512-key chunks while they still give the launch four workgroups per CU
+    // (c4: 1.26 -> 1.23 ms); shorter caches and small batches keep 256 for
+    // the parallelism.  Fewer chunks fit the partials sized for 256.
+    const int nsplit_wide = (t_max + DC_CHUNK_WIDE - 1) / DC_CHUNK_WIDE;
+    const bool wide = (long long)nsplit_wide * num_heads * batch >= 4LL * num_cus();
+    if (wide) {
+      a.nsplit = nsplit_wide;
+      grid.x = nsplit_wide;
     }
+    const dim3 cgrid(num_heads, batch);
+#define CDML_DECODE_CASE(HDV)                                                              \
+  case HDV:                                                                                \
+    if (wide)                                                                              \
+      decode_split_kernel<HDV, DC_CHUNK_WIDE><<<grid, DC_THREADS, 0, st>>>(a);             \
+    else                                                                                   \
+      decode_split_kernel<HDV, DC_CHUNK><<<grid, DC_THREADS, 0, st>>>(a);                  \
+    decode_combine_vec_kernel<HDV><<<cgrid, DC_THREADS, 0, st>>>(a);                       \
+    break;
+    switch (a.hd) {
+      CDML_DECODE_CASE(16)
+      CDML_DECODE_CASE(32)
+      CDML_DECODE_CASE(64)
+      CDML_DECODE_CASE(128)
+      default:
+      CDML_DECODE_CASE(256)
+    }
+#undef CDML_DECODE_CASE
     return check_launch("decode_split_kernel/decode_combine_vec_kernel");
   }
   decode_split_generic_kernel<<<grid, 256, sizeof(float) * (256 + 8), st>>>(a);

@@ -634,6 +634,20 @@ def test_decode_vs_oracle(B, T, D, H):
     parity(got, want, f"decode B={B} T={T} D={D} H={H}")
 
 
+def test_decode_wide_grid_ragged_lengths():
+    """A launch wide enough for 512-key chunks (64 sequences x 8 heads x 2 chunks),
+    with lengths on both sides of the chunk boundaries, against the oracle."""
+    B, T, D, H = 64, 1000, 512, 8
+    q = synth.normal(61, (B, D))
+    kc, vc = synth.normal(62, (B, T, D)), synth.normal(63, (B, T, D))
+    base = [1000, 999, 513, 512, 511, 257, 256, 1, 700, 2]
+    lens = np.array([base[i % len(base)] for i in range(B)], np.int32)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D // H)))
+    got = G.decode(q, kc, vc, lens, H, scale)
+    want = O.decode_attention_batch(q, kc, vc, lens, H, scale, parallel=True)
+    parity(got, want, "decode wide grid, ragged lengths")
+
+
 def test_decode_equals_last_prefill_row():
     T, D, H = 700, 512, 4
     q, k, v = (synth.normal(50 + i, (T, D)) for i in range(3))
