@@ -370,6 +370,17 @@ PYBIND11_MODULE(_cdml_host, m) {
                return a.BackpropOutputProjection(DL.view, X.view, W.view, WG, BG, seqLen, outputDim, embeddingDim);
              }));
            })
+      .def("BackpropInputProjection",
+           [](HipAccelerationManager &a, py::object dx, py::object x, int rowStart, py::object wg, py::object bg,
+              int seqLen, int embeddingDim, int inputFeatureDim) {
+             auto DX = mat(dx), X = mat(x);
+             MatRef WG = mat_inout(wg);
+             VecRef BG = vec_inout(bg);
+             nogil([&] {
+               a.BackpropInputProjection(DX.view, X.view, rowStart, WG, BG, seqLen, embeddingDim, inputFeatureDim);
+               return 0;
+             });
+           })
       .def("MatrixMultiply",
            [](HipAccelerationManager &a, py::object A, py::object B) {
              auto X = mat(A), Y = mat(B);
@@ -654,6 +665,7 @@ PYBIND11_MODULE(_cdml_host, m) {
       .def_readwrite("GradientClipThreshold", &TrainingConfig::GradientClipThreshold)
       .def_readwrite("UseLearningRateDecay", &TrainingConfig::UseLearningRateDecay)
       .def_readwrite("LearningRateDecay", &TrainingConfig::LearningRateDecay)
+      .def_readwrite("ValidationInterval", &TrainingConfig::ValidationInterval)
       .def_readwrite("Verbose", &TrainingConfig::Verbose);
 
   auto seqs_from = [](const py::object &o) {
@@ -703,19 +715,65 @@ PYBIND11_MODULE(_cdml_host, m) {
            },
            py::arg("batch"), py::arg("learningRate"))
       .def("Train",
-           [seqs_from](TransformerTrainer &t, py::object seqs, uint64_t seed) {
+           [seqs_from](TransformerTrainer &t, py::object seqs, uint64_t seed, py::object val) {
              auto b = seqs_from(seqs);
-             return nogil([&] { return t.Train(b, seed); });
+             std::vector<std::vector<int>> v;
+             if (!val.is_none()) v = seqs_from(val);
+             return nogil([&] { return t.Train(b, seed, val.is_none() ? nullptr : &v); });
            },
-           py::arg("sequences"), py::arg("seed") = 0)
+           py::arg("sequences"), py::arg("seed") = 0, py::arg("validationSequences") = py::none())
+      .def("TrainBatchContinuous",
+           [cont_from](TransformerTrainer &t, py::object inputs, py::object reg, py::object cls, float lr) {
+             std::vector<Matrix> xs, rs;
+             std::vector<std::vector<int>> cs;
+             cont_from(inputs, reg, cls, xs, rs, cs);
+             return nogil([&] {
+               return t.TrainBatchContinuous(xs, reg.is_none() ? nullptr : &rs, cls.is_none() ? nullptr : &cs, lr);
+             });
+           },
+           py::arg("inputs"), py::arg("regressionTargets") = py::none(), py::arg("classTargets") = py::none(),
+           py::arg("learningRate") = 0.0001f)
+      .def("TrainContinuous",
+           [cont_from](TransformerTrainer &t, py::object inputs, py::object reg, py::object cls, uint64_t seed) {
+             std::vector<Matrix> xs, rs;
+             std::vector<std::vector<int>> cs;
+             cont_from(inputs, reg, cls, xs, rs, cs);
+             return nogil([&] {
+               return t.TrainContinuous(xs, reg.is_none() ? nullptr : &rs, cls.is_none() ? nullptr : &cs, seed);
+             });
+           },
+           py::arg("inputs"), py::arg("regressionTargets") = py::none(), py::arg("classTargets") = py::none(),
+           py::arg("seed") = 0)
+      .def("Validate",
+           [seqs_from](TransformerTrainer &t, py::object seqs) {
+             auto b = seqs_from(seqs);
+             return nogil([&] { return t.Validate(b); });
+           },
+           py::arg("validationSequences"))
+      .def("ValidateContinuous",
+           [cont_from](TransformerTrainer &t, py::object inputs, py::object reg, py::object cls) {
+             std::vector<Matrix> xs, rs;
+             std::vector<std::vector<int>> cs;
+             cont_from(inputs, reg, cls, xs, rs, cs);
+             return nogil([&] {
+               return t.ValidateContinuous(xs, reg.is_none() ? nullptr : &rs, cls.is_none() ? nullptr : &cs);
+             });
+           },
+           py::arg("inputs"), py::arg("regressionTargets") = py::none(), py::arg("classTargets") = py::none())
       .def_property_readonly("last_norm", &TransformerTrainer::last_norm)
+      .def_property_readonly("validation_losses", &TransformerTrainer::validation_losses)
       .def("gradients",
            // the gradients the last update applied (after the 1/validCount and
            // clipping scales), flat names as DeviceTrainer.gradients()
            [](const TransformerTrainer &t) {
              const auto &g = t.gradients();
              py::dict d;
-             d["token_embedding"] = to_numpy(g.TokenEmbeddingGrad);
+             if (!g.InputProjectionBiasGrad.empty()) {
+               d["input_proj"] = to_numpy(g.InputProjectionGrad);
+               d["input_bias"] = vec_to_numpy(g.InputProjectionBiasGrad);
+             } else {
+               d["token_embedding"] = to_numpy(g.TokenEmbeddingGrad);
+             }
              d["out_proj"] = to_numpy(g.OutputProjectionGrad);
              d["out_bias"] = vec_to_numpy(g.OutputBiasGrad);
              for (size_t i = 0; i < g.AttentionGrads.size(); ++i) {

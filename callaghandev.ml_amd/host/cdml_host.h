@@ -259,6 +259,13 @@ class HipAccelerationManager {
   Matrix BackpropOutputProjection(MatView dLogits, MatView input, MatView weights,
                                   MatRef weightGrad, VecRef biasGrad, int seqLen, int outputDim,
                                   int embeddingDim);
+  // IAccelerationManager.BackpropInputProjection (:197): weightGrad
+  // [embeddingDim, inputFeatureDim] += dX^T continuousInput[inputRowStart ..
+  // inputRowStart + seqLen, 0 .. inputFeatureDim), biasGrad += column sums of
+  // dX.  dX is read as seqLen rows of embeddingDim floats from its start, as
+  // the reference's flat span does.
+  void BackpropInputProjection(MatView dX, MatView continuousInput, int inputRowStart, MatRef weightGrad,
+                               VecRef biasGrad, int seqLen, int embeddingDim, int inputFeatureDim);
 
   // ---- the rest of the training step with real work per call ---------------
   // IAccelerationManager.MatrixMultiply (:20) / MatrixMultiplyTranspose (:26)
@@ -550,6 +557,11 @@ class LanguageModel {
   LanguageModel(const TransformerConfig &cfg, HipAccelerationManager *accel);
   Matrix Forward(const std::vector<int> &tokenIds);
   Matrix Forward(MatView inputSequence);  // continuous inputs (InputProjection)
+  // ForwardTokenSlice / ForwardContinuousSlice (LanguageModel.cs:135-157):
+  // the forward pass of rows [start, start + count) of a sequence, which the
+  // trainer's Validate / ValidateContinuous call.
+  Matrix ForwardTokenSlice(const std::vector<int> &tokenIds, int tokenStart, int tokenCount);
+  Matrix ForwardContinuousSlice(MatView inputSequence, int rowStart, int rowCount);
   // Greedy: argmax with the lowest index on ties.  Otherwise logits / T are
   // sampled with the SplitMix64 stream seeded by `seed` (the reference uses
   // System.Random, which this does not reproduce).
@@ -662,8 +674,10 @@ class DeviceLanguageModel {
 // TrainingConfig (Transformers/Configuration/SharedConfigs.cs:24-60) is below.
 struct TrainingConfig;
 
-// Transformers/MultiTypeTransformer/TransformerTrainer.cs restated for
-// decoder token models on HipAccelerationManager, call for call: every
+// Transformers/MultiTypeTransformer/TransformerTrainer.cs restated on
+// HipAccelerationManager, call for call, for token models (Train,
+// TrainBatchDiscrete, Validate) and continuous-input models (TrainContinuous,
+// TrainBatchContinuous, ValidateContinuous): every
 // `_accel.X(...)` of the reference is the manager's X with host arrays in and
 // out (resident on the device between calls), the trainer's own host loops
 // (the sparse row tracker of the token-embedding gradient, ScaleMatrixLocal,
@@ -679,9 +693,33 @@ class TransformerTrainer {
   ~TransformerTrainer();
   // TrainBatchDiscrete(batch, 0, batch.Length, learningRate) (:217-327).
   float TrainBatch(const std::vector<std::vector<int>> &batch, float learningRate);
-  // Train (:43-128) with the SplitMix64 shuffle seeded by `seed`.
-  float Train(const std::vector<std::vector<int>> &sequences, uint64_t seed = 0);
+  // Train (:43-128) with the SplitMix64 shuffle seeded by `seed`; with
+  // validation sequences, Validate runs after every ValidationInterval-th
+  // batch of an epoch and its losses are kept (validation_losses()).
+  // Returns the last epoch's mean batch loss.
+  float Train(const std::vector<std::vector<int>> &sequences, uint64_t seed = 0,
+              const std::vector<std::vector<int>> *validationSequences = nullptr);
+  // TrainBatchContinuous(batchIndices, 0, count, ...) (:329-512) over every
+  // window of `inputs` in order: window i is inputs[i] [T_i, InputFeatureDim]
+  // (an empty matrix stands for a null entry); regression models
+  // (TimeSeriesRegression) read regressionTargets[i] [>= T_i, OutputDim],
+  // classification models classTargets[i] (>= T_i ids); row t's target is
+  // step t + 1.
+  float TrainBatchContinuous(const std::vector<Matrix> &inputs, const std::vector<Matrix> *regressionTargets,
+                             const std::vector<std::vector<int>> *classTargets, float learningRate);
+  // TrainContinuous (:130-207): epochs of SplitMix64-shuffled batches of the
+  // windows with at least 2 steps.  The reference takes validation arrays
+  // here and never reads them, so this form has none.
+  float TrainContinuous(const std::vector<Matrix> &inputs, const std::vector<Matrix> *regressionTargets,
+                        const std::vector<std::vector<int>> *classTargets, uint64_t seed = 0);
+  // Validate (:1142-1182) / ValidateContinuous (:1183-1267): the mean loss
+  // per predicted row over the usable sequences, forward passes through
+  // LanguageModel.ForwardTokenSlice / ForwardContinuousSlice.
+  float Validate(const std::vector<std::vector<int>> &validationSequences);
+  float ValidateContinuous(const std::vector<Matrix> &inputs, const std::vector<Matrix> *regressionTargets,
+                           const std::vector<std::vector<int>> *classTargets);
   float last_norm() const { return last_norm_; }
+  const std::vector<float> &validation_losses() const { return val_losses_; }
 
   struct AttentionGradients {  // AttentionGradients.cs:9-60
     Matrix WQ_Grad, WK_Grad, WV_Grad, WO_Grad;
@@ -696,6 +734,8 @@ class TransformerTrainer {
   struct Gradients {
     Matrix TokenEmbeddingGrad, OutputProjectionGrad;
     std::vector<float> OutputBiasGrad;
+    Matrix InputProjectionGrad;  // continuous models: [EmbeddingDim, InputFeatureDim]
+    std::vector<float> InputProjectionBiasGrad;
     std::vector<AttentionGradients> AttentionGrads;
     std::vector<LayerNormGradients> LN1Grads, LN2Grads;
     std::vector<int> rows;
@@ -723,11 +763,24 @@ class TransformerTrainer {
     MatPtr EmbeddedInput, FinalHiddenStates;
     std::vector<int> TokenIds;
     int TokenStart = 0, TokenCount = 0;
+    // the continuous input the embedding was projected from: the caller's
+    // window, or the bucket's flattened copy (held by ContinuousOwned)
+    MatView ContinuousInput;
+    MatPtr ContinuousOwned;
+    int ContinuousInputRowStart = 0, ContinuousInputRowCount = 0;
   };
   Matrix ForwardWithCacheDiscrete(const std::vector<int> &tokenIds, int tokenStart, int tokenCount,
                                   ForwardCache &cache);
   Matrix ForwardWithCacheDiscreteBatch(const std::vector<std::vector<int>> &sequences,
                                        const std::vector<int> &offsets, int inputLen, ForwardCache &cache);
+  float TrainBatchContinuousRange(const std::vector<int> &batchIndices, int start, int count,
+                                  const std::vector<Matrix> &allInputs, const std::vector<Matrix> *allRegTargets,
+                                  const std::vector<std::vector<int>> *allClassTargets, float learningRate);
+  bool RegressionTargetIsValid(const std::vector<Matrix> *targets, int idx, int seqLen) const;
+  bool ClassTargetIsValid(const std::vector<std::vector<int>> *targets, int idx, int seqLen) const;
+  Matrix ForwardWithCacheContinuous(MatView inputSequence, int rowStart, int rowCount, ForwardCache &cache);
+  Matrix ForwardWithCacheContinuousBatch(const std::vector<int> &sourceIndices, const std::vector<Matrix> &allInputs,
+                                         int inputLen, ForwardCache &cache);
   Matrix ForwardFromEmbeddingWithCache(MatPtr embedded, int seqLen, ForwardCache &cache, int segmentLength = 0,
                                        int segmentCount = 1);
   MatPtr AttentionForwardWithCache(MultiHeadAttention &attention, const MatPtr &input, bool causal,
@@ -751,6 +804,7 @@ class TransformerTrainer {
   std::vector<std::vector<Matrix>> ffnWeightGrads_;
   std::vector<std::vector<std::vector<float>>> ffnBiasGrads_;
   float last_norm_ = 0.f;
+  std::vector<float> val_losses_;
 };
 
 // ---- device-resident training --------------------------------------------
@@ -764,6 +818,7 @@ struct TrainingConfig {
   float GradientClipThreshold = 1.0f;
   bool UseLearningRateDecay = false;
   float LearningRateDecay = 0.95f;
+  int ValidationInterval = 100;
   bool Verbose = false;
 };
 

@@ -1276,6 +1276,54 @@ Matrix HipAccelerationManager::BackpropOutputProjection(MatView dLogits, MatView
   return dX;
 }
 
+// ---- BackpropInputProjection: AccelerationCPU.cs:2280-2330 -------------------
+// The weight gradient is the same dY^T X product as the other projections'
+// (cdml_linear_backward with no input gradient): X is the input's row slice
+// at its own row stride, dY the first seqLen * embeddingDim floats of dX.
+void HipAccelerationManager::BackpropInputProjection(MatView dX, MatView continuousInput, int inputRowStart,
+                                                     MatRef weightGrad, VecRef biasGrad, int seqLen,
+                                                     int embeddingDim, int inputFeatureDim) {
+  if (dX.null()) throw ArgumentNullException("dX");
+  if (continuousInput.null()) throw ArgumentNullException("continuousInput");
+  if (!weightGrad.data) throw ArgumentNullException("weightGrad");
+  if (biasGrad.null()) throw ArgumentNullException("biasGrad");
+  if (inputRowStart < 0 || seqLen < 0 || (long long)inputRowStart + seqLen > continuousInput.rows)
+    throw ArgumentOutOfRangeException("inputRowStart", "Invalid input row slice: start=" + std::to_string(inputRowStart) +
+                                                           ", count=" + std::to_string(seqLen) + ", rows=" +
+                                                           std::to_string(continuousInput.rows) + ".");
+  if (inputFeatureDim > continuousInput.cols || dX.rows < seqLen || dX.cols < embeddingDim)
+    throw ArgumentException("Input or gradient dimensions are smaller than the requested projection dimensions.");
+  // the reference indexes weightGrad[e * inputFeatureDim + f] and biasGrad[e]
+  // without a check (IndexOutOfRangeException mid-update); checked up front
+  if (embeddingDim < 0 || inputFeatureDim < 0 ||
+      (long long)weightGrad.rows * weightGrad.cols < (long long)embeddingDim * inputFeatureDim ||
+      biasGrad.length < embeddingDim)
+    throw ArgumentException("weightGrad or biasGrad is smaller than embeddingDim x inputFeatureDim.");
+  if (seqLen == 0 || embeddingDim == 0) return;
+  std::lock_guard<std::mutex> lock(mu_);
+  ensure_ready();
+  const int ldin = continuousInput.cols;
+  const float *din = act_in(continuousInput, S_X) + (size_t)inputRowStart * ldin;
+  const float *ddx = act_in(dX, S_Q);
+  const size_t wb = (size_t)embeddingDim * inputFeatureDim * sizeof(float), bb = (size_t)embeddingDim * sizeof(float);
+  float *gw = static_cast<float *>(scratch(S_GW0, wb > 0 ? wb : 4));
+  float *gb = static_cast<float *>(scratch(S_GB0, bb));
+  if (wb > 0) upload(gw, weightGrad.data, wb);
+  upload(gb, biasGrad.data, bb);
+  size_t ws = 0;
+  check(cdml_linear_backward_workspace_size(seqLen, inputFeatureDim, embeddingDim, &ws),
+        "cdml_linear_backward_workspace_size");
+  void *dws = ws ? scratch(S_WS, ws) : nullptr;
+  check(cdml_linear_backward(din, ldin, ddx, embeddingDim, nullptr, nullptr, inputFeatureDim, wb > 0 ? gw : nullptr,
+                             gb, seqLen, inputFeatureDim, embeddingDim, 0, dws, ws, stream_),
+        "cdml_linear_backward");
+  if (wb > 0)
+    act_done({Out{weightGrad.data, wb / 4, gw}, Out{biasGrad.data, bb / 4, gb}});
+  else
+    act_done({Out{biasGrad.data, bb / 4, gb}});
+  sync();
+}
+
 // ---- MatrixMultiply / MatrixMultiplyTranspose: AccelerationCPU.cs:159-250 ----
 Matrix HipAccelerationManager::MatrixMultiply(MatView A, MatView B) {
   if (A.null()) throw ArgumentNullException("A");

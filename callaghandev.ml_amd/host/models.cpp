@@ -213,6 +213,56 @@ Matrix LanguageModel::Forward(MatView inputSequence) {
   return ProjectToOutput(ForwardHidden(std::move(embedded)));
 }
 
+// :135-144 with ValidateTokenSlice (:602-619)
+Matrix LanguageModel::ForwardTokenSlice(const std::vector<int> &tokenIds, int tokenStart, int tokenCount) {
+  if (!cfg_.UsesDiscreteTokens)
+    throw InvalidOperationException("Use ForwardContinuousSlice(float[,], int, int) for continuous input data types.");
+  if (tokenCount <= 0) throw ArgumentException("Token slice must contain at least one token.", "tokenCount");
+  if (tokenStart < 0 || (long long)tokenStart + tokenCount > (long long)tokenIds.size())
+    throw ArgumentOutOfRangeException("tokenStart");
+  if (tokenCount > cfg_.MaxSequenceLength)
+    throw ArgumentException("Token sequence length " + std::to_string(tokenCount) + " exceeds MaxSequenceLength " +
+                                std::to_string(cfg_.MaxSequenceLength) + ".",
+                            "tokenCount");
+  for (int i = 0; i < tokenCount; ++i) {
+    const int token = tokenIds[tokenStart + i];
+    if ((unsigned)token >= (unsigned)cfg_.VocabSize)
+      throw ArgumentOutOfRangeException("tokenIds", "Token id " + std::to_string(token) + " at position " +
+                                                        std::to_string(tokenStart + i) + " is outside [0, " +
+                                                        std::to_string(cfg_.VocabSize) + ").");
+  }
+  Matrix embedded = accel_->EmbedTokenIds(tokenIds, tokenStart, tokenCount, TokenEmbedding, cfg_.EmbeddingDim);
+  return ProjectToOutput(ForwardHidden(std::move(embedded)));
+}
+
+// :146-157 with ValidateContinuousSlice (:642-668)
+Matrix LanguageModel::ForwardContinuousSlice(MatView inputSequence, int rowStart, int rowCount) {
+  if (cfg_.UsesDiscreteTokens)
+    throw InvalidOperationException("Use ForwardTokenSlice(int[], int, int) for discrete token data types.");
+  if (inputSequence.null()) throw ArgumentNullException("inputSequence");
+  if (rowCount <= 0) throw ArgumentException("Input sequence slice must contain at least one row.", "rowCount");
+  if (rowStart < 0 || (long long)rowStart + rowCount > inputSequence.rows) throw ArgumentOutOfRangeException("rowStart");
+  if (rowCount > cfg_.MaxSequenceLength)
+    throw ArgumentException("Input sequence length " + std::to_string(rowCount) + " exceeds MaxSequenceLength " +
+                                std::to_string(cfg_.MaxSequenceLength) + ".",
+                            "rowCount");
+  if (inputSequence.cols != cfg_.InputFeatureDim)
+    throw ArgumentException("Input feature dimension must be " + std::to_string(cfg_.InputFeatureDim) + ", got " +
+                                std::to_string(inputSequence.cols) + ".",
+                            "inputSequence");
+  for (int i = 0; i < rowCount; ++i)
+    for (int j = 0; j < inputSequence.cols; ++j) {
+      const float v = inputSequence.data[(size_t)(rowStart + i) * inputSequence.cols + j];
+      if (std::isnan(v) || std::isinf(v))
+        throw ArgumentException("Input value at [" + std::to_string(rowStart + i) + "," + std::to_string(j) +
+                                    "] is not finite.",
+                                "inputSequence");
+    }
+  Matrix embedded =
+      accel_->BatchDotProductAddBias(InputProjection, inputSequence, rowStart, rowCount, InputProjectionBias);
+  return ProjectToOutput(ForwardHidden(std::move(embedded)));
+}
+
 // :235-268, with the dot products on the device (the reference runs this
 // inline on the host).
 std::vector<float> LanguageModel::ProjectLastTokenOnly(const Matrix &hidden) {

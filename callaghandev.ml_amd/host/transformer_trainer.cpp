@@ -1,7 +1,7 @@
 // TransformerTrainer (Transformers/MultiTypeTransformer/TransformerTrainer.cs)
-// restated for decoder token models on HipAccelerationManager: the
-// reference's call sequence, one manager call per `_accel.X(...)`, with the
-// model's host arrays updated in place.  Line references are to that file
+// restated on HipAccelerationManager for token and continuous-input models:
+// the reference's call sequence, one manager call per `_accel.X(...)`, with
+// the model's host arrays updated in place.  Line references are to that file
 // unless another is named.
 #include <algorithm>
 #include <cmath>
@@ -25,18 +25,47 @@ bool all_finite(const Matrix &m) {
 MatRef ref(Matrix &m) { return MatRef(m.ptr(), m.rows, m.cols); }
 VecRef ref(std::vector<float> &v) { return VecRef(v.data(), (int)v.size()); }
 
+// MatrixAllFinite over a view
+bool all_finite(MatView m) {
+  for (size_t i = 0, n = (size_t)m.rows * m.cols; i < n; ++i)
+    if (!is_finite(m.data[i])) return false;
+  return true;
+}
+
+// ShuffleInPlace (:1417-1430): Fisher-Yates from the last element, j drawn
+// in [0, i]; the draws come from SplitMix64 (the reference's System.Random
+// stream is not reproduced).
+struct SplitMix64 {
+  uint64_t state;
+  uint64_t next() {
+    uint64_t z = (state += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+  }
+};
+template <class T>
+void shuffle_in_place(std::vector<T> &data, SplitMix64 &rng) {
+  for (size_t i = data.size(); i > 1; --i) std::swap(data[i - 1], data[rng.next() % i]);
+}
+
+constexpr int kTimeSeriesRegression = 1;  // TransformerDataType.TimeSeriesRegression
+
 }  // namespace
 
 TransformerTrainer::TransformerTrainer(LanguageModel &model, const TrainingConfig &config)
     : model_(model), cfg_(model.config()), tc_(new TrainingConfig(config)), accel_(model.AccelerationManager()) {
-  if (!cfg_.UsesDiscreteTokens)
-    throw InvalidOperationException("This trainer restates TrainBatchDiscrete: token models only.");
   const int D = cfg_.EmbeddingDim, L = cfg_.NumLayers, V = cfg_.EffectiveOutputDim();
   // TransformerGradients(config) (TransformerGradients.cs:28-60)
-  grads_.TokenEmbeddingGrad = Matrix(cfg_.VocabSize, D);
+  if (cfg_.UsesDiscreteTokens) {
+    grads_.TokenEmbeddingGrad = Matrix(cfg_.VocabSize, D);
+    grads_.marked.assign(cfg_.VocabSize, 0);
+  } else {
+    grads_.InputProjectionGrad = Matrix(D, cfg_.InputFeatureDim);
+    grads_.InputProjectionBiasGrad.assign(D, 0.f);
+  }
   grads_.OutputProjectionGrad = Matrix(V, D);
   grads_.OutputBiasGrad.assign(V, 0.f);
-  grads_.marked.assign(cfg_.VocabSize, 0);
   for (int i = 0; i < L; ++i) {
     AttentionGradients a;
     a.WQ_Grad = Matrix(D, D);
@@ -66,7 +95,9 @@ TransformerTrainer::TransformerTrainer(LanguageModel &model, const TrainingConfi
 TransformerTrainer::~TransformerTrainer() = default;
 
 // ---- Train / TrainBatchDiscrete ----------------------------------------------
-float TransformerTrainer::Train(const std::vector<std::vector<int>> &sequences, uint64_t seed) {
+float TransformerTrainer::Train(const std::vector<std::vector<int>> &sequences, uint64_t seed,
+                                const std::vector<std::vector<int>> *validationSequences) {
+  if (!cfg_.UsesDiscreteTokens) throw InvalidOperationException("Use TrainContinuous() for continuous data types.");
   if (tc_->BatchSize <= 0) throw ArgumentOutOfRangeException("BatchSize", "BatchSize must be positive.");
   if (tc_->Epochs < 0) throw ArgumentOutOfRangeException("Epochs", "Epochs must be non-negative.");
   std::vector<std::vector<int>> valid;
@@ -76,22 +107,68 @@ float TransformerTrainer::Train(const std::vector<std::vector<int>> &sequences, 
     throw ArgumentException("No valid sequences to train on. All sequences must contain at least 2 tokens.",
                             "sequences");
   float lr = tc_->LearningRate, epochAvg = 0.f;
-  uint64_t state = seed;
-  auto next = [&state]() {  // SplitMix64 (the reference's System.Random is not reproduced)
-    uint64_t z = (state += 0x9E3779B97F4A7C15ull);
-    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-    return z ^ (z >> 31);
-  };
+  SplitMix64 rng{seed};
+  val_losses_.clear();
   for (int epoch = 0; epoch < tc_->Epochs; ++epoch) {
-    std::vector<std::vector<int>> order = valid;
-    for (size_t i = order.size(); i > 1; --i) std::swap(order[i - 1], order[next() % i]);
+    std::vector<std::vector<int>> order = valid;  // ShuffleArray: a shuffled copy
+    shuffle_in_place(order, rng);
     float epochLoss = 0.f;
     int numBatches = 0;
     for (size_t i = 0; i < order.size(); i += tc_->BatchSize) {
       std::vector<std::vector<int>> b(order.begin() + i,
                                       order.begin() + std::min(order.size(), i + (size_t)tc_->BatchSize));
       epochLoss += TrainBatch(b, lr);
+      ++numBatches;
+      // :92-104
+      if (validationSequences && tc_->ValidationInterval > 0 && numBatches % tc_->ValidationInterval == 0)
+        val_losses_.push_back(Validate(*validationSequences));
+    }
+    epochAvg = numBatches > 0 ? epochLoss / numBatches : 0.f;
+    if (tc_->UseLearningRateDecay) lr *= tc_->LearningRateDecay;
+  }
+  return epochAvg;
+}
+
+// ---- TrainContinuous / TrainBatchContinuous (:130-207, :329-512) ---------------
+float TransformerTrainer::TrainContinuous(const std::vector<Matrix> &inputs, const std::vector<Matrix> *regressionTargets,
+                                          const std::vector<std::vector<int>> *classTargets, uint64_t seed) {
+  if (cfg_.UsesDiscreteTokens) throw InvalidOperationException("Use Train(int[][]) for discrete token data types.");
+  if (tc_->BatchSize <= 0) throw ArgumentOutOfRangeException("BatchSize", "BatchSize must be positive.");
+  if (tc_->Epochs < 0) throw ArgumentOutOfRangeException("Epochs", "Epochs must be non-negative.");
+  if (cfg_.DataType == kTimeSeriesRegression) {
+    if (!regressionTargets)
+      throw ArgumentException("regressionTargets is required for TimeSeriesRegression.", "regressionTargets");
+    if (regressionTargets->size() != inputs.size())
+      throw ArgumentException("regressionTargets length must match inputs length.", "regressionTargets");
+  } else {  // TimeSeriesClassification (:150-156)
+    if (!classTargets)
+      throw ArgumentException("classTargets is required for TimeSeriesClassification.", "classTargets");
+    if (classTargets->size() != inputs.size())
+      throw ArgumentException("classTargets length must match inputs length.", "classTargets");
+  }
+  std::vector<int> validIndices;
+  for (int i = 0; i < (int)inputs.size(); ++i) {
+    if (inputs[i].rows < 2) continue;
+    if (inputs[i].cols != cfg_.InputFeatureDim)
+      throw ArgumentException("Input sequence " + std::to_string(i) + " has feature dimension " +
+                                  std::to_string(inputs[i].cols) + ", expected " +
+                                  std::to_string(cfg_.InputFeatureDim) + ".",
+                              "inputs");
+    validIndices.push_back(i);
+  }
+  if (validIndices.empty())
+    throw ArgumentException("No valid sequences. All must have at least 2 timesteps.", "inputs");
+  float lr = tc_->LearningRate, epochAvg = 0.f;
+  SplitMix64 rng{seed};
+  for (int epoch = 0; epoch < tc_->Epochs; ++epoch) {
+    std::vector<int> shuffled = validIndices;
+    shuffle_in_place(shuffled, rng);
+    float epochLoss = 0.f;
+    int numBatches = 0;
+    for (int i = 0; i < (int)shuffled.size(); i += tc_->BatchSize) {
+      const int batchSize = std::min(tc_->BatchSize, (int)shuffled.size() - i);
+      if (batchSize == 0) continue;
+      epochLoss += TrainBatchContinuousRange(shuffled, i, batchSize, inputs, regressionTargets, classTargets, lr);
       ++numBatches;
     }
     epochAvg = numBatches > 0 ? epochLoss / numBatches : 0.f;
@@ -100,7 +177,196 @@ float TransformerTrainer::Train(const std::vector<std::vector<int>> &sequences, 
   return epochAvg;
 }
 
+float TransformerTrainer::TrainBatchContinuous(const std::vector<Matrix> &inputs,
+                                               const std::vector<Matrix> *regressionTargets,
+                                               const std::vector<std::vector<int>> *classTargets,
+                                               float learningRate) {
+  if (cfg_.UsesDiscreteTokens)
+    throw InvalidOperationException("TrainBatchContinuous needs a continuous-input model.");
+  std::vector<int> indices(inputs.size());
+  for (size_t i = 0; i < indices.size(); ++i) indices[i] = (int)i;
+  return TrainBatchContinuousRange(indices, 0, (int)indices.size(), inputs, regressionTargets, classTargets,
+                                   learningRate);
+}
+
+// RegressionTargetIsValid / ClassTargetIsValid (:1480-1502)
+bool TransformerTrainer::RegressionTargetIsValid(const std::vector<Matrix> *targets, int idx, int seqLen) const {
+  if (!targets || idx < 0 || idx >= (int)targets->size()) return false;
+  const Matrix &t = (*targets)[idx];
+  return t.rows > 0 && t.rows >= seqLen && t.cols == cfg_.OutputDim && all_finite(MatView(t));
+}
+
+bool TransformerTrainer::ClassTargetIsValid(const std::vector<std::vector<int>> *targets, int idx, int seqLen) const {
+  if (!targets || idx < 0 || idx >= (int)targets->size()) return false;
+  const std::vector<int> &t = (*targets)[idx];
+  if (t.empty() || (int)t.size() < seqLen) return false;
+  for (int i = 1; i < seqLen; ++i)
+    if ((unsigned)t[i] >= (unsigned)cfg_.OutputDim) return false;
+  return true;
+}
+
+float TransformerTrainer::TrainBatchContinuousRange(const std::vector<int> &batchIndices, int start, int count,
+                                                    const std::vector<Matrix> &allInputs,
+                                                    const std::vector<Matrix> *allRegTargets,
+                                                    const std::vector<std::vector<int>> *allClassTargets,
+                                                    float learningRate) {
+  if (start < 0 || count < 0 || (long long)start + count > (long long)batchIndices.size())
+    throw ArgumentOutOfRangeException("start");
+  ZeroAllGradients();
+  float totalLoss = 0.f;
+  int validCount = 0;
+  const bool regression = cfg_.DataType == kTimeSeriesRegression;
+  // buckets in order of first appearance (:351-386)
+  std::vector<std::pair<int, std::vector<int>>> buckets;
+  for (int batchOffset = 0; batchOffset < count; ++batchOffset) {
+    const int idx = batchIndices[start + batchOffset];
+    if ((unsigned)idx >= (unsigned)allInputs.size()) continue;
+    const Matrix &inputSeq = allInputs[idx];
+    const int seqLen = inputSeq.rows;
+    if (seqLen < 2 || inputSeq.cols != cfg_.InputFeatureDim) continue;
+    if (!all_finite(MatView(inputSeq))) continue;
+    if (regression ? !RegressionTargetIsValid(allRegTargets, idx, seqLen)
+                   : !ClassTargetIsValid(allClassTargets, idx, seqLen))
+      continue;
+    const int inputLen = seqLen - 1;
+    auto it = std::find_if(buckets.begin(), buckets.end(), [&](const auto &b) { return b.first == inputLen; });
+    if (it == buckets.end()) {
+      buckets.emplace_back(inputLen, std::vector<int>());
+      it = buckets.end() - 1;
+    }
+    it->second.push_back(idx);
+  }
+  for (auto &bucket : buckets) {
+    const int inputLen = bucket.first;
+    const std::vector<int> &sourceIndices = bucket.second;
+    if (sourceIndices.empty()) continue;
+    const int n = (int)sourceIndices.size();
+    try {
+      ForwardCache cache;
+      Matrix output = n == 1 ? ForwardWithCacheContinuous(allInputs[sourceIndices[0]], 0, inputLen, cache)
+                             : ForwardWithCacheContinuousBatch(sourceIndices, allInputs, inputLen, cache);
+      const int effectiveLen = std::min(output.rows, n * inputLen);
+      if (effectiveLen <= 0) continue;
+      std::pair<float, Matrix> r;
+      if (regression) {
+        if (n == 1) {
+          r = accel_->MSELossAndGradient(output, (*allRegTargets)[sourceIndices[0]], 1,
+                                         std::min(output.rows, inputLen));
+        } else {
+          // BuildContinuousRegressionFlatTargets (:690-708)
+          const int outputDim = cfg_.EffectiveOutputDim();
+          Matrix targets(n * inputLen, outputDim);
+          for (int b = 0; b < n; ++b) {
+            const Matrix &src = (*allRegTargets)[sourceIndices[b]];
+            for (int t = 0; t < inputLen; ++t)
+              for (int o = 0; o < outputDim; ++o) targets.at(b * inputLen + t, o) = src.at(t + 1, o);
+          }
+          r = accel_->MSELossAndGradient(output, targets, 0, effectiveLen);
+        }
+      } else {
+        if (n == 1) {
+          r = accel_->CrossEntropyLossAndGradient(output, (*allClassTargets)[sourceIndices[0]], 1,
+                                                  std::min(output.rows, inputLen));
+        } else {
+          // BuildContinuousClassFlatTargets (:676-688)
+          std::vector<int> targets((size_t)n * inputLen);
+          for (int b = 0; b < n; ++b)
+            for (int t = 0; t < inputLen; ++t)
+              targets[(size_t)b * inputLen + t] = (*allClassTargets)[sourceIndices[b]][t + 1];
+          r = accel_->CrossEntropyLossAndGradient(output, targets, 0, effectiveLen);
+        }
+      }
+      if (!is_finite(r.first) || !all_finite(r.second)) continue;
+      if (n > 1)  // ScaleMatrixLocal (:710-721)
+        for (float &x : r.second.data) x *= (float)n;
+      BackpropFromOutput(r.second, cache);
+      totalLoss += r.first * (float)n;
+      validCount += n;
+    } catch (const std::exception &) {  // :470-478
+      ZeroAllGradients();
+      totalLoss = 0.f;
+      validCount = 0;
+    }
+  }
+  if (validCount == 0) return 0.f;
+  ScaleGradients(1.0f / validCount);
+  const float gradNorm = ComputeGradientNorm();
+  last_norm_ = gradNorm;
+  if (!is_finite(gradNorm)) {
+    ZeroAllGradients();
+    return totalLoss / validCount;
+  }
+  if (tc_->UseGradientClipping) ClipGradients(tc_->GradientClipThreshold, gradNorm);
+  UpdateParameters(learningRate);
+  return totalLoss / validCount;
+}
+
+// ---- Validate / ValidateContinuous (:1142-1267) --------------------------------
+float TransformerTrainer::Validate(const std::vector<std::vector<int>> &validationSequences) {
+  float totalLoss = 0.f;
+  int totalTokens = 0;
+  for (const std::vector<int> &sequence : validationSequences) {
+    if (sequence.size() < 2) continue;
+    bool ok = true;  // TokensAreValid (:1467-1478)
+    for (int t : sequence)
+      if ((unsigned)t >= (unsigned)cfg_.VocabSize) ok = false;
+    if (!ok) continue;
+    const int inputLen = (int)sequence.size() - 1;
+    Matrix logits = model_.ForwardTokenSlice(sequence, 0, inputLen);
+    const int effectiveLen = std::min(logits.rows, inputLen);
+    if (effectiveLen <= 0) continue;
+    auto r = accel_->CrossEntropyLossAndGradient(logits, sequence, 1, effectiveLen);
+    if (!is_finite(r.first)) continue;
+    totalLoss += r.first * effectiveLen;
+    totalTokens += effectiveLen;
+  }
+  return totalTokens > 0 ? totalLoss / totalTokens : 0.0f;
+}
+
+float TransformerTrainer::ValidateContinuous(const std::vector<Matrix> &inputs,
+                                             const std::vector<Matrix> *regressionTargets,
+                                             const std::vector<std::vector<int>> *classTargets) {
+  float totalLoss = 0.f;
+  int totalItems = 0;
+  const bool regression = cfg_.DataType == kTimeSeriesRegression;
+  for (int idx = 0; idx < (int)inputs.size(); ++idx) {
+    const Matrix &inputSeq = inputs[idx];
+    const int seqLen = inputSeq.rows;
+    if (seqLen < 2) continue;  // a null window and a short one alike
+    const int inputLen = seqLen - 1;
+    Matrix output = model_.ForwardContinuousSlice(inputSeq, 0, inputLen);
+    int effectiveLen = output.rows;
+    // regressionTargets[idx] / classTargets[idx] past the array's end throw
+    // IndexOutOfRangeException in the reference
+    if (regression) {
+      if (!regressionTargets) continue;
+      if (idx >= (int)regressionTargets->size()) throw ArgumentOutOfRangeException("regressionTargets");
+      const Matrix &t = (*regressionTargets)[idx];
+      if (t.rows == 0) continue;
+      effectiveLen = std::min(effectiveLen, inputLen);
+      if (effectiveLen <= 0) continue;
+      auto r = accel_->MSELossAndGradient(output, t, 1, effectiveLen);
+      if (!is_finite(r.first)) continue;
+      totalLoss += r.first * effectiveLen;
+      totalItems += effectiveLen;
+    } else {
+      if (!classTargets) continue;
+      if (idx >= (int)classTargets->size()) throw ArgumentOutOfRangeException("classTargets");
+      const std::vector<int> &t = (*classTargets)[idx];
+      if (t.empty()) continue;
+      effectiveLen = std::min(effectiveLen, inputLen);
+      if (effectiveLen <= 0) continue;
+      auto r = accel_->CrossEntropyLossAndGradient(output, t, 1, effectiveLen);
+      if (!is_finite(r.first)) continue;
+      totalLoss += r.first * effectiveLen;
+      totalItems += effectiveLen;
+    }
+  }
+  return totalItems > 0 ? totalLoss / totalItems : 0.0f;
+}
+
 float TransformerTrainer::TrainBatch(const std::vector<std::vector<int>> &batch, float learningRate) {
+  if (!cfg_.UsesDiscreteTokens) throw InvalidOperationException("TrainBatchDiscrete needs a token model.");
   ZeroAllGradients();
   float totalLoss = 0.f;
   int validCount = 0;
@@ -204,6 +470,49 @@ Matrix TransformerTrainer::ForwardWithCacheDiscreteBatch(const std::vector<std::
   return ForwardFromEmbeddingWithCache(embedded, totalRows, cache, inputLen, batchSize);
 }
 
+// :436-457
+Matrix TransformerTrainer::ForwardWithCacheContinuous(MatView inputSequence, int rowStart, int rowCount,
+                                                      ForwardCache &cache) {
+  if (inputSequence.null()) throw ArgumentNullException("inputSequence");
+  if (rowStart < 0 || rowCount < 0 || (long long)rowStart + rowCount > inputSequence.rows)
+    throw ArgumentOutOfRangeException("rowStart");
+  auto embedded = std::make_shared<Matrix>(accel_->BatchDotProductAddBias(
+      model_.InputProjection, inputSequence, rowStart, rowCount, model_.InputProjectionBias));
+  cache.EmbeddedInput = embedded;
+  cache.TokenIds.clear();
+  cache.TokenStart = 0;
+  cache.TokenCount = 0;
+  cache.ContinuousInput = inputSequence;
+  cache.ContinuousInputRowStart = rowStart;
+  cache.ContinuousInputRowCount = rowCount;
+  return ForwardFromEmbeddingWithCache(embedded, rowCount, cache);
+}
+
+// :624-658
+Matrix TransformerTrainer::ForwardWithCacheContinuousBatch(const std::vector<int> &sourceIndices,
+                                                           const std::vector<Matrix> &allInputs, int inputLen,
+                                                           ForwardCache &cache) {
+  if (inputLen <= 0) throw ArgumentOutOfRangeException("inputLen");
+  const int count = (int)sourceIndices.size(), totalRows = count * inputLen, F = cfg_.InputFeatureDim;
+  auto flatInput = std::make_shared<Matrix>(totalRows, F);
+  for (int b = 0; b < count; ++b) {
+    const Matrix &source = allInputs[sourceIndices[b]];
+    for (int t = 0; t < inputLen; ++t)
+      for (int f = 0; f < F; ++f) flatInput->at(b * inputLen + t, f) = source.at(t, f);
+  }
+  auto embedded = std::make_shared<Matrix>(
+      accel_->BatchDotProductAddBias(model_.InputProjection, *flatInput, model_.InputProjectionBias));
+  cache.EmbeddedInput = embedded;
+  cache.TokenIds.clear();
+  cache.TokenStart = 0;
+  cache.TokenCount = 0;
+  cache.ContinuousOwned = flatInput;
+  cache.ContinuousInput = *flatInput;
+  cache.ContinuousInputRowStart = 0;
+  cache.ContinuousInputRowCount = totalRows;
+  return ForwardFromEmbeddingWithCache(embedded, totalRows, cache, inputLen, count);
+}
+
 Matrix TransformerTrainer::ForwardFromEmbeddingWithCache(MatPtr embedded, int seqLen, ForwardCache &cache,
                                                          int segmentLength, int segmentCount) {
   const bool selfCausal = cfg_.UseDecoderOnly;
@@ -301,7 +610,14 @@ void TransformerTrainer::BackpropFromOutput(Matrix &dOutput, ForwardCache &cache
                                                ref(grads_.OutputProjectionGrad), ref(grads_.OutputBiasGrad),
                                                dOutput.rows, cfg_.EffectiveOutputDim(), cfg_.EmbeddingDim);
   for (int layer = cfg_.NumLayers - 1; layer >= 0; --layer) dX = BackpropBlock(layer, dX, cache);
-  // BackpropInput (:887-896): MarkTokenRows, then the embedding gradient
+  // BackpropInput (:887-896)
+  if (!cfg_.UsesDiscreteTokens) {
+    accel_->BackpropInputProjection(dX, cache.ContinuousInput, cache.ContinuousInputRowStart,
+                                    ref(grads_.InputProjectionGrad), ref(grads_.InputProjectionBiasGrad), dX.rows,
+                                    cfg_.EmbeddingDim, cfg_.InputFeatureDim);
+    return;
+  }
+  // MarkTokenRows, then the embedding gradient
   for (int i = 0; i < dX.rows; ++i) {
     const int row = cache.TokenIds[cache.TokenStart + i];
     if ((unsigned)row >= (unsigned)cfg_.VocabSize)
@@ -378,6 +694,8 @@ void TransformerTrainer::ZeroAllGradients() {
     grads_.marked[row] = 0;
   }
   grads_.rows.clear();
+  std::fill(grads_.InputProjectionGrad.data.begin(), grads_.InputProjectionGrad.data.end(), 0.f);
+  std::fill(grads_.InputProjectionBiasGrad.begin(), grads_.InputProjectionBiasGrad.end(), 0.f);
   for (AttentionGradients &a : grads_.AttentionGrads) {
     for (Matrix *m : {&a.WQ_Grad, &a.WK_Grad, &a.WV_Grad, &a.WO_Grad}) std::fill(m->data.begin(), m->data.end(), 0.f);
     for (std::vector<float> *v : {&a.BiasQ_Grad, &a.BiasK_Grad, &a.BiasV_Grad, &a.BiasO_Grad})
@@ -399,8 +717,13 @@ void TransformerTrainer::ZeroAllGradients() {
 
 void TransformerTrainer::ScaleGradients(float scale) {  // :1354-1380
   const int D = cfg_.EmbeddingDim;
-  for (int row : grads_.rows)  // SparseRowGradientTracker.Scale, host loop
-    for (int c = 0; c < D; ++c) grads_.TokenEmbeddingGrad.at(row, c) *= scale;
+  if (cfg_.UsesDiscreteTokens) {
+    for (int row : grads_.rows)  // SparseRowGradientTracker.Scale, host loop
+      for (int c = 0; c < D; ++c) grads_.TokenEmbeddingGrad.at(row, c) *= scale;
+  } else {
+    accel_->MatrixScaleInPlace(ref(grads_.InputProjectionGrad), scale);
+    accel_->VectorScaleInPlace(ref(grads_.InputProjectionBiasGrad), scale);
+  }
   accel_->MatrixScaleInPlace(ref(grads_.OutputProjectionGrad), scale);
   accel_->VectorScaleInPlace(ref(grads_.OutputBiasGrad), scale);
   for (AttentionGradients &g : grads_.AttentionGrads) {
@@ -427,13 +750,18 @@ void TransformerTrainer::ScaleGradients(float scale) {  // :1354-1380
 float TransformerTrainer::ComputeGradientNorm() {  // :1319-1352
   const int D = cfg_.EmbeddingDim;
   float sum = 0.f;
-  float emb = 0.f;  // SparseRowGradientTracker.SquaredNorm: touched rows in first-use order, host loop
-  for (int row : grads_.rows)
-    for (int c = 0; c < D; ++c) {
-      const float v = grads_.TokenEmbeddingGrad.at(row, c);
-      emb += v * v;
-    }
-  sum += emb;
+  if (cfg_.UsesDiscreteTokens) {
+    float emb = 0.f;  // SparseRowGradientTracker.SquaredNorm: touched rows in first-use order, host loop
+    for (int row : grads_.rows)
+      for (int c = 0; c < D; ++c) {
+        const float v = grads_.TokenEmbeddingGrad.at(row, c);
+        emb += v * v;
+      }
+    sum += emb;
+  } else {
+    sum += accel_->MatrixSquaredNorm(grads_.InputProjectionGrad);
+    sum += accel_->VectorSquaredNorm(grads_.InputProjectionBiasGrad);
+  }
   sum += accel_->MatrixSquaredNorm(grads_.OutputProjectionGrad);
   sum += accel_->VectorSquaredNorm(grads_.OutputBiasGrad);
   for (AttentionGradients &g : grads_.AttentionGrads) {
@@ -461,9 +789,14 @@ void TransformerTrainer::ClipGradients(float threshold, float totalNorm) {  // :
 
 void TransformerTrainer::UpdateParameters(float learningRate) {  // :1269-1305
   const int D = cfg_.EmbeddingDim;
-  for (int row : grads_.rows)  // SparseRowGradientTracker.UpdateRows, host loop
-    for (int c = 0; c < D; ++c)
-      model_.TokenEmbedding.at(row, c) -= learningRate * grads_.TokenEmbeddingGrad.at(row, c);
+  if (cfg_.UsesDiscreteTokens) {
+    for (int row : grads_.rows)  // SparseRowGradientTracker.UpdateRows, host loop
+      for (int c = 0; c < D; ++c)
+        model_.TokenEmbedding.at(row, c) -= learningRate * grads_.TokenEmbeddingGrad.at(row, c);
+  } else {
+    accel_->MatrixUpdate(ref(model_.InputProjection), grads_.InputProjectionGrad, learningRate);
+    accel_->VectorUpdate(ref(model_.InputProjectionBias), grads_.InputProjectionBiasGrad, learningRate);
+  }
   for (int i = 0; i < cfg_.NumLayers; ++i) {
     TransformerBlock &block = model_.Blocks[i];
     AttentionGradients &g = grads_.AttentionGrads[i];

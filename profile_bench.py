@@ -2,10 +2,10 @@
 come from.  Run on the GPU box from the repository root, after the library is
 built:
 
-    python3 profile_bench.py [--passes trace,traffic,counters,backward,probe] [--out DIR]
+    python3 profile_bench.py [--passes trace,traffic,counters,backward] [--out DIR]
                              [--profiles-dir DIR]
 
-Each pass runs `rocprofv3 ... -- python3 bench.py ...` (or the probe) as a
+Each pass runs `rocprofv3 ... -- python3 bench.py ...` as a
 child process under `timeout -s KILL`; the first pass that fails ends the
 script, so no further GPU work follows a failure.  Raw rocprofv3 output goes
 to --out (a scratch folder, never committed); the summaries go to profiles/
@@ -28,8 +28,6 @@ to --out (a scratch folder, never committed); the summaries go to profiles/
                                         -> train_step_{c1,c3_shape,c5}_kernel_stats.md
   c1        kernel trace + stats of the config-1 text model leg (forward and
             greedy generation)          -> c1_text_model_generate_kernel_stats.md
-  probe     builds and runs csrc/probes/issue_rates.hip
-                                        -> gfx950_issue_rates.md
 """
 from __future__ import annotations
 
@@ -49,7 +47,7 @@ sys.path.insert(0, ROOT)
 import bench  # noqa: E402  (TRAFFIC_SOURCES, source_digest)
 
 PROFILES = os.path.join(ROOT, "profiles")
-PASSES = ("trace", "traffic", "counters", "trainc5", "backward", "train", "c1", "probe")
+PASSES = ("trace", "traffic", "counters", "trainc5", "backward", "train", "c1")
 COUNTERS_A = ("GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES SQ_INSTS_VALU_MFMA_F32 "
               "SQ_INSTS_VALU SQ_INSTS_VALU_TRANS_F32 SQ_INSTS_LDS SQ_LDS_BANK_CONFLICT")
 COUNTERS_B = ("GRBM_GUI_ACTIVE SQ_WAVES SQ_WAVE_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_ACTIVE_INST_VALU "
@@ -369,32 +367,6 @@ def pass_c1(out):
     write("c1_text_model_generate_kernel_stats.md",
           header("Kernel durations: config-1 text model, forward and greedy generation", [cmd], note) + "\n" +
           stats_table(read_stats(d)) + "\n")
-
-
-def pass_probe(out):
-    src = os.path.join("callaghandev.ml_amd", "csrc", "probes", "issue_rates.hip")
-    exe = os.path.join(out, "issue_rates")
-    build = ["/opt/rocm/bin/hipcc", "--offload-arch=gfx950", "-O3", "-Xclang", "-target-feature", "-Xclang",
-             "-packed-fp32-ops", src, "-o", exe]
-    log("build: " + " ".join(build))
-    subprocess.run(build, cwd=ROOT, check=True)
-    so = run_step([exe], 120, os.path.join(out, "probe.log"))
-    rows = ["| case | cycles per step per SIMD |", "|---|---|"]
-    for line in so.splitlines():
-        parts = line.rsplit(" ", 1)
-        if len(parts) == 2:
-            rows.append(f"| `{parts[0]}` | {parts[1]} |")
-    note = ("Cycles per step per SIMD at the 2.4 GHz peak clock, from event time.  A step is one "
-            "`v_mfma_f32_32x32x2_f32` (64 cycles at full rate) plus what the case names; `mfma=0` "
-            "cases have no MFMA.  The `16_mfma`/`48_adds` cases count one iteration of a dependent "
-            "chain of 16 MFMAs followed by a burst of 48 independent adds, the shape of a softmax "
-            "between two MFMA chains.  The cycles the VALU instructions add next to the MFMAs are at "
-            "least what they cost alone: on gfx950 the fp32 MFMA and the VALU do not overlap, and a "
-            "single wave issues VALU at about half the rate of several.")
-    write("gfx950_issue_rates.md",
-          header("gfx950 issue rates: fp32 MFMA against VALU and LDS operands",
-                 [" ".join(build[:1] + ["..."] + build[-3:]), os.path.relpath(exe, ROOT)], note) +
-          "\n" + "\n".join(rows) + "\n")
 
 
 def main():

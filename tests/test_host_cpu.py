@@ -215,6 +215,47 @@ def test_training_method_argument_rules(mgr):
         mgr.AccumulateTokenEmbeddingGrad(z((5, 2), np.float32), M(2, 2, 1), np.array([0, 5], np.int32), 0, 2, 2)
 
 
+def test_continuous_trainer_argument_rules(mgr):
+    """TrainContinuous's checks (TransformerTrainer.cs:130-168), the
+    token/continuous entry split, BackpropInputProjection's slice rules
+    (AccelerationCPU.cs:2280-2305) and the slice forwards' validation
+    (LanguageModel.cs:602-668): all raised before any device work."""
+    z = np.zeros
+    with pytest.raises(H.ArgumentOutOfRangeException, match="inputRowStart"):
+        mgr.BackpropInputProjection(M(3, 4, 1), M(4, 2, 2), 2, z((4, 2), np.float32), z(4, np.float32), 3, 4, 2)
+    with pytest.raises(H.ArgumentException, match="smaller than the requested"):
+        mgr.BackpropInputProjection(M(3, 4, 1), M(4, 2, 2), 0, z((4, 3), np.float32), z(4, np.float32), 3, 4, 3)
+    with pytest.raises(H.ArgumentException, match="weightGrad or biasGrad"):
+        mgr.BackpropInputProjection(M(3, 4, 1), M(4, 2, 2), 0, z((3, 2), np.float32), z(4, np.float32), 3, 4, 2)
+    cfg = {"dim": 8, "heads": 2, "layers": 1, "ff": 16, "max_seq": 8, "discrete": False, "input_dim": 3,
+           "output_dim": 2}
+    lm, _ = host.language_model(cfg, synth.continuous_lm_weights(cfg, 2))
+    t = H.TransformerTrainer(lm, H.TrainingConfig())
+    x = [z((5, 3), np.float32)]
+    with pytest.raises(H.ArgumentException, match="regressionTargets is required"):
+        t.TrainContinuous(x)
+    with pytest.raises(H.ArgumentException, match="length must match"):
+        t.TrainContinuous(x, regressionTargets=[])
+    with pytest.raises(H.ArgumentException, match="feature dimension 4, expected 3"):
+        t.TrainContinuous([z((5, 4), np.float32)], regressionTargets=[z((5, 2), np.float32)])
+    with pytest.raises(H.ArgumentException, match="No valid sequences"):
+        t.TrainContinuous([z((1, 3), np.float32), None], regressionTargets=[z((1, 2), np.float32), None])
+    with pytest.raises(H.InvalidOperationException, match="TrainContinuous"):
+        t.Train([np.array([1, 2], np.int32)])
+    with pytest.raises(H.InvalidOperationException, match="token model"):
+        t.TrainBatch([np.array([1, 2], np.int32)], 0.1)
+    with pytest.raises(H.InvalidOperationException, match="ForwardContinuousSlice"):
+        t.Validate([np.array([0, 1, 0], np.int32)])  # ids inside the default VocabSize 2
+    tok = {"vocab": 12, "dim": 8, "heads": 2, "layers": 1, "ff": 16, "max_seq": 8}
+    lm2, _ = host.language_model(tok, synth.lm_weights(tok, 1))
+    t2 = H.TransformerTrainer(lm2, H.TrainingConfig())
+    with pytest.raises(H.InvalidOperationException, match="Train\\(int"):
+        t2.TrainContinuous(x, regressionTargets=[z((5, 2), np.float32)])
+    with pytest.raises(H.ArgumentException, match="exceeds MaxSequenceLength"):
+        t2.Validate([np.zeros(10, np.int32)])
+    assert t2.Validate([np.array([4], np.int32), np.array([1, 12], np.int32)]) == 0.0
+
+
 def test_no_device_means_loud_failure(mgr):
     if N.device_count() > 0:
         pytest.skip("a device is visible")
