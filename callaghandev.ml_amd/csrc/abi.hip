@@ -181,9 +181,10 @@ int cdml_init(int device) {
     return fail(CDML_E_INVALID, "cdml_init: device %d out of range [0, %d)", device, n);
   hipError_t e = hipSetDevice(device);
   if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
-  // A failure here leaves the library usable; the no-allocation entry points
-  // then report it.
-  (void)noalloc_scratch_setup(device);
+  // A failure here leaves the library usable and the last error untouched;
+  // the no-allocation entry point reports it when it is called.
+  char msg[256];
+  (void)noalloc_scratch_setup(device, msg, sizeof(msg));
   g_device.store(device, std::memory_order_release);
   return CDML_OK;
 }

@@ -21,8 +21,9 @@ int ensure_device();
 
 // Finds this device's copy of the static scratch behind the no-allocation
 // entry points (hipGetSymbolAddress); called by cdml_init with `device`
-// current.
-int noalloc_scratch_setup(int device);
+// current.  It does not touch the thread's last error: a failure is
+// described in `msg` and reported by the entry point that needs the scratch.
+int noalloc_scratch_setup(int device, char *msg, size_t msg_bytes);
 
 // Compute units of the current device (queried once; 256 on MI355X).
 int num_cus();

@@ -310,17 +310,20 @@ static float *g_scratch_ptr[kScratchMaxDevices];
 }  // namespace
 
 // Looks up this device's copy of `scratch` once (the device is current).
-int noalloc_scratch_setup(int device) {
-  if (device < 0 || device >= kScratchMaxDevices)
-    return fail(CDML_E_INVALID, "device %d is beyond the %d devices the no-allocation entry points track",
-                device, kScratchMaxDevices);
+int noalloc_scratch_setup(int device, char *msg, size_t msg_bytes) {
+  if (device < 0 || device >= kScratchMaxDevices) {
+    snprintf(msg, msg_bytes, "device %d is beyond the %d devices the no-allocation entry points track", device,
+             kScratchMaxDevices);
+    return CDML_E_INVALID;
+  }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[device]) return CDML_OK;
   void *p = nullptr;
   hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
   if (e != hipSuccess || !p) {
     (void)hipGetLastError();
-    return fail(CDML_E_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
+    snprintf(msg, msg_bytes, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
+    return CDML_E_HIP;
   }
   g_scratch_ptr[device] = static_cast<float *>(p);
   return CDML_OK;
@@ -452,8 +455,9 @@ extern "C" int cdml_decode_attn_noalloc(const float *q, const float *kcache, con
   if (e != hipSuccess) return fail(CDML_E_HIP, "hipGetDevice: %s", hipGetErrorString(e));
   float *part = noalloc_scratch_ptr(dev);
   if (!part) {  // cdml_init sets it up; a device made current some other way gets it here
-    rc = noalloc_scratch_setup(dev);
-    if (rc) return rc;
+    char msg[256];
+    rc = noalloc_scratch_setup(dev, msg, sizeof(msg));
+    if (rc) return fail(rc, "cdml_decode_attn_noalloc: %s", msg);
     part = noalloc_scratch_ptr(dev);
   }
   return decode_launch(q, kcache, vcache, kv_len, o, batch, t_max, dim, num_heads, scale, part,

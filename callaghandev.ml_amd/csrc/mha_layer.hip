@@ -29,6 +29,9 @@ extern "C" int cdml_mha_layer_fwd_workspace_size(int batch, int seq_len, int dim
   if (batch < 0 || seq_len < 0 || dim <= 0 || num_heads <= 0 || dim % num_heads)
     return fail(CDML_E_INVALID, "cdml_mha_layer_fwd_workspace_size: bad size (batch %d, seq_len %d, dim %d, "
                                 "heads %d)", batch, seq_len, dim, num_heads);
+  if ((int64_t)batch * seq_len > INT32_MAX)
+    return fail(CDML_E_INVALID, "cdml_mha_layer_fwd_workspace_size: batch x seq_len = %lld rows exceeds %d",
+                (long long)batch * seq_len, INT32_MAX);
   *bytes = workspace_bytes(batch * seq_len, dim, seq_len, dim / num_heads);
   return CDML_OK;
 }
@@ -46,6 +49,9 @@ extern "C" int cdml_mha_layer_fwd(const float *x, const float *wq, const float *
     return fail(CDML_E_INVALID, "cdml_mha_layer_fwd: dim %d not divisible by num_heads %d", dim, num_heads);
   const int head_dim = dim / num_heads;
   if (head_dim & 1) return fail(CDML_E_INVALID, "cdml_mha_layer_fwd: head dim %d must be even (RoPE)", head_dim);
+  if ((int64_t)batch * seq_len > INT32_MAX)
+    return fail(CDML_E_INVALID, "cdml_mha_layer_fwd: batch x seq_len = %lld rows exceeds %d",
+                (long long)batch * seq_len, INT32_MAX);
   if (batch == 0 || seq_len == 0) return CDML_OK;
   if (!x || !wq || !wk || !wv || !wo || !y) return fail(CDML_E_INVALID, "cdml_mha_layer_fwd: NULL pointer");
   const int rows = batch * seq_len;

@@ -546,8 +546,13 @@ PYBIND11_MODULE(_cdml_host, m) {
              d["d2h_bytes"] = t.d2h_bytes;
              d["h2d_skipped_bytes"] = t.h2d_skipped_bytes;
              d["backward_from_saved"] = t.backward_from_saved;
+             d["act_alloc_failures"] = t.act_alloc_failures;
              return d;
            })
+      .def_static("SetProcessActivationCacheBudget", &HipAccelerationManager::SetProcessActivationCacheBudget)
+      .def_static("ProcessActivationCacheBudget", &HipAccelerationManager::ProcessActivationCacheBudget)
+      .def_static("ProcessActivationCacheBytes", &HipAccelerationManager::ProcessActivationCacheBytes)
+      .def_static("InjectActivationAllocFailures", &HipAccelerationManager::InjectActivationAllocFailures)
       .def("Dispose", &HipAccelerationManager::Dispose);
   m.def("host_copy_threads", &HostCopyThreads);
   // The host copy engine on byte arrays (for tests of its slicing).

@@ -361,12 +361,24 @@ class HipAccelerationManager {
   // off, so every activation crosses PCIe on every call.
   void SetActivationCacheLimit(size_t bytes);
   size_t activation_cache_limit() const { return act_limit_; }
+  // The cache memory of all managers of the process together is bounded too
+  // (4 GiB by default): a manager over it evicts its own entries first, and
+  // an array that finds no room, or whose device or pinned allocation fails
+  // after eviction, is moved through the uncached scratch path instead of
+  // failing the call.
+  static void SetProcessActivationCacheBudget(size_t bytes);
+  static size_t ProcessActivationCacheBudget();
+  static size_t ProcessActivationCacheBytes();
+  // Test hook: the next `count` cache allocations fail as an out-of-memory
+  // cdml_malloc would.
+  static void InjectActivationAllocFailures(int count);
   int activation_cache_entries();
   // Host<->device bytes this manager has moved (uploads, downloads) and how
   // many activation uploads the shadow compare saved.
   struct TransferStats {
     uint64_t h2d_bytes = 0, d2h_bytes = 0, h2d_skipped_bytes = 0;
     uint64_t backward_from_saved = 0;  // attention backwards that reused a forward's statistics
+    uint64_t act_alloc_failures = 0;   // cache allocations that failed (the array went uncached or evicted more)
   };
   TransferStats transfer_stats();
 
@@ -447,8 +459,9 @@ class HipAccelerationManager {
   };
   static Out out_of(Matrix &m, const float *dev) { return Out{m.ptr(), m.data.size(), dev}; }
   void act_done(std::initializer_list<Out> outs);
-  ActEntry act_acquire(size_t bytes);
+  ActEntry act_acquire(size_t bytes);  // dev == nullptr: no cache memory, take the scratch path
   void act_release(const ActEntry &e);
+  void act_destroy(const ActEntry &e);
   void act_drop(const float *key);
   void ensure_ready();
   void *scratch(int slot, size_t bytes);
@@ -484,6 +497,7 @@ class HipAccelerationManager {
   std::vector<Pending> pending_;
   std::unordered_map<const float *, ActEntry> acts_;
   std::multimap<size_t, ActEntry> act_free_;
+  std::vector<ActEntry> act_parked_;  // dropped while this call used them; released when it ends
   size_t act_held_ = 0, act_limit_ = size_t(1) << 30;
   uint64_t tick_ = 0, call_ = 0, ver_ = 0;
   TransferStats stats_;

@@ -6,6 +6,7 @@
 // arrays.  Nothing here computes on the CPU: a missing device or library is
 // an InvalidOperationException.
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -15,6 +16,16 @@
 namespace cdml_host {
 
 namespace {
+
+// Activation-cache memory of every manager in the process: device bytes, each
+// paired with as many pinned host bytes.  The process-wide budget bounds the
+// pinned memory however many managers a caller creates (the reference builds
+// one manager per FFN); a manager over it gives back its own least recently
+// used entries, and when it has none left to give, the array takes the
+// uncached scratch path.
+std::atomic<size_t> g_act_bytes{0};
+std::atomic<size_t> g_act_budget{size_t(4) << 30};
+std::atomic<int> g_act_alloc_failures{0};  // injected failures (tests)
 
 void check(int rc, const char *what) {
   if (rc != CDML_OK)
@@ -57,12 +68,10 @@ void HipAccelerationManager::Dispose() {
   decode_.clear();
   for (auto &kv : acts_) act_release(kv.second);
   acts_.clear();
-  for (auto &kv : act_free_) {
-    cdml_free(kv.second.dev);
-    cdml_host_free_pinned(kv.second.pin);
-  }
+  for (const ActEntry &e : act_parked_) act_release(e);
+  act_parked_.clear();
+  for (auto &kv : act_free_) act_destroy(kv.second);
   act_free_.clear();
-  act_held_ = 0;
   cdml_host_free_pinned(stage_);
   stage_ = nullptr;
   stage_cap_ = stage_off_ = 0;
@@ -95,7 +104,9 @@ void HipAccelerationManager::ensure_ready() {
 // start again, and the call gets a new id that marks the activation entries
 // it uses as not evictable.
 void HipAccelerationManager::begin_call() {
-  if (dirty_) sync();  // an earlier call that threw may have left transfers in flight
+  if (dirty_ || !act_parked_.empty()) sync();  // an earlier call that threw may have left transfers in flight
+  for (const ActEntry &e : act_parked_) act_release(e);  // the earlier call is over: its dropped buffers are free
+  act_parked_.clear();
   stage_off_ = 0;
   ++call_;
   defer_ = false;
@@ -278,36 +289,57 @@ HipAccelerationManager::ActEntry HipAccelerationManager::act_acquire(size_t byte
     act_free_.erase(fit);
     return e;
   }
-  // make room: idle buffers first, then the least recently used entries that
-  // this call does not use
-  while (act_held_ + cap > act_limit_) {
+  // give back one buffer: an idle one first, else the least recently used
+  // entry that this call does not use; false when nothing is left to give
+  auto evict_one = [this]() -> bool {
     if (!act_free_.empty()) {
       auto it = std::prev(act_free_.end());
-      cdml_free(it->second.dev);
-      cdml_host_free_pinned(it->second.pin);
-      act_held_ -= it->first;
+      act_destroy(it->second);
       act_free_.erase(it);
-      continue;
+      return true;
     }
     auto lru = acts_.end();
     for (auto it = acts_.begin(); it != acts_.end(); ++it)
       if (it->second.busy != call_ && (lru == acts_.end() || it->second.last < lru->second.last)) lru = it;
-    if (lru == acts_.end()) break;  // everything left is in use by this call
+    if (lru == acts_.end()) return false;
     const ActEntry old = lru->second;
     acts_.erase(lru);
-    cdml_free(old.dev);
-    cdml_host_free_pinned(old.pin);
-    act_held_ -= old.cap;
+    act_destroy(old);
+    return true;
+  };
+  while (act_held_ + cap > act_limit_ || g_act_bytes.load() + cap > g_act_budget.load())
+    if (!evict_one()) return ActEntry{};  // over a limit with nothing to give back: the scratch path
+  for (;;) {
+    ActEntry e;
+    e.cap = cap;
+    bool ok = true;
+    int injected = g_act_alloc_failures.load();
+    while (injected > 0 && !g_act_alloc_failures.compare_exchange_weak(injected, injected - 1)) {
+    }
+    if (injected > 0 || cdml_malloc(&e.dev, cap) != CDML_OK) {
+      ok = false;
+    } else if (cdml_host_alloc_pinned(&e.pin, cap) != CDML_OK) {
+      cdml_free(e.dev);
+      ok = false;
+    }
+    if (ok) {
+      act_held_ += cap;
+      g_act_bytes += cap;
+      return e;
+    }
+    // out of device or pinned memory: give back more and try again, or
+    // leave the array to the scratch path, which the reference's contract
+    // (no cache at all) needs anyway
+    ++stats_.act_alloc_failures;
+    if (!evict_one()) return ActEntry{};
   }
-  ActEntry e;
-  e.cap = cap;
-  check(cdml_malloc(&e.dev, cap), "cdml_malloc");
-  if (cdml_host_alloc_pinned(&e.pin, cap) != CDML_OK) {
-    cdml_free(e.dev);
-    throw InvalidOperationException(std::string("cdml_host_alloc_pinned: ") + cdml_last_error());
-  }
-  act_held_ += cap;
-  return e;
+}
+
+void HipAccelerationManager::act_destroy(const ActEntry &e) {
+  cdml_free(e.dev);
+  cdml_host_free_pinned(e.pin);
+  act_held_ -= e.cap;
+  g_act_bytes -= e.cap;
 }
 
 void HipAccelerationManager::act_release(const ActEntry &e) {
@@ -321,8 +353,14 @@ void HipAccelerationManager::act_release(const ActEntry &e) {
 void HipAccelerationManager::act_drop(const float *key) {
   auto it = acts_.find(key);
   if (it == acts_.end()) return;
-  if (it->second.busy == call_) sync();  // work of this call may still use its buffer
-  act_release(it->second);
+  // An entry this call already handed out (the same host pointer with
+  // another shape, as x and x[:n] give) may be an argument of a launch still
+  // to come: it is parked until the call ends instead of going back to the
+  // idle pool, where the next acquire could reuse or free it.
+  if (it->second.busy == call_)
+    act_parked_.push_back(it->second);
+  else
+    act_release(it->second);
   acts_.erase(it);
 }
 
@@ -337,7 +375,7 @@ const float *HipAccelerationManager::act_in(MatView m, int slot) {
     return static_cast<const float *>(d);
   }
   auto it = acts_.find(m.data);
-  if (it != acts_.end() && it->second.rows == m.rows && it->second.cols == m.cols) {
+  if (it != acts_.end() && it->second.rows == m.rows && it->second.cols == m.cols && it->second.dev) {
     ActEntry &e = it->second;
     e.last = ++tick_;
     if (e.busy != call_ && defer_) {
@@ -353,6 +391,11 @@ const float *HipAccelerationManager::act_in(MatView m, int slot) {
   }
   act_drop(m.data);
   ActEntry e = act_acquire(bytes);
+  if (!e.dev) {  // no cache memory: the uncached path
+    void *d = scratch(slot, bytes);
+    upload(d, m.data, bytes);
+    return static_cast<const float *>(d);
+  }
   e.rows = m.rows;
   e.cols = m.cols;
   e.last = ++tick_;
@@ -381,6 +424,7 @@ float *HipAccelerationManager::act_out(float *host, int rows, int cols, int slot
   if (act_limit_ == 0 || bytes == 0) return static_cast<float *>(scratch(slot, bytes));
   act_drop(host);  // an entry left by a freed array at the same address
   ActEntry e = act_acquire(bytes);
+  if (!e.dev) return static_cast<float *>(scratch(slot, bytes));  // no cache memory: the uncached path
   e.rows = rows;
   e.cols = cols;
   e.last = ++tick_;
@@ -513,13 +557,16 @@ void HipAccelerationManager::SetActivationCacheLimit(size_t bytes) {
   sync();
   for (auto &kv : acts_) act_release(kv.second);
   acts_.clear();
-  for (auto &kv : act_free_) {
-    cdml_free(kv.second.dev);
-    cdml_host_free_pinned(kv.second.pin);
-  }
+  for (const ActEntry &e : act_parked_) act_release(e);
+  act_parked_.clear();
+  for (auto &kv : act_free_) act_destroy(kv.second);
   act_free_.clear();
-  act_held_ = 0;
 }
+
+void HipAccelerationManager::SetProcessActivationCacheBudget(size_t bytes) { g_act_budget.store(bytes); }
+size_t HipAccelerationManager::ProcessActivationCacheBudget() { return g_act_budget.load(); }
+size_t HipAccelerationManager::ProcessActivationCacheBytes() { return g_act_bytes.load(); }
+void HipAccelerationManager::InjectActivationAllocFailures(int count) { g_act_alloc_failures.store(count); }
 
 int HipAccelerationManager::activation_cache_entries() {
   std::lock_guard<std::mutex> lock(mu_);

@@ -193,3 +193,9 @@ def test_mha_layer_fwd_argument_checks():
     assert call(64, 4, wsb=1024) == N.E_INVALID        # workspace too small
     assert call(64, 4, ws=None) == N.E_INVALID         # no workspace
     assert b"workspace" in lib.cdml_last_error()
+    # batch x seq_len beyond int32 rows is rejected in 64-bit arithmetic, in both entries
+    assert lib.cdml_mha_layer_fwd_workspace_size(1 << 16, 1 << 16, 64, 4, C.byref(sz)) == N.E_INVALID
+    assert b"exceeds" in lib.cdml_last_error()
+    assert lib.cdml_mha_layer_fwd(fake, *w[:8], fake, 1 << 16, 1 << 16, 64, 4, 10000.0, 1, None, None, fake,
+                                  1 << 30, None) == N.E_INVALID
+    assert b"exceeds" in lib.cdml_last_error()

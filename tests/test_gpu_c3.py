@@ -7,7 +7,10 @@ The oracle cannot run the full stack in test time, so the full-size run is
 checked through properties that do not depend on size: the causal prefix
 property (rows 0..P-1 of a sequence depend only on its first P inputs, so
 they must equal the stack run on those P rows alone), and a 256-token prefix
-through all 12 layers against the multi-threaded oracle composition.
+through all 12 layers against the multi-threaded oracle composition.  One
+whole 4096-token sequence is also recomputed through all 12 layers in
+float64 numpy (BLAS), so the deep rows, whose attention spans thousands of
+keys, meet the bar against exact arithmetic.
 """
 from __future__ import annotations
 
@@ -80,6 +83,72 @@ def test_c3_stack_prefix_vs_oracle(c3_stack):
     print("[c3] 256-token prefix vs the oracle (12 layers)", flush=True)
     want = _oracle_layers(w, np.ascontiguousarray(x[b * L:b * L + P]), C3["heads"])
     parity(out[b * L:b * L + P], want, what="c3 stack, 256-token prefix of sequence 2 vs oracle")
+
+
+def _float64_layers(w, x, heads):
+    """The post-LN decoder blocks (TransformerBlock.Forward, TransformerBlock.cs:
+    35-44; MultiHeadAttention.Forward, MultiHeadAttention.cs:96-159) in float64
+    numpy: QKV with biases, interleaved RoPE base 10000, causal softmax
+    attention with scale 1/sqrt(d_h), output projection, residual LayerNorm
+    (eps 1e-5, biased variance), FFN [D, FF, D] with ReLU, residual LayerNorm.
+
+    The RoPE angle is the reference's own fp32 quantity, theta =
+    fp32(pos / fp32(10000^fp32(2p/d_h))) (AccelerationCPU.cs:4947-4962): at
+    position 4095 a last-bit change of the denominator moves theta by
+    2e-4 rad, so the angle is taken exactly as the reference defines it and
+    only its cosine and sine are evaluated in float64."""
+    f8 = np.float64
+    n, D = x.shape
+    hd = D // heads
+    e = (np.float32(2) * np.arange(hd // 2, dtype=np.float32)) / np.float32(hd)
+    denom = (f8(10000.0) ** e.astype(f8)).astype(np.float32)
+    theta = (np.arange(n, dtype=np.float32)[:, None] / denom[None, :]).astype(f8)  # fp32 division
+    cs, sn = np.tile(np.cos(theta), heads), np.tile(np.sin(theta), heads)
+    neg = np.where(np.triu(np.ones((n, n), bool), 1), -np.inf, 0.0)  # keys j > i masked
+
+    def ln(r, g, b):
+        mu = r.mean(axis=1, keepdims=True)
+        var = ((r - mu) ** 2).mean(axis=1, keepdims=True)
+        return (r - mu) / np.sqrt(var + 1e-5) * g.astype(f8) + b.astype(f8)
+
+    h = x.astype(f8)
+    for li, Lw in enumerate(w["layers"]):
+        print(f"[c3] float64 layer {li}", flush=True)
+        q, k, v = (h @ Lw[wn].astype(f8).T + Lw[bn].astype(f8)
+                   for wn, bn in (("wq", "bq"), ("wk", "bk"), ("wv", "bv")))
+        for t in (q, k):
+            a, b = t[:, 0::2].copy(), t[:, 1::2].copy()
+            t[:, 0::2], t[:, 1::2] = a * cs - b * sn, a * sn + b * cs
+        att = np.empty_like(q)
+        for hh in range(heads):
+            c = slice(hh * hd, (hh + 1) * hd)
+            sc = q[:, c] @ k[:, c].T
+            sc /= np.sqrt(f8(hd))
+            sc += neg
+            sc -= sc.max(axis=1, keepdims=True)
+            np.exp(sc, out=sc)
+            att[:, c] = (sc @ v[:, c]) / sc.sum(axis=1, keepdims=True)
+            del sc
+        n1 = ln(h + att @ Lw["wo"].astype(f8).T + Lw["bo"].astype(f8), Lw["ln1_g"], Lw["ln1_b"])
+        f = np.maximum(n1 @ Lw["ffn_w1"].astype(f8).T + Lw["ffn_b1"].astype(f8), 0.0)
+        h = ln(n1 + f @ Lw["ffn_w2"].astype(f8).T + Lw["ffn_b2"].astype(f8), Lw["ln2_g"], Lw["ln2_b"])
+    return h
+
+
+def test_c3_stack_full_sequence_vs_float64(c3_stack):
+    """Sequence 3 of the 4 x 4096 run, all 4096 rows through all 12 layers,
+    against the float64 composition: every row meets the bar, the deep rows
+    3840..4095 (attention over up to 4096 keys in every layer) included."""
+    w, _, x, out, _ = c3_stack
+    b = 3
+    print("[c3] full 4096-token sequence vs float64 (12 layers)", flush=True)
+    want = _float64_layers(w, x[b * L:(b + 1) * L], C3["heads"])
+    got = out[b * L:(b + 1) * L]
+    deep = slice(L - 256, L)
+    print(f"[c3] max abs err: all rows {np.abs(got - want).max():.3e}, rows 3840..4095 "
+          f"{np.abs(got[deep] - want[deep]).max():.3e}", flush=True)
+    parity(got[deep], want[deep], what="c3 stack rows 3840..4095 of sequence 3 vs float64")
+    parity(got, want, what="c3 stack, all 4096 rows of sequence 3 vs float64")
 
 
 def test_project_qkv_rope_c3_full_shape_sampled():

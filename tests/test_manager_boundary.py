@@ -143,3 +143,79 @@ def test_small_activation_cache_evicts_and_stays_correct():
     for rep in range(2):
         assert_parity(_mha_manager(m, x, w, b, heads), want, what=f"cache back on, call {rep}")
     m.Dispose()
+
+
+def test_cache_allocation_failures_fall_back_to_the_uncached_path():
+    """When a cache allocation fails (injected here as an out-of-memory
+    cdml_malloc would fail), the manager evicts more and retries, and an array
+    it still cannot place takes the uncached scratch path: the call completes
+    with the same bits as a manager with the cache off.  A process-wide budget
+    smaller than one array sends every array down that path."""
+    Hm = host.module()
+    M = Hm.HipAccelerationManager
+    L, D, heads = 300, 128, 4
+    x, w, b = _mha_inputs(93, L, D)
+    plain = M(0)
+    plain.SetActivationCacheLimit(0)
+    want = _mha_manager(plain, x, w, b, heads)
+    assert_parity(want, _mha_oracle(x, w, b, heads), what="cache off")
+    budget = M.ProcessActivationCacheBudget()
+    m = None
+    try:
+        # a fresh manager allocates a cache entry for each of the sequence's
+        # six activations (x, Q, K, V, attention, output)
+        for fails in (1, 3, 50):
+            m = M(0)
+            M.InjectActivationAllocFailures(fails)
+            got = _mha_manager(m, x, w, b, heads)
+            M.InjectActivationAllocFailures(0)
+            assert np.array_equal(got, want), f"{fails} injected failures"
+            n = m.transfer_stats()["act_alloc_failures"]
+            if fails < 6:
+                assert n == fails and m.activation_cache_entries >= 1, (fails, n)
+            else:  # every allocation failed: nothing cached, every array went through scratch
+                assert n >= 6 and m.activation_cache_entries == 0, n
+                # allocations work again: the next call caches and gives the same bits
+                assert np.array_equal(_mha_manager(m, x, w, b, heads), want)
+                assert m.activation_cache_entries >= 6
+            m.Dispose()
+        # a budget below one array's 64 KiB-rounded size: nothing is cached
+        m = M(0)
+        m2 = M(0)
+        M.SetProcessActivationCacheBudget(64 << 10)
+        before = M.ProcessActivationCacheBytes()
+        got = _mha_manager(m2, x.copy(), w, b, heads)
+        assert np.array_equal(got, want)
+        assert m2.activation_cache_entries == 0
+        assert M.ProcessActivationCacheBytes() <= before
+        m2.Dispose()
+    finally:
+        M.InjectActivationAllocFailures(0)
+        M.SetProcessActivationCacheBudget(budget)
+        if m is not None:
+            m.Dispose()
+        plain.Dispose()
+
+
+def test_same_pointer_with_two_shapes_in_one_call():
+    """x and x[:n] share a data pointer.  Passed to one call (the attention's
+    query and key rows) under a small cache, the second shape replaces the
+    first's entry; the buffer already handed out for the first stays valid
+    until the call ends (it is parked, not freed or reused), and the result
+    matches the oracle."""
+    Hm = host.module()
+    L, n, D, heads = 256, 200, 64, 2
+    q = synth.normal(95, (L, D))
+    kv = synth.normal(96, (L, D))
+    m = Hm.HipAccelerationManager(0)
+    m.SetActivationCacheLimit(2 * L * D * 4)
+    try:
+        for rep in range(3):
+            # Q rows [L, D] and K = V = the first n rows of the same array
+            got = m.MultiHeadAttentionForward(q, q[:n], q[:n], heads, 0.125)
+            want = O.mha_forward(q, np.ascontiguousarray(q[:n]), np.ascontiguousarray(q[:n]), heads, 0.125)
+            assert_parity(got, want, what=f"aliased shapes, call {rep}")
+            # an unrelated call in between, which acquires and evicts
+            m.ProjectOutputBatch(kv, synth.xavier_uniform(97, D, D), np.zeros(D, np.float32), L, D)
+    finally:
+        m.Dispose()

@@ -117,3 +117,67 @@ def test_noalloc_decode_rejects_shapes_beyond_the_scratch():
     assert rc == N.E_INVALID
     msg = lib.cdml_last_error().decode()
     assert "static scratch" in msg and "cdml_decode_attn" in msg
+
+
+def test_noalloc_decode_under_graph_capture():
+    """The entry point's stated use: recorded inside cdml_graph_capture_begin /
+    _end (it launches kernels only, no allocation and no memset) and replayed.
+    Between replays new queries are uploaded and an eager no-allocation call
+    of another shape overwrites the shared scratch; every replay must still
+    equal cdml_decode_attn on the same inputs bit for bit."""
+    st = _stream()
+    lib, s = N.lib(), st.handle
+    B, T, D, H = 8, 1500, 512, 4
+    k, v, dk, dv = _full_cache(st, 300, B, T, D)
+    q0, lens = _case(30, B, T, D, H)
+    dq, dl = N.DeviceBuffer.from_array(q0, st), N.DeviceBuffer.from_array(lens, st)
+    og, oe = N.DeviceBuffer(B * D * 4), N.DeviceBuffer(B * D * 4)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D // H)))
+    ws = C.c_size_t(0)
+    N.check(lib.cdml_decode_attn_workspace_size(B, T, D, H, C.byref(ws)))
+    dws = N.DeviceBuffer(max(4, ws.value))
+    # the other shape's eager call, which reuses the scratch between replays
+    B2, T2, D2, H2 = 3, 700, 256, 2
+    _, _, dk2, dv2 = _full_cache(st, 301, B2, T2, D2)
+    q2, lens2 = _case(31, B2, T2, D2, H2)
+    dq2, dl2, o2 = N.DeviceBuffer.from_array(q2, st), N.DeviceBuffer.from_array(lens2, st), N.DeviceBuffer(B2 * D2 * 4)
+    st.synchronize()
+    print(f"[no_alloc] graph capture B={B} T={T} D={D} H={H}", flush=True)
+    N.check(lib.cdml_graph_capture_begin(s))
+    rc = lib.cdml_decode_attn_noalloc(dq.ptr, dk.ptr, dv.ptr, dl.ptr, og.ptr, B, T, D, H, scale, s)
+    g = C.c_void_p()
+    N.check(lib.cdml_graph_capture_end(s, C.byref(g)))
+    N.check(rc)
+    assert g.value
+    try:
+        for rep in range(4):
+            q = np.random.default_rng(40 + rep).standard_normal((B, D), dtype=np.float32)
+            dq.upload(q, st)
+            N.check(lib.cdml_graph_launch(g, s))
+            st.synchronize()
+            got = og.download((B, D), stream=st)
+            N.check(lib.cdml_decode_attn(dq.ptr, dk.ptr, dv.ptr, dl.ptr, oe.ptr, B, T, D, H, scale, dws.ptr,
+                                         ws.value, s))
+            want = oe.download((B, D), stream=st)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"replay {rep}"
+            if rep == 0:
+                idx = np.array([0, B - 1])
+                ref = O.decode_attention_batch(q[idx], k[idx], v[idx], lens[idx], H, scale, parallel=True)
+                assert_parity(got[idx], ref, what="graph replay of the noalloc decode vs oracle")
+            # eager work on the shared scratch between replays
+            N.check(lib.cdml_decode_attn_noalloc(dq2.ptr, dk2.ptr, dv2.ptr, dl2.ptr, o2.ptr, B2, T2, D2, H2, 0.0625,
+                                                 s))
+            st.synchronize()
+    finally:
+        N.check(lib.cdml_graph_destroy(g))
+
+
+def test_init_leaves_the_last_error_alone():
+    """cdml_init succeeds without writing the thread's last error (its
+    no-allocation scratch lookup reports only through the entry point)."""
+    lib = N.lib()
+    assert lib.cdml_decode_attn_noalloc(None, None, None, None, None, 1, 1, 4, 1, 1.0, None) == N.E_INVALID
+    before = lib.cdml_last_error()
+    assert before
+    assert lib.cdml_init(0) == N.OK
+    assert lib.cdml_last_error() == before
