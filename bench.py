@@ -639,11 +639,46 @@ def pinned_pcie_bandwidth(N, st, mib=256, reps=5):
     return res
 
 
+def _mt_mha(O, x, ws, bs, H):
+    """MultiHeadAttention.Forward's calls on the multi-threaded restatement:
+    ProjectQKV, RoPE of Q and K, causal ScaledDotProductAttention,
+    ProjectOutputBatch (AccelerationMutliThreadCPU.cs:798-831, 3910-3985,
+    1991-2098, 2331-2359)."""
+    q, k, v = O.project_qkv(x, ws[0], bs[0], ws[1], bs[1], ws[2], bs[2], mt=True)
+    q, k = O.rope(q, H, mt=True), O.rope(k, H, mt=True)
+    return O.project_output_batch(O.sdpa(q, k, v, H, causal=True, mt=True), ws[3], bs[3], mt=True)
+
+
+def _mt_block(O, x, ws, bs, ff, H):
+    """TransformerBlock.Forward (TransformerBlock.cs:35-44) on the
+    multi-threaded restatement: MHA, residual LayerNorm, FFN [D, FF, D] with
+    ReLU (BatchDotProductAddBias, :1694-1740), residual LayerNorm
+    (:3988-4018)."""
+    g, z = np.ones(x.shape[1], np.float32), np.zeros(x.shape[1], np.float32)
+    n1 = O.residual_layernorm(x, _mt_mha(O, x, ws, bs, H), g, z, mt=True)
+    h = O.activation(O.batch_dot_add_bias(ff[0], n1, ff[1], mt=True), 3)
+    return O.residual_layernorm(n1, O.batch_dot_add_bias(ff[2], h, ff[3], mt=True), g, z, mt=True)
+
+
+def _timed_units(fn, units, reps=1):
+    """One untimed warm-up call on a full-size unit, then `reps` timed passes
+    over all `units`; returns the seconds of each pass."""
+    fn(units[0])
+    out = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        for u in units:
+            fn(u)
+        out.append(time.perf_counter() - t0)
+    return out
+
+
 def cpu_baseline(sample_seqs=3):
     """The multi-threaded CPU restatement of AccelerationMutliThreadCPU's
     ProjectQKV / RoPE / ScaledDotProductAttention / ProjectOutputBatch
     (oracle/refcpu_mt.c) on `sample_seqs` of the c3 batch's sequences, one
-    LanguageModel.Forward-style call per sequence.  Timed, not checked."""
+    LanguageModel.Forward-style call per sequence, after one untimed
+    full-size sequence.  Timed, not checked."""
     from oracle import oracle as O
     from cdml import synth
 
@@ -653,52 +688,86 @@ def cpu_baseline(sample_seqs=3):
     L, D, H = C3["seq"], C3["dim"], C3["heads"]
     rng = np.random.default_rng(5)
     ws = [synth.xavier_uniform(30 + i, D, D) for i in range(4)]
-    bz = np.zeros(D, np.float32)
+    bs = [np.zeros(D, np.float32)] * 4
     xs = [rng.standard_normal((L, D), dtype=np.float32) for _ in range(sample_seqs)]
-    O.project_qkv(xs[0][:64], ws[0], bz, ws[1], bz, ws[2], bz, mt=True)  # load + warm the library
-    t0 = time.perf_counter()
-    for x in xs:
-        q, k, v = O.project_qkv(x, ws[0], bz, ws[1], bz, ws[2], bz, mt=True)
-        q, k = O.rope(q, H, mt=True), O.rope(k, H, mt=True)
-        a = O.sdpa(q, k, v, H, causal=True, mt=True)
-        O.project_output_batch(a, ws[3], bz, mt=True)
-    dt = time.perf_counter() - t0
+    dt = _timed_units(lambda x: _mt_mha(O, x, ws, bs, H), xs)[0]
     core, qkv, out = mha_flops(sample_seqs, L, D, H)
     return dict(value=(core + qkv + out) / dt / 1e12, unit="TFLOP/s", cores=threads, kind="port",
                 seconds=dt, host=host,
                 sample=f"{sample_seqs} of the 4 c3 sequences (L 4096, D 1024, H 16), full MHA forward "
                        f"through the C restatement of AccelerationMutliThreadCPU (-O2, no fast-math), "
+                       f"after one untimed full-size sequence, "
                        f"{threads} threads (Environment.ProcessorCount equivalent {host['processor_count']}, "
                        f"nproc {host['nproc']}, box share {host['box_cpu_share']}) on {host['cpu_model']}, "
                        f"{dt:.1f} s")
 
 
-def cpu_baseline_other_configs(threads):
-    """The same restatement on bounded samples of the other MFMA configs (c2,
-    c5: the MHA forward of one layer per sequence, as LanguageModel.Forward
-    calls it) and on the c4 decode step, whose reference
-    (LanguageModel.DecoderSelfAttentionStep) is inline and single-threaded:
-    timed sequentially over the batch as the reference runs it, and with the
-    batch spread over the threads (labelled).  Timed, not checked."""
+def cpu_baseline_other_configs(threads, c3_mha_s_per_seq):
+    """The same restatement on bounded samples of the other configs, each
+    after one untimed full-size unit (a sequence, a window, a decode row):
+
+    * c2: the MHA layer forward, 4 of the 16 sequences, 3 timed passes.
+    * c3: one decoder layer (MHA + residual LayerNorm + FFN 4096 + residual
+      LayerNorm) on one sequence; the MHA-only layer is the headline leg.  The
+      4-sequence 12-layer stack time is extrapolated from these and labelled so.
+    * c5: the MHA layer and the whole decoder layer, 64 of the 256 windows
+      each; the 6-layer figure is extrapolated.
+    * c4: the decode step, whose reference (LanguageModel.DecoderSelfAttention-
+      Step) is inline and single-threaded: sequentially over 8 of the 64 rows
+      as the reference runs it, and with the rows spread over the threads
+      (labelled); 3 timed passes each.
+    * c1: the config-1 text model through the single-threaded restatement of
+      LanguageModel.Forward (4 sequences of 64 tokens) and Generate (greedy,
+      20 new tokens after 32-token prompts), 3 timed passes.
+    Timed, not checked."""
     from oracle import oracle as O
     from cdml import synth
 
     out = {}
     rng = np.random.default_rng(6)
-    for name, (B, L, D, H, n) in (("c2", (16, 1024, 512, 8, 4)), ("c5", (256, 512, 256, 8, 64))):
-        ws = [synth.xavier_uniform(40 + i, D, D) for i in range(4)]
-        bz = np.zeros(D, np.float32)
+    r6 = lambda v: round(v, 6)
+    # c2: MHA layer
+    B, L, D, H, n = 16, 1024, 512, 8, 4
+    ws = [synth.xavier_uniform(40 + i, D, D) for i in range(4)]
+    bs = [np.zeros(D, np.float32)] * 4
+    xs = [rng.standard_normal((L, D), dtype=np.float32) for _ in range(n)]
+    t = _timed_units(lambda x: _mt_mha(O, x, ws, bs, H), xs, reps=3)
+    core, qkv, o = mha_flops(n, L, D, H)
+    med = float(np.median(t))
+    out["c2"] = {"value": r6((core + qkv + o) / med / 1e12), "unit": "TFLOP/s", "seconds_per_pass": [r6(v) for v in t],
+                 "sample": f"{n} of the {B} sequences (L {L}, D {D}, H {H}), MHA layer forward, one untimed "
+                           f"sequence then 3 timed passes (median), {threads} threads"}
+    # c3 and c5: MHA layer, and MHA + FFN + 2 LayerNorms
+    for name, (B, L, D, H, FF, nl, n) in (("c3", (4, 4096, 1024, 16, 4096, 12, 1)),
+                                          ("c5", (256, 512, 256, 8, 1024, 6, 64))):
+        ws = [synth.xavier_uniform(50 + i, D, D) for i in range(4)]
+        bs = [np.zeros(D, np.float32)] * 4
+        ff = [synth.xavier_uniform(60, FF, D), np.zeros(FF, np.float32), synth.xavier_uniform(61, D, FF),
+              np.zeros(D, np.float32)]
         xs = [rng.standard_normal((L, D), dtype=np.float32) for _ in range(n)]
-        t0 = time.perf_counter()
-        for x in xs:
-            q, k, v = O.project_qkv(x, ws[0], bz, ws[1], bz, ws[2], bz, mt=True)
-            q, k = O.rope(q, H, mt=True), O.rope(k, H, mt=True)
-            a = O.sdpa(q, k, v, H, causal=True, mt=True)
-            O.project_output_batch(a, ws[3], bz, mt=True)
-        dt = time.perf_counter() - t0
         core, qkv, o = mha_flops(n, L, D, H)
-        out[name] = {"value": round((core + qkv + o) / dt / 1e12, 6), "unit": "TFLOP/s", "seconds": round(dt, 3),
-                     "sample": f"{n} of the {B} sequences (L {L}, D {D}, H {H}), MHA layer forward, {threads} threads"}
+        mha_fl = core + qkv + o
+        ffn_fl = 2 * 2 * n * L * D * FF
+        leg = {}
+        if name == "c5":
+            t_mha = _timed_units(lambda x: _mt_mha(O, x, ws, bs, H), xs)[0]
+            leg["mha_layer"] = {"value": r6(mha_fl / t_mha / 1e12), "unit": "TFLOP/s", "seconds": r6(t_mha)}
+        else:
+            t_mha = c3_mha_s_per_seq * n
+            leg["mha_layer"] = {"value": r6(mha_fl / t_mha / 1e12), "unit": "TFLOP/s", "seconds": r6(t_mha),
+                                "from": "the headline cpu_baseline leg"}
+        t_blk = _timed_units(lambda x: _mt_block(O, x, ws, bs, ff, H), xs)[0]
+        leg["decoder_layer"] = {"value": r6((mha_fl + ffn_fl) / t_blk / 1e12), "unit": "TFLOP/s",
+                                "seconds": r6(t_blk)}
+        per_seq = t_blk / n
+        leg[f"stack_{nl}_layers_batch_{B}_extrapolated"] = {
+            "seconds": round(per_seq * nl * B, 2), "tokens_per_s": round(B * L / (per_seq * nl * B), 1),
+            "how": f"extrapolated: the timed decoder layer's seconds per sequence x {nl} layers x {B} "
+                   f"sequences, not run"}
+        leg["sample"] = (f"{n} of the {B} sequences (L {L}, D {D}, H {H}, FF {FF}), one untimed sequence per "
+                         f"form, {threads} threads")
+        out[name] = leg
+    # c4: decode
     B, T, D, H = 8, C4["t"], C4["dim"], C4["heads"]
     q = rng.standard_normal((B, D), dtype=np.float32)
     kc = rng.standard_normal((B, T, D), dtype=np.float32)
@@ -708,14 +777,31 @@ def cpu_baseline_other_configs(threads):
     nbytes = decode_bytes(B, T, D)
     dec = {}
     for label, parallel in (("sequential", False), ("parallel_over_batch", True)):
-        O.decode_attention_batch(q[:1], kc[:1, :64], vc[:1, :64], lens[:1] * 0 + 64, H, scale, parallel)
-        t0 = time.perf_counter()
-        O.decode_attention_batch(q, kc, vc, lens, H, scale, parallel)
-        dt = time.perf_counter() - t0
-        dec[label] = {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "ms_per_step_of_64": round(dt / B * 64 * 1e3, 3)}
-    dec["sample"] = (f"{B} of the 64 decode rows (KV {T}, D {D}, H {H}); the sequential form runs one thread as "
-                     f"the reference's inline step does, the parallel one spreads the rows over {threads} threads")
+        O.decode_attention_batch(q[:1], kc[:1], vc[:1], lens[:1], H, scale, parallel)  # one full-size row
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            O.decode_attention_batch(q, kc, vc, lens, H, scale, parallel)
+            ts.append(time.perf_counter() - t0)
+        dt = float(np.median(ts))
+        dec[label] = {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s",
+                      "ms_per_step_of_64": round(dt / B * 64 * 1e3, 3)}
+    dec["sample"] = (f"{B} of the 64 decode rows (KV {T}, D {D}, H {H}), one untimed row then 3 timed passes "
+                     f"(median); the sequential form runs one thread as the reference's inline step does, the "
+                     f"parallel one spreads the rows over {threads} threads")
     out["c4_decode"] = dec
+    # c1: the README text model, forward and greedy generation
+    cfg = {"vocab": 200, "dim": 64, "heads": 4, "layers": 2, "ff": 128, "max_seq": 64}
+    lm = O.LanguageModel(cfg, synth.lm_weights(cfg, 5, biased=True))
+    ids = synth.token_ids(7, 4 * 64, 200).reshape(4, 64)
+    fwd = _timed_units(lambda s: lm.forward(s), list(ids), reps=3)
+    gen = _timed_units(lambda s: lm.generate_greedy(s[:32], 20), list(ids), reps=3)
+    out["c1"] = {"forward_ms": round(float(np.median(fwd)) * 1e3, 3),
+                 "generate_20_tokens_batch4_ms": round(float(np.median(gen)) * 1e3, 3),
+                 "tokens_per_s_generate": round(4 * 20 / float(np.median(gen)), 1), "cores": 1,
+                 "sample": "the whole config (4 sequences of 64 tokens; 4 prompts of 32 tokens, 20 greedy tokens "
+                           "each, one sequence at a time as LanguageModel.Forward / Generate run), single-threaded "
+                           "restatement of AccelerationCPU, one untimed sequence then 3 timed passes (median)"}
     return out
 
 
@@ -807,7 +893,7 @@ def main():
         log("[bench] CPU baseline (multi-threaded restatement)")
         cb = cpu_baseline()
         res["cpu_baseline"] = {k: (round(v, 6) if isinstance(v, float) else v) for k, v in cb.items()}
-        res["cpu_baseline"]["other_configs"] = cpu_baseline_other_configs(cb["cores"])
+        res["cpu_baseline"]["other_configs"] = cpu_baseline_other_configs(cb["cores"], cb["seconds"] / 3)
     print(json.dumps(res), flush=True)
 
 
