@@ -132,15 +132,26 @@ struct KvStage {
 // BN + 4, so that the P.V step reads the four consecutive keys of one V^T
 // column it needs for four MFMA steps in a single 16-byte read.  A thread
 // takes two consecutive keys of a 4-wide column group (two 16-byte global
-// loads of adjacent lanes' contiguous row slices) and writes them as four
-// 8-byte pairs Vt[c + j][2p .. 2p + 1].  Rows past lk are clamped as in
-// KvStage.
+// loads) and writes them as four 8-byte pairs Vt[c + j][2p .. 2p + 1].
+// Lanes 8m .. 8m + 7 of a wave take key pairs 0..7 (of an 8-pair block) of
+// column group m (of an 8-group block): the sixteen lanes of an 8-byte store
+// phase then cover two column groups, whose V^T rows (4 * pitch floats apart,
+// 16 banks apart) each receive eight contiguous pairs, so no two lanes share
+// a bank, and each 16-byte load instruction still reads 128 contiguous bytes
+// of each of 8 rows.  (With consecutive lanes on consecutive column groups
+// of one key pair, sixteen lanes' rows fell on two bank groups.)  Rows past
+// lk are clamped as in KvStage.
 template <int HD, int BN, bool VEC>
 struct VtStage {
   static constexpr int NCG = HD / 4;               // 4-wide column groups
-  static constexpr int NU = BN / 2 * NCG / FA_THREADS;  // (key pair, column group) units per thread
+  static constexpr int NKP = BN / 2;               // key pairs
+  static constexpr int NU = NKP * NCG / FA_THREADS;  // (key pair, column group) units per thread
+  static_assert(NKP % 8 == 0 && NCG % 8 == 0, "V tile blocks of 8 key pairs x 8 column groups");
+  // key pair and column group of unit u (64 units per 8 x 8 block)
+  __device__ __forceinline__ static int unit_kp(int u) { return (u & 7) + 8 * ((u >> 6) % (NKP / 8)); }
+  __device__ __forceinline__ static int unit_cg(int u) { return ((u >> 3) & 7) + 8 * ((u >> 6) / (NKP / 8)); }
   static constexpr int NS = BN * HD / FA_THREADS;
-  static_assert(BN / 2 * NCG % FA_THREADS == 0, "V tile units must divide the workgroup");
+  static_assert(NKP * NCG % FA_THREADS == 0, "V tile units must divide the workgroup");
   vf4 r[VEC ? 2 * NU : 1];
   float s[VEC ? 1 : NS];
   uint32_t off[VEC ? NU : 1];  // byte offset of each unit's first row in a tile
@@ -151,8 +162,8 @@ struct VtStage {
 #pragma unroll
       for (int i = 0; i < NU; ++i) {
         const int u = threadIdx.x + FA_THREADS * i;
-        col[i] = (u % NCG) * 4;
-        off[i] = 4u * (uint32_t)(2 * (u / NCG) * ld + col[i]);
+        col[i] = unit_cg(u) * 4;
+        off[i] = 4u * (uint32_t)(2 * unit_kp(u) * ld + col[i]);
       }
     }
   }
@@ -186,7 +197,7 @@ struct VtStage {
 #pragma unroll
       for (int i = 0; i < NU; ++i) {
         const int u = threadIdx.x + FA_THREADS * i;
-        const int kp = 2 * (u / NCG);
+        const int kp = 2 * unit_kp(u);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           typedef float vf2 __attribute__((ext_vector_type(2)));
