@@ -53,6 +53,7 @@ SIGNATURES = {
     "cdml_tiny_layer_check": [_vp, _i],
     "cdml_tiny_decode": [_vp, _vp, _i, _i, _i, _vp],
     "cdml_event_create": [C.POINTER(_vp)],
+    "cdml_event_create_sync_only": [C.POINTER(_vp)],
     "cdml_event_destroy": [_vp],
     "cdml_event_record": [_vp, _vp],
     "cdml_event_synchronize": [_vp],

@@ -311,6 +311,17 @@ int cdml_event_record(cdml_event event, cdml_stream stream) {
   return CDML_OK;
 }
 
+int cdml_event_create_sync_only(cdml_event *event) {
+  if (!event) return fail(CDML_E_INVALID, "cdml_event_create_sync_only: event is NULL");
+  int rc = ensure_device();
+  if (rc) return rc;
+  hipEvent_t ev;
+  hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+  if (e != hipSuccess) return hip_fail(e, "hipEventCreateWithFlags");
+  *event = reinterpret_cast<cdml_event>(ev);
+  return CDML_OK;
+}
+
 int cdml_event_synchronize(cdml_event event) {
   if (!event) return fail(CDML_E_INVALID, "cdml_event_synchronize: event is NULL");
   hipError_t e = hipEventSynchronize(reinterpret_cast<hipEvent_t>(event));

@@ -24,6 +24,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <functional>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -174,7 +175,7 @@ struct FeedForwardNetwork {
 
 // ---- host copies (staging.cpp) ---------------------------------------------
 // memcpy / memcmp split over a process-wide pool of host threads for large
-// sizes (the pool has min(12, 3/4 of the CPUs) threads beside the caller, or
+// sizes (the pool has min(7, 3/4 of the CPUs) threads beside the caller, or
 // CDML_HOST_COPY_THREADS).
 void ParallelMemcpy(void *dst, const void *src, size_t bytes);
 bool ParallelEqual(const void *a, const void *b, size_t bytes);
@@ -448,6 +449,8 @@ class HipAccelerationManager {
   void *stage_region(size_t bytes);
   void stage_upload(void *dev, const void *host, size_t bytes, void *pin);
   void download_all(const std::vector<Xfer> &xs);
+  void download_enqueue(const std::vector<Xfer> &xs);
+  void download_finish(const std::vector<Xfer> &xs);
   const float *act_in(MatView m, int slot);
   float *act_inplace(MatRef m, int slot);
   float *act_out(float *host, int rows, int cols, int slot);
@@ -459,9 +462,14 @@ class HipAccelerationManager {
   };
   static Out out_of(Matrix &m, const float *dev) { return Out{m.ptr(), m.data.size(), dev}; }
   void act_done(std::initializer_list<Out> outs);
+  std::vector<Xfer> act_transfers(std::initializer_list<Out> outs);
+  void launch_settle_download(const std::function<void()> &launch, std::initializer_list<Out> outs);
   ActEntry act_acquire(size_t bytes);  // dev == nullptr: no cache memory, take the scratch path
   void act_release(const ActEntry &e);
   void act_destroy(const ActEntry &e);
+  bool inplace_overlapped(MatRef m, const std::function<void(float *)> &launch);
+  void *spare_pin(size_t cap);
+  void spare_put(void *p, size_t cap);
   void act_drop(const float *key);
   void ensure_ready();
   void *scratch(int slot, size_t bytes);
@@ -498,6 +506,7 @@ class HipAccelerationManager {
   std::unordered_map<const float *, ActEntry> acts_;
   std::multimap<size_t, ActEntry> act_free_;
   std::vector<ActEntry> act_parked_;  // dropped while this call used them; released when it ends
+  std::multimap<size_t, void *> pin_spare_;  // idle pinned buffers that in-place calls swap with shadows
   size_t act_held_ = 0, act_limit_ = size_t(1) << 30;
   uint64_t tick_ = 0, call_ = 0, ver_ = 0;
   TransferStats stats_;

@@ -10,6 +10,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
 
 #include "cdml_host.h"
 
@@ -72,6 +73,8 @@ void HipAccelerationManager::Dispose() {
   act_parked_.clear();
   for (auto &kv : act_free_) act_destroy(kv.second);
   act_free_.clear();
+  for (auto &kv : pin_spare_) cdml_host_free_pinned(kv.second);
+  pin_spare_.clear();
   cdml_host_free_pinned(stage_);
   stage_ = nullptr;
   stage_cap_ = stage_off_ = 0;
@@ -232,33 +235,64 @@ void HipAccelerationManager::stage_upload(void *dev, const void *host, size_t by
 // enqueued first, each followed by an event, then each chunk is copied out as
 // soon as its event has completed, while the later chunks are still moving.
 void HipAccelerationManager::download_all(const std::vector<Xfer> &xs) {
-  const size_t kChunk = stage_chunk();
-  size_t chunks = 0;
-  for (const Xfer &x : xs) chunks += (x.bytes + kChunk - 1) / kChunk;
-  while (events_.size() < chunks) {
+  download_enqueue(xs);
+  download_finish(xs);
+}
+
+// The chunks of a group of downloads, stage_chunk() bytes each.  (Splitting
+// the final chunk into quarters, so that less of the copy out trails the last
+// DMA, measured slower: every chunk costs a DMA submission and an event, and
+// below 8 MiB those costs outweigh the overlap.)
+namespace {
+struct Chunk {
+  size_t xfer, off, bytes;
+};
+std::vector<Chunk> plan_chunks(const std::vector<size_t> &sizes) {
+  const size_t big = stage_chunk();
+  std::vector<Chunk> out;
+  for (size_t i = 0; i < sizes.size(); ++i)
+    for (size_t off = 0; off < sizes[i]; off += big) out.push_back(Chunk{i, off, std::min(big, sizes[i] - off)});
+  return out;
+}
+template <class X>
+std::vector<size_t> sizes_of(const std::vector<X> &xs) {
+  std::vector<size_t> v;
+  for (const X &x : xs) v.push_back(x.bytes);
+  return v;
+}
+}  // namespace
+
+// The DMA half of download_all: every chunk's copy into pinned memory, each
+// followed by an event.  Enqueuing the same transfers again re-records the
+// events, so download_finish then waits for the later copies.
+void HipAccelerationManager::download_enqueue(const std::vector<Xfer> &xs) {
+  const std::vector<Chunk> chunks = plan_chunks(sizes_of(xs));
+  while (events_.size() < chunks.size()) {
     cdml_event e = nullptr;
-    check(cdml_event_create(&e), "cdml_event_create");
+    check(cdml_event_create_sync_only(&e), "cdml_event_create_sync_only");
     events_.push_back(e);
   }
-  size_t c = 0;
-  for (const Xfer &x : xs)
-    for (size_t off = 0; off < x.bytes; off += kChunk, ++c) {
-      const size_t n = std::min(kChunk, x.bytes - off);
-      check(cdml_memcpy_d2h_async(static_cast<char *>(x.pin) + off, static_cast<const char *>(x.dev) + off, n,
-                                  stream_),
-            "cdml_memcpy_d2h_async");
-      check(cdml_event_record(events_[c], stream_), "cdml_event_record");
-      dirty_ = true;
-    }
-  c = 0;
-  for (const Xfer &x : xs) {
-    for (size_t off = 0; off < x.bytes; off += kChunk, ++c) {
-      const size_t n = std::min(kChunk, x.bytes - off);
-      check(cdml_event_synchronize(events_[c]), "cdml_event_synchronize");
-      ParallelMemcpy(static_cast<char *>(x.host) + off, static_cast<const char *>(x.pin) + off, n);
-    }
-    stats_.d2h_bytes += x.bytes;
+  for (size_t c = 0; c < chunks.size(); ++c) {
+    const Xfer &x = xs[chunks[c].xfer];
+    check(cdml_memcpy_d2h_async(static_cast<char *>(x.pin) + chunks[c].off,
+                                static_cast<const char *>(x.dev) + chunks[c].off, chunks[c].bytes, stream_),
+          "cdml_memcpy_d2h_async");
+    check(cdml_event_record(events_[c], stream_), "cdml_event_record");
+    dirty_ = true;
   }
+}
+
+// The host half: each chunk is copied out of pinned memory as soon as its
+// event has completed.
+void HipAccelerationManager::download_finish(const std::vector<Xfer> &xs) {
+  const std::vector<Chunk> chunks = plan_chunks(sizes_of(xs));
+  for (size_t c = 0; c < chunks.size(); ++c) {
+    const Xfer &x = xs[chunks[c].xfer];
+    check(cdml_event_synchronize(events_[c]), "cdml_event_synchronize");
+    ParallelMemcpy(static_cast<char *>(x.host) + chunks[c].off, static_cast<const char *>(x.pin) + chunks[c].off,
+                   chunks[c].bytes);
+  }
+  for (const Xfer &x : xs) stats_.d2h_bytes += x.bytes;
 }
 
 void HipAccelerationManager::upload(void *dev, const void *host, size_t bytes) {
@@ -436,7 +470,9 @@ float *HipAccelerationManager::act_out(float *host, int rows, int cols, int slot
 
 // Downloads each result from its device buffer, through its entry's shadow
 // when the buffer belongs to one (the shadow then matches the host again).
-void HipAccelerationManager::act_done(std::initializer_list<Out> outs) {
+void HipAccelerationManager::act_done(std::initializer_list<Out> outs) { download_all(act_transfers(outs)); }
+
+std::vector<HipAccelerationManager::Xfer> HipAccelerationManager::act_transfers(std::initializer_list<Out> outs) {
   std::vector<Xfer> xs;
   for (const Out &o : outs) {
     const size_t bytes = o.floats * sizeof(float);
@@ -445,7 +481,28 @@ void HipAccelerationManager::act_done(std::initializer_list<Out> outs) {
     void *pin = (it != acts_.end() && it->second.dev == o.dev) ? it->second.pin : stage_region(bytes);
     xs.push_back(Xfer{o.host, const_cast<float *>(o.dev), bytes, pin});
   }
-  download_all(xs);
+  return xs;
+}
+
+// For methods whose kernels write nothing but their results, into buffers
+// the caller cannot see yet: the kernel runs on the device copies of the
+// inputs and the results' downloads into pinned memory are enqueued behind
+// it before the deferred compares of the inputs run, so the compares
+// overlap the kernel and the DMA.  If an input changed on the host, it is
+// uploaded and the kernel and the downloads run again (the stream orders
+// them after the first ones); the results reach the host arrays only after
+// the compares, from the last downloads.
+void HipAccelerationManager::launch_settle_download(const std::function<void()> &launch,
+                                                    std::initializer_list<Out> outs) {
+  launch();
+  std::vector<Xfer> xs = act_transfers(outs);
+  download_enqueue(xs);
+  if (!settle()) {
+    launch();
+    xs = act_transfers(outs);  // an upload may have moved the staging buffer
+    download_enqueue(xs);
+  }
+  download_finish(xs);
 }
 
 // ---- attention row statistics kept for the backward --------------------------
@@ -561,6 +618,8 @@ void HipAccelerationManager::SetActivationCacheLimit(size_t bytes) {
   act_parked_.clear();
   for (auto &kv : act_free_) act_destroy(kv.second);
   act_free_.clear();
+  for (auto &kv : pin_spare_) cdml_host_free_pinned(kv.second);
+  pin_spare_.clear();
 }
 
 void HipAccelerationManager::SetProcessActivationCacheBudget(size_t bytes) { g_act_budget.store(bytes); }
@@ -648,9 +707,7 @@ std::tuple<Matrix, Matrix, Matrix> HipAccelerationManager::ProjectQKV(MatView in
     check(cdml_project_qkv(dx, wq, bq, wk, bk, wv, bv, dq, dk, dv, rows, inputDim, qDim, stream_),
           "cdml_project_qkv");
   };
-  launch();
-  if (!settle()) launch();
-  act_done({out_of(Q, dq), out_of(K, dk), out_of(V, dv)});
+  launch_settle_download(launch, {out_of(Q, dq), out_of(K, dk), out_of(V, dv)});
   sync();
   return {std::move(Q), std::move(K), std::move(V)};
 }
@@ -691,7 +748,13 @@ Matrix HipAccelerationManager::attention(MatView q, MatView k, MatView v, int nu
             "cdml_sdpa_fwd");
   };
   launch();
-  if (!settle()) launch();
+  std::vector<Xfer> xs = act_transfers({out_of(out, dout)});
+  download_enqueue(xs);  // overlaps the compares below (launch_settle_download)
+  if (!settle()) {
+    launch();
+    xs = act_transfers({out_of(out, dout)});
+    download_enqueue(xs);
+  }
   if (lse) {
     auto eq = acts_.find(q.data), ek = acts_.find(k.data), ev = acts_.find(v.data), eo = acts_.find(out.ptr());
     if (eq != acts_.end() && ek != acts_.end() && ev != acts_.end() && eo != acts_.end()) {
@@ -718,7 +781,7 @@ Matrix HipAccelerationManager::attention(MatView q, MatView k, MatView v, int nu
       lse_record(r);
     }
   }
-  act_done({out_of(out, dout)});
+  download_finish(xs);
   sync();
   return out;
 }
@@ -796,9 +859,7 @@ Matrix HipAccelerationManager::linear(MatView x, int rowStart, int rowCount, Mat
   auto launch = [&] {
     check(cdml_linear(dx, in, dw, db, dy, out, rowCount, in, out, act, stream_), "cdml_linear");
   };
-  launch();
-  if (!settle()) launch();
-  act_done({out_of(y, dy)});
+  launch_settle_download(launch, {out_of(y, dy)});
   sync();
   return y;
 }
@@ -850,6 +911,77 @@ Matrix HipAccelerationManager::BatchDotProductAddBias(MatView weights, MatView i
   return linear(inputMatrix, rowStart, rowCount, weights, bias, CDML_ACT_NONE);
 }
 
+// ---- in-place kernels on resident activations ---------------------------------
+// A spare pinned buffer of exactly `cap` bytes (nullptr when none can be
+// allocated), and its return; at most two spares stay idle per manager.
+void *HipAccelerationManager::spare_pin(size_t cap) {
+  auto it = pin_spare_.find(cap);
+  if (it != pin_spare_.end()) {
+    void *p = it->second;
+    pin_spare_.erase(it);
+    return p;
+  }
+  void *p = nullptr;
+  if (cdml_host_alloc_pinned(&p, cap) != CDML_OK) return nullptr;
+  return p;
+}
+
+void HipAccelerationManager::spare_put(void *p, size_t cap) {
+  pin_spare_.emplace(cap, p);
+  while (pin_spare_.size() > 2) {
+    auto last = std::prev(pin_spare_.end());
+    cdml_host_free_pinned(last->second);
+    pin_spare_.erase(last);
+  }
+}
+
+// An in-place kernel on the resident copy of `m` with the shadow compare
+// overlapped: the kernel runs on the device copy and its result is
+// downloaded into a spare pinned buffer while the host array is compared
+// with the shadow.  If the host array is unchanged, the spare's contents go
+// to the host array and the spare becomes the shadow; otherwise the host
+// contents are uploaded and the kernel runs again, as without the cache.
+// Returns false (nothing done) when `m` has no resident entry this call may
+// use, or is too small for the overlap to pay; the caller then takes the
+// plain path.
+bool HipAccelerationManager::inplace_overlapped(MatRef m, const std::function<void(float *)> &launch) {
+  const size_t bytes = (size_t)m.rows * m.cols * sizeof(float);
+  if (act_limit_ == 0 || bytes < (size_t(4) << 20)) return false;
+  auto it = acts_.find(m.data);
+  if (it == acts_.end() || it->second.rows != m.rows || it->second.cols != m.cols || it->second.busy == call_)
+    return false;
+  const size_t cap = it->second.cap;
+  void *spare = spare_pin(cap);
+  if (!spare) return false;
+  ActEntry &e = it->second;
+  e.busy = call_;
+  e.last = ++tick_;
+  e.ver = ++ver_;  // the device copy changes in every outcome
+  float *d = static_cast<float *>(e.dev);
+  try {
+    launch(d);
+    std::vector<Xfer> xs{Xfer{m.data, d, bytes, spare}};
+    download_enqueue(xs);
+    if (ParallelEqual(m.data, e.pin, bytes)) {
+      stats_.h2d_skipped_bytes += bytes;
+      download_finish(xs);
+      spare_put(e.pin, cap);
+      e.pin = spare;
+      return true;
+    }
+    sync();  // the speculative download is done with the device buffer and the spare
+    spare_put(spare, cap);
+    spare = nullptr;
+    stage_upload(d, m.data, bytes, e.pin);
+    launch(d);
+    download_all({Xfer{m.data, d, bytes, e.pin}});
+    return true;
+  } catch (...) {
+    if (spare) spare_put(spare, cap);
+    throw;
+  }
+}
+
 // ---- RoPE: AccelerationCPU.cs:4855-4982 --------------------------------------
 void HipAccelerationManager::ApplyRotaryPositionEmbeddingInPlace(MatRef matrix, int numHeads,
                                                                  float baseTheta, bool inverse) {
@@ -864,11 +996,18 @@ void HipAccelerationManager::ApplyRotaryPositionEmbeddingInPlace(MatRef matrix, 
   if (matrix.rows == 0 || headDim == 0) return;
   std::lock_guard<std::mutex> lock(mu_);
   ensure_ready();
-  float *dx = act_inplace(matrix, S_X);
-  try {
+  auto launch = [&](float *dx) {
     check(cdml_rope(dx, matrix.rows, dim, 0, headDim, numHeads, baseTheta, inverse ? 1 : 0, 0, 0,
                     nullptr, stream_),
           "cdml_rope");
+  };
+  try {
+    if (inplace_overlapped(matrix, launch)) {
+      sync();
+      return;
+    }
+    float *dx = act_inplace(matrix, S_X);
+    launch(dx);
     act_done({Out{matrix.data, (size_t)matrix.rows * dim, dx}});
     sync();
   } catch (...) {
@@ -928,9 +1067,7 @@ Matrix HipAccelerationManager::ResidualLayerNorm(MatView input, MatView subLayer
     check(cdml_residual_layernorm(da, dbb, dg, db, dy, rows, f, epsilon, stream_),
           "cdml_residual_layernorm");
   };
-  launch();
-  if (!settle()) launch();
-  act_done({out_of(out, dy)});
+  launch_settle_download(launch, {out_of(out, dy)});
   sync();
   return out;
 }
@@ -1042,9 +1179,7 @@ Matrix HipAccelerationManager::FFNForwardBatch(MatView input, int seqLen, int ou
       wdt = w.rows;
     }
   };
-  launch();
-  if (!settle()) launch();
-  act_done({out_of(out, dout)});
+  launch_settle_download(launch, {out_of(out, dout)});
   sync();
   return out;
 }

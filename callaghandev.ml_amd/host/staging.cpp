@@ -6,6 +6,7 @@
 // which one thread cannot keep up with against PCIe.  Shadow compares of
 // resident activations (is the host array still what the device holds?)
 // read two such arrays.
+#include <immintrin.h>
 #include <sched.h>
 
 #include <algorithm>
@@ -39,7 +40,10 @@ int pool_threads() {
   cpu_set_t set;
   if (sched_getaffinity(0, sizeof(set), &set) == 0) cpus = CPU_COUNT(&set);
   if (cpus <= 0) cpus = (int)std::thread::hardware_concurrency();
-  return std::max(0, std::min(12, 3 * cpus / 4));  // plus the calling thread
+  // plus the calling thread; eight threads in all already saturate the
+  // host memory beside a running DMA on the GPU box (16 CPUs: 4.05 ms per
+  // c3 drop-in sequence with 8 threads against 4.2 ms with 13)
+  return std::max(0, std::min(7, 3 * cpus / 4));
 }
 
 class Pool {
@@ -61,6 +65,7 @@ class Pool {
     if (threads_ > 0 && n > 1) {
       std::lock_guard<std::mutex> lock(mu_);
       jobs_.push_back(job);
+      posted_.fetch_add(1, std::memory_order_release);
       cv_.notify_all();
     }
     work_on(*job);
@@ -87,8 +92,16 @@ class Pool {
     }
   }
 
+  // A worker that finished a job polls for the next one for a while before
+  // it sleeps: the jobs of one manager call (the chunks of a download, each
+  // posted when its DMA lands) come tens of microseconds apart, and a
+  // condition-variable wake-up of a dozen sleeping threads costs about that.
   void worker() {
+    uint64_t seen = posted_.load(std::memory_order_acquire);
     for (;;) {
+      for (int spin = 0; spin < kSpin && posted_.load(std::memory_order_acquire) == seen; ++spin)
+        __builtin_ia32_pause();
+      seen = posted_.load(std::memory_order_acquire);
       std::shared_ptr<Job> job;
       {
         std::unique_lock<std::mutex> lock(mu_);
@@ -103,7 +116,9 @@ class Pool {
     }
   }
 
+  static constexpr int kSpin = 20000;  // pause instructions, roughly 100-200 us
   int threads_ = 0;
+  std::atomic<uint64_t> posted_{0};
   std::mutex mu_;
   std::condition_variable cv_;
   std::deque<std::shared_ptr<Job>> jobs_;
@@ -176,6 +191,42 @@ void HostArrayFree(void *p, size_t bytes) {
 
 int HostCopyThreads() { return pool().threads() + 1; }
 
+namespace {
+
+// A slice copy with non-temporal 64-byte stores: the destination is written
+// without being read into the cache first, a third less memory traffic than
+// a cached copy, which matters while a DMA into the pinned buffers competes
+// for the same memory (measured on the GPU box: 115 against 100 GB/s from
+// pinned memory beside a running device-to-host DMA, 160 against 136 GB/s
+// alone, with eight threads).
+__attribute__((target("avx512f"))) void stream_copy_avx512(char *d, const char *s, size_t n) {
+  size_t head = (64 - (reinterpret_cast<uintptr_t>(d) & 63)) & 63;
+  if (head > n) head = n;
+  std::memcpy(d, s, head);
+  size_t i = head;
+  for (; i + 256 <= n; i += 256) {
+    const __m512i a = _mm512_loadu_si512(s + i), b = _mm512_loadu_si512(s + i + 64),
+                  c = _mm512_loadu_si512(s + i + 128), e = _mm512_loadu_si512(s + i + 192);
+    _mm512_stream_si512(reinterpret_cast<__m512i *>(d + i), a);
+    _mm512_stream_si512(reinterpret_cast<__m512i *>(d + i + 64), b);
+    _mm512_stream_si512(reinterpret_cast<__m512i *>(d + i + 128), c);
+    _mm512_stream_si512(reinterpret_cast<__m512i *>(d + i + 192), e);
+  }
+  std::memcpy(d + i, s + i, n - i);
+  _mm_sfence();  // the streaming stores are visible before the slice is reported done
+}
+
+const bool kHaveAvx512 = __builtin_cpu_supports("avx512f");
+
+void copy_slice(void *dst, const void *src, size_t n) {
+  if (kHaveAvx512 && n >= 4096)
+    stream_copy_avx512(static_cast<char *>(dst), static_cast<const char *>(src), n);
+  else
+    std::memcpy(dst, src, n);
+}
+
+}  // namespace
+
 void ParallelMemcpy(void *dst, const void *src, size_t bytes) {
   if (bytes < kParallelMin) {
     if (bytes) std::memcpy(dst, src, bytes);
@@ -186,8 +237,7 @@ void ParallelMemcpy(void *dst, const void *src, size_t bytes) {
   pool().run(n, [&](int i) {
     const size_t off = (size_t)i * per;
     if (off < bytes)
-      std::memcpy(static_cast<char *>(dst) + off, static_cast<const char *>(src) + off,
-                  std::min(per, bytes - off));
+      copy_slice(static_cast<char *>(dst) + off, static_cast<const char *>(src) + off, std::min(per, bytes - off));
   });
 }
 

@@ -78,6 +78,11 @@ int cdml_stream_create(cdml_stream *stream);
 int cdml_stream_destroy(cdml_stream stream);
 int cdml_stream_synchronize(cdml_stream stream);
 int cdml_event_create(cdml_event *event);
+/* An event for host waits only (no timestamps; cdml_event_elapsed_ms
+ * rejects it): lighter to record, for the per-chunk events of a staged
+ * download.  No counterpart in the reference, whose ILGPU copies are
+ * synchronous (TransformerCore.cs:1300-1348). */
+int cdml_event_create_sync_only(cdml_event *event);
 int cdml_event_destroy(cdml_event event);
 int cdml_event_record(cdml_event event, cdml_stream stream);
 /* Blocks until the work recorded before `event` has finished (a host that

@@ -219,3 +219,47 @@ def test_same_pointer_with_two_shapes_in_one_call():
             m.ProjectOutputBatch(kv, synth.xavier_uniform(97, D, D), np.zeros(D, np.float32), L, D)
     finally:
         m.Dispose()
+
+
+def test_inplace_rope_on_resident_arrays_follows_host_edits():
+    """In-place RoPE on a returned 4 MiB activation runs on the device copy
+    while the host array is compared with its shadow.  An unchanged array is
+    not uploaded; an array edited on the host since the manager returned it
+    is rotated from the edited contents; and the shadow after either path
+    holds the rotated contents (a third rotation starts from them)."""
+    Hm = host.module()
+    L, D, heads = 1024, 1024, 16
+    x = synth.normal(98, (L, D))
+    w = [synth.xavier_uniform(99 + j, D, D) for j in range(3)]
+    b = [np.zeros(D, np.float32)] * 3
+    m = Hm.HipAccelerationManager(0)
+    try:
+        q, _, _ = m.ProjectQKV(x, w[0], b[0], w[1], b[1], w[2], b[2])
+        want = O.rope(q, heads)
+        s0 = m.transfer_stats()
+        m.ApplyRotaryPositionEmbeddingInPlace(q, heads, 10000.0, False)  # unchanged since returned
+        s1 = m.transfer_stats()
+        assert_parity(q, want, what="in-place RoPE of an unchanged resident array")
+        assert s1["h2d_bytes"] == s0["h2d_bytes"] and s1["h2d_skipped_bytes"] - s0["h2d_skipped_bytes"] >= q.nbytes
+        q[5, 7] += 1.0  # a host edit after the last call
+        q[L - 1, D - 1] = -3.0
+        want = O.rope(q, heads)
+        m.ApplyRotaryPositionEmbeddingInPlace(q, heads, 10000.0, False)
+        s2 = m.transfer_stats()
+        assert_parity(q, want, what="in-place RoPE after a host edit")
+        assert s2["h2d_bytes"] - s1["h2d_bytes"] >= q.nbytes
+        want = O.rope(q, heads, inverse=True)
+        m.ApplyRotaryPositionEmbeddingInPlace(q, heads, 10000.0, True)  # from the shadow of the last result
+        assert_parity(q, want, what="inverse RoPE after the edited rotation")
+        # the same array through a manager without the cache gives the same bits
+        m0 = Hm.HipAccelerationManager(0)
+        m0.SetActivationCacheLimit(0)
+        q2 = want.copy()
+        m0.ApplyRotaryPositionEmbeddingInPlace(q2, heads, 10000.0, False)
+        q3 = q.copy()
+        m.ApplyRotaryPositionEmbeddingInPlace(q, heads, 10000.0, False)
+        m0.ApplyRotaryPositionEmbeddingInPlace(q3, heads, 10000.0, False)
+        assert np.array_equal(q, q3)
+        m0.Dispose()
+    finally:
+        m.Dispose()
