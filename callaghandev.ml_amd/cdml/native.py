@@ -52,6 +52,7 @@ SIGNATURES = {
     "cdml_graph_destroy": [_vp],
     "cdml_tiny_layer_check": [_vp, _i],
     "cdml_tiny_decode": [_vp, _vp, _i, _i, _i, _vp],
+    "cdml_stream_wait_event": [_vp, _vp],
     "cdml_event_create": [C.POINTER(_vp)],
     "cdml_event_create_sync_only": [C.POINTER(_vp)],
     "cdml_event_destroy": [_vp],

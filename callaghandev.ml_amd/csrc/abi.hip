@@ -286,6 +286,15 @@ int cdml_stream_synchronize(cdml_stream stream) {
   return CDML_OK;
 }
 
+int cdml_stream_wait_event(cdml_stream stream, cdml_event event) {
+  if (!event) return fail(CDML_E_INVALID, "cdml_stream_wait_event: event is NULL");
+  int rc = ensure_device();
+  if (rc) return rc;
+  hipError_t e = hipStreamWaitEvent(as_hip(stream), reinterpret_cast<hipEvent_t>(event), 0);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamWaitEvent");
+  return CDML_OK;
+}
+
 int cdml_event_create(cdml_event *event) {
   if (!event) return fail(CDML_E_INVALID, "cdml_event_create: event is NULL");
   int rc = ensure_device();

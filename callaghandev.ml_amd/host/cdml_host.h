@@ -449,8 +449,10 @@ class HipAccelerationManager {
   void *stage_region(size_t bytes);
   void stage_upload(void *dev, const void *host, size_t bytes, void *pin);
   void download_all(const std::vector<Xfer> &xs);
-  void download_enqueue(const std::vector<Xfer> &xs);
-  void download_finish(const std::vector<Xfer> &xs);
+  // on `st` (the manager's stream when null), with chunk events from index ev0
+  void download_enqueue(const std::vector<Xfer> &xs, cdml_stream st = nullptr, size_t ev0 = 0);
+  void download_finish(const std::vector<Xfer> &xs, size_t ev0 = 0);
+  cdml_stream copy_stream();
   const float *act_in(MatView m, int slot);
   float *act_inplace(MatRef m, int slot);
   float *act_out(float *host, int rows, int cols, int slot);
@@ -492,6 +494,8 @@ class HipAccelerationManager {
   int device_;
   bool ready_ = false, disposed_ = false;
   cdml_stream stream_ = nullptr;
+  cdml_stream copy_ = nullptr;     // downloads that overlap the next kernel (created on first use)
+  cdml_event kev_[2] = {nullptr, nullptr};  // ends of the kernel parts those downloads wait for
   std::mutex mu_;
   std::unordered_map<const float *, Resident> resident_;
   std::vector<DeviceBuf> scratch_;

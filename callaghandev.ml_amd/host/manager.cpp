@@ -87,6 +87,15 @@ void HipAccelerationManager::Dispose() {
   ffn_scratch_.clear();
   for (cdml_event e : events_) cdml_event_destroy(e);
   events_.clear();
+  if (copy_) {
+    cdml_stream_synchronize(copy_);
+    cdml_stream_destroy(copy_);
+    copy_ = nullptr;
+    for (cdml_event &e : kev_) {
+      cdml_event_destroy(e);
+      e = nullptr;
+    }
+  }
   cdml_stream_destroy(stream_);
   stream_ = nullptr;
 }
@@ -265,9 +274,10 @@ std::vector<size_t> sizes_of(const std::vector<X> &xs) {
 // The DMA half of download_all: every chunk's copy into pinned memory, each
 // followed by an event.  Enqueuing the same transfers again re-records the
 // events, so download_finish then waits for the later copies.
-void HipAccelerationManager::download_enqueue(const std::vector<Xfer> &xs) {
+void HipAccelerationManager::download_enqueue(const std::vector<Xfer> &xs, cdml_stream st, size_t ev0) {
+  if (!st) st = stream_;
   const std::vector<Chunk> chunks = plan_chunks(sizes_of(xs));
-  while (events_.size() < chunks.size()) {
+  while (events_.size() < ev0 + chunks.size()) {
     cdml_event e = nullptr;
     check(cdml_event_create_sync_only(&e), "cdml_event_create_sync_only");
     events_.push_back(e);
@@ -275,20 +285,20 @@ void HipAccelerationManager::download_enqueue(const std::vector<Xfer> &xs) {
   for (size_t c = 0; c < chunks.size(); ++c) {
     const Xfer &x = xs[chunks[c].xfer];
     check(cdml_memcpy_d2h_async(static_cast<char *>(x.pin) + chunks[c].off,
-                                static_cast<const char *>(x.dev) + chunks[c].off, chunks[c].bytes, stream_),
+                                static_cast<const char *>(x.dev) + chunks[c].off, chunks[c].bytes, st),
           "cdml_memcpy_d2h_async");
-    check(cdml_event_record(events_[c], stream_), "cdml_event_record");
+    check(cdml_event_record(events_[ev0 + c], st), "cdml_event_record");
     dirty_ = true;
   }
 }
 
 // The host half: each chunk is copied out of pinned memory as soon as its
 // event has completed.
-void HipAccelerationManager::download_finish(const std::vector<Xfer> &xs) {
+void HipAccelerationManager::download_finish(const std::vector<Xfer> &xs, size_t ev0) {
   const std::vector<Chunk> chunks = plan_chunks(sizes_of(xs));
   for (size_t c = 0; c < chunks.size(); ++c) {
     const Xfer &x = xs[chunks[c].xfer];
-    check(cdml_event_synchronize(events_[c]), "cdml_event_synchronize");
+    check(cdml_event_synchronize(events_[ev0 + c]), "cdml_event_synchronize");
     ParallelMemcpy(static_cast<char *>(x.host) + chunks[c].off, static_cast<const char *>(x.pin) + chunks[c].off,
                    chunks[c].bytes);
   }
@@ -305,7 +315,16 @@ void HipAccelerationManager::download(void *host, const void *dev, size_t bytes)
   download_all({Xfer{host, const_cast<void *>(dev), bytes, stage_region(bytes)}});
 }
 
+cdml_stream HipAccelerationManager::copy_stream() {
+  if (!copy_) {
+    check(cdml_stream_create(&copy_), "cdml_stream_create");
+    for (cdml_event &e : kev_) check(cdml_event_create_sync_only(&e), "cdml_event_create_sync_only");
+  }
+  return copy_;
+}
+
 void HipAccelerationManager::sync() {
+  if (copy_) check(cdml_stream_synchronize(copy_), "cdml_stream_synchronize");
   check(cdml_stream_synchronize(stream_), "cdml_stream_synchronize");
   dirty_ = false;
 }
@@ -703,11 +722,50 @@ std::tuple<Matrix, Matrix, Matrix> HipAccelerationManager::ProjectQKV(MatView in
   defer_ = false;
   Matrix Q = Matrix::Uninit(rows, qDim), K = Matrix::Uninit(rows, kDim), V = Matrix::Uninit(rows, vDim);
   float *dq = act_out(Q, S_Q), *dk = act_out(K, S_K), *dv = act_out(V, S_V);
-  auto launch = [&] {
-    check(cdml_project_qkv(dx, wq, bq, wk, bk, wv, bv, dq, dk, dv, rows, inputDim, qDim, stream_),
+  auto launch_rows = [&](int r0, int n) {
+    const size_t o = (size_t)r0 * qDim;
+    check(cdml_project_qkv(dx + (size_t)r0 * inputDim, wq, bq, wk, bk, wv, bv, dq + o, dk + o, dv + o, n, inputDim,
+                           qDim, stream_),
           "cdml_project_qkv");
   };
-  launch_settle_download(launch, {out_of(Q, dq), out_of(K, dk), out_of(V, dv)});
+  const size_t outBytes = (size_t)rows * qDim * sizeof(float);
+  if (rows < 2048 || outBytes < (size_t(16) << 20)) {
+    launch_settle_download([&] { launch_rows(0, rows); }, {out_of(Q, dq), out_of(K, dk), out_of(V, dv)});
+  } else {
+    // Two row halves: the first half's rows of Q, K and V move on the copy
+    // stream while the kernel computes the second half, so most of the
+    // kernel time hides behind the DMA that bounds the call.
+    const int h = (rows / 2 + 255) / 256 * 256;
+    const std::vector<Xfer> all = act_transfers({out_of(Q, dq), out_of(K, dk), out_of(V, dv)});
+    auto part = [&](int r0, int n) {
+      std::vector<Xfer> p;
+      const size_t off = (size_t)r0 * qDim * sizeof(float), b = (size_t)n * qDim * sizeof(float);
+      for (const Xfer &x : all)
+        p.push_back(Xfer{static_cast<char *>(x.host) + off, static_cast<char *>(x.dev) + off, b,
+                         static_cast<char *>(x.pin) + off});
+      return p;
+    };
+    const std::vector<Xfer> xs0 = part(0, h), xs1 = part(h, rows - h);
+    const size_t n0 = plan_chunks(sizes_of(xs0)).size();
+    cdml_stream cs = copy_stream();
+    auto run = [&] {
+      launch_rows(0, h);
+      check(cdml_event_record(kev_[0], stream_), "cdml_event_record");
+      check(cdml_stream_wait_event(cs, kev_[0]), "cdml_stream_wait_event");
+      download_enqueue(xs0, cs, 0);
+      launch_rows(h, rows - h);
+      check(cdml_event_record(kev_[1], stream_), "cdml_event_record");
+      check(cdml_stream_wait_event(cs, kev_[1]), "cdml_stream_wait_event");
+      download_enqueue(xs1, cs, n0);
+    };
+    run();
+    if (!settle()) {  // an input changed: the first downloads finish before the kernel runs again
+      check(cdml_stream_synchronize(cs), "cdml_stream_synchronize");
+      run();
+    }
+    download_finish(xs0, 0);
+    download_finish(xs1, n0);
+  }
   sync();
   return {std::move(Q), std::move(K), std::move(V)};
 }

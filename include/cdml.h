@@ -77,6 +77,11 @@ const char *cdml_version(void);
 int cdml_stream_create(cdml_stream *stream);
 int cdml_stream_destroy(cdml_stream stream);
 int cdml_stream_synchronize(cdml_stream stream);
+/* Makes later work on `stream` wait for the work recorded before `event`
+ * (on any stream), without blocking the host: a host that downloads one part
+ * of a result on a copy stream while the kernel computes the next part on
+ * its own stream.  No counterpart in the reference (ILGPU runs one stream). */
+int cdml_stream_wait_event(cdml_stream stream, cdml_event event);
 int cdml_event_create(cdml_event *event);
 /* An event for host waits only (no timestamps; cdml_event_elapsed_ms
  * rejects it): lighter to record, for the per-chunk events of a staged

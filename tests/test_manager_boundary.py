@@ -263,3 +263,31 @@ def test_inplace_rope_on_resident_arrays_follows_host_edits():
         m0.Dispose()
     finally:
         m.Dispose()
+
+
+def test_project_qkv_split_downloads_and_host_edits():
+    """ProjectQKV with at least 2048 rows and 16 MiB per output runs in two
+    row halves, the first half's downloads overlapping the second half's
+    kernel on a copy stream.  Rows on both sides of the split (1280 of 2500)
+    meet the bar against the oracle, and a host edit of the resident input
+    between two calls reruns both halves from the edited contents."""
+    Hm = host.module()
+    rows, D = 2500, 2048
+    x = synth.normal(110, (rows, D))
+    w = [synth.xavier_uniform(111 + j, D, D) for j in range(3)]
+    b = [np.float32(0.1) * synth.normal(114 + j, (D,)) for j in range(3)]
+    m = Hm.HipAccelerationManager(0)
+    try:
+        sample = np.array([0, 1, 1279, 1280, 1281, 2047, 2048, rows - 1])
+        for step in range(3):
+            if step == 2:
+                x[1279, 3] += 2.0  # edited on the host after the manager saw it
+                x[2400, :] *= 0.5
+            q, k, v = m.ProjectQKV(x, w[0], b[0], w[1], b[1], w[2], b[2])
+            rws = np.concatenate([sample, [2400]])
+            want = O.project_qkv(np.ascontiguousarray(x[rws]), w[0], b[0], w[1], b[1], w[2], b[2])
+            for got, wnt, n in zip((q, k, v), want, "QKV"):
+                assert_parity(got[rws], wnt, what=f"split ProjectQKV {n}, call {step}")
+        assert m.transfer_stats()["h2d_skipped_bytes"] >= x.nbytes  # the unedited second call
+    finally:
+        m.Dispose()
