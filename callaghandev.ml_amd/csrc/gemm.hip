@@ -64,6 +64,11 @@ struct GemmArgs {
   int ksplit, kchunk, tiles;
   float *ws, *wsb;
   int small;  // split-K by wgrad_small_kernel (kchunk counts rows, not k-tiles)
+  // K segments of an input-gradient launch (opB stored [K, N], one problem):
+  // when kseg > 0, k-tiles [s * kseg, (s + 1) * kseg) read opA from p[s].a
+  // and opB from p[s].w (s < 3), so dX = dQ WQ + dK WK + dV WV is one
+  // product with K = 3 * out.  (It fills the padding before `pre`.)
+  int kseg;
   // Single-problem epilogue options (store_elem): pre receives the
   // pre-activation acc + bias (forward layers whose backward needs it); dz
   // multiplies the result by act'(dz) with act = dact (the hidden deltas of
@@ -89,6 +94,9 @@ template <int BI, int BJ>
 __device__ __forceinline__ void store_rope(const GemmArgs &args, const GemmProblem &P,
                                            const floatx16 (&acc)[BI][BJ], int mrow0, int ncol0,
                                            int li, int hf) {
+  // each rotation product rounded before the sum, as the reference and the
+  // in-place rope kernels evaluate it: no fused multiply-add
+#pragma clang fp contract(off)
   const int pairs = args.rope_hd >> 1;
   int n[BJ], pidx[BJ];
   bool odd[BJ];
@@ -518,20 +526,40 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const Gem
   const int nk = args.ksplit > 1 ? min(args.kchunk, K / BKK - kt0) : K / BKK;
   const float *__restrict__ A = StageA::tile(P.a, kt0, args.lda);
   const float *__restrict__ W = StageB::tile(P.w, kt0, args.ldb);
+  // K segments exist only in the plain input-gradient instance (in the
+  // epilogue instances their selects would cost the registers of the second
+  // workgroup per CU); the segment of k-tile kt is wave-uniform, so choosing
+  // it takes scalar selects only.
+  constexpr bool SEG = TB && !TA && !EPI;
+  const bool seg = SEG && args.kseg > 0;
+  auto load_seg = [&](int kt) {
+    const int sg = (kt >= args.kseg) + (kt >= 2 * args.kseg);
+    const int kl = kt - sg * args.kseg;
+    sa.load(StageA::tile(sg == 0 ? args.p[0].a : sg == 1 ? args.p[1].a : args.p[2].a, kl, args.lda));
+    sb.load(StageB::tile(sg == 0 ? args.p[0].w : sg == 1 ? args.p[1].w : args.p[2].w, kl, args.ldb));
+  };
   const bool bsum = TA && P.bgrad && tn == 0;
   constexpr int KCH = NT / TM;  // k slices per row for the bias-gradient sums
   static_assert(NT % TM == 0 && BKK % (4 * KCH) == 0, "bias-gradient slices");
   float bpart = 0.f;
 
   // k-tile 0 -> LDS, k-tile 1 -> registers
-  sa.load(StageA::tile(A, 0, args.lda));
-  sb.load(StageB::tile(W, 0, args.ldb));
+  if (SEG && seg) {
+    load_seg(0);
+  } else {
+    sa.load(StageA::tile(A, 0, args.lda));
+    sb.load(StageB::tile(W, 0, args.ldb));
+  }
   sa.store(As[0]);
   sb.store(Bs[0]);
   {
     const int k1 = min(1, nk - 1);
-    sa.load(StageA::tile(A, k1, args.lda));
-    sb.load(StageB::tile(W, k1, args.ldb));
+    if (SEG && seg) {
+      load_seg(k1);
+    } else {
+      sa.load(StageA::tile(A, k1, args.lda));
+      sb.load(StageB::tile(W, k1, args.ldb));
+    }
   }
   __syncthreads();
 
@@ -583,8 +611,12 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const Gem
       }
     }
     const int k2 = min(kt + 2, nk - 1);
-    sa.load(StageA::tile(A, k2, args.lda));
-    sb.load(StageB::tile(W, k2, args.ldb));
+    if (SEG && seg) {
+      load_seg(k2);
+    } else {
+      sa.load(StageA::tile(A, k2, args.lda));
+      sb.load(StageB::tile(W, k2, args.ldb));
+    }
     __syncthreads();
   }
 
@@ -770,6 +802,7 @@ __global__ void __launch_bounds__(256) gemm_rows_kernel(const GemmArgs args) {
   z0 += P.bias ? P.bias[n0] : 0.f;
   if (has1) z1 += P.bias ? P.bias[n0 + 1] : 0.f;
   if (args.rope_cs && prob < 2) {  // AccelerationCPU.cs:4947-4975 on the pair (n0, n0 + 1)
+#pragma clang fp contract(off)
     int pos = args.rope_pos0 + (args.rope_seg > 0 ? m % args.rope_seg : m);
     pos = min(pos, args.rope_npos - 1);
     const float2 t = args.rope_cs[(size_t)pos * (args.rope_hd >> 1) + ((n0 % args.rope_hd) >> 1)];
@@ -1211,6 +1244,13 @@ int launch_gemm(GemmArgs &g, bool ta, bool tb, hipStream_t stream, const char *w
   bool fast = g.K % 16 == 0 && g.K > 0;
   for (int i = 0; i < g.nprob; ++i)
     fast = fast && stage_ok(g.p[i].a, g.M, g.lda, ta, 16) && stage_ok(g.p[i].w, g.N, g.ldb, tb, 16);
+  if (g.kseg) {  // only the tiled input-gradient kernel reads K segments
+    bool ok = !ta && tb && !has_epi(g) && g.nprob == 1 && g.ksplit <= 1 && g.kseg * 16 * 3 == g.K;
+    for (int i = 0; ok && i < 3; ++i)
+      ok = stage_ok(g.p[i].a, g.M, g.lda, false, 16) && stage_ok(g.p[i].w, g.N, g.ldb, true, 16);
+    if (!ok) return fail(CDML_E_INVALID, "%s: K segments need the tiled input-gradient kernel", what);
+    fast = true;
+  }
   if (ta || tb) {
     int rc;
     // A ragged K: the tiled kernel covers the whole 16-row k-tiles (it never
@@ -1605,10 +1645,28 @@ extern "C" int cdml_backprop_qkv(const float *x, const float *dq, const float *d
     if (rc) return rc;
   }
   if (in_dim > 0) {
-    // dX = dQ WQ + dK WK + dV WV, the three products accumulated in turn
+    // dX = dQ WQ + dK WK + dV WV: one product over K = 3 * out_dim when the
+    // tiled kernel can stage all three operand pairs (the k-loop switches
+    // source at each third), else the three products accumulated in turn
     // (out_dim == 0: dX = 0)
     const float *d[3] = {dq, dk, dv};
     const float *w[3] = {wq, wk, wv};
+    bool fused = out_dim > 0 && out_dim % 16 == 0 && (long long)3 * out_dim <= INT32_MAX;
+    for (int s = 0; fused && s < 3; ++s)
+      fused = stage_ok(d[s], rows, out_dim, false, 16) && stage_ok(w[s], in_dim, in_dim, true, 16);
+    if (fused) {
+      GemmArgs g{};
+      g.lda = out_dim;
+      g.ldb = in_dim;
+      g.ldc = in_dim;
+      g.M = rows;
+      g.N = in_dim;
+      g.K = 3 * out_dim;
+      g.nprob = 1;
+      for (int s = 0; s < 3; ++s) g.p[s] = {d[s], w[s], nullptr, dx, nullptr};
+      g.kseg = out_dim / 16;
+      return launch_gemm(g, false, true, st, "cdml_backprop_qkv (input gradient)");
+    }
     for (int s = 0; s < 3; ++s) {
       GemmArgs g{};
       g.lda = out_dim;

@@ -7,6 +7,7 @@
 // every device thread forms theta = pos / denom[p] from bit-identical
 // operands (the rotation angle reaches thousands of radians at long
 // positions, where a one-ulp difference in denom would show in sin/cos).
+#include <algorithm>
 #include <cmath>
 
 #include "common.h"
@@ -25,6 +26,9 @@ struct RopeArgs {
 };
 
 __global__ void __launch_bounds__(256) rope_kernel(const RopeArgs a) {
+  // (x0 cos) - (x1 sin) with both products rounded, as the reference
+  // evaluates it: no fused multiply-add
+#pragma clang fp contract(off)
   const long long total = (long long)a.rows * a.num_heads * a.pairs;
   for (long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
        idx += (long long)gridDim.x * blockDim.x) {
@@ -62,10 +66,82 @@ __global__ void __launch_bounds__(256) rope_table_kernel(const RopeArgs a, float
   }
 }
 
+// Q and K rotated together from a cdml_rope_table (the trainer's
+// ApplySegmentedRotaryInPlace, TransformerTrainer.cs:811-848): blockIdx.y
+// picks the matrix, each thread one unit of W floats (W = 4: two pairs moved
+// as float4, the head dim a multiple of 4; W = 2: one pair) of row
+// idx / units.  The rotation is rope_kernel's expression on the table's
+// (cos, sin), so the bits equal cdml_rope's.
+template <int W>
+__global__ void __launch_bounds__(256) rope_qk_table_kernel(float *q, float *k, int rows, int ld, int units,
+                                                            int head_dim, int pairs, const float2 *__restrict__ cs,
+                                                            int pos_offset, int seg_len, int inverse) {
+#pragma clang fp contract(off)
+  float *x = blockIdx.y ? k : q;
+  const unsigned total = (unsigned)rows * (unsigned)units;
+  for (unsigned idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
+    const unsigned row = idx / (unsigned)units;
+    const int col = W * (int)(idx - row * (unsigned)units);
+    const int pos = pos_offset + (seg_len > 0 ? (int)(row % (unsigned)seg_len) : (int)row);
+    const int p0 = (col % head_dim) / 2;
+    float *px = x + (size_t)row * ld + col;
+    if constexpr (W == 4) {
+      const float4 t = *reinterpret_cast<const float4 *>(cs + (size_t)pos * pairs + p0);
+      const float4 v = *reinterpret_cast<const float4 *>(px);
+      const float s0 = inverse ? -t.y : t.y, s1 = inverse ? -t.w : t.w;
+      float4 o;
+      o.x = v.x * t.x - v.y * s0;
+      o.y = v.x * s0 + v.y * t.x;
+      o.z = v.z * t.z - v.w * s1;
+      o.w = v.z * s1 + v.w * t.z;
+      *reinterpret_cast<float4 *>(px) = o;
+    } else {
+      const float2 t = cs[(size_t)pos * pairs + p0];
+      const float s0 = inverse ? -t.y : t.y;
+      const float x0 = px[0], x1 = px[1];
+      px[0] = x0 * t.x - x1 * s0;
+      px[1] = x0 * s0 + x1 * t.x;
+    }
+  }
+}
+
 }  // namespace
 }  // namespace cdml
 
 using namespace cdml;
+
+extern "C" int cdml_rope_qk_table(float *q, float *k, int rows, int ld, int head_dim, int num_heads,
+                                  const float *rope_cs, int n_pos, int pos_offset, int seg_len, int inverse,
+                                  cdml_stream stream) {
+  if (rows < 0 || ld < 0 || head_dim < 0 || num_heads <= 0 || n_pos < 0 || seg_len < 0 || pos_offset < 0)
+    return fail(CDML_E_INVALID, "cdml_rope_qk_table: bad size");
+  if (head_dim & 1) return fail(CDML_E_INVALID, "cdml_rope_qk_table: RoPE requires an even head dimension");
+  if ((long long)head_dim * num_heads > ld) return fail(CDML_E_INVALID, "cdml_rope_qk_table: heads exceed the row");
+  if (rows == 0 || head_dim == 0) return CDML_OK;
+  if (!q || !rope_cs) return fail(CDML_E_INVALID, "cdml_rope_qk_table: NULL pointer");
+  if (q == k) return fail(CDML_E_INVALID, "cdml_rope_qk_table: q and k must be different arrays");
+  if (reinterpret_cast<uintptr_t>(rope_cs) % 8)
+    return fail(CDML_E_INVALID, "cdml_rope_qk_table: rope_cs must be 8-byte aligned");
+  const long long last = (long long)pos_offset + (seg_len > 0 ? std::min(seg_len, rows) : rows) - 1;
+  if (last >= n_pos)
+    return fail(CDML_E_INVALID, "cdml_rope_qk_table: position %lld outside the table's %d", last, n_pos);
+  const bool v4 = head_dim % 4 == 0 && ld % 4 == 0 && aligned16(q) && (!k || aligned16(k)) && aligned16(rope_cs);
+  const int width = head_dim * num_heads, units = v4 ? width / 4 : width / 2;
+  if ((long long)rows * units >= (1ll << 31))
+    return fail(CDML_E_INVALID, "cdml_rope_qk_table: %d rows of %d heads exceed 2^31 units", rows, num_heads);
+  int rc = ensure_device();
+  if (rc) return rc;
+  const long long total = (long long)rows * units;
+  const dim3 grid((unsigned)std::min<long long>((total + 255) / 256, 8192), k ? 2 : 1), block(256);
+  const float2 *cs = reinterpret_cast<const float2 *>(rope_cs);
+  if (v4)
+    rope_qk_table_kernel<4><<<grid, block, 0, as_hip(stream)>>>(q, k, rows, ld, units, head_dim, head_dim / 2, cs,
+                                                                pos_offset, seg_len, inverse ? 1 : 0);
+  else
+    rope_qk_table_kernel<2><<<grid, block, 0, as_hip(stream)>>>(q, k, rows, ld, units, head_dim, head_dim / 2, cs,
+                                                                pos_offset, seg_len, inverse ? 1 : 0);
+  return check_launch("rope_qk_table_kernel");
+}
 
 extern "C" int cdml_rope(float *x, int rows, int ld, int start_col, int head_dim, int num_heads,
                          float base_theta, int inverse, int pos_offset, int seg_len,

@@ -187,6 +187,7 @@ __global__ void __launch_bounds__(kTinyThreads) tiny_decode_kernel(const cdml_ti
       // RoPE of q and k at `pos` (AccelerationCPU.cs:4947-4975): pair p of a
       // head is columns 2p and 2p + 1, (cos, sin) from the model's table
       for (int e = t; e < D; e += kTinyThreads) {
+#pragma clang fp contract(off)
         if (e & 1) continue;
         const float2 cs = reinterpret_cast<const float2 *>(m.rope_cs)[(size_t)pos * (hd / 2) + (e % hd) / 2];
         const float q0 = q[e], q1 = q[e + 1], k0 = kv[0][e], k1 = kv[0][e + 1];

@@ -365,6 +365,51 @@ __global__ void __launch_bounds__(1024) ln_param_grad_kernel(const float *__rest
   }
 }
 
+// First pass of the dGamma / dBeta sums for many row blocks: workgroup
+// (c, s) adds the partials of blocks s * chunk .. min((s + 1) * chunk, nblk)
+// - 1 for columns 64 c .. 64 c + 63 (wave w takes the slice's blocks w, w + 4,
+// ..., the four wave sums then added in wave order) and writes them as row s
+// of out_g / out_b, which ln_param_grad_kernel then sums.  The order is fixed,
+// so results do not depend on timing.
+__global__ void __launch_bounds__(256) ln_param_slice_kernel(const float *__restrict__ part_g,
+                                                             const float *__restrict__ part_b,
+                                                             float *__restrict__ out_g,
+                                                             float *__restrict__ out_b, int nblk,
+                                                             int chunk, int f) {
+  __shared__ float rg[4][64], rb[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = blockIdx.x * 64 + lane;
+  const int k0 = blockIdx.y * chunk, k1 = min(k0 + chunk, nblk);
+  float sg = 0.f, sb = 0.f;
+  if (j < f) {
+    int k = k0 + wave;
+    for (; k + 12 < k1; k += 16) {  // four blocks in flight per wave
+      const float g0 = part_g[(size_t)k * f + j], g1 = part_g[(size_t)(k + 4) * f + j];
+      const float g2 = part_g[(size_t)(k + 8) * f + j], g3 = part_g[(size_t)(k + 12) * f + j];
+      const float b0 = part_b[(size_t)k * f + j], b1 = part_b[(size_t)(k + 4) * f + j];
+      const float b2 = part_b[(size_t)(k + 8) * f + j], b3 = part_b[(size_t)(k + 12) * f + j];
+      sg = (((sg + g0) + g1) + g2) + g3;
+      sb = (((sb + b0) + b1) + b2) + b3;
+    }
+    for (; k < k1; k += 4) {
+      sg += part_g[(size_t)k * f + j];
+      sb += part_b[(size_t)k * f + j];
+    }
+  }
+  rg[wave][lane] = sg;
+  rb[wave][lane] = sb;
+  __syncthreads();
+  if (wave == 0 && j < f) {
+    out_g[(size_t)blockIdx.y * f + j] = ((rg[0][lane] + rg[1][lane]) + rg[2][lane]) + rg[3][lane];
+    out_b[(size_t)blockIdx.y * f + j] = ((rb[0][lane] + rb[1][lane]) + rb[2][lane]) + rb[3][lane];
+  }
+}
+
+// Row-block count above which the dGamma / dBeta sums take two passes, and
+// the first pass's slice count.
+constexpr int kLnSlices = 64;
+inline int ln_slices(int nblk) { return nblk > 4 * kLnSlices ? kLnSlices : 0; }
+
 // CrossEntropyLossAndGradient (AccelerationCPU.cs:2377-2440): one workgroup per
 // row.  Rows below effective_len: p = exp(l - max) / sum, loss term
 // -log(p[target] + 1e-10), gradient (p / effective_len, minus 1 / effective_len
@@ -751,7 +796,8 @@ extern "C" int cdml_layernorm_backward_workspace_size(int rows, int features, si
   if (!bytes || rows < 0 || features < 0)
     return fail(CDML_E_INVALID, "cdml_layernorm_backward_workspace_size: bad argument");
   const size_t nblk = ((size_t)rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock;
-  *bytes = 2 * nblk * (size_t)features * sizeof(float);
+  const size_t slices = nblk > (size_t)4 * kLnSlices ? kLnSlices : 0;
+  *bytes = 2 * (nblk + slices) * (size_t)features * sizeof(float);
   return CDML_OK;
 }
 
@@ -809,8 +855,20 @@ extern "C" int cdml_layernorm_backward(const float *dout, const float *dout2,
     if (rc) return rc;
   }
   if (dgamma || dbeta) {
-    ln_param_grad_kernel<<<dim3((features + 63) / 64), dim3(1024), 0, st>>>(pg, pb, dgamma, dbeta, nblk,
-                                                                            features, accumulate);
+    const int slices = ln_slices(nblk);
+    if (slices) {  // many row blocks: sum slices of them on many CUs first
+      float *sg = pb + (size_t)nblk * features, *sb = sg + (size_t)slices * features;
+      const int chunk = (nblk + slices - 1) / slices;
+      ln_param_slice_kernel<<<dim3((features + 63) / 64, slices), dim3(256), 0, st>>>(pg, pb, sg, sb, nblk,
+                                                                                      chunk, features);
+      rc = check_launch("ln_param_slice_kernel");
+      if (rc) return rc;
+      ln_param_grad_kernel<<<dim3((features + 63) / 64), dim3(1024), 0, st>>>(sg, sb, dgamma, dbeta, slices,
+                                                                              features, accumulate);
+    } else {
+      ln_param_grad_kernel<<<dim3((features + 63) / 64), dim3(1024), 0, st>>>(pg, pb, dgamma, dbeta, nblk,
+                                                                              features, accumulate);
+    }
     rc = check_launch("ln_param_grad_kernel");
   }
   return rc;

@@ -423,8 +423,7 @@ void DeviceTrainer::bucket_backward(int batch, int seqLen) {
       check(cdml_sdpa_bwd(Y.q, D, Y.k, D, Y.v, D, dcat_, D, dq_, D, dk_, D, dv_, D, batch, seqLen, seqLen, D, H,
                           scale, 1, nullptr, ws_, ws_bytes_, s),
             "cdml_sdpa_bwd");
-    check(cdml_rope(dq_, rows, D, 0, hd, H, 10000.0f, 1, 0, seqLen, nullptr, s), "cdml_rope");
-    check(cdml_rope(dk_, rows, D, 0, hd, H, 10000.0f, 1, 0, seqLen, nullptr, s), "cdml_rope");
+    check(cdml_rope_qk_table(dq_, dk_, rows, D, hd, H, rope_cs_, cap_s_, 0, seqLen, 1, s), "cdml_rope_qk_table");
     check(cdml_backprop_qkv(Y.x, dq_, dk_, dv_, Y.wq, Y.wk, Y.wv, Y.gwq, Y.gbq, Y.gwk, Y.gbk, Y.gwv, Y.gbv, dxa_,
                             rows, D, D, ws_, ws_bytes_, s),
           "cdml_backprop_qkv");

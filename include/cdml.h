@@ -233,6 +233,19 @@ int cdml_rope(float *x, int rows, int ld, int start_col, int head_dim,
 int cdml_rope_table(float *cs, int n_pos, int head_dim, float base_theta,
                     cdml_stream stream);
 
+/* The trainer's ApplySegmentedRotaryInPlace(q, k, numHeads, segmentLength,
+ * inverse) (TransformerTrainer.cs:811-848, the inverse at :980): heads
+ * h = 0..num_heads-1 of width head_dim, from column 0 of q and of k (both
+ * [rows, ld], device, different arrays; k may be NULL), rotated in place from
+ * a cdml_rope_table of n_pos positions, with the same bits as cdml_rope at
+ * that table's base.  Row r has position pos_offset + (seg_len > 0 ?
+ * r % seg_len : r), which must be below n_pos; rows * num_heads * head_dim / 2
+ * below 2^31. */
+int cdml_rope_qk_table(float *q, float *k, int rows, int ld, int head_dim,
+                       int num_heads, const float *rope_cs, int n_pos,
+                       int pos_offset, int seg_len, int inverse,
+                       cdml_stream stream);
+
 /* cdml_project_qkv followed by the forward rotary embedding of Q and K, as
  * MultiHeadAttention.Forward calls ProjectQKV and then
  * applies the rotary embedding to Q and K (MultiHeadAttention.cs:108-110,

@@ -121,6 +121,17 @@ def backprop_qkv(x, dq, dk, dv, wq, wk, wv, wq_grad, bq_grad, wk_grad, bk_grad, 
     return (down(bdx, (rows, ind)), *(down(g, sh) for g, sh in zip(grads, shapes)))
 
 
+def rope_qk_table(q, k, head_dim, num_heads, n_pos, pos_offset=0, seg_len=0, inverse=True, base=10000.0):
+    """cdml_rope_qk_table on copies of q and k (k may be None) -> (q, k)."""
+    rows, ld = q.shape
+    cs = N.DeviceBuffer(max(8, n_pos * head_dim * 4))
+    N.check(N.lib().cdml_rope_table(cs.ptr, n_pos, head_dim, base, stream().handle))
+    bq, bk = up(q), (up(k) if k is not None else None)
+    N.check(N.lib().cdml_rope_qk_table(bq.ptr, bk.ptr if bk else None, rows, ld, head_dim, num_heads, cs.ptr, n_pos,
+                                       pos_offset, seg_len, int(inverse), stream().handle))
+    return down(bq, (rows, ld)), (down(bk, (rows, ld)) if bk else None)
+
+
 def rope(x, num_heads=None, start_col=0, head_dim=None, base=10000.0, inverse=False,
          pos_offset=0, seg_len=0, positions=None):
     rows, dim = x.shape

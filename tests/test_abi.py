@@ -57,6 +57,16 @@ def test_other_argument_checks():
     assert L.cdml_rope_table(None, 4, 5, 10000.0, None) == N.E_INVALID                     # odd head_dim
     assert L.cdml_rope_table(None, 4, 4, 0.0, None) == N.E_INVALID                         # bad base
     assert L.cdml_rope_table(None, 0, 4, 10000.0, None) == N.OK                            # empty
+    fake, fake2 = C.c_void_p(4096), C.c_void_p(8192)  # never dereferenced: every case fails a host check
+    assert L.cdml_rope_qk_table(fake, fake2, 4, 8, 3, 2, fake, 4, 0, 0, 1, None) == N.E_INVALID   # odd head dim
+    assert L.cdml_rope_qk_table(fake, fake2, 4, 8, 4, 3, fake, 4, 0, 0, 1, None) == N.E_INVALID   # heads past row
+    assert L.cdml_rope_qk_table(fake, fake2, 4, 8, 4, 2, fake, 3, 0, 0, 1, None) == N.E_INVALID   # table too short
+    assert L.cdml_rope_qk_table(fake, fake2, 8, 8, 4, 2, fake, 5, 2, 4, 1, None) == N.E_INVALID   # offset + segment
+    assert L.cdml_rope_qk_table(fake, fake, 4, 8, 4, 2, fake, 4, 0, 0, 1, None) == N.E_INVALID    # q is k
+    assert L.cdml_rope_qk_table(None, fake2, 4, 8, 4, 2, fake, 4, 0, 0, 1, None) == N.E_INVALID   # NULL q
+    assert L.cdml_rope_qk_table(fake, fake2, 4, 8, 4, 2, C.c_void_p(4100), 4, 0, 0, 1, None) == N.E_INVALID  # cs
+    assert L.cdml_rope_qk_table(fake, fake2, -1, 8, 4, 2, fake, 4, 0, 0, 1, None) == N.E_INVALID  # negative rows
+    assert L.cdml_rope_qk_table(None, None, 0, 8, 4, 2, None, 0, 0, 0, 1, None) == N.OK           # empty
     sz = C.c_size_t(0)
     assert L.cdml_decode_attn_workspace_size(64, 8192, 2048, 16, C.byref(sz)) == N.OK
     assert sz.value == 4 * 64 * 16 * 32 * 130

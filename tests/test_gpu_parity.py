@@ -134,6 +134,28 @@ def test_rope_segmented_and_absolute_positions():
     parity(G.rope(xr, 4, positions=pos), want, "RoPE absolute positions")
 
 
+@pytest.mark.parametrize("rows,ld,hd,heads,seg,off,inv", [
+    (300, 128, 32, 4, 100, 0, 1),    # the trainer's inverse over 100-row segments, two pairs per thread
+    (300, 132, 32, 4, 0, 7, 0),      # row longer than the heads, position offset, forward
+    (2044, 256, 32, 8, 511, 0, 1),   # eight 511-row windows of the config-5 model
+    (77, 36, 6, 6, 0, 0, 1),         # head dim 6: one pair per thread
+    (50, 66, 64, 1, 16, 3, 1),       # odd row pitch: one pair per thread
+])
+def test_rope_qk_table_equals_rope(rows, ld, hd, heads, seg, off, inv):
+    """ApplySegmentedRotaryInPlace (TransformerTrainer.cs:811-848) from the
+    table: the same bits as cdml_rope on each matrix, columns past the heads
+    untouched; the known answers of cdml_rope pin those bits."""
+    q, k = synth.normal(rows + ld, (rows, ld)), synth.normal(rows + ld + 1, (rows, ld))
+    n_pos = off + (min(seg, rows) if seg else rows)
+    gq, gk = G.rope_qk_table(q, k, hd, heads, n_pos, off, seg, inv)
+    for got, x, n in ((gq, q, "Q"), (gk, k, "K")):
+        want = G.rope(x, heads, head_dim=hd, inverse=bool(inv), pos_offset=off, seg_len=seg)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"{n} {rows}x{ld} hd {hd}"
+        assert np.array_equal(got[:, heads * hd:], x[:, heads * hd:])
+    only_q, none = G.rope_qk_table(q, None, hd, heads, n_pos, off, seg, inv)
+    assert none is None and np.array_equal(only_q, gq)
+
+
 def test_rope_table_values():
     cs = G.rope_table(4096, 64)
     # position 1, pair 0: theta = 1 (the known answer of the reference's RoPE tests)
@@ -179,6 +201,12 @@ def test_project_qkv_rope(rows, ind, out, hd, seg, off):
     parity(q, rotated(wq), f"QKV+RoPE {rows}x{ind}->{out} Q")
     parity(k, rotated(wk), f"QKV+RoPE {rows}x{ind}->{out} K")
     parity(v, wv, f"QKV+RoPE {rows}x{ind}->{out} V")
+    # the epilogue's rotation is the in-place kernel's, bit for bit
+    pq, pk, pv = G.project_qkv(x, *args)
+    for got, plain, n in ((q, pq, "Q"), (k, pk, "K")):
+        want = G.rope(plain, heads, head_dim=hd, pos_offset=off, seg_len=seg)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"{n}: epilogue RoPE != cdml_rope"
+    assert np.array_equal(v, pv)
 
 
 # ------------------------------------------------------- projection gradients
