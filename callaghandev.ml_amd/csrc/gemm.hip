@@ -181,6 +181,14 @@ __device__ __forceinline__ float stable_sigmoid(float x) {
   return z / (1.f + z);
 }
 
+// Activation and derivative codes of the derivative-from-output form
+// (cdml_linear_preact without z, CDML_ACT_FROM_OUTPUT): ReLU whose zero output
+// is -0 where z < 0 or z is NaN, and ReLU's derivative read from that sign.
+// Leaky ReLU needs neither: its output has the sign of z, so act'(y) equals
+// act'(z) with the same expression.
+constexpr int kActReluMarked = 6;
+constexpr int kDerivReluOut = 7;
+
 // Activation derivative at the pre-activation z, as FillActivationAndDerivative
 // (Neural Network/NeuralNetwork.cs:885-944) defines it, including its ReLU
 // derivative of 1 at z = 0 and leaky-ReLU slope 0.1 for z <= 0.
@@ -198,6 +206,8 @@ __device__ __forceinline__ float act_deriv(float z, int act) {
       return z >= 0.f ? 1.f : 0.f;
     case CDML_ACT_LEAKYRELU:
       return z <= 0.f ? 0.1f : 1.f;
+    case kDerivReluOut:  // z >= 0 exactly where the marked output is not -0
+      return __float_as_int(z) < 0 ? 0.f : 1.f;
     case CDML_ACT_SWISH: {
       const float s = stable_sigmoid(z);
       return s + z * s * (1.f - s);
@@ -215,6 +225,8 @@ __device__ __forceinline__ float activate(float x, int act) {
       return tanhf(x);
     case CDML_ACT_RELU:
       return x > 0.f ? x : 0.f;
+    case kActReluMarked:
+      return x > 0.f ? x : (x >= 0.f ? 0.f : -0.f);
     case CDML_ACT_LEAKYRELU:
       return x > 0.f ? x : 0.01f * x;
     case CDML_ACT_SWISH:
@@ -1174,6 +1186,12 @@ void launch_tile_act(const GemmArgs &g, dim3 grid, dim3 block, hipStream_t strea
     case CDML_ACT_TANH: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_TANH, false, false, EPI><<<grid, block, 0, stream>>>(g); break;
     case CDML_ACT_RELU: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_RELU, false, false, EPI><<<grid, block, 0, stream>>>(g); break;
     case CDML_ACT_LEAKYRELU: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_LEAKYRELU, false, false, EPI><<<grid, block, 0, stream>>>(g); break;
+    case kActReluMarked:
+      if constexpr (!EPI) {  // only launches without z use it
+        gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, kActReluMarked, false, false, false><<<grid, block, 0, stream>>>(g);
+        break;
+      }
+      [[fallthrough]];
     default: gemm_tile_kernel<TM, TN, BKK, WM, WN, MINB, CDML_ACT_SWISH, false, false, EPI><<<grid, block, 0, stream>>>(g); break;
   }
 }
@@ -1550,9 +1568,14 @@ extern "C" int cdml_linear_backward_act(const float *x, int ldx, const float *dy
                                         float *bgrad, int rows, int in_dim, int out_dim,
                                         void *workspace, size_t workspace_bytes,
                                         cdml_stream stream) {
-  if (activation < CDML_ACT_NONE || activation > CDML_ACT_SWISH)
+  const int base = activation & ~CDML_ACT_FROM_OUTPUT;
+  if (base < CDML_ACT_NONE || base > CDML_ACT_SWISH)
     return fail(CDML_E_INVALID, "cdml_linear_backward_act: unknown activation %d", activation);
-  return linear_backward_impl(x, ldx, dy, lddy, w, dz, activation, add, dx, lddx, wgrad, bgrad,
+  const bool from_out = (activation & CDML_ACT_FROM_OUTPUT) != 0;
+  if (from_out && base != CDML_ACT_RELU && base != CDML_ACT_LEAKYRELU)
+    return fail(CDML_E_INVALID, "cdml_linear_backward_act: CDML_ACT_FROM_OUTPUT needs ReLU or leaky ReLU");
+  const int dact = from_out && base == CDML_ACT_RELU ? kDerivReluOut : base;
+  return linear_backward_impl(x, ldx, dy, lddy, w, dz, dact, add, dx, lddx, wgrad, bgrad,
                               rows, in_dim, out_dim, 0, workspace, workspace_bytes, stream,
                               "cdml_linear_backward_act");
 }
@@ -1584,8 +1607,10 @@ extern "C" int cdml_linear_preact(const float *x, int ldx, const float *w, const
     return fail(CDML_E_INVALID, "cdml_linear_preact: negative size");
   if (activation < CDML_ACT_NONE || activation > CDML_ACT_SWISH)
     return fail(CDML_E_INVALID, "cdml_linear_preact: unknown activation %d", activation);
+  if (!z && activation != CDML_ACT_RELU && activation != CDML_ACT_LEAKYRELU)
+    return fail(CDML_E_INVALID, "cdml_linear_preact: z may be NULL only with ReLU or leaky ReLU");
   if (rows == 0 || out_dim == 0) return CDML_OK;
-  if (!x || !w || !y || !z) return fail(CDML_E_INVALID, "cdml_linear_preact: NULL pointer");
+  if (!x || !w || !y) return fail(CDML_E_INVALID, "cdml_linear_preact: NULL pointer");
   if (ldx < in_dim || ldy < out_dim)
     return fail(CDML_E_INVALID, "cdml_linear_preact: row stride smaller than the row");
   int rc = ensure_device();
@@ -1599,7 +1624,7 @@ extern "C" int cdml_linear_preact(const float *x, int ldx, const float *w, const
   g.K = in_dim;
   g.nprob = 1;
   g.p[0] = {x, w, b, y, nullptr};
-  g.act = activation;
+  g.act = !z && activation == CDML_ACT_RELU ? kActReluMarked : activation;
   g.pre = z;
   g.ldpre = ldy;
   return launch_gemm(g, false, false, as_hip(stream), "cdml_linear_preact");

@@ -26,6 +26,10 @@ void check(int rc, const char *what) {
 
 size_t round64(size_t n) { return (n + 63) / 64 * 64; }  // 256-byte aligned tensors
 
+// Hidden FFN activations whose output alone gives the derivative: the layer
+// keeps no pre-activation (cdml_linear_preact with z = NULL).
+bool from_output(int act) { return act == Relu || act == Leakyrelu; }
+
 }  // namespace
 
 float *DeviceTrainer::alloc(size_t floats) {
@@ -191,7 +195,9 @@ DeviceTrainer::DeviceTrainer(const LanguageModel &model, const TrainingConfig &c
         Y.ffact.push_back(f.activations[i]);
         width = f.weights[i].rows;
         if (i + 1 < f.weights.size()) {
-          Y.z.push_back(alloc(rows * width));
+          // ReLU and leaky ReLU layers keep only their output: it carries
+          // the derivative (CDML_ACT_FROM_OUTPUT)
+          Y.z.push_back(from_output(f.activations[i]) ? nullptr : alloc(rows * width));
           Y.h.push_back(alloc(rows * width));
           ffmax = std::max(ffmax, width);
         }
@@ -401,8 +407,10 @@ void DeviceTrainer::bucket_backward(int batch, int seqLen) {
     for (int i = nf - 1; i >= 0; --i) {
       const float *xin = i > 0 ? Y.h[i - 1] : Y.n1;
       float *dxo = i > 0 ? dh_[i & 1] : dn1_;
-      check(cdml_linear_backward_act(xin, Y.ffcols[i], delta, Y.ffrows[i], Y.ffw[i], i > 0 ? Y.z[i - 1] : nullptr,
-                                     i > 0 ? Y.ffact[i - 1] : CDML_ACT_NONE, i > 0 ? nullptr : dr2_, dxo,
+      const bool fo = i > 0 && !Y.z[i - 1];  // the layer below kept only its output
+      check(cdml_linear_backward_act(xin, Y.ffcols[i], delta, Y.ffrows[i], Y.ffw[i],
+                                     i > 0 ? (fo ? Y.h[i - 1] : Y.z[i - 1]) : nullptr,
+                                     i > 0 ? Y.ffact[i - 1] | (fo ? CDML_ACT_FROM_OUTPUT : 0) : CDML_ACT_NONE, i > 0 ? nullptr : dr2_, dxo,
                                      Y.ffcols[i], Y.gffw[i], Y.gffb[i], rows, Y.ffcols[i], Y.ffrows[i], ws_,
                                      ws_bytes_, s),
             "cdml_linear_backward_act");

@@ -48,6 +48,9 @@ extern "C" {
 #define CDML_ACT_RELU 3
 #define CDML_ACT_LEAKYRELU 4
 #define CDML_ACT_SWISH 5
+/* Or'ed into cdml_linear_backward_act's activation: dz holds the output y of
+ * a cdml_linear_preact call made without z (ReLU or leaky ReLU only). */
+#define CDML_ACT_FROM_OUTPUT 0x100
 
 typedef struct cdml_stream_opaque *cdml_stream; /* a hipStream_t */
 typedef struct cdml_event_opaque *cdml_event;   /* a hipEvent_t  */
@@ -369,7 +372,11 @@ int cdml_sdpa_bwd_saved(const float *q, int ldq, const float *k, int ldk,
 /* IAccelerationManager.FFNForwardBatch's layer with its cache, the forward
  * pass that NeuralNetwork.ComputeInputGradientBatch recomputes
  * (Neural Network/NeuralNetwork.cs:824-839): z = x w^T + b and y = act(z),
- * both [rows, out_dim] with row stride ldy. */
+ * both [rows, out_dim] with row stride ldy.  With ReLU or leaky ReLU, z may
+ * be NULL: y alone then carries the derivative (CDML_ACT_FROM_OUTPUT), ReLU
+ * writing its zero as -0 where z < 0 or z is NaN (the reference's
+ * derivative is 1 at z >= 0, 0 elsewhere); leaky ReLU's y has the sign of z.
+ * The values equal y = act(z) as numbers. */
 int cdml_linear_preact(const float *x, int ldx, const float *w, const float *b,
                        float *z, float *y, int ldy, int rows, int in_dim,
                        int out_dim, int activation, cdml_stream stream);
@@ -381,7 +388,9 @@ int cdml_linear_preact(const float *x, int ldx, const float *w, const float *b,
  * dz (the layer below's pre-activation, for its hidden deltas) and add (a
  * residual gradient, MatrixAddInPlace) may be NULL; both have row stride
  * lddx.  act' follows FillActivationAndDerivative (NeuralNetwork.cs:885-944).
- * workspace as cdml_linear_backward. */
+ * activation | CDML_ACT_FROM_OUTPUT: dz is instead the output y of a
+ * cdml_linear_preact call made without z, and act' comes from it with the
+ * same values.  workspace as cdml_linear_backward. */
 int cdml_linear_backward_act(const float *x, int ldx, const float *dy,
                              int lddy, const float *w, const float *dz,
                              int activation, const float *add, float *dx,

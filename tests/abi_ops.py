@@ -222,6 +222,17 @@ def linear_preact(x, w, b, act):
     return down(z, (rows, out)), down(y, (rows, out))
 
 
+def linear_preact_output_only(x, w, b, act):
+    """cdml_linear_preact with z = NULL (ReLU / leaky ReLU) -> y."""
+    rows, ind = x.shape
+    out = w.shape[0]
+    bx, bw, bb = up(x), up(w), up(b)
+    y = N.DeviceBuffer(max(4, rows * out * 4))
+    N.check(N.lib().cdml_linear_preact(bx.ptr, ind, bw.ptr, bb.ptr, None, y.ptr, out, rows, ind, out, act,
+                                       stream().handle))
+    return down(y, (rows, out))
+
+
 def linear_backward_act(x, dy, w, wgrad, bgrad, dz=None, act=0, add=None):
     """cdml_linear_backward_act -> (dx, wgrad, bgrad)."""
     rows, ind = x.shape

@@ -67,6 +67,12 @@ def test_other_argument_checks():
     assert L.cdml_rope_qk_table(fake, fake2, 4, 8, 4, 2, C.c_void_p(4100), 4, 0, 0, 1, None) == N.E_INVALID  # cs
     assert L.cdml_rope_qk_table(fake, fake2, -1, 8, 4, 2, fake, 4, 0, 0, 1, None) == N.E_INVALID  # negative rows
     assert L.cdml_rope_qk_table(None, None, 0, 8, 4, 2, None, 0, 0, 0, 1, None) == N.OK           # empty
+    # z = NULL only for ReLU / leaky ReLU; CDML_ACT_FROM_OUTPUT only with those
+    assert L.cdml_linear_preact(fake, 4, fake, None, None, fake2, 4, 4, 4, 4, 1, None) == N.E_INVALID
+    assert L.cdml_linear_preact(None, 4, None, None, None, None, 4, 0, 4, 4, 3, None) == N.OK
+    for act in (0x100 | 1, 0x100 | 5, 0x100 | 0, 0x200 | 3):
+        assert L.cdml_linear_backward_act(None, 4, None, 4, None, None, act, None, None, 4, None, None, 0, 4, 4,
+                                          None, 0, None) == N.E_INVALID, act
     sz = C.c_size_t(0)
     assert L.cdml_decode_attn_workspace_size(64, 8192, 2048, 16, C.byref(sz)) == N.OK
     assert sz.value == 4 * 64 * 16 * 32 * 130

@@ -37,6 +37,41 @@ def test_linear_preact(rows, ind, out, act):
     assert np.array_equal(y, O.activation(z, act)) if act == 3 else True  # ReLU of the stored z, exactly
 
 
+@pytest.mark.parametrize("rows,ind,out,act", [(600, 256, 512, 3), (16384, 64, 1024, 3), (77, 130, 33, 3),
+                                              (600, 256, 512, 4), (40, 32, 64, 4)])
+def test_ffn_backward_from_output(rows, ind, out, act):
+    """The hidden layer without its pre-activation (z = NULL, then
+    CDML_ACT_FROM_OUTPUT): y equals act(z) as numbers, ReLU's zero carries
+    the sign of z < 0, and every gradient has the bits of the z form --
+    including rows whose z is exactly 0, where the reference's ReLU
+    derivative is 1 (NeuralNetwork.cs:885-944)."""
+    x = synth.normal(4, (rows, ind))
+    x[::7] = 0.0                                  # z = b on these rows ...
+    b1 = synth.normal(6, (out,)) * np.float32(0.1)
+    b1[::3] = 0.0                                 # ... and exactly 0 in every third column
+    w1 = synth.xavier_uniform(5, out, ind)
+    w2 = synth.xavier_uniform(7, ind, out)
+    dout, resid = synth.normal(9, (rows, ind)), synth.normal(10, (rows, ind))
+    wg = [synth.normal(11, (out, ind)), synth.normal(12, (ind, out))]
+    bg = [synth.normal(13, (out,)), synth.normal(14, (ind,))]
+    z, h = G.linear_preact(x, w1, b1, act)
+    y = G.linear_preact_output_only(x, w1, b1, act)
+    assert (z == 0).any() and (z < 0).any()
+    assert np.array_equal(y, h)                   # as numbers (-0 == 0)
+    if act == 3:
+        assert np.array_equal(np.signbit(y), z < 0)
+    else:
+        assert np.array_equal(y.view(np.uint32), h.view(np.uint32))
+    want = G.linear_backward_act(h, dout, w2, wg[1], bg[1], dz=z, act=act)
+    got = G.linear_backward_act(y, dout, w2, wg[1], bg[1], dz=y, act=act | 0x100)
+    for a, e, n in zip(got, want, ("dh", "W2 grad", "b2 grad")):
+        assert np.array_equal(a.view(np.uint32), e.view(np.uint32)), n
+    d1 = G.linear_backward_act(x, got[0], w1, wg[0], bg[0], add=resid)
+    d0 = G.linear_backward_act(x, want[0], w1, wg[0], bg[0], add=resid)
+    for a, e in zip(d1, d0):
+        assert np.array_equal(a.view(np.uint32), e.view(np.uint32))
+
+
 @pytest.mark.parametrize("rows,ind,out,act", [(64, 64, 128, 3), (600, 256, 512, 3), (77, 130, 33, 1),
                                               (2048, 128, 512, 5), (40, 32, 64, 4)])
 def test_ffn_backward_layers(rows, ind, out, act):
