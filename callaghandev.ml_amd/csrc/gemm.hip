@@ -828,29 +828,32 @@ __global__ void __launch_bounds__(256) gemm_rows_kernel(const GemmArgs args) {
 }
 
 // A short reduction (K <= 16: the input projection of a time-series model,
-// F features -> D), non-transposed operands, N * K <= kSmallKW: W is staged
-// in LDS as [K][N], and each thread computes four consecutive outputs of one
-// row -- the row's K values are the same for the 64 lanes of a wave that
-// share it (broadcast loads), W's four columns come from LDS, and the four
-// results leave as one float4 when the row layout allows it.  Every output
-// sums its K products in k order.
-constexpr int kSmallKW = 8192;
-template <bool EPI>
+// F features -> D), non-transposed operands, N <= 1024: thread t owns the
+// four columns 4 (t % n4) .. + 3 (n4 = ceil(N / 4)) of rows t / n4,
+// t / n4 + 256 / n4, ..., and keeps their K x 4 weights and biases in
+// registers.  The threads of one row read the same K inputs (broadcast
+// loads) and the four results leave as one float4 when the row layout
+// allows it.  Every output sums its K products in k order.  TB: W is read as
+// [K, N] (the input gradient dX = dY W of a layer with few outputs).
+template <bool EPI, bool TB = false>
 __global__ void __launch_bounds__(256) gemm_smallk_kernel(const GemmArgs args) {
-  __shared__ float ws[kSmallKW];
-  const int prob = blockIdx.y;
-  const GemmProblem P = args.p[prob];
+  const GemmProblem P = args.p[blockIdx.y];
   const int M = args.M, N = args.N, K = args.K;
-  for (int i = threadIdx.x; i < N * K; i += 256) {
-    const int n = i / K, k = i % K;
-    ws[k * N + n] = P.w[(size_t)n * args.ldb + k];
-  }
-  __syncthreads();
   const int n4 = (N + 3) / 4;
-  const long long total = (long long)M * n4;
-  // grid-stride over the outputs, so W is staged once per workgroup
-  for (long long e = (long long)blockIdx.x * 256 + threadIdx.x; e < total; e += (long long)gridDim.x * 256) {
-    const int m = (int)(e / n4), n0 = (int)(e % n4) * 4;
+  const int rpp = 256 / n4;  // rows per pass of the workgroup (n4 <= 256)
+  const int r = threadIdx.x / n4, n0 = (threadIdx.x % n4) * 4;
+  if (r >= rpp) return;      // threads past the last whole row group
+  float w[16][4], bias[4];
+#pragma unroll
+  for (int k = 0; k < 16; ++k)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int n = min(n0 + c, N - 1);
+      w[k][c] = k < K ? P.w[TB ? (size_t)k * args.ldb + n : (size_t)n * args.ldb + k] : 0.f;
+    }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) bias[c] = P.bias && n0 + c < N ? P.bias[n0 + c] : 0.f;
+  for (int m = blockIdx.x * rpp + r; m < M; m += gridDim.x * rpp) {
     const float *__restrict__ x = P.a + (size_t)m * args.lda;
     float z[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -858,20 +861,56 @@ __global__ void __launch_bounds__(256) gemm_smallk_kernel(const GemmArgs args) {
       if (k < K) {
         const float xv = x[k];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) z[c] += xv * ws[k * N + min(n0 + c, N - 1)];
+        for (int c = 0; c < 4; ++c) z[c] += xv * w[k][c];
       }
     }
     float *crow = P.c + (size_t)m * args.ldc;
     if (!EPI && !args.beta && n0 + 3 < N && ((reinterpret_cast<uintptr_t>(crow + n0) & 15) == 0)) {
       vf4 y;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) y[c] = activate(z[c] + (P.bias ? P.bias[n0 + c] : 0.f), args.act);
+      for (int c = 0; c < 4; ++c) y[c] = activate(z[c] + bias[c], args.act);
       *reinterpret_cast<vf4 *>(crow + n0) = y;
       continue;
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-      if (n0 + c < N) store_elem<EPI>(args, P, m, n0 + c, z[c] + (P.bias ? P.bias[n0 + c] : 0.f), args.act);
+      if (n0 + c < N) store_elem<EPI>(args, P, m, n0 + c, z[c] + bias[c], args.act);
+  }
+}
+
+// Few output columns (N <= 4: a regression head, D -> 1), non-transposed
+// operands, K % 4 == 0 with 16-byte aligned rows: the 16 lanes of a group
+// take every 16th float4 of one row, their partial dot products meet through
+// four xor shuffles inside the group, and its first lane stores the N
+// outputs.  (The tiled kernel would run a 128 x 128 MFMA tile for one live
+// column.)
+constexpr int kNarrowN = 4;
+template <bool EPI>
+__global__ void __launch_bounds__(256) gemm_narrow_n_kernel(const GemmArgs args) {
+  const GemmProblem P = args.p[blockIdx.y];
+  const int M = args.M, N = args.N, K4 = args.K / 4;
+  const int g = threadIdx.x & 15;
+  for (int m = (blockIdx.x * 256 + threadIdx.x) >> 4; m < M; m += gridDim.x * 16) {
+    const float *__restrict__ x = P.a + (size_t)m * args.lda;
+    float z[kNarrowN] = {0.f, 0.f, 0.f, 0.f};
+    for (int i = g; i < K4; i += 16) {
+      const vf4 xv = *reinterpret_cast<const vf4 *>(x + 4 * i);
+#pragma unroll
+      for (int n = 0; n < kNarrowN; ++n)
+        if (n < N) {
+          const vf4 wv = *reinterpret_cast<const vf4 *>(P.w + (size_t)n * args.ldb + 4 * i);
+          z[n] += (xv[0] * wv[0] + xv[1] * wv[1]) + (xv[2] * wv[2] + xv[3] * wv[3]);
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < kNarrowN; ++n)
+#pragma unroll
+      for (int off = 8; off > 0; off >>= 1) z[n] += __shfl_xor(z[n], off, 16);
+    if (g == 0) {
+#pragma unroll
+      for (int n = 0; n < kNarrowN; ++n)
+        if (n < N) store_elem<EPI>(args, P, m, n, z[n] + (P.bias ? P.bias[n] : 0.f), args.act);
+    }
   }
 }
 
@@ -1279,6 +1318,13 @@ int launch_gemm(GemmArgs &g, bool ta, bool tb, hipStream_t stream, const char *w
     bool split_tail = tb && ktail != 0 && g.K >= 16 && !g.dz && !g.add && !g.pre && g.act == CDML_ACT_NONE;
     for (int i = 0; split_tail && i < g.nprob; ++i)
       split_tail = stage_ok(g.p[i].a, g.M, g.lda, ta, 16) && stage_ok(g.p[i].w, g.N, g.ldb, tb, 16);
+    if (!ta && tb && g.K <= 16 && g.K > 0 && g.M > 16 && g.N <= 1024) {  // few layer outputs
+      const int rpp = 256 / ((g.N + 3) / 4);
+      const dim3 grid((unsigned)std::min((g.M + rpp - 1) / rpp, 2048), (unsigned)g.nprob), block(256);
+      has_epi(g) ? gemm_smallk_kernel<true, true><<<grid, block, 0, stream>>>(g)
+                 : gemm_smallk_kernel<false, true><<<grid, block, 0, stream>>>(g);
+      return check_launch(what);
+    }
     if (ta && tb && g.small && g.ksplit > 1) {  // small output, long reduction
       if (g.N <= kNarrow)
         wgrad_narrow_kernel<true><<<dim3(g.ksplit, (g.M + 255) / 256, g.nprob), dim3(256), 0, stream>>>(g);
@@ -1315,12 +1361,17 @@ int launch_gemm(GemmArgs &g, bool ta, bool tb, hipStream_t stream, const char *w
   g.padded = pad_to_xcd(g.total);
   bool vec = (g.K % 4 == 0) && (g.lda % 4 == 0) && (g.ldb % 4 == 0);
   for (int i = 0; i < g.nprob; ++i) vec = vec && aligned16(g.p[i].a) && aligned16(g.p[i].w);
-  if (g.K <= 16 && g.K > 0 && g.M > 16 && !g.rope_cs && g.N * g.K <= kSmallKW &&
-      (long long)g.M * g.N <= (1LL << 38)) {
-    const long long n = (long long)g.M * ((g.N + 3) / 4);
-    const dim3 grid((unsigned)std::min<long long>((n + 255) / 256, 2048), (unsigned)g.nprob), block(256);
+  if (g.K <= 16 && g.K > 0 && g.M > 16 && !g.rope_cs && g.N <= 1024) {
+    const int rpp = 256 / ((g.N + 3) / 4);
+    const dim3 grid((unsigned)std::min((g.M + rpp - 1) / rpp, 2048), (unsigned)g.nprob), block(256);
     has_epi(g) ? gemm_smallk_kernel<true><<<grid, block, 0, stream>>>(g)
                : gemm_smallk_kernel<false><<<grid, block, 0, stream>>>(g);
+    return check_launch(what);
+  }
+  if (vec && g.N <= kNarrowN && g.K > 16 && g.M > 16 && !g.rope_cs) {
+    const dim3 grid((unsigned)std::min((g.M + 15) / 16, 4096), (unsigned)g.nprob), block(256);
+    has_epi(g) ? gemm_narrow_n_kernel<true><<<grid, block, 0, stream>>>(g)
+               : gemm_narrow_n_kernel<false><<<grid, block, 0, stream>>>(g);
     return check_launch(what);
   }
   if (vec && g.M <= 16 && g.K > 0 && (g.rope_cs == nullptr || g.rope_hd % 2 == 0)) {

@@ -65,7 +65,12 @@ def test_project_qkv_shapes(rows, ind, out):
                                           (1024, 64, 256),    # 128x128 tiles (256x128 would not fill a round)
                                           (300, 128, 256),    # 128x128 tiles, full and ragged wave blocks
                                           (16384, 64, 1024),  # 512 tiles of 256x128, every wave block full
-                                          (16484, 64, 1000)])  # 256x128 tiles, ragged last row and column tiles
+                                          (16484, 64, 1000),  # 256x128 tiles, ragged last row and column tiles
+                                          (20000, 256, 1),    # regression head: 16 lanes per row
+                                          (5003, 132, 3),     # few columns, ragged K / 64
+                                          (20000, 5, 256),    # input projection: 4 rows per pass
+                                          (3001, 3, 1000),    # short K, one row per pass
+                                          (500, 7, 2000)])    # short K, too wide for the register path
 def test_linear_with_activation(act, rows, ind, out):
     """BatchDotProductAddBias + activation on both tile configurations, a
     short reduction (the input projection of F 5 features, K 16) and few rows."""
@@ -77,7 +82,9 @@ def test_linear_with_activation(act, rows, ind, out):
 
 
 @pytest.mark.parametrize("rows,ind,out,act", [(1024, 128, 256, 3), (300, 64, 160, 5), (2048, 256, 384, 0),
-                                              (16384, 64, 1024, 3)])  # 256x128 tiles
+                                              (16384, 64, 1024, 3),   # 256x128 tiles
+                                              (5000, 64, 3, 1),       # few columns
+                                              (5000, 5, 256, 3)])     # short K
 def test_linear_row_strides(rows, ind, out, act):
     """cdml_linear with row strides above the widths (ldx = in + 8, ldy = out + 12):
     the full wave blocks of the unpredicated epilogue and the ragged ones give

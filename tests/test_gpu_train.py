@@ -26,7 +26,9 @@ def parity(a, e, what=""):
 @pytest.mark.parametrize("rows,ind,out,act", [(64, 64, 128, 3), (300, 256, 1024, 3), (77, 130, 33, 1),
                                               (1024, 512, 2048, 5), (40, 32, 64, 2),
                                               (16384, 64, 1024, 3),   # 256x128 tiles, full wave blocks
-                                              (16484, 64, 1000, 1)])  # 256x128 tiles, ragged row and column tiles
+                                              (16484, 64, 1000, 1),  # 256x128 tiles, ragged row and column tiles
+                                              (5000, 64, 3, 1),      # few columns: 16 lanes per row
+                                              (5000, 5, 256, 5)])    # short K
 def test_linear_preact(rows, ind, out, act):
     """The FFN hidden layer with its cache: z = x W^T + b, y = act(z)."""
     x, w, b = synth.normal(1, (rows, ind)), synth.xavier_uniform(2, out, ind), synth.normal(3, (out,))
@@ -73,7 +75,8 @@ def test_ffn_backward_from_output(rows, ind, out, act):
 
 
 @pytest.mark.parametrize("rows,ind,out,act", [(64, 64, 128, 3), (600, 256, 512, 3), (77, 130, 33, 1),
-                                              (2048, 128, 512, 5), (40, 32, 64, 4)])
+                                              (2048, 128, 512, 5), (40, 32, 64, 4),
+                                              (3000, 64, 3, 3)])  # 3-wide hidden layer: short-K input gradient
 def test_ffn_backward_layers(rows, ind, out, act):
     """NeuralNetwork.ComputeInputGradientBatch of a [ind, out, ind] FFN as two
     cdml_linear_backward_act calls (hidden deltas through act'(z), the input
