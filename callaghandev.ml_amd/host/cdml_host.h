@@ -466,6 +466,8 @@ class HipAccelerationManager {
   void act_done(std::initializer_list<Out> outs);
   std::vector<Xfer> act_transfers(std::initializer_list<Out> outs);
   void launch_settle_download(const std::function<void()> &launch, std::initializer_list<Out> outs);
+  void launch_split_download(const std::function<void(int, int)> &launch_rows, int rows, int h,
+                             std::initializer_list<Out> outs, const std::function<void()> &before_finish);
   ActEntry act_acquire(size_t bytes);  // dev == nullptr: no cache memory, take the scratch path
   void act_release(const ActEntry &e);
   void act_destroy(const ActEntry &e);

@@ -524,6 +524,52 @@ void HipAccelerationManager::launch_settle_download(const std::function<void()> 
   download_finish(xs);
 }
 
+// The same for a long result computed in two row ranges: launch_rows(0, h),
+// then launch_rows(h, rows - h), with the first range's rows of every output
+// moving on the copy stream (behind an event) while the kernel computes the
+// second, so most of the kernel time hides behind the DMA that bounds the
+// call.  before_finish runs after the compares, before the results reach the
+// host arrays.
+void HipAccelerationManager::launch_split_download(const std::function<void(int, int)> &launch_rows, int rows,
+                                                   int h, std::initializer_list<Out> outs,
+                                                   const std::function<void()> &before_finish) {
+  std::vector<Xfer> xs0, xs1;
+  auto plan = [&] {
+    const std::vector<Xfer> all = act_transfers(outs);
+    xs0.clear();
+    xs1.clear();
+    for (const Xfer &x : all) {
+      const size_t row = x.bytes / rows, off = (size_t)h * row;
+      xs0.push_back(Xfer{x.host, x.dev, off, x.pin});
+      xs1.push_back(Xfer{static_cast<char *>(x.host) + off, static_cast<char *>(x.dev) + off, x.bytes - off,
+                         static_cast<char *>(x.pin) + off});
+    }
+  };
+  plan();
+  size_t n0 = plan_chunks(sizes_of(xs0)).size();
+  cdml_stream cs = copy_stream();
+  auto run = [&] {
+    launch_rows(0, h);
+    check(cdml_event_record(kev_[0], stream_), "cdml_event_record");
+    check(cdml_stream_wait_event(cs, kev_[0]), "cdml_stream_wait_event");
+    download_enqueue(xs0, cs, 0);
+    launch_rows(h, rows - h);
+    check(cdml_event_record(kev_[1], stream_), "cdml_event_record");
+    check(cdml_stream_wait_event(cs, kev_[1]), "cdml_stream_wait_event");
+    download_enqueue(xs1, cs, n0);
+  };
+  run();
+  if (!settle()) {  // an input changed: the first downloads finish before the kernel runs again
+    check(cdml_stream_synchronize(cs), "cdml_stream_synchronize");
+    plan();  // an upload may have moved the staging buffer
+    n0 = plan_chunks(sizes_of(xs0)).size();
+    run();
+  }
+  if (before_finish) before_finish();
+  download_finish(xs0, 0);
+  download_finish(xs1, n0);
+}
+
 // ---- attention row statistics kept for the backward --------------------------
 namespace {
 constexpr size_t kLseRecords = 64;
@@ -732,39 +778,10 @@ std::tuple<Matrix, Matrix, Matrix> HipAccelerationManager::ProjectQKV(MatView in
   if (rows < 2048 || outBytes < (size_t(16) << 20)) {
     launch_settle_download([&] { launch_rows(0, rows); }, {out_of(Q, dq), out_of(K, dk), out_of(V, dv)});
   } else {
-    // Two row halves: the first half's rows of Q, K and V move on the copy
-    // stream while the kernel computes the second half, so most of the
-    // kernel time hides behind the DMA that bounds the call.
+    // Two row halves, the first half's rows downloaded while the kernel
+    // computes the second.
     const int h = (rows / 2 + 255) / 256 * 256;
-    const std::vector<Xfer> all = act_transfers({out_of(Q, dq), out_of(K, dk), out_of(V, dv)});
-    auto part = [&](int r0, int n) {
-      std::vector<Xfer> p;
-      const size_t off = (size_t)r0 * qDim * sizeof(float), b = (size_t)n * qDim * sizeof(float);
-      for (const Xfer &x : all)
-        p.push_back(Xfer{static_cast<char *>(x.host) + off, static_cast<char *>(x.dev) + off, b,
-                         static_cast<char *>(x.pin) + off});
-      return p;
-    };
-    const std::vector<Xfer> xs0 = part(0, h), xs1 = part(h, rows - h);
-    const size_t n0 = plan_chunks(sizes_of(xs0)).size();
-    cdml_stream cs = copy_stream();
-    auto run = [&] {
-      launch_rows(0, h);
-      check(cdml_event_record(kev_[0], stream_), "cdml_event_record");
-      check(cdml_stream_wait_event(cs, kev_[0]), "cdml_stream_wait_event");
-      download_enqueue(xs0, cs, 0);
-      launch_rows(h, rows - h);
-      check(cdml_event_record(kev_[1], stream_), "cdml_event_record");
-      check(cdml_stream_wait_event(cs, kev_[1]), "cdml_stream_wait_event");
-      download_enqueue(xs1, cs, n0);
-    };
-    run();
-    if (!settle()) {  // an input changed: the first downloads finish before the kernel runs again
-      check(cdml_stream_synchronize(cs), "cdml_stream_synchronize");
-      run();
-    }
-    download_finish(xs0, 0);
-    download_finish(xs1, n0);
+    launch_split_download(launch_rows, rows, h, {out_of(Q, dq), out_of(K, dk), out_of(V, dv)}, nullptr);
   }
   sync();
   return {std::move(Q), std::move(K), std::move(V)};
