@@ -324,6 +324,9 @@ def bench_mha_backward(N, st, steps, warmup, cfg=None):
     N.check(lib.cdml_sdpa_fwd_lse(b["q"].ptr, D, b["k"].ptr, D, b["v"].ptr, D, osv.ptr, D, lse.ptr,
                                   B, L, L, D, H, scale, 1, None, s))
 
+    rcs = N.DeviceBuffer(L * hd * 4)
+    N.check(lib.cdml_rope_table(rcs.ptr, L, hd, 10000.0, s))
+
     def core(saved):
         if saved:
             N.check(lib.cdml_sdpa_bwd_saved(b["q"].ptr, D, b["k"].ptr, D, b["v"].ptr, D, osv.ptr, D, lse.ptr,
@@ -341,8 +344,8 @@ def bench_mha_backward(N, st, steps, warmup, cfg=None):
         core(saved)
         if t_core:
             t_core.stop(st)
-        for t in (dq, dk):
-            N.check(lib.cdml_rope(t.ptr, rows, D, 0, hd, H, 10000.0, 1, 0, L, None, s))
+        # the inverse rotation of dQ and dK in one launch from the table, as the trainer does
+        N.check(lib.cdml_rope_qk_table(dq.ptr, dk.ptr, rows, D, hd, H, rcs.ptr, L, 0, L, 1, s))
         N.check(lib.cdml_backprop_qkv(b["x"].ptr, dq.ptr, dk.ptr, dv.ptr, dw[0].ptr, dw[1].ptr, dw[2].ptr,
                                       gw[0].ptr, gb[0].ptr, gw[1].ptr, gb[1].ptr, gw[2].ptr, gb[2].ptr,
                                       dxin.ptr, rows, D, D, dwsg.ptr, wsq.value, s))
