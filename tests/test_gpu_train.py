@@ -424,6 +424,39 @@ C5S = {"dim": 64, "heads": 2, "layers": 2, "ff": 128, "max_seq": 64, "discrete":
        "output_dim": 3}
 
 
+def test_device_trainer_continuous_c5_width_matches_oracle():
+    """One TrainBatchContinuous step at the config-5 layer width (F 5 -> D 256,
+    8 heads of 32, FF 1024 ReLU, a 1-wide regression head) on four 300-step
+    windows, 1196 rows: the Q/K/V input gradient as one K-segmented product,
+    the ReLU layer cached by its output alone, the short-K input projection and
+    its gradient, the 16-lanes-per-row head and its K = 1 input gradient all
+    run at their real widths; loss, norm, gradients and weights against the
+    oracle."""
+    cfg = {"dim": 256, "heads": 8, "layers": 2, "ff": 1024, "max_seq": 512, "discrete": False,
+           "input_dim": 5, "output_dim": 1, "data_type": 1}
+    w = synth.continuous_lm_weights(cfg, 16)
+    rng = np.random.default_rng(22)
+    wins = [rng.uniform(0, 1, (300, 5)).astype(np.float32) for _ in range(4)]
+    tg = [rng.standard_normal((300, 1)).astype(np.float32) for _ in range(4)]
+    t, _ = _trainer(cfg, w, 4, 300)
+    loss = t.TrainBatchContinuous(wins, regressionTargets=tg, learningRate=0.01)
+    want_loss, want_g, want_w = O.train_batch_continuous(cfg, w, wins, 0.01, reg_targets=tg)
+    assert abs(loss - want_loss) <= 1e-5 + 1e-5 * abs(want_loss)
+    assert t.last_norm == pytest.approx(want_g["norm"], rel=1e-4)
+
+    def named(d):
+        out = {k: d[k] for k in ("input_proj", "input_bias", "out_proj", "out_bias")}
+        for i, L in enumerate(d["layers"]):
+            for k, v in L.items():
+                out[f"layers.{i}.{k}"] = v
+        return out
+
+    for got, want, what in ((t.gradients(), want_g, "gradient"), (t.weights(), want_w, "weight")):
+        ww = named(want)
+        for k, v in got.items():
+            parity(v, np.asarray(ww[k]).reshape(-1), f"c5-width {what} {k}")
+
+
 @pytest.mark.parametrize("kind", ["regression", "classification"])
 def test_device_trainer_continuous_matches_oracle(kind):
     """TrainBatchContinuous of a time-series model (input projection F 5 ->
