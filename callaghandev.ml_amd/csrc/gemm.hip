@@ -49,6 +49,11 @@ struct GemmArgs {
   int total, padded;
   int act;
   int beta;  // 1: add the result to C
+  // Split-K weight gradient with a ragged K: the tiled chunks cover rows
+  // [0, ktail0) and splitk_reduce_kernel adds rows [ktail0, K) of opA^T opB
+  // (and of opA's row sums) itself; 0 when K % 16 == 0.  (It fills the
+  // padding before rope_cs.)
+  int ktail0;
   // Rotary position embedding applied to problems 0 and 1 (Q and K) in the
   // epilogue when rope_cs is set: rope_cs[pos * rope_hd / 2 + p] holds
   // (cos, sin) of position pos for pair p; row m has position
@@ -1003,6 +1008,13 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs args)
       s[2] += x[2];
       s[3] += x[3];
     }
+    // the ragged last rows: opA stored [K, M], opB [K, N] (16-byte rows)
+    for (int k = args.ktail0 + g; args.ktail0 > 0 && k < args.K; k += kReduceLanes) {
+      const float av = P.a[(size_t)k * args.lda + m];
+      const vf4 bv = *reinterpret_cast<const vf4 *>(P.w + (size_t)k * args.ldb + n);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) s[q] += av * bv[q];
+    }
 #pragma unroll
     for (int off = kReduceLanes / 2; off > 0; off >>= 1)
 #pragma unroll
@@ -1018,6 +1030,8 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs args)
     float s = 0.f;
     for (int c = g; c < args.ksplit; c += kReduceLanes)
       s += args.wsb[((size_t)c * args.nprob + prob) * M + e];
+    for (int k = args.ktail0 + g; args.ktail0 > 0 && k < args.K; k += kReduceLanes)
+      s += P.a[(size_t)k * args.lda + e];
 #pragma unroll
     for (int off = kReduceLanes / 2; off > 0; off >>= 1) s += __shfl_xor(s, off);
     if (g == 0) P.bgrad[e] += s;
@@ -1336,7 +1350,12 @@ int launch_gemm(GemmArgs &g, bool ta, bool tb, hipStream_t stream, const char *w
       wgrad_small_reduce_kernel<<<dim3((n + 255) / 256, g.nprob), dim3(256), 0, stream>>>(g);
       return check_launch(what);
     }
-    if (ta && tb) rc = launch_layout<true, true>(g, fast || split_tail, stream);
+    if (ta && tb && split_tail && g.ksplit > 1 && !g.small && g.N % 4 == 0) {
+      // split-K: the reduce adds the last K % 16 rows, no tail launch
+      g.ktail0 = g.K - ktail;
+      split_tail = false;
+      rc = launch_layout<true, true>(g, true, stream);
+    } else if (ta && tb) rc = launch_layout<true, true>(g, fast || split_tail, stream);
     else if (tb) rc = launch_layout<false, true>(g, fast || split_tail, stream);
     else rc = launch_layout<true, false>(g, false, stream);
     if (rc) return rc;
