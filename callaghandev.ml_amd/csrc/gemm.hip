@@ -1040,7 +1040,8 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs args)
 
 // Split-K plan of a weight-gradient GEMM (M = out, N = in, K = rows): enough
 // chunks to give every CU two resident workgroups when the output alone has
-// too few tiles, at least eight k-tiles (128 rows) per chunk.
+// too few tiles, at least eight k-tiles (128 rows) per chunk (two for small
+// outputs).
 struct SplitPlan {
   int ksplit = 1, kchunk = 0;
   bool small = false;  // small output: wgrad_small_kernel, kchunk in rows
@@ -1199,7 +1200,7 @@ inline bool big_tiles(int M, bool wgrad) { return M >= 1024 || (wgrad && M % 256
 
 SplitPlan splitk_plan(int M, int N, int K, int nprob) {
   SplitPlan sp;
-  const int nk = K / 16;  // whole k-tiles; a ragged tail is added by a separate launch
+  const int nk = K / 16;  // whole k-tiles; the reduce or a tail launch adds a ragged tail
   sp.kchunk = nk;
   if (M <= 0 || N <= 0) return sp;
   if (nk < 1 || N % 4 || M % 4) {  // not the tiled kernel's shape
@@ -1207,17 +1208,24 @@ SplitPlan splitk_plan(int M, int N, int K, int nprob) {
     sp.small = true;
     // chunks of 64 rows (at most 4096 chunks): each workgroup's row loop is
     // short, so the launch is not bound by one loop's load latency
-    sp.ksplit = std::min(4096, (K + 63) / 64);
+    const int bound = std::min(4096, (K + 63) / 64);
+    sp.ksplit = bound;
     sp.kchunk = (K + sp.ksplit - 1) / sp.ksplit;
     sp.ksplit = (K + sp.kchunk - 1) / sp.kchunk;
-    sp.bytes = (size_t)sp.ksplit * nprob * ((size_t)M * N + M) * sizeof(float);
+    // sized for the bound, which never decreases with K: a workspace sized
+    // for a caller's largest row count covers every smaller one
+    sp.bytes = (size_t)bound * nprob * ((size_t)M * N + M) * sizeof(float);
     return sp;
   }
   const bool big = big_tiles(M, true);
   const int TM = big ? 256 : 128, TN = 128;
   const int tiles = ((M + TM - 1) / TM) * ((N + TN - 1) / TN) * nprob;
   const int slots = big ? 512 : 1024;
-  const int s = std::min(slots / tiles, nk / 8);
+  // at least eight k-tiles per chunk, or two for a small output (at most
+  // 64 K elements, so a chunk's partial is at most 256 KB): a short
+  // reduction into a few tiles is otherwise one workgroup's serial k-loop
+  const int min_kt = (long long)M * N * nprob <= 65536 ? 2 : 8;
+  const int s = std::min(slots / tiles, nk / min_kt);
   if (s <= 1) return sp;
   sp.kchunk = (nk + s - 1) / s;
   sp.ksplit = (nk + sp.kchunk - 1) / sp.kchunk;
@@ -1226,7 +1234,11 @@ SplitPlan splitk_plan(int M, int N, int K, int nprob) {
     sp.kchunk = nk;
     return sp;
   }
-  sp.bytes = (size_t)sp.ksplit * nprob * ((size_t)M * N + M) * sizeof(float);
+  // sized for s (at least ksplit, and never decreasing with K, unlike
+  // ksplit itself: 75 k-tiles in 3-tile chunks take 25, 74 in 2-tile chunks
+  // 37), so a workspace sized for a caller's largest row count covers every
+  // smaller one
+  sp.bytes = (size_t)s * nprob * ((size_t)M * N + M) * sizeof(float);
   return sp;
 }
 

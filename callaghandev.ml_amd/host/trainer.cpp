@@ -250,6 +250,9 @@ DeviceTrainer::DeviceTrainer(const LanguageModel &model, const TrainingConfig &c
     need = std::max(need, n);
     check(cdml_backprop_qkv_workspace_size(R, D, D, &n), "workspace size");
     need = std::max(need, n);
+    // the attention output projection (its split need not match Q/K/V's)
+    check(cdml_linear_backward_workspace_size(R, D, D, &n), "workspace size");
+    need = std::max(need, n);
     check(cdml_linear_backward_workspace_size(R, D, V, &n), "workspace size");
     need = std::max(need, n);
     if (!discrete) {

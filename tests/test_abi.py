@@ -215,3 +215,19 @@ def test_mha_layer_fwd_argument_checks():
     assert lib.cdml_mha_layer_fwd(fake, *w[:8], fake, 1 << 16, 1 << 16, 64, 4, 10000.0, 1, None, None, fake,
                                   1 << 30, None) == N.E_INVALID
     assert b"exceeds" in lib.cdml_last_error()
+
+
+def test_weight_gradient_workspace_never_shrinks_with_rows():
+    """A caller sizes the weight-gradient workspace once for its largest row
+    count (the trainers do, per capacity): the size asked for must never
+    decrease as rows grow, though the split-K chunk count itself can."""
+    L = N.lib()
+    n = C.c_size_t(0)
+    for ind, out in ((64, 64), (64, 200), (256, 256), (1024, 1024), (256, 5), (5, 256), (4096, 1024)):
+        for fn in ("cdml_linear_backward_workspace_size", "cdml_backprop_qkv_workspace_size"):
+            prev = 0
+            for rows in list(range(1, 3000)) + [4095 * 4, 4096 * 4, 511 * 256]:
+                assert getattr(L, fn)(rows, ind, out, C.byref(n)) == N.OK
+                assert n.value >= prev, f"{fn}({rows}, {ind}, {out}) = {n.value} < {prev}"
+                prev = n.value
+
