@@ -180,6 +180,99 @@ __device__ __forceinline__ void store_rope(const GemmArgs &args, const GemmProbl
   }
 }
 
+// The same epilogue with the (cos, sin) table staged through LDS, for full
+// row tiles inside one position segment and head dims 2^(LP+1) (8 .. 64).
+// The k-loop ends on a barrier, so the operand tiles in `tab` (As) are free.
+// Phase i covers block i of every wave row: the workgroup copies the table
+// rows of those WM x 32 output rows into tab[pair * RS + row] with coalesced
+// loads (a thread keeps one pair for all its fetches, so every fetch and LDS
+// write is its base plus a constant), and each lane then reads its (cos, sin)
+// from LDS, which never waits on the stores (a global load issued after a
+// store waits for it: one round trip per group of rows in store_rope).
+// Same arithmetic, same bits as store_rope.
+template <int TM, int WM, int NT, int BI, int BJ, int LP>
+__device__ __forceinline__ void store_rope_lds(const GemmArgs &args, const GemmProblem &P,
+                                               const floatx16 (&acc)[BI][BJ], int mseg, int wm, int mw, int nw,
+                                               int li, int hf, float2 *tab) {
+#pragma clang fp contract(off)
+  constexpr int PAIRS = 1 << LP;
+  constexpr int ROWS = WM * 32;             // table rows per phase
+  constexpr int RS = ROWS + 2;              // pitch of one pair's column (float2)
+  constexpr int STEP = NT / PAIRS;          // rows between a thread's fetches
+  constexpr int KN = ROWS * PAIRS / NT;     // fetches per thread and phase
+  constexpr int WR = TM / WM;               // tile rows per wave row
+  static_assert(KN >= 1 && KN * NT == ROWS * PAIRS && (STEP % 32 == 0 || 32 % STEP == 0), "fetch shape");
+  const int t = threadIdx.x;
+  const int p = t & (PAIRS - 1), q0 = t >> LP;
+  // table row q of a phase is tile row (q / 32) * WR + q % 32 (+ 32 i); for
+  // q = q0 + k * STEP that is the lane's base row plus a constant
+  const int ro0 = STEP <= 32 ? q0 : (q0 >> 5) * WR + (q0 & 31);
+  const float2 *__restrict__ src = args.rope_cs + (size_t)(args.rope_pos0 + mseg + ro0) * PAIRS + p;
+  float2 *wr = tab + p * RS + q0;
+  float2 pre[KN];
+  int n[BJ], pcol[BJ];
+  float bias[BJ];
+  const bool odd = li & 1;  // column parity (nw is a multiple of 32)
+#pragma unroll
+  for (int j = 0; j < BJ; ++j) {
+    n[j] = nw + j * 32 + li;
+    pcol[j] = ((n[j] & (2 * PAIRS - 1)) >> 1) * RS;
+    bias[j] = (P.bias && n[j] < args.N) ? P.bias[n[j]] : 0.f;
+  }
+  const bool full_n = nw + 32 * BJ <= args.N;
+  const float2 *tl = tab + wm * 32 + 4 * hf;  // row 8 (r / 4) + r % 4 of this lane's half
+#pragma unroll
+  for (int i = 0; i < BI; ++i) {
+#pragma unroll
+    for (int k = 0; k < KN; ++k) {
+      const int qk = k * STEP;  // constant
+      const int c = (qk >> 5) * WR + (STEP <= 32 ? (qk & 31) : 0) + 32 * i;
+      pre[k] = src[(size_t)c * PAIRS];
+    }
+    if (i > 0) __syncthreads();  // phase i - 1's reads are done
+#pragma unroll
+    for (int k = 0; k < KN; ++k) wr[k * STEP] = pre[k];
+    __syncthreads();
+    const int mb = mw + i * 32;  // wave-uniform
+    if (full_n) {
+      float *__restrict__ cb = P.c + (size_t)(mb + 4 * hf) * args.ldc;
+      // groups of four rows: the scheduling barrier keeps later groups' LDS
+      // reads from being hoisted (their registers would cost the second
+      // workgroup per CU)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int dr = 8 * g + rr;
+          float *c = cb + (size_t)dr * args.ldc;
+#pragma unroll
+          for (int j = 0; j < BJ; ++j) {
+            const float2 cs = tl[pcol[j] + dr];
+            const float y = acc[i][j][4 * g + rr] + bias[j];
+            const float yp = swap_pair(y);
+            c[n[j]] = odd ? yp * cs.y + y * cs.x : y * cs.x - yp * cs.y;
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int dr = 8 * (r >> 2) + (r & 3);
+        const int m = mb + 4 * hf + dr;
+#pragma unroll
+        for (int j = 0; j < BJ; ++j) {
+          const float2 cs = tl[pcol[j] + dr];
+          const float y = acc[i][j][r] + bias[j];
+          const float yp = swap_pair(y);  // in every lane; only the store is predicated
+          const float out = odd ? yp * cs.y + y * cs.x : y * cs.x - yp * cs.y;
+          if (n[j] < args.N) P.c[(size_t)m * args.ldc + n[j]] = out;
+        }
+      }
+    }
+  }
+}
+
 __device__ __forceinline__ float stable_sigmoid(float x) {
   if (x >= 0.f) return 1.f / (1.f + expf(-x));
   const float z = expf(x);
@@ -515,7 +608,11 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const Gem
   const int gsize = min(args.tiles_m - first_m, GROUP_M);
   const int tm = first_m + (lid % in_group) % gsize;
   const int tn_all = (lid % in_group) / gsize;
-  const int prob = tn_all / args.tiles_n;
+  // The RoPE instance keeps the problem index in a scalar register (the
+  // divisions above run on the vector unit; left there, the values it keeps
+  // for the staged-table epilogue cost its k-loop the VGPRs of the second
+  // workgroup per CU).  Other instances allocate better without the hint.
+  const int prob = ACT == kActRope ? __builtin_amdgcn_readfirstlane(tn_all / args.tiles_n) : tn_all / args.tiles_n;
   const int tn = tn_all % args.tiles_n;
 
   const GemmProblem P = args.p[prob];
@@ -672,7 +769,25 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile_kernel(const Gem
 
   if constexpr (ACT == kActRope) {
     if (prob < 2) {
-      store_rope<BI, BJ>(args, P, acc, m0 + wm * (TM / WM), n0 + wn * (TN / WN), li, hf);
+      // uniform: the whole workgroup takes one form
+      const int pairs = args.rope_hd >> 1, seg = args.rope_seg;
+      const int mseg = seg > 0 ? m0 % seg : m0;
+      static_assert(sizeof(As) >= sizeof(float2) * 32 * (WM * 32 + 2), "RoPE table in LDS");
+      // (the 128 x 128 configuration keeps store_rope: with the LDS form its
+      // k-loop needs more than the 128 VGPRs of four waves per SIMD)
+      const bool lds = TM == 256 && m0 + TM <= M && (seg <= 0 || mseg + TM <= seg);
+      float2 *tab = reinterpret_cast<float2 *>(&As[0][0][0]);
+      const int mw = m0 + wm * (TM / WM), nw = n0 + wn * (TN / WN);
+      if (lds && pairs == 32)
+        store_rope_lds<TM, WM, NT, BI, BJ, 5>(args, P, acc, mseg, wm, mw, nw, li, hf, tab);
+      else if (lds && pairs == 16)
+        store_rope_lds<TM, WM, NT, BI, BJ, 4>(args, P, acc, mseg, wm, mw, nw, li, hf, tab);
+      else if (lds && pairs == 8)
+        store_rope_lds<TM, WM, NT, BI, BJ, 3>(args, P, acc, mseg, wm, mw, nw, li, hf, tab);
+      else if (lds && pairs == 4)
+        store_rope_lds<TM, WM, NT, BI, BJ, 2>(args, P, acc, mseg, wm, mw, nw, li, hf, tab);
+      else
+        store_rope<BI, BJ>(args, P, acc, m0 + wm * (TM / WM), n0 + wn * (TN / WN), li, hf);
       return;
     }
   }

@@ -180,6 +180,9 @@ def test_rope_table_values():
     (1024, 512, 512, 64, 0, 0),    # 128x128 tiles (256x128 would not fill a round)
     (16384, 64, 384, 64, 1024, 0),  # 576 tiles of 256x128 over 1024-row sequences, full wave blocks
     (16484, 64, 384, 32, 0, 3),    # 256x128 tiles, ragged last row tile, position offset
+    (16384, 64, 384, 16, 512, 0),  # 256x128 tiles, head dim 16, table staged in LDS
+    (16384, 32, 384, 8, 0, 7),     # 256x128 tiles, head dim 8, position offset
+    (16384, 64, 384, 64, 640, 0),  # 256x128 tiles inside one segment (LDS table) and across two (per row)
     (300, 1024, 1024, 64, 0, 0),   # 128x128 tiles, ragged rows
     (150, 64, 64, 16, 50, 0),      # segmented positions (row % 50)
     (1024, 256, 256, 32, 256, 0),  # segments of whole 32-row blocks, full tiles (unpredicated epilogue)
