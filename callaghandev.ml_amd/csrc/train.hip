@@ -125,13 +125,22 @@ __global__ void __launch_bounds__(256) ln_forward_kernel(const float *__restrict
 // LayerNormBackward (AccelerationCPU.cs:1516-1564), dX part: one row per
 // wave.  g = dout (+ dout2: the two gradients of a residual branch, summed
 // first as MatrixAddInPlace does); normalized is recomputed from the
-// residual input when not given.  Each workgroup owns kLnRowsPerBlock rows
+// residual input when not given.  Each workgroup owns ln_block_rows(RC) rows
 // and writes its partial column sums of g * normalized and g to the
 // workspace for ln_param_grad_kernel.
 constexpr int kLnRowsPerBlock = 64;  // rows per workgroup (16 waves x 4, or 4 waves x 16 for the longest rows)
 constexpr int ln_waves(int rc) { return rc >= 32 ? 4 : 16; }
+// Rows per workgroup by row cache: rows of 129 .. 256 features take 32 (16
+// waves x 2 rows: c5's 131072 x 256 backward 124 -> 108 us), longer rows 64
+// (at 1024 features 32 rows measured 52 -> 62 us).  The workspace size
+// follows it, so the choice depends on the feature count only.
+constexpr int ln_block_rows(int rc) { return rc == 4 ? 32 : kLnRowsPerBlock; }
+inline int ln_blocks(int rows, int features) {
+  const int r = ln_block_rows(row_cache(features));
+  return (rows + r - 1) / r;
+}
 
-template <int RC, int WAVES = ln_waves(RC)>
+template <int RC, int WAVES = ln_waves(RC), int ROWS = ln_block_rows(RC)>
 __global__ void __launch_bounds__(64 * WAVES) ln_backward_kernel(
     const float *__restrict__ dout, const float *__restrict__ dout2,
     const float *__restrict__ normalized, const float *__restrict__ gamma,
@@ -139,16 +148,16 @@ __global__ void __launch_bounds__(64 * WAVES) ln_backward_kernel(
     float *__restrict__ dx, float *__restrict__ part_g, float *__restrict__ part_b, int rows,
     int f, float eps) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int row0 = blockIdx.x * kLnRowsPerBlock;
+  const int row0 = blockIdx.x * ROWS;
   float pg[RC], pb[RC];
 #pragma unroll
   for (int i = 0; i < RC; ++i) pg[i] = pb[i] = 0.f;
   // Short rows (RC <= 4): the wave's U rows are handled together so that
   // their loads and reductions overlap; rows past the end are clamped for
   // the loads and contribute nothing.
-  constexpr int U = RC <= 4 ? kLnRowsPerBlock / WAVES : 1;
+  constexpr int U = RC <= 4 ? ROWS / WAVES : 1;
   const float inv_n = 1.0f / (float)f;
-  for (int rr0 = wave; rr0 < kLnRowsPerBlock; rr0 += WAVES * U) {
+  for (int rr0 = wave; rr0 < ROWS; rr0 += WAVES * U) {
     float gv[U][RC], xm[U][RC], dvar[U], dmean[U], istd[U];
     size_t base[U];
     bool live[U];
@@ -230,7 +239,7 @@ __global__ void __launch_bounds__(64 * WAVES) ln_backward_kernel(
 // so every load and store moves a float4.  The column partials of the
 // waves meet in LDS 256 columns at a time and two waves add them, in wave
 // order, for the workspace.
-template <int R4, int WAVES>
+template <int R4, int WAVES, int ROWS>
 __global__ void __launch_bounds__(64 * WAVES) ln_backward_vec_kernel(
     const float *__restrict__ dout, const float *__restrict__ dout2,
     const float *__restrict__ normalized, const float *__restrict__ gamma,
@@ -238,8 +247,8 @@ __global__ void __launch_bounds__(64 * WAVES) ln_backward_vec_kernel(
     float *__restrict__ dx, float *__restrict__ part_g, float *__restrict__ part_b, int rows,
     int f, float eps) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int row0 = blockIdx.x * kLnRowsPerBlock;
-  constexpr int U = R4 == 1 ? kLnRowsPerBlock / WAVES : 1;
+  const int row0 = blockIdx.x * ROWS;
+  constexpr int U = R4 == 1 ? ROWS / WAVES : 1;
   const float inv_n = 1.0f / (float)f;
   vf4 pg[R4], pb[R4], gm[R4];
   bool colok[R4];
@@ -250,7 +259,7 @@ __global__ void __launch_bounds__(64 * WAVES) ln_backward_vec_kernel(
     gm[i] = colok[i] ? *reinterpret_cast<const vf4 *>(gamma + col) : vf4{0.f, 0.f, 0.f, 0.f};
     pg[i] = pb[i] = vf4{0.f, 0.f, 0.f, 0.f};
   }
-  for (int rr0 = wave; rr0 < kLnRowsPerBlock; rr0 += WAVES * U) {
+  for (int rr0 = wave; rr0 < ROWS; rr0 += WAVES * U) {
     vf4 gv[U][R4], xm[U][R4];
     float dvar[U], dmean[U], istd[U];
     size_t base[U];
@@ -795,7 +804,7 @@ extern "C" int cdml_residual_layernorm_fwd(const float *a, const float *b, const
 extern "C" int cdml_layernorm_backward_workspace_size(int rows, int features, size_t *bytes) {
   if (!bytes || rows < 0 || features < 0)
     return fail(CDML_E_INVALID, "cdml_layernorm_backward_workspace_size: bad argument");
-  const size_t nblk = ((size_t)rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock;
+  const size_t nblk = features > 0 ? (size_t)ln_blocks(rows, features) : 0;
   const size_t slices = nblk > (size_t)4 * kLnSlices ? kLnSlices : 0;
   *bytes = 2 * (nblk + slices) * (size_t)features * sizeof(float);
   return CDML_OK;
@@ -823,14 +832,14 @@ extern "C" int cdml_layernorm_backward(const float *dout, const float *dout2,
   int rc = ensure_device();
   if (rc) return rc;
   hipStream_t st = as_hip(stream);
-  const int nblk = (rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock;
+  const int nblk = ln_blocks(rows, features);
   float *pg = static_cast<float *>(workspace), *pb = pg + (size_t)nblk * features;
   const int rcache = row_cache(features);
   const bool vec = rcache >= 4 && features % 4 == 0 && aligned16(dout) && (!dout2 || aligned16(dout2)) &&
                    (!normalized || aligned16(normalized)) && aligned16(gamma) && aligned16(input) &&
                    aligned16(dinput) && aligned16(pg);
   if (rows > 0 && vec) {
-#define CDML_LN_BWDV(RC) ln_backward_vec_kernel<RC / 4, ln_waves(RC)><<<dim3(nblk), dim3(64 * ln_waves(RC)), 0, st>>>(dout, dout2, normalized, gamma, input, mean, variance, dinput, pg, pb, rows, features, eps)
+#define CDML_LN_BWDV(RC) ln_backward_vec_kernel<RC / 4, ln_waves(RC), ln_block_rows(RC)><<<dim3(nblk), dim3(64 * ln_waves(RC)), 0, st>>>(dout, dout2, normalized, gamma, input, mean, variance, dinput, pg, pb, rows, features, eps)
     switch (rcache) {
       case 4: CDML_LN_BWDV(4); break;
       case 8: CDML_LN_BWDV(8); break;

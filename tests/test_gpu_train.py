@@ -122,7 +122,9 @@ def test_residual_layernorm_forward_cache(rows, f):
                                               (1000, 1024, False), (130, 2048, True), (200, 300, False),
                                               (77, 516, True), (70, 258, False),
                                               (20000, 256, False),  # 313 row blocks: sums in two passes
-                                              (33000, 300, True)])  # the same with ragged rows
+                                              (33000, 300, True),  # the same with ragged rows
+                                              (1000, 130, True),  # 32-row blocks, scalar loads
+                                              (33001, 200, False)])  # 32-row blocks, ragged, float4
 def test_layernorm_backward(rows, f, with_norm):
     a, b = synth.normal(19, (rows, f)), synth.normal(20, (rows, f))
     g, be = synth.positive_vector(f, 21), synth.normal(22, (f,))
