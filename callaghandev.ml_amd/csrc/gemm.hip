@@ -507,7 +507,13 @@ __global__ void __launch_bounds__(NTHREADS) gemm_nt_kernel(const GemmArgs args) 
 // Global -> LDS staging of one ROWS x BKK operand tile of the tiled kernel;
 // the tile lands in LDS as [rows][k] (pitch BKK + 4) for either source layout.
 //   T = false: the source is [rows][K] (k contiguous, row stride ld): each
-//     thread moves 16-byte row pieces straight into LDS.
+//     thread moves 16-byte row pieces straight into LDS.  The F4R lanes of a
+//     row are consecutive; the rows of a wave's 16 are interleaved, so that
+//     consecutive lane quads write rows r, r + 4, r + 8, r + 12, whose 64-byte
+//     pieces fall in disjoint bank ranges at pitch BKK + 4 (rows r and r + 1
+//     share banks: c3's Q/K/V and output projections had 19.2 M and 6.4 M
+//     conflict cycles per dispatch, now 0.5 M and 0, with the matrix pipes
+//     busy 87.2% instead of 85.3% of the Q/K/V product's active cycles).
 //   T = true:  the source is [K][rows] (rows contiguous, k-row stride ld):
 //     each thread loads four consecutive rows of one k and stores them as four
 //     LDS words.  Consecutive lanes take consecutive k, so the four stores of
@@ -537,7 +543,9 @@ struct OpStage {
       for (int i = 0; i < NP; ++i)
         off[i] = (uint32_t)sa * (uint32_t)ld + (uint32_t)min(row0 + 4 * (sb + G * i), rows - 4);
     } else {
-      sa = t / F4R;
+      static_assert(F4R == 4 && RPP % 16 == 0, "row interleave");
+      const int q = t / F4R;  // q's 16-row group keeps its rows, taken in the order 0, 4, 8, 12, 1, 5, ...
+      sa = (q & ~15) | ((q & 3) << 2) | ((q >> 2) & 3);
       sb = (t % F4R) * 4;
 #pragma unroll
       for (int i = 0; i < NP; ++i) off[i] = (uint32_t)min(row0 + sa + RPP * i, rows - 1) * (uint32_t)ld + sb;
