@@ -286,14 +286,17 @@ def bench_mha_backward(N, st, steps, warmup, cfg=None):
     RoPE of dQ and dK, BackpropQKV.  Events around the attention-core kernels
     and around the whole chain.
 
-    Two forms of the attention core are timed:
-      * from the forward's saved output and row statistics
-        (cdml_sdpa_bwd_saved; the forward with statistics, cdml_sdpa_fwd_lse,
-        runs once before timing, as in the training step).  The device trainer
-        always takes it, and the drop-in manager takes it whenever it still
-        holds the statistics of the forward call on the same arrays;
-      * recomputing the row statistics (cdml_sdpa_bwd): the drop-in manager's
-        form when no forward on those arrays preceded the call."""
+    Two forms of the attention core (with the inverse RoPE of dQ and dK) are
+    timed:
+      * from the forward's saved output and row statistics, the rotation
+        applied as the kernels store dQ and dK (cdml_sdpa_bwd_saved_rope; the
+        forward with statistics, cdml_sdpa_fwd_lse, runs once before timing,
+        as in the training step).  The device trainer always takes it, and
+        the drop-in manager takes cdml_sdpa_bwd_saved whenever it still holds
+        the statistics of the forward call on the same arrays;
+      * recomputing the row statistics (cdml_sdpa_bwd), then one
+        cdml_rope_qk_table launch: the drop-in manager's form when no forward
+        on those arrays preceded the call."""
     lib = N.lib()
     cfg = cfg or C3
     B, L, D, H = cfg["batch"], cfg["seq"], cfg["dim"], cfg["heads"]
@@ -328,13 +331,16 @@ def bench_mha_backward(N, st, steps, warmup, cfg=None):
     N.check(lib.cdml_rope_table(rcs.ptr, L, hd, 10000.0, s))
 
     def core(saved):
+        # with the inverse rotation of dQ and dK, as the trainer applies it: fused into the saved form's
+        # stores, a separate table-driven launch after the recomputing form
         if saved:
-            N.check(lib.cdml_sdpa_bwd_saved(b["q"].ptr, D, b["k"].ptr, D, b["v"].ptr, D, osv.ptr, D, lse.ptr,
-                                            dcat.ptr, D, dq.ptr, D, dk.ptr, D, dv.ptr, D, B, L, L, D, H, scale,
-                                            1, None, dwss.ptr, wss.value, s))
+            N.check(lib.cdml_sdpa_bwd_saved_rope(b["q"].ptr, D, b["k"].ptr, D, b["v"].ptr, D, osv.ptr, D, lse.ptr,
+                                                 dcat.ptr, D, dq.ptr, D, dk.ptr, D, dv.ptr, D, B, L, L, D, H, scale,
+                                                 1, None, rcs.ptr, L, dwss.ptr, wss.value, s))
         else:
             N.check(lib.cdml_sdpa_bwd(b["q"].ptr, D, b["k"].ptr, D, b["v"].ptr, D, dcat.ptr, D, dq.ptr, D,
                                       dk.ptr, D, dv.ptr, D, B, L, L, D, H, scale, 1, None, dws.ptr, wsz.value, s))
+            N.check(lib.cdml_rope_qk_table(dq.ptr, dk.ptr, rows, D, hd, H, rcs.ptr, L, 0, L, 1, s))
 
     def step(saved, t_core=None):
         N.check(lib.cdml_linear_backward(b["att"].ptr, D, b["dy"].ptr, D, dw[3].ptr, dcat.ptr, D, gw[3].ptr,
@@ -344,8 +350,6 @@ def bench_mha_backward(N, st, steps, warmup, cfg=None):
         core(saved)
         if t_core:
             t_core.stop(st)
-        # the inverse rotation of dQ and dK in one launch from the table, as the trainer does
-        N.check(lib.cdml_rope_qk_table(dq.ptr, dk.ptr, rows, D, hd, H, rcs.ptr, L, 0, L, 1, s))
         N.check(lib.cdml_backprop_qkv(b["x"].ptr, dq.ptr, dk.ptr, dv.ptr, dw[0].ptr, dw[1].ptr, dw[2].ptr,
                                       gw[0].ptr, gb[0].ptr, gw[1].ptr, gb[1].ptr, gw[2].ptr, gb[2].ptr,
                                       dxin.ptr, rows, D, D, dwsg.ptr, wsq.value, s))
@@ -378,13 +382,15 @@ def bench_mha_backward(N, st, steps, warmup, cfg=None):
             "attention_core_ms": round(core_ms, 4),
             "attention_core_tflops": round(tf(core_fl, core_ms), 2),
             "attention_core_frac_of_fp32_mfma_peak": round(tf(core_fl, core_ms) / FP32_MFMA_PEAK_TFLOPS, 4),
-            "attention_core_form": "cdml_sdpa_bwd_saved: from the forward's saved output and row statistics",
+            "attention_core_form": "cdml_sdpa_bwd_saved_rope: from the forward's saved output and row "
+                                   "statistics, the inverse RoPE of dQ and dK applied as they are stored",
             "recomputing_statistics": {
                 "ms": round(step_rc, 4), "tflops": round(tf(core_fl + proj_fl, step_rc), 2),
                 "attention_core_ms": round(core_rc, 4),
                 "attention_core_tflops": round(tf(core_fl, core_rc), 2),
                 "attention_core_frac_of_fp32_mfma_peak": round(tf(core_fl, core_rc) / FP32_MFMA_PEAK_TFLOPS, 4),
-                "form": "cdml_sdpa_bwd: the row statistics are recomputed by a forward pass inside the call"},
+                "form": "cdml_sdpa_bwd (the row statistics are recomputed by a forward pass inside the call), "
+                        "then cdml_rope_qk_table"},
             "flop_count": "matmul FLOPs of the gradients only: 8 x head_dim per causal (query, key) pair "
                           "for the core (no recompute counted), 4 x rows x D^2 per projection"}
 

@@ -85,6 +85,8 @@ SIGNATURES = {
     "cdml_sdpa_fwd_lse": [_vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _f, _i, _vp, _vp],
     "cdml_sdpa_bwd_saved": [_vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _vp, _i, _vp, _i, _vp, _i, _vp, _i,
                             _i, _i, _i, _i, _i, _f, _i, _vp, _vp, _sz, _vp],
+    "cdml_sdpa_bwd_saved_rope": [_vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _vp, _i, _vp, _i, _vp, _i, _vp, _i,
+                                 _i, _i, _i, _i, _i, _f, _i, _vp, _vp, _i, _vp, _sz, _vp],
     "cdml_rope_table": [_vp, _i, _i, _f, _vp],
     "cdml_rope_qk_table": [_vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _i, _i, _vp],
     "cdml_project_qkv_rope": [_vp] * 10 + [_i, _i, _i, _i, _vp, _i, _i, _i, _vp],

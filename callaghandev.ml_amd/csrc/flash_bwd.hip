@@ -49,7 +49,21 @@ struct BwdArgs {
   int batch, lq, lk, dim, heads, hd;
   float scale, scale_log2;
   int n_tiles, total;
+  // Inverse rotary embedding applied to dQ and dK as they are stored
+  // (cdml_sdpa_bwd_saved_rope): rope_cs[pos * hd / 2 + p] holds (cos, sin) of
+  // position pos for pair p, and a row's position is its index in its
+  // sequence.  NULL: no rotation.
+  const float2 *rope_cs;
 };
+
+// The inverse rotation of one pair (x0, x1) = dims (2p, 2p + 1) by (cos, sin)
+// t, rounded as rope_qk_table_kernel rounds it (each product before the sum),
+// so the fused form stores the same bits as a separate cdml_rope_qk_table.
+__device__ __forceinline__ float2 rope_inverse_pair(float x0, float x1, float2 t) {
+#pragma clang fp contract(off)
+  const float s = -t.y;
+  return make_float2(x0 * t.x - x1 * s, x0 * s + x1 * t.x);
+}
 
 // Offset of accumulator register r's row inside its 32-row block for a lane of
 // half-wave h: 8 * (r / 4) + 4 * h + r % 4 (the 32x32 MFMA D layout).
@@ -359,6 +373,21 @@ __global__ void __launch_bounds__(BW_THREADS, (HD <= 32 && !HAS_MASK) ? 3 : (HD 
   if (key < a.lk) {
     float *dkrow = a.dk + ((size_t)b * a.lk + key) * a.lddk + col0;
     float *dvrow = a.dv + ((size_t)b * a.lk + key) * a.lddv + col0;
+    // (cos, sin) of this key's pairs, loaded before any store (a load issued
+    // after a store waits for it)
+    float2 cs[NDB][4][2];
+    if (a.rope_cs) {
+      const float2 *t = a.rope_cs + (size_t)key * (a.hd >> 1);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int d = db * 32 + 8 * g + 4 * hf + 2 * j;
+            cs[db][g][j] = d < a.hd ? t[d >> 1] : make_float2(1.f, 0.f);
+          }
+    }
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
 #pragma unroll
@@ -369,6 +398,14 @@ __global__ void __launch_bounds__(BW_THREADS, (HD <= 32 && !HAS_MASK) ? 3 : (HD 
         for (int c = 0; c < 4; ++c) {
           x[c] = dk[db][4 * g + c] * a.scale;
           y[c] = dv[db][4 * g + c];
+        }
+        if (a.rope_cs) {  // dims d + c and d + c + 1 are one pair, in this lane
+#pragma unroll
+          for (int c = 0; c < 4; c += 2) {
+            const float2 r = rope_inverse_pair(x[c], x[c + 1], cs[db][g][c >> 1]);
+            x[c] = r.x;
+            x[c + 1] = r.y;
+          }
         }
         if constexpr (VEC) {
           *reinterpret_cast<vf4 *>(dkrow + d) = x;
@@ -533,6 +570,19 @@ __global__ void __launch_bounds__(BW_THREADS, 2) flash_bwd_dq_kernel(const BwdAr
 
   if (qi < a.lq) {
     float *dqrow = a.dq + ((size_t)b * a.lq + qi) * a.lddq + col0;
+    float2 cs[NDB][4][2];  // (cos, sin) of this row's pairs, loaded before any store
+    if (a.rope_cs) {
+      const float2 *t = a.rope_cs + (size_t)qi * (a.hd >> 1);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int d = db * 32 + 8 * g + 4 * hf + 2 * j;
+            cs[db][g][j] = d < a.hd ? t[d >> 1] : make_float2(1.f, 0.f);
+          }
+    }
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
 #pragma unroll
@@ -541,6 +591,14 @@ __global__ void __launch_bounds__(BW_THREADS, 2) flash_bwd_dq_kernel(const BwdAr
         vf4 x;
 #pragma unroll
         for (int c = 0; c < 4; ++c) x[c] = dq[db][4 * g + c] * a.scale;
+        if (a.rope_cs) {
+#pragma unroll
+          for (int c = 0; c < 4; c += 2) {
+            const float2 r = rope_inverse_pair(x[c], x[c + 1], cs[db][g][c >> 1]);
+            x[c] = r.x;
+            x[c + 1] = r.y;
+          }
+        }
         if constexpr (VEC) {
           *reinterpret_cast<vf4 *>(dqrow + d) = x;
         } else {
@@ -846,8 +904,11 @@ int zero_rows(float *p, long long rows, int cols, int ld, hipStream_t st) {
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
+// Returns whether dQ left rotated (a.rope_cs set and a dQ kernel that
+// applies it: the stored-dS dQ kernels do not, their 16 rows per lane would
+// cost the table registers they need for their occupancy).
 template <int HD, int BQ, int BN, bool CAUSAL, bool HAS_MASK, bool VEC>
-void launch_bwd(BwdArgs &a, hipStream_t st) {
+bool launch_bwd(BwdArgs &a, hipStream_t st) {
   const int n_bh = a.batch * a.heads;
   const int kt = (a.lk + BW_TILE - 1) / BW_TILE;
   a.n_tiles = (a.lq + BW_TILE - 1) / BW_TILE;
@@ -860,28 +921,27 @@ void launch_bwd(BwdArgs &a, hipStream_t st) {
         flash_bwd_dq_ds_short_kernel<HD, kShortQB><<<dim3(n_bh), dim3(64 * ((nqb + 1) / 2)), 0, st>>>(a);
       else
         flash_bwd_dq_ds_kernel<HD, 64><<<dim3(n_bh * a.n_tiles), dim3(BW_THREADS), 0, st>>>(a);
-      return;
+      return false;
     }
   }
   flash_bwd_dkdv_kernel<HD, BQ, CAUSAL, HAS_MASK, VEC, false><<<dim3(n_bh * kt), dim3(BW_THREADS), 0, st>>>(a);
   flash_bwd_dq_kernel<HD, BN, CAUSAL, HAS_MASK, VEC><<<dim3(n_bh * a.n_tiles), dim3(BW_THREADS), 0, st>>>(a);
+  return a.rope_cs != nullptr;
 }
 
 template <int HD, int BQ, int BN, bool VEC>
-void launch_bwd_mode(BwdArgs &a, bool causal, hipStream_t st) {
+bool launch_bwd_mode(BwdArgs &a, bool causal, hipStream_t st) {
   if (causal) {
-    if (a.mask) launch_bwd<HD, BQ, BN, true, true, VEC>(a, st);
-    else launch_bwd<HD, BQ, BN, true, false, VEC>(a, st);
-  } else {
-    if (a.mask) launch_bwd<HD, BQ, BN, false, true, VEC>(a, st);
-    else launch_bwd<HD, BQ, BN, false, false, VEC>(a, st);
+    if (a.mask) return launch_bwd<HD, BQ, BN, true, true, VEC>(a, st);
+    return launch_bwd<HD, BQ, BN, true, false, VEC>(a, st);
   }
+  if (a.mask) return launch_bwd<HD, BQ, BN, false, true, VEC>(a, st);
+  return launch_bwd<HD, BQ, BN, false, false, VEC>(a, st);
 }
 
 template <int HD, int BQ, int BN>
-void launch_bwd_hd(BwdArgs &a, bool causal, bool vec, hipStream_t st) {
-  if (vec) launch_bwd_mode<HD, BQ, BN, true>(a, causal, st);
-  else launch_bwd_mode<HD, BQ, BN, false>(a, causal, st);
+bool launch_bwd_hd(BwdArgs &a, bool causal, bool vec, hipStream_t st) {
+  return vec ? launch_bwd_mode<HD, BQ, BN, true>(a, causal, st) : launch_bwd_mode<HD, BQ, BN, false>(a, causal, st);
 }
 
 }  // namespace
@@ -944,7 +1004,7 @@ int sdpa_bwd_impl(const float *q, int ldq, const float *k, int ldk, const float 
                   int lddo, float *dq, int lddq, float *dk, int lddk, float *dv, int lddv, int batch,
                   int lq, int lk, int dim, int num_heads, float scale, int causal,
                   const uint8_t *mask, void *workspace, size_t workspace_bytes, cdml_stream stream,
-                  const char *what) {
+                  const char *what, const float *rope_cs = nullptr, int rope_npos = 0) {
   const bool saved = o_saved != nullptr;
   size_t need = 0;
   int rc = cdml_sdpa_bwd_workspace_size(batch, lq, lk, dim, num_heads, &need);
@@ -1002,6 +1062,7 @@ int sdpa_bwd_impl(const float *q, int ldq, const float *k, int ldk, const float 
   a.hd = dim / num_heads;
   a.scale = scale;
   a.scale_log2 = scale * kLog2e;
+  a.rope_cs = reinterpret_cast<const float2 *>(rope_cs);
   char *ws = static_cast<char *>(workspace);
   const size_t f = sizeof(float), bh = (size_t)batch * num_heads;
   float *o = reinterpret_cast<float *>(ws);
@@ -1062,10 +1123,14 @@ int sdpa_bwd_impl(const float *q, int ldq, const float *k, int ldk, const float 
       a.ds_bh = (long long)(extra / sizeof(float) / bh);
     }
   }
-  if (hd_pad == 32) launch_bwd_hd<32, 64, 64>(a, causal != 0, vec, st);
-  else if (hd_pad == 64) launch_bwd_hd<64, 64, 32>(a, causal != 0, vec, st);
-  else launch_bwd_hd<128, 32, 32>(a, causal != 0, vec, st);
-  return check_launch("flash_bwd_dkdv_kernel / flash_bwd_dq_kernel");
+  bool dq_rotated;
+  if (hd_pad == 32) dq_rotated = launch_bwd_hd<32, 64, 64>(a, causal != 0, vec, st);
+  else if (hd_pad == 64) dq_rotated = launch_bwd_hd<64, 64, 32>(a, causal != 0, vec, st);
+  else dq_rotated = launch_bwd_hd<128, 32, 32>(a, causal != 0, vec, st);
+  rc = check_launch("flash_bwd_dkdv_kernel / flash_bwd_dq_kernel");
+  if (rc || !rope_cs || dq_rotated) return rc;
+  // dK left rotated; dQ from the stored dS blocks takes the table RoPE
+  return cdml_rope_qk_table(dq, nullptr, batch * lq, lddq, hd, num_heads, rope_cs, rope_npos, 0, lq, 1, stream);
 }
 
 }  // namespace
@@ -1091,4 +1156,25 @@ extern "C" int cdml_sdpa_bwd_saved(const float *q, int ldq, const float *k, int 
   return sdpa_bwd_impl(q, ldq, k, ldk, v, ldv, o, ldo, lse, dout, lddo, dq, lddq, dk, lddk, dv, lddv,
                        batch, lq, lk, dim, num_heads, scale, causal, mask, workspace, workspace_bytes,
                        stream, "cdml_sdpa_bwd_saved");
+}
+
+extern "C" int cdml_sdpa_bwd_saved_rope(const float *q, int ldq, const float *k, int ldk, const float *v,
+                                        int ldv, const float *o, int ldo, const float *lse,
+                                        const float *dout, int lddo, float *dq, int lddq, float *dk,
+                                        int lddk, float *dv, int lddv, int batch, int lq, int lk, int dim,
+                                        int num_heads, float scale, int causal, const uint8_t *mask,
+                                        const float *rope_cs, int n_pos, void *workspace,
+                                        size_t workspace_bytes, cdml_stream stream) {
+  const char *what = "cdml_sdpa_bwd_saved_rope";
+  if (!o) return fail(CDML_E_INVALID, "%s: o is NULL", what);
+  if (num_heads > 0 && dim > 0 && dim % num_heads == 0 && ((dim / num_heads) & 1))
+    return fail(CDML_E_INVALID, "%s: RoPE requires an even head dimension", what);
+  if (!rope_cs) return fail(CDML_E_INVALID, "%s: rope_cs is NULL", what);
+  if (reinterpret_cast<uintptr_t>(rope_cs) % 8)
+    return fail(CDML_E_INVALID, "%s: rope_cs must be 8-byte aligned", what);
+  if (n_pos < std::max(lq, lk))
+    return fail(CDML_E_INVALID, "%s: a %d-row table does not cover %d positions", what, n_pos, std::max(lq, lk));
+  return sdpa_bwd_impl(q, ldq, k, ldk, v, ldv, o, ldo, lse, dout, lddo, dq, lddq, dk, lddk, dv, lddv,
+                       batch, lq, lk, dim, num_heads, scale, causal, mask, workspace, workspace_bytes,
+                       stream, what, rope_cs, n_pos);
 }

@@ -426,15 +426,18 @@ void DeviceTrainer::bucket_backward(int batch, int seqLen) {
     // attention (BackpropAttention, :933-987)
     check(cdml_linear_backward(Y.att, D, dr1_, D, Y.wo, dcat_, D, Y.gwo, Y.gbo, rows, D, D, 0, ws_, ws_bytes_, s),
           "cdml_linear_backward");
-    if (Y.lse)
-      check(cdml_sdpa_bwd_saved(Y.q, D, Y.k, D, Y.v, D, Y.att, D, Y.lse, dcat_, D, dq_, D, dk_, D, dv_, D, batch,
-                                seqLen, seqLen, D, H, scale, 1, nullptr, ws_, ws_bytes_, s),
-            "cdml_sdpa_bwd_saved");
-    else
+    // and the inverse rotation of dQ and dK (:978-985), as the kernels store them
+    if (Y.lse) {
+      check(cdml_sdpa_bwd_saved_rope(Y.q, D, Y.k, D, Y.v, D, Y.att, D, Y.lse, dcat_, D, dq_, D, dk_, D, dv_, D,
+                                     batch, seqLen, seqLen, D, H, scale, 1, nullptr, rope_cs_, cap_s_, ws_,
+                                     ws_bytes_, s),
+            "cdml_sdpa_bwd_saved_rope");
+    } else {
       check(cdml_sdpa_bwd(Y.q, D, Y.k, D, Y.v, D, dcat_, D, dq_, D, dk_, D, dv_, D, batch, seqLen, seqLen, D, H,
                           scale, 1, nullptr, ws_, ws_bytes_, s),
             "cdml_sdpa_bwd");
-    check(cdml_rope_qk_table(dq_, dk_, rows, D, hd, H, rope_cs_, cap_s_, 0, seqLen, 1, s), "cdml_rope_qk_table");
+      check(cdml_rope_qk_table(dq_, dk_, rows, D, hd, H, rope_cs_, cap_s_, 0, seqLen, 1, s), "cdml_rope_qk_table");
+    }
     check(cdml_backprop_qkv(Y.x, dq_, dk_, dv_, Y.wq, Y.wk, Y.wv, Y.gwq, Y.gbq, Y.gwk, Y.gbk, Y.gwv, Y.gbv, dxa_,
                             rows, D, D, ws_, ws_bytes_, s),
           "cdml_backprop_qkv");

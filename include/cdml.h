@@ -366,6 +366,27 @@ int cdml_sdpa_bwd_saved(const float *q, int ldq, const float *k, int ldk,
                         const uint8_t *mask, void *workspace,
                         size_t workspace_bytes, cdml_stream stream);
 
+/* cdml_sdpa_bwd_saved followed by the inverse rotary embedding of dQ and dK,
+ * as TransformerTrainer.BackpropAttention applies it to the attention's
+ * input gradients (TransformerTrainer.cs:978-985, the inverse of the rotation
+ * at :811-848): every head of a row at the row's index within its sequence,
+ * with rope_cs a cdml_rope_table of n_pos >= max(lq, lk) positions for the
+ * head dim (8-byte aligned).  dK, and dQ where it is recomputed, are rotated
+ * as the kernels store them; dQ from stored dS blocks takes one table-RoPE
+ * launch on dQ alone.  The bits are those of cdml_sdpa_bwd_saved then
+ * cdml_rope_qk_table(dq, dk, ..., pos_offset 0, seg_len lq, inverse 1) on
+ * the same rows.  Same workspace as cdml_sdpa_bwd_saved; the head dim must
+ * be even. */
+int cdml_sdpa_bwd_saved_rope(const float *q, int ldq, const float *k, int ldk,
+                             const float *v, int ldv, const float *o, int ldo,
+                             const float *lse, const float *dout, int lddo,
+                             float *dq, int lddq, float *dk, int lddk,
+                             float *dv, int lddv, int batch, int lq, int lk,
+                             int dim, int num_heads, float scale, int causal,
+                             const uint8_t *mask, const float *rope_cs,
+                             int n_pos, void *workspace,
+                             size_t workspace_bytes, cdml_stream stream);
+
 /* ---- training step (TransformerTrainer.TrainBatchDiscrete,
  * Transformers/MultiTypeTransformer/TransformerTrainer.cs:217-327) -------- */
 

@@ -311,7 +311,8 @@ def pass_backward(out):
     leg = bench_line(so).get("other_configs", {}).get("c3_mha_layer_backward", {})
     rc = leg.get("recomputing_statistics", {})
     note = ("The c3 MHA layer backward leg: 3 warm-up + 5 timed steps in the saved-statistics form "
-            "(`cdml_sdpa_bwd_saved`), then the same with the statistics recomputed (`cdml_sdpa_bwd`), "
+            "(`cdml_sdpa_bwd_saved_rope`, the inverse RoPE of dQ and dK applied as they are stored), then the "
+            "same with the statistics recomputed (`cdml_sdpa_bwd`, then `cdml_rope_qk_table`), "
             "after one `cdml_sdpa_fwd_lse`.  The bench line of the same run: attention core "
             f"{leg.get('attention_core_ms')} ms ({leg.get('attention_core_tflops')} TFLOP/s) saved, "
             f"{rc.get('attention_core_ms')} ms recomputing; whole layer backward {leg.get('ms')} ms "

@@ -187,6 +187,24 @@ def test_sdpa_bwd_workspace_sizes():
     assert lib.cdml_sdpa_bwd_stored_ds_workspace_size(1, 8, 8, 12, 3, 1, None) == N.E_INVALID
 
 
+def test_sdpa_bwd_saved_rope_argument_checks():
+    """cdml_sdpa_bwd_saved_rope refuses, before any device work, a NULL saved output,
+    an odd head dim, a NULL or misaligned (cos, sin) table and a table shorter than
+    the sequences."""
+    lib = N.lib()
+    f = C.c_void_p(0x1000)
+
+    def call(o=f, dim=64, heads=4, cs=f, n_pos=100, lq=100, lk=100):
+        return lib.cdml_sdpa_bwd_saved_rope(f, dim, f, dim, f, dim, o, dim, f, f, dim, f, dim, f, dim, f, dim,
+                                            2, lq, lk, dim, heads, 0.25, 1, None, cs, n_pos, f, 1 << 20, None)
+    assert call(o=None) == N.E_INVALID
+    assert call(dim=60, heads=4) == N.E_INVALID          # head dim 15
+    assert call(cs=None) == N.E_INVALID
+    assert call(cs=C.c_void_p(0x1004)) == N.E_INVALID    # 4-byte aligned table
+    assert call(n_pos=99) == N.E_INVALID                 # one position short
+    assert call(n_pos=120, lq=100, lk=121) == N.E_INVALID
+
+
 def test_mha_layer_fwd_argument_checks():
     """cdml_mha_layer_fwd rejects its arguments before any device work: a head dim that
     does not divide D, an odd head dim (RoPE pairs), NULL buffers and a short workspace;

@@ -389,6 +389,53 @@ def test_sdpa_bwd_from_saved_statistics(batch, L, dim, heads):
         parity(dq3[r], want[0], f"stored-dS dQ, sequence {sq}")
 
 
+# head dim 32: the short stored-dS dQ kernel (300, 512 rows), the long one
+# (700); head dim 64: short (256) and long (257); head dims 16 and 48: scalar
+# loads and the recomputing dQ kernel; each with the minimum workspace
+# (recomputing dQ) and with room for the stored dS blocks.
+@pytest.mark.parametrize("batch,L,dim,heads", [(2, 300, 256, 8), (1, 512, 256, 8), (1, 700, 64, 2),
+                                               (1, 256, 128, 2), (1, 257, 128, 2), (2, 100, 64, 4),
+                                               (3, 130, 96, 2)])
+@pytest.mark.parametrize("stored", [False, True])
+def test_sdpa_bwd_saved_rope_equals_saved_then_table_rope(batch, L, dim, heads, stored):
+    """cdml_sdpa_bwd_saved_rope rotates dQ and dK as its kernels store them:
+    the same bits as cdml_sdpa_bwd_saved followed by cdml_rope_qk_table
+    (inverse, each row at its index in its sequence), dV untouched; the
+    rotation itself is pinned by the table RoPE's own tests."""
+    import ctypes as C
+    from cdml import native as N
+    rows, hd = batch * L, dim // heads
+    q, k, v, g = (synth.normal(90 + i, (rows, dim)) for i in range(4))
+    scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
+    bq, bk, bv, bg = (G.up(a) for a in (q, k, v, g))
+    o, lse = N.DeviceBuffer(rows * dim * 4), N.DeviceBuffer(batch * heads * L * 4)
+    s = G.stream().handle
+    lib = N.lib()
+    N.check(lib.cdml_sdpa_fwd_lse(bq.ptr, dim, bk.ptr, dim, bv.ptr, dim, o.ptr, dim, lse.ptr, batch, L, L, dim,
+                                  heads, scale, 1, None, s))
+    ws = C.c_size_t(batch * heads * L * 4)
+    if stored:
+        N.check(lib.cdml_sdpa_bwd_saved_workspace_size(batch, L, L, dim, heads, 1, C.byref(ws)))
+    bws = N.DeviceBuffer(ws.value)
+    cs = N.DeviceBuffer(L * hd * 4)
+    N.check(lib.cdml_rope_table(cs.ptr, L, hd, 10000.0, s))
+    outs = [[N.DeviceBuffer(rows * dim * 4) for _ in range(3)] for _ in range(2)]
+    N.check(lib.cdml_sdpa_bwd_saved(bq.ptr, dim, bk.ptr, dim, bv.ptr, dim, o.ptr, dim, lse.ptr, bg.ptr, dim,
+                                    outs[0][0].ptr, dim, outs[0][1].ptr, dim, outs[0][2].ptr, dim, batch, L, L, dim,
+                                    heads, scale, 1, None, bws.ptr, ws.value, s))
+    N.check(lib.cdml_rope_qk_table(outs[0][0].ptr, outs[0][1].ptr, rows, dim, hd, heads, cs.ptr, L, 0, L, 1, s))
+    N.check(lib.cdml_sdpa_bwd_saved_rope(bq.ptr, dim, bk.ptr, dim, bv.ptr, dim, o.ptr, dim, lse.ptr, bg.ptr, dim,
+                                         outs[1][0].ptr, dim, outs[1][1].ptr, dim, outs[1][2].ptr, dim, batch, L,
+                                         L, dim, heads, scale, 1, None, cs.ptr, L, bws.ptr, ws.value, s))
+    for a, b, n in zip(outs[0], outs[1], "QKV"):
+        assert np.array_equal(G.down(a, (rows, dim)).view(np.uint32), G.down(b, (rows, dim)).view(np.uint32)), \
+            f"d{n}: fused inverse RoPE != saved + cdml_rope_qk_table"
+    # a table one position short, and an odd head dim, are refused
+    assert lib.cdml_sdpa_bwd_saved_rope(bq.ptr, dim, bk.ptr, dim, bv.ptr, dim, o.ptr, dim, lse.ptr, bg.ptr, dim,
+                                        outs[1][0].ptr, dim, outs[1][1].ptr, dim, outs[1][2].ptr, dim, batch, L,
+                                        L, dim, heads, scale, 1, None, cs.ptr, L - 1, bws.ptr, ws.value, s) == -1
+
+
 def test_sdpa_bwd_stored_scores_c3_shape():
     """The c3 shape (4 x 4096, 16 heads of 64, causal) through
     cdml_sdpa_fwd_lse + cdml_sdpa_bwd_saved with the stored-dS workspace
