@@ -371,12 +371,13 @@ int cdml_sdpa_bwd_saved(const float *q, int ldq, const float *k, int ldk,
  * input gradients (TransformerTrainer.cs:978-985, the inverse of the rotation
  * at :811-848): every head of a row at the row's index within its sequence
  * (dQ rows modulo lq, dK rows modulo lk), with rope_cs a cdml_rope_table of
- * n_pos >= max(lq, lk) positions for the head dim (8-byte aligned).  dK, and dQ where it is recomputed, are rotated
- * as the kernels store them; dQ from stored dS blocks takes one table-RoPE
- * launch on dQ alone.  With lq == lk (the trainer's causal self-attention)
- * the bits are those of cdml_sdpa_bwd_saved then cdml_rope_qk_table(dq, dk,
- * ..., pos_offset 0, seg_len lq, inverse 1) on the same rows.  Same workspace as cdml_sdpa_bwd_saved; the head dim must
- * be even. */
+ * n_pos >= max(lq, lk) positions for the head dim (8-byte aligned).  dK, and
+ * dQ where it is recomputed, are rotated as the kernels store them; dQ from
+ * stored dS blocks takes one table-RoPE launch on dQ alone.  With lq == lk
+ * (the trainer's causal self-attention) the bits are those of
+ * cdml_sdpa_bwd_saved then cdml_rope_qk_table(dq, dk, ..., pos_offset 0,
+ * seg_len lq, inverse 1) on the same rows.  Same workspace as
+ * cdml_sdpa_bwd_saved; the head dim must be even. */
 int cdml_sdpa_bwd_saved_rope(const float *q, int ldq, const float *k, int ldk,
                              const float *v, int ldv, const float *o, int ldo,
                              const float *lse, const float *dout, int lddo,
